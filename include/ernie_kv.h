@@ -1,0 +1,219 @@
+/*
+ * ernie_kv.h -- C ABI of the MI355X (gfx950) ERNIE 5.5 attention KV-cache path.
+ *
+ * Every entry point takes device pointers, sizes and strides (in elements
+ * unless marked "bytes"), enqueues its kernels on `stream` (a hipStream_t,
+ * NULL = default stream) and returns 0 on success or a nonzero status
+ * (1 invalid argument, 2 launch failure, 3 workspace too small);
+ * ekv_last_error() names the failure.  Nothing here allocates device memory:
+ * callers pass outputs and workspaces, as the reference's layers preallocate
+ * `out`, `o_padded` and the top-k buffers.  No entry point synchronizes the
+ * host.
+ *
+ * Data formats
+ *   bf16          uint16_t bit patterns.
+ *   fp8 page      64 token rows of `dim` e4m3fn bytes, then 64 fp32 scales
+ *                 (values first, then scales -- the page layout of
+ *                 src/vllm_ernie/models/ernie5_5/nvidia/attention.py:852-860);
+ *                 pages `page_stride` bytes apart.  Latent rows: dim 512/576.
+ *                 Indexer K rows: dim 128 (128 fp8 + 4-byte scale = 132 B per
+ *                 token, attention.py:933-935).
+ *   slot          block_table[seq][pos / 64] * 64 + pos % 64; negative = skip
+ *                 (attention.py:845-847).
+ *   quant rule    per-token scale 2^ceil(log2(max(amax,1e-10) * (1/448))),
+ *                 values clamp(x / scale, +-448) rounded to nearest-even e4m3fn
+ *                 (attention.py:221-227, 317-319); scale stored as fp32.
+ *
+ * Citations are path:line into the baidu/vLLM-ERNIE tree
+ * (src/vllm_ernie/models/ernie5_5/...).
+ */
+#ifndef ERNIE_KV_H_
+#define ERNIE_KV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread. */
+const char* ekv_last_error(void);
+/* ABI revision of this header (1). */
+int ekv_abi_version(void);
+
+/*
+ * Latent append with fused fp8 quantization.  rows [num_tokens, row_stride]
+ * bf16 (dim in {128, 512, 576}) -> the fp8 page row of slot_mapping[t].
+ * Replaces the latent write MLAAttention performs on
+ * `mla_attn(q, kv_c_normed, k_pe)` (nvidia/attention.py:1226, inputs built at
+ * :1186-1190), the concat_and_cache-style write vLLM runs for it.
+ */
+int ekv_kv_append_quant(const uint16_t* rows, int64_t row_stride, int32_t num_tokens, int32_t dim,
+                        const int64_t* slot_mapping, uint8_t* cache, int64_t page_stride /*bytes*/,
+                        int64_t num_pages, void* stream);
+
+/*
+ * Indexer K-cache insert: k [num_tokens, k_stride] bf16 (128 wide, after
+ * LayerNorm, RoPE and Hadamard) -> 128 fp8 + fp32 scale per token.
+ * Replaces the K insert of SparseAttnIndexer (nvidia/attention.py:942-953,
+ * `skip_k_cache_insert=False` path; FP4 writer counterpart at :831-860).
+ */
+int ekv_indexer_k_insert(const uint16_t* k, int64_t k_stride, int32_t num_tokens,
+                         const int64_t* slot_mapping, uint8_t* kcache, int64_t page_stride /*bytes*/,
+                         int64_t num_pages, void* stream);
+
+/*
+ * HCA 128->1 compressor.  For each sequence b (tokens qsl[b]..qsl[b+1]-1 at
+ * consecutive positions from positions[qsl[b]]), compresses every 128-token
+ * span that completes in this call from kv_score rows ([kv | score], bf16,
+ * 2*dim wide) of this call and of the state ring, and writes the fp8 row to
+ * compressed slot comp_block_table[b][j/64]*64 + j%64.  ape [128, dim] fp32,
+ * norm_w [dim] fp32, cos_sin [max_spans, 64] fp32 (cos | sin at position
+ * 128*j).  Must be called before ekv_hca_append of the same step.
+ * Replaces Ernie5_5Compressor.forward -> DeepseekCompressor.forward
+ * (nvidia/attention.py:398-408; weights compressor.fused_wkv_wgate,
+ * nvidia/model.py:684-685).
+ */
+int ekv_hca_compress(const uint16_t* kv_score, int64_t kvs_stride, const int64_t* positions,
+                     const int32_t* qsl, int32_t num_seqs, int32_t max_query_len, int32_t dim,
+                     const uint16_t* state, const int32_t* state_slot, int32_t num_state,
+                     const float* ape, const float* norm_w, float eps, const float* cos_sin,
+                     int32_t max_spans, const int32_t* comp_block_table, int32_t comp_bt_stride,
+                     uint8_t* pool, int64_t page_stride /*bytes*/, int64_t num_pages, void* stream);
+
+/*
+ * HCA append: quantize latent rows into slot_mapping slots, into the window
+ * ring (the last `ring` positions of each sequence, ring slot
+ * ring_pages[b][(p % ring)/64]*64 + (p % ring)%64) and copy the kv_score rows
+ * of the last 256 positions into the state ring state[state_slot[b]][p % 256].
+ * ring_pages / state may be NULL.  Replaces the SWA write of
+ * DeepseekV4Attention._prepare_and_attn_fn (nvidia/attention.py:494-505).
+ */
+int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                   int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                   const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                   int32_t num_seqs, uint8_t* pool, int64_t page_stride /*bytes*/, int64_t num_pages,
+                   const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* state,
+                   const int32_t* state_slot, int32_t num_state, void* stream);
+
+/*
+ * HCA decode index rows: [compressed slots 0..n_c-1 | ring slots of positions
+ * p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window), and the row
+ * lengths.  Replaces the compressed+window index construction inside
+ * DeepseekV4Attention (nvidia/attention.py:471-539).
+ */
+int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
+                           const int32_t* comp_block_table, int32_t comp_bt_stride,
+                           const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window,
+                           int32_t* out, int64_t out_stride, int32_t width, int32_t* lengths,
+                           void* stream);
+
+/*
+ * merge_swa_topk: out[t] = [topk[t][:n] | seq-w .. seq-1 | -1 ...] with
+ * seq = positions[t]+1, n = min(max(seq-window,0), topk_width),
+ * w = min(seq, window).  Replaces merge_swa_topk / _merge_swa_topk_kernel
+ * (nvidia/attention.py:582-641).
+ */
+int ekv_merge_swa_topk(const int32_t* topk, int64_t topk_stride, int32_t* out, int64_t out_stride,
+                       const int64_t* positions, int32_t num_tokens, int32_t topk_width,
+                       int32_t out_width, int32_t window, void* stream);
+
+/*
+ * Orthonormal Walsh-Hadamard transform of 128-wide bf16 rows (Sylvester
+ * order, times 1/sqrt(128)).  Replaces hadamard_rows / ops.hadacore_transform
+ * (nvidia/attention.py:102-108).
+ */
+int ekv_hadamard_rows(const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, int32_t rows,
+                      int32_t dim, void* stream);
+
+/*
+ * Indexer q quant: q [T, heads, 128] bf16 -> fp8 with a per-(token, head)
+ * UE8M0 scale folded into the head weights:
+ *   w_out = (w * q_scale) * 128^-0.5 * 64^-0.5.
+ * Also writes q's int8 digit planes [T, 3, heads, 128] (may be NULL) used by
+ * the exact scorer.  Replaces per_token_group_quant_fp8(..., use_ue8m0=True)
+ * and the weight fold (nvidia/attention.py:925, 976-980).
+ */
+int ekv_indexer_q_quant(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                        const void* weights, int32_t weights_is_bf16, int64_t w_stride,
+                        int32_t num_tokens, int32_t heads, uint8_t* q_fp8, float* w_out,
+                        int8_t* q_digits, void* stream);
+
+/*
+ * Windowed indexer lengths out[t] = max(positions[t] + 1 - window, 0).
+ * Replaces the decode seq_lens rewrite of Ernie5_5IndexerMetadataBuilder.build
+ * (nvidia/attention.py:669-675), per query row.
+ */
+int ekv_indexer_windowed_lengths(const int64_t* positions, int32_t num_tokens, int32_t window,
+                                 int32_t* out, void* stream);
+
+/*
+ * Exact lightning-indexer scores: for query row t (request req_ids[t]) and
+ * every token s < lengths[t],
+ *   score = kscale_s * sum_h w[t,h] * relu(q[t,h] . k[s])
+ * with the dot product exact and a fixed fp32 head-sum order.
+ * Replaces the paged MQA logits of SparseAttnIndexer (DeepGEMM,
+ * nvidia/attention.py:56-61, 677-685, 982-984).
+ */
+int ekv_indexer_score(const int8_t* q_digits, const float* w, const uint8_t* kcache,
+                      int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
+                      int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
+                      int32_t num_tokens, int32_t max_len, float* scores, int64_t scores_stride,
+                      void* stream);
+
+/*
+ * Exact top-k of each score row (first lengths[t] entries): the k largest by
+ * (score desc, index asc), written in ascending index order, -1 padded.
+ * Replaces the top-k inside SparseAttnIndexer (nvidia/attention.py:942-953)
+ * that fills indexer_topk_buffer (nvidia/model.py:71-79).
+ */
+int ekv_topk_select(const float* scores, int64_t scores_stride, const int32_t* lengths,
+                    int32_t num_tokens, int32_t max_len, int32_t* out, int64_t out_stride, int32_t k,
+                    void* stream);
+
+/* Workspace bytes ekv_indexer_topk needs. */
+int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len);
+
+/*
+ * Indexer scoring + exact top-k in one call (the SparseAttnIndexer decode
+ * path, nvidia/attention.py:942-953, 982-984).
+ */
+int ekv_indexer_topk(const int8_t* q_digits, const float* w, const uint8_t* kcache,
+                     int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
+                     int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
+                     int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride,
+                     int32_t k, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes ekv_sparse_mla_decode needs. */
+int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int32_t heads, int32_t width);
+
+/*
+ * Sparse MLA decode with attention sink.  q [T, heads, dim] bf16 (dim 512 or
+ * 576, heads a multiple of 16, <= 64); cache fp8 pages (cache_bf16 = 0) or
+ * bf16 flat rows [num_pages*64, dim] (cache_bf16 = 1); indices [T, width]
+ * global slots, or request-local token indices when block_table != NULL
+ * (converted in-kernel, -1 kept); lengths [T] optional; sinks [heads] fp32
+ * optional (natural-log units, enters the denominator only).
+ *   out [T, heads, 512] bf16, lse [T, heads] fp32 = log sum_j exp(s_j).
+ * Replaces Ernie5_5FlashMLASparseImpl._fp8_flash_mla_kernel /
+ * _bf16_flash_mla_kernel -> flash_mla_with_kvcache / flash_mla_sparse_fwd
+ * (nvidia/attention.py:701-790) and the logical->global conversion behind
+ * record_logical_topk_ready (nvidia/attention.py:1225).
+ */
+int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          int32_t num_tokens, int32_t heads, int32_t dim, const uint8_t* cache,
+                          int32_t cache_bf16, int64_t page_stride /*bytes*/, int64_t num_pages,
+                          const int32_t* indices, int64_t idx_stride, int32_t width,
+                          const int32_t* lengths, const int32_t* block_table, int64_t bt_stride,
+                          const int32_t* req_ids, const float* sinks, float scale, uint16_t* out,
+                          int64_t out_tok_stride, int64_t out_head_stride, float* lse,
+                          int64_t lse_stride, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The 256-entry byte -> packed signed base-64 digit table the scorer uses. */
+int ekv_fp8_digit_table(uint32_t* table, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ERNIE_KV_H_ */

@@ -1,0 +1,100 @@
+"""GPU parity: HCA write path (compress + append + window ring + state ring)
+and the HCA decode index rows, bit-exact against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_tensor, bf16_values, randn_bf16, to_dev
+from oracle import hca as oh
+from oracle import indexer as oi
+from oracle import paged
+
+pytestmark = pytest.mark.gpu
+
+
+class HcaCase:
+    def __init__(self, rng, dim, num_seqs, max_pos, ring):
+        self.dim, self.B, self.ring = dim, num_seqs, ring
+        lp = (max_pos + 63) // 64
+        spans = max_pos // 128 + 1
+        cp = (spans + 63) // 64
+        rp = ring // 64
+        perm = rng.permutation(num_seqs * (lp + cp + rp)).astype(np.int32)
+        self.bt = perm[: num_seqs * lp].reshape(num_seqs, lp)
+        self.comp_bt = perm[num_seqs * lp : num_seqs * (lp + cp)].reshape(num_seqs, cp)
+        self.ring_pages = perm[num_seqs * (lp + cp) :].reshape(num_seqs, rp)
+        self.pages = len(perm)
+        self.ape = (rng.standard_normal((128, dim)) * 0.5).astype(np.float32)
+        self.norm_w = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+        self.cos_sin = oi.rope_cos_sin(np.arange(spans) * 128, 64, 1.6e5)
+        self.state_slot = rng.permutation(num_seqs + 2)[:num_seqs].astype(np.int32)
+        self.st = oh.HcaState(self.pages, dim, num_seqs + 2)
+
+
+def _run_call(dev, case, rng, starts, counts, gpu):
+    D = case.dim
+    positions, token_seq, qsl = [], [], [0]
+    for b, (p0, n) in enumerate(zip(starts, counts)):
+        positions += list(range(p0, p0 + n))
+        token_seq += [b] * n
+        qsl.append(qsl[-1] + n)
+    positions = np.array(positions, np.int64)
+    token_seq = np.array(token_seq, np.int32)
+    qsl = np.array(qsl, np.int32)
+    T = len(positions)
+    latent = randn_bf16(rng, (T, D))
+    kv_score = randn_bf16(rng, (T, 2 * D))
+    slots = paged.slots_from_block_table(case.bt, token_seq, positions)
+    oh.hca_write(case.st, latent, kv_score, positions, token_seq, qsl, slots, case.ring_pages, case.ring,
+                 case.comp_bt, case.state_slot, case.ape, case.norm_w, 1e-6, case.cos_sin)
+    from ernie_kv import ops
+
+    d = lambda a: to_dev(a, dev)  # noqa: E731
+    kvs_t = bf16_tensor(kv_score, dev)
+    ops.hca_compress(kvs_t, d(positions), d(qsl), int(max(counts)), gpu["state"], d(case.state_slot),
+                     d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin), d(case.comp_bt), gpu["pool"])
+    ops.hca_append(bf16_tensor(latent, dev), kvs_t, d(slots), d(positions), d(token_seq), d(qsl), gpu["pool"],
+                   d(case.ring_pages), case.ring, gpu["state"], d(case.state_slot))
+
+
+@pytest.mark.parametrize("dim", [576, 512])
+def test_hca_write_path_exact(dev, dim):
+    rng = np.random.default_rng(dim)
+    case = HcaCase(rng, dim, num_seqs=3, max_pos=1400, ring=192)
+    gpu = {
+        "pool": torch.zeros((case.pages, paged.fp8_page_bytes(dim)), dtype=torch.uint8, device=dev),
+        "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
+    }
+    # chunked prefill, partial spans carried in the state ring, then MTP-style
+    # 3-token steps, a rollback re-append, and a long chunk.
+    calls = [
+        ([0, 0, 0], [300, 100, 128]),
+        ([300, 100, 128], [3, 200, 2]),
+        ([303, 300, 130], [3, 3, 3]),
+        ([304, 301, 131], [3, 3, 3]),  # rollback: re-append from one position back
+        ([307, 304, 134], [900, 1, 700]),
+    ]
+    for starts, counts in calls:
+        _run_call(dev, case, rng, starts, counts, gpu)
+        torch.cuda.synchronize()
+        assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool), f"pool mismatch after call {starts}"
+        got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
+        assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
+
+
+def test_hca_decode_indices(dev):
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(4)
+    case = HcaCase(rng, 576, num_seqs=4, max_pos=9000, ring=192)
+    positions = np.array([0, 126, 127, 128, 5000, 8999], np.int64)
+    req = np.array([0, 1, 2, 3, 1, 2], np.int32)
+    width = 9000 // 128 + 128
+    out = torch.full((6, width), -9, dtype=torch.int32, device=dev)
+    lens = torch.zeros(6, dtype=torch.int32, device=dev)
+    ops.hca_decode_indices(to_dev(positions, dev), to_dev(req, dev), to_dev(case.comp_bt, dev),
+                           to_dev(case.ring_pages, dev), case.ring, out, lens)
+    ref, rl = oh.hca_decode_indices(positions, req, case.comp_bt, case.ring_pages, case.ring, width)
+    assert np.array_equal(out.cpu().numpy(), ref)
+    assert np.array_equal(lens.cpu().numpy(), rl)

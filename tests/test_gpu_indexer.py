@@ -1,0 +1,156 @@
+"""GPU parity for the DSA read path's indexer: merge, Hadamard, q quant,
+exact scoring and exact top-k (all bit-exact against the oracle)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_tensor, bf16_values, permuted_block_table, randn_bf16, to_dev
+from oracle import indexer as oi
+from oracle import paged
+from oracle.fp8 import quantize_rows
+from oracle.merge import merge_swa_topk as merge_ref
+
+pytestmark = pytest.mark.gpu
+WINDOW, TOPK = 128, 2048
+
+
+def test_merge_swa_topk_known_answer(dev):
+    """Transcription of test_dsa_backend.py:18-37 (exact)."""
+    from ernie_kv import ops
+
+    positions = torch.tensor([0, 5, 127, 128, 200, 2175, 2176, 5000], device=dev)
+    num_tokens, width = positions.shape[0], TOPK + WINDOW
+    g = torch.Generator().manual_seed(0)
+    topk = torch.randint(0, 1 << 20, (num_tokens, TOPK), dtype=torch.int32, generator=g).to(dev)
+    out = torch.full((num_tokens, width), -7, dtype=torch.int32, device=dev)
+    ops.merge_swa_topk(topk, out, positions, WINDOW)
+    for row, pos in enumerate(positions.tolist()):
+        seq = pos + 1
+        n, w = min(max(seq - WINDOW, 0), TOPK), min(seq, WINDOW)
+        expected = torch.full((width,), -1, dtype=torch.int32)
+        expected[:n] = topk[row, :n].cpu()
+        expected[n : n + w] = torch.arange(seq - w, seq, dtype=torch.int32)
+        torch.testing.assert_close(out[row].cpu(), expected, rtol=0, atol=0)
+    ref = merge_ref(topk.cpu().numpy(), positions.cpu().numpy(), width, WINDOW)
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("num_rows", [1, 2, 5, 6, 7, 64, 129, 1026])
+def test_hadamard_rows_exact(dev, num_rows):
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(num_rows)
+    x = randn_bf16(rng, (num_rows, 128))
+    y = bf16_values(ops.hadamard_rows(bf16_tensor(x, dev)))
+    assert np.array_equal(y, oi.hadamard_rows(x))
+    h = oi.hadamard_matrix() / np.sqrt(128)
+    ref = x.astype(np.float64) @ h
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-2  # test_dsa_backend.py:73-89 bound
+
+
+@pytest.mark.parametrize("w_dtype", ["bf16", "fp32"])
+def test_indexer_q_quant_exact(dev, w_dtype):
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(3)
+    T, H = 5, 64
+    q = randn_bf16(rng, (T, H, 128), scale=2.0)
+    q[0, 0] = 0.0
+    w = randn_bf16(rng, (T, H)) if w_dtype == "bf16" else rng.standard_normal((T, H)).astype(np.float32)
+    wt = bf16_tensor(w, dev) if w_dtype == "bf16" else to_dev(w, dev)
+    q8, wf, dig = ops.indexer_q_quant(bf16_tensor(q, dev), wt)
+    codes, wref = oi.quantize_q(q, w)
+    assert np.array_equal(q8.cpu().numpy(), codes)
+    assert np.array_equal(wf.cpu().numpy().view(np.uint32), wref.view(np.uint32))
+    iq = oi.int_repr(codes)
+    d = dig.cpu().numpy().astype(np.int64)  # [T, 3, H, 128]
+    recon = d[:, 0] + 64 * d[:, 1] + 4096 * d[:, 2]
+    assert np.array_equal(recon, iq)
+    assert np.abs(d).max() <= 63
+
+
+def _indexer_setup(dev, rng, lengths, num_seqs=None, pages_per_seq=None, spikes=0.0):
+    T = len(lengths)
+    num_seqs = num_seqs or T
+    max_len = max(max(lengths), 1)
+    pages_per_seq = pages_per_seq or (max_len + 63) // 64 + 1
+    bt = permuted_block_table(rng, num_seqs, pages_per_seq)
+    kv_pages = num_seqs * pages_per_seq
+    kcache = np.zeros((kv_pages, paged.fp8_page_bytes(128)), np.uint8)
+    req = np.arange(T, dtype=np.int32) % num_seqs
+    spike_row = randn_bf16(rng, (128,), 3.0)
+    for b in range(num_seqs):
+        n = pages_per_seq * 64
+        k = randn_bf16(rng, (n, 128))
+        if spikes > 0:
+            m = rng.random(n) < spikes
+            k[m] = spike_row
+        s = np.arange(n)
+        slots = bt[b, s // 64] * 64 + s % 64
+        c, sc = quantize_rows(k)
+        paged.write_fp8_rows(kcache, slots, c, sc, 128)
+    q = randn_bf16(rng, (T, 64, 128))
+    w = randn_bf16(rng, (T, 64))
+    return dict(bt=bt, kcache=kcache, req=req, q=q, w=w, max_len=max_len)
+
+
+def test_indexer_scores_exact(dev):
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(7)
+    lengths = np.array([0, 1, 100, 777, 3000], np.int32)
+    st = _indexer_setup(dev, rng, lengths)
+    q8, wf, dig = ops.indexer_q_quant(bf16_tensor(st["q"], dev), bf16_tensor(st["w"], dev))
+    T = len(lengths)
+    scores = torch.full((T, st["max_len"]), -123.0, device=dev)
+    ops.indexer_score(dig, wf, to_dev(st["kcache"], dev), to_dev(st["bt"], dev), to_dev(st["req"], dev),
+                      to_dev(lengths, dev), st["max_len"], scores)
+    codes, wref = oi.quantize_q(st["q"], st["w"])
+    got = scores.cpu().numpy()
+    for t in range(T):
+        n = int(lengths[t])
+        s = np.arange(n)
+        slots = st["bt"][st["req"][t], s // 64] * 64 + s % 64
+        kc, ks = paged.read_fp8_rows(st["kcache"], slots, 128)
+        ref = oi.exact_scores(codes[t], wref[t], kc, ks)
+        assert np.array_equal(got[t, :n].view(np.uint32), ref.view(np.uint32)), f"row {t}"
+        assert np.all(got[t, n:] == -123.0)
+
+
+@pytest.mark.parametrize("n", [0, 1, 2047, 2048, 2049, 131072])
+def test_topk_select_spikes_and_ties(dev, n):
+    """Scores N(0,1) with 5% exactly +4.0 (more spikes than k), lowest index wins ties."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(n)
+    rows = 3
+    L = max(n, 1)
+    sc = rng.standard_normal((rows, L)).astype(np.float32)
+    sc[rng.random((rows, L)) < 0.05] = 4.0
+    sc[1] = 1.5  # all equal
+    sc[2, : L // 2] = -0.0  # signed zeros tie with +0
+    sc[2, L // 2 :] = 0.0
+    lengths = np.array([n, n, n], np.int32)
+    out = torch.full((rows, TOPK), -9, dtype=torch.int32, device=dev)
+    ops.topk_select(to_dev(sc, dev), to_dev(lengths, dev), TOPK, out)
+    got = out.cpu().numpy()
+    for r in range(rows):
+        ref = oi.topk_ascending((sc[r, :n] + np.float32(0.0)).astype(np.float32), TOPK)
+        assert np.array_equal(got[r], ref), f"row {r}"
+
+
+def test_indexer_topk_end_to_end(dev):
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(17)
+    lengths = np.array([0, 50, 2048, 2100, 9000, 20000], np.int32)
+    st = _indexer_setup(dev, rng, lengths, spikes=0.05)
+    q8, wf, dig = ops.indexer_q_quant(bf16_tensor(st["q"], dev), bf16_tensor(st["w"], dev))
+    T = len(lengths)
+    out = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    ops.indexer_topk(dig, wf, to_dev(st["kcache"], dev), to_dev(st["bt"], dev), to_dev(st["req"], dev),
+                     to_dev(lengths, dev), st["max_len"], out)
+    codes, wref = oi.quantize_q(st["q"], st["w"])
+    ref, _ = oi.indexer_topk(codes, wref, st["kcache"], st["bt"], st["req"], lengths, TOPK)
+    assert np.array_equal(out.cpu().numpy(), ref)

@@ -1,0 +1,415 @@
+// Write-side and small kernels of the ERNIE KV-cache path.
+//
+//  * kv_append_quant   latent / indexer-K append: bf16 row -> per-token UE8M0
+//                      fp8 row scattered by slot (values-then-scales pages),
+//                      optionally also into the window ring and the
+//                      compressor state ring (HCA layers).
+//  * merge_swa_topk    [topk[:n] | seq-w .. seq-1 | -1 ...] per row.
+//  * hadamard_rows     orthonormal Sylvester Walsh-Hadamard of 128-wide rows.
+//  * indexer_q_quant   per-(token, head) UE8M0 fp8 q, scale folded into the
+//                      head weights, plus the int8 digit planes of q used by
+//                      the exact scorer.
+//  * windowed_lengths  indexer candidate count max(pos + 1 - window, 0).
+//  * hca_decode_indices  [compressed slots | window ring slots | -1 ...].
+//
+// Built with -ffp-contract=off: the arithmetic is mirrored bit for bit by the
+// CPU oracle, so no multiply-add may be fused behind its back.
+#include "ekv_common.h"
+#include "ekv_internal.h"
+
+namespace ekv {
+
+// ---------------------------------------------------------------------------
+// kv_append_quant
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  const uint16_t* rows;      // [T, row_stride] bf16
+  int64_t row_stride;        // elements
+  int32_t num_tokens;
+  const int64_t* slot_mapping;  // [T], < 0 -> skip
+  uint8_t* cache;            // [num_pages, page_stride]
+  int64_t page_stride;
+  int64_t num_pages;
+  // HCA extras (all optional)
+  const int64_t* positions;  // [T]
+  const int32_t* token_seq;  // [T], < 0 -> padding
+  const int32_t* qsl;        // [B + 1]
+  const int32_t* ring_pages; // [B, ring_stride]
+  int32_t ring_stride;
+  int32_t ring;              // ring length R (multiple of 64)
+  const uint16_t* kv_score;  // [T, kvs_stride] bf16, 2*D wide
+  int64_t kvs_stride;
+  uint16_t* state;           // [num_state, 256, 2*D] bf16
+  const int32_t* state_slot; // [B]
+  int32_t num_state;
+};
+
+template <int D>
+__global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
+  constexpr int kRowsPerWave = (D == 128) ? 4 : 1;
+  constexpr int kLanes = 64 / kRowsPerWave;       // lanes per row
+  constexpr int kChunks = D / 8;                  // 16-byte bf16 chunks per row
+  constexpr int kPerLane = (kChunks + kLanes - 1) / kLanes;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / kLanes;                  // row within the wave
+  const int ln = lane % kLanes;                   // lane within the row
+  const int64_t t = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kRowsPerWave + sub;
+  if (t >= a.num_tokens) return;                  // whole row group exits together
+
+  const uint16_t* src = a.rows + t * a.row_stride;
+  float v[kPerLane][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kPerLane; ++k) {
+    const int c = ln + k * kLanes;
+    if (c < kChunks) {
+      uint4 w = *reinterpret_cast<const uint4*>(src + 8 * c);
+      uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[k][2 * i] = __uint_as_float(ww[i] << 16);
+        v[k][2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+        amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
+      }
+    }
+  }
+  amax = wave_max_xor(amax, kLanes);
+  const int e = ue8m0_exponent(amax);
+  const float inv = exp2i(-e);
+  const float scale = exp2i(e);
+
+  uint2 packed[kPerLane];
+#pragma unroll
+  for (int k = 0; k < kPerLane; ++k) {
+    uint32_t b0 = f32x2_to_fp8(v[k][0] * inv, v[k][1] * inv);
+    uint32_t b1 = f32x2_to_fp8(v[k][2] * inv, v[k][3] * inv);
+    uint32_t b2 = f32x2_to_fp8(v[k][4] * inv, v[k][5] * inv);
+    uint32_t b3 = f32x2_to_fp8(v[k][6] * inv, v[k][7] * inv);
+    packed[k] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+  }
+
+  auto store_row = [&](int64_t slot) {
+    if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
+    uint8_t* page = a.cache + (slot / kPageTokens) * a.page_stride;
+    const int64_t off = slot % kPageTokens;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const int c = ln + k * kLanes;
+      if (c < kChunks) *reinterpret_cast<uint2*>(page + off * D + 8 * c) = packed[k];
+    }
+    if (ln == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = scale;
+  };
+
+  store_row(a.slot_mapping[t]);
+
+  if (a.token_seq == nullptr) return;
+  const int b = a.token_seq[t];
+  if (b < 0) return;
+  const int t0 = a.qsl[b];
+  const int n = a.qsl[b + 1] - t0;
+  const int64_t p = a.positions[t];
+  const int64_t last = a.positions[t0] + n - 1;
+  if (a.ring_pages != nullptr && p > last - a.ring) {
+    const int64_t r = p % a.ring;
+    const int64_t slot =
+        static_cast<int64_t>(a.ring_pages[static_cast<int64_t>(b) * a.ring_stride + r / kPageTokens]) *
+            kPageTokens + r % kPageTokens;
+    store_row(slot);
+  }
+  if (a.state != nullptr && p > last - kStateRing) {
+    const int st = a.state_slot[b];
+    if (st >= 0 && st < a.num_state) {
+      const uint4* s = reinterpret_cast<const uint4*>(a.kv_score + t * a.kvs_stride);
+      uint4* d = reinterpret_cast<uint4*>(a.state + (static_cast<int64_t>(st) * kStateRing + p % kStateRing) * (2 * D));
+      for (int c = ln; c < 2 * kChunks; c += kLanes) d[c] = s[c];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// merge_swa_topk   (attention.py:582-641)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) merge_swa_topk_kernel(
+    const int32_t* topk, int64_t topk_stride, int32_t* out, int64_t out_stride,
+    const int64_t* positions, int32_t k, int32_t width, int32_t window) {
+  const int64_t row = blockIdx.x;
+  const int64_t seq = positions[row] + 1;
+  const int64_t n = min(max(seq - window, static_cast<int64_t>(0)), static_cast<int64_t>(k));
+  const int64_t w = min(seq, static_cast<int64_t>(window));
+  for (int c = threadIdx.x; c < width; c += blockDim.x) {
+    int64_t v;
+    if (c < n) v = topk[row * topk_stride + c];
+    else if (c < n + w) v = seq - w + (c - n);
+    else v = -1;
+    out[row * out_stride + c] = static_cast<int32_t>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// hadamard_rows: one wave per 128-wide row; lane l holds elements 2l, 2l+1.
+// Butterfly spans 1, 2, ..., 64 with (a, b) -> (a + b, a - b), then times
+// fl32(1/sqrt(128)), rounded to bf16.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) hadamard_rows_kernel(
+    const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride, int32_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(x + r * x_stride + 2 * lane);
+  float e0 = __uint_as_float(w << 16);
+  float e1 = __uint_as_float(w & 0xffff0000u);
+  float a0 = e0 + e1, a1 = e0 - e1;  // span 1, in-lane
+  e0 = a0; e1 = a1;
+#pragma unroll
+  for (int h = 2; h < 128; h <<= 1) {
+    const int m = h >> 1;  // partner lane offset
+    const float p0 = __shfl_xor(e0, m);
+    const float p1 = __shfl_xor(e1, m);
+    const bool lower = ((2 * lane) & h) == 0;
+    e0 = lower ? (e0 + p0) : (p0 - e0);
+    e1 = lower ? (e1 + p1) : (p1 - e1);
+  }
+  const float s = 0x1.6a09e6p-4f;  // fl32(1/sqrt(128))
+  const uint32_t o = static_cast<uint32_t>(f32_to_bf16(e0 * s)) |
+                     (static_cast<uint32_t>(f32_to_bf16(e1 * s)) << 16);
+  *reinterpret_cast<uint32_t*>(y + r * y_stride + 2 * lane) = o;
+}
+
+// ---------------------------------------------------------------------------
+// indexer_q_quant: one 16-lane group per (token, head) row of 128.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) indexer_q_quant_kernel(
+    const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const void* w,
+    int32_t w_is_bf16, int64_t w_stride, int32_t num_tokens, int32_t heads,
+    uint8_t* q_fp8, float* w_out, int8_t* q_digits) {
+  const int lane = threadIdx.x & 63;
+  const int ln = lane & 15;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  if (row >= static_cast<int64_t>(num_tokens) * heads) return;
+  const int64_t t = row / heads;
+  const int h = static_cast<int>(row % heads);
+  const uint16_t* src = q + t * q_tok_stride + h * q_head_stride;
+  uint4 wv = *reinterpret_cast<const uint4*>(src + 8 * ln);
+  uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  float v[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ww[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+    amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
+  }
+  amax = wave_max_xor(amax, 16);
+  const int e = ue8m0_exponent(amax);
+  const float inv = exp2i(-e);
+  uint32_t b0 = f32x2_to_fp8(v[0] * inv, v[1] * inv);
+  uint32_t b1 = f32x2_to_fp8(v[2] * inv, v[3] * inv);
+  uint32_t b2 = f32x2_to_fp8(v[4] * inv, v[5] * inv);
+  uint32_t b3 = f32x2_to_fp8(v[6] * inv, v[7] * inv);
+  uint32_t lo = b0 | (b1 << 16), hi = b2 | (b3 << 16);
+  *reinterpret_cast<uint2*>(q_fp8 + row * 128 + 8 * ln) = make_uint2(lo, hi);
+  if (q_digits != nullptr) {
+    // planes [t][digit][h][128]
+    uint32_t d[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t code = ((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu;
+      const uint32_t pk = fp8_digit_pack(code);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) d[p][i >> 2] |= ((pk >> (8 * p)) & 0xffu) << (8 * (i & 3));
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      int8_t* dst = q_digits + ((t * 3 + p) * heads + h) * 128 + 8 * ln;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(d[p][0], d[p][1]);
+    }
+  }
+  if (ln == 0) {
+    float wt = w_is_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(w)[t * w_stride + h])
+                         : static_cast<const float*>(w)[t * w_stride + h];
+    const float ws = 0x1.6a09e6p-7f;  // fl32(128**-0.5 * 64**-0.5)
+    w_out[t * heads + h] = (wt * exp2i(e)) * ws;
+  }
+}
+
+__global__ void fp8_digit_table_kernel(uint32_t* table) {
+  const int i = threadIdx.x;
+  if (i < 256) table[i] = fp8_digit_pack(static_cast<uint32_t>(i));
+}
+
+// ---------------------------------------------------------------------------
+// windowed_lengths and hca_decode_indices
+// ---------------------------------------------------------------------------
+__global__ void windowed_lengths_kernel(const int64_t* positions, int32_t n, int32_t window,
+                                        int32_t* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = static_cast<int32_t>(max(positions[i] + 1 - window, static_cast<int64_t>(0)));
+}
+
+__global__ void __launch_bounds__(256) hca_decode_indices_kernel(
+    const int64_t* positions, const int32_t* req_ids, const int32_t* comp_bt, int32_t comp_bt_stride,
+    const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window, int32_t* out,
+    int64_t out_stride, int32_t width, int32_t* lengths) {
+  const int64_t t = blockIdx.x;
+  const int64_t p = positions[t];
+  const int64_t b = req_ids[t];
+  const int64_t nc = (p + 1) / kSpan;
+  const int64_t w = min(p + 1, static_cast<int64_t>(window));
+  const int64_t len = min(nc + w, static_cast<int64_t>(width));
+  for (int c = threadIdx.x; c < width; c += blockDim.x) {
+    int64_t v = -1;
+    if (c < nc) {
+      v = static_cast<int64_t>(comp_bt[b * comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
+    } else if (c < len) {
+      const int64_t pos = p - w + 1 + (c - nc);
+      const int64_t r = pos % ring;
+      v = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
+    }
+    out[t * out_stride + c] = static_cast<int32_t>(v);
+  }
+  if (threadIdx.x == 0) lengths[t] = static_cast<int32_t>(len);
+}
+
+}  // namespace ekv
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace ekv;
+
+extern "C" int ekv_kv_append_quant(const uint16_t* rows, int64_t row_stride, int32_t num_tokens,
+                                   int32_t dim, const int64_t* slot_mapping, uint8_t* cache,
+                                   int64_t page_stride, int64_t num_pages, void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(rows && slot_mapping && cache, "null pointer");
+  EKV_CHECK(dim == 128 || dim == 512 || dim == 576, "dim must be 128, 512 or 576");
+  EKV_CHECK(row_stride >= dim && row_stride % 8 == 0, "row_stride must be >= dim and a multiple of 8");
+  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0,
+            "page_stride must hold 64 rows + 64 scales and be a multiple of 16");
+  EKV_CHECK(aligned16(rows) && aligned16(cache), "rows and cache must be 16-byte aligned");
+  AppendArgs a{};
+  a.rows = rows; a.row_stride = row_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
+  a.cache = cache; a.page_stride = page_stride; a.num_pages = num_pages;
+  const int rows_per_block = (dim == 128) ? 16 : 4;
+  dim3 grid((num_tokens + rows_per_block - 1) / rows_per_block);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dim == 128) hipLaunchKernelGGL(kv_append_quant_kernel<128>, grid, dim3(256), 0, s, a);
+  else if (dim == 512) hipLaunchKernelGGL(kv_append_quant_kernel<512>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(kv_append_quant_kernel<576>, grid, dim3(256), 0, s, a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_k_insert(const uint16_t* k, int64_t k_stride, int32_t num_tokens,
+                                    const int64_t* slot_mapping, uint8_t* kcache, int64_t page_stride,
+                                    int64_t num_pages, void* stream) {
+  return ekv_kv_append_quant(k, k_stride, num_tokens, 128, slot_mapping, kcache, page_stride,
+                             num_pages, stream);
+}
+
+extern "C" int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                              int64_t kvs_stride, int32_t num_tokens, int32_t dim,
+                              const int64_t* slot_mapping, const int64_t* positions,
+                              const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs,
+                              uint8_t* pool, int64_t page_stride, int64_t num_pages,
+                              const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
+                              uint16_t* state, const int32_t* state_slot, int32_t num_state,
+                              void* stream) {
+  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
+  EKV_CHECK(latent && slot_mapping && positions && token_seq && qsl && pool, "null pointer");
+  EKV_CHECK(latent_stride >= dim && latent_stride % 8 == 0, "bad latent_stride");
+  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(ring_pages == nullptr || (ring >= kWindow && ring % kPageTokens == 0 && ring_stride >= ring / kPageTokens),
+            "ring must be a multiple of 64, >= 128, with ring_stride >= ring/64");
+  EKV_CHECK(state == nullptr || (kv_score && state_slot && kvs_stride >= 2 * dim && kvs_stride % 8 == 0),
+            "state needs kv_score (stride >= 2*dim, multiple of 8) and state_slot");
+  EKV_CHECK(aligned16(latent) && aligned16(pool) && (state == nullptr || (aligned16(state) && aligned16(kv_score))),
+            "buffers must be 16-byte aligned");
+  AppendArgs a{};
+  a.rows = latent; a.row_stride = latent_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
+  a.cache = pool; a.page_stride = page_stride; a.num_pages = num_pages;
+  a.positions = positions; a.token_seq = token_seq; a.qsl = qsl;
+  a.ring_pages = ring_pages; a.ring_stride = ring_stride; a.ring = ring;
+  a.kv_score = kv_score; a.kvs_stride = kvs_stride; a.state = state; a.state_slot = state_slot;
+  a.num_state = num_state;
+  dim3 grid((num_tokens + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dim == 512) hipLaunchKernelGGL(kv_append_quant_kernel<512>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(kv_append_quant_kernel<576>, grid, dim3(256), 0, s, a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_merge_swa_topk(const int32_t* topk, int64_t topk_stride, int32_t* out,
+                                  int64_t out_stride, const int64_t* positions, int32_t num_tokens,
+                                  int32_t topk_width, int32_t out_width, int32_t window, void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(topk && out && positions, "null pointer");
+  EKV_CHECK(out_width >= topk_width + window, "width must be >= topk + window");
+  hipLaunchKernelGGL(merge_swa_topk_kernel, dim3(num_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     topk, topk_stride, out, out_stride, positions, topk_width, out_width, window);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_hadamard_rows(const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t y_stride,
+                                 int32_t rows, int32_t dim, void* stream) {
+  EKV_CHECK(rows >= 0, "rows must be >= 0");
+  if (rows == 0) return 0;
+  EKV_CHECK(dim == 128, "hadamard_rows supports 128-wide rows");
+  EKV_CHECK(x && y && x_stride >= 128 && y_stride >= 128 && x_stride % 2 == 0 && y_stride % 2 == 0,
+            "bad pointers or strides");
+  EKV_CHECK(aligned4(x) && aligned4(y), "rows must be 4-byte aligned");
+  hipLaunchKernelGGL(hadamard_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, x_stride, y, y_stride, rows);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_q_quant(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   const void* weights, int32_t weights_is_bf16, int64_t w_stride,
+                                   int32_t num_tokens, int32_t heads, uint8_t* q_fp8, float* w_out,
+                                   int8_t* q_digits, void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(q && weights && q_fp8 && w_out, "null pointer");
+  EKV_CHECK(heads > 0 && q_head_stride % 8 == 0 && q_tok_stride % 8 == 0, "strides must be multiples of 8");
+  EKV_CHECK(aligned16(q) && aligned8(q_fp8) && (q_digits == nullptr || aligned8(q_digits)), "misaligned buffers");
+  const int64_t rows = static_cast<int64_t>(num_tokens) * heads;
+  hipLaunchKernelGGL(indexer_q_quant_kernel, dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), q, q_tok_stride, q_head_stride, weights,
+                     weights_is_bf16, w_stride, num_tokens, heads, q_fp8, w_out, q_digits);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_windowed_lengths(const int64_t* positions, int32_t num_tokens, int32_t window,
+                                            int32_t* out, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && window >= 0, "bad sizes");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(positions && out, "null pointer");
+  hipLaunchKernelGGL(windowed_lengths_kernel, dim3((num_tokens + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), positions, num_tokens, window, out);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
+                                      const int32_t* comp_block_table, int32_t comp_bt_stride,
+                                      const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
+                                      int32_t window, int32_t* out, int64_t out_stride, int32_t width,
+                                      int32_t* lengths, void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(positions && req_ids && comp_block_table && ring_pages && out && lengths, "null pointer");
+  EKV_CHECK(ring >= window && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
+  hipLaunchKernelGGL(hca_decode_indices_kernel, dim3(num_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     positions, req_ids, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                     window, out, out_stride, width, lengths);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_fp8_digit_table(uint32_t* table, void* stream) {
+  EKV_CHECK(table != nullptr, "null pointer");
+  hipLaunchKernelGGL(fp8_digit_table_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), table);
+  return ekv_launch_status();
+}

@@ -1,0 +1,99 @@
+// Shared device helpers for the ERNIE KV-cache kernels (gfx950 / CDNA4).
+//
+// fp8 is OCP e4m3fn.  The hardware conversions used here were checked on the
+// device against the e4m3fn definition: v_cvt_pk_fp8_f32 rounds to nearest
+// even for |x| <= 448 (4M values incl. every midpoint), v_cvt_pk_f32_fp8
+// decodes all 256 codes exactly.  Every caller clamps to +-448 first.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ekv {
+
+constexpr int kPageTokens = 64;     // DSA_BLOCK_SIZE
+constexpr float kE4M3Max = 448.0f;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round to nearest even (inputs are finite).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Exponent e of the UE8M0 scale 2**e for a row amax:
+//   r = fl32(max(amax, 1e-10) * fl32(1/448));  e = ceil(log2(r)) taken exactly
+// from r's bits (r is always a normal float here).
+__device__ __forceinline__ int ue8m0_exponent(float amax) {
+  float r = fmaxf(amax, 0x1.b7cdfep-34f) * 0x1.24924ap-9f;  // fl32(1e-10), fl32(1/448)
+  uint32_t u = __float_as_uint(r);
+  int e = static_cast<int>((u >> 23) & 0xffu) - 127;
+  return (u & 0x7fffffu) ? e + 1 : e;
+}
+
+__device__ __forceinline__ float exp2i(int e) {  // 2**e for e in [-126, 127]
+  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// Two fp32 -> two e4m3fn bytes (low 16 bits), after clamping to +-448.
+__device__ __forceinline__ uint32_t f32x2_to_fp8(float a, float b) {
+  a = fminf(fmaxf(a, -kE4M3Max), kE4M3Max);
+  b = fminf(fmaxf(b, -kE4M3Max), kE4M3Max);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
+}
+
+// Four e4m3fn bytes packed in a word -> four floats.
+__device__ __forceinline__ f32x4 fp8x4_to_f32(uint32_t w) {
+  f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  return f32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// Four e4m3fn bytes -> four bf16 packed in two words (exact: every e4m3fn
+// value is a bf16 value, so the high half of its fp32 image is the bf16).
+__device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  lo = __builtin_amdgcn_perm(__float_as_uint(a[1]), __float_as_uint(a[0]), 0x07060302u);
+  hi = __builtin_amdgcn_perm(__float_as_uint(b[1]), __float_as_uint(b[0]), 0x07060302u);
+}
+
+// Order-preserving uint32 key of an fp32 score (larger score -> larger key).
+__device__ __forceinline__ uint32_t score_key(float s) {
+  uint32_t u = __float_as_uint(s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Signed base-64 digits of the integer I = value * 2**9 of an e4m3fn code
+// (|I| < 2**18): byte p of the result is digit p as two's complement int8,
+// so I = d0 + 64*d1 + 4096*d2 exactly.
+__device__ __forceinline__ uint32_t fp8_digit_pack(uint32_t code) {
+  const uint32_t ex = (code >> 3) & 15u, m = code & 7u;
+  uint32_t mag = ex ? ((8u + m) << (ex - 1)) : m;
+  if (ex == 15u && m == 7u) mag = 0;  // NaN code: never produced by the quantizer
+  const uint32_t d0 = mag & 63u, d1 = (mag >> 6) & 63u, d2 = mag >> 12;
+  if (code & 0x80u) {
+    return (static_cast<uint32_t>(-static_cast<int>(d0)) & 0xffu) |
+           ((static_cast<uint32_t>(-static_cast<int>(d1)) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(-static_cast<int>(d2)) & 0xffu) << 16);
+  }
+  return d0 | (d1 << 8) | (d2 << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max_xor(T v, int width) {
+  for (int m = width >> 1; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, width));
+  return v;
+}
+
+}  // namespace ekv

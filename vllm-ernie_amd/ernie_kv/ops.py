@@ -1,0 +1,316 @@
+"""Torch-facing wrappers of the C ABI (``include/ernie_kv.h``).
+
+Tensors are device memory and the current HIP stream is passed through; torch
+is plumbing here, every byte of the path is computed by the HIP library.  All
+outputs are caller-provided (written in place), as in the reference layers.
+Caches are ``uint8`` tensors ``[num_pages, page_stride_bytes]``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+PAGE_TOKENS = 64  # DSA_BLOCK_SIZE (attention.py:97-98)
+INDEX_HEAD_DIM = 128
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_dev(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("ERNIE KV ops take device tensors (no CPU path)")
+
+
+def fp8_page_bytes(dim: int) -> int:
+    return PAGE_TOKENS * (dim + 4)
+
+
+def _bits16(t: torch.Tensor) -> torch.Tensor:
+    _need(t.dtype == torch.bfloat16, f"expected bfloat16, got {t.dtype}")
+    return t
+
+
+# --------------------------------------------------------------------------- writes
+def kv_append_quant(rows: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
+    """Quantize bf16 rows ``[T, D]`` to fp8 + fp32 scale into ``cache`` slots."""
+    _check_dev(rows, slot_mapping, cache)
+    _bits16(rows)
+    T, D = rows.shape
+    _need(rows.stride(1) == 1, "rows must be row-contiguous")
+    _need(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= T, "slot_mapping int64 [T]")
+    _need(cache.dtype == torch.uint8 and cache.dim() == 2 and cache.stride(1) == 1, "cache uint8 [pages, bytes]")
+    _lib.call(
+        "ekv_kv_append_quant", rows.data_ptr(), rows.stride(0), T, D, slot_mapping.data_ptr(),
+        cache.data_ptr(), cache.stride(0), cache.shape[0], _stream(),
+    )
+
+
+def indexer_k_insert(k: torch.Tensor, slot_mapping: torch.Tensor, kcache: torch.Tensor) -> None:
+    """Indexer K rows ``[T, 128]`` bf16 -> 132-byte fp8 rows in ``kcache``."""
+    _check_dev(k, slot_mapping, kcache)
+    _bits16(k)
+    _need(k.shape[1] == INDEX_HEAD_DIM and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
+    _need(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
+    _lib.call(
+        "ekv_indexer_k_insert", k.data_ptr(), k.stride(0), k.shape[0], slot_mapping.data_ptr(),
+        kcache.data_ptr(), kcache.stride(0), kcache.shape[0], _stream(),
+    )
+
+
+def hca_compress(
+    kv_score: torch.Tensor,
+    positions: torch.Tensor,
+    qsl: torch.Tensor,
+    max_query_len: int,
+    state: torch.Tensor | None,
+    state_slot: torch.Tensor | None,
+    ape: torch.Tensor,
+    norm_w: torch.Tensor,
+    eps: float,
+    cos_sin: torch.Tensor,
+    comp_block_table: torch.Tensor,
+    pool: torch.Tensor,
+) -> None:
+    _check_dev(kv_score, positions, qsl, state, state_slot, ape, norm_w, cos_sin, comp_block_table, pool)
+    _bits16(kv_score)
+    D = ape.shape[1]
+    _need(kv_score.shape[1] >= 2 * D and kv_score.stride(1) == 1, "kv_score must be [T, 2D]")
+    _need(ape.shape == (128, D) and ape.dtype == torch.float32 and ape.is_contiguous(), "ape fp32 [128, D]")
+    _need(norm_w.shape == (D,) and norm_w.dtype == torch.float32, "norm_w fp32 [D]")
+    _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(), "cos_sin fp32 [S, 64]")
+    _need(comp_block_table.dtype == torch.int32 and comp_block_table.stride(1) == 1, "comp_block_table int32")
+    _need(positions.dtype == torch.int64 and qsl.dtype == torch.int32, "positions int64, qsl int32")
+    if state is not None:
+        _bits16(state)
+        _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
+    _lib.call(
+        "ekv_hca_compress", kv_score.data_ptr(), kv_score.stride(0), positions.data_ptr(), qsl.data_ptr(),
+        qsl.numel() - 1, int(max_query_len), D, _ptr(state), _ptr(state_slot),
+        0 if state is None else state.shape[0], ape.data_ptr(), norm_w.data_ptr(), float(eps),
+        cos_sin.data_ptr(), cos_sin.shape[0], comp_block_table.data_ptr(), comp_block_table.stride(0),
+        pool.data_ptr(), pool.stride(0), pool.shape[0], _stream(),
+    )
+
+
+def hca_append(
+    latent: torch.Tensor,
+    kv_score: torch.Tensor | None,
+    slot_mapping: torch.Tensor,
+    positions: torch.Tensor,
+    token_seq: torch.Tensor,
+    qsl: torch.Tensor,
+    pool: torch.Tensor,
+    ring_pages: torch.Tensor | None,
+    ring: int,
+    state: torch.Tensor | None,
+    state_slot: torch.Tensor | None,
+) -> None:
+    _check_dev(latent, kv_score, slot_mapping, positions, token_seq, qsl, pool, ring_pages, state, state_slot)
+    _bits16(latent)
+    T, D = latent.shape
+    _need(latent.stride(1) == 1, "latent must be row-contiguous")
+    _need(slot_mapping.dtype == torch.int64 and positions.dtype == torch.int64, "slot_mapping/positions int64")
+    _need(token_seq.dtype == torch.int32 and qsl.dtype == torch.int32, "token_seq/qsl int32")
+    if ring_pages is not None:
+        _need(ring_pages.dtype == torch.int32 and ring_pages.stride(1) == 1, "ring_pages int32 [B, R/64]")
+    _lib.call(
+        "ekv_hca_append", latent.data_ptr(), latent.stride(0), _ptr(kv_score),
+        0 if kv_score is None else kv_score.stride(0), T, D, slot_mapping.data_ptr(), positions.data_ptr(),
+        token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1, pool.data_ptr(), pool.stride(0), pool.shape[0],
+        _ptr(ring_pages), 0 if ring_pages is None else ring_pages.stride(0), int(ring), _ptr(state),
+        _ptr(state_slot), 0 if state is None else state.shape[0], _stream(),
+    )
+
+
+def hca_decode_indices(
+    positions: torch.Tensor,
+    req_ids: torch.Tensor,
+    comp_block_table: torch.Tensor,
+    ring_pages: torch.Tensor,
+    ring: int,
+    out: torch.Tensor,
+    lengths: torch.Tensor,
+    window: int = 128,
+) -> None:
+    _check_dev(positions, req_ids, comp_block_table, ring_pages, out, lengths)
+    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32 [T, W]")
+    _lib.call(
+        "ekv_hca_decode_indices", positions.data_ptr(), req_ids.data_ptr(), positions.numel(),
+        comp_block_table.data_ptr(), comp_block_table.stride(0), ring_pages.data_ptr(), ring_pages.stride(0),
+        int(ring), int(window), out.data_ptr(), out.stride(0), out.shape[1], lengths.data_ptr(), _stream(),
+    )
+
+
+# --------------------------------------------------------------------------- indexer
+def merge_swa_topk(topk_indices: torch.Tensor, out: torch.Tensor, positions: torch.Tensor, window: int) -> None:
+    """Reference signature and semantics (attention.py:606-641)."""
+    num_tokens = positions.shape[0]
+    if num_tokens == 0:
+        return
+    topk, width = topk_indices.shape[1], out.shape[1]
+    assert width >= topk + window
+    _check_dev(topk_indices, out, positions)
+    _need(topk_indices.dtype == torch.int32 and out.dtype == torch.int32, "int32 index buffers")
+    _need(topk_indices.stride(1) == 1 and out.stride(1) == 1, "rows must be contiguous")
+    pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
+    _lib.call(
+        "ekv_merge_swa_topk", topk_indices.data_ptr(), topk_indices.stride(0), out.data_ptr(), out.stride(0),
+        pos.data_ptr(), num_tokens, topk, width, int(window), _stream(),
+    )
+
+
+def hadamard_rows(x: torch.Tensor) -> torch.Tensor:
+    """Reference semantics of ``hadamard_rows`` (attention.py:102-108)."""
+    _check_dev(x)
+    _bits16(x)
+    _need(x.dim() == 2 and x.shape[1] == 128 and x.stride(1) == 1, "x must be [n, 128] row-contiguous")
+    y = torch.empty_like(x, memory_format=torch.contiguous_format)
+    _lib.call("ekv_hadamard_rows", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), x.shape[0], 128, _stream())
+    return y
+
+
+def indexer_q_quant(
+    q: torch.Tensor, weights: torch.Tensor, with_digits: bool = True
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """``q [T, H, 128]`` bf16 -> (q fp8 [T,H,128] uint8, folded weights fp32 [T,H],
+    int8 digit planes [T,3,H,128])."""
+    _check_dev(q, weights)
+    _bits16(q)
+    T, H, Dh = q.shape
+    _need(Dh == 128 and q.stride(2) == 1, "q must be [T, H, 128] with unit last stride")
+    _need(weights.shape[:2] == (T, H) and weights.stride(1) == 1, "weights [T, H]")
+    _need(weights.dtype in (torch.bfloat16, torch.float32), "weights bf16 or fp32")
+    q_fp8 = torch.empty((T, H, 128), dtype=torch.uint8, device=q.device)
+    w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
+    digits = torch.empty((T, 3, H, 128), dtype=torch.int8, device=q.device) if with_digits else None
+    _lib.call(
+        "ekv_indexer_q_quant", q.data_ptr(), q.stride(0), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), weights.stride(0), T, H, q_fp8.data_ptr(), w_out.data_ptr(),
+        _ptr(digits), _stream(),
+    )
+    return q_fp8, w_out, digits
+
+
+def indexer_windowed_lengths(positions: torch.Tensor, window: int, out: torch.Tensor) -> None:
+    _check_dev(positions, out)
+    _need(positions.dtype == torch.int64 and out.dtype == torch.int32, "positions int64, out int32")
+    _lib.call("ekv_indexer_windowed_lengths", positions.data_ptr(), positions.numel(), int(window), out.data_ptr(), _stream())
+
+
+def indexer_score(
+    q_digits: torch.Tensor,
+    w: torch.Tensor,
+    kcache: torch.Tensor,
+    block_table: torch.Tensor,
+    req_ids: torch.Tensor,
+    lengths: torch.Tensor,
+    max_len: int,
+    scores: torch.Tensor,
+) -> None:
+    _check_dev(q_digits, w, kcache, block_table, req_ids, lengths, scores)
+    T = q_digits.shape[0]
+    _need(q_digits.shape[1:] == (3, 64, 128) and q_digits.is_contiguous(), "q_digits [T, 3, 64, 128]")
+    _need(w.shape == (T, 64) and w.dtype == torch.float32 and w.is_contiguous(), "w fp32 [T, 64]")
+    _need(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table int32")
+    _need(scores.dtype == torch.float32 and scores.stride(1) == 1 and scores.shape[1] >= max_len, "scores")
+    _lib.call(
+        "ekv_indexer_score", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), kcache.stride(0),
+        kcache.shape[0], block_table.data_ptr(), block_table.stride(0), req_ids.data_ptr(), lengths.data_ptr(),
+        T, int(max_len), scores.data_ptr(), scores.stride(0), _stream(),
+    )
+
+
+def topk_select(scores: torch.Tensor, lengths: torch.Tensor, k: int, out: torch.Tensor) -> None:
+    _check_dev(scores, lengths, out)
+    _need(scores.dtype == torch.float32 and scores.stride(1) == 1, "scores fp32 rows")
+    _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[1] >= k, "out int32 [T, >=k]")
+    _lib.call(
+        "ekv_topk_select", scores.data_ptr(), scores.stride(0), lengths.data_ptr(), scores.shape[0],
+        scores.shape[1], out.data_ptr(), out.stride(0), int(k), _stream(),
+    )
+
+
+def indexer_topk(
+    q_digits: torch.Tensor,
+    w: torch.Tensor,
+    kcache: torch.Tensor,
+    block_table: torch.Tensor,
+    req_ids: torch.Tensor,
+    lengths: torch.Tensor,
+    max_len: int,
+    topk_out: torch.Tensor,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Exact scores over ``s < lengths[t]`` and top-k (ascending, -1 padded)."""
+    _check_dev(q_digits, w, kcache, block_table, req_ids, lengths, topk_out)
+    T = q_digits.shape[0]
+    _need(q_digits.shape[1:] == (3, 64, 128) and q_digits.is_contiguous(), "q_digits [T, 3, 64, 128]")
+    _need(w.shape == (T, 64) and w.dtype == torch.float32 and w.is_contiguous(), "w fp32 [T, 64]")
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    need = _lib.load().ekv_indexer_topk_workspace_size(T, int(max_len))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q_digits.device)
+    _lib.call(
+        "ekv_indexer_topk", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), kcache.stride(0),
+        kcache.shape[0], block_table.data_ptr(), block_table.stride(0), req_ids.data_ptr(), lengths.data_ptr(),
+        T, int(max_len), topk_out.data_ptr(), topk_out.stride(0), topk_out.shape[1], workspace.data_ptr(),
+        workspace.numel(), _stream(),
+    )
+
+
+# --------------------------------------------------------------------------- decode
+def sparse_mla_decode(
+    q: torch.Tensor,
+    cache: torch.Tensor,
+    indices: torch.Tensor,
+    scale: float,
+    out: torch.Tensor,
+    lse: torch.Tensor | None = None,
+    sinks: torch.Tensor | None = None,
+    lengths: torch.Tensor | None = None,
+    block_table: torch.Tensor | None = None,
+    req_ids: torch.Tensor | None = None,
+    cache_bf16: bool = False,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Sparse MLA decode (attention.py:701-790): q [T, H, D] bf16 -> out [T, H, 512]."""
+    _check_dev(q, cache, indices, out, lse, sinks, lengths, block_table, req_ids)
+    _bits16(q)
+    T, H, D = q.shape
+    _need(q.stride(2) == 1, "q last dim must be contiguous")
+    _need(indices.dtype == torch.int32 and indices.stride(-1) == 1, "indices int32 [T, W]")
+    idx = indices.reshape(T, -1) if indices.dim() != 2 else indices
+    _need(out.dtype == torch.bfloat16 and out.shape[0] == T and out.shape[1] >= H and out.shape[2] == 512, "out bf16 [T, H, 512]")
+    if cache_bf16:
+        _need(cache.dtype == torch.bfloat16, "bf16 cache expected")
+        num_pages = cache.numel() // (PAGE_TOKENS * D)
+        page_stride = PAGE_TOKENS * D * 2
+    else:
+        _need(cache.dtype == torch.uint8 and cache.dim() == 2, "fp8 cache must be uint8 [pages, bytes]")
+        num_pages, page_stride = cache.shape[0], cache.stride(0)
+    if sinks is not None:
+        _need(sinks.dtype == torch.float32 and sinks.numel() >= H, "sinks fp32 [H]")
+    need = _lib.load().ekv_sparse_mla_decode_workspace_size(T, H, idx.shape[1])
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _lib.call(
+        "ekv_sparse_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), T, H, D, cache.data_ptr(),
+        int(cache_bf16), page_stride, num_pages, idx.data_ptr(), idx.stride(0), idx.shape[1], _ptr(lengths),
+        _ptr(block_table), 0 if block_table is None else block_table.stride(0), _ptr(req_ids), _ptr(sinks),
+        float(scale), out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse),
+        0 if lse is None else lse.stride(0), workspace.data_ptr(), workspace.numel(), _stream(),
+    )
