@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X ERNIE 5.5 attention KV-cache path.
+
+Default workload (the headline): one decode step of a DSA layer at batch 32 x
+131,072-token context -- append the new token's latent (fp8) and indexer key,
+quantize the indexer queries, score every non-window token exactly, select the
+top-2048 (lowest index on ties), append the 128-token window, gather the 2176
+rows and run 64-head sparse MLA decode with a sink.  Inputs are synthetic
+(seeded) and resident in HBM before the timed region.
+
+Prints ONE JSON line.  ``value`` = algorithmic HBM bytes per step / step time
+(GB/s), the metric's unit; ``tok_per_s`` = decode tokens per second.
+Algorithmic bytes per step: indexer K rows 132 B x sum of windowed lengths,
+gathered latent rows 580 B x 2176 per row, plus q / out tensors.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "vllm-ernie_amd"))
+
+METRIC = "KV gather+decode HBM GB/s (% of 8 TB/s); decode tok/s/GPU at 128K ctx"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--ctx", type=int, default=131072)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
+    """Synthetic DSA-layer decode state at batch B x context ctx."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pages_per_seq = ctx // 64
+    num_pages = B * pages_per_seq
+    block_table = torch.randperm(num_pages, device=dev, generator=g).to(torch.int32).view(B, pages_per_seq)
+
+    def random_fp8_pages(dim: int, scale_exp: int):
+        pages = torch.randint(0, 256, (num_pages, 64 * dim), device=dev, dtype=torch.uint8, generator=g)
+        pages -= ((pages & 0x7F) == 0x7F).to(torch.uint8)  # no NaN codes (0x7f/0xff -> 0x7e/0xfe)
+        scales = torch.full((num_pages, 64), 2.0 ** scale_exp, device=dev, dtype=torch.float32)
+        return torch.cat([pages, scales.view(torch.uint8)], dim=1).contiguous()
+
+    kcache = random_fp8_pages(128, -8)
+    # 5% of tokens hold one identical "spike" key row: exact score ties
+    spike = kcache[0, :128].clone()
+    mask = torch.rand(num_pages, 64, device=dev, generator=g) < 0.05
+    vals = kcache[:, : 64 * 128].unflatten(1, (64, 128))
+    vals[mask] = spike
+    latent = random_fp8_pages(576, -8)
+    positions = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
+    req_ids = torch.arange(B, dtype=torch.int32, device=dev)
+    pos = positions
+    slots = (block_table[torch.arange(B, device=dev), (pos // 64)].to(torch.int64) * 64 + pos % 64).contiguous()
+    rnd = lambda *s: torch.randn(*s, device=dev, generator=g).to(torch.bfloat16)  # noqa: E731
+    st = dict(
+        B=B, ctx=ctx, block_table=block_table, kcache=kcache, latent=latent, positions=positions,
+        req_ids=req_ids, slots=slots, k_new=rnd(B, 128), latent_new=rnd(B, 576), q_idx=rnd(B, 64, 128),
+        w_idx=rnd(B, 64), q=rnd(B, 64, 576), sinks=torch.randn(64, device=dev, generator=g),
+        lengths=torch.empty(B, dtype=torch.int32, device=dev),
+        scores=torch.empty((B, ctx), dtype=torch.float32, device=dev),
+        topk=torch.empty((B, 2048), dtype=torch.int32, device=dev),
+        merged=torch.empty((B, 2176), dtype=torch.int32, device=dev),
+        out=torch.empty((B, 64, 512), dtype=torch.bfloat16, device=dev),
+        lse=torch.empty((B, 64), dtype=torch.float32, device=dev),
+    )
+    need = ops._lib.load().ekv_sparse_mla_decode_workspace_size(B, 64, 2176)
+    st["dec_ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
+    return st
+
+
+def dsa_step(ops, st, ev=None):
+    """One DSA decode step; ``ev`` = (start, end) events around the scorer."""
+    ops.indexer_k_insert(st["k_new"], st["slots"], st["kcache"])
+    ops.kv_append_quant(st["latent_new"], st["slots"], st["latent"])
+    _, w, digits = ops.indexer_q_quant(st["q_idx"], st["w_idx"])
+    ops.indexer_windowed_lengths(st["positions"], 128, st["lengths"])
+    if ev is not None:
+        ev[0].record()
+    ops.indexer_score(digits, w, st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"],
+                      st["scores"])
+    if ev is not None:
+        ev[1].record()
+    ops.topk_select(st["scores"], st["lengths"], 2048, st["topk"])
+    ops.merge_swa_topk(st["topk"], st["merged"], st["positions"], 128)
+    ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
+                          block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
+
+
+def dsa_bytes(B: int, ctx: int) -> dict:
+    n = max(ctx - 128, 0)
+    k_read = B * n * 132
+    gather = B * (min(n, 2048) + min(ctx, 128)) * 580
+    qo = B * 64 * 576 * 2 + B * 64 * 512 * 2 + B * 64 * 128 * 2 + B * 64 * 2 + B * 64 * 4
+    return {"indexer_k": k_read, "gather": gather, "q_out": qo, "total": k_read + gather + qo}
+
+
+def cpu_baseline(B: int, ctx: int, seed: int) -> dict:
+    """Oracle (numpy, this build's CPU restatement) on a bounded sample: one
+    query row of the same workload (scoring all its tokens, top-2048, decode)."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import decode as od
+    from oracle import indexer as oi
+    from oracle.fp8 import bf16_round
+
+    rng = np.random.default_rng(seed)
+    n = max(ctx - 128, 0)
+    codes = rng.integers(0, 256, (n, 128)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] ^= 1
+    kscale = np.full(n, 2.0 ** -8, np.float32)
+    q = bf16_round(rng.standard_normal((64, 128)).astype(np.float32))
+    w = bf16_round(rng.standard_normal(64).astype(np.float32))
+    qc, wf = oi.quantize_q(q[None], w[None])
+    lat_codes = rng.integers(0, 256, (2176, 576)).astype(np.uint8)
+    lat_codes[(lat_codes & 0x7F) == 0x7F] ^= 1
+    from oracle.fp8 import decode_e4m3
+
+    rows = decode_e4m3(lat_codes).astype(np.float64) * 2.0 ** -8
+    qm = bf16_round(rng.standard_normal((1, 64, 576)).astype(np.float32))
+    sinks = rng.standard_normal(64).astype(np.float32)
+    t0 = time.perf_counter()
+    sc = oi.exact_scores(qc[0], wf[0], codes, kscale)
+    top = oi.topk_ascending(sc, 2048)
+    idx = np.concatenate([np.arange(2176)])[None].astype(np.int32)
+    od.sparse_mla_decode(qm, lambda s: rows[s], idx, 256 ** -0.5, 512, sinks)
+    dt = time.perf_counter() - t0
+    row_bytes = dsa_bytes(1, ctx)["total"]
+    return {
+        "value": round(row_bytes / dt / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"1 query row of the same step (ctx {ctx}: exact scores of {n} keys, top-2048, "
+                  f"64-head decode over 2176 rows); numpy oracle, {dt:.2f} s; {1.0 / dt:.4f} tok/s",
+        "tok_per_s": round(1.0 / dt, 5),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU (one DP rank's share of the attention "
+                                   "work); --gpus must be 1", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from ernie_kv import ops
+
+    torch.cuda.init()
+    st = build_dsa_decode(torch, ops, args.batch, args.ctx, args.seed)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        dsa_step(ops, st)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(args.steps):
+        dsa_step(ops, st, evs[i])
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+    score_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    by = dsa_bytes(args.batch, args.ctx)
+    gbs = by["total"] / (ms_step * 1e-3) / 1e9
+    n = max(args.ctx - 128, 0)
+    score_ops = args.batch * n * 64 * 128 * 2 * 9  # int8 digit-pair ops
+    score_gbs = by["indexer_k"] / (score_ms * 1e-3) / 1e9
+    score_tops = score_ops / (score_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "tok_per_s": round(args.batch / (ms_step * 1e-3), 1),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"dsa_decode_b{args.batch}_ctx{args.ctx}",
+            "batch": args.batch, "ctx": args.ctx, "index_topk": 2048, "window": 128, "heads": 64,
+            "latent_dim": 576, "indexer": "64x128 fp8", "kv_cache": "fp8 e4m3 + fp32 per-token scale",
+            "bytes_per_step": by,
+        },
+        "roofline": {
+            "kernel": "score_exact_kernel (exact indexer scoring, int8 digit-pair MFMA)",
+            "bound": "mfma",
+            "achieved": round(score_tops, 2),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s (int8)",
+            "frac": round(score_tops / INT8_PEAK_TOPS, 4),
+            "traffic": None,
+            "ms": round(score_ms, 4),
+            "hbm_gbs": round(score_gbs, 1),
+            "hbm_frac": round(score_gbs / HBM_PEAK_GBS, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.batch, args.ctx, args.seed)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+"""Host-side checks (CPU): the C-ABI library loads and exports every symbol
+the header declares; the ctypes signatures agree with the header; the
+reference-interface mirror behaves like the reference's host logic."""
+
+import re
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ernie_kv.h"
+
+
+def _header_functions() -> dict[str, int]:
+    """name -> number of parameters, parsed from include/ernie_kv.h."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(ekv_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_library_exports_every_header_symbol():
+    import ctypes
+
+    from ernie_kv import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libernie_kv.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _header_functions():
+        assert hasattr(lib, name), f"{name} declared in ernie_kv.h but not exported"
+
+
+def test_ctypes_signatures_match_header():
+    from ernie_kv import _lib
+
+    decl = _header_functions()
+    assert set(decl) == set(_lib.exported_symbols())
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == decl[name], f"{name}: {len(args)} ctypes args vs {decl[name]} in header"
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from ernie_kv import _lib
+
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.EkvError, match="no CPU fallback"):
+        _lib.load()
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+
+    from ernie_kv import ops
+
+    with pytest.raises(ValueError, match="device tensors"):
+        ops.kv_append_quant(torch.zeros(1, 576, dtype=torch.bfloat16), torch.zeros(1, dtype=torch.int64),
+                            torch.zeros(1, 64 * 580, dtype=torch.uint8))
+
+
+def test_packed_block_stride_alignment():
+    """test_dsa_backend.py:40-55."""
+    from ernie_kv.attention import packed_block_stride_alignment, simple_vllm_config
+
+    a = packed_block_stride_alignment(simple_vllm_config())
+    assert a % 512 == 0 and a % (512 * 2) == 0 and a % ((512 + 64) * 2) == 0
+
+
+@pytest.mark.parametrize("spec", [None, SimpleNamespace()])
+def test_dsa_kernel_block_sizes_accept_kv_cache_spec(spec):
+    """test_dsa_backend.py:58-70."""
+    from ernie_kv.attention import Ernie5_5FlashMLASparseBackend, Ernie5_5IndexerBackend, MultipleOf
+
+    for backend in (Ernie5_5FlashMLASparseBackend, Ernie5_5IndexerBackend):
+        assert backend.get_supported_kernel_block_sizes() == [MultipleOf(64)]
+        assert backend.get_supported_kernel_block_sizes(spec) == [MultipleOf(64)]
+
+
+def test_backend_surface():
+    from ernie_kv import attention as A
+
+    assert A.Ernie5_5FlashMLASparseBackend.supports_sink()
+    assert A.Ernie5_5FlashMLASparseBackend.get_impl_cls() is A.Ernie5_5FlashMLASparseImpl
+    assert A.Ernie5_5FlashMLASparseBackend.get_name() == "FLASHMLA_SPARSE"
+    assert A.Ernie5_5IndexerBackend.supported_kv_cache_layouts() == (A.KVCacheLayout.BLNHC, A.KVCacheLayout.BLHNC)
+    assert A.Ernie5_5IndexerBackend.get_builder_cls() is A.Ernie5_5IndexerMetadataBuilder
+    assert A.select_ernie5_5_hca_cls("fp8_ds_mla") is A.Ernie5_5HCAFlashMLAAttention
+    assert A.select_ernie5_5_hca_cls("auto") is A.Ernie5_5HCAFlashInferAttention
+
+
+def test_kv_cache_specs_use_dsa_pages():
+    from ernie_kv import attention as A
+
+    cfg = A.simple_vllm_config(block_size=256)
+    spec = A.Ernie5_5MLAAttention().get_kv_cache_spec(cfg)
+    assert spec.block_size == 64 and spec.block_stride_alignment == 9216
+    ic = A.Ernie5_5IndexerCache(head_dim=132, dtype="uint8", prefix="model.layers.0.indexer.k_cache")
+    s2 = ic.get_kv_cache_spec(cfg)
+    assert s2.block_size == 64 and s2.head_size == 132 and ic.get_attn_backend() is A.Ernie5_5IndexerBackend
+
+
+def test_padded_sinks_are_noop_minus_inf():
+    import torch
+
+    from ernie_kv.attention import Ernie5_5FlashMLASparseImpl
+
+    impl = Ernie5_5FlashMLASparseImpl(num_heads=16, head_size=576, scale=0.0625, sinks=torch.arange(16.0))
+    p = impl._padded_sinks(64)
+    assert torch.equal(p[:16], torch.arange(16.0)) and torch.all(torch.isneginf(p[16:]))
+    assert impl._padded_sinks(16) is impl.sinks
+
+
+def test_attn_tp_and_sink_backend_errors():
+    from ernie_kv.attention import _check_attn_tp, _check_sink_backend
+
+    cfg = SimpleNamespace(o_groups=8, num_attention_heads=64, hybrid_mla_num_attention_heads=64)
+    _check_attn_tp(cfg, 8)
+    with pytest.raises(ValueError, match="must divide"):
+        _check_attn_tp(cfg, 3)
+    with pytest.raises(RuntimeError, match="sink-capable"):
+        _check_sink_backend(384, "fp8")

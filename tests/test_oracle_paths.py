@@ -1,0 +1,305 @@
+"""Pins of the oracle's path functions (CPU): page geometry, merge, indexer,
+compressor and decode, against reference known-answer tests, closed forms,
+library routines and brute force."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+from oracle import hca as oh
+from oracle import indexer as oi
+from oracle import paged
+from oracle.fp8 import bf16_round, decode_e4m3, quantize_rows
+from oracle.merge import logical_to_global, merge_swa_topk
+
+WINDOW, TOPK = 128, 2048
+
+
+# ---------------------------------------------------------------- geometry
+def test_packed_block_stride_alignment_closed_form():
+    """test_dsa_backend.py:40-55 and attention.py:561-571."""
+    a = math.lcm(512, 512 * 2, (512 + 64) * 2)
+    assert a == 9216 and a % 512 == 0 and a % 1024 == 0 and a % 1152 == 0
+
+
+def test_indexer_page_layout_values_then_scales():
+    """Layout analog of test_indexer_fp4.py:71-90 for 132-byte fp8 rows:
+    values at slot*128, scales at 64*128 + slot*4 of a page filled with 173."""
+    rng = np.random.default_rng(0)
+    k = bf16_round(rng.standard_normal((2, 128)).astype(np.float32))
+    cache = np.full((1, 64 * 132), 173, np.uint8)
+    oi.k_insert(cache, k, np.array([0, 1]))
+    codes, scale = quantize_rows(k)
+    assert np.array_equal(cache[0, :256].reshape(2, 128), codes)
+    assert np.array_equal(cache[0, 8192:8200].view(np.float32), scale)
+    assert np.all(cache[0, 256:8192] == 173) and np.all(cache[0, 8200:] == 173)
+
+
+def test_slot_math_brute_force():
+    rng = np.random.default_rng(1)
+    bt = rng.permutation(40).astype(np.int32).reshape(4, 10)
+    seq = rng.integers(0, 4, 500)
+    pos = rng.integers(0, 640, 500)
+    slots = paged.slots_from_block_table(bt, seq, pos)
+    for s, p, sl in zip(seq, pos, slots):
+        assert sl == bt[s][p // 64] * 64 + p % 64
+    # logical->global keeps -1
+    idx = np.array([[0, 63, 64, -1, 639]], np.int32)
+    g = logical_to_global(idx, np.array([2]), bt)
+    assert g[0, 3] == -1 and g[0, 2] == bt[2, 1] * 64 and g[0, 4] == bt[2, 9] * 64 + 63
+
+
+def test_negative_slots_skipped():
+    cache = np.zeros((1, paged.fp8_page_bytes(128)), np.uint8)
+    paged.write_fp8_rows(cache, [-1], np.ones((1, 128), np.uint8), np.ones(1, np.float32), 128)
+    assert not cache.any()
+
+
+# ---------------------------------------------------------------- merge
+def test_merge_swa_topk_known_answer():
+    """Transcription of test_dsa_backend.py:18-37."""
+    positions = np.array([0, 5, 127, 128, 200, 2175, 2176, 5000])
+    rng = np.random.default_rng(0)
+    topk = rng.integers(0, 1 << 20, (len(positions), TOPK)).astype(np.int32)
+    width = TOPK + WINDOW
+    out = merge_swa_topk(topk, positions, width, WINDOW)
+    for row, pos in enumerate(positions):
+        seq = pos + 1
+        n, w = min(max(seq - WINDOW, 0), TOPK), min(seq, WINDOW)
+        exp = np.full(width, -1, np.int32)
+        exp[:n] = topk[row, :n]
+        exp[n : n + w] = np.arange(seq - w, seq)
+        assert np.array_equal(out[row], exp)
+
+
+# ---------------------------------------------------------------- indexer prep
+@pytest.mark.parametrize("num_rows", [1, 2, 5, 6, 7, 64, 129, 1026])
+def test_hadamard_matches_dense(num_rows):
+    """test_dsa_backend.py:73-89 bound, and exact orthonormality in fp64."""
+    rng = np.random.default_rng(num_rows)
+    x = bf16_round(rng.standard_normal((num_rows, 128)).astype(np.float32))
+    h = oi.hadamard_matrix() / math.sqrt(128)
+    ref = x.astype(np.float64) @ h
+    out = oi.hadamard_rows(x)
+    assert np.linalg.norm(out - ref) / np.linalg.norm(ref) < 1e-2
+    assert np.allclose(h @ h.T, np.eye(128))
+
+
+def test_partial_rope_split_cat_bit_exact():
+    """test_indexer_rope.py:14-48: rotating dims 0..63 of the full head equals
+    rotating the split part and concatenating; dims 64..127 untouched."""
+    rng = np.random.default_rng(3)
+    T, H = 7, 64
+    pos = rng.integers(0, 65536, T)
+    cs = oi.rope_cos_sin(pos, 64, 8e6)
+    q = bf16_round(rng.standard_normal((T, H, 128)).astype(np.float32))
+    full = oi.neox_partial_rope(q, cs[:, None, :], 64)
+    part = oi.neox_partial_rope(q[..., :64], cs[:, None, :], 64)
+    assert np.array_equal(full, np.concatenate([part, q[..., 64:]], -1))
+    # rotation preserves the pair norm up to bf16 rounding
+    n0 = np.hypot(q[..., :32], q[..., 32:64])
+    n1 = np.hypot(full[..., :32], full[..., 32:64])
+    assert np.allclose(n0, n1, rtol=2e-2, atol=1e-2)
+
+
+def test_q_quant_weight_fold():
+    """attention.py:925, 980: w * q_scale * 128**-0.5 * 64**-0.5."""
+    rng = np.random.default_rng(4)
+    q = bf16_round(rng.standard_normal((3, 64, 128)).astype(np.float32) * 5)
+    w = bf16_round(rng.standard_normal((3, 64)).astype(np.float32))
+    codes, folded = oi.quantize_q(q, w)
+    _, qs = quantize_rows(q)
+    np.testing.assert_allclose(folded, w * qs / (8 * math.sqrt(128)), rtol=1e-6)
+
+
+# ---------------------------------------------------------------- scoring / top-k
+def test_exact_dot_equals_fp64_dot():
+    """The int representation is exact: int64 dot == fp64 dot of decoded values."""
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 256, (500, 128)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    q = rng.integers(0, 256, (64, 128)).astype(np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0
+    d_int = oi.int_repr(codes) @ oi.int_repr(q).T
+    d_f64 = decode_e4m3(codes).astype(np.float64) @ decode_e4m3(q).astype(np.float64).T
+    assert np.array_equal(d_int.astype(np.float64) * 2.0 ** -18, d_f64)
+
+
+def test_scores_match_fp64_formula():
+    rng = np.random.default_rng(6)
+    k = bf16_round(rng.standard_normal((300, 128)).astype(np.float32))
+    kc, ks = quantize_rows(k)
+    q = bf16_round(rng.standard_normal((64, 128)).astype(np.float32))
+    w = rng.standard_normal(64).astype(np.float32)
+    qc, wf = oi.quantize_q(q[None], w[None])
+    s = oi.exact_scores(qc[0], wf[0], kc, ks)
+    kv = decode_e4m3(kc).astype(np.float64) * ks[:, None]
+    qv = decode_e4m3(qc[0]).astype(np.float64)
+    ref = (np.maximum(kv @ qv.T, 0) * wf[0].astype(np.float64)).sum(1)
+    np.testing.assert_allclose(s, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+
+
+def test_head_sum_order_is_pinned():
+    """A planted mistake: summing heads in natural order differs from the
+    kernel order on some inputs, so the pin is not vacuous."""
+    rng = np.random.default_rng(7)
+    p = (rng.standard_normal((2000, 64)) * np.exp2(rng.integers(-20, 20, (2000, 64)))).astype(np.float32)
+    pinned = oi.head_sum_pinned(p)
+    natural = np.zeros(2000, np.float32)
+    for h in range(64):
+        natural = (natural + p[:, h]).astype(np.float32)
+    assert np.any(pinned != natural)
+    np.testing.assert_allclose(pinned, p.astype(np.float64).sum(1), rtol=1e-4, atol=1e-3 * np.abs(p).max())
+
+
+@pytest.mark.parametrize("n", [0, 5, 2048, 2049, 40000])
+def test_topk_reduces_to_stable_sort(n):
+    rng = np.random.default_rng(n)
+    s = rng.standard_normal(n).astype(np.float32)
+    s[rng.random(n) < 0.05] = 4.0
+    got = oi.topk_ascending(s, TOPK)
+    if n:
+        order = torch.sort(-torch.from_numpy(s), stable=True).indices[: min(n, TOPK)].numpy()
+        exp = np.sort(order)
+    else:
+        exp = np.zeros(0, np.int64)
+    assert np.array_equal(got[: len(exp)], exp) and np.all(got[len(exp) :] == -1)
+
+
+def test_topk_special_cases():
+    assert np.array_equal(oi.topk_ascending(np.full(5000, 1.5, np.float32), TOPK), np.arange(TOPK))
+    s = np.zeros(3000, np.float32)
+    s[:1500] = -0.0
+    assert np.array_equal(oi.topk_ascending(s + np.float32(0.0), TOPK), np.arange(TOPK))
+
+
+def test_windowed_lengths():
+    assert list(oi.windowed_lengths(np.array([0, 127, 128, 200]), 128)) == [0, 0, 1, 73]
+
+
+# ---------------------------------------------------------------- compressor
+def _span(rng, D=576):
+    kv = bf16_round(rng.standard_normal((128, D)).astype(np.float32))
+    sc = bf16_round(rng.standard_normal((128, D)).astype(np.float32))
+    return kv, sc
+
+
+def _fp64_compress(kv, score, ape, w, eps, cs):
+    g = score.astype(np.float64) + ape
+    p = np.exp(g - g.max(0))
+    p /= p.sum(0)
+    x = (p * kv).sum(0)
+    y = x / np.sqrt((x * x).mean() + eps) * w
+    D = len(y)
+    x0, x1 = y[D - 64 :: 2].copy(), y[D - 63 :: 2].copy()
+    y[D - 64 :: 2] = x0 * cs[:32] - x1 * cs[32:]
+    y[D - 63 :: 2] = x0 * cs[32:] + x1 * cs[:32]
+    return y
+
+
+def test_compressor_fp64_brute_force():
+    rng = np.random.default_rng(8)
+    kv, sc = _span(rng)
+    ape = (rng.standard_normal((128, 576)) * 0.5).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(576)).astype(np.float32)
+    cs = oi.rope_cos_sin(np.array([128 * 7]), 64, 1.6e5)[0]
+    got = oh.compress_span(kv, sc, ape, w, 1e-6, cs)
+    ref = _fp64_compress(kv, sc, ape, w, 1e-6, cs)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_compressor_constant_gate_is_mean_and_one_hot_is_copy():
+    rng = np.random.default_rng(9)
+    kv, _ = _span(rng)
+    zero = np.zeros((128, 576), np.float32)
+    one = np.ones(576, np.float32)
+    ident = np.concatenate([np.ones(32), np.zeros(32)]).astype(np.float32)
+    y = oh.compress_span(kv, zero, zero, one, 0.0, ident)
+    m = kv.astype(np.float64).mean(0)
+    np.testing.assert_allclose(y, m / np.sqrt((m * m).mean()), rtol=1e-5, atol=1e-6)
+    hot = zero.copy()
+    hot[37] = 100.0
+    y = oh.compress_span(kv, hot, zero, one, 0.0, ident)
+    c = kv[37].astype(np.float64)
+    np.testing.assert_allclose(y, c / np.sqrt((c * c).mean()), rtol=1e-5)
+
+
+def test_compressor_permutation_invariance():
+    rng = np.random.default_rng(10)
+    kv, sc = _span(rng)
+    ape = (rng.standard_normal((128, 576)) * 0.5).astype(np.float32)
+    one = np.ones(576, np.float32)
+    cs = oi.rope_cos_sin(np.array([0]), 64, 1.6e5)[0]
+    perm = rng.permutation(128)
+    a = oh.compress_span(kv, sc, ape, one, 1e-6, cs)
+    b = oh.compress_span(kv[perm], sc[perm], ape[perm], one, 1e-6, cs)
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_exp_ekv_accuracy():
+    x = np.linspace(-60, 0, 200001).astype(np.float32)
+    np.testing.assert_allclose(oh.exp_ekv(x), np.exp(x.astype(np.float64)), rtol=5e-6)
+    assert oh.exp_ekv(np.float32(0.0)) == 1.0 and oh.exp_ekv(np.float32(-200.0)) == 0.0
+
+
+def test_hca_rollback_recompresses_from_latest_rows():
+    """Every compressed row equals the compressor over the last-written kv_score
+    rows of its 128 positions, across chunked calls and a rollback."""
+    rng = np.random.default_rng(11)
+    D = 512
+    st = oh.HcaState(num_pages=64, dim=D, num_state=1)
+    bt = np.arange(16, dtype=np.int32)[None]
+    cbt = np.array([[20]], np.int32)
+    ring_pages = np.array([[30, 31, 32]], np.int32)
+    ape = np.zeros((128, D), np.float32)
+    w = np.ones(D, np.float32)
+    cs = oi.rope_cos_sin(np.arange(8) * 128, 64, 1.6e5)
+    latest = {}
+    for p0, n in [(0, 100), (100, 30), (130, 3), (128, 3), (131, 200), (329, 3), (327, 5)]:
+        pos = np.arange(p0, p0 + n)
+        lat = bf16_round(rng.standard_normal((n, D)).astype(np.float32))
+        kvs = bf16_round(rng.standard_normal((n, 2 * D)).astype(np.float32))
+        for p, r in zip(pos, kvs):
+            latest[int(p)] = r
+        slots = paged.slots_from_block_table(bt, np.zeros(n, int), pos)
+        oh.hca_write(st, lat, kvs, pos, np.zeros(n, np.int32), np.array([0, n]), slots, ring_pages, 192,
+                     cbt, np.array([0], np.int32), ape, w, 1e-6, cs)
+    top = max(latest)
+    for j in range((top + 1) // 128):
+        rows = np.stack([latest[128 * j + i] for i in range(128)])
+        y = oh.compress_span(rows[:, :D], rows[:, D:], ape, w, 1e-6, cs[j])
+        codes, scale = quantize_rows(y[None])
+        got_c, got_s = paged.read_fp8_rows(st.pool, np.array([20 * 64 + j]), D)
+        assert np.array_equal(got_c, codes) and np.array_equal(got_s, scale), f"span {j}"
+
+
+# ---------------------------------------------------------------- decode
+def test_decode_matches_softmax_with_sink_logit():
+    """Independent formulation: the sink is one more logit whose value row is 0."""
+    rng = np.random.default_rng(12)
+    T, H, D, n = 2, 16, 576, 50
+    q = rng.standard_normal((T, H, D))
+    rows = rng.standard_normal((200, D))
+    idx = rng.integers(0, 200, (T, n)).astype(np.int32)
+    idx[1, 10:] = -1
+    sinks = rng.standard_normal(H)
+    sinks[3] = -np.inf
+    out, lse = od.sparse_mla_decode(q, lambda s: rows[s], idx, 0.0625, 512, sinks)
+    for t in range(T):
+        valid = idx[t][idx[t] >= 0]
+        kv = rows[valid]
+        s = q[t] @ kv.T * 0.0625
+        logits = np.concatenate([s, sinks[:, None]], 1)
+        p = np.exp(logits - logits.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        np.testing.assert_allclose(out[t], p[:, :-1] @ kv[:, :512], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(lse[t], np.log(np.exp(s).sum(1)), rtol=1e-12)
+
+
+def test_decode_empty_row():
+    out, lse = od.sparse_mla_decode(np.ones((1, 16, 576)), lambda s: None, np.full((1, 4), -1), 0.1, 512,
+                                    np.zeros(16))
+    assert not out.any() and np.all(np.isneginf(lse))

@@ -20,6 +20,12 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+def _rs(t: torch.Tensor) -> int:
+    """Row stride of a 2-D+ tensor; a size-1 leading dim may carry stride 0
+    (e.g. a numpy ``[None]`` view), which would read as zero columns."""
+    return t.stride(0) if t.shape[0] > 1 else t[0].numel()
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -54,8 +60,8 @@ def kv_append_quant(rows: torch.Tensor, slot_mapping: torch.Tensor, cache: torch
     _need(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= T, "slot_mapping int64 [T]")
     _need(cache.dtype == torch.uint8 and cache.dim() == 2 and cache.stride(1) == 1, "cache uint8 [pages, bytes]")
     _lib.call(
-        "ekv_kv_append_quant", rows.data_ptr(), rows.stride(0), T, D, slot_mapping.data_ptr(),
-        cache.data_ptr(), cache.stride(0), cache.shape[0], _stream(),
+        "ekv_kv_append_quant", rows.data_ptr(), _rs(rows), T, D, slot_mapping.data_ptr(),
+        cache.data_ptr(), _rs(cache), cache.shape[0], _stream(),
     )
 
 
@@ -66,8 +72,8 @@ def indexer_k_insert(k: torch.Tensor, slot_mapping: torch.Tensor, kcache: torch.
     _need(k.shape[1] == INDEX_HEAD_DIM and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
     _need(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
     _lib.call(
-        "ekv_indexer_k_insert", k.data_ptr(), k.stride(0), k.shape[0], slot_mapping.data_ptr(),
-        kcache.data_ptr(), kcache.stride(0), kcache.shape[0], _stream(),
+        "ekv_indexer_k_insert", k.data_ptr(), _rs(k), k.shape[0], slot_mapping.data_ptr(),
+        kcache.data_ptr(), _rs(kcache), kcache.shape[0], _stream(),
     )
 
 
@@ -98,11 +104,11 @@ def hca_compress(
         _bits16(state)
         _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
     _lib.call(
-        "ekv_hca_compress", kv_score.data_ptr(), kv_score.stride(0), positions.data_ptr(), qsl.data_ptr(),
+        "ekv_hca_compress", kv_score.data_ptr(), _rs(kv_score), positions.data_ptr(), qsl.data_ptr(),
         qsl.numel() - 1, int(max_query_len), D, _ptr(state), _ptr(state_slot),
         0 if state is None else state.shape[0], ape.data_ptr(), norm_w.data_ptr(), float(eps),
-        cos_sin.data_ptr(), cos_sin.shape[0], comp_block_table.data_ptr(), comp_block_table.stride(0),
-        pool.data_ptr(), pool.stride(0), pool.shape[0], _stream(),
+        cos_sin.data_ptr(), cos_sin.shape[0], comp_block_table.data_ptr(), _rs(comp_block_table),
+        pool.data_ptr(), _rs(pool), pool.shape[0], _stream(),
     )
 
 
@@ -128,10 +134,10 @@ def hca_append(
     if ring_pages is not None:
         _need(ring_pages.dtype == torch.int32 and ring_pages.stride(1) == 1, "ring_pages int32 [B, R/64]")
     _lib.call(
-        "ekv_hca_append", latent.data_ptr(), latent.stride(0), _ptr(kv_score),
-        0 if kv_score is None else kv_score.stride(0), T, D, slot_mapping.data_ptr(), positions.data_ptr(),
-        token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1, pool.data_ptr(), pool.stride(0), pool.shape[0],
-        _ptr(ring_pages), 0 if ring_pages is None else ring_pages.stride(0), int(ring), _ptr(state),
+        "ekv_hca_append", latent.data_ptr(), _rs(latent), _ptr(kv_score),
+        0 if kv_score is None else _rs(kv_score), T, D, slot_mapping.data_ptr(), positions.data_ptr(),
+        token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1, pool.data_ptr(), _rs(pool), pool.shape[0],
+        _ptr(ring_pages), 0 if ring_pages is None else _rs(ring_pages), int(ring), _ptr(state),
         _ptr(state_slot), 0 if state is None else state.shape[0], _stream(),
     )
 
@@ -150,8 +156,8 @@ def hca_decode_indices(
     _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32 [T, W]")
     _lib.call(
         "ekv_hca_decode_indices", positions.data_ptr(), req_ids.data_ptr(), positions.numel(),
-        comp_block_table.data_ptr(), comp_block_table.stride(0), ring_pages.data_ptr(), ring_pages.stride(0),
-        int(ring), int(window), out.data_ptr(), out.stride(0), out.shape[1], lengths.data_ptr(), _stream(),
+        comp_block_table.data_ptr(), _rs(comp_block_table), ring_pages.data_ptr(), _rs(ring_pages),
+        int(ring), int(window), out.data_ptr(), _rs(out), out.shape[1], lengths.data_ptr(), _stream(),
     )
 
 
@@ -168,7 +174,7 @@ def merge_swa_topk(topk_indices: torch.Tensor, out: torch.Tensor, positions: tor
     _need(topk_indices.stride(1) == 1 and out.stride(1) == 1, "rows must be contiguous")
     pos = positions if positions.dtype == torch.int64 else positions.to(torch.int64)
     _lib.call(
-        "ekv_merge_swa_topk", topk_indices.data_ptr(), topk_indices.stride(0), out.data_ptr(), out.stride(0),
+        "ekv_merge_swa_topk", topk_indices.data_ptr(), _rs(topk_indices), out.data_ptr(), _rs(out),
         pos.data_ptr(), num_tokens, topk, width, int(window), _stream(),
     )
 
@@ -179,7 +185,7 @@ def hadamard_rows(x: torch.Tensor) -> torch.Tensor:
     _bits16(x)
     _need(x.dim() == 2 and x.shape[1] == 128 and x.stride(1) == 1, "x must be [n, 128] row-contiguous")
     y = torch.empty_like(x, memory_format=torch.contiguous_format)
-    _lib.call("ekv_hadamard_rows", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), x.shape[0], 128, _stream())
+    _lib.call("ekv_hadamard_rows", x.data_ptr(), _rs(x), y.data_ptr(), _rs(y), x.shape[0], 128, _stream())
     return y
 
 
@@ -198,8 +204,8 @@ def indexer_q_quant(
     w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
     digits = torch.empty((T, 3, H, 128), dtype=torch.int8, device=q.device) if with_digits else None
     _lib.call(
-        "ekv_indexer_q_quant", q.data_ptr(), q.stride(0), q.stride(1), weights.data_ptr(),
-        int(weights.dtype == torch.bfloat16), weights.stride(0), T, H, q_fp8.data_ptr(), w_out.data_ptr(),
+        "ekv_indexer_q_quant", q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), _rs(weights), T, H, q_fp8.data_ptr(), w_out.data_ptr(),
         _ptr(digits), _stream(),
     )
     return q_fp8, w_out, digits
@@ -228,9 +234,9 @@ def indexer_score(
     _need(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table int32")
     _need(scores.dtype == torch.float32 and scores.stride(1) == 1 and scores.shape[1] >= max_len, "scores")
     _lib.call(
-        "ekv_indexer_score", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), kcache.stride(0),
-        kcache.shape[0], block_table.data_ptr(), block_table.stride(0), req_ids.data_ptr(), lengths.data_ptr(),
-        T, int(max_len), scores.data_ptr(), scores.stride(0), _stream(),
+        "ekv_indexer_score", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache),
+        kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(),
+        T, int(max_len), scores.data_ptr(), _rs(scores), _stream(),
     )
 
 
@@ -239,8 +245,8 @@ def topk_select(scores: torch.Tensor, lengths: torch.Tensor, k: int, out: torch.
     _need(scores.dtype == torch.float32 and scores.stride(1) == 1, "scores fp32 rows")
     _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[1] >= k, "out int32 [T, >=k]")
     _lib.call(
-        "ekv_topk_select", scores.data_ptr(), scores.stride(0), lengths.data_ptr(), scores.shape[0],
-        scores.shape[1], out.data_ptr(), out.stride(0), int(k), _stream(),
+        "ekv_topk_select", scores.data_ptr(), _rs(scores), lengths.data_ptr(), scores.shape[0],
+        scores.shape[1], out.data_ptr(), _rs(out), int(k), _stream(),
     )
 
 
@@ -265,9 +271,9 @@ def indexer_topk(
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q_digits.device)
     _lib.call(
-        "ekv_indexer_topk", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), kcache.stride(0),
-        kcache.shape[0], block_table.data_ptr(), block_table.stride(0), req_ids.data_ptr(), lengths.data_ptr(),
-        T, int(max_len), topk_out.data_ptr(), topk_out.stride(0), topk_out.shape[1], workspace.data_ptr(),
+        "ekv_indexer_topk", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache),
+        kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(),
+        T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(),
         workspace.numel(), _stream(),
     )
 
@@ -301,16 +307,16 @@ def sparse_mla_decode(
         page_stride = PAGE_TOKENS * D * 2
     else:
         _need(cache.dtype == torch.uint8 and cache.dim() == 2, "fp8 cache must be uint8 [pages, bytes]")
-        num_pages, page_stride = cache.shape[0], cache.stride(0)
+        num_pages, page_stride = cache.shape[0], _rs(cache)
     if sinks is not None:
         _need(sinks.dtype == torch.float32 and sinks.numel() >= H, "sinks fp32 [H]")
     need = _lib.load().ekv_sparse_mla_decode_workspace_size(T, H, idx.shape[1])
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     _lib.call(
-        "ekv_sparse_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), T, H, D, cache.data_ptr(),
-        int(cache_bf16), page_stride, num_pages, idx.data_ptr(), idx.stride(0), idx.shape[1], _ptr(lengths),
-        _ptr(block_table), 0 if block_table is None else block_table.stride(0), _ptr(req_ids), _ptr(sinks),
-        float(scale), out.data_ptr(), out.stride(0), out.stride(1), _ptr(lse),
-        0 if lse is None else lse.stride(0), workspace.data_ptr(), workspace.numel(), _stream(),
+        "ekv_sparse_mla_decode", q.data_ptr(), _rs(q), q.stride(1), T, H, D, cache.data_ptr(),
+        int(cache_bf16), page_stride, num_pages, idx.data_ptr(), _rs(idx), idx.shape[1], _ptr(lengths),
+        _ptr(block_table), 0 if block_table is None else _rs(block_table), _ptr(req_ids), _ptr(sinks),
+        float(scale), out.data_ptr(), _rs(out), out.stride(1), _ptr(lse),
+        0 if lse is None else _rs(lse), workspace.data_ptr(), workspace.numel(), _stream(),
     )
