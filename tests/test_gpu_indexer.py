@@ -70,7 +70,24 @@ def test_indexer_q_quant_exact(dev, w_dtype):
     assert np.abs(d).max() <= 63
 
 
-def _indexer_setup(dev, rng, lengths, num_seqs=None, pages_per_seq=None, spikes=0.0):
+def _keys(rng, n, kind, spikes):
+    """Key rows of one sequence: N(0,1), plus structure that stresses the selection."""
+    k = randn_bf16(rng, (n, 128))
+    if kind == "prototypes":  # 40 distinct rows -> many exact ties at many levels
+        k = randn_bf16(rng, (40, 128))[rng.integers(0, 40, n)]
+    elif kind == "near_ties":  # one base row with tiny perturbations -> near-equal scores
+        base = randn_bf16(rng, (128,))
+        k = np.repeat(base[None], n, 0)
+        j = rng.integers(0, 128, n)
+        k[np.arange(n), j] = randn_bf16(rng, (n,)) * 0.05
+    elif kind == "constant":  # every score equal -> every token is a candidate
+        k = np.repeat(randn_bf16(rng, (1, 128)), n, 0)
+    if spikes > 0:
+        k[rng.random(n) < spikes] = randn_bf16(rng, (128,), 3.0)
+    return k
+
+
+def _indexer_setup(dev, rng, lengths, num_seqs=None, pages_per_seq=None, spikes=0.0, kind="normal"):
     T = len(lengths)
     num_seqs = num_seqs or T
     max_len = max(max(lengths), 1)
@@ -79,13 +96,9 @@ def _indexer_setup(dev, rng, lengths, num_seqs=None, pages_per_seq=None, spikes=
     kv_pages = num_seqs * pages_per_seq
     kcache = np.zeros((kv_pages, paged.fp8_page_bytes(128)), np.uint8)
     req = np.arange(T, dtype=np.int32) % num_seqs
-    spike_row = randn_bf16(rng, (128,), 3.0)
     for b in range(num_seqs):
         n = pages_per_seq * 64
-        k = randn_bf16(rng, (n, 128))
-        if spikes > 0:
-            m = rng.random(n) < spikes
-            k[m] = spike_row
+        k = _keys(rng, n, kind, spikes)
         s = np.arange(n)
         slots = bt[b, s // 64] * 64 + s % 64
         c, sc = quantize_rows(k)
@@ -140,17 +153,44 @@ def test_topk_select_spikes_and_ties(dev, n):
         assert np.array_equal(got[r], ref), f"row {r}"
 
 
-def test_indexer_topk_end_to_end(dev):
+@pytest.mark.parametrize("kind,spikes", [("normal", 0.05), ("normal", 0.0), ("prototypes", 0.0),
+                                         ("near_ties", 0.0), ("constant", 0.0)])
+def test_indexer_topk_end_to_end(dev, kind, spikes):
+    """Filter + exact rescoring + exact select == oracle top-k, bit for bit."""
     from ernie_kv import ops
 
     rng = np.random.default_rng(17)
-    lengths = np.array([0, 50, 2048, 2100, 9000, 20000], np.int32)
-    st = _indexer_setup(dev, rng, lengths, spikes=0.05)
+    lengths = np.array([0, 50, 2047, 2048, 2049, 2100, 9000, 20000], np.int32)
+    st = _indexer_setup(dev, rng, lengths, spikes=spikes, kind=kind)
     q8, wf, dig = ops.indexer_q_quant(bf16_tensor(st["q"], dev), bf16_tensor(st["w"], dev))
     T = len(lengths)
     out = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
-    ops.indexer_topk(dig, wf, to_dev(st["kcache"], dev), to_dev(st["bt"], dev), to_dev(st["req"], dev),
+    ops.indexer_topk(q8, dig, wf, to_dev(st["kcache"], dev), to_dev(st["bt"], dev), to_dev(st["req"], dev),
                      to_dev(lengths, dev), st["max_len"], out)
     codes, wref = oi.quantize_q(st["q"], st["w"])
     ref, _ = oi.indexer_topk(codes, wref, st["kcache"], st["bt"], st["req"], lengths, TOPK)
     assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def test_indexer_topk_stages_match_one_call(dev):
+    """ekv_indexer_filter + ekv_indexer_select == ekv_indexer_topk, and the
+    top-k rows hold only tokens of their own (windowed) range."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(23)
+    lengths = np.array([3000, 12000, 64], np.int32)
+    st = _indexer_setup(dev, rng, lengths, num_seqs=2, spikes=0.05)
+    q8, wf, dig = ops.indexer_q_quant(bf16_tensor(st["q"], dev), bf16_tensor(st["w"], dev))
+    args = (to_dev(st["kcache"], dev), to_dev(st["bt"], dev), to_dev(st["req"], dev), to_dev(lengths, dev))
+    T = len(lengths)
+    a = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    b = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    ops.indexer_topk(q8, dig, wf, *args, st["max_len"], a)
+    ws = ops.indexer_topk_workspace(T, st["max_len"], dev)
+    ops.indexer_filter(q8, wf, *args, st["max_len"], ws)
+    ops.indexer_select(dig, wf, *args, st["max_len"], b, ws)
+    assert torch.equal(a, b)
+    got = a.cpu().numpy()
+    for t in range(T):
+        row = got[t][got[t] >= 0]
+        assert len(row) == min(lengths[t], TOPK) and np.all(row < lengths[t]) and np.all(np.diff(row) > 0)

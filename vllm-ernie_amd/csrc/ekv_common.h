@@ -74,6 +74,14 @@ __device__ __forceinline__ uint32_t score_key(float s) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// bf16 bits of the smallest bf16 >= f (finite f): a conservative upper bound.
+__device__ __forceinline__ uint16_t bf16_round_up(float f) {
+  const uint32_t u = __float_as_uint(f);
+  uint32_t hi = u >> 16;
+  if (!(u >> 31) && (u & 0xffffu)) hi += 1u;  // positive with dropped bits: next bf16 up
+  return static_cast<uint16_t>(hi);           // negative: truncation moves toward +inf
+}
+
 // Signed base-64 digits of the integer I = value * 2**9 of an e4m3fn code
 // (|I| < 2**18): byte p of the result is digit p as two's complement int8,
 // so I = d0 + 64*d1 + 4096*d2 exactly.

@@ -1,6 +1,6 @@
 // Lightning-indexer scoring and exact top-k.
 //
-// Scoring is exact.  Every e4m3fn value is an integer I = value * 2**9 with
+// Exact scores.  Every e4m3fn value is an integer I = value * 2**9 with
 // |I| < 2**18, split into three signed base-64 digits (int8).  A head's dot
 // product over the 128 dims is the exact int64
 //
@@ -9,19 +9,34 @@
 // whose nine digit-pair sums run on v_mfma_i32_16x16x64_i8 (exact int32
 // accumulation; partial sums stay below 2**21).  Then
 //   dot = fl32(D * 2**-18), p_h = fl32(w_h * max(dot, 0)),
-//   heads summed in fp32 in a fixed order (see head sum below),
+//   heads summed in fp32 in a fixed order (see exact_block),
 //   score = fl32(acc * kscale) + 0.
-// The CPU oracle evaluates the same formula, so scores -- and hence the
-// top-k with its lowest-index tie-break -- are bit-exact.
+// The CPU oracle evaluates the same formula, so scores -- and the top-k with
+// its lowest-index tie-break -- are bit-exact.
 //
-// MFMA layout (16x16x64 i8): lane l holds A row l%16 (a head of the head
-// block) and B column l%16 (a token), K bytes [16*(l/16), +16) of a 64-byte
-// half; C lane l holds rows 4*(l/16)+i, column l%16.
+// Fast top-k (ekv_indexer_filter + ekv_indexer_select): exact scoring costs
+// nine int8 MFMAs per fp8 product, so it runs only on candidates.
+//   1. filter:  fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4) approximate score a_s
+//      of every token, streamed at HBM rate, with an error bound
+//      e_s = kscale_s * 448^2 * (2^-8 + 2^-9) * sum_h |w_h|.
+//      Writes U_s = a_s + e_s (rounded up to bf16) and a per-row histogram of
+//      the 12-bit key prefix of L_s = a_s - e_s; bound_kernel turns the
+//      histogram into a key bound: the bin holding the k-th largest L.
+//   2. verify: per 2048-token chunk, tokens with key(U_s) >= bound are the
+//      candidates (any other token has k tokens whose exact score is strictly
+//      larger); they are scored exactly into a per-chunk list.
+//   3. select: the chunk lists, concatenated in order, go through an exact
+//      radix select; output ascending, -1 padded.
+// The filter's error term is eight times the largest fp8-MFMA error measured
+// on the device (2^-10.95 of the largest product over 1M random and
+// adversarial dot products; |q|, |k| <= 448 by the UE8M0 quantization), and
+// 2^-9 covers the fp32 rounding of both head sums (each at most
+// 66 * 2^-24 * 128 * 448^2 * sum_h |w_h| ~ 2^-11 * 448^2 * sum_h |w_h|).
 //
-// The top-k kernel is a radix select on order-preserving uint32 keys (three
-// passes of 11/11/10 bits over the row's scores, LDS histograms) followed by
-// an ordered compaction: keys above the threshold key, then threshold ties by
-// ascending index; the output indices are ascending, padded with -1.
+// MFMA layouts (A = 16 heads of a head block, B = 16 tokens):
+//   i8 16x16x64:        lane l: row/col l%16, K bytes [16*(l/16), +16)
+//   f8f6f4 16x16x128:   lane l: row/col l%16, K bytes [32*(l/16), +32)
+//   C (both):           lane l: rows 4*(l/16)+i, column l%16
 #include "ekv_common.h"
 #include "ekv_internal.h"
 
@@ -30,7 +45,113 @@ namespace ekv {
 constexpr int kIdxDim = 128;
 constexpr int kIdxHeads = 64;
 constexpr int kIdxPageBytes = kPageTokens * kIdxDim;  // scales follow the values
+constexpr int kHistBits = 12;
+constexpr int kHistBins = 1 << kHistBits;
+constexpr int kChunk = 2048;  // verify chunk (tokens)
 
+// ---------------------------------------------------------------------------
+// Exact scoring helpers
+// ---------------------------------------------------------------------------
+struct ExactOperands {
+  i32x4 qd[4][3][2];  // [head block][digit][K half]
+  float wv[4][4];     // this lane's 16 head weights: heads 16hb + 4g + i
+};
+
+__device__ __forceinline__ void load_exact_operands(ExactOperands& op, const int8_t* q_digits, const float* w,
+                                                    int64_t t, int g, int col) {
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int d = 0; d < 3; ++d)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        const int8_t* src = q_digits + ((t * 3 + d) * kIdxHeads + 16 * hb + col) * kIdxDim + 64 * kh + 16 * g;
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        op.qd[hb][d][kh] = i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z),
+                                 static_cast<int>(v.w)};
+      }
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) op.wv[hb][i] = w[t * kIdxHeads + 16 * hb + 4 * g + i];
+}
+
+__device__ __forceinline__ uint32_t plane_word(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, int p) {
+  const uint32_t sel = static_cast<uint32_t>(p) | (static_cast<uint32_t>(4 + p) << 8) | 0x0c0c0000u;
+  const uint32_t x01 = __builtin_amdgcn_perm(e1, e0, sel);
+  const uint32_t x23 = __builtin_amdgcn_perm(e3, e2, sel);
+  return x01 | (x23 << 16);
+}
+
+// Loads key row s (this lane's 32 bytes: [16g, +16) of each 64-byte half) and
+// its scale; zeros when the token has no page.
+__device__ __forceinline__ void load_key_i8(const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                            const int32_t* bt, int64_t bt_stride, int64_t s, int g, uint4 kb[2],
+                                            float& kscale) {
+  kb[0] = make_uint4(0, 0, 0, 0);
+  kb[1] = make_uint4(0, 0, 0, 0);
+  kscale = 0.0f;
+  if (s < 0 || (s >> 6) >= bt_stride) return;
+  const int64_t page = bt[s >> 6];
+  if (page < 0 || page >= num_pages) return;
+  const uint8_t* base = kcache + page * page_stride;
+  const int row = static_cast<int>(s & 63);
+  kb[0] = *reinterpret_cast<const uint4*>(base + row * kIdxDim + 16 * g);
+  kb[1] = *reinterpret_cast<const uint4*>(base + row * kIdxDim + 64 + 16 * g);
+  kscale = *reinterpret_cast<const float*>(base + kIdxPageBytes + row * 4);
+}
+
+// Exact score of the 16 tokens of a block (token = lane % 16); every lane of
+// the column returns the same value.  The head sum order is fixed: per lane
+// hb = 0..3, i = 0..3 from +0, then (g0 + g1) + (g2 + g3) across lane groups.
+__device__ __forceinline__ float exact_block(const ExactOperands& op, const uint32_t* s_table, const uint4 kb[2],
+                                             float kscale) {
+  i32x4 kd[3][2];
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh) {
+    const uint32_t w4[4] = {kb[kh].x, kb[kh].y, kb[kh].z, kb[kh].w};
+    uint32_t e[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) e[j] = s_table[(w4[j >> 2] >> (8 * (j & 3))) & 0xffu];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      kd[d][kh] = i32x4{static_cast<int>(plane_word(e[0], e[1], e[2], e[3], d)),
+                        static_cast<int>(plane_word(e[4], e[5], e[6], e[7], d)),
+                        static_cast<int>(plane_word(e[8], e[9], e[10], e[11], d)),
+                        static_cast<int>(plane_word(e[12], e[13], e[14], e[15], d))};
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    i32x4 c[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) c[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int da = 0; da < 3; ++da)
+#pragma unroll
+      for (int db = 0; db < 3; ++db)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+          c[da + db] = __builtin_amdgcn_mfma_i32_16x16x64_i8(op.qd[hb][da][kh], kd[db][kh], c[da + db], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t D = static_cast<int64_t>(c[0][i]) + (static_cast<int64_t>(c[1][i]) << 6) +
+                        (static_cast<int64_t>(c[2][i]) << 12) + (static_cast<int64_t>(c[3][i]) << 18) +
+                        (static_cast<int64_t>(c[4][i]) << 24);
+      const float dot = static_cast<float>(static_cast<double>(D) * 0x1p-18);
+      const float r = fmaxf(dot, 0.0f);
+      acc = acc + op.wv[hb][i] * r;
+    }
+  }
+  const float a01 = acc + __shfl_xor(acc, 16);
+  const float tot = a01 + __shfl_xor(a01, 32);
+  return tot * kscale + 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Exact scores of every token s < lengths[t] (ekv_indexer_score).
+// ---------------------------------------------------------------------------
 struct ScoreArgs {
   const int8_t* q_digits;    // [T, 3, 64, 128]
   const float* w;            // [T, 64] folded head weights
@@ -40,177 +161,502 @@ struct ScoreArgs {
   const int32_t* block_table;  // [B, bt_stride]
   int64_t bt_stride;
   const int32_t* req_ids;    // [T]
-  const int32_t* lengths;    // [T] candidate count (implicit range) or null
-  const int32_t* cand;       // [T, cand_stride] explicit token list or null
-  const int32_t* cand_count; // [T] when cand != null
-  int64_t cand_stride;
+  const int32_t* lengths;    // [T]
   float* scores;             // [T, scores_stride]
   int64_t scores_stride;
-  int32_t max_len;           // candidates beyond this are ignored
+  int32_t max_len;
 };
 
 constexpr int kScoreIters = 8;                        // 16-token blocks per wave
 constexpr int kScoreChunk = 4 * 16 * kScoreIters;     // tokens per workgroup
-
-__device__ __forceinline__ uint32_t plane_word(uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, int p) {
-  const uint32_t sel = static_cast<uint32_t>(p) | (static_cast<uint32_t>(4 + p) << 8) | 0x0c0c0000u;
-  const uint32_t x01 = __builtin_amdgcn_perm(e1, e0, sel);
-  const uint32_t x23 = __builtin_amdgcn_perm(e3, e2, sel);
-  return x01 | (x23 << 16);
-}
 
 __global__ void __launch_bounds__(256) score_exact_kernel(ScoreArgs a) {
   __shared__ uint32_t s_table[256];
   const int tid = threadIdx.x;
   s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
   const int t = blockIdx.y;
-  const int n = min(a.cand ? a.cand_count[t] : a.lengths[t], a.max_len);
-  const int64_t chunk0 = static_cast<int64_t>(blockIdx.x) * kScoreChunk;
+  const int n = min(a.lengths[t], a.max_len);
   __syncthreads();
+  const int64_t chunk0 = static_cast<int64_t>(blockIdx.x) * kScoreChunk;
   if (chunk0 >= n) return;
-
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, col = lane & 15;
-  const int req = a.req_ids[t];
-  const int32_t* bt = a.block_table + static_cast<int64_t>(req) * a.bt_stride;
-
-  // q digit operands: [hb][digit][kh]
-  i32x4 qd[4][3][2];
-#pragma unroll
-  for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-    for (int d = 0; d < 3; ++d)
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
-        const int8_t* src = a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + col) * kIdxDim +
-                            64 * kh + 16 * g;
-        const uint4 v = *reinterpret_cast<const uint4*>(src);
-        qd[hb][d][kh] = i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z),
-                              static_cast<int>(v.w)};
-      }
-  float wv[4][4];
-#pragma unroll
-  for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wv[hb][i] = a.w[static_cast<int64_t>(t) * kIdxHeads + 16 * hb + 4 * g + i];
-
+  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
+  ExactOperands op;
+  load_exact_operands(op, a.q_digits, a.w, t, g, col);
   for (int it = 0; it < kScoreIters; ++it) {
-    const int64_t li = chunk0 + (static_cast<int64_t>(wave) * kScoreIters + it) * 16 + col;  // local index
-    const bool valid = li < n;
-    int64_t s = 0;
-    if (valid) s = a.cand ? a.cand[static_cast<int64_t>(t) * a.cand_stride + li] : li;
-    uint4 kb[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    float kscale = 0.0f;
-    if (valid && (s >> 6) < a.bt_stride) {
-      const int64_t page = bt[s >> 6];
-      if (page >= 0 && page < a.num_pages) {
-        const uint8_t* base = a.kcache + page * a.page_stride;
-        const int row = static_cast<int>(s & 63);
-        kb[0] = *reinterpret_cast<const uint4*>(base + row * kIdxDim + 16 * g);
-        kb[1] = *reinterpret_cast<const uint4*>(base + row * kIdxDim + 64 + 16 * g);
-        kscale = *reinterpret_cast<const float*>(base + kIdxPageBytes + row * 4);
-      }
-    }
-    // digit planes of this lane's 32 key bytes: kd[digit][kh]
-    i32x4 kd[3][2];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      const uint32_t w4[4] = {kb[kh].x, kb[kh].y, kb[kh].z, kb[kh].w};
-      uint32_t e[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) e[j] = s_table[(w4[j >> 2] >> (8 * (j & 3))) & 0xffu];
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        kd[d][kh] = i32x4{static_cast<int>(plane_word(e[0], e[1], e[2], e[3], d)),
-                          static_cast<int>(plane_word(e[4], e[5], e[6], e[7], d)),
-                          static_cast<int>(plane_word(e[8], e[9], e[10], e[11], d)),
-                          static_cast<int>(plane_word(e[12], e[13], e[14], e[15], d))};
-      }
-    }
-    // head sum in the fixed order: hb = 0..3, then i = 0..3, from +0
-    float acc = 0.0f;
-#pragma unroll
-    for (int hb = 0; hb < 4; ++hb) {
-      i32x4 c[5];
-#pragma unroll
-      for (int k = 0; k < 5; ++k) c[k] = i32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int da = 0; da < 3; ++da)
-#pragma unroll
-        for (int db = 0; db < 3; ++db)
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-            c[da + db] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[hb][da][kh], kd[db][kh], c[da + db], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t D = static_cast<int64_t>(c[0][i]) + (static_cast<int64_t>(c[1][i]) << 6) +
-                          (static_cast<int64_t>(c[2][i]) << 12) + (static_cast<int64_t>(c[3][i]) << 18) +
-                          (static_cast<int64_t>(c[4][i]) << 24);
-        const float dot = static_cast<float>(static_cast<double>(D) * 0x1p-18);
-        const float r = fmaxf(dot, 0.0f);
-        acc = acc + wv[hb][i] * r;
-      }
-    }
-    const float a01 = acc + __shfl_xor(acc, 16);
-    const float tot = a01 + __shfl_xor(a01, 32);
-    if (valid && g == 0) a.scores[static_cast<int64_t>(t) * a.scores_stride + li] = tot * kscale + 0.0f;
+    const int64_t s = chunk0 + (static_cast<int64_t>(wave) * kScoreIters + it) * 16 + col;
+    uint4 kb[2];
+    float ks;
+    load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, s < n ? s : -1, g, kb, ks);
+    const float sc = exact_block(op, s_table, kb, ks);
+    if (s < n && g == 0) a.scores[static_cast<int64_t>(t) * a.scores_stride + s] = sc;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Exact top-k of one row per workgroup (1024 threads).
+// Filter: approximate fp8-MFMA scores of every token with an error bound.
+// Workgroup = (16 pages of one row); each wave streams 4 pages.
 // ---------------------------------------------------------------------------
-constexpr int kSelThreads = 1024;
-constexpr int kSelWaves = kSelThreads / 64;
-
-struct SelectArgs {
-  const float* scores;       // [T, scores_stride]
-  int64_t scores_stride;
-  const int32_t* lengths;    // [T] (implicit indices 0..n-1) or null
-  const int32_t* cand;       // [T, cand_stride] explicit ascending indices or null
-  const int32_t* cand_count;
-  int64_t cand_stride;
-  int32_t* out;              // [T, out_stride]
-  int64_t out_stride;
+struct FilterArgs {
+  const uint8_t* q_fp8;      // [T, 64, 128]
+  const float* w;            // [T, 64]
+  const uint8_t* kcache;
+  int64_t page_stride;
+  int64_t num_pages;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* req_ids;
+  const int32_t* lengths;
+  int32_t max_len;
   int32_t k;
-  int32_t max_len;           // candidates beyond this are ignored
+  uint16_t* upper;           // [T, max_len] U_s rounded up to bf16
+  uint32_t* hist;            // [T, kHistBins] counts of L_s key prefixes
 };
 
-// Block-wide exclusive prefix of a 0/1 flag; returns the prefix, writes total.
-__device__ __forceinline__ int block_flag_scan(bool flag, int* s_wave, int& total) {
+#ifndef EKV_FILTER_PAGES_PER_WAVE
+#define EKV_FILTER_PAGES_PER_WAVE 4
+#endif
+constexpr int kFilterPagesPerWave = EKV_FILTER_PAGES_PER_WAVE;
+constexpr int kFilterTokens = 4 * kFilterPagesPerWave * kPageTokens;  // per workgroup
+
+// Block-wide exclusive prefix sum of an int; writes the block total.
+template <int kThreads>
+__device__ __forceinline__ int block_scan_excl(int v, int* s_wave, int& total) {
+  constexpr int kWaves = kThreads / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t bal = __ballot(flag);
-  const int in_wave = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
-                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
-  if (lane == 0) s_wave[wave] = __popcll(bal);
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wave[wave] = x;
   __syncthreads();
   int before = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) {
+  for (int w = 0; w < kWaves; ++w) {
     const int c = s_wave[w];
     before += (w < wave) ? c : 0;
     tot += c;
   }
   __syncthreads();
   total = tot;
-  return before + in_wave;
+  return before + x - v;
 }
 
+// Bin b of an nb-bin histogram (nb <= 2 * kThreads) with
+// (count above b) < remaining <= (count above b) + hist[b]; `above` gets the
+// count above b.
+template <int kThreads>
+__device__ __forceinline__ int find_bin(const uint32_t* hist, int nb, int remaining, int* s_wave, int* s_res,
+                                        int& above) {
+  const int tid = threadIdx.x;
+  const int r0 = 2 * tid, r1 = 2 * tid + 1;  // reversed order: bin = nb-1-r
+  const int c0 = (r0 < nb) ? static_cast<int>(hist[nb - 1 - r0]) : 0;
+  const int c1 = (r1 < nb) ? static_cast<int>(hist[nb - 1 - r1]) : 0;
+  int total;
+  const int excl = block_scan_excl<kThreads>(c0 + c1, s_wave, total);
+  if (r0 < nb && excl < remaining && remaining <= excl + c0) { s_res[0] = nb - 1 - r0; s_res[1] = excl; }
+  if (r1 < nb && excl + c0 < remaining && remaining <= excl + c0 + c1) {
+    s_res[0] = nb - 1 - r1;
+    s_res[1] = excl + c0;
+  }
+  __syncthreads();
+  const int bin = s_res[0];
+  above = s_res[1];
+  __syncthreads();
+  return bin;
+}
+
+// LDS histogram increment with one atomic per distinct bin per wave.
+__device__ __forceinline__ void wave_hist_add(uint32_t* hist, int bin) {
+  const int lane = threadIdx.x & 63;
+  uint64_t active = __ballot(bin >= 0);
+  while (active) {
+    const int leader = __builtin_ctzll(active);
+    const int lb = __shfl(bin, leader);
+    const uint64_t m = __ballot(bin == lb);
+    if (lane == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(m)));
+    active &= ~m;
+  }
+}
+
+__global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
+  __shared__ uint32_t s_hist[kHistBins];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.y;
+  const int n = min(a.lengths[t], a.max_len);
+  const int64_t base_tok = static_cast<int64_t>(blockIdx.x) * kFilterTokens;
+  if (base_tok >= n || n <= a.k) return;  // rows with n <= k need no filtering
+  for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0;
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  i32x8 qa[4];
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.q_fp8 + (static_cast<int64_t>(t) * kIdxHeads + 16 * hb + col) * kIdxDim +
+                                                      32 * g);
+    const uint4 v0 = src[0], v1 = src[1];
+    qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
+                   static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
+  }
+  float wv[4][4];
+  float wabs = 0.0f;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wv[hb][i] = a.w[static_cast<int64_t>(t) * kIdxHeads + 16 * hb + 4 * g + i];
+      wabs += fabsf(wv[hb][i]);
+    }
+  float ws = (col == 0) ? wabs : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
+  for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
+  const float ebound = ws * (448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+  __syncthreads();
+
+  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform: scalar page-table loads
+  const int64_t wave_tok = base_tok + static_cast<int64_t>(uwave) * kFilterPagesPerWave * kPageTokens;
+  // page of each of this wave's pages, fetched up front; pages outside the
+  // table read page 0 (always mapped) and are never scored
+  int64_t pages[kFilterPagesPerWave];
+#pragma unroll
+  for (int pg = 0; pg < kFilterPagesPerWave; ++pg) {
+    const int64_t blk = (wave_tok >> 6) + pg;
+    const int64_t p = (blk < a.bt_stride) ? static_cast<int64_t>(bt[blk]) : 0;
+    pages[pg] = (p >= 0 && p < a.num_pages) ? p : 0;
+  }
+  // One page = 4 blocks of 16 tokens; this lane's 32 bytes of each block row,
+  // and the scale of row `lane` (one coalesced 256-byte load per page).
+  // Loads are unconditional so the compiler keeps them in flight.
+  auto load_page = [&](int pg, uint4 (&kb)[4][2], float& ks) {
+    const uint8_t* pbase = a.kcache + pages[pg] * a.page_stride;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int row = 16 * b + col;
+      const uint4* src = reinterpret_cast<const uint4*>(pbase + row * kIdxDim + 32 * g);
+      kb[b][0] = src[0];
+      kb[b][1] = src[1];
+    }
+    ks = *reinterpret_cast<const float*>(pbase + kIdxPageBytes + lane * 4);
+  };
+  uint4 nxt[4][2];
+  float nks;
+  load_page(0, nxt, nks);
+  for (int pg = 0; pg < kFilterPagesPerWave; ++pg) {
+    const int64_t ptok = wave_tok + pg * kPageTokens;
+    if (ptok >= n) break;
+    uint4 kb[4][2];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      kb[b][0] = nxt[b][0];
+      kb[b][1] = nxt[b][1];
+    }
+    const float page_scale = nks;  // scale of page row `lane`
+    if (pg + 1 < kFilterPagesPerWave) load_page(pg + 1, nxt, nks);  // in flight while this page is scored
+    float mine = 0.0f;  // after the 4 blocks: approximate head sum of token `lane` of the page
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const i32x8 kv = i32x8{static_cast<int>(kb[b][0].x), static_cast<int>(kb[b][0].y), static_cast<int>(kb[b][0].z),
+                             static_cast<int>(kb[b][0].w), static_cast<int>(kb[b][1].x), static_cast<int>(kb[b][1].y),
+                             static_cast<int>(kb[b][1].z), static_cast<int>(kb[b][1].w)};
+      float acc = 0.0f;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb) {
+        const f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[hb], kv, f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                          0, 0, 0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += wv[hb][i] * fmaxf(c[i], 0.0f);
+      }
+      acc += __shfl_xor(acc, 16);
+      acc += __shfl_xor(acc, 32);
+      if (g == b) mine = acc;  // block b's token col is page row 16b + col = this lane
+    }
+    const int64_t s = ptok + lane;
+    if (s < n) {
+      const float sc = mine * page_scale;
+      const float e = page_scale * ebound;
+      a.upper[static_cast<int64_t>(t) * a.max_len + s] = bf16_round_up(sc + e);
+      atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* gh = a.hist + static_cast<int64_t>(t) * kHistBins;
+  for (int i = tid; i < kHistBins; i += 256) {
+    const uint32_t c = s_hist[i];
+    if (c) atomicAdd(&gh[i], c);
+  }
+}
+
+// Candidate key bound of each row: the 12-bit bin holding the k-th largest
+// lower bound (one 256-thread workgroup per row, after the filter).
+__global__ void __launch_bounds__(256) bound_kernel(const uint32_t* hist, const int32_t* lengths, int32_t max_len,
+                                                    int32_t k, uint32_t* kbound) {
+  __shared__ int s_wave[4];
+  __shared__ int s_res[2];
+  const int tid = threadIdx.x, t = blockIdx.x;
+  const int n = min(lengths[t], max_len);
+  if (n <= k) return;  // unused: every token is selected
+  const uint32_t* gh = hist + static_cast<int64_t>(t) * kHistBins;
+  // 4096 bins, 16 per thread, scanned from the top bin down
+  const int r0 = 16 * tid;
+  int c[16];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    c[j] = static_cast<int>(gh[kHistBins - 1 - (r0 + j)]);
+    sum += c[j];
+  }
+  int total;
+  int excl = block_scan_excl<256>(sum, s_wave, total);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (excl < k && k <= excl + c[j]) s_res[0] = kHistBins - 1 - (r0 + j);
+    excl += c[j];
+  }
+  __syncthreads();
+  if (tid == 0) kbound[t] = static_cast<uint32_t>(s_res[0]) << (32 - kHistBits);
+}
+
+__global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Verify: candidates of a 2048-token chunk, scored exactly into the chunk's
+// slice of the list buffers ([t][chunk0 ...]), count per chunk.
+// ---------------------------------------------------------------------------
+struct VerifyArgs {
+  const int8_t* q_digits;
+  const float* w;
+  const uint8_t* kcache;
+  int64_t page_stride;
+  int64_t num_pages;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* req_ids;
+  const int32_t* lengths;
+  int32_t max_len;
+  int32_t k;
+  const uint16_t* upper;     // [T, max_len] bf16 upper bounds
+  const uint32_t* kbound;    // [T]
+  float* cand_score;         // [T, max_len] (chunk slices)
+  int32_t* cand_idx;         // [T, max_len]
+  int32_t* cand_count;       // [T, chunks]
+  int32_t chunks;
+};
+
+constexpr int kVerifyChunks = 4;  // chunks per verify workgroup
+
+__global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
+  __shared__ uint32_t s_table[256];
+  __shared__ int32_t s_list[kVerifyChunks * kChunk];  // candidate token indices, ascending
+  __shared__ int16_t s_slot[kVerifyChunks * kChunk];  // position inside its chunk list
+  __shared__ int8_t s_chunk[kVerifyChunks * kChunk];  // chunk (0..kVerifyChunks-1) of the entry
+  __shared__ int s_wave[4];
+  const int tid = threadIdx.x;
+  s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  const int t = blockIdx.y;
+  const int n = min(a.lengths[t], a.max_len);
+  const int64_t row = static_cast<int64_t>(t) * a.max_len;
+  const int c_begin = blockIdx.x * kVerifyChunks;
+  int32_t* counts = a.cand_count + static_cast<int64_t>(t) * a.chunks;
+  if (n <= a.k) {  // every token is selected: list them, no scores needed
+    for (int c = c_begin; c < min(c_begin + kVerifyChunks, a.chunks); ++c) {
+      const int chunk0 = c * kChunk;
+      const int len = max(0, min(kChunk, n - chunk0));
+      for (int i = tid; i < len; i += 256) a.cand_idx[row + chunk0 + i] = chunk0 + i;
+      if (tid == 0) counts[c] = len;
+    }
+    return;
+  }
+  // candidates of each chunk (ascending), appended to one list
+  const uint32_t kbound = a.kbound[t];
+  constexpr int kPer = kChunk / 256;
+  int total = 0;
+  for (int cc = 0; cc < kVerifyChunks; ++cc) {
+    const int c = c_begin + cc;
+    if (c >= a.chunks) break;
+    const int chunk0 = c * kChunk;
+    const int len = max(0, min(kChunk, n - chunk0));
+    uint32_t flags = 0;
+    int cnt = 0;
+    const int start = tid * kPer;
+    if (start < len) {
+      const uint16_t* up = a.upper + row + chunk0 + start;
+      float u[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) u[j] = (start + j < len) ? bf16_to_f32(up[j]) : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j)
+        if (start + j < len && score_key(u[j] + 0.0f) >= kbound) {
+          flags |= 1u << j;
+          ++cnt;
+        }
+    }
+    int ctot;
+    const int ex = block_scan_excl<256>(cnt, s_wave, ctot);
+    int pos = total + ex, slot = ex;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (flags & (1u << j)) {
+        s_list[pos] = chunk0 + start + j;
+        s_slot[pos] = static_cast<int16_t>(slot);
+        s_chunk[pos] = static_cast<int8_t>(cc);
+        ++pos;
+        ++slot;
+      }
+    if (tid == 0) counts[c] = ctot;
+    total += ctot;
+  }
+  __syncthreads();
+  if (total == 0) return;
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
+  ExactOperands op;
+  load_exact_operands(op, a.q_digits, a.w, t, g, col);
+  // wave w scores blocks w, w+4, ...; the next block's key rows are in flight
+  // while the current block is scored
+  int b0 = wave * 16;
+  uint4 kb[2];
+  float ks;
+  load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, (b0 + col < total) ? s_list[b0 + col] : -1, g,
+              kb, ks);
+  for (; b0 < total; b0 += 64) {
+    const uint4 cur[2] = {kb[0], kb[1]};
+    const float cks = ks;
+    const int nb0 = b0 + 64;
+    if (nb0 < total)
+      load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, (nb0 + col < total) ? s_list[nb0 + col] : -1,
+                  g, kb, ks);
+    const float sc = exact_block(op, s_table, cur, cks);
+    const int li = b0 + col;
+    if (li < total && g == 0) {
+      const int64_t dst = row + static_cast<int64_t>(c_begin + s_chunk[li]) * kChunk + s_slot[li];
+      a.cand_score[dst] = sc;
+      a.cand_idx[dst] = s_list[li];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact select: top-k by (score desc, index asc), written ascending, -1 padded.
+// Sources: an implicit range of scores, or per-chunk candidate lists that are
+// concatenated (in chunk order) into LDS, or -- when they do not fit -- into a
+// contiguous global staging row.
+// ---------------------------------------------------------------------------
+constexpr int kSelThreads = 1024;
+constexpr int kSelLds = 16384;
+constexpr int kSelPerThread = 8;
+
+struct SelectArgs {
+  const float* scores;       // implicit mode: [T, scores_stride]
+  int64_t scores_stride;
+  const int32_t* lengths;    // implicit mode: [T]
+  const float* cand_score;   // chunk mode: [T, max_len]
+  const int32_t* cand_idx;
+  const int32_t* cand_count; // [T, chunks]
+  int32_t chunks;
+  float* stage_score;        // chunk mode spill: [T, max_len]
+  int32_t* stage_idx;
+  int32_t* out;              // [T, out_stride]
+  int64_t out_stride;
+  int32_t k;
+  int32_t max_len;
+};
+
+constexpr int kSelMaxChunks = 4096;  // up to 8M-token rows
+
+struct SelectSmem {
+  uint32_t key[kSelLds];
+  int32_t idx[kSelLds];
+  int off[kSelMaxChunks + 1];
+  uint32_t hist[2048];
+  int wave[kSelThreads / 64];
+  int res[2];
+};
+
 __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) {
-  __shared__ uint32_t s_hist[2048];
-  __shared__ uint32_t s_part[kSelThreads];
-  __shared__ int s_wave[kSelWaves];
-  __shared__ uint32_t s_res[2];
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  SelectSmem& sm = *reinterpret_cast<SelectSmem*>(smem_raw);
+  uint32_t* s_hist = sm.hist;
+  uint32_t* s_key = sm.key;
+  int32_t* s_idx = sm.idx;
+  int* s_wave = sm.wave;
+  int* s_res = sm.res;
   const int tid = threadIdx.x;
   const int t = blockIdx.x;
-  const int n = max(0, min(a.cand ? a.cand_count[t] : a.lengths[t], a.max_len));
-  const float* sc = a.scores + static_cast<int64_t>(t) * a.scores_stride;
-  const int32_t* idx = a.cand ? a.cand + static_cast<int64_t>(t) * a.cand_stride : nullptr;
-  int32_t* out = a.out + static_cast<int64_t>(t) * a.out_stride;
   const int k = a.k;
+  int32_t* out = a.out + static_cast<int64_t>(t) * a.out_stride;
+
+  // gather the elements
+  int n;
+  const float* gsc = nullptr;     // global scores (implicit mode or spilled lists)
+  const int32_t* gidx = nullptr;  // global indices (spilled lists); null = implicit
+  bool in_lds;
+  if (a.cand_count == nullptr) {
+    n = max(0, min(a.lengths[t], a.max_len));
+    gsc = a.scores + static_cast<int64_t>(t) * a.scores_stride;
+    in_lds = n <= kSelLds;
+    if (in_lds)
+      for (int i = tid; i < n; i += kSelThreads) {
+        s_key[i] = score_key(gsc[i] + 0.0f);  // -0 ties with +0
+        s_idx[i] = i;
+      }
+  } else {
+    const int32_t* cnt = a.cand_count + static_cast<int64_t>(t) * a.chunks;
+    // exclusive offsets of the chunk lists
+    int base = 0;
+    for (int c0 = 0; c0 < a.chunks; c0 += kSelThreads) {
+      const int c = c0 + tid;
+      const int v = (c < a.chunks) ? cnt[c] : 0;
+      int total;
+      const int ex = block_scan_excl<kSelThreads>(v, s_wave, total);
+      if (c < a.chunks) sm.off[c] = base + ex;
+      base += total;
+    }
+    n = base;
+    if (tid == 0) sm.off[a.chunks] = n;
+    __syncthreads();
+    in_lds = n <= kSelLds;
+    const int64_t row = static_cast<int64_t>(t) * a.max_len;
+    float* st_sc = a.stage_score + row;
+    int32_t* st_ix = a.stage_idx + row;
+    // element p lives in the last chunk c with off[c] <= p
+    for (int p = tid; p < n; p += kSelThreads) {
+      int lo = 0, hi = a.chunks - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sm.off[mid] <= p) lo = mid;
+        else hi = mid - 1;
+      }
+      const int64_t src = row + static_cast<int64_t>(lo) * kChunk + (p - sm.off[lo]);
+      if (in_lds) {
+        s_key[p] = score_key(a.cand_score[src] + 0.0f);
+        s_idx[p] = a.cand_idx[src];
+      } else {
+        st_sc[p] = a.cand_score[src];
+        st_ix[p] = a.cand_idx[src];
+      }
+    }
+    if (!in_lds) {
+      __threadfence_block();
+      gsc = st_sc;
+      gidx = st_ix;
+    }
+  }
+  __syncthreads();
+  auto key_at = [&](int i) -> uint32_t { return in_lds ? s_key[i] : score_key(gsc[i] + 0.0f); };
+  auto idx_at = [&](int i) -> int32_t { return in_lds ? s_idx[i] : (gidx ? gidx[i] : i); };
 
   uint32_t kstar = 0;
-  int need = 0;
+  int need = n;
   if (n > k) {
     uint32_t prefix = 0, mask = 0;
     int remaining = k;
@@ -221,62 +667,65 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
       const int nb = 1 << widths[pass];
       for (int b = tid; b < 2048; b += kSelThreads) s_hist[b] = 0;
       __syncthreads();
-      for (int i = tid; i < n; i += kSelThreads) {
-        const uint32_t key = score_key(sc[i] + 0.0f);  // -0 ties with +0
-        if ((key & mask) == prefix) atomicAdd(&s_hist[(key >> sh) & (nb - 1)], 1u);
+      for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
+#pragma unroll
+        for (int j = 0; j < kSelPerThread; ++j) {
+          const int i = i0 + j * kSelThreads + tid;
+          int bin = -1;
+          if (i < n) {
+            const uint32_t key = key_at(i);
+            if ((key & mask) == prefix) bin = static_cast<int>((key >> sh) & static_cast<uint32_t>(nb - 1));
+          }
+          wave_hist_add(s_hist, bin);
+        }
       }
       __syncthreads();
-      // suffix counts over bins, scanning from the top bin downwards:
-      // thread i owns reversed bins r = 2i, 2i+1 (bin = nb-1-r).
-      uint32_t c0 = 0, c1 = 0;
-      const int r0 = 2 * tid, r1 = 2 * tid + 1;
-      if (r0 < nb) c0 = s_hist[nb - 1 - r0];
-      if (r1 < nb) c1 = s_hist[nb - 1 - r1];
-      s_part[tid] = c0 + c1;
-      __syncthreads();
-      // inclusive scan of s_part (Hillis-Steele in LDS)
-      for (int off = 1; off < kSelThreads; off <<= 1) {
-        const uint32_t v = (tid >= off) ? s_part[tid - off] : 0u;
-        __syncthreads();
-        s_part[tid] += v;
-        __syncthreads();
-      }
-      const uint32_t incl = s_part[tid];
-      const uint32_t excl = incl - (c0 + c1);
-      const uint32_t rem = static_cast<uint32_t>(remaining);
-      if (r0 < nb && excl < rem && rem <= excl + c0) { s_res[0] = nb - 1 - r0; s_res[1] = excl; }
-      if (r1 < nb && excl + c0 < rem && rem <= excl + c0 + c1) { s_res[0] = nb - 1 - r1; s_res[1] = excl + c0; }
-      __syncthreads();
-      const uint32_t bin = s_res[0];
-      remaining -= static_cast<int>(s_res[1]);
-      prefix |= bin << sh;
+      int above;
+      const int bin = find_bin<kSelThreads>(s_hist, nb, remaining, s_wave, s_res, above);
+      remaining -= above;
+      prefix |= static_cast<uint32_t>(bin) << sh;
       mask |= static_cast<uint32_t>(nb - 1) << sh;
-      __syncthreads();
     }
     kstar = prefix;
     need = remaining;  // threshold-valued elements to take, lowest index first
   }
 
-  // ordered compaction
+  // ordered compaction: thread owns kSelPerThread consecutive elements
   int out_base = 0, eq_base = 0;
-  for (int i0 = 0; i0 < n; i0 += kSelThreads) {
-    const int i = i0 + tid;
-    bool gt = false, eq = false;
-    if (i < n) {
-      if (n <= k) {
-        gt = true;
-      } else {
-        const uint32_t key = score_key(sc[i] + 0.0f);  // -0 ties with +0
-        gt = key > kstar;
-        eq = key == kstar;
+  for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
+    const int start = i0 + tid * kSelPerThread;
+    uint32_t gt = 0, eq = 0;
+    int eq_cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kSelPerThread; ++j) {
+      const int i = start + j;
+      if (i < n) {
+        if (n <= k) {
+          gt |= 1u << j;
+        } else {
+          const uint32_t key = key_at(i);
+          if (key > kstar) gt |= 1u << j;
+          else if (key == kstar) { eq |= 1u << j; ++eq_cnt; }
+        }
       }
     }
     int eq_total;
-    const int eq_rank = block_flag_scan(eq, s_wave, eq_total);
-    const bool sel = gt || (eq && eq_base + eq_rank < need);
+    int eq_rank = eq_base + block_scan_excl<kSelThreads>(eq_cnt, s_wave, eq_total);
+    uint32_t sel = gt;
+#pragma unroll
+    for (int j = 0; j < kSelPerThread; ++j)
+      if (eq & (1u << j)) {
+        if (eq_rank < need) sel |= 1u << j;
+        ++eq_rank;
+      }
     int sel_total;
-    const int pos = block_flag_scan(sel, s_wave, sel_total);
-    if (sel && out_base + pos < k) out[out_base + pos] = idx ? idx[i] : i;
+    int pos = out_base + block_scan_excl<kSelThreads>(__popc(sel), s_wave, sel_total);
+#pragma unroll
+    for (int j = 0; j < kSelPerThread; ++j)
+      if (sel & (1u << j)) {
+        if (pos < k) out[pos] = idx_at(start + j);
+        ++pos;
+      }
     out_base += sel_total;
     eq_base += eq_total;
   }
@@ -287,9 +736,53 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
 
 using namespace ekv;
 
+namespace {
+
+void launch_select(const SelectArgs& a, int32_t rows, hipStream_t s) {
+  const int smem = static_cast<int>(sizeof(SelectSmem));
+  hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                      smem);
+  hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(kSelThreads), smem, s, a);
+}
+
+int num_chunks(int32_t max_len) { return max_len > 0 ? (max_len + kChunk - 1) / kChunk : 1; }
+
+// workspace: upper f32 [T,L] | cand_score f32 [T,L] | cand_idx i32 [T,L] |
+//            stage_score f32 [T,L] | stage_idx i32 [T,L] | hist u32 [T,4096] |
+//            done u32 [T] | kbound u32 [T] | counts i32 [T, chunks]
+struct TopkWorkspace {
+  uint16_t* upper;
+  float* cand_score;
+  int32_t* cand_idx;
+  float* stage_score;
+  int32_t* stage_idx;
+  uint32_t* hist;
+  uint32_t* done;
+  uint32_t* kbound;
+  int32_t* counts;
+};
+
+TopkWorkspace carve(void* workspace, int64_t T, int64_t L, int chunks) {
+  TopkWorkspace w;
+  w.upper = static_cast<uint16_t*>(workspace);
+  w.cand_score = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + T * L * 4);
+  w.cand_idx = reinterpret_cast<int32_t*>(w.cand_score + T * L);
+  w.stage_score = reinterpret_cast<float*>(w.cand_idx + T * L);
+  w.stage_idx = reinterpret_cast<int32_t*>(w.stage_score + T * L);
+  w.hist = reinterpret_cast<uint32_t*>(w.stage_idx + T * L);
+  w.done = w.hist + T * kHistBins;
+  w.kbound = w.done + T;
+  w.counts = reinterpret_cast<int32_t*>(w.kbound + T);
+  (void)chunks;
+  return w;
+}
+
+}  // namespace
+
 extern "C" int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len) {
-  if (num_tokens <= 0 || max_len <= 0) return 0;
-  return static_cast<int64_t>(num_tokens) * max_len * 4 + 256;
+  if (num_tokens <= 0) return 0;
+  const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
+  return T * L * 20 + T * kHistBins * 4 + T * 8 + T * num_chunks(max_len) * 4 + 256;
 }
 
 extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const uint8_t* kcache,
@@ -304,7 +797,7 @@ extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const u
   EKV_CHECK(scores_stride >= max_len, "scores_stride must be >= max_len");
   EKV_CHECK(aligned16(q_digits) && aligned16(kcache), "misaligned buffers");
   ScoreArgs a{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-              nullptr, nullptr, 0, scores, scores_stride, max_len};
+              scores, scores_stride, max_len};
   dim3 grid((max_len + kScoreChunk - 1) / kScoreChunk, num_tokens);
   hipLaunchKernelGGL(score_exact_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return ekv_launch_status();
@@ -318,32 +811,92 @@ extern "C" int ekv_topk_select(const float* scores, int64_t scores_stride, const
   EKV_CHECK(scores && lengths && out, "null pointer");
   EKV_CHECK(out_stride >= k, "out_stride must be >= k");
   EKV_CHECK(max_len >= 0 && scores_stride >= max_len, "scores_stride must be >= max_len");
-  SelectArgs s{scores, scores_stride, lengths, nullptr, nullptr, 0, out, out_stride, k, max_len};
-  hipLaunchKernelGGL(topk_select_kernel, dim3(num_tokens), dim3(kSelThreads), 0,
-                     static_cast<hipStream_t>(stream), s);
+  SelectArgs s{scores, scores_stride, lengths, nullptr, nullptr, nullptr, 0, nullptr, nullptr, out, out_stride, k,
+               max_len};
+  launch_select(s, num_tokens, static_cast<hipStream_t>(stream));
   return ekv_launch_status();
 }
 
-extern "C" int ekv_indexer_topk(const int8_t* q_digits, const float* w, const uint8_t* kcache,
-                                int64_t page_stride, int64_t num_pages, const int32_t* block_table,
-                                int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
-                                int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride,
-                                int32_t k, void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_t page_stride,
+                    const int32_t* block_table, const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
+                    int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes) {
   EKV_CHECK(num_tokens >= 0 && max_len >= 0 && k > 0, "bad sizes");
-  if (num_tokens == 0) return 0;
+  EKV_CHECK(q && w && kcache && block_table && req_ids && lengths, "null pointer");
+  EKV_CHECK(page_stride >= kPageTokens * (kIdxDim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(aligned16(q) && aligned16(kcache), "misaligned buffers");
   const int64_t need = ekv_indexer_topk_workspace_size(num_tokens, max_len);
   EKV_CHECK(workspace != nullptr || need == 0, "workspace is null");
   if (workspace_bytes < need) {
     set_error("workspace too small (see ekv_indexer_topk_workspace_size)");
     return kWorkspaceTooSmall;
   }
-  float* scores = static_cast<float*>(workspace);
-  const int64_t sstride = max_len > 0 ? max_len : 1;
-  int rc = 0;
-  if (max_len > 0) {
-    rc = ekv_indexer_score(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids,
-                           lengths, num_tokens, max_len, scores, sstride, stream);
-    if (rc) return rc;
-  }
-  return ekv_topk_select(scores, sstride, lengths, num_tokens, max_len, topk_out, out_stride, k, stream);
+  return 0;
+}
+
+}  // namespace
+
+// Stage 1: fp8-MFMA filter (upper bounds, lower-bound histogram, key bound).
+extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const float* w, const uint8_t* kcache, int64_t page_stride,
+                                  int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
+                                  const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
+                                  int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  int rc = check_topk_args(q_fp8, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
+                           workspace, workspace_bytes);
+  if (rc) return rc;
+  if (num_tokens == 0 || max_len == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t T = num_tokens;
+  TopkWorkspace ws = carve(workspace, T, max_len, num_chunks(max_len));
+  const int64_t nz = T * kHistBins + 2 * T;  // hist, done (kbound is written before use)
+  const int64_t zero_blocks = (nz + 255) / 256;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
+                     dim3(256), 0, s, ws.hist, nz);
+  FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+               max_len, k, ws.upper, ws.hist};
+  hipLaunchKernelGGL(filter_kernel, dim3((max_len + kFilterTokens - 1) / kFilterTokens, num_tokens), dim3(256), 0,
+                     s, f);
+  hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
+  return ekv_launch_status();
+}
+
+// Stage 2: exact scores of the candidates of each chunk, then exact select.
+extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache, int64_t page_stride,
+                                  int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
+                                  const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
+                                  int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_topk_args(q_digits, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
+                           workspace, workspace_bytes);
+  if (rc) return rc;
+  EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
+  if (num_tokens == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
+  const int chunks = num_chunks(max_len);
+  TopkWorkspace ws = carve(workspace, T, L, chunks);
+  VerifyArgs v{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+               max_len, k, ws.upper, ws.kbound, ws.cand_score, ws.cand_idx, ws.counts, chunks};
+  hipLaunchKernelGGL(verify_kernel, dim3((chunks + kVerifyChunks - 1) / kVerifyChunks, num_tokens), dim3(256), 0, s,
+                     v);
+  SelectArgs sel{nullptr, 0, nullptr, ws.cand_score, ws.cand_idx, ws.counts, chunks, ws.stage_score, ws.stage_idx,
+                 topk_out, out_stride, k, static_cast<int32_t>(L)};
+  EKV_CHECK(chunks <= kSelMaxChunks, "max_len too large for the select stage");
+  launch_select(sel, num_tokens, s);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
+                                const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                                int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  int rc = ekv_indexer_filter(q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+                              num_tokens, max_len, k, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+                            num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, stream);
 }

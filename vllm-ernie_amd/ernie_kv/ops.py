@@ -250,7 +250,49 @@ def topk_select(scores: torch.Tensor, lengths: torch.Tensor, k: int, out: torch.
     )
 
 
+def indexer_topk_workspace(num_tokens: int, max_len: int, device) -> torch.Tensor:
+    need = _lib.load().ekv_indexer_topk_workspace_size(int(num_tokens), int(max_len))
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+
+def _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T):
+    _check_dev(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths)
+    if q_fp8 is not None:
+        _need(q_fp8.shape == (T, 64, 128) and q_fp8.dtype == torch.uint8 and q_fp8.is_contiguous(), "q_fp8 [T, 64, 128]")
+    if q_digits is not None:
+        _need(q_digits.shape == (T, 3, 64, 128) and q_digits.is_contiguous(), "q_digits [T, 3, 64, 128]")
+    _need(w.shape == (T, 64) and w.dtype == torch.float32 and w.is_contiguous(), "w fp32 [T, 64]")
+    _need(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table int32")
+    _need(lengths.dtype == torch.int32 and req_ids.dtype == torch.int32, "lengths/req_ids int32")
+
+
+def indexer_filter(q_fp8, w, kcache, block_table, req_ids, lengths, max_len: int, workspace: torch.Tensor,
+                   k: int = 2048) -> None:
+    """Stage 1: fp8-MFMA filter (upper bounds, lower-bound histogram, top-k bound) into ``workspace``."""
+    T = q_fp8.shape[0]
+    _topk_common(q_fp8, None, w, kcache, block_table, req_ids, lengths, T)
+    _lib.call(
+        "ekv_indexer_filter", q_fp8.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
+        block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T, int(max_len), int(k),
+        workspace.data_ptr(), workspace.numel(), _stream(),
+    )
+
+
+def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: int, topk_out: torch.Tensor,
+                   workspace: torch.Tensor) -> None:
+    """Stage 2: candidates, their exact scores, exact top-k (ascending, -1 padded)."""
+    T = q_digits.shape[0]
+    _topk_common(None, q_digits, w, kcache, block_table, req_ids, lengths, T)
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    _lib.call(
+        "ekv_indexer_select", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
+        block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T, int(max_len),
+        topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(), workspace.numel(), _stream(),
+    )
+
+
 def indexer_topk(
+    q_fp8: torch.Tensor,
     q_digits: torch.Tensor,
     w: torch.Tensor,
     kcache: torch.Tensor,
@@ -261,17 +303,14 @@ def indexer_topk(
     topk_out: torch.Tensor,
     workspace: torch.Tensor | None = None,
 ) -> None:
-    """Exact scores over ``s < lengths[t]`` and top-k (ascending, -1 padded)."""
-    _check_dev(q_digits, w, kcache, block_table, req_ids, lengths, topk_out)
-    T = q_digits.shape[0]
-    _need(q_digits.shape[1:] == (3, 64, 128) and q_digits.is_contiguous(), "q_digits [T, 3, 64, 128]")
-    _need(w.shape == (T, 64) and w.dtype == torch.float32 and w.is_contiguous(), "w fp32 [T, 64]")
+    """Exact top-k over ``s < lengths[t]`` (filter + exact rescoring), ascending, -1 padded."""
+    T = q_fp8.shape[0]
+    _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T)
     _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
-    need = _lib.load().ekv_indexer_topk_workspace_size(T, int(max_len))
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q_digits.device)
+        workspace = indexer_topk_workspace(T, max_len, q_fp8.device)
     _lib.call(
-        "ekv_indexer_topk", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache),
+        "ekv_indexer_topk", q_fp8.data_ptr(), q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache),
         kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(),
         T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(),
         workspace.numel(), _stream(),
