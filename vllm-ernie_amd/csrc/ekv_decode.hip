@@ -2,35 +2,57 @@
 // compressed + window), with the per-head attention sink in the softmax
 // denominator.
 //
-// Workgroup = (query row t, split s of its index row); one wave per 16 heads.
-// Each tile of 32 index entries is gathered from the paged cache (fp8 rows of
-// D bytes + fp32 scale per token, or bf16 flat rows), staged in LDS, and
-// widened once to bf16 in two LDS images: K [entry][dim] (row-major, the B
-// operand of S = Q K^T) and V^T [dim][entry] (the B operand of O = P V).
-// Both products run on v_mfma_f32_16x16x32_bf16 with q held in registers for
-// the whole workgroup.  The softmax is online in the log2 domain; the fp8
-// row scale multiplies the scores and is folded into P for the values.
-// Partial (O, m, l) per split go to a workspace; the combine kernel merges the
-// splits, adds the sink and writes bf16 out and the natural-log lse
-// (log sum_j exp(s_j), sink excluded).
+// Workgroup = (query row t, split s of its index row), 512 threads in two
+// roles, one barrier per tile of 32 index entries.  Between two barriers:
+//   * score waves 0..3 (q for heads 16w .. 16w+15 held in registers) first
+//     finish tile t-1 (below), then compute S = Q K^T of tile t on
+//     v_mfma_f32_16x16x32_bf16 from a bf16 K image in LDS, run the online
+//     softmax and write P (bf16, row scale folded in) for their heads;
+//   * data waves 4..7 finish tile t-1, widen tile t+1 (exact fp8 -> bf16) into
+//     the next of three K images, and issue the loads of tile t+3 (8 rows per
+//     wave, row addresses in scalar registers, 256-byte coalesced loads into
+//     registers, two tiles in flight);
+//   * "finish tile t-1" = O[:, 64w .. 64w+63] += P V for all heads, every wave
+//     taking its 64 channels.  The B operand (V, entries x channels) is read
+//     straight from the row-major K image with ds_read_b64_tr_b16, which
+//     transposes 4 x 4 blocks of 16-bit elements across each 16-lane row; no
+//     separate V^T image is built.
+// A prologue resolves every index entry of the split to a cache slot (block
+// table lookup) and fp32 row scale once.  The softmax reference max only
+// moves when a score exceeds it by more than 8 (log2 units), so O is rescaled
+// rarely.  Each split leaves O / l in bf16 plus (m, l) in fp32; the combine
+// kernel merges the splits, adds the sink and writes bf16 out and the
+// natural-log lse (log sum_j exp(s_j), sink excluded).
 #include "ekv_common.h"
 #include "ekv_internal.h"
+
+#include <type_traits>
 
 namespace ekv {
 
 constexpr int kDv = 512;
 constexpr int kTile = 32;
-constexpr int kMaxWaves = 4;   // up to 64 heads (one wave per 16)
+constexpr int kScoreWaves = 4;               // up to 64 heads (one wave per 16)
+constexpr int kDataWaves = 4;
+constexpr int kThreads = 64 * (kScoreWaves + kDataWaves);
+constexpr int kRowsPerDataWave = kTile / kDataWaves;   // 8
+constexpr int kKImages = 3;                  // tile t-1 (P V), t (S), t+1 (being widened)
+constexpr int kMaxSplitEntries = 1024;       // index entries one workgroup resolves
+constexpr int kTargetGroups = 256;           // one workgroup per CU
+constexpr float kRescaleSlack = 8.0f;        // log2 units: P <= 2**8 between rescales
 constexpr float kLog2e = 0x1.715476p+0f;
 constexpr float kLn2 = 0x1.62e430p-1f;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 struct DecodeArgs {
   const uint16_t* q;        // [T, H, D] bf16
   int64_t q_tok_stride, q_head_stride;
   const uint8_t* cache;     // fp8 pages [num_pages, page_stride] or bf16 rows
   int64_t page_stride;      // bytes (fp8 layout)
-  int64_t num_rows;         // addressable rows (num_pages * 64)
-  int32_t cache_bf16;       // 0 fp8 paged, 1 bf16 flat rows
+  int64_t num_rows;         // addressable rows (num_pages * 64), < 2**31
   const int32_t* indices;   // [T, idx_stride]
   int64_t idx_stride;
   int32_t width;            // entries per index row
@@ -40,260 +62,493 @@ struct DecodeArgs {
   const int32_t* req_ids;   // [T] with block_table
   float scale;              // softmax scale
   int32_t heads;
-  int32_t per_split;        // entries per split (multiple of kTile)
-  float* ws_o;              // [T, NS, H, 512]
-  float* ws_ml;             // [T, NS, H, 2]
+  int32_t per_split;        // entries per split (multiple of kTile, <= kMaxSplitEntries)
+  uint16_t* ws_o;           // [T, NS, H, 512] bf16, O / l of the split
+  float* ws_ml;             // [T, NS, H, 2] (m in log2 units, l)
   int32_t splits;
 };
 
 template <int D>
 struct DecodeSmem {
-  static constexpr int kStage = D + 16;     // fp8 staging row stride (bytes)
   static constexpr int kKRow = D + 8;       // bf16 K row stride (elements)
-  static constexpr int kVRow = kTile + 8;   // bf16 V^T row stride (elements)
-  uint8_t stage[kTile * kStage];
-  uint16_t k[kTile * kKRow];
-  uint16_t vt[kDv * kVRow];
-  uint16_t p[kMaxWaves][16 * kTile];
-  int64_t slot[kTile];
-  float kscale[kTile];
+  static constexpr int kPRow = kTile + 8;   // bf16 P row stride (elements)
+  static constexpr int kORow = kDv + 8;     // bf16 output staging row stride
+  uint16_t k[kKImages][kTile * kKRow];
+  uint16_t p[2][64 * kPRow];                // P of tiles t (written) and t-1 (read)
+  float alpha[2][64];                       // rescale factor per head (valid when grow[.][head / 16])
+  int32_t grow[2][kScoreWaves];
+  float row_l[64];
+  int32_t slot[kMaxSplitEntries];
+  float kscale[kMaxSplitEntries];
+};
+// The epilogue stages the 64 x 512 bf16 output over the K images.
+static_assert(kKImages * kTile * (512 + 8) >= 64 * (kDv + 8), "output staging must fit in the K images");
+
+// Four e4m3fn bytes -> four bf16 (exact: every e4m3fn value is a bf16 value).
+__device__ __forceinline__ uint2 fp8x4_bf16(uint32_t w) {
+  const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
+// Max / sum over each row of 16 lanes, every lane receiving the result:
+// DPP row rotations by 8, 4, 2, 1 (VALU only, no LDS round trip).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
+  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_f32<0x122>(v));  // row_ror:2
+  return fmaxf(v, dpp_f32<0x121>(v));  // row_ror:1
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0x128>(v);
+  v += dpp_f32<0x124>(v);
+  v += dpp_f32<0x122>(v);
+  return v + dpp_f32<0x121>(v);
+}
+
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};  // round to nearest even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ds_read_b64_tr_b16: in each row of 16 lanes, lane j receives 16-bit element
+// j % 4 of the 8 bytes addressed by lanes j / 4 + 4m (m = 0..3).
+__device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)((__attribute__((address_space(3))) uint16_t*)(p)));
+}
+
+// ---------------------------------------------------------------------------
+// Data role: rows 8u .. 8u+7 of a tile, 4-channel units lane + 64 j.
+template <int D, bool BF16>
+struct RowRegs {
+  using Unit = typename std::conditional<BF16, uint2, uint32_t>::type;
+  static constexpr int kUnits = D / 4;                   // 4-channel units per row
+  static constexpr int kJ = (kUnits + 63) / 64;
+  Unit v[kRowsPerDataWave][kJ];
+  uint32_t valid;                                        // bit rr: row rr holds data (wave-uniform)
 };
 
-__device__ __forceinline__ uint32_t byte_column(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int i) {
-  const uint32_t sel = static_cast<uint32_t>(i) | (static_cast<uint32_t>(4 + i) << 8) | 0x0c0c0000u;
-  return __builtin_amdgcn_perm(w1, w0, sel) | (__builtin_amdgcn_perm(w3, w2, sel) << 16);
+// Issue every load of tile `tile` for this data wave.  Masked rows and tiles
+// past the end read the first cache row and stay flagged invalid, so that the
+// wait before each widening counts exactly the loads issued after it.
+template <int D, bool BF16>
+__device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem<D>& sm, int u, int tile, int ntiles,
+                                           RowRegs<D, BF16>& rr) {
+  using RR = RowRegs<D, BF16>;
+  const bool live = tile < ntiles;
+  const int tb = (live ? tile : 0) * kTile + kRowsPerDataWave * u;
+  const int lane = threadIdx.x & 63;
+  uint32_t valid = 0;
+  // One LDS read gives lane r the slot of row r; rows then become uniform.
+  const int my_slot = sm.slot[tb + (lane & (kRowsPerDataWave - 1))];
+  // Keep each tile's loads in issue order relative to the other tiles' loads
+  // (the register buffers are consumed oldest first).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < kRowsPerDataWave; ++r) {
+    const int slot = __builtin_amdgcn_readlane(my_slot, r);
+    const bool ok = live && slot >= 0;
+    const int s = ok ? slot : 0;
+    const uint8_t* row = BF16 ? a.cache + static_cast<int64_t>(s) * (2 * D)
+                              : a.cache + static_cast<int64_t>(s >> 6) * a.page_stride + (s & 63) * D;
+    valid |= static_cast<uint32_t>(ok) << r;
+#pragma unroll
+    for (int j = 0; j < RR::kJ; ++j) {
+      const int unit = (RR::kUnits % 64 == 0 || lane + 64 * j < RR::kUnits) ? lane + 64 * j : RR::kUnits - 1;
+      rr.v[r][j] = *reinterpret_cast<const typename RR::Unit*>(row + unit * sizeof(typename RR::Unit));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  rr.valid = valid;
 }
+
+// Widen the wave's 8 rows into a K image (masked rows become zero, so that
+// P = 0 never meets a non-finite value in P V).  Lanes past the end of a row
+// repeat its last unit: a duplicate store of equal data, no divergence.
+template <int D, bool BF16>
+__device__ __forceinline__ void widen_rows(const RowRegs<D, BF16>& rr, int u, uint16_t* k) {
+  using RR = RowRegs<D, BF16>;
+  using SM = DecodeSmem<D>;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kRowsPerDataWave; ++r) {
+    const bool ok = (rr.valid >> r) & 1u;
+#pragma unroll
+    for (int j = 0; j < RR::kJ; ++j) {
+      const int unit = (RR::kUnits % 64 == 0 || lane + 64 * j < RR::kUnits) ? lane + 64 * j : RR::kUnits - 1;
+      uint2 x;
+      if constexpr (BF16) x = ok ? rr.v[r][j] : make_uint2(0u, 0u);
+      else x = fp8x4_bf16(ok ? rr.v[r][j] : 0u);
+      *reinterpret_cast<uint2*>(&k[(kRowsPerDataWave * u + r) * SM::kKRow + 4 * unit]) = x;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// O[:, 64w .. 64w+63] += P V for every head group (all waves).  o[hf][nt]
+// holds heads 16hf + 4g + i, channels 64w + 16nt + col.
+template <int D>
+__device__ __forceinline__ void accumulate_pv(const DecodeSmem<D>& sm, const uint16_t* kimg, int pb, int hgroups,
+                                              f32x4 (&o)[4][4]) {
+  using SM = DecodeSmem<D>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  // B operand (entries 8g .. 8g+7, channel 64w + 16nt + col): two transposed
+  // reads of rows 8g + 4h + col/4, channels 64w + 16nt + 4 (col % 4) .. +3.
+  bf16x8 vb[4];
+  const uint16_t* vbase = kimg + (8 * g + (col >> 2)) * SM::kKRow + 64 * wave + 4 * (col & 3);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const i16x4 lo = lds_read_tr16(vbase + 16 * nt);
+    const i16x4 hi = lds_read_tr16(vbase + 4 * SM::kKRow + 16 * nt);
+    const i16x4 both[2] = {lo, hi};
+    vb[nt] = __builtin_bit_cast(bf16x8, both);
+  }
+  // All operands are read before the first product; the rescale (rare) and
+  // the products of head groups past `hgroups` (unused) need no branches.
+  bf16x8 pa[4];
+#pragma unroll
+  for (int hf = 0; hf < 4; ++hf)
+    pa[hf] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.p[pb][(16 * hf + col) * SM::kPRow + 8 * g]));
+  const int4 gr = *reinterpret_cast<const int4*>(sm.grow[pb]);
+  const int grow_any = (gr.x | (hgroups > 1 ? gr.y : 0) | (hgroups > 2 ? gr.z : 0) | (hgroups > 3 ? gr.w : 0));
+  if (__builtin_amdgcn_readfirstlane(grow_any)) {
+    const int grs[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+    for (int hf = 0; hf < 4; ++hf) {
+      if (!grs[hf]) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float al = sm.alpha[pb][16 * hf + 4 * g + i];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) o[hf][nt][i] *= al;
+      }
+    }
+  }
+#pragma unroll
+  for (int hf = 0; hf < 4; ++hf)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hf], vb[nt], o[hf][nt], 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Score role: S = Q K^T for heads 16w .. 16w+15 over one tile, online softmax,
+// P (times the row scale, bf16) and the rescale factors to LDS buffer pb.
+struct SoftmaxState {
+  float m2[4];    // reference max (log2 units) of heads 4g + i
+  float lsum[4];  // this lane's share of the denominator relative to m2
+};
 
 template <int D>
-__global__ void __launch_bounds__(256) sparse_decode_kernel(DecodeArgs a) {
-  extern __shared__ __align__(16) uint8_t smem_raw[];
-  DecodeSmem<D>& sm = *reinterpret_cast<DecodeSmem<D>*>(smem_raw);
-  constexpr int KS = D / 32;  // k-steps of the QK product
-  const int tid = threadIdx.x;
-  const int nthreads = blockDim.x;
-  const int lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void score_tile(DecodeSmem<D>& sm, const uint16_t* kimg, int pb, int tb, float sc2,
+                                           const bf16x8 (&qa)[D / 32], SoftmaxState& st) {
+  using SM = DecodeSmem<D>;
+  constexpr int KS = D / 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int t = blockIdx.y, split = blockIdx.x;
-  const int len = a.lengths ? min(a.lengths[t], a.width) : a.width;
-  const int e_begin = split * a.per_split;
-  const int e_end = min(e_begin + a.per_split, len);
-  const int head0 = 16 * wave;
-
-  // q operands (A of S = Q K^T): lane holds head head0 + col, dims 32ks + 8g .. +8
-  bf16x8 qa[KS];
-  {
-    const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (head0 + col) * a.q_head_stride;
+  // Four independent accumulation chains (entry half x even/odd k-step).
+  f32x4 s2[2][2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g);
-      qa[ks] = __builtin_bit_cast(bf16x8, v);
-    }
-  }
-  f32x4 o[kDv / 16];
+  for (int nt = 0; nt < 2; ++nt) s2[nt][0] = s2[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* kbase = kimg + col * SM::kKRow + 8 * g;
 #pragma unroll
-  for (int i = 0; i < kDv / 16; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m2[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-  const float sc2 = a.scale * kLog2e;
-
-  for (int e0 = e_begin; e0 < e_end; e0 += kTile) {
-    // 1. indices -> slots and scales
-    if (tid < kTile) {
-      const int e = e0 + tid;
-      int64_t slot = -1;
-      if (e < e_end) {
-        int64_t idx = a.indices[static_cast<int64_t>(t) * a.idx_stride + e];
-        if (idx >= 0 && a.block_table != nullptr) {
-          const int64_t blk = idx >> 6;
-          idx = (blk < a.bt_stride)
-                    ? static_cast<int64_t>(a.block_table[static_cast<int64_t>(a.req_ids[t]) * a.bt_stride + blk]) *
-                              kPageTokens + (idx & 63)
-                    : -1;
-        }
-        slot = (idx >= 0 && idx < a.num_rows) ? idx : -1;
-      }
-      sm.slot[tid] = slot;
-      float ks = 0.0f;
-      if (slot >= 0) {
-        ks = a.cache_bf16 ? 1.0f
-                          : *reinterpret_cast<const float*>(a.cache + (slot / kPageTokens) * a.page_stride +
-                                                            kPageTokens * D + (slot % kPageTokens) * 4);
-      }
-      sm.kscale[tid] = ks;
-    }
-    __syncthreads();
-    // 2. gather rows
-    if (!a.cache_bf16) {
-      constexpr int kParts = D / 16;
-      for (int c = tid; c < kTile * kParts; c += nthreads) {
-        const int r = c / kParts, part = c % kParts;
-        const int64_t slot = sm.slot[r];
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (slot >= 0)
-          v = *reinterpret_cast<const uint4*>(a.cache + (slot / kPageTokens) * a.page_stride +
-                                              (slot % kPageTokens) * D + 16 * part);
-        *reinterpret_cast<uint4*>(&sm.stage[r * DecodeSmem<D>::kStage + 16 * part]) = v;
-      }
-    } else {
-      constexpr int kParts = D / 8;
-      for (int c = tid; c < kTile * kParts; c += nthreads) {
-        const int r = c / kParts, part = c % kParts;
-        const int64_t slot = sm.slot[r];
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (slot >= 0)
-          v = *reinterpret_cast<const uint4*>(a.cache + slot * (2 * D) + 16 * part);
-        *reinterpret_cast<uint4*>(&sm.k[r * DecodeSmem<D>::kKRow + 8 * part]) = v;
-      }
-    }
-    __syncthreads();
-    // 3. widen to bf16 K rows and V^T columns, 4 entries x 4 dims per item
-    {
-      constexpr int kDimGroups = D / 4;
-      for (int it = tid; it < (kTile / 4) * kDimGroups; it += nthreads) {
-        const int rg = it / kDimGroups, dg = it % kDimGroups;
-        const int r0 = 4 * rg, d0 = 4 * dg;
-        if (!a.cache_bf16) {
-          uint32_t w[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            w[r] = *reinterpret_cast<const uint32_t*>(&sm.stage[(r0 + r) * DecodeSmem<D>::kStage + d0]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            uint32_t lo, hi;
-            fp8x4_to_bf16x4(w[r], lo, hi);
-            *reinterpret_cast<uint2*>(&sm.k[(r0 + r) * DecodeSmem<D>::kKRow + d0]) = make_uint2(lo, hi);
-          }
-          if (d0 < kDv) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              uint32_t lo, hi;
-              fp8x4_to_bf16x4(byte_column(w[0], w[1], w[2], w[3], i), lo, hi);
-              *reinterpret_cast<uint2*>(&sm.vt[(d0 + i) * DecodeSmem<D>::kVRow + r0]) = make_uint2(lo, hi);
-            }
-          }
-        } else if (d0 < kDv) {
-          uint2 w[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            w[r] = *reinterpret_cast<const uint2*>(&sm.k[(r0 + r) * DecodeSmem<D>::kKRow + d0]);
-          // 16-bit transpose of a 4x4 block
-          const uint32_t c0lo = __builtin_amdgcn_perm(w[1].x, w[0].x, 0x05040100u);
-          const uint32_t c0hi = __builtin_amdgcn_perm(w[3].x, w[2].x, 0x05040100u);
-          const uint32_t c1lo = __builtin_amdgcn_perm(w[1].x, w[0].x, 0x07060302u);
-          const uint32_t c1hi = __builtin_amdgcn_perm(w[3].x, w[2].x, 0x07060302u);
-          const uint32_t c2lo = __builtin_amdgcn_perm(w[1].y, w[0].y, 0x05040100u);
-          const uint32_t c2hi = __builtin_amdgcn_perm(w[3].y, w[2].y, 0x05040100u);
-          const uint32_t c3lo = __builtin_amdgcn_perm(w[1].y, w[0].y, 0x07060302u);
-          const uint32_t c3hi = __builtin_amdgcn_perm(w[3].y, w[2].y, 0x07060302u);
-          *reinterpret_cast<uint2*>(&sm.vt[(d0 + 0) * DecodeSmem<D>::kVRow + r0]) = make_uint2(c0lo, c0hi);
-          *reinterpret_cast<uint2*>(&sm.vt[(d0 + 1) * DecodeSmem<D>::kVRow + r0]) = make_uint2(c1lo, c1hi);
-          *reinterpret_cast<uint2*>(&sm.vt[(d0 + 2) * DecodeSmem<D>::kVRow + r0]) = make_uint2(c2lo, c2hi);
-          *reinterpret_cast<uint2*>(&sm.vt[(d0 + 3) * DecodeSmem<D>::kVRow + r0]) = make_uint2(c3lo, c3hi);
-        }
-      }
-    }
-    __syncthreads();
-    // 4. S = Q K^T for this wave's 16 heads x 32 entries
-    f32x4 s[2];
+  for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      s[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = &sm.k[(16 * nt + col) * DecodeSmem<D>::kKRow + 8 * g];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(krow + 32 * ks));
-        s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s[nt], 0, 0, 0);
-      }
+      const bf16x8 kb =
+          __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(kbase + 16 * nt * SM::kKRow + 32 * ks));
+      s2[nt][ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s2[nt][ks & 1], 0, 0, 0);
     }
-    // 5. online softmax (log2 domain); lane owns heads 4g+i, entries 16nt+col
-    float pv[2][4];
-    float alpha[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float x0 = (sm.slot[col] >= 0) ? s[0][i] * (sc2 * sm.kscale[col]) : -INFINITY;
-      float x1 = (sm.slot[16 + col] >= 0) ? s[1][i] * (sc2 * sm.kscale[16 + col]) : -INFINITY;
-      float mx = fmaxf(x0, x1);
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
-      const float mnew = fmaxf(m2[i], mx);
-      if (mnew == -INFINITY) {
-        alpha[i] = 1.0f;
-        pv[0][i] = 0.0f;
-        pv[1][i] = 0.0f;
-      } else {
-        alpha[i] = exp2f(m2[i] - mnew);
-        pv[0][i] = exp2f(x0 - mnew);
-        pv[1][i] = exp2f(x1 - mnew);
-      }
-      lsum[i] = lsum[i] * alpha[i] + (pv[0][i] + pv[1][i]);
-      m2[i] = mnew;
-    }
-#pragma unroll
-    for (int nt = 0; nt < kDv / 16; ++nt) {
-      o[nt][0] *= alpha[0]; o[nt][1] *= alpha[1]; o[nt][2] *= alpha[2]; o[nt][3] *= alpha[3];
-    }
-    // 6. P' = P * kscale (bf16) to LDS in A layout source order [head][entry]
-    {
-      uint16_t* pw = sm.p[wave];
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const float ks = sm.kscale[16 * nt + col];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pw[(4 * g + i) * kTile + 16 * nt + col] = f32_to_bf16(pv[nt][i] * ks);
-      }
-    }
-    __syncthreads();
-    // 7. O += P' V
-    {
-      const bf16x8 pa = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.p[wave][col * kTile + 8 * g]));
-#pragma unroll
-      for (int nt = 0; nt < kDv / 16; ++nt) {
-        const bf16x8 vb = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const uint4*>(&sm.vt[(16 * nt + col) * DecodeSmem<D>::kVRow + 8 * g]));
-        o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[nt], 0, 0, 0);
-      }
-    }
-    __syncthreads();
   }
-  // partial results: l summed over the 16 lanes of each head
+  const f32x4 s[2] = {s2[0][0] + s2[0][1], s2[1][0] + s2[1][1]};
+  // lane owns heads 4g+i, entries 16nt+col
+  const bool ok0 = sm.slot[tb + col] >= 0, ok1 = sm.slot[tb + 16 + col] >= 0;
+  const float ks0 = sm.kscale[tb + col], ks1 = sm.kscale[tb + 16 + col];
+  float x[2][4], mx[4];
+  bool grow = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) lsum[i] += __shfl_xor(lsum[i], off, 16);
+    x[0][i] = ok0 ? s[0][i] * (sc2 * ks0) : -INFINITY;
+    x[1][i] = ok1 ? s[1][i] * (sc2 * ks1) : -INFINITY;
+    const float m = row16_max(fmaxf(x[0][i], x[1][i]));
+    mx[i] = m;
+    grow |= m > st.m2[i] + kRescaleSlack || (st.m2[i] == -INFINITY && m != -INFINITY);
   }
-  const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
-#pragma unroll
-  for (int nt = 0; nt < kDv / 16; ++nt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      a.ws_o[(base + head0 + 4 * g + i) * kDv + 16 * nt + col] = o[nt][i];
-  if (col == 0) {
+  const bool any = __any(grow);
+  if (any) {  // wave-uniform: move every head's reference to its max so far
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      a.ws_ml[(base + head0 + 4 * g + i) * 2 + 0] = m2[i];
-      a.ws_ml[(base + head0 + 4 * g + i) * 2 + 1] = lsum[i];
+      const float mnew = fmaxf(st.m2[i], mx[i]);
+      float al = 1.0f;
+      if (mnew != -INFINITY) {
+        al = (st.m2[i] == -INFINITY) ? 0.0f : exp2f(st.m2[i] - mnew);
+        st.lsum[i] *= al;
+        st.m2[i] = mnew;
+      }
+      if (col == 0) sm.alpha[pb][16 * wave + 4 * g + i] = al;
     }
+  }
+  if (lane == 0) sm.grow[pb][wave] = any ? 1 : 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool live = st.m2[i] != -INFINITY;
+    const float p0 = live ? exp2f(x[0][i] - st.m2[i]) : 0.0f;
+    const float p1 = live ? exp2f(x[1][i] - st.m2[i]) : 0.0f;
+    st.lsum[i] += p0 + p1;
+    uint16_t* prow = &sm.p[pb][(16 * wave + 4 * g + i) * SM::kPRow];
+    const uint32_t pk = bf16x2_bits(p0 * ks0, p1 * ks1);
+    prow[col] = static_cast<uint16_t>(pk & 0xffffu);
+    prow[16 + col] = static_cast<uint16_t>(pk >> 16);
   }
 }
 
-// One workgroup of 128 threads per (t, h): merge the splits, add the sink.
-__global__ void __launch_bounds__(128) decode_combine_kernel(
-    const float* ws_o, const float* ws_ml, int32_t splits, int32_t heads, const float* sinks,
+// ---------------------------------------------------------------------------
+template <int D, bool BF16>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+sparse_decode_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) uint8_t smem_raw[];
+  using SM = DecodeSmem<D>;
+  SM& sm = *reinterpret_cast<SM*>(smem_raw);
+  constexpr int KS = D / 32;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int t = blockIdx.y, split = blockIdx.x;
+  const int hgroups = a.heads / 16;
+  const bool scorer = wave < kScoreWaves;
+
+  // q operands of the score waves (A of S = Q K^T): head 16w + col, dims 32ks + 8g .. +8
+  bf16x8 qa[KS];
+  if (scorer && wave < hgroups) {
+    const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (16 * wave + col) * a.q_head_stride;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qa[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
+  }
+
+  // Prologue: entries -> slots and scales, three dependent gathers (index,
+  // block table, scale) each issued for all of the thread's entries first.
+  int len = a.width;
+  if (a.lengths) len = min(max(a.lengths[t], 0), a.width);
+  const int e_begin = split * a.per_split;
+  const int e_cnt = max(0, min(e_begin + a.per_split, len) - e_begin);
+  const int ntiles = (e_cnt + kTile - 1) / kTile;
+  const int e_pad = ntiles * kTile;
+  // Steps of the main loop: step s finishes tile s-1 and scores tile s, so
+  // ntiles + 1 steps, rounded up to even (the data waves take steps in pairs).
+  const int steps = (ntiles + 2) & ~1;
+  constexpr int kPrologue = kMaxSplitEntries / kThreads;
+  int64_t sv[kPrologue];
+#pragma unroll
+  for (int j = 0; j < kPrologue; ++j) {
+    const int e = tid + kThreads * j;
+    sv[j] = (e < e_cnt) ? a.indices[static_cast<int64_t>(t) * a.idx_stride + e_begin + e] : -1;
+  }
+  if (a.block_table != nullptr) {
+    const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
+#pragma unroll
+    for (int j = 0; j < kPrologue; ++j) {
+      const int64_t idx = sv[j];
+      const bool ok = idx >= 0 && (idx >> 6) < a.bt_stride;
+      const int64_t page = bt[ok ? (idx >> 6) : 0];
+      sv[j] = ok ? page * kPageTokens + (idx & 63) : -1;
+    }
+  }
+  float ksv[kPrologue];
+#pragma unroll
+  for (int j = 0; j < kPrologue; ++j) {
+    const int e = tid + kThreads * j;
+    const int64_t slot = (sv[j] >= 0 && sv[j] < a.num_rows) ? sv[j] : -1;
+    if (e < e_pad) sm.slot[e] = static_cast<int32_t>(slot);
+    sv[j] = slot;
+    if constexpr (BF16) {
+      ksv[j] = 1.0f;
+    } else {
+      const int64_t sc = slot >= 0 ? slot : 0;
+      ksv[j] = *reinterpret_cast<const float*>(a.cache + (sc >> 6) * a.page_stride + kPageTokens * D + (sc & 63) * 4);
+    }
+  }
+  if (tid < 2 * kScoreWaves) sm.grow[tid / kScoreWaves][tid % kScoreWaves] = 0;
+  __syncthreads();
+
+  f32x4 o[4][4];
+#pragma unroll
+  for (int hf = 0; hf < 4; ++hf)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) o[hf][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (!scorer) {
+    // ---------------- data waves ----------------
+    const int u = wave - kScoreWaves;
+    RowRegs<D, BF16> bufA, bufB;  // even tiles in A, odd tiles in B
+    fetch_rows<D, BF16>(a, sm, u, 0, ntiles, bufA);
+    fetch_rows<D, BF16>(a, sm, u, 1, ntiles, bufB);
+#pragma unroll
+    for (int j = 0; j < kPrologue; ++j) {
+      const int e = tid + kThreads * j;
+      if (e < e_pad) sm.kscale[e] = sv[j] >= 0 ? ksv[j] : 0.0f;
+    }
+    widen_rows<D, BF16>(bufA, u, sm.k[0]);
+    fetch_rows<D, BF16>(a, sm, u, 2, ntiles, bufA);
+    __syncthreads();  // tile 0 widened
+    // Step s finishes tile s-1 (P V from image (s-1) % 3), widens tile s+1 into
+    // image (s+1) % 3 and issues the loads of tile s+3.  Every load and
+    // widening is unconditional (tiles past the end are zero rows nobody
+    // reads), so each wait leaves the newer tile in flight.
+    widen_rows<D, BF16>(bufB, u, sm.k[1]);  // step 0
+    fetch_rows<D, BF16>(a, sm, u, 3, ntiles, bufB);
+    __syncthreads();
+    int s = 1, kp = 0;  // kp: image of tile s-1
+    for (; s + 1 <= ntiles; s += 2) {
+      const int k1 = (kp == 2) ? 0 : kp + 1, k2 = (k1 == 2) ? 0 : k1 + 1;
+      accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
+      widen_rows<D, BF16>(bufA, u, sm.k[k2]);
+      fetch_rows<D, BF16>(a, sm, u, s + 3, ntiles, bufA);
+      __syncthreads();
+      accumulate_pv<D>(sm, sm.k[k1], s & 1, hgroups, o);
+      widen_rows<D, BF16>(bufB, u, sm.k[kp]);
+      fetch_rows<D, BF16>(a, sm, u, s + 4, ntiles, bufB);
+      __syncthreads();
+      kp = k2;
+    }
+    // the last (odd) step
+    if (s - 1 < ntiles) accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
+    __syncthreads();
+  } else {
+    // ---------------- score waves ----------------
+#pragma unroll
+    for (int j = 0; j < kPrologue; ++j) {
+      const int e = tid + kThreads * j;
+      if (e < e_pad) sm.kscale[e] = sv[j] >= 0 ? ksv[j] : 0.0f;
+    }
+    SoftmaxState st;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st.m2[i] = -INFINITY;
+      st.lsum[i] = 0.0f;
+    }
+    const float sc2 = a.scale * kLog2e;
+    __syncthreads();  // tile 0 widened
+    // Step s finishes tile s-1 and scores tile s (image s % 3, P buffer s & 1).
+    // Score waves past `hgroups` run on unused heads rather than branching.
+    if (ntiles == 0) {
+      for (int s = 0; s < steps; ++s) __syncthreads();
+    } else {
+      score_tile<D>(sm, sm.k[0], 0, 0, sc2, qa, st);
+      __syncthreads();
+      int kp = 0;  // image of tile s-1
+      for (int s = 1; s < ntiles; ++s) {
+        const int kr = (kp == 2) ? 0 : kp + 1;
+        accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
+        score_tile<D>(sm, sm.k[kr], s & 1, s * kTile, sc2, qa, st);
+        __syncthreads();
+        kp = kr;
+      }
+      accumulate_pv<D>(sm, sm.k[kp], (ntiles - 1) & 1, hgroups, o);
+      __syncthreads();
+      for (int s = ntiles + 1; s < steps; ++s) __syncthreads();
+    }
+    // final denominators and maxima of this wave's heads
+    if (wave < hgroups) {
+      const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float l = row16_sum(st.lsum[i]);
+        if (col == 0) {
+          const int h = 16 * wave + 4 * g + i;
+          sm.row_l[h] = l;
+          a.ws_ml[(base + h) * 2 + 0] = st.m2[i];
+          a.ws_ml[(base + h) * 2 + 1] = l;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Epilogue: O / l as bf16 through LDS (over the K images), then out.
+  uint16_t* ostage = sm.k[0];
+#pragma unroll
+  for (int hf = 0; hf < 4; ++hf) {
+    if (hf >= hgroups) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float l = sm.row_l[16 * hf + 4 * g + i];
+      const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
+      uint16_t* orow = &ostage[(16 * hf + 4 * g + i) * SM::kORow + 64 * wave + col];
+#pragma unroll
+      for (int nt = 0; nt < 4; nt += 2) {
+        const uint32_t pk = bf16x2_bits(o[hf][nt][i] * inv, o[hf][nt + 1][i] * inv);
+        orow[16 * nt] = static_cast<uint16_t>(pk & 0xffffu);
+        orow[16 * nt + 16] = static_cast<uint16_t>(pk >> 16);
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
+  const int chunks = a.heads * (kDv / 8);
+  for (int c = tid; c < chunks; c += kThreads) {
+    const int h = c / (kDv / 8), part = c % (kDv / 8);
+    const uint4 v = *reinterpret_cast<const uint4*>(&ostage[h * SM::kORow + 8 * part]);
+    *reinterpret_cast<uint4*>(a.ws_o + (base + h) * kDv + 8 * part) = v;
+  }
+}
+
+// 256 threads per (t, 4 heads): wave = head, lane = 8 output channels.
+__global__ void __launch_bounds__(256) decode_combine_kernel(
+    const uint16_t* ws_o, const float* ws_ml, int32_t splits, int32_t heads, const float* sinks,
     uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, float* lse, int64_t lse_stride) {
-  const int t = blockIdx.y, h = blockIdx.x, tid = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, ws_ml[((static_cast<int64_t>(t) * splits + s) * heads + h) * 2]);
-  float L = 0.0f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (M != -INFINITY) {
-    for (int s = 0; s < splits; ++s) {
-      const int64_t b = (static_cast<int64_t>(t) * splits + s) * heads + h;
-      const float ms = ws_ml[b * 2];
-      if (ms == -INFINITY) continue;
-      const float f = exp2f(ms - M);
-      L += ws_ml[b * 2 + 1] * f;
-      const float4 v = *reinterpret_cast<const float4*>(ws_o + b * kDv + 4 * tid);
-      acc[0] += v.x * f; acc[1] += v.y * f; acc[2] += v.z * f; acc[3] += v.w * f;
+  const int t = blockIdx.y;
+  const int h = 4 * blockIdx.x + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (h >= heads) return;
+  const int64_t b0 = static_cast<int64_t>(t) * splits * heads + h;
+  // Splits in batches of 8 with every load of a batch issued before any is
+  // used; a running max rescales the partial sums between batches.
+  constexpr int kBatch = 8;
+  float M = -INFINITY, L = 0.0f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += kBatch) {
+    float ms[kBatch], ls[kBatch];
+    uint4 v[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const bool ok = s0 + b < splits;
+      const int64_t row = b0 + static_cast<int64_t>(ok ? s0 + b : s0) * heads;
+      const float2 ml = *reinterpret_cast<const float2*>(ws_ml + row * 2);
+      ms[b] = ok ? ml.x : -INFINITY;
+      ls[b] = ml.y;
+      v[b] = *reinterpret_cast<const uint4*>(ws_o + row * kDv + 8 * lane);
+    }
+    float mb = M;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) mb = fmaxf(mb, ms[b]);
+    if (mb == -INFINITY) continue;
+    if (M != mb) {
+      const float sc = (M == -INFINITY) ? 0.0f : exp2f(M - mb);
+      L *= sc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= sc;
+      M = mb;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (ms[b] == -INFINITY) continue;
+      const float f = exp2f(ms[b] - M) * ls[b];
+      L += f;
+      const uint32_t w[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * f;
+        acc[2 * i + 1] += bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * f;
+      }
     }
   }
   float den = L;
@@ -307,11 +562,14 @@ __global__ void __launch_bounds__(128) decode_combine_kernel(
     }
   }
   const float inv = (den > 0.0f) ? numf / den : 0.0f;
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16(acc[2 * i] * inv)) |
+           (static_cast<uint32_t>(f32_to_bf16(acc[2 * i + 1] * inv)) << 16);
   uint16_t* orow = out + static_cast<int64_t>(t) * out_tok_stride + h * out_head_stride;
-  const uint32_t w0 = static_cast<uint32_t>(f32_to_bf16(acc[0] * inv)) | (static_cast<uint32_t>(f32_to_bf16(acc[1] * inv)) << 16);
-  const uint32_t w1 = static_cast<uint32_t>(f32_to_bf16(acc[2] * inv)) | (static_cast<uint32_t>(f32_to_bf16(acc[3] * inv)) << 16);
-  *reinterpret_cast<uint2*>(orow + 4 * tid) = make_uint2(w0, w1);
-  if (tid == 0 && lse != nullptr)
+  *reinterpret_cast<uint4*>(orow + 8 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+  if (lane == 0 && lse != nullptr)
     lse[static_cast<int64_t>(t) * lse_stride + h] = (L > 0.0f) ? (M + log2f(L)) * kLn2 : -INFINITY;
 }
 
@@ -321,7 +579,9 @@ using namespace ekv;
 
 static int decode_splits(int32_t num_tokens, int32_t width) {
   const int tiles = (width + kTile - 1) / kTile;
-  int splits = (512 + num_tokens - 1) / (num_tokens > 0 ? num_tokens : 1);
+  int splits = (kTargetGroups + num_tokens - 1) / (num_tokens > 0 ? num_tokens : 1);
+  const int need = (width + kMaxSplitEntries - 1) / kMaxSplitEntries;
+  if (splits < need) splits = need;
   if (splits > tiles) splits = tiles;
   if (splits < 1) splits = 1;
   return splits;
@@ -329,8 +589,16 @@ static int decode_splits(int32_t num_tokens, int32_t width) {
 
 extern "C" int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int32_t heads, int32_t width) {
   if (num_tokens <= 0 || heads <= 0) return 0;
-  const int64_t splits = decode_splits(num_tokens, width);
-  return static_cast<int64_t>(num_tokens) * splits * heads * (kDv + 2) * 4 + 256;
+  const int64_t n = static_cast<int64_t>(num_tokens) * decode_splits(num_tokens, width) * heads;
+  return n * kDv * 2 + n * 2 * 4 + 256;
+}
+
+template <int D, bool BF16>
+static void launch_decode(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  const size_t smem = sizeof(DecodeSmem<D>);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_decode_kernel<D, BF16>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+  hipLaunchKernelGGL((sparse_decode_kernel<D, BF16>), grid, dim3(kThreads), smem, s, a);
 }
 
 extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -345,15 +613,18 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   EKV_CHECK(num_tokens >= 0 && width >= 0, "sizes must be >= 0");
   if (num_tokens == 0) return 0;
   EKV_CHECK(dim == 512 || dim == 576, "dim must be 512 or 576");
-  EKV_CHECK(heads > 0 && heads % 16 == 0 && heads <= 16 * kMaxWaves, "heads must be a multiple of 16, <= 64");
+  EKV_CHECK(heads > 0 && heads % 16 == 0 && heads <= 16 * kScoreWaves, "heads must be a multiple of 16, <= 64");
   EKV_CHECK(q && cache && indices && out, "null pointer");
   EKV_CHECK(block_table == nullptr || req_ids != nullptr, "block_table needs req_ids");
   EKV_CHECK(q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 && aligned16(q), "q must be 16-byte aligned rows");
-  EKV_CHECK(out_tok_stride % 4 == 0 && out_head_stride % 4 == 0 && aligned8(out), "out rows must be 8-byte aligned");
+  EKV_CHECK(out_tok_stride % 8 == 0 && out_head_stride % 8 == 0 && aligned16(out),
+            "out rows must be 16-byte aligned");
   EKV_CHECK(cache_bf16 || (page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0), "bad page_stride");
   EKV_CHECK(aligned16(cache), "cache must be 16-byte aligned");
+  EKV_CHECK(num_pages >= 1 && num_pages * kPageTokens < (int64_t{1} << 31), "cache must hold 1 .. 2**31 / 64 pages");
   const int64_t need = ekv_sparse_mla_decode_workspace_size(num_tokens, heads, width);
   EKV_CHECK(workspace != nullptr, "workspace is null");
+  EKV_CHECK(aligned16(workspace), "workspace must be 16-byte aligned");
   if (workspace_bytes < need) {
     set_error("workspace too small (see ekv_sparse_mla_decode_workspace_size)");
     return kWorkspaceTooSmall;
@@ -361,28 +632,22 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   const int splits = decode_splits(num_tokens, width);
   const int tiles = (width + kTile - 1) / kTile;
   const int per_split = ((tiles + splits - 1) / splits) * kTile;
-  float* ws_o = static_cast<float*>(workspace);
-  float* ws_ml = ws_o + static_cast<int64_t>(num_tokens) * splits * heads * kDv;
-  DecodeArgs a{q, q_tok_stride, q_head_stride, cache, page_stride,
-               num_pages * kPageTokens, cache_bf16, indices, idx_stride, width,
-               lengths, block_table, bt_stride, req_ids, scale, heads, per_split, ws_o, ws_ml, splits};
+  uint16_t* ws_o = static_cast<uint16_t*>(workspace);
+  float* ws_ml = reinterpret_cast<float*>(ws_o + static_cast<int64_t>(num_tokens) * splits * heads * kDv);
+  DecodeArgs a{q, q_tok_stride, q_head_stride, cache, page_stride, num_pages * kPageTokens, indices, idx_stride,
+               width, lengths, block_table, bt_stride, req_ids, scale, heads, per_split, ws_o, ws_ml, splits};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(splits, num_tokens);
-  dim3 block(4 * heads);
+  const dim3 grid(splits, num_tokens);
   if (dim == 576) {
-    const size_t smem = sizeof(DecodeSmem<576>);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_decode_kernel<576>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-    hipLaunchKernelGGL(sparse_decode_kernel<576>, grid, block, smem, s, a);
+    if (cache_bf16) launch_decode<576, true>(a, grid, s);
+    else launch_decode<576, false>(a, grid, s);
   } else {
-    const size_t smem = sizeof(DecodeSmem<512>);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_decode_kernel<512>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-    hipLaunchKernelGGL(sparse_decode_kernel<512>, grid, block, smem, s, a);
+    if (cache_bf16) launch_decode<512, true>(a, grid, s);
+    else launch_decode<512, false>(a, grid, s);
   }
   int rc = ekv_launch_status();
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads, num_tokens), dim3(128), 0, s, ws_o, ws_ml, splits, heads,
-                     sinks, out, out_tok_stride, out_head_stride, lse, lse_stride);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads / 4, num_tokens), dim3(256), 0, s, ws_o, ws_ml, splits,
+                     heads, sinks, out, out_tok_stride, out_head_stride, lse, lse_stride);
   return ekv_launch_status();
 }
