@@ -136,10 +136,14 @@ __device__ __forceinline__ float exact_block(const ExactOperands& op, const uint
           c[da + db] = __builtin_amdgcn_mfma_i32_16x16x64_i8(op.qd[hb][da][kh], kd[db][kh], c[da + db], 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t D = static_cast<int64_t>(c[0][i]) + (static_cast<int64_t>(c[1][i]) << 6) +
-                        (static_cast<int64_t>(c[2][i]) << 12) + (static_cast<int64_t>(c[3][i]) << 18) +
-                        (static_cast<int64_t>(c[4][i]) << 24);
-      const float dot = static_cast<float>(static_cast<double>(D) * 0x1p-18);
+      // D = lo + 2^12 c2 + 2^18 hi with lo = c0 + 64 c1, hi = c3 + 64 c4 (each
+      // |c| < 2^21, so |lo|, |hi| < 2^27); the two fmas below are exact in
+      // double (every partial result is an integer below 2^53), so dot is the
+      // single rounding fl32(D * 2^-18).
+      const int lo = c[0][i] + (c[1][i] << 6), hi = c[3][i] + (c[4][i] << 6);
+      const double Dd = __builtin_fma(__builtin_fma(static_cast<double>(hi), 64.0, static_cast<double>(c[2][i])), 4096.0,
+                                      static_cast<double>(lo));
+      const float dot = static_cast<float>(Dd * 0x1p-18);
       const float r = fmaxf(dot, 0.0f);
       acc = acc + op.wv[hb][i] * r;
     }
@@ -267,19 +271,6 @@ __device__ __forceinline__ int find_bin(const uint32_t* hist, int nb, int remain
   above = s_res[1];
   __syncthreads();
   return bin;
-}
-
-// LDS histogram increment with one atomic per distinct bin per wave.
-__device__ __forceinline__ void wave_hist_add(uint32_t* hist, int bin) {
-  const int lane = threadIdx.x & 63;
-  uint64_t active = __ballot(bin >= 0);
-  while (active) {
-    const int leader = __builtin_ctzll(active);
-    const int lb = __shfl(bin, leader);
-    const uint64_t m = __ballot(bin == lb);
-    if (lane == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(m)));
-    active &= ~m;
-  }
 }
 
 __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
@@ -451,12 +442,13 @@ struct VerifyArgs {
 };
 
 constexpr int kVerifyChunks = 4;  // chunks per verify workgroup
+constexpr int kVerifyPages = kVerifyChunks * kChunk / kPageTokens;
 
 __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
   __shared__ uint32_t s_table[256];
-  __shared__ int32_t s_list[kVerifyChunks * kChunk];  // candidate token indices, ascending
-  __shared__ int16_t s_slot[kVerifyChunks * kChunk];  // position inside its chunk list
-  __shared__ int8_t s_chunk[kVerifyChunks * kChunk];  // chunk (0..kVerifyChunks-1) of the entry
+  __shared__ int16_t s_list[kVerifyChunks * kChunk];  // candidate token offsets in the group, ascending
+  __shared__ int16_t s_meta[kVerifyChunks * kChunk];  // chunk (bits 11..12) and position in its chunk list
+  __shared__ int32_t s_pages[kVerifyPages];           // block-table entries of the group's pages
   __shared__ int s_wave[4];
   const int tid = threadIdx.x;
   s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
@@ -474,29 +466,52 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
     }
     return;
   }
-  // candidates of each chunk (ascending), appended to one list
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  // The q operands and the block-table entries of the group's pages are
+  // independent of the candidate scan: in flight first.
+  const int tok0 = c_begin * kChunk;  // first token of the group
+  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
+  if (tid < kVerifyPages) {
+    const int64_t blk = (tok0 >> 6) + tid;
+    s_pages[tid] = (blk < a.bt_stride) ? bt[blk] : -1;
+  }
+  ExactOperands op;
+  load_exact_operands(op, a.q_digits, a.w, t, g, col);
+  // Candidates of each chunk (ascending), appended to one list.  The upper
+  // bounds of all the workgroup's chunks are loaded before any is tested.
   const uint32_t kbound = a.kbound[t];
   constexpr int kPer = kChunk / 256;
+  const int start = tid * kPer;
+  uint4 ub[kVerifyChunks];
+#pragma unroll
+  for (int cc = 0; cc < kVerifyChunks; ++cc) {
+    const int chunk0 = (c_begin + cc) * kChunk;
+    const bool full = (row & 7) == 0 && chunk0 + start + kPer <= n;  // aligned and in bounds
+    ub[cc] = full ? *reinterpret_cast<const uint4*>(a.upper + row + chunk0 + start) : make_uint4(0, 0, 0, 0);
+    if (!full && chunk0 + start < n) {  // ragged tail of the row
+      uint16_t tmp[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) tmp[j] = (chunk0 + start + j < n) ? a.upper[row + chunk0 + start + j] : 0;
+      ub[cc] = *reinterpret_cast<const uint4*>(tmp);
+    }
+  }
   int total = 0;
+#pragma unroll
   for (int cc = 0; cc < kVerifyChunks; ++cc) {
     const int c = c_begin + cc;
-    if (c >= a.chunks) break;
     const int chunk0 = c * kChunk;
-    const int len = max(0, min(kChunk, n - chunk0));
+    const int len = (c < a.chunks) ? max(0, min(kChunk, n - chunk0)) : 0;
+    const uint32_t uw[4] = {ub[cc].x, ub[cc].y, ub[cc].z, ub[cc].w};
     uint32_t flags = 0;
     int cnt = 0;
-    const int start = tid * kPer;
-    if (start < len) {
-      const uint16_t* up = a.upper + row + chunk0 + start;
-      float u[kPer];
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) u[j] = (start + j < len) ? bf16_to_f32(up[j]) : -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kPer; ++j)
-        if (start + j < len && score_key(u[j] + 0.0f) >= kbound) {
-          flags |= 1u << j;
-          ++cnt;
-        }
+    for (int j = 0; j < kPer; ++j) {
+      const uint16_t bits = static_cast<uint16_t>((uw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+      if (start + j < len && score_key(bf16_to_f32(bits) + 0.0f) >= kbound) {
+        flags |= 1u << j;
+        ++cnt;
+      }
     }
     int ctot;
     const int ex = block_scan_excl<256>(cnt, s_wave, ctot);
@@ -504,43 +519,55 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
 #pragma unroll
     for (int j = 0; j < kPer; ++j)
       if (flags & (1u << j)) {
-        s_list[pos] = chunk0 + start + j;
-        s_slot[pos] = static_cast<int16_t>(slot);
-        s_chunk[pos] = static_cast<int8_t>(cc);
+        s_list[pos] = static_cast<int16_t>(chunk0 + start + j - tok0);
+        s_meta[pos] = static_cast<int16_t>((cc << 11) | slot);
         ++pos;
         ++slot;
       }
-    if (tid == 0) counts[c] = ctot;
+    if (tid == 0 && c < a.chunks) counts[c] = ctot;
     total += ctot;
   }
   __syncthreads();
   if (total == 0) return;
 
-  const int lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, col = lane & 15;
-  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
-  ExactOperands op;
-  load_exact_operands(op, a.q_digits, a.w, t, g, col);
-  // wave w scores blocks w, w+4, ...; the next block's key rows are in flight
-  // while the current block is scored
-  int b0 = wave * 16;
-  uint4 kb[2];
-  float ks;
-  load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, (b0 + col < total) ? s_list[b0 + col] : -1, g,
-              kb, ks);
-  for (; b0 < total; b0 += 64) {
-    const uint4 cur[2] = {kb[0], kb[1]};
-    const float cks = ks;
-    const int nb0 = b0 + 64;
-    if (nb0 < total)
-      load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, (nb0 + col < total) ? s_list[nb0 + col] : -1,
-                  g, kb, ks);
-    const float sc = exact_block(op, s_table, cur, cks);
-    const int li = b0 + col;
-    if (li < total && g == 0) {
-      const int64_t dst = row + static_cast<int64_t>(c_begin + s_chunk[li]) * kChunk + s_slot[li];
-      a.cand_score[dst] = sc;
-      a.cand_idx[dst] = s_list[li];
+  // Wave w scores blocks w, w+4, ... in batches of kVerifyBatch: the key rows
+  // of a whole batch are loaded together (pages come from LDS).
+  constexpr int kVerifyBatch = 4;
+  for (int bb = wave * 16; bb < total; bb += 64 * kVerifyBatch) {
+    int tok[kVerifyBatch];
+    int64_t page[kVerifyBatch];
+#pragma unroll
+    for (int j = 0; j < kVerifyBatch; ++j) {
+      const int li = bb + 64 * j + col;
+      tok[j] = (li < total) ? s_list[li] : -1;  // offset in the group
+      page[j] = (tok[j] >= 0) ? static_cast<int64_t>(s_pages[tok[j] >> 6]) : -1;
+    }
+    uint4 kb[kVerifyBatch][2];
+    float ks[kVerifyBatch];
+#pragma unroll
+    for (int j = 0; j < kVerifyBatch; ++j) {
+      const bool ok = page[j] >= 0 && page[j] < a.num_pages;
+      const uint8_t* base = a.kcache + (ok ? page[j] : 0) * a.page_stride;
+      const int r = static_cast<int>(tok[j] & 63);
+      const uint4 k0 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 16 * g);
+      const uint4 k1 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 64 + 16 * g);
+      const float sc = *reinterpret_cast<const float*>(base + kIdxPageBytes + r * 4);
+      kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
+      kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
+      ks[j] = ok ? sc : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kVerifyBatch; ++j) {
+      const int b0 = bb + 64 * j;
+      if (b0 >= total) break;
+      const float sc = exact_block(op, s_table, kb[j], ks[j]);
+      const int li = b0 + col;
+      if (li < total && g == 0) {
+        const int meta = s_meta[li];
+        const int64_t dst = row + static_cast<int64_t>(c_begin + (meta >> 11)) * kChunk + (meta & 2047);
+        a.cand_score[dst] = sc;
+        a.cand_idx[dst] = tok0 + s_list[li];
+      }
     }
   }
 }
@@ -581,6 +608,21 @@ struct SelectSmem {
   int wave[kSelThreads / 64];
   int res[2];
 };
+
+// LDS histogram increment: one atomic for the whole wave when every active
+// lane falls in the same bin (runs of equal keys), else one per lane.
+__device__ __forceinline__ void hist_add_ties(uint32_t* hist, int bin) {
+  const uint64_t act = __ballot(bin >= 0);
+  if (act == 0) return;
+  const int leader = static_cast<int>(__builtin_ctzll(act));
+  const int lb = __builtin_amdgcn_readlane(bin, leader);
+  const uint64_t same = __ballot(bin == lb);
+  if (same == act) {
+    if ((threadIdx.x & 63) == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(act)));
+  } else if (bin >= 0) {
+    atomicAdd(&hist[bin], 1u);
+  }
+}
 
 __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
@@ -628,21 +670,43 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     const int64_t row = static_cast<int64_t>(t) * a.max_len;
     float* st_sc = a.stage_score + row;
     int32_t* st_ix = a.stage_idx + row;
-    // element p lives in the last chunk c with off[c] <= p
-    for (int p = tid; p < n; p += kSelThreads) {
-      int lo = 0, hi = a.chunks - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (sm.off[mid] <= p) lo = mid;
-        else hi = mid - 1;
-      }
-      const int64_t src = row + static_cast<int64_t>(lo) * kChunk + (p - sm.off[lo]);
+    // Wave w copies chunks w, w+16, ...: four chunks at a time, the first 256
+    // entries of each loaded together; longer lists finish in a plain loop.
+    const int lane = tid & 63, wave = tid >> 6;
+    constexpr int kWaves = kSelThreads / 64;
+    auto put = [&](int p, float sc, int32_t ix) {
       if (in_lds) {
-        s_key[p] = score_key(a.cand_score[src] + 0.0f);
-        s_idx[p] = a.cand_idx[src];
+        s_key[p] = score_key(sc + 0.0f);
+        s_idx[p] = ix;
       } else {
-        st_sc[p] = a.cand_score[src];
-        st_ix[p] = a.cand_idx[src];
+        st_sc[p] = sc;
+        st_ix[p] = ix;
+      }
+    };
+    for (int cg = wave; cg < a.chunks; cg += 4 * kWaves) {
+      int cnt_q[4], off_q[4];
+      float sv[4][4];
+      int32_t iv[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = cg + kWaves * q;
+        cnt_q[q] = (c < a.chunks) ? sm.off[c + 1] - sm.off[c] : 0;
+        off_q[q] = (c < a.chunks) ? sm.off[c] : 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = lane + 64 * r;
+          const int64_t src = row + static_cast<int64_t>(c) * kChunk + i;
+          sv[q][r] = (i < cnt_q[q]) ? a.cand_score[src] : 0.0f;
+          iv[q][r] = (i < cnt_q[q]) ? a.cand_idx[src] : 0;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (lane + 64 * r < cnt_q[q]) put(off_q[q] + lane + 64 * r, sv[q][r], iv[q][r]);
+        const int64_t cbase = row + static_cast<int64_t>(cg + kWaves * q) * kChunk;
+        for (int i = 256 + lane; i < cnt_q[q]; i += 64) put(off_q[q] + i, a.cand_score[cbase + i], a.cand_idx[cbase + i]);
       }
     }
     if (!in_lds) {
@@ -676,7 +740,7 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
             const uint32_t key = key_at(i);
             if ((key & mask) == prefix) bin = static_cast<int>((key >> sh) & static_cast<uint32_t>(nb - 1));
           }
-          wave_hist_add(s_hist, bin);
+          hist_add_ties(s_hist, bin);
         }
       }
       __syncthreads();
