@@ -6,7 +6,9 @@ Default workload (the headline): one decode step of a DSA layer at batch 32 x
 quantize the indexer queries, score every non-window token exactly, select the
 top-2048 (lowest index on ties), append the 128-token window, gather the 2176
 rows and run 64-head sparse MLA decode with a sink.  Inputs are synthetic
-(seeded) and resident in HBM before the timed region.
+(seeded) and resident in HBM before the timed region.  The step is issued
+eagerly on one stream (the GPU, not the host, is the bottleneck: HIP graph
+replay and a forked stream for the cache appends both measured slower).
 
 Prints ONE JSON line.  ``value`` = algorithmic HBM bytes per step / step time
 (GB/s), the metric's unit; ``tok_per_s`` = decode tokens per second.
@@ -28,6 +30,11 @@ sys.path.insert(0, str(ROOT / "vllm-ernie_amd"))
 
 METRIC = "KV gather+decode HBM GB/s (% of 8 TB/s); decode tok/s/GPU at 128K ctx"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes one filter_kernel launch moves on the default workload: rocprofv3
+# FETCH_SIZE (557.2 MB) + WRITE_SIZE (9.05 MB) per dispatch, each scaled by what
+# the counter reads for a 512 MiB device copy (x2.0 fetch, x1.0 write; run
+# bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
+FILTER_TRAFFIC_BYTES = 557_203_826 + 9_048_256
 FP8_PEAK_TFLOPS = 5000.0
 
 
@@ -40,6 +47,9 @@ def parse():
     p.add_argument("--ctx", type=int, default=131072)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--copy-mb", type=int, default=0,
+                   help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return p.parse_args()
 
 
@@ -87,18 +97,33 @@ def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
 
 
 def dsa_step(ops, st, ev=None):
-    """One DSA decode step; ``ev`` = (start, end) events around the scorer."""
-    ops.indexer_k_insert(st["k_new"], st["slots"], st["kcache"])
-    ops.kv_append_quant(st["latent_new"], st["slots"], st["latent"])
-    q8, w, digits = ops.indexer_q_quant(st["q_idx"], st["w_idx"])
-    ops.indexer_windowed_lengths(st["positions"], 128, st["lengths"])
-    common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
+    """One DSA decode step, eager; ``ev`` = (start, end) events around the scorer."""
+    dsa_pre(ops, st)
     if ev is not None:
         ev[0].record()
-    ops.indexer_filter(q8, w, *common, st["idx_ws"])
+    dsa_filter(ops, st)
     if ev is not None:
         ev[1].record()
-    ops.indexer_select(digits, w, *common, st["topk"], st["idx_ws"])
+    dsa_post(ops, st)
+
+
+def dsa_pre(ops, st):
+    """Cache appends of the new token, the indexer's q quantization and the
+    windowed lengths."""
+    ops.indexer_k_insert(st["k_new"], st["slots"], st["kcache"])
+    ops.kv_append_quant(st["latent_new"], st["slots"], st["latent"])
+    st["q8"], st["wf"], st["digits"] = ops.indexer_q_quant(st["q_idx"], st["w_idx"])
+    ops.indexer_windowed_lengths(st["positions"], 128, st["lengths"])
+
+
+def dsa_filter(ops, st):
+    common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
+    ops.indexer_filter(st["q8"], st["wf"], *common, st["idx_ws"])
+
+
+def dsa_post(ops, st):
+    common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
+    ops.indexer_select(st["digits"], st["wf"], *common, st["topk"], st["idx_ws"])
     ops.merge_swa_topk(st["topk"], st["merged"], st["positions"], 128)
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
                           block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
@@ -166,6 +191,11 @@ def main():
 
     torch.cuda.init()
     st = build_dsa_decode(torch, ops, args.batch, args.ctx, args.seed)
+    if args.copy_mb > 0:
+        src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        del src, dst
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         dsa_step(ops, st)
@@ -208,13 +238,16 @@ def main():
             "bytes_per_step": by,
         },
         "roofline": {
-            "kernel": "filter_kernel (indexer fp8-MFMA filter over every key row; ekv_indexer_filter)",
+            "kernel": "ekv_indexer_filter = zero_u32_kernel + filter_kernel + bound_kernel (fp8-MFMA filter over "
+                      "every key row); the events bracket the call, so the figure includes the two small kernels",
             "bound": "hbm",
             "achieved": round(filt_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(filt_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": FILTER_TRAFFIC_BYTES if (args.batch, args.ctx) == (32, 131072) else None,
+            "traffic_vs_algorithmic": round(FILTER_TRAFFIC_BYTES / by["indexer_k"], 4)
+            if (args.batch, args.ctx) == (32, 131072) else None,
             "ms": round(filt_ms, 4),
             "bytes_per_launch": by["indexer_k"],
             "mfma_fp8_tflops": round(filt_tflops, 1),

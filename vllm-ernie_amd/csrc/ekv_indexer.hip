@@ -40,6 +40,8 @@
 #include "ekv_common.h"
 #include "ekv_internal.h"
 
+#include <algorithm>
+
 namespace ekv {
 
 constexpr int kIdxDim = 128;
@@ -218,11 +220,6 @@ struct FilterArgs {
   uint32_t* hist;            // [T, kHistBins] counts of L_s key prefixes
 };
 
-#ifndef EKV_FILTER_PAGES_PER_WAVE
-#define EKV_FILTER_PAGES_PER_WAVE 4
-#endif
-constexpr int kFilterPagesPerWave = EKV_FILTER_PAGES_PER_WAVE;
-constexpr int kFilterTokens = 4 * kFilterPagesPerWave * kPageTokens;  // per workgroup
 
 // Block-wide exclusive prefix sum of an int; writes the block total.
 template <int kThreads>
@@ -273,13 +270,25 @@ __device__ __forceinline__ int find_bin(const uint32_t* hist, int nb, int remain
   return bin;
 }
 
+// Workgroup = (group x of row t).  The row's 64-token pages are split into
+// contiguous ranges, one per wave of the row (4 * gridDim.x waves).  A wave
+// streams its range with the next page's rows in flight and the block-table
+// entry of the one after that already read, so start-up latency is paid once
+// per wave.  Upper bounds are staged in LDS and written 16 pages at a time:
+// a store between two page loads would make the wait for the later load also
+// wait for the store (vector memory counts retire in order).
+constexpr int kFilterStage = 32;  // pages of upper bounds staged per wave
+
 __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   __shared__ uint32_t s_hist[kHistBins];
+  __shared__ __align__(16) uint16_t s_up[4][kFilterStage * kPageTokens];
   const int tid = threadIdx.x;
   const int t = blockIdx.y;
   const int n = min(a.lengths[t], a.max_len);
-  const int64_t base_tok = static_cast<int64_t>(blockIdx.x) * kFilterTokens;
-  if (base_tok >= n || n <= a.k) return;  // rows with n <= k need no filtering
+  const int npages = (n + kPageTokens - 1) / kPageTokens;
+  const int W = 4 * static_cast<int>(gridDim.x);  // waves of the row
+  const int per_wave = (npages + W - 1) / W;
+  if (4 * static_cast<int>(blockIdx.x) * per_wave >= npages || n <= a.k) return;  // rows with n <= k need no filtering
   for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0;
 
   const int lane = tid & 63, wave = tid >> 6;
@@ -308,22 +317,19 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   __syncthreads();
 
   const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
-  const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform: scalar page-table loads
-  const int64_t wave_tok = base_tok + static_cast<int64_t>(uwave) * kFilterPagesPerWave * kPageTokens;
-  // page of each of this wave's pages, fetched up front; pages outside the
-  // table read page 0 (always mapped) and are never scored
-  int64_t pages[kFilterPagesPerWave];
-#pragma unroll
-  for (int pg = 0; pg < kFilterPagesPerWave; ++pg) {
-    const int64_t blk = (wave_tok >> 6) + pg;
-    const int64_t p = (blk < a.bt_stride) ? static_cast<int64_t>(bt[blk]) : 0;
-    pages[pg] = (p >= 0 && p < a.num_pages) ? p : 0;
-  }
+  const int wr = __builtin_amdgcn_readfirstlane(4 * static_cast<int>(blockIdx.x) + wave);  // wave of the row
+  const int p_begin = min(wr * per_wave, npages), p_end = min(p_begin + per_wave, npages);
+  // Page-table entry of logical page lp (outside the range or the table:
+  // page 0, always mapped, loaded but never scored).
+  auto page_of = [&](int lp) -> int64_t {
+    const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : 0;
+    return (p >= 0 && p < a.num_pages) ? p : 0;
+  };
   // One page = 4 blocks of 16 tokens; this lane's 32 bytes of each block row,
   // and the scale of row `lane` (one coalesced 256-byte load per page).
   // Loads are unconditional so the compiler keeps them in flight.
-  auto load_page = [&](int pg, uint4 (&kb)[4][2], float& ks) {
-    const uint8_t* pbase = a.kcache + pages[pg] * a.page_stride;
+  auto load_page = [&](int64_t page, uint4 (&kb)[4][2], float& ks) {
+    const uint8_t* pbase = a.kcache + page * a.page_stride;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int row = 16 * b + col;
@@ -333,12 +339,28 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
     }
     ks = *reinterpret_cast<const float*>(pbase + kIdxPageBytes + lane * 4);
   };
+  uint16_t* up_row = a.upper + static_cast<int64_t>(t) * a.max_len;
+  uint16_t* stage = s_up[wave];
+  // Upper bounds of pages [first, first + count) of the stage to global
+  // (coalesced 16-byte stores; element-wise at the end of the row).
+  auto flush = [&](int first, int count) {
+    const int64_t base = static_cast<int64_t>(first) * kPageTokens;
+    const int elems = min(count * kPageTokens, n - static_cast<int>(base));
+    const bool vec = (reinterpret_cast<uintptr_t>(up_row + base) & 15) == 0;
+    for (int e = 8 * lane; e < elems; e += 8 * 64) {
+      if (vec && e + 8 <= elems) {
+        *reinterpret_cast<uint4*>(up_row + base + e) = *reinterpret_cast<const uint4*>(stage + e);
+      } else {
+        for (int j = e; j < min(e + 8, elems); ++j) up_row[base + j] = stage[j];
+      }
+    }
+  };
   uint4 nxt[4][2];
   float nks;
-  load_page(0, nxt, nks);
-  for (int pg = 0; pg < kFilterPagesPerWave; ++pg) {
-    const int64_t ptok = wave_tok + pg * kPageTokens;
-    if (ptok >= n) break;
+  load_page(page_of(p_begin), nxt, nks);
+  int64_t page_after = page_of(p_begin + 1);
+  int staged = 0, stage_first = p_begin;
+  for (int lp = p_begin; lp < p_end; ++lp) {
     uint4 kb[4][2];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -346,7 +368,8 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
       kb[b][1] = nxt[b][1];
     }
     const float page_scale = nks;  // scale of page row `lane`
-    if (pg + 1 < kFilterPagesPerWave) load_page(pg + 1, nxt, nks);  // in flight while this page is scored
+    load_page(page_after, nxt, nks);  // in flight while this page is scored
+    page_after = page_of(lp + 2);
     float mine = 0.0f;  // after the 4 blocks: approximate head sum of token `lane` of the page
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -356,28 +379,37 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
       float acc = 0.0f;
 #pragma unroll
       for (int hb = 0; hb < 4; ++hb) {
-        const f32x4 c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[hb], kv, f32x4{0.f, 0.f, 0.f, 0.f},
-                                                                          0, 0, 0, 0, 0, 0);
+        const f32x4 cc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[hb], kv, f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                           0, 0, 0, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += wv[hb][i] * fmaxf(c[i], 0.0f);
+        for (int i = 0; i < 4; ++i) acc += wv[hb][i] * fmaxf(cc[i], 0.0f);
       }
       acc += __shfl_xor(acc, 16);
       acc += __shfl_xor(acc, 32);
       if (g == b) mine = acc;  // block b's token col is page row 16b + col = this lane
     }
-    const int64_t s = ptok + lane;
-    if (s < n) {
-      const float sc = mine * page_scale;
-      const float e = page_scale * ebound;
-      a.upper[static_cast<int64_t>(t) * a.max_len + s] = bf16_round_up(sc + e);
-      atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
+    const int64_t s = static_cast<int64_t>(lp) * kPageTokens + lane;
+    const float sc = mine * page_scale;
+    const float e = page_scale * ebound;
+    stage[staged * kPageTokens + lane] = bf16_round_up(sc + e);
+    if (s < n) atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
+    if (++staged == kFilterStage) {  // wave-uniform
+      __builtin_amdgcn_wave_barrier();
+      flush(stage_first, staged);
+      __builtin_amdgcn_wave_barrier();
+      staged = 0;
+      stage_first = lp + 1;
     }
+  }
+  if (staged > 0) {
+    __builtin_amdgcn_wave_barrier();
+    flush(stage_first, staged);
   }
   __syncthreads();
   uint32_t* gh = a.hist + static_cast<int64_t>(t) * kHistBins;
   for (int i = tid; i < kHistBins; i += 256) {
-    const uint32_t c = s_hist[i];
-    if (c) atomicAdd(&gh[i], c);
+    const uint32_t v = s_hist[i];
+    if (v) atomicAdd(&gh[i], v);
   }
 }
 
@@ -920,8 +952,10 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const float* w, const ui
                      dim3(256), 0, s, ws.hist, nz);
   FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                max_len, k, ws.upper, ws.hist};
-  hipLaunchKernelGGL(filter_kernel, dim3((max_len + kFilterTokens - 1) / kFilterTokens, num_tokens), dim3(256), 0,
-                     s, f);
+  // About three workgroups per CU in all, each wave streaming many pages.
+  const int64_t pages = (static_cast<int64_t>(max_len) + kPageTokens - 1) / kPageTokens;
+  const int64_t groups = std::max<int64_t>(1, std::min<int64_t>((pages + 3) / 4, (768 + T - 1) / T));
+  hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(groups), num_tokens), dim3(256), 0, s, f);
   hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
   return ekv_launch_status();
 }
