@@ -118,7 +118,7 @@ def dsa_pre(ops, st):
 
 def dsa_filter(ops, st):
     common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
-    ops.indexer_filter(st["q8"], st["wf"], *common, st["idx_ws"])
+    ops.indexer_filter(st["q8"], st["digits"], st["wf"], *common, st["idx_ws"])
 
 
 def dsa_post(ops, st):

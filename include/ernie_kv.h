@@ -176,23 +176,25 @@ int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len);
 
 /*
  * Indexer top-k, stage 1 of 2: fp8-MFMA filter over every token s <
- * lengths[t]: writes an upper bound of each exact score, a histogram of the
- * lower bounds and the resulting candidate bound for top-k into `workspace`.
- * q_fp8 [T, 64, 128] and the folded weights come from ekv_indexer_q_quant.
- * (Paged MQA logits of SparseAttnIndexer, nvidia/attention.py:56-61,
- * 677-685, 982-984.)
+ * lengths[t] with an error bound, then the candidates (tokens whose upper
+ * bound reaches the k-th largest lower bound), scored exactly, into
+ * `workspace`.  When the shape does not allow that in one launch, this stage
+ * leaves the upper bounds and the bound in `workspace` and stage 2 scores the
+ * candidates.  q_fp8 [T, 64, 128], q_digits [T, 3, 64, 128] and the folded
+ * weights come from ekv_indexer_q_quant.  (Paged MQA logits of
+ * SparseAttnIndexer, nvidia/attention.py:56-61, 677-685, 982-984.)
  */
-int ekv_indexer_filter(const uint8_t* q_fp8, const float* w, const uint8_t* kcache,
+int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float* w, const uint8_t* kcache,
                        int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
                        int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
                        int32_t num_tokens, int32_t max_len, int32_t k, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
 /*
- * Indexer top-k, stage 2 of 2 (same workspace): keeps the tokens whose upper
- * bound reaches the k-th largest lower bound, scores them exactly (as
- * ekv_indexer_score) and writes the exact top-k: the k largest by (score
- * desc, index asc), in ascending index order, -1 padded.  Replaces the top-k
+ * Indexer top-k, stage 2 of 2 (same workspace and arguments): scores the
+ * candidates exactly (as ekv_indexer_score) if stage 1 did not, and writes
+ * the exact top-k: the k largest by (score desc, index asc), in ascending
+ * index order, -1 padded.  Replaces the top-k
  * of SparseAttnIndexer (nvidia/attention.py:942-953) that fills
  * indexer_topk_buffer (nvidia/model.py:71-79).
  */

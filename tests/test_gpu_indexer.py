@@ -187,10 +187,79 @@ def test_indexer_topk_stages_match_one_call(dev):
     b = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
     ops.indexer_topk(q8, dig, wf, *args, st["max_len"], a)
     ws = ops.indexer_topk_workspace(T, st["max_len"], dev)
-    ops.indexer_filter(q8, wf, *args, st["max_len"], ws)
+    ops.indexer_filter(q8, dig, wf, *args, st["max_len"], ws)
     ops.indexer_select(dig, wf, *args, st["max_len"], b, ws)
     assert torch.equal(a, b)
     got = a.cpu().numpy()
     for t in range(T):
         row = got[t][got[t] >= 0]
         assert len(row) == min(lengths[t], TOPK) and np.all(row < lengths[t]) and np.all(np.diff(row) > 0)
+
+
+def _device_cache(dev, seed, num_seqs, pages_per_seq, kind):
+    """Indexer cache written on the device by ekv_indexer_k_insert (whose bytes
+    are checked against the oracle in test_gpu_write), pages permuted."""
+    from ernie_kv import ops
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    n = pages_per_seq * 64
+    bt = torch.randperm(num_seqs * pages_per_seq, generator=g, device=dev).to(torch.int32)
+    bt = bt.view(num_seqs, pages_per_seq).contiguous()
+    kcache = torch.zeros((num_seqs * pages_per_seq, 64 * 132), dtype=torch.uint8, device=dev)
+    s = torch.arange(n, device=dev)
+    for b in range(num_seqs):
+        if kind == "constant":  # every score of the row equal: every token is a candidate
+            k = torch.randn(1, 128, generator=g, device=dev).to(torch.bfloat16).expand(n, 128).contiguous()
+        else:
+            k = torch.randn(n, 128, generator=g, device=dev).to(torch.bfloat16)
+        slots = (bt[b, s // 64].to(torch.int64) * 64 + s % 64).contiguous()
+        ops.indexer_k_insert(k, slots, kcache)
+    return bt, kcache
+
+
+def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed):
+    """ekv_indexer_topk against ekv_topk_select over ekv_indexer_score's exact
+    scores (both bit-exact against the oracle in the tests above); returns the
+    workspace of the top-k call."""
+    from ernie_kv import ops
+
+    T = len(lengths)
+    bt, kcache = _device_cache(dev, seed, num_seqs, max_len // 64 + 1, kind)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    req = (torch.arange(T, dtype=torch.int32, device=dev) % num_seqs).contiguous()
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    q = torch.randn(T, 64, 128, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(T, 64, generator=g, device=dev).to(torch.bfloat16)
+    q8, wf, dig = ops.indexer_q_quant(q, w)
+    out = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    ws = ops.indexer_topk_workspace(T, max_len, dev)
+    ops.indexer_topk(q8, dig, wf, kcache, bt, req, lens, max_len, out, ws)
+    scores = torch.empty((T, max_len), dtype=torch.float32, device=dev)
+    ops.indexer_score(dig, wf, kcache, bt, req, lens, max_len, scores)
+    ref = torch.full_like(out, -9)
+    ops.topk_select(scores, lens, TOPK, ref)
+    bad = (out != ref).any(dim=1).nonzero().flatten().tolist()
+    assert not bad, f"rows {bad} differ"
+    return ws
+
+
+@pytest.mark.parametrize("kind", ["normal", "constant"])
+def test_indexer_topk_long_rows_match_exact_path(dev, kind):
+    """Rows long enough that one filter workgroup owns more than 2048 tokens
+    (constant keys: all of them candidates, scored over several passes)."""
+    lengths = [262144, 200000, 131072, 70000, 2049, 5000, 0, 180000]
+    T, max_len = len(lengths), 262144
+    ws = _topk_vs_exact_path(dev, lengths, T, max_len, kind, seed=5)
+    # workspace: 20 B per (row, token), the row histograms, 8 B per row, then
+    # four counters of waits for the bound that gave up
+    off = T * max_len * 20 + T * 4096 * 4 + T * 8
+    assert int(ws[off: off + 16].view(torch.int32).sum()) == 0
+
+
+def test_indexer_topk_many_rows(dev):
+    """More query rows (1100) than one launch of the fused filter can hold
+    at once: the filter / bound / verify kernels run instead."""
+    rng = np.random.default_rng(29)
+    lengths = rng.integers(0, 6000, 1100).astype(np.int32).tolist()
+    lengths[:4] = [0, 2048, 2049, 6000]
+    _topk_vs_exact_path(dev, lengths, 16, 6000, "normal", seed=9)

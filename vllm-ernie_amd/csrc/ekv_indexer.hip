@@ -104,10 +104,14 @@ __device__ __forceinline__ void load_key_i8(const uint8_t* kcache, int64_t page_
 }
 
 // Exact score of the 16 tokens of a block (token = lane % 16); every lane of
-// the column returns the same value.  The head sum order is fixed: per lane
+// the column returns the same value.  qd(hb, d, kh) yields this lane's q digit
+// operand and wv its 16 head weights.  The head sum order is fixed: per lane
 // hb = 0..3, i = 0..3 from +0, then (g0 + g1) + (g2 + g3) across lane groups.
-__device__ __forceinline__ float exact_block(const ExactOperands& op, const uint32_t* s_table, const uint4 kb[2],
-                                             float kscale) {
+// kStaged keeps each head block's operand reads inside its own schedule
+// region (for operands read from LDS: 24 registers live instead of 96).
+template <bool kStaged = false, class QDigits>
+__device__ __forceinline__ float exact_block_with(QDigits qd, const float (&wv)[4][4], const uint32_t* s_table,
+                                                  const uint4 kb[2], float kscale) {
   i32x4 kd[3][2];
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh) {
@@ -126,6 +130,7 @@ __device__ __forceinline__ float exact_block(const ExactOperands& op, const uint
   float acc = 0.0f;
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) {
+    if (kStaged) __builtin_amdgcn_sched_barrier(0);
     i32x4 c[5];
 #pragma unroll
     for (int k = 0; k < 5; ++k) c[k] = i32x4{0, 0, 0, 0};
@@ -135,7 +140,7 @@ __device__ __forceinline__ float exact_block(const ExactOperands& op, const uint
       for (int db = 0; db < 3; ++db)
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
-          c[da + db] = __builtin_amdgcn_mfma_i32_16x16x64_i8(op.qd[hb][da][kh], kd[db][kh], c[da + db], 0, 0, 0);
+          c[da + db] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd(hb, da, kh), kd[db][kh], c[da + db], 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // D = lo + 2^12 c2 + 2^18 hi with lo = c0 + 64 c1, hi = c3 + 64 c4 (each
@@ -147,12 +152,17 @@ __device__ __forceinline__ float exact_block(const ExactOperands& op, const uint
                                       static_cast<double>(lo));
       const float dot = static_cast<float>(Dd * 0x1p-18);
       const float r = fmaxf(dot, 0.0f);
-      acc = acc + op.wv[hb][i] * r;
+      acc = acc + wv[hb][i] * r;
     }
   }
   const float a01 = acc + __shfl_xor(acc, 16);
   const float tot = a01 + __shfl_xor(a01, 32);
   return tot * kscale + 0.0f;
+}
+
+__device__ __forceinline__ float exact_block(const ExactOperands& op, const uint32_t* s_table, const uint4 kb[2],
+                                             float kscale) {
+  return exact_block_with([&](int hb, int d, int kh) { return op.qd[hb][d][kh]; }, op.wv, s_table, kb, kscale);
 }
 
 // ---------------------------------------------------------------------------
@@ -270,30 +280,19 @@ __device__ __forceinline__ int find_bin(const uint32_t* hist, int nb, int remain
   return bin;
 }
 
-// Workgroup = (group x of row t).  The row's 64-token pages are split into
-// contiguous ranges, one per wave of the row (4 * gridDim.x waves).  A wave
-// streams its range with the next page's rows in flight and the block-table
-// entry of the one after that already read, so start-up latency is paid once
-// per wave.  Upper bounds are staged in LDS and written 16 pages at a time:
-// a store between two page loads would make the wait for the later load also
-// wait for the store (vector memory counts retire in order).
-constexpr int kFilterStage = 32;  // pages of upper bounds staged per wave
-
-__global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
-  __shared__ uint32_t s_hist[kHistBins];
-  __shared__ __align__(16) uint16_t s_up[4][kFilterStage * kPageTokens];
-  const int tid = threadIdx.x;
-  const int t = blockIdx.y;
-  const int n = min(a.lengths[t], a.max_len);
+// Pages of each wave: the row's 64-token pages are split into contiguous
+// ranges, one per wave of the row (4 waves per workgroup, `groups`
+// workgroups per row), so workgroup x owns pages [4x, 4x + 4) * per_wave.
+__host__ __device__ inline int filter_per_wave(int n, int groups) {
   const int npages = (n + kPageTokens - 1) / kPageTokens;
-  const int W = 4 * static_cast<int>(gridDim.x);  // waves of the row
-  const int per_wave = (npages + W - 1) / W;
-  if (4 * static_cast<int>(blockIdx.x) * per_wave >= npages || n <= a.k) return;  // rows with n <= k need no filtering
-  for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0;
+  return (npages + 4 * groups - 1) / (4 * groups);
+}
 
-  const int lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, col = lane & 15;
-  i32x8 qa[4];
+// Filter operands of row t for this lane: the fp8 q rows in f8f6f4 A layout,
+// the 16 head weights wv[hb][i] = w[16hb + 4g + i] and the error bound
+// factor 448^2 (2^-8 + 2^-9) sum_h |w_h| (scaled by a token's kscale).
+__device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t, int g, int col, i32x8 (&qa)[4],
+                                                     float (&wv)[4][4], float& ebound) {
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) {
     const uint4* src = reinterpret_cast<const uint4*>(a.q_fp8 + (static_cast<int64_t>(t) * kIdxHeads + 16 * hb + col) * kIdxDim +
@@ -302,7 +301,6 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
     qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
                    static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
   }
-  float wv[4][4];
   float wabs = 0.0f;
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb)
@@ -313,23 +311,36 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
     }
   float ws = (col == 0) ? wabs : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
   for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
-  const float ebound = ws * (448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
-  __syncthreads();
+  ebound = ws * (448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+}
 
+// Streams logical pages of row t: `first`, then the pages next() returns (an
+// increasing sequence; the stream ends at the first page >= p_end).  The next
+// page's rows are in flight and the block-table entry of the one after that
+// already read while a page is scored, so start-up latency is paid once per
+// wave.  Per page, lane l gets the approximate score sc and error e of token
+// 64 lp + l (sc = e = 0 on an unmapped page, whose exact scores are 0) and
+// calls emit(lp, page, sc, e) with page = the block-table entry, or -1 when the
+// page is unmapped; the lower bound sc - e of every token s < n goes into the
+// LDS histogram.
+template <class Next, class Emit>
+__device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
+                                              uint32_t* s_hist, const i32x8 (&qa)[4], const float (&wv)[4][4],
+                                              float ebound, Emit emit) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, col = lane & 15;
   const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
-  const int wr = __builtin_amdgcn_readfirstlane(4 * static_cast<int>(blockIdx.x) + wave);  // wave of the row
-  const int p_begin = min(wr * per_wave, npages), p_end = min(p_begin + per_wave, npages);
-  // Page-table entry of logical page lp (outside the range or the table:
-  // page 0, always mapped, loaded but never scored).
+  // Block-table entry of logical page lp, -1 outside the range, the table or
+  // the cache.  Unmapped pages load page 0 (always present) and score 0.
   auto page_of = [&](int lp) -> int64_t {
-    const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : 0;
-    return (p >= 0 && p < a.num_pages) ? p : 0;
+    const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : -1;
+    return (p >= 0 && p < a.num_pages) ? p : -1;
   };
   // One page = 4 blocks of 16 tokens; this lane's 32 bytes of each block row,
   // and the scale of row `lane` (one coalesced 256-byte load per page).
   // Loads are unconditional so the compiler keeps them in flight.
   auto load_page = [&](int64_t page, uint4 (&kb)[4][2], float& ks) {
-    const uint8_t* pbase = a.kcache + page * a.page_stride;
+    const uint8_t* pbase = a.kcache + (page >= 0 ? page : 0) * a.page_stride;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int row = 16 * b + col;
@@ -339,37 +350,26 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
     }
     ks = *reinterpret_cast<const float*>(pbase + kIdxPageBytes + lane * 4);
   };
-  uint16_t* up_row = a.upper + static_cast<int64_t>(t) * a.max_len;
-  uint16_t* stage = s_up[wave];
-  // Upper bounds of pages [first, first + count) of the stage to global
-  // (coalesced 16-byte stores; element-wise at the end of the row).
-  auto flush = [&](int first, int count) {
-    const int64_t base = static_cast<int64_t>(first) * kPageTokens;
-    const int elems = min(count * kPageTokens, n - static_cast<int>(base));
-    const bool vec = (reinterpret_cast<uintptr_t>(up_row + base) & 15) == 0;
-    for (int e = 8 * lane; e < elems; e += 8 * 64) {
-      if (vec && e + 8 <= elems) {
-        *reinterpret_cast<uint4*>(up_row + base + e) = *reinterpret_cast<const uint4*>(stage + e);
-      } else {
-        for (int j = e; j < min(e + 8, elems); ++j) up_row[base + j] = stage[j];
-      }
-    }
-  };
   uint4 nxt[4][2];
   float nks;
-  load_page(page_of(p_begin), nxt, nks);
-  int64_t page_after = page_of(p_begin + 1);
-  int staged = 0, stage_first = p_begin;
-  for (int lp = p_begin; lp < p_end; ++lp) {
+  int lp = first;
+  int lp1 = next();
+  int64_t cur_page = page_of(lp);
+  load_page(cur_page, nxt, nks);
+  int64_t page1 = page_of(lp1);
+  while (lp < p_end) {
     uint4 kb[4][2];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       kb[b][0] = nxt[b][0];
       kb[b][1] = nxt[b][1];
     }
-    const float page_scale = nks;  // scale of page row `lane`
-    load_page(page_after, nxt, nks);  // in flight while this page is scored
-    page_after = page_of(lp + 2);
+    const int64_t page = cur_page;
+    const float page_scale = page >= 0 ? nks : 0.0f;  // scale of page row `lane`
+    load_page(page1, nxt, nks);  // in flight while this page is scored
+    cur_page = page1;
+    const int lp2 = next();
+    page1 = page_of(lp2);
     float mine = 0.0f;  // after the 4 blocks: approximate head sum of token `lane` of the page
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -391,8 +391,67 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
     const int64_t s = static_cast<int64_t>(lp) * kPageTokens + lane;
     const float sc = mine * page_scale;
     const float e = page_scale * ebound;
-    stage[staged * kPageTokens + lane] = bf16_round_up(sc + e);
     if (s < n) atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
+    emit(lp, page, sc, e);
+    lp = lp1;
+    lp1 = lp2;
+  }
+}
+
+// 12-bit key prefix of the upper bound sc + e rounded up to bf16: a token is a
+// candidate when this prefix reaches the bound bin.
+__device__ __forceinline__ uint16_t upper_prefix(float sc, float e) {
+  return static_cast<uint16_t>(score_key(bf16_to_f32(bf16_round_up(sc + e)) + 0.0f) >> (32 - kHistBits));
+}
+
+// Workgroup = (group x of row t), waves streaming the contiguous page ranges
+// above.  Upper bounds are staged in LDS and written kFilterStage pages at a
+// time: a store between two page loads would make the wait for the later load
+// also wait for the store (vector memory counts retire in order).
+constexpr int kFilterStage = 32;  // pages of upper bounds staged per wave
+
+__global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
+  __shared__ uint32_t s_hist[kHistBins];
+  __shared__ __align__(16) uint16_t s_up[4][kFilterStage * kPageTokens];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.y;
+  const int n = min(a.lengths[t], a.max_len);
+  const int npages = (n + kPageTokens - 1) / kPageTokens;
+  const int per_wave = filter_per_wave(n, static_cast<int>(gridDim.x));
+  if (4 * static_cast<int>(blockIdx.x) * per_wave >= npages || n <= a.k) return;  // rows with n <= k need no filtering
+  for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0;
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  i32x8 qa[4];
+  float wv[4][4];
+  float ebound;
+  load_filter_operands(a, t, g, col, qa, wv, ebound);
+  __syncthreads();
+
+  const int wr = __builtin_amdgcn_readfirstlane(4 * static_cast<int>(blockIdx.x) + wave);  // wave of the row
+  const int p_begin = min(wr * per_wave, npages), p_end = min(p_begin + per_wave, npages);
+  uint16_t* up_row = a.upper + static_cast<int64_t>(t) * a.max_len;
+  uint16_t* stage = s_up[wave];
+  // Upper bounds of pages [first, first + count) of the stage to global
+  // (coalesced 16-byte stores; element-wise at the end of the row).
+  auto flush = [&](int first, int count) {
+    const int64_t base = static_cast<int64_t>(first) * kPageTokens;
+    const int elems = min(count * kPageTokens, n - static_cast<int>(base));
+    const bool vec = (reinterpret_cast<uintptr_t>(up_row + base) & 15) == 0;
+    for (int e = 8 * lane; e < elems; e += 8 * 64) {
+      if (vec && e + 8 <= elems) {
+        *reinterpret_cast<uint4*>(up_row + base + e) = *reinterpret_cast<const uint4*>(stage + e);
+      } else {
+        for (int j = e; j < min(e + 8, elems); ++j) up_row[base + j] = stage[j];
+      }
+    }
+  };
+  int staged = 0, stage_first = p_begin;
+  int seq = p_begin;
+  filter_stream(a, t, n, p_begin, p_end, [&] { return ++seq; }, s_hist, qa, wv, ebound,
+                [&](int lp, int64_t, float sc, float e) {
+    stage[staged * kPageTokens + lane] = bf16_round_up(sc + e);
     if (++staged == kFilterStage) {  // wave-uniform
       __builtin_amdgcn_wave_barrier();
       flush(stage_first, staged);
@@ -400,7 +459,7 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
       staged = 0;
       stage_first = lp + 1;
     }
-  }
+  });
   if (staged > 0) {
     __builtin_amdgcn_wave_barrier();
     flush(stage_first, staged);
@@ -605,6 +664,263 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Filter + verify in one launch.  Every workgroup of the grid is resident at
+// once (the host sizes the grid from the occupancy), so the upper bounds stay
+// in LDS: each workgroup streams its contiguous page range, adds its
+// lower-bound histogram to the row's, and the last workgroup of the row to
+// arrive turns the complete histogram into the bound and publishes it.  Each
+// workgroup then lists its own candidates in token order and scores them
+// exactly into its segment's slice.
+// Within a workgroup the waves take pages one at a time from an LDS counter:
+// the hardware issues the oldest waves first, so a static split would leave
+// the youngest waves finishing last.
+// The wait for the bound is bounded: a workgroup that gives up takes bin 0,
+// which makes every token of its segment a candidate -- slower, still exact.
+// ---------------------------------------------------------------------------
+struct FusedArgs {
+  FilterArgs f;              // f.upper is not used
+  const int8_t* q_digits;    // [T, 3, 64, 128]
+  uint32_t* arrive;          // [T] workgroups past their histogram flush (zeroed)
+  uint32_t* kword;           // [T] (bound bin << 20) | 1 once published (zeroed)
+  uint32_t* timeouts;        // waits that gave up (diagnostic; zeroed)
+  float* cand_score;         // [T, max_len] segment slices
+  int32_t* cand_idx;
+  int32_t* cand_count;       // [T, groups]
+  int32_t groups;
+  int32_t stage_pages;       // LDS capacity in pages (>= pages per workgroup of every row)
+};
+
+// Pages of each workgroup's segment: workgroup x of a row owns logical pages
+// [x, x + 1) * fused_group_pages.
+__host__ __device__ inline int fused_group_pages(int n, int groups) {
+  const int npages = (n + kPageTokens - 1) / kPageTokens;
+  return (npages + groups - 1) / groups;
+}
+
+constexpr int kFusedQdBytes = 4 * 3 * 2 * 64 * 16;  // q digit operands [hb][digit][K half][lane]
+constexpr int kFusedSpinLimit = 1 << 14;
+
+template <int kWaves>
+struct FusedLayout {
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kList = 8 * kThreads;  // candidates scored per pass (>= one compaction round)
+  static constexpr int kFixed = kFusedQdBytes + 256 * 4 + kList * 4 + 32 * 4;
+  static constexpr int bytes(int stage_pages) { return kFixed + stage_pages * (4 + 2 * kPageTokens); }
+};
+
+template <int kWaves>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) filter_verify_kernel(FusedArgs a) {
+  using Lay = FusedLayout<kWaves>;
+  constexpr int kThreads = Lay::kThreads;
+  extern __shared__ __align__(16) uint8_t fused_smem[];
+  uint32_t* s_hist = reinterpret_cast<uint32_t*>(fused_smem);     // phase 1
+  const uint4* s_qd = reinterpret_cast<const uint4*>(fused_smem);  // phases 2-3 (same bytes)
+  uint32_t* s_table = reinterpret_cast<uint32_t*>(fused_smem + kFusedQdBytes);
+  int32_t* s_list = reinterpret_cast<int32_t*>(s_table + 256);
+  int* s_misc = reinterpret_cast<int*>(s_list + Lay::kList);  // [0..15] scans, [16] last, [17] bin, [18] next page
+  int32_t* s_pages = reinterpret_cast<int32_t*>(s_misc + 32);
+  uint16_t* s_pref = reinterpret_cast<uint16_t*>(s_pages + a.stage_pages);
+
+  const int tid = threadIdx.x;
+  const int t = blockIdx.y, x = blockIdx.x;
+  const FilterArgs& f = a.f;
+  const int n = max(0, min(f.lengths[t], f.max_len));
+  const int npages = (n + kPageTokens - 1) / kPageTokens;
+  const int per_group = fused_group_pages(n, a.groups);
+  const int wg_p0 = x * per_group, wg_p1 = min(wg_p0 + per_group, npages);
+  const int seg0 = wg_p0 * kPageTokens;  // first token of this workgroup's segment
+  const int seg_len = min(per_group * kPageTokens, n - seg0);
+  const int64_t out0 = static_cast<int64_t>(t) * f.max_len + seg0;
+  int32_t* count = a.cand_count + static_cast<int64_t>(t) * a.groups + x;
+  if (seg_len <= 0) {  // no pages in this segment
+    if (tid == 0) *count = 0;
+    return;
+  }
+  if (n <= f.k) {  // every token is selected: list them, no scores needed
+    for (int i = tid; i < seg_len; i += kThreads) a.cand_idx[out0 + i] = seg0 + i;
+    if (tid == 0) *count = seg_len;
+    return;
+  }
+  for (int i = tid; i < kHistBins; i += kThreads) s_hist[i] = 0;
+  if (tid < 256) s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  if (tid == 0) s_misc[18] = wg_p0 + kWaves;  // wave w starts at page wg_p0 + w
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  i32x8 qa[4];
+  float wv[4][4];
+  float ebound;
+  load_filter_operands(f, t, g, col, qa, wv, ebound);
+  __syncthreads();
+
+  // Phase 1: stream the pages; upper-bound prefixes and page entries to LDS.
+  auto grab = [&]() -> int {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&s_misc[18], 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  filter_stream(f, t, n, wg_p0 + wave, wg_p1, grab, s_hist, qa, wv, ebound,
+                [&](int lp, int64_t page, float sc, float e) {
+                  s_pref[(lp - wg_p0) * kPageTokens + lane] = upper_prefix(sc, e);
+                  if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
+                });
+  __syncthreads();
+  uint32_t* gh = f.hist + static_cast<int64_t>(t) * kHistBins;
+  for (int i = tid; i < kHistBins; i += kThreads) {
+    const uint32_t v = s_hist[i];
+    if (v) atomicAdd(&gh[i], v);
+  }
+  // q digit operands, into the histogram's LDS once every lane is past it.
+  constexpr int kQdPer = (kFusedQdBytes / 16) / kThreads;
+  static_assert(kQdPer * kThreads * 16 == kFusedQdBytes, "q digit staging must divide evenly");
+  uint4 qd_regs[kQdPer];
+#pragma unroll
+  for (int j = 0; j < kQdPer; ++j) {
+    const int idx = tid + kThreads * j;  // entry e = (hb * 3 + d) * 2 + kh, lane ln
+    const int e = idx >> 6, ln = idx & 63;
+    const int hb = e / 6, d = (e / 2) % 3, kh = e & 1;
+    const int lg = ln >> 4, lc = ln & 15;
+    qd_regs[j] = *reinterpret_cast<const uint4*>(a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + lc) *
+                                                                  kIdxDim + 64 * kh + 16 * lg);
+  }
+  // Every histogram atomic of the workgroup has completed before it arrives.
+  // No cache maintenance is needed: device-scope atomics and the agent-scope
+  // loads and stores below are coherent across the L2s, and a histogram read
+  // before some adds were visible could only lower the bound (more
+  // candidates, still exact).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // Phase 2: arrive; the last workgroup of the row publishes the bound.
+  const int groups_row = (npages + per_group - 1) / per_group;
+  if (tid == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(a.arrive + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_misc[16] = (before + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
+    s_misc[17] = 0;
+  }
+  uint4* s_qd_w = reinterpret_cast<uint4*>(fused_smem);
+#pragma unroll
+  for (int j = 0; j < kQdPer; ++j) s_qd_w[tid + kThreads * j] = qd_regs[j];
+  __syncthreads();
+  if (s_misc[16]) {
+    constexpr int kBinsPer = (kHistBins + kThreads - 1) / kThreads;  // scanned from the top bin down
+    const int r0 = kBinsPer * tid;
+    int c[kBinsPer];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j) {
+      c[j] = (r0 + j < kHistBins) ? static_cast<int>(__hip_atomic_load(gh + (kHistBins - 1 - (r0 + j)), __ATOMIC_RELAXED,
+                                                                        __HIP_MEMORY_SCOPE_AGENT))
+                                  : 0;
+      sum += c[j];
+    }
+    int total;
+    int excl = block_scan_excl<kThreads>(sum, s_misc, total);
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j) {
+      if (excl < f.k && f.k <= excl + c[j]) s_misc[17] = kHistBins - 1 - (r0 + j);
+      excl += c[j];
+    }
+    __syncthreads();
+    if (tid == 0)
+      __hip_atomic_store(a.kword + t, (static_cast<uint32_t>(s_misc[17]) << (32 - kHistBits)) | 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  } else if (tid == 0) {
+    uint32_t v = 0;
+    for (int spins = 0; spins < kFusedSpinLimit; ++spins) {
+      v = __hip_atomic_load(a.kword + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v != 0) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+    if (v == 0) atomicAdd(a.timeouts, 1u);  // bin 0: every token is a candidate
+    s_misc[17] = static_cast<int>(v >> (32 - kHistBits));
+  }
+  __syncthreads();
+  const uint32_t bin = static_cast<uint32_t>(s_misc[17]);
+
+  // Phase 3: candidates of the segment in order, scored Lay::kList at a time.
+  auto score_list = [&](int cnt, int base) {
+    __syncthreads();
+    constexpr int kBatch = 2;
+    for (int bb = wave * 16; bb < cnt; bb += 16 * kWaves * kBatch) {
+      int tok[kBatch];
+      int64_t page[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int li = bb + 16 * kWaves * j + col;
+        tok[j] = (li < cnt) ? s_list[li] : -1;  // offset in the segment
+        page[j] = (tok[j] >= 0) ? static_cast<int64_t>(s_pages[tok[j] >> 6]) : -1;
+      }
+      uint4 kb[kBatch][2];
+      float ks[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const bool ok = page[j] >= 0;  // mapped pages only (checked when streamed)
+        const uint8_t* base_p = f.kcache + (ok ? page[j] : 0) * f.page_stride;
+        const int r = tok[j] & 63;
+        const uint4 k0 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 16 * g);
+        const uint4 k1 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 64 + 16 * g);
+        const float sc = *reinterpret_cast<const float*>(base_p + kIdxPageBytes + r * 4);
+        kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
+        kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
+        ks[j] = ok ? sc : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int b0 = bb + 16 * kWaves * j;
+        if (b0 >= cnt) break;
+        const float sc = exact_block_with<true>(
+            [&](int hb, int d, int kh) {
+              const uint4 v = s_qd[((hb * 3 + d) * 2 + kh) * 64 + lane];
+              return i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+            },
+            wv, s_table, kb[j], ks[j]);
+        const int li = b0 + col;
+        if (li < cnt && g == 0) {
+          a.cand_score[out0 + base + li] = sc;
+          a.cand_idx[out0 + base + li] = seg0 + tok[j];
+        }
+      }
+    }
+    __syncthreads();
+  };
+  int out_n = 0, list_n = 0;
+  for (int r0 = 0; r0 < seg_len; r0 += 8 * kThreads) {
+    const int o0 = r0 + 8 * tid;
+    uint32_t flags = 0;
+    int cnt = 0;
+    if (o0 < seg_len) {
+      const uint4 v = *reinterpret_cast<const uint4*>(s_pref + o0);
+      const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t pref = (wds[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+        if (o0 + j < seg_len && pref >= bin) {
+          flags |= 1u << j;
+          ++cnt;
+        }
+      }
+    }
+    int rtot;
+    const int ex = block_scan_excl<kThreads>(cnt, s_misc, rtot);
+    if (list_n + rtot > Lay::kList) {  // uniform
+      score_list(list_n, out_n);
+      out_n += list_n;
+      list_n = 0;
+    }
+    int pos = list_n + ex;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (flags & (1u << j)) s_list[pos++] = o0 + j;
+    list_n += rtot;
+  }
+  if (list_n > 0) {
+    score_list(list_n, out_n);
+    out_n += list_n;
+  }
+  if (tid == 0) *count = out_n;
+}
+
+// ---------------------------------------------------------------------------
 // Exact select: top-k by (score desc, index asc), written ascending, -1 padded.
 // Sources: an implicit range of scores, or per-chunk candidate lists that are
 // concatenated (in chunk order) into LDS, or -- when they do not fit -- into a
@@ -628,6 +944,8 @@ struct SelectArgs {
   int64_t out_stride;
   int32_t k;
   int32_t max_len;
+  int32_t seg_groups;        // chunk mode: 0 = lists of kChunk-token chunks, else of
+                             // filter_verify_kernel segments (`seg_groups` per row)
 };
 
 constexpr int kSelMaxChunks = 4096;  // up to 8M-token rows
@@ -700,6 +1018,9 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     __syncthreads();
     in_lds = n <= kSelLds;
     const int64_t row = static_cast<int64_t>(t) * a.max_len;
+    const int64_t seg = a.seg_groups > 0
+                            ? kPageTokens * fused_group_pages(max(0, min(a.lengths[t], a.max_len)), a.seg_groups)
+                            : kChunk;  // tokens per list slice
     float* st_sc = a.stage_score + row;
     int32_t* st_ix = a.stage_idx + row;
     // Wave w copies chunks w, w+16, ...: four chunks at a time, the first 256
@@ -727,7 +1048,7 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = lane + 64 * r;
-          const int64_t src = row + static_cast<int64_t>(c) * kChunk + i;
+          const int64_t src = row + c * seg + i;
           sv[q][r] = (i < cnt_q[q]) ? a.cand_score[src] : 0.0f;
           iv[q][r] = (i < cnt_q[q]) ? a.cand_idx[src] : 0;
         }
@@ -737,7 +1058,7 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (lane + 64 * r < cnt_q[q]) put(off_q[q] + lane + 64 * r, sv[q][r], iv[q][r]);
-        const int64_t cbase = row + static_cast<int64_t>(cg + kWaves * q) * kChunk;
+        const int64_t cbase = row + (cg + kWaves * q) * seg;
         for (int i = 256 + lane; i < cnt_q[q]; i += 64) put(off_q[q] + i, a.cand_score[cbase + i], a.cand_idx[cbase + i]);
       }
     }
@@ -843,9 +1164,18 @@ void launch_select(const SelectArgs& a, int32_t rows, hipStream_t s) {
 
 int num_chunks(int32_t max_len) { return max_len > 0 ? (max_len + kChunk - 1) / kChunk : 1; }
 
-// workspace: upper f32 [T,L] | cand_score f32 [T,L] | cand_idx i32 [T,L] |
-//            stage_score f32 [T,L] | stage_idx i32 [T,L] | hist u32 [T,4096] |
-//            done u32 [T] | kbound u32 [T] | counts i32 [T, chunks]
+// Workgroups the filter targets in all: about three per CU, each wave
+// streaming many pages.
+constexpr int64_t kFilterTargetGroups = 768;
+
+// Count slots [T, groups] of either path: chunks per row, or segments (at most
+// ceil(kFilterTargetGroups / T) per row).
+int64_t count_slots(int64_t T, int32_t max_len) { return T * num_chunks(max_len) + T + kFilterTargetGroups; }
+
+// workspace: upper u16 [T,L] (4 B per entry reserved) | cand_score f32 [T,L] |
+//            cand_idx i32 [T,L] | stage_score f32 [T,L] | stage_idx i32 [T,L] |
+//            hist u32 [T,4096] | arrive u32 [T] | kbound u32 [T] |
+//            timeouts u32 [4] | counts i32 [count_slots]
 struct TopkWorkspace {
   uint16_t* upper;
   float* cand_score;
@@ -853,12 +1183,13 @@ struct TopkWorkspace {
   float* stage_score;
   int32_t* stage_idx;
   uint32_t* hist;
-  uint32_t* done;
+  uint32_t* arrive;
   uint32_t* kbound;
+  uint32_t* timeouts;
   int32_t* counts;
 };
 
-TopkWorkspace carve(void* workspace, int64_t T, int64_t L, int chunks) {
+TopkWorkspace carve(void* workspace, int64_t T, int64_t L) {
   TopkWorkspace w;
   w.upper = static_cast<uint16_t*>(workspace);
   w.cand_score = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + T * L * 4);
@@ -866,11 +1197,78 @@ TopkWorkspace carve(void* workspace, int64_t T, int64_t L, int chunks) {
   w.stage_score = reinterpret_cast<float*>(w.cand_idx + T * L);
   w.stage_idx = reinterpret_cast<int32_t*>(w.stage_score + T * L);
   w.hist = reinterpret_cast<uint32_t*>(w.stage_idx + T * L);
-  w.done = w.hist + T * kHistBins;
-  w.kbound = w.done + T;
-  w.counts = reinterpret_cast<int32_t*>(w.kbound + T);
-  (void)chunks;
+  w.arrive = w.hist + T * kHistBins;
+  w.kbound = w.arrive + T;
+  w.timeouts = w.kbound + T;
+  w.counts = reinterpret_cast<int32_t*>(w.timeouts + 4);
   return w;
+}
+
+// How the filter runs for (T, max_len) on the current device.  Fused: one
+// 12-wave workgroup per CU when the rows allow, else 4-wave workgroups (about
+// three per CU), if the grid fits on the device at once and its LDS staging
+// fits a CU.  Otherwise the filter / bound / verify kernels.  Both stages of
+// a top-k call make the same plan.
+struct FilterPlan {
+  bool fused;
+  int waves;        // fused: waves per workgroup (12 or 4)
+  int groups;       // workgroups per row
+  int stage_pages;  // fused: LDS pages per workgroup
+  int smem;         // fused: dynamic LDS bytes
+};
+
+constexpr int kLdsPerCu = 160 * 1024;
+
+// Workgroups of `kernel` (threads, smem) resident per CU; cached per thread.
+int occupancy(const void* kernel, int threads, int smem) {
+  struct Entry {
+    const void* kernel;
+    int smem, occ;
+  };
+  static thread_local Entry cache[4] = {};
+  static thread_local int next = 0;
+  for (const Entry& e : cache)
+    if (e.kernel == kernel && e.smem == smem) return e.occ;
+  int occ = 0;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, smem) != hipSuccess)
+    occ = 0;
+  cache[next] = Entry{kernel, smem, occ};
+  next = (next + 1) & 3;
+  return occ;
+}
+
+template <int kWaves>
+bool plan_fused(int64_t T, int32_t max_len, int64_t pages, int cus, int64_t target_groups, FilterPlan& p) {
+  const void* kernel = reinterpret_cast<const void*>(filter_verify_kernel<kWaves>);
+  int64_t groups = std::max<int64_t>(1, std::min<int64_t>((pages + kWaves - 1) / kWaves, (target_groups + T - 1) / T));
+  for (int attempt = 0; attempt < 4 && groups >= 1; ++attempt) {
+    const int per_group = fused_group_pages(max_len, static_cast<int>(groups));
+    const int stage = std::max(4, (per_group + 3) & ~3);
+    const int smem = FusedLayout<kWaves>::bytes(stage);
+    if (smem > kLdsPerCu) return false;
+    const int64_t capacity = static_cast<int64_t>(occupancy(kernel, 64 * kWaves, smem)) * cus;
+    if (T * groups <= capacity && T * groups <= count_slots(T, max_len)) {
+      p = FilterPlan{true, kWaves, static_cast<int>(groups), stage, smem};
+      return true;
+    }
+    groups = capacity / T;
+  }
+  return false;
+}
+
+FilterPlan plan_filter(int64_t T, int32_t max_len) {
+  const int64_t pages = (static_cast<int64_t>(max_len) + kPageTokens - 1) / kPageTokens;
+  FilterPlan p{false, 4, 1, 0, 0};
+  p.groups = static_cast<int>(
+      std::max<int64_t>(1, std::min<int64_t>((pages + 3) / 4, (kFilterTargetGroups + T - 1) / T)));
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return p;
+  if (T <= cus && plan_fused<12>(T, max_len, pages, cus, cus, p)) return p;
+  if (plan_fused<4>(T, max_len, pages, cus, kFilterTargetGroups, p)) return p;
+  return p;
 }
 
 }  // namespace
@@ -878,7 +1276,7 @@ TopkWorkspace carve(void* workspace, int64_t T, int64_t L, int chunks) {
 extern "C" int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len) {
   if (num_tokens <= 0) return 0;
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
-  return T * L * 20 + T * kHistBins * 4 + T * 8 + T * num_chunks(max_len) * 4 + 256;
+  return T * L * 20 + T * kHistBins * 4 + T * 8 + 16 + count_slots(T, max_len) * 4 + 256;
 }
 
 extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const uint8_t* kcache,
@@ -908,7 +1306,7 @@ extern "C" int ekv_topk_select(const float* scores, int64_t scores_stride, const
   EKV_CHECK(out_stride >= k, "out_stride must be >= k");
   EKV_CHECK(max_len >= 0 && scores_stride >= max_len, "scores_stride must be >= max_len");
   SelectArgs s{scores, scores_stride, lengths, nullptr, nullptr, nullptr, 0, nullptr, nullptr, out, out_stride, k,
-               max_len};
+               max_len, 0};
   launch_select(s, num_tokens, static_cast<hipStream_t>(stream));
   return ekv_launch_status();
 }
@@ -933,34 +1331,46 @@ int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_
 
 }  // namespace
 
-// Stage 1: fp8-MFMA filter (upper bounds, lower-bound histogram, key bound).
-extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const float* w, const uint8_t* kcache, int64_t page_stride,
-                                  int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
-                                  const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
-                                  int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes,
-                                  void* stream) {
+// Stage 1: fp8-MFMA filter.  Fused plan: filter, bound and exact scoring of
+// the candidates in one launch.  Otherwise: upper bounds, lower-bound
+// histogram and key bound; the candidates are scored in stage 2.
+extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
+                                  const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                  const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                  const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t k,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_topk_args(q_fp8, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
                            workspace, workspace_bytes);
   if (rc) return rc;
-  if (num_tokens == 0 || max_len == 0) return 0;
+  EKV_CHECK(q_digits != nullptr && aligned16(q_digits), "q_digits must be a 16-byte aligned [T, 3, 64, 128]");
+  if (num_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t T = num_tokens;
-  TopkWorkspace ws = carve(workspace, T, max_len, num_chunks(max_len));
-  const int64_t nz = T * kHistBins + 2 * T;  // hist, done (kbound is written before use)
+  const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
+  TopkWorkspace ws = carve(workspace, T, L);
+  const int64_t nz = T * kHistBins + 2 * T + 4;  // hist, arrive, kbound, timeouts
   const int64_t zero_blocks = (nz + 255) / 256;
   hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
                      dim3(256), 0, s, ws.hist, nz);
   FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                max_len, k, ws.upper, ws.hist};
-  // About three workgroups per CU in all, each wave streaming many pages.
-  const int64_t pages = (static_cast<int64_t>(max_len) + kPageTokens - 1) / kPageTokens;
-  const int64_t groups = std::max<int64_t>(1, std::min<int64_t>((pages + 3) / 4, (768 + T - 1) / T));
-  hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(groups), num_tokens), dim3(256), 0, s, f);
-  hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
+  const FilterPlan plan = plan_filter(T, max_len);
+  if (plan.fused) {
+    FusedArgs fa{f, q_digits, ws.arrive, ws.kbound, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
+                 plan.groups, plan.stage_pages};
+    const dim3 grid(static_cast<unsigned>(plan.groups), num_tokens);
+    if (plan.waves == 12)
+      hipLaunchKernelGGL(filter_verify_kernel<12>, grid, dim3(64 * 12), plan.smem, s, fa);
+    else
+      hipLaunchKernelGGL(filter_verify_kernel<4>, grid, dim3(64 * 4), plan.smem, s, fa);
+  } else if (max_len > 0) {
+    hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(plan.groups), num_tokens), dim3(256), 0, s, f);
+    hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
+  }
   return ekv_launch_status();
 }
 
-// Stage 2: exact scores of the candidates of each chunk, then exact select.
+// Stage 2: (unfused plan) exact scores of the candidates of each chunk; then
+// the exact select over the candidate lists.
 extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache, int64_t page_stride,
                                   int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
                                   const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
@@ -974,14 +1384,18 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   const int chunks = num_chunks(max_len);
-  TopkWorkspace ws = carve(workspace, T, L, chunks);
-  VerifyArgs v{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-               max_len, k, ws.upper, ws.kbound, ws.cand_score, ws.cand_idx, ws.counts, chunks};
-  hipLaunchKernelGGL(verify_kernel, dim3((chunks + kVerifyChunks - 1) / kVerifyChunks, num_tokens), dim3(256), 0, s,
-                     v);
-  SelectArgs sel{nullptr, 0, nullptr, ws.cand_score, ws.cand_idx, ws.counts, chunks, ws.stage_score, ws.stage_idx,
-                 topk_out, out_stride, k, static_cast<int32_t>(L)};
   EKV_CHECK(chunks <= kSelMaxChunks, "max_len too large for the select stage");
+  TopkWorkspace ws = carve(workspace, T, L);
+  const FilterPlan plan = plan_filter(T, max_len);
+  if (!plan.fused) {
+    VerifyArgs v{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+                 max_len, k, ws.upper, ws.kbound, ws.cand_score, ws.cand_idx, ws.counts, chunks};
+    hipLaunchKernelGGL(verify_kernel, dim3((chunks + kVerifyChunks - 1) / kVerifyChunks, num_tokens), dim3(256), 0,
+                       s, v);
+  }
+  SelectArgs sel{nullptr, 0, lengths, ws.cand_score, ws.cand_idx, ws.counts, plan.fused ? plan.groups : chunks,
+                 ws.stage_score, ws.stage_idx, topk_out, out_stride, k, static_cast<int32_t>(L),
+                 plan.fused ? plan.groups : 0};
   launch_select(sel, num_tokens, s);
   return ekv_launch_status();
 }
@@ -992,8 +1406,8 @@ extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, co
                                 const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
                                 int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
                                 void* stream) {
-  int rc = ekv_indexer_filter(q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-                              num_tokens, max_len, k, workspace, workspace_bytes, stream);
+  int rc = ekv_indexer_filter(q_fp8, q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids,
+                              lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                             num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, stream);

@@ -266,21 +266,23 @@ def _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T):
     _need(lengths.dtype == torch.int32 and req_ids.dtype == torch.int32, "lengths/req_ids int32")
 
 
-def indexer_filter(q_fp8, w, kcache, block_table, req_ids, lengths, max_len: int, workspace: torch.Tensor,
-                   k: int = 2048) -> None:
-    """Stage 1: fp8-MFMA filter (upper bounds, lower-bound histogram, top-k bound) into ``workspace``."""
+def indexer_filter(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, max_len: int,
+                   workspace: torch.Tensor, k: int = 2048) -> None:
+    """Stage 1: fp8-MFMA filter, candidate bound and (when it fits one launch)
+    the candidates' exact scores, into ``workspace``."""
     T = q_fp8.shape[0]
-    _topk_common(q_fp8, None, w, kcache, block_table, req_ids, lengths, T)
+    _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T)
     _lib.call(
-        "ekv_indexer_filter", q_fp8.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
-        block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T, int(max_len), int(k),
-        workspace.data_ptr(), workspace.numel(), _stream(),
+        "ekv_indexer_filter", q_fp8.data_ptr(), q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache),
+        kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T,
+        int(max_len), int(k), workspace.data_ptr(), workspace.numel(), _stream(),
     )
 
 
 def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: int, topk_out: torch.Tensor,
                    workspace: torch.Tensor) -> None:
-    """Stage 2: candidates, their exact scores, exact top-k (ascending, -1 padded)."""
+    """Stage 2: the candidates' exact scores (if stage 1 left them), exact top-k
+    (ascending, -1 padded)."""
     T = q_digits.shape[0]
     _topk_common(None, q_digits, w, kcache, block_table, req_ids, lengths, T)
     _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
