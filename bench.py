@@ -30,11 +30,11 @@ sys.path.insert(0, str(ROOT / "vllm-ernie_amd"))
 
 METRIC = "KV gather+decode HBM GB/s (% of 8 TB/s); decode tok/s/GPU at 128K ctx"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes one filter_kernel launch moves on the default workload: rocprofv3
-# FETCH_SIZE (557.2 MB) + WRITE_SIZE (9.05 MB) per dispatch, each scaled by what
-# the counter reads for a 512 MiB device copy (x2.0 fetch, x1.0 write; run
-# bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
-FILTER_TRAFFIC_BYTES = 557_203_826 + 9_048_256
+# HBM bytes one filter_verify_kernel launch moves on the default workload:
+# rocprofv3 FETCH_SIZE (588.8 MB) + WRITE_SIZE (7.56 MB) per dispatch, each
+# scaled by what the counter reads for a 512 MiB device copy (x2.0 fetch, x1.0
+# write; run bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
+FILTER_TRAFFIC_BYTES = 588_804_045 + 7_559_136
 FP8_PEAK_TFLOPS = 5000.0
 
 
@@ -238,8 +238,9 @@ def main():
             "bytes_per_step": by,
         },
         "roofline": {
-            "kernel": "ekv_indexer_filter = zero_u32_kernel + filter_kernel + bound_kernel (fp8-MFMA filter over "
-                      "every key row); the events bracket the call, so the figure includes the two small kernels",
+            "kernel": "ekv_indexer_filter = zero_u32_kernel + filter_verify_kernel<12> (fp8-MFMA filter over every "
+                      "key row, candidate bound, exact scoring of the candidates); the events bracket the call, so "
+                      "the figure includes the small zeroing kernel",
             "bound": "hbm",
             "achieved": round(filt_gbs, 1),
             "peak": HBM_PEAK_GBS,
