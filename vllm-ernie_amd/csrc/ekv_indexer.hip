@@ -840,7 +840,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // Phase 3: candidates of the segment in order, scored Lay::kList at a time.
   auto score_list = [&](int cnt, int base) {
     __syncthreads();
-    constexpr int kBatch = 2;
+    constexpr int kBatch = 3;  // blocks whose key rows are loaded together
     for (int bb = wave * 16; bb < cnt; bb += 16 * kWaves * kBatch) {
       int tok[kBatch];
       int64_t page[kBatch];
@@ -883,6 +883,40 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     __syncthreads();
   };
+  // One scan over the whole segment (kOnePass groups of 8 tokens per thread)
+  // when it is short enough and its candidates fit the list.
+  constexpr int kOnePass = 3;
+  if (seg_len <= 8 * kOnePass * kThreads) {
+    const int o0 = 8 * kOnePass * tid;
+    uint32_t flags = 0;
+    int cnt = 0;
+#pragma unroll
+    for (int v4 = 0; v4 < kOnePass; ++v4) {
+      const int o = o0 + 8 * v4;
+      if (o < seg_len) {
+        const uint4 v = *reinterpret_cast<const uint4*>(s_pref + o);
+        const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t pref = (wds[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+          if (o + j < seg_len && pref >= bin) {
+            flags |= 1u << (8 * v4 + j);
+            ++cnt;
+          }
+        }
+      }
+    }
+    int tot;
+    int pos = block_scan_excl<kThreads>(cnt, s_misc, tot);
+    if (tot <= Lay::kList) {  // uniform
+#pragma unroll
+      for (int b = 0; b < 8 * kOnePass; ++b)
+        if (flags & (1u << b)) s_list[pos++] = o0 + b;
+      if (tot > 0) score_list(tot, 0);
+      if (tid == 0) *count = tot;
+      return;
+    }
+  }
   int out_n = 0, list_n = 0;
   for (int r0 = 0; r0 < seg_len; r0 += 8 * kThreads) {
     const int o0 = r0 + 8 * tid;
@@ -953,10 +987,12 @@ constexpr int kSelMaxChunks = 4096;  // up to 8M-token rows
 struct SelectSmem {
   uint32_t key[kSelLds];
   int32_t idx[kSelLds];
-  int off[kSelMaxChunks + 1];
   uint32_t hist[2048];
+  int off[kSelMaxChunks + 1];
   int wave[kSelThreads / 64];
+  uint32_t wmin[kSelThreads / 64], wmax[kSelThreads / 64];  // per-wave key range
   int res[2];
+  int cnt;
 };
 
 // LDS histogram increment: one atomic for the whole wave when every active
@@ -987,7 +1023,8 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   const int k = a.k;
   int32_t* out = a.out + static_cast<int64_t>(t) * a.out_stride;
 
-  // gather the elements
+  // gather the elements; lo / hi track the range of the keys put in LDS
+  uint32_t lo = 0xffffffffu, hi = 0u;
   int n;
   const float* gsc = nullptr;     // global scores (implicit mode or spilled lists)
   const int32_t* gidx = nullptr;  // global indices (spilled lists); null = implicit
@@ -998,8 +1035,11 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     in_lds = n <= kSelLds;
     if (in_lds)
       for (int i = tid; i < n; i += kSelThreads) {
-        s_key[i] = score_key(gsc[i] + 0.0f);  // -0 ties with +0
+        const uint32_t key = score_key(gsc[i] + 0.0f);  // -0 ties with +0
+        s_key[i] = key;
         s_idx[i] = i;
+        lo = min(lo, key);
+        hi = max(hi, key);
       }
   } else {
     const int32_t* cnt = a.cand_count + static_cast<int64_t>(t) * a.chunks;
@@ -1023,43 +1063,48 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
                             : kChunk;  // tokens per list slice
     float* st_sc = a.stage_score + row;
     int32_t* st_ix = a.stage_idx + row;
-    // Wave w copies chunks w, w+16, ...: four chunks at a time, the first 256
-    // entries of each loaded together; longer lists finish in a plain loop.
-    const int lane = tid & 63, wave = tid >> 6;
-    constexpr int kWaves = kSelThreads / 64;
-    auto put = [&](int p, float sc, int32_t ix) {
-      if (in_lds) {
-        s_key[p] = score_key(sc + 0.0f);
-        s_idx[p] = ix;
-      } else {
-        st_sc[p] = sc;
-        st_ix[p] = ix;
+    // Position p of the concatenation lies in list c = the last with
+    // off[c] <= p (binary search; empty lists are skipped by construction).
+    // Every thread copies kGather positions per round, loads issued together.
+    auto list_of = [&](int p) -> int {
+      int lo = 0, hi = a.chunks - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sm.off[mid] <= p) lo = mid;
+        else hi = mid - 1;
       }
+      return lo;
     };
-    for (int cg = wave; cg < a.chunks; cg += 4 * kWaves) {
-      int cnt_q[4], off_q[4];
-      float sv[4][4];
-      int32_t iv[4][4];
+    constexpr int kGather = 4;
+    for (int p0 = 0; p0 < n; p0 += kGather * kSelThreads) {
+      float sv[kGather];
+      int32_t iv[kGather];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = cg + kWaves * q;
-        cnt_q[q] = (c < a.chunks) ? sm.off[c + 1] - sm.off[c] : 0;
-        off_q[q] = (c < a.chunks) ? sm.off[c] : 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = lane + 64 * r;
-          const int64_t src = row + c * seg + i;
-          sv[q][r] = (i < cnt_q[q]) ? a.cand_score[src] : 0.0f;
-          iv[q][r] = (i < cnt_q[q]) ? a.cand_idx[src] : 0;
+      for (int q = 0; q < kGather; ++q) {
+        const int p = p0 + q * kSelThreads + tid;
+        sv[q] = 0.0f;
+        iv[q] = 0;
+        if (p < n) {
+          const int c = list_of(p);
+          const int64_t src = row + c * seg + (p - sm.off[c]);
+          sv[q] = a.cand_score[src];
+          iv[q] = a.cand_idx[src];
         }
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (lane + 64 * r < cnt_q[q]) put(off_q[q] + lane + 64 * r, sv[q][r], iv[q][r]);
-        const int64_t cbase = row + (cg + kWaves * q) * seg;
-        for (int i = 256 + lane; i < cnt_q[q]; i += 64) put(off_q[q] + i, a.cand_score[cbase + i], a.cand_idx[cbase + i]);
+      for (int q = 0; q < kGather; ++q) {
+        const int p = p0 + q * kSelThreads + tid;
+        if (p >= n) continue;
+        if (in_lds) {
+          const uint32_t key = score_key(sv[q] + 0.0f);
+          s_key[p] = key;
+          s_idx[p] = iv[q];
+          lo = min(lo, key);
+          hi = max(hi, key);
+        } else {
+          st_sc[p] = sv[q];
+          st_ix[p] = iv[q];
+        }
       }
     }
     if (!in_lds) {
@@ -1068,6 +1113,14 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
       gidx = st_ix;
     }
   }
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = min(lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo), off)));
+    hi = max(hi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi), off)));
+  }
+  if ((tid & 63) == 0) {
+    sm.wmin[tid >> 6] = lo;
+    sm.wmax[tid >> 6] = hi;
+  }
   __syncthreads();
   auto key_at = [&](int i) -> uint32_t { return in_lds ? s_key[i] : score_key(gsc[i] + 0.0f); };
   auto idx_at = [&](int i) -> int32_t { return in_lds ? s_idx[i] : (gidx ? gidx[i] : i); };
@@ -1075,13 +1128,28 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   uint32_t kstar = 0;
   int need = n;
   if (n > k) {
-    uint32_t prefix = 0, mask = 0;
+    // Bits every key shares need no pass: with the keys in LDS their range
+    // is known, so the first pass splits the bits just below the common
+    // prefix (where the candidates, all near the threshold, differ).
+    uint32_t kmin = 0u, kmax = 0xffffffffu;
+    if (in_lds) {
+      kmin = 0xffffffffu;
+      kmax = 0u;
+#pragma unroll
+      for (int w = 0; w < kSelThreads / 64; ++w) {
+        kmin = min(kmin, sm.wmin[w]);
+        kmax = max(kmax, sm.wmax[w]);
+      }
+    }
+    const int common = (kmin == kmax) ? 32 : __clz(static_cast<int>(kmin ^ kmax));
+    uint32_t mask = common == 0 ? 0u : (common == 32 ? 0xffffffffu : 0xffffffffu << (32 - common));
+    uint32_t prefix = kmin & mask;
     int remaining = k;
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    for (int pass = 0; pass < 3; ++pass) {
-      const int sh = shifts[pass];
-      const int nb = 1 << widths[pass];
+    int top = 32 - common;  // bits [0, top) are still open
+    while (top > 0) {
+      const int width = min(11, top);
+      const int sh = top - width;
+      const int nb = 1 << width;
       for (int b = tid; b < 2048; b += kSelThreads) s_hist[b] = 0;
       __syncthreads();
       for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
@@ -1102,17 +1170,58 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
       remaining -= above;
       prefix |= static_cast<uint32_t>(bin) << sh;
       mask |= static_cast<uint32_t>(nb - 1) << sh;
+      top = sh;
+      if (top == 0) break;
+      const int m = static_cast<int>(s_hist[bin]);  // keys sharing the threshold's prefix
+      __syncthreads();                              // before s_hist is reused
+      if (m <= 64) {
+        // Few keys share the prefix: rank them directly.  The threshold is
+        // the key with (count above) < remaining <= (count above) + (count equal).
+        if (tid == 0) sm.cnt = 0;
+        __syncthreads();
+        uint32_t* s_small = s_hist;
+        for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
+#pragma unroll
+          for (int j = 0; j < kSelPerThread; ++j) {
+            const int i = i0 + j * kSelThreads + tid;
+            if (i < n) {
+              const uint32_t key = key_at(i);
+              if ((key & mask) == prefix) s_small[atomicAdd(&sm.cnt, 1)] = key;
+            }
+          }
+        }
+        __syncthreads();
+        if (tid < m) {
+          const uint32_t mine = s_small[tid];
+          int gt = 0, eq = 0;
+          for (int j = 0; j < m; ++j) {
+            const uint32_t o = s_small[j];
+            gt += o > mine;
+            eq += o == mine;
+          }
+          if (gt < remaining && remaining <= gt + eq) {  // every such thread holds the same key
+            s_res[0] = static_cast<int>(mine);
+            s_res[1] = remaining - gt;
+          }
+        }
+        __syncthreads();
+        prefix = static_cast<uint32_t>(s_res[0]);
+        remaining = s_res[1];
+        break;
+      }
     }
     kstar = prefix;
     need = remaining;  // threshold-valued elements to take, lowest index first
   }
 
-  // ordered compaction: thread owns kSelPerThread consecutive elements
-  int out_base = 0, eq_base = 0;
+  // Ordered compaction: thread owns kSelPerThread consecutive elements.  An
+  // element's output position is (greater keys before it) + min(threshold
+  // keys before it, need); both counts come from one scan, packed as
+  // gt | eq << 16 (each below 2^14 per round).
+  int gt_base = 0, eq_base = 0;
   for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
     const int start = i0 + tid * kSelPerThread;
     uint32_t gt = 0, eq = 0;
-    int eq_cnt = 0;
 #pragma unroll
     for (int j = 0; j < kSelPerThread; ++j) {
       const int i = start + j;
@@ -1122,31 +1231,31 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
         } else {
           const uint32_t key = key_at(i);
           if (key > kstar) gt |= 1u << j;
-          else if (key == kstar) { eq |= 1u << j; ++eq_cnt; }
+          else if (key == kstar) eq |= 1u << j;
         }
       }
     }
-    int eq_total;
-    int eq_rank = eq_base + block_scan_excl<kSelThreads>(eq_cnt, s_wave, eq_total);
-    uint32_t sel = gt;
+    int packed_total;
+    const int packed = block_scan_excl<kSelThreads>(__popc(gt) | (__popc(eq) << 16), s_wave, packed_total);
+    int gt_before = gt_base + (packed & 0xffff), eq_before = eq_base + (packed >> 16);
 #pragma unroll
-    for (int j = 0; j < kSelPerThread; ++j)
-      if (eq & (1u << j)) {
-        if (eq_rank < need) sel |= 1u << j;
-        ++eq_rank;
-      }
-    int sel_total;
-    int pos = out_base + block_scan_excl<kSelThreads>(__popc(sel), s_wave, sel_total);
-#pragma unroll
-    for (int j = 0; j < kSelPerThread; ++j)
-      if (sel & (1u << j)) {
+    for (int j = 0; j < kSelPerThread; ++j) {
+      if (gt & (1u << j)) {
+        const int pos = gt_before + min(eq_before, need);
         if (pos < k) out[pos] = idx_at(start + j);
-        ++pos;
+        ++gt_before;
+      } else if (eq & (1u << j)) {
+        if (eq_before < need) {
+          const int pos = gt_before + eq_before;
+          if (pos < k) out[pos] = idx_at(start + j);
+        }
+        ++eq_before;
       }
-    out_base += sel_total;
-    eq_base += eq_total;
+    }
+    gt_base += packed_total & 0xffff;
+    eq_base += packed_total >> 16;
   }
-  for (int i = out_base + tid; i < k; i += kSelThreads) out[i] = -1;
+  for (int i = gt_base + min(eq_base, need) + tid; i < k; i += kSelThreads) out[i] = -1;
 }
 
 }  // namespace ekv
