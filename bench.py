@@ -123,8 +123,8 @@ def dsa_filter(ops, st):
 
 def dsa_post(ops, st):
     common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
-    ops.indexer_select(st["digits"], st["wf"], *common, st["topk"], st["idx_ws"])
-    ops.merge_swa_topk(st["topk"], st["merged"], st["positions"], 128)
+    ops.indexer_select(st["digits"], st["wf"], *common, st["topk"], st["idx_ws"], merged=st["merged"],
+                       positions=st["positions"], window=128)
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
                           block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
 

@@ -194,15 +194,19 @@ int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float
  * Indexer top-k, stage 2 of 2 (same workspace and arguments): scores the
  * candidates exactly (as ekv_indexer_score) if stage 1 did not, and writes
  * the exact top-k: the k largest by (score desc, index asc), in ascending
- * index order, -1 padded.  Replaces the top-k
- * of SparseAttnIndexer (nvidia/attention.py:942-953) that fills
- * indexer_topk_buffer (nvidia/model.py:71-79).
+ * index order, -1 padded.  Replaces the top-k of SparseAttnIndexer
+ * (nvidia/attention.py:942-953) that fills indexer_topk_buffer
+ * (nvidia/model.py:71-79).  With merged_out non-null it also writes what
+ * ekv_merge_swa_topk would make of the result (merged_width entries per row,
+ * from positions and window), saving that launch.
  */
 int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache,
                        int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
                        int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
                        int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride,
-                       int32_t k, void* workspace, int64_t workspace_bytes, void* stream);
+                       int32_t k, void* workspace, int64_t workspace_bytes, int32_t* merged_out,
+                       int64_t merged_stride, int32_t merged_width, const int64_t* positions,
+                       int32_t window, void* stream);
 
 /*
  * ekv_indexer_filter followed by ekv_indexer_select: the SparseAttnIndexer

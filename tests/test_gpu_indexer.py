@@ -190,6 +190,16 @@ def test_indexer_topk_stages_match_one_call(dev):
     ops.indexer_filter(q8, dig, wf, *args, st["max_len"], ws)
     ops.indexer_select(dig, wf, *args, st["max_len"], b, ws)
     assert torch.equal(a, b)
+    # the select's merged output == ekv_merge_swa_topk of its top-k
+    positions = torch.tensor(lengths.astype(np.int64) + WINDOW - 1, device=dev)
+    positions[2] = 40  # shorter than the window: no top-k entries, a partial window
+    c = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    merged = torch.full((T, TOPK + WINDOW + 5), -9, dtype=torch.int32, device=dev)
+    ops.indexer_select(dig, wf, *args, st["max_len"], c, ws, merged=merged, positions=positions, window=WINDOW)
+    assert torch.equal(a, c)
+    ref_merged = torch.full_like(merged, -9)
+    ops.merge_swa_topk(c, ref_merged, positions, WINDOW)
+    assert torch.equal(merged, ref_merged)
     got = a.cpu().numpy()
     for t in range(T):
         row = got[t][got[t] >= 0]

@@ -980,6 +980,14 @@ struct SelectArgs {
   int32_t max_len;
   int32_t seg_groups;        // chunk mode: 0 = lists of kChunk-token chunks, else of
                              // filter_verify_kernel segments (`seg_groups` per row)
+  // Optional merged output (merge_swa_topk of the result): [T, merged_stride]
+  // rows of merged_width = [top-k[:n] | seq-w .. seq-1 | -1 ...] with
+  // seq = positions[t] + 1, n = min(max(seq - window, 0), k), w = min(seq, window).
+  int32_t* merged;
+  int64_t merged_stride;
+  int32_t merged_width;
+  const int64_t* positions;
+  int32_t window;
 };
 
 constexpr int kSelMaxChunks = 4096;  // up to 8M-token rows
@@ -1022,6 +1030,16 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   const int t = blockIdx.x;
   const int k = a.k;
   int32_t* out = a.out + static_cast<int64_t>(t) * a.out_stride;
+  int32_t* merged = a.merged ? a.merged + static_cast<int64_t>(t) * a.merged_stride : nullptr;
+  int64_t seq = 0, m_topk = 0;  // merged: sequence length, top-k entries taken
+  if (merged) {
+    seq = a.positions[t] + 1;
+    m_topk = min(max(seq - a.window, static_cast<int64_t>(0)), static_cast<int64_t>(k));
+  }
+  auto emit = [&](int pos, int32_t v) {
+    out[pos] = v;
+    if (merged && pos < m_topk) merged[pos] = v;
+  };
 
   // gather the elements; lo / hi track the range of the keys put in LDS
   uint32_t lo = 0xffffffffu, hi = 0u;
@@ -1242,12 +1260,12 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     for (int j = 0; j < kSelPerThread; ++j) {
       if (gt & (1u << j)) {
         const int pos = gt_before + min(eq_before, need);
-        if (pos < k) out[pos] = idx_at(start + j);
+        if (pos < k) emit(pos, idx_at(start + j));
         ++gt_before;
       } else if (eq & (1u << j)) {
         if (eq_before < need) {
           const int pos = gt_before + eq_before;
-          if (pos < k) out[pos] = idx_at(start + j);
+          if (pos < k) emit(pos, idx_at(start + j));
         }
         ++eq_before;
       }
@@ -1255,7 +1273,12 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     gt_base += packed_total & 0xffff;
     eq_base += packed_total >> 16;
   }
-  for (int i = gt_base + min(eq_base, need) + tid; i < k; i += kSelThreads) out[i] = -1;
+  for (int i = gt_base + min(eq_base, need) + tid; i < k; i += kSelThreads) emit(i, -1);
+  if (merged) {
+    const int64_t w = min(seq, static_cast<int64_t>(a.window));
+    for (int64_t c = m_topk + tid; c < a.merged_width; c += kSelThreads)
+      merged[c] = (c < m_topk + w) ? static_cast<int32_t>(seq - w + (c - m_topk)) : -1;
+  }
 }
 
 }  // namespace ekv
@@ -1415,7 +1438,7 @@ extern "C" int ekv_topk_select(const float* scores, int64_t scores_stride, const
   EKV_CHECK(out_stride >= k, "out_stride must be >= k");
   EKV_CHECK(max_len >= 0 && scores_stride >= max_len, "scores_stride must be >= max_len");
   SelectArgs s{scores, scores_stride, lengths, nullptr, nullptr, nullptr, 0, nullptr, nullptr, out, out_stride, k,
-               max_len, 0};
+               max_len, 0, nullptr, 0, 0, nullptr, 0};
   launch_select(s, num_tokens, static_cast<hipStream_t>(stream));
   return ekv_launch_status();
 }
@@ -1484,11 +1507,16 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
                                   int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
                                   const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
                                   int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+                                  void* workspace, int64_t workspace_bytes, int32_t* merged_out,
+                                  int64_t merged_stride, int32_t merged_width, const int64_t* positions,
+                                  int32_t window, void* stream) {
   int rc = check_topk_args(q_digits, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
                            workspace, workspace_bytes);
   if (rc) return rc;
   EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
+  EKV_CHECK(merged_out == nullptr || (positions != nullptr && window >= 0 && merged_width >= 0 &&
+                                      merged_stride >= merged_width),
+            "merged_out needs positions, window >= 0 and merged_stride >= merged_width");
   if (num_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
@@ -1504,7 +1532,7 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
   }
   SelectArgs sel{nullptr, 0, lengths, ws.cand_score, ws.cand_idx, ws.counts, plan.fused ? plan.groups : chunks,
                  ws.stage_score, ws.stage_idx, topk_out, out_stride, k, static_cast<int32_t>(L),
-                 plan.fused ? plan.groups : 0};
+                 plan.fused ? plan.groups : 0, merged_out, merged_stride, merged_width, positions, window};
   launch_select(sel, num_tokens, s);
   return ekv_launch_status();
 }
@@ -1519,5 +1547,6 @@ extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, co
                               lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
   if (rc) return rc;
   return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-                            num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, stream);
+                            num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, nullptr, 0, 0,
+                            nullptr, 0, stream);
 }

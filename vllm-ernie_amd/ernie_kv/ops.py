@@ -280,16 +280,27 @@ def indexer_filter(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, ma
 
 
 def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: int, topk_out: torch.Tensor,
-                   workspace: torch.Tensor) -> None:
+                   workspace: torch.Tensor, merged: torch.Tensor | None = None,
+                   positions: torch.Tensor | None = None, window: int = 128) -> None:
     """Stage 2: the candidates' exact scores (if stage 1 left them), exact top-k
-    (ascending, -1 padded)."""
+    (ascending, -1 padded).  With ``merged`` (and ``positions``) it also writes
+    ``merge_swa_topk(topk_out, merged, positions, window)`` in the same launch."""
     T = q_digits.shape[0]
     _topk_common(None, q_digits, w, kcache, block_table, req_ids, lengths, T)
     _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    m_ptr, m_stride, m_width, p_ptr = 0, 0, 0, 0
+    if merged is not None:
+        _need(positions is not None, "merged output needs positions")
+        _check_dev(merged, positions)
+        _need(merged.dtype == torch.int32 and merged.stride(1) == 1 and merged.shape[0] == T, "merged int32 [T, W]")
+        _need(positions.dtype == torch.int64 and positions.shape[0] == T, "positions int64 [T]")
+        _need(merged.shape[1] >= topk_out.shape[1] + window, "merged width must be >= k + window")
+        m_ptr, m_stride, m_width, p_ptr = merged.data_ptr(), _rs(merged), merged.shape[1], positions.data_ptr()
     _lib.call(
         "ekv_indexer_select", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
         block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T, int(max_len),
-        topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(), workspace.numel(), _stream(),
+        topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(), workspace.numel(),
+        m_ptr, m_stride, m_width, p_ptr, int(window), _stream(),
     )
 
 
