@@ -198,7 +198,11 @@ int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float
  * (nvidia/attention.py:942-953) that fills indexer_topk_buffer
  * (nvidia/model.py:71-79).  With merged_out non-null it also writes what
  * ekv_merge_swa_topk would make of the result (merged_width entries per row,
- * from positions and window), saving that launch.
+ * from positions and window), saving that launch; with merged_slots != 0 those
+ * entries are cache slots block_table[req][i / 64] * 64 + i % 64 (-1 when
+ * unmapped), the global indices the decode kernel of FlashMLASparseImpl
+ * takes [vLLM: the request-to-global index conversion before
+ * flash_mla_with_kvcache, nvidia/attention.py:737-748].
  */
 int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache,
                        int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
@@ -206,7 +210,7 @@ int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kc
                        int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride,
                        int32_t k, void* workspace, int64_t workspace_bytes, int32_t* merged_out,
                        int64_t merged_stride, int32_t merged_width, const int64_t* positions,
-                       int32_t window, void* stream);
+                       int32_t window, int32_t merged_slots, void* stream);
 
 /*
  * ekv_indexer_filter followed by ekv_indexer_select: the SparseAttnIndexer

@@ -200,6 +200,16 @@ def test_indexer_topk_stages_match_one_call(dev):
     ref_merged = torch.full_like(merged, -9)
     ops.merge_swa_topk(c, ref_merged, positions, WINDOW)
     assert torch.equal(merged, ref_merged)
+    # merged_slots: the same entries as cache slots through the block table
+    slots = torch.full_like(merged, -9)
+    ops.indexer_select(dig, wf, *args, st["max_len"], c, ws, merged=slots, positions=positions, window=WINDOW,
+                       merged_slots=True)
+    bt = st["bt"][st["req"]]  # [T, pages] rows of each query's request
+    m = ref_merged.cpu().numpy().astype(np.int64)
+    in_table = (m >= 0) & (m // 64 < bt.shape[1])  # entries past the table are unmapped
+    page = np.take_along_axis(bt, np.clip(m // 64, 0, bt.shape[1] - 1), axis=1)
+    ref_slots = np.where(in_table, page * 64 + m % 64, -1)
+    assert np.array_equal(slots.cpu().numpy(), ref_slots)
     got = a.cpu().numpy()
     for t in range(T):
         row = got[t][got[t] >= 0]

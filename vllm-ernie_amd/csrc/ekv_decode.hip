@@ -7,15 +7,16 @@
 //   * score waves 0..3 (q for heads 16w .. 16w+15 held in registers) first
 //     finish tile t-1 (below), then compute S = Q K^T of tile t on
 //     v_mfma_f32_16x16x32_bf16 from a bf16 K image in LDS, run the online
-//     softmax and write P (bf16, row scale folded in) for their heads;
-//   * data waves 4..7 finish tile t-1, widen tile t+1 (exact fp8 -> bf16) into
-//     the next of three K images, and issue the loads of tile t+3 (8 rows per
-//     wave, row addresses in scalar registers, 256-byte coalesced loads into
-//     registers, two tiles in flight);
+//     softmax and write P (bf16, row scale folded in) for their heads; fp8
+//     K fragments become bf16 in registers (exact conversion);
+//   * data waves 4..7 finish tile t-1, store tile t+1 (the rows as cached:
+//     e4m3fn bytes, or bf16) into the next of three K images, and issue the
+//     loads of tile t+3 (8 rows per wave, row addresses in scalar registers,
+//     256-byte coalesced loads into registers, two tiles in flight);
 //   * "finish tile t-1" = O[:, 64w .. 64w+63] += P V for all heads, every wave
 //     taking its 64 channels.  The B operand (V, entries x channels) is read
-//     straight from the row-major K image with ds_read_b64_tr_b16, which
-//     transposes 4 x 4 blocks of 16-bit elements across each 16-lane row; no
+//     straight from the row-major K image with a transposing LDS read
+//     (ds_read_b64_tr_b8 for fp8 rows, ds_read_b64_tr_b16 for bf16); no
 //     separate V^T image is built.
 // A prologue resolves every index entry of the split to a cache slot (block
 // table lookup) and fp32 row scale once.  The softmax reference max only
@@ -36,7 +37,7 @@ constexpr int kScoreWaves = 4;               // up to 64 heads (one wave per 16)
 constexpr int kDataWaves = 4;
 constexpr int kThreads = 64 * (kScoreWaves + kDataWaves);
 constexpr int kRowsPerDataWave = kTile / kDataWaves;   // 8
-constexpr int kKImages = 3;                  // tile t-1 (P V), t (S), t+1 (being widened)
+constexpr int kKImages = 3;                  // tile t-1 (P V), t (S), t+1 (being stored)
 constexpr int kMaxSplitEntries = 1024;       // index entries one workgroup resolves
 constexpr int kTargetGroups = 256;           // one workgroup per CU
 constexpr float kRescaleSlack = 8.0f;        // log2 units: P <= 2**8 between rescales
@@ -68,12 +69,18 @@ struct DecodeArgs {
   int32_t splits;
 };
 
-template <int D>
+// K images hold the tile's rows as stored: raw e4m3fn bytes (fp8 cache) or
+// bf16.  The fp8 row stride D + 8 bytes is 8 (mod 16) words: the 16 rows a
+// QK fragment read touches land on distinct bank pairs.
+template <int D, bool BF16>
 struct DecodeSmem {
-  static constexpr int kKRow = D + 8;       // bf16 K row stride (elements)
+  static constexpr int kKRowB = BF16 ? 2 * (D + 8) : D + 8;  // K row stride (bytes)
+  static constexpr int kImgB = kTile * kKRowB;
   static constexpr int kPRow = kTile + 8;   // bf16 P row stride (elements)
   static constexpr int kORow = kDv + 8;     // bf16 output staging row stride
-  uint16_t k[kKImages][kTile * kKRow];
+  static constexpr int kImgRegion =
+      kKImages * kImgB > 64 * kORow * 2 ? kKImages * kImgB : 64 * kORow * 2;  // images, then output staging
+  __align__(16) uint8_t img[kImgRegion];
   uint16_t p[2][64 * kPRow];                // P of tiles t (written) and t-1 (read)
   float alpha[2][64];                       // rescale factor per head (valid when grow[.][head / 16])
   int32_t grow[2][kScoreWaves];
@@ -81,8 +88,6 @@ struct DecodeSmem {
   int32_t slot[kMaxSplitEntries];
   float kscale[kMaxSplitEntries];
 };
-// The epilogue stages the 64 x 512 bf16 output over the K images.
-static_assert(kKImages * kTile * (512 + 8) >= 64 * (kDv + 8), "output staging must fit in the K images");
 
 // Four e4m3fn bytes -> four bf16 (exact: every e4m3fn value is a bf16 value).
 __device__ __forceinline__ uint2 fp8x4_bf16(uint32_t w) {
@@ -130,14 +135,16 @@ struct RowRegs {
   static constexpr int kUnits = D / 4;                   // 4-channel units per row
   static constexpr int kJ = (kUnits + 63) / 64;
   Unit v[kRowsPerDataWave][kJ];
+  float ks;                                              // lane r < 8: fp32 scale of row r
   uint32_t valid;                                        // bit rr: row rr holds data (wave-uniform)
+  bool live;                                             // the tile exists
 };
 
 // Issue every load of tile `tile` for this data wave.  Masked rows and tiles
 // past the end read the first cache row and stay flagged invalid, so that the
-// wait before each widening counts exactly the loads issued after it.
+// wait before each store to LDS counts exactly the loads issued after it.
 template <int D, bool BF16>
-__device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem<D>& sm, int u, int tile, int ntiles,
+__device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem<D, BF16>& sm, int u, int tile, int ntiles,
                                            RowRegs<D, BF16>& rr) {
   using RR = RowRegs<D, BF16>;
   const bool live = tile < ntiles;
@@ -146,6 +153,7 @@ __device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem
   uint32_t valid = 0;
   // One LDS read gives lane r the slot of row r; rows then become uniform.
   const int my_slot = sm.slot[tb + (lane & (kRowsPerDataWave - 1))];
+  const int ks_slot = (live && my_slot >= 0) ? my_slot : 0;
   // Keep each tile's loads in issue order relative to the other tiles' loads
   // (the register buffers are consumed oldest first).
   __builtin_amdgcn_sched_barrier(0);
@@ -163,52 +171,84 @@ __device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem
       rr.v[r][j] = *reinterpret_cast<const typename RR::Unit*>(row + unit * sizeof(typename RR::Unit));
     }
   }
+  // the rows' fp32 scales, lane r for row r (after the values of the page)
+  if constexpr (BF16) rr.ks = 1.0f;
+  else rr.ks = *reinterpret_cast<const float*>(a.cache + static_cast<int64_t>(ks_slot >> 6) * a.page_stride +
+                                                kPageTokens * D + (ks_slot & 63) * 4);
   __builtin_amdgcn_sched_barrier(0);
   rr.valid = valid;
+  rr.live = live;
 }
 
-// Widen the wave's 8 rows into a K image (masked rows become zero, so that
-// P = 0 never meets a non-finite value in P V).  Lanes past the end of a row
-// repeat its last unit: a duplicate store of equal data, no divergence.
+// Store the wave's 8 rows into a K image as they are (masked rows become
+// zero, so that P = 0 never meets a non-finite value in P V).  Lanes past the
+// end of a row repeat its last unit: a duplicate store of equal data.
 template <int D, bool BF16>
-__device__ __forceinline__ void widen_rows(const RowRegs<D, BF16>& rr, int u, uint16_t* k) {
+__device__ __forceinline__ void store_rows(const RowRegs<D, BF16>& rr, int u, int tile, DecodeSmem<D, BF16>& sm,
+                                           uint8_t* k) {
   using RR = RowRegs<D, BF16>;
-  using SM = DecodeSmem<D>;
+  using SM = DecodeSmem<D, BF16>;
   const int lane = threadIdx.x & 63;
+  if (rr.live && lane < kRowsPerDataWave)
+    sm.kscale[tile * kTile + kRowsPerDataWave * u + lane] = ((rr.valid >> lane) & 1u) ? rr.ks : 0.0f;
 #pragma unroll
   for (int r = 0; r < kRowsPerDataWave; ++r) {
     const bool ok = (rr.valid >> r) & 1u;
+    uint8_t* row = k + (kRowsPerDataWave * u + r) * SM::kKRowB;
 #pragma unroll
     for (int j = 0; j < RR::kJ; ++j) {
       const int unit = (RR::kUnits % 64 == 0 || lane + 64 * j < RR::kUnits) ? lane + 64 * j : RR::kUnits - 1;
-      uint2 x;
-      if constexpr (BF16) x = ok ? rr.v[r][j] : make_uint2(0u, 0u);
-      else x = fp8x4_bf16(ok ? rr.v[r][j] : 0u);
-      *reinterpret_cast<uint2*>(&k[(kRowsPerDataWave * u + r) * SM::kKRow + 4 * unit]) = x;
+      if constexpr (BF16) *reinterpret_cast<uint2*>(row + 8 * unit) = ok ? rr.v[r][j] : make_uint2(0u, 0u);
+      else *reinterpret_cast<uint32_t*>(row + 4 * unit) = ok ? rr.v[r][j] : 0u;
     }
   }
+}
+
+// Eight e4m3fn bytes -> bf16x8 (exact).
+__device__ __forceinline__ bf16x8 fp8x8_bf16(uint2 w) {
+  const uint2 lo = fp8x4_bf16(w.x), hi = fp8x4_bf16(w.y);
+  return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// ds_read_b64_tr_b8: in each row of 16 lanes, lane j receives byte j % 8 of
+// the 8 bytes addressed by lanes j / 8 + 2m (m = 0..7), as byte m.
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
+  const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+      (__attribute__((address_space(3))) i32x2*)((__attribute__((address_space(3))) uint8_t*)(p)));
+  return make_uint2(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y));
 }
 
 // ---------------------------------------------------------------------------
 // O[:, 64w .. 64w+63] += P V for every head group (all waves).  o[hf][nt]
 // holds heads 16hf + 4g + i, channels 64w + 16nt + col.
-template <int D>
-__device__ __forceinline__ void accumulate_pv(const DecodeSmem<D>& sm, const uint16_t* kimg, int pb, int hgroups,
+template <int D, bool BF16>
+__device__ __forceinline__ void accumulate_pv(const DecodeSmem<D, BF16>& sm, const uint8_t* kimg, int pb, int hgroups,
                                               f32x4 (&o)[4][4]) {
-  using SM = DecodeSmem<D>;
+  using SM = DecodeSmem<D, BF16>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int g = lane >> 4, col = lane & 15;
-  // B operand (entries 8g .. 8g+7, channel 64w + 16nt + col): two transposed
-  // reads of rows 8g + 4h + col/4, channels 64w + 16nt + 4 (col % 4) .. +3.
+  // B operand: entries 8g .. 8g+7 at channel 64w + 16nt + col.
   bf16x8 vb[4];
-  const uint16_t* vbase = kimg + (8 * g + (col >> 2)) * SM::kKRow + 64 * wave + 4 * (col & 3);
+  if constexpr (BF16) {
+    // two 16-bit transposed reads of rows 8g + 4h + col/4, channels
+    // 64w + 16nt + 4 (col % 4) .. +3
+    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(kimg + (8 * g + (col >> 2)) * SM::kKRowB) + 64 * wave +
+                            4 * (col & 3);
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const i16x4 lo = lds_read_tr16(vbase + 16 * nt);
-    const i16x4 hi = lds_read_tr16(vbase + 4 * SM::kKRow + 16 * nt);
-    const i16x4 both[2] = {lo, hi};
-    vb[nt] = __builtin_bit_cast(bf16x8, both);
+    for (int nt = 0; nt < 4; ++nt) {
+      const i16x4 lo = lds_read_tr16(vbase + 16 * nt);
+      const i16x4 hi = lds_read_tr16(vbase + 2 * SM::kKRowB + 16 * nt);
+      const i16x4 both[2] = {lo, hi};
+      vb[nt] = __builtin_bit_cast(bf16x8, both);
+    }
+  } else {
+    // one 8-bit transposed read: lane col of row block g addresses row
+    // 8g + col/2, channels 64w + 16nt + 8 (col % 2) .. +7
+    const uint8_t* vbase = kimg + (8 * g + (col >> 1)) * SM::kKRowB + 64 * wave + 8 * (col & 1);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) vb[nt] = fp8x8_bf16(lds_read_tr8(vbase + 16 * nt));
   }
   // All operands are read before the first product; the rescale (rare) and
   // the products of head groups past `hgroups` (unused) need no branches.
@@ -245,10 +285,10 @@ struct SoftmaxState {
   float lsum[4];  // this lane's share of the denominator relative to m2
 };
 
-template <int D>
-__device__ __forceinline__ void score_tile(DecodeSmem<D>& sm, const uint16_t* kimg, int pb, int tb, float sc2,
+template <int D, bool BF16>
+__device__ __forceinline__ void score_tile(DecodeSmem<D, BF16>& sm, const uint8_t* kimg, int pb, int tb, float sc2,
                                            const bf16x8 (&qa)[D / 32], SoftmaxState& st) {
-  using SM = DecodeSmem<D>;
+  using SM = DecodeSmem<D, BF16>;
   constexpr int KS = D / 32;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -257,13 +297,16 @@ __device__ __forceinline__ void score_tile(DecodeSmem<D>& sm, const uint16_t* ki
   f32x4 s2[2][2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) s2[nt][0] = s2[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* kbase = kimg + col * SM::kKRow + 8 * g;
+  // B operand: entry 16nt + col, dims 32ks + 8g .. +7.
+  const uint8_t* kbase = kimg + col * SM::kKRowB + (BF16 ? 16 : 8) * g;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const bf16x8 kb =
-          __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(kbase + 16 * nt * SM::kKRow + 32 * ks));
+      const uint8_t* src = kbase + 16 * nt * SM::kKRowB + (BF16 ? 64 : 32) * ks;
+      bf16x8 kb;
+      if constexpr (BF16) kb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src));
+      else kb = fp8x8_bf16(*reinterpret_cast<const uint2*>(src));
       s2[nt][ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s2[nt][ks & 1], 0, 0, 0);
     }
   }
@@ -314,8 +357,9 @@ template <int D, bool BF16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
-  using SM = DecodeSmem<D>;
+  using SM = DecodeSmem<D, BF16>;
   SM& sm = *reinterpret_cast<SM*>(smem_raw);
+  auto kimg = [&](int i) -> uint8_t* { return sm.img + i * SM::kImgB; };
   constexpr int KS = D / 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -334,8 +378,9 @@ sparse_decode_kernel(DecodeArgs a) {
       qa[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
   }
 
-  // Prologue: entries -> slots and scales, three dependent gathers (index,
-  // block table, scale) each issued for all of the thread's entries first.
+  // Prologue: entries -> slots, two dependent gathers (index, block table;
+  // one without a block table) each issued for all of the thread's entries
+  // first.  The rows' scales come with the rows.
   int len = a.width;
   if (a.lengths) len = min(max(a.lengths[t], 0), a.width);
   const int e_begin = split * a.per_split;
@@ -362,19 +407,11 @@ sparse_decode_kernel(DecodeArgs a) {
       sv[j] = ok ? page * kPageTokens + (idx & 63) : -1;
     }
   }
-  float ksv[kPrologue];
 #pragma unroll
   for (int j = 0; j < kPrologue; ++j) {
     const int e = tid + kThreads * j;
     const int64_t slot = (sv[j] >= 0 && sv[j] < a.num_rows) ? sv[j] : -1;
     if (e < e_pad) sm.slot[e] = static_cast<int32_t>(slot);
-    sv[j] = slot;
-    if constexpr (BF16) {
-      ksv[j] = 1.0f;
-    } else {
-      const int64_t sc = slot >= 0 ? slot : 0;
-      ksv[j] = *reinterpret_cast<const float*>(a.cache + (sc >> 6) * a.page_stride + kPageTokens * D + (sc & 63) * 4);
-    }
   }
   if (tid < 2 * kScoreWaves) sm.grow[tid / kScoreWaves][tid % kScoreWaves] = 0;
   __syncthreads();
@@ -391,44 +428,34 @@ sparse_decode_kernel(DecodeArgs a) {
     RowRegs<D, BF16> bufA, bufB;  // even tiles in A, odd tiles in B
     fetch_rows<D, BF16>(a, sm, u, 0, ntiles, bufA);
     fetch_rows<D, BF16>(a, sm, u, 1, ntiles, bufB);
-#pragma unroll
-    for (int j = 0; j < kPrologue; ++j) {
-      const int e = tid + kThreads * j;
-      if (e < e_pad) sm.kscale[e] = sv[j] >= 0 ? ksv[j] : 0.0f;
-    }
-    widen_rows<D, BF16>(bufA, u, sm.k[0]);
+    store_rows<D, BF16>(bufA, u, 0, sm, kimg(0));
     fetch_rows<D, BF16>(a, sm, u, 2, ntiles, bufA);
-    __syncthreads();  // tile 0 widened
-    // Step s finishes tile s-1 (P V from image (s-1) % 3), widens tile s+1 into
+    __syncthreads();  // tile 0 stored
+    // Step s finishes tile s-1 (P V from image (s-1) % 3), stores tile s+1 into
     // image (s+1) % 3 and issues the loads of tile s+3.  Every load and
-    // widening is unconditional (tiles past the end are zero rows nobody
+    // store is unconditional (tiles past the end are zero rows nobody
     // reads), so each wait leaves the newer tile in flight.
-    widen_rows<D, BF16>(bufB, u, sm.k[1]);  // step 0
+    store_rows<D, BF16>(bufB, u, 1, sm, kimg(1));  // step 0
     fetch_rows<D, BF16>(a, sm, u, 3, ntiles, bufB);
     __syncthreads();
     int s = 1, kp = 0;  // kp: image of tile s-1
     for (; s + 1 <= ntiles; s += 2) {
       const int k1 = (kp == 2) ? 0 : kp + 1, k2 = (k1 == 2) ? 0 : k1 + 1;
-      accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
-      widen_rows<D, BF16>(bufA, u, sm.k[k2]);
+      accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
+      store_rows<D, BF16>(bufA, u, s + 1, sm, kimg(k2));
       fetch_rows<D, BF16>(a, sm, u, s + 3, ntiles, bufA);
       __syncthreads();
-      accumulate_pv<D>(sm, sm.k[k1], s & 1, hgroups, o);
-      widen_rows<D, BF16>(bufB, u, sm.k[kp]);
+      accumulate_pv<D, BF16>(sm, kimg(k1), s & 1, hgroups, o);
+      store_rows<D, BF16>(bufB, u, s + 2, sm, kimg(kp));
       fetch_rows<D, BF16>(a, sm, u, s + 4, ntiles, bufB);
       __syncthreads();
       kp = k2;
     }
     // the last (odd) step
-    if (s - 1 < ntiles) accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
+    if (s - 1 < ntiles) accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
     __syncthreads();
   } else {
     // ---------------- score waves ----------------
-#pragma unroll
-    for (int j = 0; j < kPrologue; ++j) {
-      const int e = tid + kThreads * j;
-      if (e < e_pad) sm.kscale[e] = sv[j] >= 0 ? ksv[j] : 0.0f;
-    }
     SoftmaxState st;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -436,23 +463,23 @@ sparse_decode_kernel(DecodeArgs a) {
       st.lsum[i] = 0.0f;
     }
     const float sc2 = a.scale * kLog2e;
-    __syncthreads();  // tile 0 widened
+    __syncthreads();  // tile 0 stored
     // Step s finishes tile s-1 and scores tile s (image s % 3, P buffer s & 1).
     // Score waves past `hgroups` run on unused heads rather than branching.
     if (ntiles == 0) {
       for (int s = 0; s < steps; ++s) __syncthreads();
     } else {
-      score_tile<D>(sm, sm.k[0], 0, 0, sc2, qa, st);
+      score_tile<D, BF16>(sm, kimg(0), 0, 0, sc2, qa, st);
       __syncthreads();
       int kp = 0;  // image of tile s-1
       for (int s = 1; s < ntiles; ++s) {
         const int kr = (kp == 2) ? 0 : kp + 1;
-        accumulate_pv<D>(sm, sm.k[kp], (s - 1) & 1, hgroups, o);
-        score_tile<D>(sm, sm.k[kr], s & 1, s * kTile, sc2, qa, st);
+        accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
+        score_tile<D, BF16>(sm, kimg(kr), s & 1, s * kTile, sc2, qa, st);
         __syncthreads();
         kp = kr;
       }
-      accumulate_pv<D>(sm, sm.k[kp], (ntiles - 1) & 1, hgroups, o);
+      accumulate_pv<D, BF16>(sm, kimg(kp), (ntiles - 1) & 1, hgroups, o);
       __syncthreads();
       for (int s = ntiles + 1; s < steps; ++s) __syncthreads();
     }
@@ -474,7 +501,7 @@ sparse_decode_kernel(DecodeArgs a) {
   __syncthreads();
 
   // Epilogue: O / l as bf16 through LDS (over the K images), then out.
-  uint16_t* ostage = sm.k[0];
+  uint16_t* ostage = reinterpret_cast<uint16_t*>(sm.img);
 #pragma unroll
   for (int hf = 0; hf < 4; ++hf) {
     if (hf >= hgroups) break;
@@ -595,7 +622,7 @@ extern "C" int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int3
 
 template <int D, bool BF16>
 static void launch_decode(const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  const size_t smem = sizeof(DecodeSmem<D>);
+  const size_t smem = sizeof(DecodeSmem<D, BF16>);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sparse_decode_kernel<D, BF16>),
                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   hipLaunchKernelGGL((sparse_decode_kernel<D, BF16>), grid, dim3(kThreads), smem, s, a);

@@ -988,6 +988,12 @@ struct SelectArgs {
   int32_t merged_width;
   const int64_t* positions;
   int32_t window;
+  // With slot_bt non-null the merged entries are cache slots:
+  // slot_bt[req[t]][i >> 6] * 64 + (i & 63), -1 when unmapped.
+  const int32_t* slot_bt;
+  int64_t slot_bt_stride;
+  const int32_t* slot_req;
+  int64_t num_pages;
 };
 
 constexpr int kSelMaxChunks = 4096;  // up to 8M-token rows
@@ -1032,13 +1038,31 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   int32_t* out = a.out + static_cast<int64_t>(t) * a.out_stride;
   int32_t* merged = a.merged ? a.merged + static_cast<int64_t>(t) * a.merged_stride : nullptr;
   int64_t seq = 0, m_topk = 0;  // merged: sequence length, top-k entries taken
+  const int32_t* mbt = nullptr;
   if (merged) {
     seq = a.positions[t] + 1;
     m_topk = min(max(seq - a.window, static_cast<int64_t>(0)), static_cast<int64_t>(k));
+    if (a.slot_bt) mbt = a.slot_bt + static_cast<int64_t>(a.slot_req[t]) * a.slot_bt_stride;
   }
+  // Slot conversion reads the row's first kSelBtPages block-table entries
+  // from LDS (loaded now, stored over the histogram once the passes are done).
+  constexpr int kSelBtPages = 2048;
+  const int64_t bt_lds = mbt ? min(a.slot_bt_stride, static_cast<int64_t>(kSelBtPages)) : 0;
+  int32_t btv[kSelBtPages / kSelThreads];
+#pragma unroll
+  for (int j = 0; j < kSelBtPages / kSelThreads; ++j) {
+    const int pg = tid + kSelThreads * j;
+    btv[j] = (pg < bt_lds) ? mbt[pg] : -1;
+  }
+  auto to_merged = [&](int64_t i) -> int32_t {  // token index -> merged entry
+    if (i < 0 || mbt == nullptr) return static_cast<int32_t>(i);
+    if ((i >> 6) >= a.slot_bt_stride) return -1;
+    const int64_t page = ((i >> 6) < bt_lds) ? static_cast<int64_t>(static_cast<int32_t>(s_hist[i >> 6])) : mbt[i >> 6];
+    return (page >= 0 && page < a.num_pages) ? static_cast<int32_t>(page * kPageTokens + (i & 63)) : -1;
+  };
   auto emit = [&](int pos, int32_t v) {
     out[pos] = v;
-    if (merged && pos < m_topk) merged[pos] = v;
+    if (merged && pos < m_topk) merged[pos] = to_merged(v);
   };
 
   // gather the elements; lo / hi track the range of the keys put in LDS
@@ -1232,6 +1256,11 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     need = remaining;  // threshold-valued elements to take, lowest index first
   }
 
+  if (mbt) {  // every pass is done with s_hist (each ended with a barrier)
+#pragma unroll
+    for (int j = 0; j < kSelBtPages / kSelThreads; ++j) s_hist[tid + kSelThreads * j] = static_cast<uint32_t>(btv[j]);
+    __syncthreads();
+  }
   // Ordered compaction: thread owns kSelPerThread consecutive elements.  An
   // element's output position is (greater keys before it) + min(threshold
   // keys before it, need); both counts come from one scan, packed as
@@ -1277,7 +1306,7 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   if (merged) {
     const int64_t w = min(seq, static_cast<int64_t>(a.window));
     for (int64_t c = m_topk + tid; c < a.merged_width; c += kSelThreads)
-      merged[c] = (c < m_topk + w) ? static_cast<int32_t>(seq - w + (c - m_topk)) : -1;
+      merged[c] = (c < m_topk + w) ? to_merged(seq - w + (c - m_topk)) : -1;
   }
 }
 
@@ -1438,7 +1467,7 @@ extern "C" int ekv_topk_select(const float* scores, int64_t scores_stride, const
   EKV_CHECK(out_stride >= k, "out_stride must be >= k");
   EKV_CHECK(max_len >= 0 && scores_stride >= max_len, "scores_stride must be >= max_len");
   SelectArgs s{scores, scores_stride, lengths, nullptr, nullptr, nullptr, 0, nullptr, nullptr, out, out_stride, k,
-               max_len, 0, nullptr, 0, 0, nullptr, 0};
+               max_len, 0, nullptr, 0, 0, nullptr, 0, nullptr, 0, nullptr, 0};
   launch_select(s, num_tokens, static_cast<hipStream_t>(stream));
   return ekv_launch_status();
 }
@@ -1509,7 +1538,7 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
                                   int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
                                   void* workspace, int64_t workspace_bytes, int32_t* merged_out,
                                   int64_t merged_stride, int32_t merged_width, const int64_t* positions,
-                                  int32_t window, void* stream) {
+                                  int32_t window, int32_t merged_slots, void* stream) {
   int rc = check_topk_args(q_digits, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
                            workspace, workspace_bytes);
   if (rc) return rc;
@@ -1532,7 +1561,8 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
   }
   SelectArgs sel{nullptr, 0, lengths, ws.cand_score, ws.cand_idx, ws.counts, plan.fused ? plan.groups : chunks,
                  ws.stage_score, ws.stage_idx, topk_out, out_stride, k, static_cast<int32_t>(L),
-                 plan.fused ? plan.groups : 0, merged_out, merged_stride, merged_width, positions, window};
+                 plan.fused ? plan.groups : 0, merged_out, merged_stride, merged_width, positions, window,
+                 merged_slots ? block_table : nullptr, bt_stride, req_ids, num_pages};
   launch_select(sel, num_tokens, s);
   return ekv_launch_status();
 }
@@ -1548,5 +1578,5 @@ extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, co
   if (rc) return rc;
   return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                             num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, nullptr, 0, 0,
-                            nullptr, 0, stream);
+                            nullptr, 0, 0, stream);
 }

@@ -39,7 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_topk_select": (I32, [P, I64, P, I32, I32, P, I64, I32, P]),
     "ekv_indexer_topk_workspace_size": (I64, [I32, I32]),
     "ekv_indexer_filter": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, I32, P, I64, P]),
-    "ekv_indexer_select": (I32, [P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, P]),
+    "ekv_indexer_select": (I32, [P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P]),
     "ekv_indexer_topk": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P]),
     "ekv_sparse_mla_decode_workspace_size": (I64, [I32, I32, I32]),
     "ekv_sparse_mla_decode": (

@@ -281,10 +281,12 @@ def indexer_filter(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, ma
 
 def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: int, topk_out: torch.Tensor,
                    workspace: torch.Tensor, merged: torch.Tensor | None = None,
-                   positions: torch.Tensor | None = None, window: int = 128) -> None:
+                   positions: torch.Tensor | None = None, window: int = 128, merged_slots: bool = False) -> None:
     """Stage 2: the candidates' exact scores (if stage 1 left them), exact top-k
     (ascending, -1 padded).  With ``merged`` (and ``positions``) it also writes
-    ``merge_swa_topk(topk_out, merged, positions, window)`` in the same launch."""
+    ``merge_swa_topk(topk_out, merged, positions, window)`` in the same launch;
+    ``merged_slots`` turns those entries into cache slots through the block
+    table (-1 when unmapped)."""
     T = q_digits.shape[0]
     _topk_common(None, q_digits, w, kcache, block_table, req_ids, lengths, T)
     _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
@@ -300,7 +302,7 @@ def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: 
         "ekv_indexer_select", q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
         block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(), lengths.data_ptr(), T, int(max_len),
         topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(), workspace.numel(),
-        m_ptr, m_stride, m_width, p_ptr, int(window), _stream(),
+        m_ptr, m_stride, m_width, p_ptr, int(window), int(bool(merged_slots)), _stream(),
     )
 
 
