@@ -109,11 +109,10 @@ def dsa_step(ops, st, ev=None):
 
 def dsa_pre(ops, st):
     """Cache appends of the new token, the indexer's q quantization and the
-    windowed lengths."""
-    ops.indexer_k_insert(st["k_new"], st["slots"], st["kcache"])
-    ops.kv_append_quant(st["latent_new"], st["slots"], st["latent"])
-    st["q8"], st["wf"], st["digits"] = ops.indexer_q_quant(st["q_idx"], st["w_idx"])
-    ops.indexer_windowed_lengths(st["positions"], 128, st["lengths"])
+    windowed lengths, in one launch."""
+    st["q8"], st["wf"], st["digits"] = ops.dsa_decode_prologue(
+        st["k_new"], st["kcache"], st["latent_new"], st["latent"], st["slots"], st["q_idx"], st["w_idx"],
+        st["positions"], 128, st["lengths"])
 
 
 def dsa_filter(ops, st):

@@ -70,3 +70,32 @@ def test_append_with_block_table_slots(dev):
 
     ops.kv_append_quant(bf16_tensor(rows, dev), to_dev(slots, dev), cache)
     assert np.array_equal(cache.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dim", [576, 512])
+def test_dsa_decode_prologue_matches_separate_calls(dev, dim):
+    """ekv_dsa_decode_prologue == K insert + latent append + q quant + windowed
+    lengths issued one by one (each checked against the oracle elsewhere)."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(dim)
+    T, H, pages = 21, 64, 40
+    slots = rng.choice(pages * 64, T, replace=False).astype(np.int64)
+    slots[3] = -1  # skipped row
+    slots_t = to_dev(slots, dev)
+    positions = to_dev(rng.integers(0, 5000, T).astype(np.int64), dev)
+    k = bf16_tensor(randn_bf16(rng, (T, 128)), dev)
+    lat = bf16_tensor(randn_bf16(rng, (T, dim)), dev)
+    q = bf16_tensor(randn_bf16(rng, (T, H, 128), 2.0), dev)
+    w = bf16_tensor(randn_bf16(rng, (T, H)), dev)
+    kc = [torch.zeros((pages, 64 * 132), dtype=torch.uint8, device=dev) for _ in range(2)]
+    lc = [torch.zeros((pages, 64 * (dim + 4)), dtype=torch.uint8, device=dev) for _ in range(2)]
+    lens = [torch.full((T,), -5, dtype=torch.int32, device=dev) for _ in range(2)]
+    ops.indexer_k_insert(k, slots_t, kc[0])
+    ops.kv_append_quant(lat, slots_t, lc[0])
+    ref_q = ops.indexer_q_quant(q, w)
+    ops.indexer_windowed_lengths(positions, 128, lens[0])
+    got_q = ops.dsa_decode_prologue(k, kc[1], lat, lc[1], slots_t, q, w, positions, 128, lens[1])
+    assert torch.equal(kc[0], kc[1]) and torch.equal(lc[0], lc[1]) and torch.equal(lens[0], lens[1])
+    for a, b in zip(ref_q, got_q):
+        assert torch.equal(a, b)

@@ -44,8 +44,9 @@ struct AppendArgs {
   int32_t num_state;
 };
 
+// Rows of workgroup `block` (16 rows for D = 128, else 4).
 template <int D>
-__global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
+__device__ __forceinline__ void append_rows(const AppendArgs& a, int block) {
   constexpr int kRowsPerWave = (D == 128) ? 4 : 1;
   constexpr int kLanes = 64 / kRowsPerWave;       // lanes per row
   constexpr int kChunks = D / 8;                  // 16-byte bf16 chunks per row
@@ -54,7 +55,7 @@ __global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
   const int wave = threadIdx.x >> 6;
   const int sub = lane / kLanes;                  // row within the wave
   const int ln = lane % kLanes;                   // lane within the row
-  const int64_t t = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kRowsPerWave + sub;
+  const int64_t t = (static_cast<int64_t>(block) * 4 + wave) * kRowsPerWave + sub;
   if (t >= a.num_tokens) return;                  // whole row group exits together
 
   const uint16_t* src = a.rows + t * a.row_stride;
@@ -127,6 +128,11 @@ __global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
   }
 }
 
+template <int D>
+__global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
+  append_rows<D>(a, blockIdx.x);
+}
+
 // ---------------------------------------------------------------------------
 // merge_swa_topk   (attention.py:582-641)
 // ---------------------------------------------------------------------------
@@ -179,13 +185,32 @@ __global__ void __launch_bounds__(256) hadamard_rows_kernel(
 // ---------------------------------------------------------------------------
 // indexer_q_quant: one 16-lane group per (token, head) row of 128.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) indexer_q_quant_kernel(
-    const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const void* w,
-    int32_t w_is_bf16, int64_t w_stride, int32_t num_tokens, int32_t heads,
-    uint8_t* q_fp8, float* w_out, int8_t* q_digits) {
+struct QQuantArgs {
+  const uint16_t* q;         // [T, heads, 128] bf16
+  int64_t q_tok_stride, q_head_stride;
+  const void* w;             // [T, w_stride] bf16 or fp32
+  int32_t w_is_bf16;
+  int64_t w_stride;
+  int32_t num_tokens, heads;
+  uint8_t* q_fp8;            // [T, heads, 128]
+  float* w_out;              // [T, heads]
+  int8_t* q_digits;          // [T, 3, heads, 128] or null
+};
+
+// Rows (token, head) 16 * block .. +15, 16 lanes per row.
+__device__ __forceinline__ void q_quant_rows(const QQuantArgs& qa, int block) {
+  const uint16_t* q = qa.q;
+  const int64_t q_tok_stride = qa.q_tok_stride, q_head_stride = qa.q_head_stride;
+  const void* w = qa.w;
+  const int32_t w_is_bf16 = qa.w_is_bf16;
+  const int64_t w_stride = qa.w_stride;
+  const int32_t num_tokens = qa.num_tokens, heads = qa.heads;
+  uint8_t* q_fp8 = qa.q_fp8;
+  float* w_out = qa.w_out;
+  int8_t* q_digits = qa.q_digits;
   const int lane = threadIdx.x & 63;
   const int ln = lane & 15;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int64_t row = static_cast<int64_t>(block) * 16 + (threadIdx.x >> 4);
   if (row >= static_cast<int64_t>(num_tokens) * heads) return;
   const int64_t t = row / heads;
   const int h = static_cast<int>(row % heads);
@@ -233,6 +258,8 @@ __global__ void __launch_bounds__(256) indexer_q_quant_kernel(
   }
 }
 
+__global__ void __launch_bounds__(256) indexer_q_quant_kernel(QQuantArgs a) { q_quant_rows(a, blockIdx.x); }
+
 __global__ void fp8_digit_table_kernel(uint32_t* table) {
   const int i = threadIdx.x;
   if (i < 256) table[i] = fp8_digit_pack(static_cast<uint32_t>(i));
@@ -271,6 +298,45 @@ __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
   if (threadIdx.x == 0) lengths[t] = static_cast<int32_t>(len);
 }
 
+// ---------------------------------------------------------------------------
+// DSA decode prologue: the new token's indexer K row and latent row appended
+// (fp8 + UE8M0), the indexer q quantized and the windowed lengths, in one
+// launch.  Workgroups [0, k_blocks) append K rows, then latent rows, then q
+// rows; the last ones write the lengths.
+// ---------------------------------------------------------------------------
+struct DsaPrologueArgs {
+  AppendArgs k_rows;         // indexer K (D = 128)
+  AppendArgs latent;         // latent rows (D = the kernel's D)
+  QQuantArgs q;
+  const int64_t* positions;  // [T]
+  int32_t window;
+  int32_t* lengths;          // [T]
+  int32_t k_blocks, latent_blocks, q_blocks;
+};
+
+template <int D>
+__global__ void __launch_bounds__(256) dsa_prologue_kernel(DsaPrologueArgs a) {
+  int b = blockIdx.x;
+  if (b < a.k_blocks) {
+    append_rows<128>(a.k_rows, b);
+    return;
+  }
+  b -= a.k_blocks;
+  if (b < a.latent_blocks) {
+    append_rows<D>(a.latent, b);
+    return;
+  }
+  b -= a.latent_blocks;
+  if (b < a.q_blocks) {
+    q_quant_rows(a.q, b);
+    return;
+  }
+  b -= a.q_blocks;
+  const int i = b * 256 + threadIdx.x;
+  if (i < a.q.num_tokens)
+    a.lengths[i] = static_cast<int32_t>(max(a.positions[i] + 1 - a.window, static_cast<int64_t>(0)));
+}
+
 }  // namespace ekv
 
 // ===========================================================================
@@ -278,20 +344,46 @@ __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
 // ===========================================================================
 using namespace ekv;
 
-extern "C" int ekv_kv_append_quant(const uint16_t* rows, int64_t row_stride, int32_t num_tokens,
-                                   int32_t dim, const int64_t* slot_mapping, uint8_t* cache,
-                                   int64_t page_stride, int64_t num_pages, void* stream) {
-  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
-  if (num_tokens == 0) return 0;
+namespace {
+
+// Argument checks shared by the entry points that append rows / quantize q.
+int check_append(const uint16_t* rows, int64_t row_stride, int32_t dim, const int64_t* slot_mapping,
+                 const uint8_t* cache, int64_t page_stride) {
   EKV_CHECK(rows && slot_mapping && cache, "null pointer");
   EKV_CHECK(dim == 128 || dim == 512 || dim == 576, "dim must be 128, 512 or 576");
   EKV_CHECK(row_stride >= dim && row_stride % 8 == 0, "row_stride must be >= dim and a multiple of 8");
   EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0,
             "page_stride must hold 64 rows + 64 scales and be a multiple of 16");
   EKV_CHECK(aligned16(rows) && aligned16(cache), "rows and cache must be 16-byte aligned");
+  return 0;
+}
+
+int check_q_quant(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const void* weights,
+                  int32_t heads, const uint8_t* q_fp8, const float* w_out, const int8_t* q_digits) {
+  EKV_CHECK(q && weights && q_fp8 && w_out, "null pointer");
+  EKV_CHECK(heads > 0 && q_head_stride % 8 == 0 && q_tok_stride % 8 == 0, "strides must be multiples of 8");
+  EKV_CHECK(aligned16(q) && aligned8(q_fp8) && (q_digits == nullptr || aligned8(q_digits)), "misaligned buffers");
+  return 0;
+}
+
+AppendArgs append_args(const uint16_t* rows, int64_t row_stride, int32_t num_tokens, const int64_t* slot_mapping,
+                       uint8_t* cache, int64_t page_stride, int64_t num_pages) {
   AppendArgs a{};
   a.rows = rows; a.row_stride = row_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
   a.cache = cache; a.page_stride = page_stride; a.num_pages = num_pages;
+  return a;
+}
+
+}  // namespace
+
+extern "C" int ekv_kv_append_quant(const uint16_t* rows, int64_t row_stride, int32_t num_tokens,
+                                   int32_t dim, const int64_t* slot_mapping, uint8_t* cache,
+                                   int64_t page_stride, int64_t num_pages, void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  int rc = check_append(rows, row_stride, dim, slot_mapping, cache, page_stride);
+  if (rc) return rc;
+  const AppendArgs a = append_args(rows, row_stride, num_tokens, slot_mapping, cache, page_stride, num_pages);
   const int rows_per_block = (dim == 128) ? 16 : 4;
   dim3 grid((num_tokens + rows_per_block - 1) / rows_per_block);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -373,13 +465,50 @@ extern "C" int ekv_indexer_q_quant(const uint16_t* q, int64_t q_tok_stride, int6
                                    int8_t* q_digits, void* stream) {
   EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
   if (num_tokens == 0) return 0;
-  EKV_CHECK(q && weights && q_fp8 && w_out, "null pointer");
-  EKV_CHECK(heads > 0 && q_head_stride % 8 == 0 && q_tok_stride % 8 == 0, "strides must be multiples of 8");
-  EKV_CHECK(aligned16(q) && aligned8(q_fp8) && (q_digits == nullptr || aligned8(q_digits)), "misaligned buffers");
+  int rc = check_q_quant(q, q_tok_stride, q_head_stride, weights, heads, q_fp8, w_out, q_digits);
+  if (rc) return rc;
   const int64_t rows = static_cast<int64_t>(num_tokens) * heads;
+  const QQuantArgs a{q, q_tok_stride, q_head_stride, weights, weights_is_bf16, w_stride, num_tokens, heads,
+                     q_fp8, w_out, q_digits};
   hipLaunchKernelGGL(indexer_q_quant_kernel, dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), q, q_tok_stride, q_head_stride, weights,
-                     weights_is_bf16, w_stride, num_tokens, heads, q_fp8, w_out, q_digits);
+                     static_cast<hipStream_t>(stream), a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride,
+                                       int64_t k_num_pages, const uint16_t* latent, int64_t latent_stride,
+                                       int32_t dim, uint8_t* cache, int64_t page_stride, int64_t num_pages,
+                                       const int64_t* slot_mapping, int32_t num_tokens, const uint16_t* q,
+                                       int64_t q_tok_stride, int64_t q_head_stride, const void* weights,
+                                       int32_t weights_is_bf16, int64_t w_stride, int32_t heads, uint8_t* q_fp8,
+                                       float* w_out, int8_t* q_digits, const int64_t* positions, int32_t window,
+                                       int32_t* lengths, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && window >= 0, "bad sizes");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(dim == 512 || dim == 576, "latent dim must be 512 or 576");
+  int rc = check_append(k, k_stride, 128, slot_mapping, kcache, k_page_stride);
+  if (rc) return rc;
+  rc = check_append(latent, latent_stride, dim, slot_mapping, cache, page_stride);
+  if (rc) return rc;
+  rc = check_q_quant(q, q_tok_stride, q_head_stride, weights, heads, q_fp8, w_out, q_digits);
+  if (rc) return rc;
+  EKV_CHECK(positions && lengths, "null pointer");
+  DsaPrologueArgs a{};
+  a.k_rows = append_args(k, k_stride, num_tokens, slot_mapping, kcache, k_page_stride, k_num_pages);
+  a.latent = append_args(latent, latent_stride, num_tokens, slot_mapping, cache, page_stride, num_pages);
+  a.q = QQuantArgs{q, q_tok_stride, q_head_stride, weights, weights_is_bf16, w_stride, num_tokens, heads,
+                   q_fp8, w_out, q_digits};
+  a.positions = positions;
+  a.window = window;
+  a.lengths = lengths;
+  a.k_blocks = (num_tokens + 15) / 16;
+  a.latent_blocks = (num_tokens + 3) / 4;
+  a.q_blocks = static_cast<int32_t>((static_cast<int64_t>(num_tokens) * heads + 15) / 16);
+  const int len_blocks = (num_tokens + 255) / 256;
+  const dim3 grid(a.k_blocks + a.latent_blocks + a.q_blocks + len_blocks);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dim == 576) hipLaunchKernelGGL(dsa_prologue_kernel<576>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(dsa_prologue_kernel<512>, grid, dim3(256), 0, s, a);
   return ekv_launch_status();
 }
 

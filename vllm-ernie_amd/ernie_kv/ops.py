@@ -211,6 +211,50 @@ def indexer_q_quant(
     return q_fp8, w_out, digits
 
 
+def dsa_decode_prologue(
+    k: torch.Tensor,
+    kcache: torch.Tensor,
+    latent: torch.Tensor,
+    cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    q: torch.Tensor,
+    weights: torch.Tensor,
+    positions: torch.Tensor,
+    window: int,
+    lengths: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One launch doing ``indexer_k_insert(k, slot_mapping, kcache)``,
+    ``kv_append_quant(latent, slot_mapping, cache)``, ``indexer_q_quant(q,
+    weights)`` (returned) and ``indexer_windowed_lengths(positions, window,
+    lengths)``."""
+    _check_dev(k, kcache, latent, cache, slot_mapping, q, weights, positions, lengths)
+    _bits16(k)
+    _bits16(latent)
+    _bits16(q)
+    T = k.shape[0]
+    _need(k.shape == (T, 128) and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
+    _need(latent.dim() == 2 and latent.shape[0] == T and latent.stride(1) == 1, "latent must be [T, D] row-contiguous")
+    _need(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= T, "slot_mapping int64 [T]")
+    for c in (kcache, cache):
+        _need(c.dtype == torch.uint8 and c.dim() == 2 and c.stride(1) == 1, "caches uint8 [pages, bytes]")
+    _need(q.dim() == 3 and q.shape[0] == T and q.shape[2] == 128 and q.stride(2) == 1, "q must be [T, H, 128]")
+    H = q.shape[1]
+    _need(weights.shape[:2] == (T, H) and weights.stride(1) == 1, "weights [T, H]")
+    _need(weights.dtype in (torch.bfloat16, torch.float32), "weights bf16 or fp32")
+    _need(positions.dtype == torch.int64 and lengths.dtype == torch.int32, "positions int64, lengths int32")
+    q_fp8 = torch.empty((T, H, 128), dtype=torch.uint8, device=q.device)
+    w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
+    digits = torch.empty((T, 3, H, 128), dtype=torch.int8, device=q.device)
+    _lib.call(
+        "ekv_dsa_decode_prologue", k.data_ptr(), _rs(k), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
+        latent.data_ptr(), _rs(latent), latent.shape[1], cache.data_ptr(), _rs(cache), cache.shape[0],
+        slot_mapping.data_ptr(), T, q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), _rs(weights), H, q_fp8.data_ptr(), w_out.data_ptr(), digits.data_ptr(),
+        positions.data_ptr(), int(window), lengths.data_ptr(), _stream(),
+    )
+    return q_fp8, w_out, digits
+
+
 def indexer_windowed_lengths(positions: torch.Tensor, window: int, out: torch.Tensor) -> None:
     _check_dev(positions, out)
     _need(positions.dtype == torch.int64 and out.dtype == torch.int32, "positions int64, out int32")
