@@ -1007,6 +1007,7 @@ struct SelectSmem {
   uint32_t wmin[kSelThreads / 64], wmax[kSelThreads / 64];  // per-wave key range
   int res[2];
   int cnt;
+  uint32_t pmin, pmax;  // range of the current pass's keys
 };
 
 // LDS histogram increment: one atomic for the whole wave when every active
@@ -1188,12 +1189,18 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
     uint32_t prefix = kmin & mask;
     int remaining = k;
     int top = 32 - common;  // bits [0, top) are still open
+    bool first = true;      // the first pass's key range is [kmin, kmax]
     while (top > 0) {
       const int width = min(11, top);
       const int sh = top - width;
       const int nb = 1 << width;
       for (int b = tid; b < 2048; b += kSelThreads) s_hist[b] = 0;
+      if (tid == 0) {
+        sm.pmin = 0xffffffffu;
+        sm.pmax = 0u;
+      }
       __syncthreads();
+      uint32_t plo = 0xffffffffu, phi = 0u;  // range of the keys under the prefix
       for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
 #pragma unroll
         for (int j = 0; j < kSelPerThread; ++j) {
@@ -1201,12 +1208,31 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
           int bin = -1;
           if (i < n) {
             const uint32_t key = key_at(i);
-            if ((key & mask) == prefix) bin = static_cast<int>((key >> sh) & static_cast<uint32_t>(nb - 1));
+            if ((key & mask) == prefix) {
+              bin = static_cast<int>((key >> sh) & static_cast<uint32_t>(nb - 1));
+              plo = min(plo, key);
+              phi = max(phi, key);
+            }
           }
           hist_add_ties(s_hist, bin);
         }
       }
+      if (!first) {
+        for (int off = 32; off > 0; off >>= 1) {
+          plo = min(plo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(plo), off)));
+          phi = max(phi, static_cast<uint32_t>(__shfl_xor(static_cast<int>(phi), off)));
+        }
+        if ((tid & 63) == 0) {
+          atomicMin(&sm.pmin, plo);
+          atomicMax(&sm.pmax, phi);
+        }
+      }
       __syncthreads();
+      if (!first && sm.pmin == sm.pmax) {  // every key left is the same: it is the threshold
+        prefix = sm.pmin;
+        break;
+      }
+      first = false;
       int above;
       const int bin = find_bin<kSelThreads>(s_hist, nb, remaining, s_wave, s_res, above);
       remaining -= above;
@@ -1216,19 +1242,31 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
       if (top == 0) break;
       const int m = static_cast<int>(s_hist[bin]);  // keys sharing the threshold's prefix
       __syncthreads();                              // before s_hist is reused
-      if (m <= 64) {
+      if (m <= kSelThreads) {
         // Few keys share the prefix: rank them directly.  The threshold is
-        // the key with (count above) < remaining <= (count above) + (count equal).
+        // the key with (count above) < remaining <= (count above) + (count
+        // equal).  The keys are collected with one LDS atomic per wave.
         if (tid == 0) sm.cnt = 0;
         __syncthreads();
-        uint32_t* s_small = s_hist;
+        uint32_t* s_small = s_hist;  // 2048 entries, 16-byte aligned
+        const int lane = tid & 63;
         for (int i0 = 0; i0 < n; i0 += kSelThreads * kSelPerThread) {
 #pragma unroll
           for (int j = 0; j < kSelPerThread; ++j) {
             const int i = i0 + j * kSelThreads + tid;
+            uint32_t key = 0;
+            bool hit = false;
             if (i < n) {
-              const uint32_t key = key_at(i);
-              if ((key & mask) == prefix) s_small[atomicAdd(&sm.cnt, 1)] = key;
+              key = key_at(i);
+              hit = (key & mask) == prefix;
+            }
+            const uint64_t bal = __ballot(hit);
+            if (bal != 0) {  // wave-uniform
+              const int leader = static_cast<int>(__builtin_ctzll(bal));
+              int base = 0;
+              if (lane == leader) base = atomicAdd(&sm.cnt, static_cast<int>(__popcll(bal)));
+              base = __shfl(base, leader);
+              if (hit) s_small[base + static_cast<int>(__popcll(bal & ((uint64_t{1} << lane) - 1)))] = key;
             }
           }
         }
@@ -1236,7 +1274,17 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
         if (tid < m) {
           const uint32_t mine = s_small[tid];
           int gt = 0, eq = 0;
-          for (int j = 0; j < m; ++j) {
+          auto rank4 = [&](uint4 v) {
+            gt += (v.x > mine) + (v.y > mine) + (v.z > mine) + (v.w > mine);
+            eq += (v.x == mine) + (v.y == mine) + (v.z == mine) + (v.w == mine);
+          };
+          int j = 0;
+#pragma unroll 4
+          for (; j + 8 <= m; j += 8) {  // broadcast reads, two 16-byte loads per step
+            rank4(*reinterpret_cast<const uint4*>(s_small + j));
+            rank4(*reinterpret_cast<const uint4*>(s_small + j + 4));
+          }
+          for (; j < m; ++j) {
             const uint32_t o = s_small[j];
             gt += o > mine;
             eq += o == mine;
