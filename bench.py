@@ -46,6 +46,7 @@ def parse():
     p.add_argument("--batch", type=int, default=32)
     p.add_argument("--ctx", type=int, default=131072)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-hca", action="store_true", help="skip the HCA chunked-prefill write measurement")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
@@ -126,6 +127,86 @@ def dsa_post(ops, st):
                        positions=st["positions"], window=128)
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
                           block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
+
+
+def build_hca_write(torch, ops, seed: int, B: int = 16, chunk: int = 8192, max_off: int = 65536, D: int = 576):
+    """Chunked-prefill cache write: B sequences each appending a `chunk`-token
+    chunk at a random offset in [0, max_off), scattered by a random slot
+    mapping into a 1M-slot fp8 pool; every completed 128-token span is
+    compressed and the 128-token window ring is updated.  Synthetic inputs."""
+    dev = torch.device("cuda:0")
+    gc = torch.Generator().manual_seed(seed + 1)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    pages = 16384  # 1,048,576 slots
+    spans = (max_off + chunk) // 128 + 1
+    comp_pages, ring_pages_per = (spans + 63) // 64, 2
+    perm = torch.randperm(pages, generator=gc)
+    comp_bt = perm[: B * comp_pages].view(B, comp_pages).to(torch.int32).to(dev)
+    ring_pages = perm[B * comp_pages: B * (comp_pages + ring_pages_per)].view(B, ring_pages_per).to(torch.int32)
+    rest = perm[B * (comp_pages + ring_pages_per):]
+    T = B * chunk
+    free_slots = (rest[:, None] * 64 + torch.arange(64)[None, :]).flatten()
+    slots = free_slots[torch.randperm(free_slots.numel(), generator=gc)[:T]].to(torch.int64).to(dev)
+    offs = torch.randint(0, max_off, (B,), generator=gc)
+    positions = (offs[:, None] + torch.arange(chunk)[None, :]).flatten().to(torch.int64).to(dev)
+    token_seq = torch.arange(B, dtype=torch.int32).repeat_interleave(chunk).to(dev)
+    qsl = (torch.arange(B + 1, dtype=torch.int32) * chunk).to(dev)
+    ang = (torch.arange(spans, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    cos_sin = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(dev)
+    st = dict(
+        B=B, T=T, chunk=chunk, D=D, spans_done=int(((offs + chunk) // 128 - offs // 128).sum()),
+        pool=torch.zeros((pages, 64 * (D + 4)), dtype=torch.uint8, device=dev),
+        latent=torch.randn(T, D, device=dev, generator=gd).to(torch.bfloat16),
+        kv_score=torch.randn(T, 2 * D, device=dev, generator=gd).to(torch.bfloat16),
+        state=torch.randn(B + 2, 256, 2 * D, device=dev, generator=gd).to(torch.bfloat16),
+        state_slot=torch.randperm(B + 2, generator=gc)[:B].to(torch.int32).to(dev),
+        ape=(torch.randn(128, D, device=dev, generator=gd) * 0.5).contiguous(),
+        norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=gd)).contiguous(),
+        cos_sin=cos_sin, comp_bt=comp_bt, ring_pages=ring_pages.to(dev), slots=slots, positions=positions,
+        token_seq=token_seq, qsl=qsl,
+    )
+    return st
+
+
+def hca_write_step(ops, st):
+    """Compress the completed spans, then append (fp8 rows, window ring, state ring)."""
+    ops.hca_compress(st["kv_score"], st["positions"], st["qsl"], st["chunk"], st["state"], st["state_slot"], st["ape"],
+                     st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"], st["pool"])
+    ops.hca_append(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["pool"],
+                   st["ring_pages"], 128, st["state"], st["state_slot"])
+
+
+def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
+    st = build_hca_write(torch, ops, seed)
+    for _ in range(2):
+        hca_write_step(ops, st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        hca_write_step(ops, st)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    T, D, B = st["T"], st["D"], st["B"]
+    # the survey's algorithmic bytes: latent rows read (bf16) and written
+    # (fp8 + scale), compressed entries and window-ring rows written
+    surveyed = T * D * 2 + T * (D + 4) + st["spans_done"] * (D + 4) + B * 128 * (D + 4)
+    # plus the compressor's kv || score rows (bf16, 2D per token) read once and
+    # the state-ring rows (last 256 positions per sequence) copied
+    full = surveyed + T * 2 * D * 2 + 2 * B * 256 * 2 * D * 2
+    return {
+        "workload": f"hca_chunked_prefill_b{B}_chunk{st['chunk']}",
+        "kernels": "hca_compress_kernel<576> + kv_append_quant_kernel<576> (HCA rows, window ring, state ring)",
+        "ms": round(ms, 4),
+        "bytes_latent_rows": surveyed,
+        "GB/s_latent_rows": round(surveyed / (ms * 1e-3) / 1e9, 1),
+        "frac_latent_rows": round(surveyed / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_with_kv_score": full,
+        "GB/s_with_kv_score": round(full / (ms * 1e-3) / 1e9, 1),
+        "frac_with_kv_score": round(full / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
 
 
 def dsa_bytes(B: int, ctx: int) -> dict:
@@ -254,6 +335,10 @@ def main():
             "mfma_frac": round(filt_tflops / FP8_PEAK_TFLOPS, 4),
         },
     }
+    if not args.no_hca:
+        del st
+        torch.cuda.empty_cache()
+        line["hca_write"] = measure_hca_write(torch, ops, args.seed)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.batch, args.ctx, args.seed)
     print(json.dumps(line), flush=True)

@@ -97,6 +97,24 @@ int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t
                    const int32_t* state_slot, int32_t num_state, void* stream);
 
 /*
+ * The whole HCA write of one step in one launch: exactly ekv_hca_compress
+ * followed by ekv_hca_append with the same arguments (same bytes in the pool
+ * and the state ring), with the compression of completed spans, the row
+ * appends and the ring updates running concurrently.  comp_block_table must
+ * not be NULL; ring_pages / state may be.  Replaces the cache-write half of
+ * DeepseekV4Attention._prepare_and_attn_fn (nvidia/attention.py:494-505) with
+ * its compressor call (Ernie5_5Compressor.forward, nvidia/attention.py:398-408).
+ */
+int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score, int64_t kvs_stride,
+                  int32_t num_tokens, int32_t dim, const int64_t* slot_mapping, const int64_t* positions,
+                  const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs, int32_t max_query_len,
+                  uint16_t* state, const int32_t* state_slot, int32_t num_state, const float* ape,
+                  const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                  const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                  int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride /*bytes*/,
+                  int64_t num_pages, void* stream);
+
+/*
  * HCA decode index rows: [compressed slots 0..n_c-1 | ring slots of positions
  * p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window), and the row
  * lengths.  Replaces the compressed+window index construction inside

@@ -11,20 +11,35 @@ sites -- **parity unpinned** against upstream; it is pinned against closed
 forms (constant gate -> mean, one-hot gate -> copy, permutation invariance) and
 an fp64 brute force in ``tests/test_oracle_hca.py``.
 
-Compressor of span j (positions 128j .. 128j+127), per channel c < D::
+Compressor of span j (positions 128j .. 128j+127), per channel c < D: the
+softmax over the span of g_i = fl32(score_i[c] + ape[i, c]) weights kv_i[c].
+It is evaluated in one pass, as an online softmax over 4 interleaved row
+groups (group r holds rows r, r+4, ..., r+124) in chunks of 4 of a group's
+rows, then a fixed-order merge of the groups.  A group's shift m_r moves (and
+its sums are rescaled) only when a chunk's max exceeds it by more than
+SLACK = 8, so every term is at most e**8::
 
-    g_i = fl32(score_i[c] + ape[i, c]);   m = max_i g_i
-    e_i = exp_ekv(fl32(g_i - m))
-    Z, N = 0, 0;  for i in 0..127:  Z = fl32(Z + e_i);  N = fl32(N + fl32(e_i * kv_i[c]))
+    for r in 0..3:
+        m_r, Z_r, N_r = -inf, 0, 0
+        for each chunk C of group r's rows, in order:
+            mc = max(m_r, max_{i in C} g_i)
+            if mc > fl32(m_r + SLACK):
+                s = exp_ekv(fl32(m_r - mc));  Z_r = fl32(Z_r * s);  N_r = fl32(N_r * s);  m_r = mc
+            for i in C, in order:
+                e = exp_ekv(fl32(g_i - m_r))
+                Z_r = fl32(Z_r + e);  N_r = fma(e, kv_i[c], N_r)
+    M = max_r m_r;  Z, N = 0, 0
+    for r in 0..3:  s = exp_ekv(fl32(m_r - M));  Z = fma(Z_r, s, Z);  N = fma(N_r, s, N)
     x_c = fl32(N / Z)
     RMSNorm over D (eps from rms_norm_eps), sums in the kernel's order
     RoPE (interleaved pairs) on channels D-64..D-1 at position 128j
     UE8M0 fp8 quant -> compressed row j
 
 ``exp_ekv`` is this build's own exp: ``2**n * P(f)`` with ``n = rint(x*log2 e)``,
-``f = x*log2 e - n`` and ``P`` the degree-6 Taylor polynomial of ``2**f``
-evaluated by Horner in fp32 (no fused multiply-add), flushing to 0 below
-``2**-125``.  The kernel evaluates the same operations.
+``f = x*log2 e - n`` and ``P`` a degree-5 polynomial fit of ``2**f`` (``EXP_C``)
+evaluated by Horner in fp32 with fused multiply-adds, flushing to 0 below
+``2**-125``.  ``fma(a, b, c)`` is ``a*b + c`` with one fp32 rounding (``fma32``
+below).  The kernel evaluates the same operations.
 
 State: the kv_score rows of a sequence's most recent 256 positions live in a
 ring ``state[state_slot, pos % 256]`` so a span that completes in a later call
@@ -47,7 +62,38 @@ STATE_RING = 256
 WINDOW = 128
 
 LOG2E = np.float32(1.0 / math.log(2.0))
-EXP_C = [np.float32(math.log(2.0) ** k / math.factorial(k)) for k in range(7)]
+# P(f) ~ 2**f on [-1/2, 1/2]: degree 5, coefficients from a Remez exchange on
+# the relative error (then rounded to fp32, P(0) = 1 exactly); evaluated in
+# fp32 Horner with fused multiply-adds its relative error is below 2.2e-7.
+EXP_C = [np.float32(float.fromhex(h)) for h in (
+    "0x1.0p+0", "0x1.62e428p-1", "0x1.ebf918p-3", "0x1.c6b6e4p-5", "0x1.3d0c52p-7", "0x1.5c08e6p-10")]
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """fp32 fused multiply-add ``round_fp32(a*b + c)`` with one rounding
+    (nearest-even), for finite fp32 inputs whose result is a normal fp32.
+
+    ``a*b`` is exact in fp64 (48 significant bits); ``s = fl64(a*b + c)`` and
+    its exact remainder ``err`` (Knuth's TwoSum) give the exact sum
+    ``s + err``.  Rounding ``s`` to fp32 is then the correct rounding of the
+    exact sum unless ``s`` sits exactly halfway between two fp32 neighbours
+    and ``err != 0``; in that case the neighbour on ``err``'s side is the
+    correctly rounded result."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    p = a64 * b64
+    s = p + c64
+    bb = s - p
+    err = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(np.float32)
+    d = s - r.astype(np.float64)
+    toward = np.where(d > 0, np.float32(np.inf), np.float32(-np.inf)).astype(np.float32)
+    other = np.nextafter(r, toward).astype(np.float32)
+    mid = (d != 0) & (s == (r.astype(np.float64) + other.astype(np.float64)) * 0.5)
+    # at a midpoint r is the even neighbour; err decides between r and other
+    pick_other = mid & (err != 0) & (np.sign(err) == np.sign(d))
+    return np.where(pick_other, other, r).astype(np.float32)
 
 
 def exp_ekv(x: np.ndarray) -> np.ndarray:
@@ -55,11 +101,51 @@ def exp_ekv(x: np.ndarray) -> np.ndarray:
     t = (x * LOG2E).astype(np.float32)
     n = np.rint(t).astype(np.float32)
     f = (t - n).astype(np.float32)
-    p = EXP_C[6]
-    for k in range(5, -1, -1):
-        p = ((p * f).astype(np.float32) + EXP_C[k]).astype(np.float32)
+    p = np.broadcast_to(EXP_C[5], f.shape).astype(np.float32)
+    for k in range(4, -1, -1):
+        p = fma32(p, f, EXP_C[k])
     out = np.ldexp(p, np.clip(n, -200, 200).astype(np.int32)).astype(np.float32)
     return np.where(t < np.float32(-125.0), np.float32(0.0), out).astype(np.float32)
+
+
+ROW_GROUPS = 4           # interleaved row groups of the online softmax
+CHUNK = 4                # rows of a group per online-softmax step
+SLACK = np.float32(8.0)  # a chunk max above shift + SLACK moves the shift
+
+
+def span_softmax_sum(g: np.ndarray, kv: np.ndarray) -> np.ndarray:
+    """sum_i softmax_i(g) * kv_i per channel, in the one-pass order above
+    (``g, kv [128, D]`` fp32; returns ``x [D]``)."""
+    f32 = np.float32
+    D = g.shape[1]
+    ms, Zs, Ns = [], [], []
+    with np.errstate(invalid="ignore", over="ignore"):
+        for r in range(ROW_GROUPS):
+            m = np.full(D, -np.inf, f32)
+            Z = np.zeros(D, f32)
+            N = np.zeros(D, f32)
+            rows = np.arange(r, SPAN, ROW_GROUPS)
+            for k0 in range(0, len(rows), CHUNK):
+                chunk = rows[k0 : k0 + CHUNK]
+                mc = np.maximum(m, g[chunk].max(axis=0))
+                move = mc > (m + SLACK).astype(f32)
+                s = exp_ekv((m - mc).astype(f32))
+                Z = np.where(move, (Z * s).astype(f32), Z)
+                N = np.where(move, (N * s).astype(f32), N)
+                m = np.where(move, mc, m)
+                for i in chunk:
+                    e = exp_ekv((g[i] - m).astype(f32))
+                    Z = (Z + e).astype(f32)
+                    N = fma32(e, kv[i], N)
+            ms.append(m), Zs.append(Z), Ns.append(N)
+        M = np.max(np.stack(ms), axis=0)
+        Z = np.zeros(D, f32)
+        N = np.zeros(D, f32)
+        for r in range(ROW_GROUPS):
+            s = exp_ekv((ms[r] - M).astype(f32))
+            Z = fma32(Zs[r], s, Z)
+            N = fma32(Ns[r], s, N)
+    return (N / Z).astype(f32)
 
 
 def compress_span(
@@ -74,14 +160,7 @@ def compress_span(
     kv = np.asarray(kv, np.float32)
     D = kv.shape[1]
     g = (np.asarray(score, np.float32) + np.asarray(ape, np.float32)).astype(np.float32)
-    m = g.max(axis=0)
-    e = exp_ekv((g - m[None, :]).astype(np.float32))
-    Z = np.zeros(D, np.float32)
-    N = np.zeros(D, np.float32)
-    for i in range(SPAN):
-        Z = (Z + e[i]).astype(np.float32)
-        N = (N + (e[i] * kv[i]).astype(np.float32)).astype(np.float32)
-    x = (N / Z).astype(np.float32)
+    x = span_softmax_sum(g, kv)
     sq = (x * x).astype(np.float32).reshape(D // 4, 4)
     part = np.zeros(D // 4, np.float32)
     for k in range(4):

@@ -32,7 +32,7 @@ class HcaCase:
         self.st = oh.HcaState(self.pages, dim, num_seqs + 2)
 
 
-def _run_call(dev, case, rng, starts, counts, gpu):
+def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
     D = case.dim
     positions, token_seq, qsl = [], [], [0]
     for b, (p0, n) in enumerate(zip(starts, counts)):
@@ -52,14 +52,20 @@ def _run_call(dev, case, rng, starts, counts, gpu):
 
     d = lambda a: to_dev(a, dev)  # noqa: E731
     kvs_t = bf16_tensor(kv_score, dev)
+    if fused:
+        ops.hca_write(bf16_tensor(latent, dev), kvs_t, d(slots), d(positions), d(token_seq), d(qsl), int(max(counts)),
+                      gpu["state"], d(case.state_slot), d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin),
+                      d(case.comp_bt), d(case.ring_pages), case.ring, gpu["pool"])
+        return
     ops.hca_compress(kvs_t, d(positions), d(qsl), int(max(counts)), gpu["state"], d(case.state_slot),
                      d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin), d(case.comp_bt), gpu["pool"])
     ops.hca_append(bf16_tensor(latent, dev), kvs_t, d(slots), d(positions), d(token_seq), d(qsl), gpu["pool"],
                    d(case.ring_pages), case.ring, gpu["state"], d(case.state_slot))
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
 @pytest.mark.parametrize("dim", [576, 512])
-def test_hca_write_path_exact(dev, dim):
+def test_hca_write_path_exact(dev, dim, fused):
     rng = np.random.default_rng(dim)
     case = HcaCase(rng, dim, num_seqs=3, max_pos=1400, ring=192)
     gpu = {
@@ -76,7 +82,7 @@ def test_hca_write_path_exact(dev, dim):
         ([307, 304, 134], [900, 1, 700]),
     ]
     for starts, counts in calls:
-        _run_call(dev, case, rng, starts, counts, gpu)
+        _run_call(dev, case, rng, starts, counts, gpu, fused)
         torch.cuda.synchronize()
         assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool), f"pool mismatch after call {starts}"
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)

@@ -211,6 +211,21 @@ def test_compressor_fp64_brute_force():
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
 
 
+def test_compressor_fp64_brute_force_with_moving_shift():
+    """Gates that rise along the span (0 .. 60, plus noise): every row group's
+    shift moves many times, and the result still matches the fp64 softmax."""
+    rng = np.random.default_rng(13)
+    kv, sc = _span(rng)
+    ramp = np.linspace(0.0, 60.0, 128, dtype=np.float32)[:, None]
+    sc = bf16_round((ramp + rng.standard_normal((128, 576))).astype(np.float32))
+    ape = (rng.standard_normal((128, 576)) * 0.5).astype(np.float32)
+    w = np.ones(576, np.float32)
+    cs = oi.rope_cos_sin(np.array([128 * 3]), 64, 1.6e5)[0]
+    got = oh.compress_span(kv, sc, ape, w, 1e-6, cs)
+    ref = _fp64_compress(kv, sc, ape, w, 1e-6, cs)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
 def test_compressor_constant_gate_is_mean_and_one_hot_is_copy():
     rng = np.random.default_rng(9)
     kv, _ = _span(rng)
@@ -237,6 +252,51 @@ def test_compressor_permutation_invariance():
     a = oh.compress_span(kv, sc, ape, one, 1e-6, cs)
     b = oh.compress_span(kv[perm], sc[perm], ape[perm], one, 1e-6, cs)
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def _fma32_exact(a, b, c):
+    """Correctly rounded fp32 a*b + c by exact rational arithmetic: the
+    nearest of the fp32 values around the fp64 approximation, ties to the
+    even significand."""
+    from fractions import Fraction
+
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    r = np.float32(float(exact))
+    cands = [r]
+    for _ in range(2):
+        cands += [np.nextafter(cands[-1], np.float32(np.inf))]
+    lo = r
+    for _ in range(2):
+        lo = np.nextafter(lo, np.float32(-np.inf))
+        cands.append(lo)
+    best = min(cands, key=lambda v: (abs(Fraction(float(v)) - exact), int(np.float32(v).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_fma32_is_correctly_rounded():
+    """The oracle's fp32 fused multiply-add against exact rational rounding,
+    on random operands and on products that land exactly halfway between two
+    fp32 values, nudged either way by a tiny addend (where rounding the fp64
+    sum would round twice and pick the even neighbour wrongly)."""
+    rng = np.random.default_rng(12)
+    n = 3000
+    a = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    b = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    c = (rng.standard_normal(n) * 2.0 ** rng.integers(-40, 20, n)).astype(np.float32)
+    cases = list(zip(a, b, c))
+    for m in range(12, 24):
+        x = np.float32(1.0 + 2.0 ** -m)
+        for scale in (1.0, 2.0 ** -30, 2.0 ** 20):
+            for tiny in (0.0, 2.0 ** -60, -(2.0 ** -60), 2.0 ** -90):
+                cases.append((np.float32(x * scale), x, np.float32(tiny * scale)))
+    a, b, c = (np.array(v, np.float32) for v in zip(*cases))
+    got = oh.fma32(a, b, c)
+    want = np.array([_fma32_exact(*t) for t in cases], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the halfway case: 1 + 2^-11 + 2^-24 is a midpoint; + 2^-60 rounds up
+    x = np.float32(1.0 + 2.0 ** -12)
+    assert oh.fma32(x, x, np.float32(2.0 ** -60)) == np.float32(1.0 + 2.0 ** -11 + 2.0 ** -23)
+    assert oh.fma32(x, x, np.float32(0.0)) == np.float32(1.0 + 2.0 ** -11)
 
 
 def test_exp_ekv_accuracy():

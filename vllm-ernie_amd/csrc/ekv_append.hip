@@ -16,121 +16,32 @@
 // CPU oracle, so no multiply-add may be fused behind its back.
 #include "ekv_common.h"
 #include "ekv_internal.h"
+#include "ekv_rows.h"
 
 namespace ekv {
 
-// ---------------------------------------------------------------------------
-// kv_append_quant
-// ---------------------------------------------------------------------------
-struct AppendArgs {
-  const uint16_t* rows;      // [T, row_stride] bf16
-  int64_t row_stride;        // elements
-  int32_t num_tokens;
-  const int64_t* slot_mapping;  // [T], < 0 -> skip
-  uint8_t* cache;            // [num_pages, page_stride]
-  int64_t page_stride;
-  int64_t num_pages;
-  // HCA extras (all optional)
-  const int64_t* positions;  // [T]
-  const int32_t* token_seq;  // [T], < 0 -> padding
-  const int32_t* qsl;        // [B + 1]
-  const int32_t* ring_pages; // [B, ring_stride]
-  int32_t ring_stride;
-  int32_t ring;              // ring length R (multiple of 64)
-  const uint16_t* kv_score;  // [T, kvs_stride] bf16, 2*D wide
-  int64_t kvs_stride;
-  uint16_t* state;           // [num_state, 256, 2*D] bf16
-  const int32_t* state_slot; // [B]
-  int32_t num_state;
-};
-
-// Rows of workgroup `block` (16 rows for D = 128, else 4).
-template <int D>
-__device__ __forceinline__ void append_rows(const AppendArgs& a, int block) {
-  constexpr int kRowsPerWave = (D == 128) ? 4 : 1;
-  constexpr int kLanes = 64 / kRowsPerWave;       // lanes per row
-  constexpr int kChunks = D / 8;                  // 16-byte bf16 chunks per row
-  constexpr int kPerLane = (kChunks + kLanes - 1) / kLanes;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int sub = lane / kLanes;                  // row within the wave
-  const int ln = lane % kLanes;                   // lane within the row
-  const int64_t t = (static_cast<int64_t>(block) * 4 + wave) * kRowsPerWave + sub;
-  if (t >= a.num_tokens) return;                  // whole row group exits together
-
-  const uint16_t* src = a.rows + t * a.row_stride;
-  float v[kPerLane][8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    const int c = ln + k * kLanes;
-    if (c < kChunks) {
-      uint4 w = *reinterpret_cast<const uint4*>(src + 8 * c);
-      uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[k][2 * i] = __uint_as_float(ww[i] << 16);
-        v[k][2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
-        amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
-      }
-    }
-  }
-  amax = wave_max_xor(amax, kLanes);
-  const int e = ue8m0_exponent(amax);
-  const float inv = exp2i(-e);
-  const float scale = exp2i(e);
-
-  uint2 packed[kPerLane];
-#pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    uint32_t b0 = f32x2_to_fp8(v[k][0] * inv, v[k][1] * inv);
-    uint32_t b1 = f32x2_to_fp8(v[k][2] * inv, v[k][3] * inv);
-    uint32_t b2 = f32x2_to_fp8(v[k][4] * inv, v[k][5] * inv);
-    uint32_t b3 = f32x2_to_fp8(v[k][6] * inv, v[k][7] * inv);
-    packed[k] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-  }
-
-  auto store_row = [&](int64_t slot) {
-    if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
-    uint8_t* page = a.cache + (slot / kPageTokens) * a.page_stride;
-    const int64_t off = slot % kPageTokens;
-#pragma unroll
-    for (int k = 0; k < kPerLane; ++k) {
-      const int c = ln + k * kLanes;
-      if (c < kChunks) *reinterpret_cast<uint2*>(page + off * D + 8 * c) = packed[k];
-    }
-    if (ln == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = scale;
-  };
-
-  store_row(a.slot_mapping[t]);
-
-  if (a.token_seq == nullptr) return;
-  const int b = a.token_seq[t];
-  if (b < 0) return;
-  const int t0 = a.qsl[b];
-  const int n = a.qsl[b + 1] - t0;
-  const int64_t p = a.positions[t];
-  const int64_t last = a.positions[t0] + n - 1;
-  if (a.ring_pages != nullptr && p > last - a.ring) {
-    const int64_t r = p % a.ring;
-    const int64_t slot =
-        static_cast<int64_t>(a.ring_pages[static_cast<int64_t>(b) * a.ring_stride + r / kPageTokens]) *
-            kPageTokens + r % kPageTokens;
-    store_row(slot);
-  }
-  if (a.state != nullptr && p > last - kStateRing) {
-    const int st = a.state_slot[b];
-    if (st >= 0 && st < a.num_state) {
-      const uint4* s = reinterpret_cast<const uint4*>(a.kv_score + t * a.kvs_stride);
-      uint4* d = reinterpret_cast<uint4*>(a.state + (static_cast<int64_t>(st) * kStateRing + p % kStateRing) * (2 * D));
-      for (int c = ln; c < 2 * kChunks; c += kLanes) d[c] = s[c];
-    }
-  }
-}
-
 template <int D>
 __global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
-  append_rows<D>(a, blockIdx.x);
+  append_rows<D, kAppendSeq<D>>(a, blockIdx.x);
+}
+
+// HCA append: workgroups [0, main_blocks) store every row at its slot, the
+// rest write the window ring and state ring rows of each sequence's tail,
+// kTailBlockRows rows of one sequence each.
+constexpr int kTailBlockRows = 16;
+
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
+hca_append_kernel(AppendArgs a, int main_blocks, int tail_rows) {
+  const int block = static_cast<int>(blockIdx.x);
+  if (block < main_blocks) {
+    append_rows<D, kAppendSeq<D>>(a, block);
+    return;
+  }
+  const int tb = block - main_blocks;
+  const int blocks_per_seq = tail_rows / kTailBlockRows;
+  const int k_lo = (tb % blocks_per_seq) * kTailBlockRows;
+  hca_tail_range<D, 4, 1>(a, tb / blocks_per_seq, k_lo, k_lo + kTailBlockRows);
 }
 
 // ---------------------------------------------------------------------------
@@ -318,12 +229,12 @@ template <int D>
 __global__ void __launch_bounds__(256) dsa_prologue_kernel(DsaPrologueArgs a) {
   int b = blockIdx.x;
   if (b < a.k_blocks) {
-    append_rows<128>(a.k_rows, b);
+    append_rows<128, 1>(a.k_rows, b);
     return;
   }
   b -= a.k_blocks;
   if (b < a.latent_blocks) {
-    append_rows<D>(a.latent, b);
+    append_rows<D, 1>(a.latent, b);
     return;
   }
   b -= a.latent_blocks;
@@ -384,7 +295,7 @@ extern "C" int ekv_kv_append_quant(const uint16_t* rows, int64_t row_stride, int
   int rc = check_append(rows, row_stride, dim, slot_mapping, cache, page_stride);
   if (rc) return rc;
   const AppendArgs a = append_args(rows, row_stride, num_tokens, slot_mapping, cache, page_stride, num_pages);
-  const int rows_per_block = (dim == 128) ? 16 : 4;
+  const int rows_per_block = append_block_rows(dim, dim == 128 ? kAppendSeq<128> : kAppendSeq<576>);
   dim3 grid((num_tokens + rows_per_block - 1) / rows_per_block);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dim == 128) hipLaunchKernelGGL(kv_append_quant_kernel<128>, grid, dim3(256), 0, s, a);
@@ -408,29 +319,25 @@ extern "C" int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, con
                               const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
                               uint16_t* state, const int32_t* state_slot, int32_t num_state,
                               void* stream) {
-  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
   if (num_tokens == 0) return 0;
-  EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
-  EKV_CHECK(latent && slot_mapping && positions && token_seq && qsl && pool, "null pointer");
-  EKV_CHECK(latent_stride >= dim && latent_stride % 8 == 0, "bad latent_stride");
-  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
-  EKV_CHECK(ring_pages == nullptr || (ring >= kWindow && ring % kPageTokens == 0 && ring_stride >= ring / kPageTokens),
-            "ring must be a multiple of 64, >= 128, with ring_stride >= ring/64");
-  EKV_CHECK(state == nullptr || (kv_score && state_slot && kvs_stride >= 2 * dim && kvs_stride % 8 == 0),
-            "state needs kv_score (stride >= 2*dim, multiple of 8) and state_slot");
-  EKV_CHECK(aligned16(latent) && aligned16(pool) && (state == nullptr || (aligned16(state) && aligned16(kv_score))),
-            "buffers must be 16-byte aligned");
-  AppendArgs a{};
-  a.rows = latent; a.row_stride = latent_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
-  a.cache = pool; a.page_stride = page_stride; a.num_pages = num_pages;
-  a.positions = positions; a.token_seq = token_seq; a.qsl = qsl;
-  a.ring_pages = ring_pages; a.ring_stride = ring_stride; a.ring = ring;
-  a.kv_score = kv_score; a.kvs_stride = kvs_stride; a.state = state; a.state_slot = state_slot;
-  a.num_state = num_state;
-  dim3 grid((num_tokens + 3) / 4);
+  AppendArgs a;
+  const int rc = hca_append_args(a, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping,
+                                 positions, token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages,
+                                 ring_stride, ring, state, state_slot, num_state);
+  if (rc) return rc;
+  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>);
+  const int main_blocks = (num_tokens + rows_per_block - 1) / rows_per_block;
+  // each sequence's last max(ring, 256) rows, in whole tail workgroups
+  const int tail_rows =
+      (hca_tail_span(ring_pages != nullptr, ring) + kTailBlockRows - 1) / kTailBlockRows * kTailBlockRows;
+  const bool tail = ring_pages != nullptr || state != nullptr;
+  const int64_t blocks = main_blocks + (tail ? static_cast<int64_t>(num_seqs) * (tail_rows / kTailBlockRows) : 0);
+  EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
+  dim3 grid(static_cast<uint32_t>(blocks));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dim == 512) hipLaunchKernelGGL(kv_append_quant_kernel<512>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(kv_append_quant_kernel<576>, grid, dim3(256), 0, s, a);
+  if (dim == 512) hipLaunchKernelGGL(hca_append_kernel<512>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
+  else hipLaunchKernelGGL(hca_append_kernel<576>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
   return ekv_launch_status();
 }
 
@@ -501,8 +408,8 @@ extern "C" int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint
   a.positions = positions;
   a.window = window;
   a.lengths = lengths;
-  a.k_blocks = (num_tokens + 15) / 16;
-  a.latent_blocks = (num_tokens + 3) / 4;
+  a.k_blocks = (num_tokens + append_block_rows(128, 1) - 1) / append_block_rows(128, 1);
+  a.latent_blocks = (num_tokens + append_block_rows(dim, 1) - 1) / append_block_rows(dim, 1);
   a.q_blocks = static_cast<int32_t>((static_cast<int64_t>(num_tokens) * heads + 15) / 16);
   const int len_blocks = (num_tokens + 255) / 256;
   const dim3 grid(a.k_blocks + a.latent_blocks + a.q_blocks + len_blocks);

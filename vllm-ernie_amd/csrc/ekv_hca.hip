@@ -4,41 +4,50 @@
 // kv_score (the compressor projection [kv | score], bf16) come from this
 // call's input for positions >= the sequence's first new position, and from
 // the per-sequence state ring (positions % 256) for earlier positions.  Per
-// channel c the workgroup forms
+// channel c the workgroup forms the softmax over the span of
+// g_i = score_i[c] + ape[i, c] weighting kv_i[c], in one pass: an online
+// softmax per row group (group r holds rows r, r+4, ..., r+124), in chunks of
+// 4 of the group's rows,
 //
-//   g_i = score_i[c] + ape[i, c];  m = max_i g_i;  e_i = exp_ekv(g_i - m)
-//   Z = sum_i e_i;  N = sum_i e_i * kv_i[c]   (sequential over i, fp32)
-//   x_c = N / Z
+//   mc = max(m, g over the chunk)
+//   if mc > m + 8:  s = exp_ekv(m - mc);  Z *= s;  N *= s;  m = mc
+//   per row in order:  e = exp_ekv(g_i - m);  Z += e;  N = fma(e, kv_i[c], N)
 //
-// then RMSNorm over the row (sum of squares: per thread over its 4 channels,
-// then thread 0 over the threads in order), interleaved RoPE on the last 64
+// then the groups merged in order, M = max_r m_r, Z = fma(Z_r, s_r, Z),
+// N = fma(N_r, s_r, N) with s_r = exp_ekv(m_r - M), and x_c = N / Z.
+// Then RMSNorm over the row (sum of squares: per lane over its 4 channels,
+// then thread 0 over the lanes in order), interleaved RoPE on the last 64
 // channels at position 128*j (cos/sin table row j), and the per-token UE8M0
 // fp8 quant; the row is written to the compressed page slot of span j.
 //
 // Must run before ekv_hca_append of the same call (the append overwrites the
 // state ring rows this kernel may still read).  Built with -ffp-contract=off
-// and correctly rounded fp32 division / square root: the CPU oracle evaluates
-// the same operations in the same order.
+// (the only fused multiply-adds are the explicit ones) and correctly rounded
+// fp32 division / square root: the CPU oracle evaluates the same operations
+// in the same order.
 #include "ekv_common.h"
 #include "ekv_internal.h"
+#include "ekv_rows.h"
 
 namespace ekv {
 
-// exp(x) for x <= 0 as 2**n * P(f): n = rint(x * log2 e), f = x * log2 e - n,
-// P = degree-6 Taylor polynomial of 2**f (coefficients ln2^k / k!), Horner.
+// exp(x) for x <= 88 as 2**n * P(f): n = rint(x * log2 e), f = x * log2 e - n,
+// P a degree-5 polynomial fit of 2**f on [-1/2, 1/2] (Remez exchange on the
+// relative error, fp32 coefficients, P(0) = 1), Horner with fused
+// multiply-adds; 0 when x * log2 e < -125.  Branch-free: the polynomial is
+// evaluated for every x and the flush is a select.
 __device__ __forceinline__ float exp_ekv(float x) {
   const float t = x * 0x1.715476p+0f;
-  if (t < -125.0f) return 0.0f;
   const float n = rintf(t);
   const float f = t - n;
-  float p = 0x1.430912p-13f;
-  p = p * f + 0x1.5d87fep-10f;
-  p = p * f + 0x1.3b2ab6p-7f;
-  p = p * f + 0x1.c6b08ep-5f;
-  p = p * f + 0x1.ebfbe0p-3f;
-  p = p * f + 0x1.62e430p-1f;
-  p = p * f + 0x1.0p+0f;
-  return ldexpf(p, static_cast<int>(n));
+  float p = 0x1.5c08e6p-10f;
+  p = __builtin_fmaf(p, f, 0x1.3d0c52p-7f);
+  p = __builtin_fmaf(p, f, 0x1.c6b6e4p-5f);
+  p = __builtin_fmaf(p, f, 0x1.ebf918p-3f);
+  p = __builtin_fmaf(p, f, 0x1.62e428p-1f);
+  p = __builtin_fmaf(p, f, 0x1.0p+0f);
+  const float r = ldexpf(p, static_cast<int>(n));
+  return t < -125.0f ? 0.0f : r;
 }
 
 struct CompressArgs {
@@ -61,105 +70,242 @@ struct CompressArgs {
   int64_t num_pages;
 };
 
-template <int D>
-__global__ void __launch_bounds__(256) hca_compress_kernel(CompressArgs a) {
-  constexpr int kThreads = D / 4;  // threads owning 4 channels each
-  __shared__ float s_part[kThreads];
-  __shared__ float s_bcast[2];
-  const int tid = threadIdx.x;
-  const int b = blockIdx.y;
-  const int t0 = a.qsl[b];
-  const int n = a.qsl[b + 1] - t0;
-  if (n <= 0) return;
-  const int64_t p0 = a.positions[t0];
-  const int64_t pl = p0 + n - 1;
-  const int64_t j = p0 / kSpan + blockIdx.x;
-  if (j * kSpan + kSpan - 1 > pl) return;  // span not completed by this call
-  if (j >= a.max_spans) return;
-  const int st = a.state_slot != nullptr ? a.state_slot[b] : -1;
-  const bool active = tid < kThreads;
-  const int c0 = 4 * tid;
+// Third descriptor word of a raw (unswizzled, unformatted) buffer resource.
+constexpr int kBufferWord3 = 0x00020000;
 
-  auto row_ptr = [&](int i) -> const uint16_t* {
-    const int64_t p = j * kSpan + i;
-    if (p >= p0) return a.kv_score + (t0 + (p - p0)) * a.kvs_stride;
-    if (st < 0 || st >= a.num_state) return nullptr;
-    return a.state + (static_cast<int64_t>(st) * kStateRing + p % kStateRing) * (2 * D);
-  };
+constexpr int kRowGroups = 4;  // interleaved row groups: group r holds rows r, r+4, ...
+constexpr int kChunk = 4;      // rows of a group per online-softmax step
+constexpr int kGroupRows = kSpan / kRowGroups;
 
-  float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  if (active) {
-    for (int i = 0; i < kSpan; ++i) {
-      const uint16_t* r = row_ptr(i);
-      const uint2 sv = r ? *reinterpret_cast<const uint2*>(r + D + c0) : make_uint2(0, 0);
-      const float4 ap = *reinterpret_cast<const float4*>(a.ape + i * D + c0);
-      const float g0 = __uint_as_float(sv.x << 16) + ap.x;
-      const float g1 = __uint_as_float(sv.x & 0xffff0000u) + ap.y;
-      const float g2 = __uint_as_float(sv.y << 16) + ap.z;
-      const float g3 = __uint_as_float(sv.y & 0xffff0000u) + ap.w;
-      m[0] = fmaxf(m[0], g0); m[1] = fmaxf(m[1], g1); m[2] = fmaxf(m[2], g2); m[3] = fmaxf(m[3], g3);
-    }
-  }
-  float Z[4] = {0.f, 0.f, 0.f, 0.f}, N[4] = {0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    for (int i = 0; i < kSpan; ++i) {
-      const uint16_t* r = row_ptr(i);
-      const uint2 sv = r ? *reinterpret_cast<const uint2*>(r + D + c0) : make_uint2(0, 0);
-      const uint2 kv = r ? *reinterpret_cast<const uint2*>(r + c0) : make_uint2(0, 0);
-      const float4 ap = *reinterpret_cast<const float4*>(a.ape + i * D + c0);
-      const float g[4] = {__uint_as_float(sv.x << 16) + ap.x, __uint_as_float(sv.x & 0xffff0000u) + ap.y,
-                          __uint_as_float(sv.y << 16) + ap.z, __uint_as_float(sv.y & 0xffff0000u) + ap.w};
-      const float v[4] = {__uint_as_float(kv.x << 16), __uint_as_float(kv.x & 0xffff0000u),
-                          __uint_as_float(kv.y << 16), __uint_as_float(kv.y & 0xffff0000u)};
+// Online-softmax state of one lane: 4 channels of one row group.
+struct SoftmaxState {
+  float m[4], Z[4], N[4];
+};
+
+__device__ __forceinline__ void bf16x4(uint2 v, float (&f)[4]) {
+  f[0] = __uint_as_float(v.x << 16);
+  f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16);
+  f[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
+constexpr float kShiftSlack = 8.0f;  // a chunk max above shift + slack moves the shift
+
+// One chunk of kChunk rows (in group order): the shift m moves to the running
+// max (and the sums are rescaled) only when the chunk's max exceeds it by
+// more than kShiftSlack -- a wave-uniform branch, rarely taken after the
+// first chunk, which sets m without rescaling (its sums are still 0) -- then
+// the rows' terms in order.
+template <bool kFirst>
+__device__ __forceinline__ void softmax_chunk(SoftmaxState& s, const uint2 (&sc)[kChunk], const uint2 (&kv)[kChunk],
+                                              const float4 (&ap)[kChunk]) {
+  float g[kChunk][4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float e = exp_ekv(g[k] - m[k]);
-        Z[k] = Z[k] + e;
-        N[k] = N[k] + e * v[k];
-      }
+  for (int u = 0; u < kChunk; ++u) {
+    float f[4];
+    bf16x4(sc[u], f);
+    g[u][0] = f[0] + ap[u].x;
+    g[u][1] = f[1] + ap[u].y;
+    g[u][2] = f[2] + ap[u].z;
+    g[u][3] = f[3] + ap[u].w;
+  }
+  float mc[4];
+  bool move = false;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mc[k] = s.m[k];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) mc[k] = fmaxf(mc[k], g[u][k]);
+    if (kFirst) s.m[k] = mc[k];
+    else move |= mc[k] > s.m[k] + kShiftSlack;
+  }
+  if (!kFirst && __builtin_amdgcn_ballot_w64(move) != 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool mv = mc[k] > s.m[k] + kShiftSlack;
+      const float r = exp_ekv(s.m[k] - mc[k]);
+      s.Z[k] = mv ? s.Z[k] * r : s.Z[k];
+      s.N[k] = mv ? s.N[k] * r : s.N[k];
+      s.m[k] = mv ? mc[k] : s.m[k];
     }
   }
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) {
+    float v[4];
+    bf16x4(kv[u], v);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float e = exp_ekv(g[u][k] - s.m[k]);
+      s.Z[k] = s.Z[k] + e;
+      s.N[k] = __builtin_fmaf(e, v[k], s.N[k]);
+    }
+  }
+}
+
+// Workgroup-shared scratch of compress_span.
+template <int D>
+struct CompressLds {
+  __align__(16) float part[D / 4];
+  float wmax[D / 64];
+  float rn;
+};
+
+// Compress span j of sequence b (first row t0 at position p0, state slot st)
+// with one workgroup of D threads.  Wave w owns channels 64w .. 64w+63;
+// lane l of it owns the 4 channels 64w + 4 (l % 16) + 0..3 of row group
+// l / 16.  Every kv_score element is read from memory once: the softmax is
+// an online one per (row group, channel), merged over the groups in order.
+// Every thread of the workgroup must call it (it synchronizes).
+template <int D>
+__device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds<D>& ls, int b, int t0, int64_t p0,
+                                              int64_t j, int st) {
+  constexpr int kWaves = D / 64;
+  constexpr int kQuads = D / 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int grp = lane >> 4;                            // row group r
+  const int quad = (tid >> 6) * 16 + (lane & 15);       // channel quad
+  const int c0 = 4 * quad;
+
+  SoftmaxState sm;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    sm.m[k] = -INFINITY;
+    sm.Z[k] = 0.0f;
+    sm.N[k] = 0.0f;
+  }
+  // Row i of the span: this call's input for positions >= p0, else the
+  // state ring (positions % 256), whose rows of span j are consecutive from
+  // (j % 2) * 128; without a ring those rows count as score 0, kv 0.
+  const int64_t split64 = p0 - j * kSpan;
+  const __amdgpu_buffer_rsrc_t ape_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ape), 0, kSpan * 4 * D, kBufferWord3);
+  const uint32_t ape_off = static_cast<uint32_t>(grp * 4 * D + 4 * c0);
+  auto load_ape = [&](int i0) -> float4 {  // row i0 + grp
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(ape_rsrc, ape_off, i0 * (4 * D), 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+  };
+  if (split64 <= 0) {
+    // Every row from the input, row i at t0 - split64 + i, loaded through a
+    // buffer resource: uniform base, the lane's constant byte offset (its
+    // row group's row, its channels), a uniform row offset.  Chunk c + 1's
+    // loads are issued before chunk c is consumed; the scheduling barriers
+    // keep them at the start of the step (not sunk into its arithmetic) and
+    // keep the compiler from hoisting more.
+    const uint32_t in_row = static_cast<uint32_t>(a.kvs_stride) * 2u;
+    const __amdgpu_buffer_rsrc_t in_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.kv_score + (t0 - split64) * a.kvs_stride), 0, kSpan * in_row, kBufferWord3);
+    const uint32_t kv_off = static_cast<uint32_t>(grp) * in_row + 2u * c0;
+    const uint32_t sc_off = kv_off + 2u * D;
+    auto load2 = [&](uint32_t off, int i0) -> uint2 {  // row i0 + grp
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(in_rsrc, off, i0 * in_row, 0);
+      return make_uint2(v[0], v[1]);
+    };
+    constexpr int kSteps = kGroupRows / kChunk;  // chunks per row group
+    uint2 sc[2][kChunk], kv[2][kChunk];
+    float4 ap[2][kChunk];
+    auto issue = [&](int step, uint2 (&s_)[kChunk], uint2 (&k_)[kChunk], float4 (&a_)[kChunk]) {
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int i0 = kRowGroups * (step * kChunk + u);
+        s_[u] = load2(sc_off, i0);
+        k_[u] = load2(kv_off, i0);
+        a_[u] = load_ape(i0);
+      }
+    };
+    issue(0, sc[0], kv[0], ap[0]);
+#pragma unroll
+    for (int step = 0; step < kSteps; ++step) {
+      const int cur = step & 1;
+      if (step + 1 < kSteps) issue(step + 1, sc[cur ^ 1], kv[cur ^ 1], ap[cur ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (step == 0) softmax_chunk<true>(sm, sc[cur], kv[cur], ap[cur]);
+      else softmax_chunk<false>(sm, sc[cur], kv[cur], ap[cur]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // The span's first rows precede this call: rows i < split64 come from
+    // the state ring.  Same arithmetic, plain per-row addressing.
+    const int split = static_cast<int>(split64);
+    const bool has_state = st >= 0 && st < a.num_state;
+    auto load_row = [&](int i, int col) -> uint2 {
+      const uint16_t* r;
+      if (i >= split) r = a.kv_score + (t0 + (i - split)) * a.kvs_stride;
+      else if (has_state) r = a.state + (static_cast<int64_t>(st) * kStateRing + (j & 1) * kSpan + i) * (2 * D);
+      else return make_uint2(0, 0);
+      return *reinterpret_cast<const uint2*>(r + col + c0);
+    };
+    for (int step = 0; step < kGroupRows / kChunk; ++step) {
+      uint2 sc[kChunk], kv[kChunk];
+      float4 ap[kChunk];
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int i0 = kRowGroups * (step * kChunk + u);
+        sc[u] = load_row(i0 + grp, D);
+        kv[u] = load_row(i0 + grp, 0);
+        ap[u] = load_ape(i0);
+      }
+      if (step == 0) softmax_chunk<true>(sm, sc, kv, ap);
+      else softmax_chunk<false>(sm, sc, kv, ap);
+    }
+  }
+
+  // Merge the 4 row groups in order (lanes l, l+16, l+32, l+48 of a wave).
   float x[4];
   float part = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    x[k] = active ? __fdiv_rn(N[k], Z[k]) : 0.0f;
+    float m_g[kRowGroups];
+#pragma unroll
+    for (int r = 0; r < kRowGroups; ++r) m_g[r] = __shfl(sm.m[k], (lane & 15) + 16 * r);
+    float M = m_g[0];
+#pragma unroll
+    for (int r = 1; r < kRowGroups; ++r) M = fmaxf(M, m_g[r]);
+    float Z = 0.0f, N = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kRowGroups; ++r) {
+      const float s = exp_ekv(m_g[r] - M);
+      Z = __builtin_fmaf(__shfl(sm.Z[k], (lane & 15) + 16 * r), s, Z);
+      N = __builtin_fmaf(__shfl(sm.N[k], (lane & 15) + 16 * r), s, N);
+    }
+    x[k] = __fdiv_rn(N, Z);
     part = part + x[k] * x[k];
   }
-  if (active) s_part[tid] = part;
+  // From here on the lanes of row group 0 carry the row: quad q's channels.
+  const bool owner = grp == 0;
+  if (owner) ls.part[quad] = part;
   __syncthreads();
   if (tid == 0) {
     float S = 0.0f;
-    for (int i = 0; i < kThreads; ++i) S = S + s_part[i];
-    const float ms = __fdiv_rn(S, static_cast<float>(D));
-    s_bcast[0] = __fdiv_rn(1.0f, __fsqrt_rn(ms + a.eps));
-  }
-  __syncthreads();
-  const float rn = s_bcast[0];
-  float y[4] = {0.f, 0.f, 0.f, 0.f};
-  float amax = 0.0f;
-  if (active) {
-    const float4 w = *reinterpret_cast<const float4*>(a.norm_w + c0);
-    y[0] = (x[0] * rn) * w.x; y[1] = (x[1] * rn) * w.y; y[2] = (x[2] * rn) * w.z; y[3] = (x[3] * rn) * w.w;
-    if (c0 >= D - 64) {
-      const float* cs = a.cos_sin + j * 64;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int pi = (c0 - (D - 64)) / 2 + q;
-        const float c = cs[pi], s = cs[32 + pi];
-        const float x0 = y[2 * q], x1 = y[2 * q + 1];
-        y[2 * q] = x0 * c - x1 * s;
-        y[2 * q + 1] = x0 * s + x1 * c;
-      }
+    for (int q = 0; q < kQuads; q += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&ls.part[q]);
+      S = S + v.x; S = S + v.y; S = S + v.z; S = S + v.w;
     }
-    amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+    const float ms = __fdiv_rn(S, static_cast<float>(D));
+    ls.rn = __fdiv_rn(1.0f, __fsqrt_rn(ms + a.eps));
   }
-  // block max of amax (order-free): wave reduce, then 4 wave partials
-  amax = wave_max_xor(amax, 64);
-  __shared__ float s_wmax[4];
-  if ((tid & 63) == 0) s_wmax[tid >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3]));
+  const float rn = ls.rn;
+  const float4 w = *reinterpret_cast<const float4*>(a.norm_w + c0);
+  float y[4] = {(x[0] * rn) * w.x, (x[1] * rn) * w.y, (x[2] * rn) * w.z, (x[3] * rn) * w.w};
+  if (c0 >= D - 64) {
+    const float* cs = a.cos_sin + j * 64;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pi = (c0 - (D - 64)) / 2 + q;
+      const float cz = cs[pi], sz = cs[32 + pi];
+      const float x0 = y[2 * q], x1 = y[2 * q + 1];
+      y[2 * q] = x0 * cz - x1 * sz;
+      y[2 * q + 1] = x0 * sz + x1 * cz;
+    }
+  }
+  float amax = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+  amax = wave_max_xor(amax, 64);  // the row-group copies are equal
+  if (lane == 0) ls.wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = ls.wmax[0];
+#pragma unroll
+  for (int wv = 1; wv < kWaves; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
   const int64_t slot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
@@ -167,7 +313,7 @@ __global__ void __launch_bounds__(256) hca_compress_kernel(CompressArgs a) {
   if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
   const int64_t off = slot % kPageTokens;
-  if (active) {
+  if (owner) {
     const uint32_t lo = f32x2_to_fp8(y[0] * inv, y[1] * inv);
     const uint32_t hi = f32x2_to_fp8(y[2] * inv, y[3] * inv);
     *reinterpret_cast<uint32_t*>(page + off * D + c0) = lo | (hi << 16);
@@ -175,9 +321,156 @@ __global__ void __launch_bounds__(256) hca_compress_kernel(CompressArgs a) {
   if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
+// The span of sequence b that completes in this call and starts before it
+// (its first rows in the state ring), or -1.
+__device__ __forceinline__ int64_t straddling_span(int64_t p0, int n) {
+  const int64_t j = p0 / kSpan;
+  return (p0 % kSpan != 0 && j * kSpan + kSpan - 1 <= p0 + n - 1) ? j : -1;
+}
+
+// One workgroup per (span slot, sequence): span p0 / 128 + blockIdx.x of
+// sequence blockIdx.y, when this call completes it.
+template <int D>
+__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca_compress_kernel(CompressArgs a) {
+  __shared__ CompressLds<D> ls;
+  const int b = blockIdx.y;
+  const int t0 = a.qsl[b];
+  const int n = a.qsl[b + 1] - t0;
+  if (n <= 0) return;
+  const int64_t p0 = a.positions[t0];
+  const int64_t j = p0 / kSpan + blockIdx.x;
+  if (j * kSpan + kSpan - 1 > p0 + n - 1) return;  // span not completed by this call
+  if (j >= a.max_spans) return;
+  compress_span<D>(a, ls, b, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
+}
+
+// The whole HCA write of one call in one launch (compress, then append, as
+// ekv_hca_compress followed by ekv_hca_append).  Workgroups, D threads each:
+//  * [0, B): sequence b's straddling span j0 (its rows before the call come
+//    from the state ring), then the state-ring rows this call writes over
+//    the slots it read, inside one workgroup;
+//  * next B * tail_blocks: the window-ring rows and the other state-ring rows
+//    of each sequence's last rows, kTailRows per workgroup;
+//  * the rest, interleaved in proportion (workgroups are dispatched in order,
+//    so each CU gets both kinds): B * spans workgroups compressing the other
+//    completed spans (read from this call's input only), and the append
+//    workgroups storing every row at its slot.
+// No group writes what another reads, so they all run concurrently.
+constexpr int kTailSteps = 4;  // tail rows per wave of a tail workgroup
+
+struct HcaWriteArgs {
+  CompressArgs c;
+  AppendArgs ap;
+  int32_t num_seqs, spans, tail_span, tail_blocks;
+  int32_t mixed;  // compress + append workgroups, interleaved
+};
+
+// State-ring slots read by sequence b's straddling span j0: positions
+// 128*j0 .. p0-1, i.e. slots [lo, lo + n) with lo = 128 * (j0 % 2) and
+// n = p0 - 128*j0 < 128 (n = 0 without such a span).
+struct AliasSlots {
+  int lo, n;
+};
+
+__device__ __forceinline__ AliasSlots aliased_state_slots(int64_t p0, int n) {
+  const int64_t j = straddling_span(p0, n);
+  if (j < 0) return {0, 0};
+  return {static_cast<int>(j & 1) * kSpan, static_cast<int>(p0 - j * kSpan)};
+}
+
+template <int D>
+__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca_write_kernel(HcaWriteArgs w) {
+  __shared__ CompressLds<D> ls;
+  constexpr int kWaves = D / 64;
+  int block = static_cast<int>(blockIdx.x);
+  if (block < w.num_seqs) {
+    const int b = block;
+    const int t0 = w.c.qsl[b];
+    const int n = w.c.qsl[b + 1] - t0;
+    if (n <= 0) return;
+    const int64_t p0 = w.c.positions[t0];
+    const int64_t j = straddling_span(p0, n);
+    if (j < 0) return;
+    if (j < w.c.max_spans)
+      compress_span<D>(w.c, ls, b, t0, p0, j, w.c.state_slot != nullptr ? w.c.state_slot[b] : -1);
+    __syncthreads();
+    // the state rows written over the slots it read: row k from the end
+    // (position last - k) hits slot lo + s for s < n when k = d - s mod 256,
+    // d = (last - lo) mod 256, a range of k that may wrap below 0
+    const AliasSlots al = aliased_state_slots(p0, n);
+    const int d = static_cast<int>((p0 + n - 1 - al.lo) % kStateRing);
+    const int k0 = d - al.n + 1;
+    if (k0 >= 0) {
+      hca_tail_range<D, kWaves, 1>(w.ap, b, k0, d + 1, false, al.lo, al.n, true);
+    } else {
+      hca_tail_range<D, kWaves, 1>(w.ap, b, 0, d + 1, false, al.lo, al.n, true);
+      hca_tail_range<D, kWaves, 1>(w.ap, b, k0 + kStateRing, kStateRing, false, al.lo, al.n, true);
+    }
+    return;
+  }
+  block -= w.num_seqs;
+  if (block < w.num_seqs * w.tail_blocks) {
+    const int b = block / w.tail_blocks;
+    const int t0 = w.c.qsl[b];
+    const int n = w.c.qsl[b + 1] - t0;
+    if (n <= 0) return;
+    const AliasSlots al = aliased_state_slots(w.c.positions[t0], n);
+    constexpr int kTailRows = kWaves * kTailSteps;
+    const int k_lo = (block % w.tail_blocks) * kTailRows;
+    hca_tail_range<D, kWaves, 1>(w.ap, b, k_lo, min(k_lo + kTailRows, w.tail_span), true, al.lo, al.n, false);
+    return;
+  }
+  block -= w.num_seqs * w.tail_blocks;
+  // block i of the mixed range is a compress block when the count of compress
+  // blocks before it, floor(i * NC / N), steps up at i + 1
+  const int64_t nc = static_cast<int64_t>(w.num_seqs) * w.spans;
+  const int64_t before = static_cast<int64_t>(block) * nc / w.mixed;
+  const int64_t upto = static_cast<int64_t>(block + 1) * nc / w.mixed;
+  if (upto > before) {
+    const int cb = static_cast<int>(before);
+    const int b = cb / w.spans;
+    const int t0 = w.c.qsl[b];
+    const int n = w.c.qsl[b + 1] - t0;
+    if (n <= 0) return;
+    const int64_t p0 = w.c.positions[t0];
+    const int64_t j = p0 / kSpan + cb % w.spans;
+    if (j * kSpan < p0) return;                       // the straddling span
+    if (j * kSpan + kSpan - 1 > p0 + n - 1) return;   // not completed by this call
+    if (j >= w.c.max_spans) return;
+    compress_span<D>(w.c, ls, b, t0, p0, j, -1);
+    return;
+  }
+  block -= static_cast<int>(before);
+  append_rows<D, kAppendSeq<D>, kWaves>(w.ap, block);
+}
+
 }  // namespace ekv
 
 using namespace ekv;
+
+namespace {
+
+// Argument checks and CompressArgs of an HCA compress; 0 or an error status.
+int hca_compress_args(CompressArgs& a, const uint16_t* kv_score, int64_t kvs_stride, const int64_t* positions,
+                      const int32_t* qsl, int32_t dim, const uint16_t* state, const int32_t* state_slot,
+                      int32_t num_state, const float* ape, const float* norm_w, float eps, const float* cos_sin,
+                      int32_t max_spans, const int32_t* comp_block_table, int32_t comp_bt_stride, uint8_t* pool,
+                      int64_t page_stride, int64_t num_pages) {
+  EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
+  EKV_CHECK(kv_score && positions && qsl && ape && norm_w && cos_sin && comp_block_table && pool,
+            "null pointer");
+  EKV_CHECK(kvs_stride >= 2 * dim && kvs_stride % 4 == 0 && kvs_stride <= (int64_t{1} << 22),
+            "kv_score stride must be in [2*dim, 2^22], a multiple of 4");
+  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(aligned16(ape) && aligned16(norm_w) && aligned8(kv_score) && aligned16(pool) &&
+                (state == nullptr || aligned8(state)),
+            "misaligned buffers");
+  a = CompressArgs{kv_score, kvs_stride, positions, qsl, state, state_slot, num_state, ape, norm_w, eps,
+                   cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride, num_pages};
+  return 0;
+}
+
+}  // namespace
 
 extern "C" int ekv_hca_compress(const uint16_t* kv_score, int64_t kvs_stride, const int64_t* positions,
                                 const int32_t* qsl, int32_t num_seqs, int32_t max_query_len, int32_t dim,
@@ -187,21 +480,55 @@ extern "C" int ekv_hca_compress(const uint16_t* kv_score, int64_t kvs_stride, co
                                 uint8_t* pool, int64_t page_stride, int64_t num_pages, void* stream) {
   EKV_CHECK(num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
   if (num_seqs == 0 || max_query_len == 0) return 0;
-  EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
-  EKV_CHECK(kv_score && positions && qsl && ape && norm_w && cos_sin && comp_block_table && pool,
-            "null pointer");
-  EKV_CHECK(kvs_stride >= 2 * dim && kvs_stride % 4 == 0, "kv_score stride must be >= 2*dim, multiple of 4");
-  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
-  EKV_CHECK(aligned16(ape) && aligned16(norm_w) && aligned8(kv_score) && aligned16(pool) &&
-                (state == nullptr || aligned8(state)),
-            "misaligned buffers");
-  CompressArgs a{kv_score, kvs_stride, positions, qsl, state, state_slot, num_state, ape, norm_w, eps,
-                 cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride, num_pages};
+  CompressArgs a;
+  const int rc = hca_compress_args(a, kv_score, kvs_stride, positions, qsl, dim, state, state_slot, num_state, ape,
+                                   norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool,
+                                   page_stride, num_pages);
+  if (rc) return rc;
   // spans that can complete among max_query_len new positions
   const int spans = max_query_len / kSpan + 1;
   dim3 grid(spans, num_seqs);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(256), 0, s, a);
+  if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(512), 0, s, a);
+  else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                             int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                             const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                             int32_t num_seqs, int32_t max_query_len, uint16_t* state,
+                             const int32_t* state_slot, int32_t num_state, const float* ape,
+                             const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                             const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                             int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride,
+                             int64_t num_pages, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
+  if (num_tokens == 0 || num_seqs == 0) return 0;
+  HcaWriteArgs w{};
+  int rc = hca_compress_args(w.c, kv_score, kvs_stride, positions, qsl, dim, state, state_slot, num_state, ape,
+                             norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride,
+                             num_pages);
+  if (rc) return rc;
+  rc = hca_append_args(w.ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+                       token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages, ring_stride, ring, state,
+                       state_slot, num_state);
+  if (rc) return rc;
+  w.num_seqs = num_seqs;
+  w.spans = max_query_len / kSpan + 1;
+  w.tail_span = hca_tail_span(ring_pages != nullptr, ring);
+  const int waves = dim / 64;
+  const int tail_rows = waves * kTailSteps;
+  w.tail_blocks = (ring_pages != nullptr || state != nullptr) ? (w.tail_span + tail_rows - 1) / tail_rows : 0;
+  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>, waves);
+  const int64_t main_blocks = (static_cast<int64_t>(num_tokens) + rows_per_block - 1) / rows_per_block;
+  const int64_t mixed = static_cast<int64_t>(num_seqs) * w.spans + main_blocks;
+  const int64_t blocks = static_cast<int64_t>(num_seqs) * (1 + w.tail_blocks) + mixed;
+  EKV_CHECK(blocks < (int64_t{1} << 31) && mixed * num_seqs * w.spans < (int64_t{1} << 62), "too many rows");
+  w.mixed = static_cast<int32_t>(mixed);
+  dim3 grid(static_cast<uint32_t>(blocks));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dim == 512) hipLaunchKernelGGL(hca_write_kernel<512>, grid, dim3(512), 0, s, w);
+  else hipLaunchKernelGGL(hca_write_kernel<576>, grid, dim3(576), 0, s, w);
   return ekv_launch_status();
 }

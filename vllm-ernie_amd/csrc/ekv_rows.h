@@ -1,0 +1,246 @@
+// Device-side row append shared by the write kernels: a bf16 row ->
+// per-token UE8M0 scale + e4m3 codes stored in a values-then-scales page
+// pool, the per-call row append, and the HCA tail (window ring and
+// compressor state ring rows of each sequence).
+#pragma once
+
+#include "ekv_common.h"
+#include "ekv_internal.h"
+
+namespace ekv {
+
+// ---------------------------------------------------------------------------
+// kv_append_quant
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  const uint16_t* rows;      // [T, row_stride] bf16
+  int64_t row_stride;        // elements
+  int32_t num_tokens;
+  const int64_t* slot_mapping;  // [T], < 0 -> skip
+  uint8_t* cache;            // [num_pages, page_stride]
+  int64_t page_stride;
+  int64_t num_pages;
+  // HCA extras (all optional)
+  const int64_t* positions;  // [T]
+  const int32_t* token_seq;  // [T], < 0 -> padding
+  const int32_t* qsl;        // [B + 1]
+  const int32_t* ring_pages; // [B, ring_stride]
+  int32_t ring_stride;
+  int32_t ring;              // ring length R (multiple of 64)
+  const uint16_t* kv_score;  // [T, kvs_stride] bf16, 2*D wide
+  int64_t kvs_stride;
+  uint16_t* state;           // [num_state, 256, 2*D] bf16
+  const int32_t* state_slot; // [B]
+  int32_t num_state;
+};
+
+// One row's fp8 image: lane `ln` of the row's kLanes lanes holds the 8-byte
+// pieces ln, ln + kLanes, ... of the D fp8 codes, plus the row's scale.
+template <int D, int kLanes>
+struct Fp8Row {
+  static constexpr int kChunks = D / 8;  // 16-byte bf16 chunks per row
+  static constexpr int kPerLane = (kChunks + kLanes - 1) / kLanes;
+  uint2 packed[kPerLane];
+  float scale;
+};
+
+template <int D, int kLanes>
+__device__ __forceinline__ void load_bf16_row(const uint16_t* src, int ln,
+                                              uint4 (&raw)[Fp8Row<D, kLanes>::kPerLane]) {
+  using R = Fp8Row<D, kLanes>;
+#pragma unroll
+  for (int k = 0; k < R::kPerLane; ++k) {
+    const int c = ln + k * kLanes;
+    raw[k] = c < R::kChunks ? *reinterpret_cast<const uint4*>(src + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Per-token UE8M0 scale and e4m3 codes of one bf16 row (kLanes lanes).
+template <int D, int kLanes>
+__device__ __forceinline__ Fp8Row<D, kLanes> quantize_row(const uint4 (&raw)[Fp8Row<D, kLanes>::kPerLane]) {
+  using R = Fp8Row<D, kLanes>;
+  float v[R::kPerLane][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < R::kPerLane; ++k) {
+    const uint32_t ww[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[k][2 * i] = __uint_as_float(ww[i] << 16);
+      v[k][2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+      amax = fmaxf(amax, fmaxf(fabsf(v[k][2 * i]), fabsf(v[k][2 * i + 1])));
+    }
+  }
+  amax = wave_max_xor(amax, kLanes);
+  const int e = ue8m0_exponent(amax);
+  const float inv = exp2i(-e);
+  R out;
+  out.scale = exp2i(e);
+#pragma unroll
+  for (int k = 0; k < R::kPerLane; ++k) {
+    const uint32_t b0 = f32x2_to_fp8(v[k][0] * inv, v[k][1] * inv);
+    const uint32_t b1 = f32x2_to_fp8(v[k][2] * inv, v[k][3] * inv);
+    const uint32_t b2 = f32x2_to_fp8(v[k][4] * inv, v[k][5] * inv);
+    const uint32_t b3 = f32x2_to_fp8(v[k][6] * inv, v[k][7] * inv);
+    out.packed[k] = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+  }
+  return out;
+}
+
+// Store a quantized row at `slot` of a values-then-scales page pool; slots
+// outside the pool (negative = skip) are not written.
+template <int D, int kLanes>
+__device__ __forceinline__ void store_fp8_row(const AppendArgs& a, int64_t slot, int ln,
+                                              const Fp8Row<D, kLanes>& row) {
+  using R = Fp8Row<D, kLanes>;
+  if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
+  uint8_t* page = a.cache + (slot / kPageTokens) * a.page_stride;
+  const int64_t off = slot % kPageTokens;
+#pragma unroll
+  for (int k = 0; k < R::kPerLane; ++k) {
+    const int c = ln + k * kLanes;
+    if (c < R::kChunks) *reinterpret_cast<uint2*>(page + off * D + 8 * c) = row.packed[k];
+  }
+  if (ln == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = row.scale;
+}
+
+// Rows of workgroup `block`, stored at their slot_mapping slots: kWaves
+// waves, each taking kSeq groups of kRowsPerWave rows (4 rows of 16 lanes for
+// D = 128, else one row of 64 lanes).  A wave issues the loads of all its
+// rows (and their slots) before it quantizes and stores any of them.
+template <int D, int kSeq, int kWaves = 4>
+__device__ __forceinline__ void append_rows(const AppendArgs& a, int block) {
+  constexpr int kRowsPerWave = (D == 128) ? 4 : 1;
+  constexpr int kLanes = 64 / kRowsPerWave;       // lanes per row
+  using R = Fp8Row<D, kLanes>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / kLanes;                  // row within the wave
+  const int ln = lane % kLanes;                   // lane within the row
+  const int64_t t_first = (static_cast<int64_t>(block) * kWaves + wave) * kSeq * kRowsPerWave + sub;
+
+  uint4 raw[kSeq][R::kPerLane];
+  int64_t slot[kSeq];
+#pragma unroll
+  for (int r = 0; r < kSeq; ++r) {
+    const int64_t t = t_first + r * kRowsPerWave;
+    const int64_t tt = t < a.num_tokens ? t : 0;
+    load_bf16_row<D, kLanes>(a.rows + tt * a.row_stride, ln, raw[r]);
+    slot[r] = a.slot_mapping[tt];
+  }
+#pragma unroll
+  for (int r = 0; r < kSeq; ++r) {
+    if (t_first + r * kRowsPerWave >= a.num_tokens) return;  // whole row group exits together
+    store_fp8_row<D, kLanes>(a, slot[r], ln, quantize_row<D, kLanes>(raw[r]));
+  }
+}
+
+// HCA extras of one call, for the last rows of each sequence: row k from the
+// end of sequence b (position last - k, positions of a sequence's rows in a
+// call being consecutive) goes to the window ring when k < ring, and its
+// kv_score row to the compressor state ring when k < 256.  This takes rows
+// k_lo <= k < k_hi of sequence b, kBatch per wave and step (the loads of a
+// step issued before its stores), over the workgroup's kWaves waves.  Of the
+// state rows it writes those whose ring slot p % 256 lies in
+// [alias_lo, alias_lo + alias_n) exactly when `in_alias`, and ring rows only
+// when `ring_rows`.
+template <int D, int kWaves, int kBatch>
+__device__ __forceinline__ void hca_tail_range(const AppendArgs& a, int b, int k_lo, int k_hi, bool ring_rows = true,
+                                               int alias_lo = 0, int alias_n = 0, bool in_alias = false) {
+  using R = Fp8Row<D, 64>;
+  constexpr int kStateChunks = 2 * R::kChunks;            // 16-byte chunks of a kv_score row
+  constexpr int kStatePerLane = (kStateChunks + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int t0 = a.qsl[b];
+  const int n = a.qsl[b + 1] - t0;
+  const int64_t last = a.positions[t0] + n - 1;
+  const int st = a.state != nullptr ? a.state_slot[b] : -1;
+  const bool state_ok = st >= 0 && st < a.num_state;
+  const bool ring_ok = ring_rows && a.ring_pages != nullptr;
+  if (k_hi > n) k_hi = n;
+  for (int kb = k_lo + wave * kBatch; kb < k_hi; kb += kWaves * kBatch) {
+    uint4 raw[kBatch][R::kPerLane];
+    uint4 sv[kBatch][kStatePerLane];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = kb + u < k_hi ? kb + u : kb;
+      const int64_t t = t0 + n - 1 - k;
+      if (ring_ok) load_bf16_row<D, 64>(a.rows + t * a.row_stride, lane, raw[u]);
+      if (state_ok && k < kStateRing) {
+        const uint4* sp = reinterpret_cast<const uint4*>(a.kv_score + t * a.kvs_stride);
+#pragma unroll
+        for (int i = 0; i < kStatePerLane; ++i) {
+          const int c = lane + 64 * i;
+          sv[u][i] = c < kStateChunks ? sp[c] : make_uint4(0, 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = kb + u;
+      if (k >= k_hi) break;
+      const int64_t p = last - k;
+      if (ring_ok && k < a.ring) {
+        const int64_t rp = p % a.ring;
+        const int64_t sl =
+            static_cast<int64_t>(a.ring_pages[static_cast<int64_t>(b) * a.ring_stride + rp / kPageTokens]) *
+                kPageTokens + rp % kPageTokens;
+        store_fp8_row<D, 64>(a, sl, lane, quantize_row<D, 64>(raw[u]));
+      }
+      const int64_t rel = p % kStateRing - alias_lo;
+      if (state_ok && k < kStateRing && (rel >= 0 && rel < alias_n) == in_alias) {
+        uint4* d =
+            reinterpret_cast<uint4*>(a.state + (static_cast<int64_t>(st) * kStateRing + p % kStateRing) * (2 * D));
+#pragma unroll
+        for (int i = 0; i < kStatePerLane; ++i) {
+          const int c = lane + 64 * i;
+          if (c < kStateChunks) d[c] = sv[u][i];
+        }
+      }
+    }
+  }
+}
+
+// Rows from the end of a sequence that hca_tail_range has to cover: the
+// window ring's and the state ring's, whichever is longer.
+inline int hca_tail_span(bool ring_ok, int ring) { return ring_ok && ring > kStateRing ? ring : kStateRing; }
+
+// Rows per workgroup of append_rows<D, kSeq, waves>.
+constexpr int append_block_rows(int d, int seq, int waves = 4) { return waves * seq * (d == 128 ? 4 : 1); }
+
+// Rows each wave keeps in flight in the standalone append launches.
+template <int D>
+constexpr int kAppendSeq = (D == 128) ? 1 : 4;
+
+
+// Argument checks and AppendArgs of an HCA append (the latent rows, the
+// window ring and the compressor state ring); 0 or an error status.
+inline int hca_append_args(AppendArgs& a, const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                           int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                           const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                           int32_t num_seqs, uint8_t* pool, int64_t page_stride, int64_t num_pages,
+                           const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* state,
+                           const int32_t* state_slot, int32_t num_state) {
+  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
+  EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
+  EKV_CHECK(latent && slot_mapping && positions && token_seq && qsl && pool, "null pointer");
+  EKV_CHECK(latent_stride >= dim && latent_stride % 8 == 0, "bad latent_stride");
+  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(ring_pages == nullptr || (ring >= kWindow && ring % kPageTokens == 0 && ring_stride >= ring / kPageTokens),
+            "ring must be a multiple of 64, >= 128, with ring_stride >= ring/64");
+  EKV_CHECK(state == nullptr || (kv_score && state_slot && kvs_stride >= 2 * dim && kvs_stride % 8 == 0),
+            "state needs kv_score (stride >= 2*dim, multiple of 8) and state_slot");
+  EKV_CHECK(aligned16(latent) && aligned16(pool) && (state == nullptr || (aligned16(state) && aligned16(kv_score))),
+            "buffers must be 16-byte aligned");
+  a = AppendArgs{};
+  a.rows = latent; a.row_stride = latent_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
+  a.cache = pool; a.page_stride = page_stride; a.num_pages = num_pages;
+  a.positions = positions; a.token_seq = token_seq; a.qsl = qsl;
+  a.ring_pages = ring_pages; a.ring_stride = ring_stride; a.ring = ring;
+  a.kv_score = kv_score; a.kvs_stride = kvs_stride; a.state = state; a.state_slot = state_slot;
+  a.num_state = num_state;
+  return 0;
+}
+
+}  // namespace ekv
