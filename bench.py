@@ -170,11 +170,11 @@ def build_hca_write(torch, ops, seed: int, B: int = 16, chunk: int = 8192, max_o
 
 
 def hca_write_step(ops, st):
-    """Compress the completed spans, then append (fp8 rows, window ring, state ring)."""
-    ops.hca_compress(st["kv_score"], st["positions"], st["qsl"], st["chunk"], st["state"], st["state_slot"], st["ape"],
-                     st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"], st["pool"])
-    ops.hca_append(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["pool"],
-                   st["ring_pages"], 128, st["state"], st["state_slot"])
+    """One HCA write call: compress the completed spans, then append (fp8
+    rows, window ring, state ring)."""
+    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["chunk"],
+                  st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
+                  st["ring_pages"], 128, st["pool"])
 
 
 def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
@@ -198,7 +198,7 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
     full = surveyed + T * 2 * D * 2 + 2 * B * 256 * 2 * D * 2
     return {
         "workload": f"hca_chunked_prefill_b{B}_chunk{st['chunk']}",
-        "kernels": "hca_compress_kernel<576> + kv_append_quant_kernel<576> (HCA rows, window ring, state ring)",
+        "kernels": "hca_compress_kernel<576> + hca_append_kernel<576> (rows, window ring, state ring)",
         "ms": round(ms, 4),
         "bytes_latent_rows": surveyed,
         "GB/s_latent_rows": round(surveyed / (ms * 1e-3) / 1e9, 1),

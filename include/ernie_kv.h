@@ -97,11 +97,10 @@ int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t
                    const int32_t* state_slot, int32_t num_state, void* stream);
 
 /*
- * The whole HCA write of one step in one launch: exactly ekv_hca_compress
- * followed by ekv_hca_append with the same arguments (same bytes in the pool
- * and the state ring), with the compression of completed spans, the row
- * appends and the ring updates running concurrently.  comp_block_table must
- * not be NULL; ring_pages / state may be.  Replaces the cache-write half of
+ * The whole HCA write of one step in one call: ekv_hca_compress followed by
+ * ekv_hca_append with the same arguments, both on `stream` (same bytes in the
+ * pool and the state ring).  comp_block_table must not be NULL; ring_pages /
+ * state may be.  Replaces the cache-write half of
  * DeepseekV4Attention._prepare_and_attn_fn (nvidia/attention.py:494-505) with
  * its compressor call (Ernie5_5Compressor.forward, nvidia/attention.py:398-408).
  */

@@ -248,6 +248,22 @@ __global__ void __launch_bounds__(256) dsa_prologue_kernel(DsaPrologueArgs a) {
     a.lengths[i] = static_cast<int32_t>(max(a.positions[i] + 1 - a.window, static_cast<int64_t>(0)));
 }
 
+int launch_hca_append(const AppendArgs& a, int dim, int num_seqs, bool rows, bool tail, hipStream_t s) {
+  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>);
+  const int main_blocks = rows ? (a.num_tokens + rows_per_block - 1) / rows_per_block : 0;
+  // each sequence's last max(ring, 256) rows, in whole tail workgroups
+  const int tail_rows =
+      (hca_tail_span(a.ring_pages != nullptr, a.ring) + kTailBlockRows - 1) / kTailBlockRows * kTailBlockRows;
+  const bool any_tail = tail && (a.ring_pages != nullptr || a.state != nullptr);
+  const int64_t blocks = main_blocks + (any_tail ? static_cast<int64_t>(num_seqs) * (tail_rows / kTailBlockRows) : 0);
+  EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
+  if (blocks == 0) return 0;
+  dim3 grid(static_cast<uint32_t>(blocks));
+  if (dim == 512) hipLaunchKernelGGL(hca_append_kernel<512>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
+  else hipLaunchKernelGGL(hca_append_kernel<576>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
+  return ekv_launch_status();
+}
+
 }  // namespace ekv
 
 // ===========================================================================
@@ -326,19 +342,7 @@ extern "C" int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, con
                                  positions, token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages,
                                  ring_stride, ring, state, state_slot, num_state);
   if (rc) return rc;
-  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>);
-  const int main_blocks = (num_tokens + rows_per_block - 1) / rows_per_block;
-  // each sequence's last max(ring, 256) rows, in whole tail workgroups
-  const int tail_rows =
-      (hca_tail_span(ring_pages != nullptr, ring) + kTailBlockRows - 1) / kTailBlockRows * kTailBlockRows;
-  const bool tail = ring_pages != nullptr || state != nullptr;
-  const int64_t blocks = main_blocks + (tail ? static_cast<int64_t>(num_seqs) * (tail_rows / kTailBlockRows) : 0);
-  EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
-  dim3 grid(static_cast<uint32_t>(blocks));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dim == 512) hipLaunchKernelGGL(hca_append_kernel<512>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
-  else hipLaunchKernelGGL(hca_append_kernel<576>, grid, dim3(256), 0, s, a, main_blocks, tail_rows);
-  return ekv_launch_status();
+  return launch_hca_append(a, dim, num_seqs, true, true, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ekv_merge_swa_topk(const int32_t* topk, int64_t topk_stride, int32_t* out,

@@ -91,15 +91,9 @@ __device__ __forceinline__ void bf16x4(uint2 v, float (&f)[4]) {
 
 constexpr float kShiftSlack = 8.0f;  // a chunk max above shift + slack moves the shift
 
-// One chunk of kChunk rows (in group order): the shift m moves to the running
-// max (and the sums are rescaled) only when the chunk's max exceeds it by
-// more than kShiftSlack -- a wave-uniform branch, rarely taken after the
-// first chunk, which sets m without rescaling (its sums are still 0) -- then
-// the rows' terms in order.
-template <bool kFirst>
-__device__ __forceinline__ void softmax_chunk(SoftmaxState& s, const uint2 (&sc)[kChunk], const uint2 (&kv)[kChunk],
-                                              const float4 (&ap)[kChunk]) {
-  float g[kChunk][4];
+// Gate values g = score + ape of one chunk of kChunk rows (in group order).
+__device__ __forceinline__ void gate_chunk(const uint2 (&sc)[kChunk], const float4 (&ap)[kChunk],
+                                           float (&g)[kChunk][4]) {
 #pragma unroll
   for (int u = 0; u < kChunk; ++u) {
     float f[4];
@@ -109,6 +103,15 @@ __device__ __forceinline__ void softmax_chunk(SoftmaxState& s, const uint2 (&sc)
     g[u][2] = f[2] + ap[u].z;
     g[u][3] = f[3] + ap[u].w;
   }
+}
+
+// One chunk's terms: the shift m moves to the running max (and the sums are
+// rescaled) only when the chunk's max exceeds it by more than kShiftSlack --
+// a wave-uniform branch, rarely taken after the first chunk, which sets m
+// without rescaling (its sums are still 0) -- then the rows' terms in order.
+template <bool kFirst>
+__device__ __forceinline__ void softmax_terms(SoftmaxState& s, const float (&g)[kChunk][4],
+                                              const uint2 (&kv)[kChunk]) {
   float mc[4];
   bool move = false;
 #pragma unroll
@@ -139,6 +142,7 @@ __device__ __forceinline__ void softmax_chunk(SoftmaxState& s, const uint2 (&sc)
       s.Z[k] = s.Z[k] + e;
       s.N[k] = __builtin_fmaf(e, v[k], s.N[k]);
     }
+    if (u + 1 < kChunk) __builtin_amdgcn_sched_barrier(0);  // one row's exps at a time: fewer live temporaries
   }
 }
 
@@ -189,9 +193,10 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
     // Every row from the input, row i at t0 - split64 + i, loaded through a
     // buffer resource: uniform base, the lane's constant byte offset (its
     // row group's row, its channels), a uniform row offset.  Chunk c + 1's
-    // loads are issued before chunk c is consumed; the scheduling barriers
-    // keep them at the start of the step (not sunk into its arithmetic) and
-    // keep the compiler from hoisting more.
+    // kv rows are loaded (double-buffered) before chunk c is consumed, its
+    // score and ape rows as soon as chunk c's gate values are formed (into
+    // the same registers); the scheduling barriers keep the loads where they
+    // are issued and keep the compiler from hoisting more.
     const uint32_t in_row = static_cast<uint32_t>(a.kvs_stride) * 2u;
     const __amdgpu_buffer_rsrc_t in_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.kv_score + (t0 - split64) * a.kvs_stride), 0, kSpan * in_row, kBufferWord3);
@@ -202,25 +207,34 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
       return make_uint2(v[0], v[1]);
     };
     constexpr int kSteps = kGroupRows / kChunk;  // chunks per row group
-    uint2 sc[2][kChunk], kv[2][kChunk];
-    float4 ap[2][kChunk];
-    auto issue = [&](int step, uint2 (&s_)[kChunk], uint2 (&k_)[kChunk], float4 (&a_)[kChunk]) {
+    uint2 sc[kChunk], kv[2][kChunk];
+    float4 ap[kChunk];
+    auto issue_kv = [&](int step, uint2 (&k_)[kChunk]) {
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) k_[u] = load2(kv_off, kRowGroups * (step * kChunk + u));
+    };
+    auto issue_gate = [&](int step) {
 #pragma unroll
       for (int u = 0; u < kChunk; ++u) {
         const int i0 = kRowGroups * (step * kChunk + u);
-        s_[u] = load2(sc_off, i0);
-        k_[u] = load2(kv_off, i0);
-        a_[u] = load_ape(i0);
+        sc[u] = load2(sc_off, i0);
+        ap[u] = load_ape(i0);
       }
     };
-    issue(0, sc[0], kv[0], ap[0]);
+    issue_kv(0, kv[0]);
+    issue_gate(0);
 #pragma unroll
     for (int step = 0; step < kSteps; ++step) {
       const int cur = step & 1;
-      if (step + 1 < kSteps) issue(step + 1, sc[cur ^ 1], kv[cur ^ 1], ap[cur ^ 1]);
+      if (step + 1 < kSteps) issue_kv(step + 1, kv[cur ^ 1]);
       __builtin_amdgcn_sched_barrier(0);
-      if (step == 0) softmax_chunk<true>(sm, sc[cur], kv[cur], ap[cur]);
-      else softmax_chunk<false>(sm, sc[cur], kv[cur], ap[cur]);
+      float g[kChunk][4];
+      gate_chunk(sc, ap, g);
+      __builtin_amdgcn_sched_barrier(0);
+      if (step + 1 < kSteps) issue_gate(step + 1);  // into the score / ape registers just consumed
+      __builtin_amdgcn_sched_barrier(0);
+      if (step == 0) softmax_terms<true>(sm, g, kv[cur]);
+      else softmax_terms<false>(sm, g, kv[cur]);
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
@@ -245,8 +259,10 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
         kv[u] = load_row(i0 + grp, 0);
         ap[u] = load_ape(i0);
       }
-      if (step == 0) softmax_chunk<true>(sm, sc, kv, ap);
-      else softmax_chunk<false>(sm, sc, kv, ap);
+      float g[kChunk][4];
+      gate_chunk(sc, ap, g);
+      if (step == 0) softmax_terms<true>(sm, g, kv);
+      else softmax_terms<false>(sm, g, kv);
     }
   }
 
@@ -321,13 +337,6 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
-// The span of sequence b that completes in this call and starts before it
-// (its first rows in the state ring), or -1.
-__device__ __forceinline__ int64_t straddling_span(int64_t p0, int n) {
-  const int64_t j = p0 / kSpan;
-  return (p0 % kSpan != 0 && j * kSpan + kSpan - 1 <= p0 + n - 1) ? j : -1;
-}
-
 // One workgroup per (span slot, sequence): span p0 / 128 + blockIdx.x of
 // sequence blockIdx.y, when this call completes it.
 template <int D>
@@ -342,106 +351,6 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
   if (j * kSpan + kSpan - 1 > p0 + n - 1) return;  // span not completed by this call
   if (j >= a.max_spans) return;
   compress_span<D>(a, ls, b, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
-}
-
-// The whole HCA write of one call in one launch (compress, then append, as
-// ekv_hca_compress followed by ekv_hca_append).  Workgroups, D threads each:
-//  * [0, B): sequence b's straddling span j0 (its rows before the call come
-//    from the state ring), then the state-ring rows this call writes over
-//    the slots it read, inside one workgroup;
-//  * next B * tail_blocks: the window-ring rows and the other state-ring rows
-//    of each sequence's last rows, kTailRows per workgroup;
-//  * the rest, interleaved in proportion (workgroups are dispatched in order,
-//    so each CU gets both kinds): B * spans workgroups compressing the other
-//    completed spans (read from this call's input only), and the append
-//    workgroups storing every row at its slot.
-// No group writes what another reads, so they all run concurrently.
-constexpr int kTailSteps = 4;  // tail rows per wave of a tail workgroup
-
-struct HcaWriteArgs {
-  CompressArgs c;
-  AppendArgs ap;
-  int32_t num_seqs, spans, tail_span, tail_blocks;
-  int32_t mixed;  // compress + append workgroups, interleaved
-};
-
-// State-ring slots read by sequence b's straddling span j0: positions
-// 128*j0 .. p0-1, i.e. slots [lo, lo + n) with lo = 128 * (j0 % 2) and
-// n = p0 - 128*j0 < 128 (n = 0 without such a span).
-struct AliasSlots {
-  int lo, n;
-};
-
-__device__ __forceinline__ AliasSlots aliased_state_slots(int64_t p0, int n) {
-  const int64_t j = straddling_span(p0, n);
-  if (j < 0) return {0, 0};
-  return {static_cast<int>(j & 1) * kSpan, static_cast<int>(p0 - j * kSpan)};
-}
-
-template <int D>
-__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca_write_kernel(HcaWriteArgs w) {
-  __shared__ CompressLds<D> ls;
-  constexpr int kWaves = D / 64;
-  int block = static_cast<int>(blockIdx.x);
-  if (block < w.num_seqs) {
-    const int b = block;
-    const int t0 = w.c.qsl[b];
-    const int n = w.c.qsl[b + 1] - t0;
-    if (n <= 0) return;
-    const int64_t p0 = w.c.positions[t0];
-    const int64_t j = straddling_span(p0, n);
-    if (j < 0) return;
-    if (j < w.c.max_spans)
-      compress_span<D>(w.c, ls, b, t0, p0, j, w.c.state_slot != nullptr ? w.c.state_slot[b] : -1);
-    __syncthreads();
-    // the state rows written over the slots it read: row k from the end
-    // (position last - k) hits slot lo + s for s < n when k = d - s mod 256,
-    // d = (last - lo) mod 256, a range of k that may wrap below 0
-    const AliasSlots al = aliased_state_slots(p0, n);
-    const int d = static_cast<int>((p0 + n - 1 - al.lo) % kStateRing);
-    const int k0 = d - al.n + 1;
-    if (k0 >= 0) {
-      hca_tail_range<D, kWaves, 1>(w.ap, b, k0, d + 1, false, al.lo, al.n, true);
-    } else {
-      hca_tail_range<D, kWaves, 1>(w.ap, b, 0, d + 1, false, al.lo, al.n, true);
-      hca_tail_range<D, kWaves, 1>(w.ap, b, k0 + kStateRing, kStateRing, false, al.lo, al.n, true);
-    }
-    return;
-  }
-  block -= w.num_seqs;
-  if (block < w.num_seqs * w.tail_blocks) {
-    const int b = block / w.tail_blocks;
-    const int t0 = w.c.qsl[b];
-    const int n = w.c.qsl[b + 1] - t0;
-    if (n <= 0) return;
-    const AliasSlots al = aliased_state_slots(w.c.positions[t0], n);
-    constexpr int kTailRows = kWaves * kTailSteps;
-    const int k_lo = (block % w.tail_blocks) * kTailRows;
-    hca_tail_range<D, kWaves, 1>(w.ap, b, k_lo, min(k_lo + kTailRows, w.tail_span), true, al.lo, al.n, false);
-    return;
-  }
-  block -= w.num_seqs * w.tail_blocks;
-  // block i of the mixed range is a compress block when the count of compress
-  // blocks before it, floor(i * NC / N), steps up at i + 1
-  const int64_t nc = static_cast<int64_t>(w.num_seqs) * w.spans;
-  const int64_t before = static_cast<int64_t>(block) * nc / w.mixed;
-  const int64_t upto = static_cast<int64_t>(block + 1) * nc / w.mixed;
-  if (upto > before) {
-    const int cb = static_cast<int>(before);
-    const int b = cb / w.spans;
-    const int t0 = w.c.qsl[b];
-    const int n = w.c.qsl[b + 1] - t0;
-    if (n <= 0) return;
-    const int64_t p0 = w.c.positions[t0];
-    const int64_t j = p0 / kSpan + cb % w.spans;
-    if (j * kSpan < p0) return;                       // the straddling span
-    if (j * kSpan + kSpan - 1 > p0 + n - 1) return;   // not completed by this call
-    if (j >= w.c.max_spans) return;
-    compress_span<D>(w.c, ls, b, t0, p0, j, -1);
-    return;
-  }
-  block -= static_cast<int>(before);
-  append_rows<D, kAppendSeq<D>, kWaves>(w.ap, block);
 }
 
 }  // namespace ekv
@@ -505,30 +414,21 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
                              int64_t num_pages, void* stream) {
   EKV_CHECK(num_tokens >= 0 && num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
   if (num_tokens == 0 || num_seqs == 0) return 0;
-  HcaWriteArgs w{};
-  int rc = hca_compress_args(w.c, kv_score, kvs_stride, positions, qsl, dim, state, state_slot, num_state, ape,
+  CompressArgs c;
+  int rc = hca_compress_args(c, kv_score, kvs_stride, positions, qsl, dim, state, state_slot, num_state, ape,
                              norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride,
                              num_pages);
   if (rc) return rc;
-  rc = hca_append_args(w.ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+  AppendArgs ap;
+  rc = hca_append_args(ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
                        token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages, ring_stride, ring, state,
                        state_slot, num_state);
   if (rc) return rc;
-  w.num_seqs = num_seqs;
-  w.spans = max_query_len / kSpan + 1;
-  w.tail_span = hca_tail_span(ring_pages != nullptr, ring);
-  const int waves = dim / 64;
-  const int tail_rows = waves * kTailSteps;
-  w.tail_blocks = (ring_pages != nullptr || state != nullptr) ? (w.tail_span + tail_rows - 1) / tail_rows : 0;
-  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>, waves);
-  const int64_t main_blocks = (static_cast<int64_t>(num_tokens) + rows_per_block - 1) / rows_per_block;
-  const int64_t mixed = static_cast<int64_t>(num_seqs) * w.spans + main_blocks;
-  const int64_t blocks = static_cast<int64_t>(num_seqs) * (1 + w.tail_blocks) + mixed;
-  EKV_CHECK(blocks < (int64_t{1} << 31) && mixed * num_seqs * w.spans < (int64_t{1} << 62), "too many rows");
-  w.mixed = static_cast<int32_t>(mixed);
-  dim3 grid(static_cast<uint32_t>(blocks));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dim == 512) hipLaunchKernelGGL(hca_write_kernel<512>, grid, dim3(512), 0, s, w);
-  else hipLaunchKernelGGL(hca_write_kernel<576>, grid, dim3(576), 0, s, w);
-  return ekv_launch_status();
+  const dim3 grid(max_query_len / kSpan + 1, num_seqs);
+  if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(512), 0, s, c);
+  else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, c);
+  rc = ekv_launch_status();
+  if (rc) return rc;
+  return launch_hca_append(ap, dim, num_seqs, true, true, s);
 }

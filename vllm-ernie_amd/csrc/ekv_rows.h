@@ -243,4 +243,9 @@ inline int hca_append_args(AppendArgs& a, const uint16_t* latent, int64_t latent
   return 0;
 }
 
+// Launch the HCA append of `a` on s: the rows at their slots (`rows`) and/or
+// each sequence's window-ring and state-ring tail (`tail`); 0 or an error
+// status.  Defined with the append kernels.
+int launch_hca_append(const AppendArgs& a, int dim, int num_seqs, bool rows, bool tail, hipStream_t s);
+
 }  // namespace ekv

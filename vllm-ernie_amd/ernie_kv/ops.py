@@ -162,7 +162,7 @@ def hca_write(
     pool: torch.Tensor,
 ) -> None:
     """``hca_compress`` then ``hca_append`` (same arguments, same result) in
-    one launch."""
+    one call."""
     _check_dev(latent, kv_score, slot_mapping, positions, token_seq, qsl, state, state_slot, ape, norm_w, cos_sin,
                comp_block_table, ring_pages, pool)
     _bits16(latent)
