@@ -207,7 +207,13 @@ int ekv_topk_select(const float* scores, int64_t scores_stride, const int32_t* l
                     int32_t num_tokens, int32_t max_len, int32_t* out, int64_t out_stride, int32_t k,
                     void* stream);
 
-/* Workspace bytes the ekv_indexer_topk family needs (shared by its stages). */
+/*
+ * Workspace bytes the ekv_indexer_topk family needs (shared by its stages).
+ * The workspace must be zero-filled once, when it is allocated: its first
+ * bytes hold counters that every call expects zero and leaves zero (the
+ * first 4 bytes count bound waits that timed out, cumulatively).  A
+ * workspace sized for (T, L) serves every call with fewer rows or tokens.
+ */
 int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len);
 
 /*

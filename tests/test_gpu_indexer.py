@@ -237,10 +237,10 @@ def _device_cache(dev, seed, num_seqs, pages_per_seq, kind):
     return bt, kcache
 
 
-def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed):
+def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed, ws=None):
     """ekv_indexer_topk against ekv_topk_select over ekv_indexer_score's exact
     scores (both bit-exact against the oracle in the tests above); returns the
-    workspace of the top-k call."""
+    workspace of the top-k call (a new zero-filled one unless `ws` is given)."""
     from ernie_kv import ops
 
     T = len(lengths)
@@ -252,7 +252,8 @@ def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed):
     w = torch.randn(T, 64, generator=g, device=dev).to(torch.bfloat16)
     q8, wf, dig = ops.indexer_q_quant(q, w)
     out = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
-    ws = ops.indexer_topk_workspace(T, max_len, dev)
+    if ws is None:
+        ws = ops.indexer_topk_workspace(T, max_len, dev)
     ops.indexer_topk(q8, dig, wf, kcache, bt, req, lens, max_len, out, ws)
     scores = torch.empty((T, max_len), dtype=torch.float32, device=dev)
     ops.indexer_score(dig, wf, kcache, bt, req, lens, max_len, scores)
@@ -270,10 +271,28 @@ def test_indexer_topk_long_rows_match_exact_path(dev, kind):
     lengths = [262144, 200000, 131072, 70000, 2049, 5000, 0, 180000]
     T, max_len = len(lengths), 262144
     ws = _topk_vs_exact_path(dev, lengths, T, max_len, kind, seed=5)
-    # workspace: 20 B per (row, token), the row histograms, 8 B per row, then
-    # four counters of waits for the bound that gave up
-    off = T * max_len * 20 + T * 4096 * 4 + T * 8
-    assert int(ws[off: off + 16].view(torch.int32).sum()) == 0
+    # the workspace starts with four counters of waits for the bound that
+    # gave up, then (from byte 256) the fused kernel's per-row counters,
+    # which every call leaves zero
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+    assert int(ws[256: 256 + T * 4100 * 4].view(torch.int32).abs().sum()) == 0
+
+
+def test_indexer_topk_workspace_reused_across_shapes(dev):
+    """One zero-filled workspace for calls of different row counts and
+    lengths (the fused kernel's counters sit at fixed offsets and are left
+    zero), including a call that takes the unfused kernels in between."""
+    from ernie_kv import ops
+
+    ws = ops.indexer_topk_workspace(1100, 70000, dev)
+    _topk_vs_exact_path(dev, [70000, 3000, 65000, 12345], 4, 70000, "normal", seed=31, ws=ws)
+    _topk_vs_exact_path(dev, [5000, 2100, 0, 4096, 3333, 2048, 4097], 3, 5000, "normal", seed=32, ws=ws)
+    rng = np.random.default_rng(33)
+    _topk_vs_exact_path(dev, rng.integers(0, 3000, 1100).astype(np.int32).tolist(), 8, 3000, "normal", seed=34,
+                        ws=ws)
+    _topk_vs_exact_path(dev, [60000, 4000], 2, 60000, "constant", seed=35, ws=ws)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+    assert int(ws[256: 256 + 1024 * 4100 * 4].view(torch.int32).abs().sum()) == 0
 
 
 def test_indexer_topk_many_rows(dev):

@@ -677,12 +677,23 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
 // The wait for the bound is bounded: a workgroup that gives up takes bin 0,
 // which makes every token of its segment a candidate -- slower, still exact.
 // ---------------------------------------------------------------------------
+// Per-row counters of the fused kernel, kCounterRow words per row at fixed
+// offsets at the front of the workspace: the row histogram, the arrival word
+// (arrivals in bits 0..15, departures in bits 16..31) and the bound word
+// ((bin << 20) | 1 once published).  They are zero when a call starts and the
+// call leaves them zero: the last workgroup to arrive zeroes the histogram
+// after reading it, the last to depart (after reading the bound) clears the
+// arrival and bound words.  So the fused path needs no clearing launch, only
+// a workspace that was zero-filled once.
+constexpr int kCounterRow = kHistBins + 4;
+constexpr int kCounterRows = 1024;  // rows the fused path takes (at most 3 x CUs)
+constexpr int64_t kCounterBytes = 256 + int64_t{kCounterRows} * kCounterRow * 4;
+
 struct FusedArgs {
-  FilterArgs f;              // f.upper is not used
+  FilterArgs f;              // f.upper and f.hist are not used
   const int8_t* q_digits;    // [T, 3, 64, 128]
-  uint32_t* arrive;          // [T] workgroups past their histogram flush (zeroed)
-  uint32_t* kword;           // [T] (bound bin << 20) | 1 once published (zeroed)
-  uint32_t* timeouts;        // waits that gave up (diagnostic; zeroed)
+  uint32_t* counters;        // [kCounterRows, kCounterRow]
+  uint32_t* timeouts;        // waits that gave up (diagnostic, cumulative)
   float* cand_score;         // [T, max_len] segment slices
   int32_t* cand_idx;
   int32_t* cand_count;       // [T, groups]
@@ -764,7 +775,9 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                   if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
                 });
   __syncthreads();
-  uint32_t* gh = f.hist + static_cast<int64_t>(t) * kHistBins;
+  uint32_t* gh = a.counters + static_cast<int64_t>(t) * kCounterRow;
+  uint32_t* const arrive = gh + kHistBins;
+  uint32_t* const kword = gh + kHistBins + 1;
   for (int i = tid; i < kHistBins; i += kThreads) {
     const uint32_t v = s_hist[i];
     if (v) atomicAdd(&gh[i], v);
@@ -793,8 +806,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // Phase 2: arrive; the last workgroup of the row publishes the bound.
   const int groups_row = (npages + per_group - 1) / per_group;
   if (tid == 0) {
-    const uint32_t before = __hip_atomic_fetch_add(a.arrive + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_misc[16] = (before + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
+    const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_misc[16] = ((before & 0xffffu) + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
     s_misc[17] = 0;
   }
   uint4* s_qd_w = reinterpret_cast<uint4*>(fused_smem);
@@ -813,6 +826,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                                   : 0;
       sum += c[j];
     }
+    // every workgroup of the row has added its histogram (its adds completed
+    // before it arrived): leave the row histogram zero for the next call
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j)
+      if (r0 + j < kHistBins)
+        __hip_atomic_store(gh + (kHistBins - 1 - (r0 + j)), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int total;
     int excl = block_scan_excl<kThreads>(sum, s_misc, total);
 #pragma unroll
@@ -821,18 +840,30 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       excl += c[j];
     }
     __syncthreads();
-    if (tid == 0)
-      __hip_atomic_store(a.kword + t, (static_cast<uint32_t>(s_misc[17]) << (32 - kHistBits)) | 1u, __ATOMIC_RELAXED,
+    if (tid == 0) {
+      __builtin_amdgcn_s_waitcnt(0);  // the histogram is zero before the bound is out
+      __hip_atomic_store(kword, (static_cast<uint32_t>(s_misc[17]) << (32 - kHistBits)) | 1u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+    }
   } else if (tid == 0) {
     uint32_t v = 0;
     for (int spins = 0; spins < kFusedSpinLimit; ++spins) {
-      v = __hip_atomic_load(a.kword + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v = __hip_atomic_load(kword, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (v != 0) break;
       __builtin_amdgcn_s_sleep(4);
     }
     if (v == 0) atomicAdd(a.timeouts, 1u);  // bin 0: every token is a candidate
     s_misc[17] = static_cast<int>(v >> (32 - kHistBits));
+  }
+  // depart: the last workgroup of the row to hold the bound clears the
+  // bound and arrival words (the last arriver departs after publishing)
+  if (tid == 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t before = __hip_atomic_fetch_add(arrive, 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((before >> 16) + 1u == static_cast<uint32_t>(groups_row)) {
+      __hip_atomic_store(kword, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   const uint32_t bin = static_cast<uint32_t>(s_misc[17]);
@@ -1381,11 +1412,17 @@ constexpr int64_t kFilterTargetGroups = 768;
 // ceil(kFilterTargetGroups / T) per row).
 int64_t count_slots(int64_t T, int32_t max_len) { return T * num_chunks(max_len) + T + kFilterTargetGroups; }
 
-// workspace: upper u16 [T,L] (4 B per entry reserved) | cand_score f32 [T,L] |
-//            cand_idx i32 [T,L] | stage_score f32 [T,L] | stage_idx i32 [T,L] |
-//            hist u32 [T,4096] | arrive u32 [T] | kbound u32 [T] |
-//            timeouts u32 [4] | counts i32 [count_slots]
+// workspace: timeouts u32 [4] (cumulative), padded to 256 B | fused-path
+//            counters u32 [kCounterRows, kCounterRow] (kept zero between
+//            calls) | upper u16 [T,L] (4 B per entry reserved) |
+//            cand_score f32 [T,L] | cand_idx i32 [T,L] | stage_score f32 [T,L] |
+//            stage_idx i32 [T,L] | hist u32 [T,4096] | arrive u32 [T] |
+//            kbound u32 [T] (the unfused path's, cleared per call) |
+//            counts i32 [count_slots]
+// The front (timeouts and counters) sits at the same offsets for every
+// (T, L), so one zero-filled allocation serves calls of any shape.
 struct TopkWorkspace {
+  uint32_t* counters;
   uint16_t* upper;
   float* cand_score;
   int32_t* cand_idx;
@@ -1400,16 +1437,18 @@ struct TopkWorkspace {
 
 TopkWorkspace carve(void* workspace, int64_t T, int64_t L) {
   TopkWorkspace w;
-  w.upper = static_cast<uint16_t*>(workspace);
-  w.cand_score = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + T * L * 4);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  w.timeouts = reinterpret_cast<uint32_t*>(base);
+  w.counters = reinterpret_cast<uint32_t*>(base + 256);
+  w.upper = reinterpret_cast<uint16_t*>(base + kCounterBytes);
+  w.cand_score = reinterpret_cast<float*>(base + kCounterBytes + T * L * 4);
   w.cand_idx = reinterpret_cast<int32_t*>(w.cand_score + T * L);
   w.stage_score = reinterpret_cast<float*>(w.cand_idx + T * L);
   w.stage_idx = reinterpret_cast<int32_t*>(w.stage_score + T * L);
   w.hist = reinterpret_cast<uint32_t*>(w.stage_idx + T * L);
   w.arrive = w.hist + T * kHistBins;
   w.kbound = w.arrive + T;
-  w.timeouts = w.kbound + T;
-  w.counts = reinterpret_cast<int32_t*>(w.timeouts + 4);
+  w.counts = reinterpret_cast<int32_t*>(w.kbound + T);
   return w;
 }
 
@@ -1449,6 +1488,7 @@ int occupancy(const void* kernel, int threads, int smem) {
 
 template <int kWaves>
 bool plan_fused(int64_t T, int32_t max_len, int64_t pages, int cus, int64_t target_groups, FilterPlan& p) {
+  if (T > kCounterRows) return false;
   const void* kernel = reinterpret_cast<const void*>(filter_verify_kernel<kWaves>);
   int64_t groups = std::max<int64_t>(1, std::min<int64_t>((pages + kWaves - 1) / kWaves, (target_groups + T - 1) / T));
   for (int attempt = 0; attempt < 4 && groups >= 1; ++attempt) {
@@ -1485,7 +1525,7 @@ FilterPlan plan_filter(int64_t T, int32_t max_len) {
 extern "C" int64_t ekv_indexer_topk_workspace_size(int32_t num_tokens, int32_t max_len) {
   if (num_tokens <= 0) return 0;
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
-  return T * L * 20 + T * kHistBins * 4 + T * 8 + 16 + count_slots(T, max_len) * 4 + 256;
+  return kCounterBytes + T * L * 20 + T * kHistBins * 4 + T * 8 + count_slots(T, max_len) * 4 + 256;
 }
 
 extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const uint8_t* kcache,
@@ -1556,15 +1596,12 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   TopkWorkspace ws = carve(workspace, T, L);
-  const int64_t nz = T * kHistBins + 2 * T + 4;  // hist, arrive, kbound, timeouts
-  const int64_t zero_blocks = (nz + 255) / 256;
-  hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
-                     dim3(256), 0, s, ws.hist, nz);
   FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                max_len, k, ws.upper, ws.hist};
   const FilterPlan plan = plan_filter(T, max_len);
   if (plan.fused) {
-    FusedArgs fa{f, q_digits, ws.arrive, ws.kbound, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
+    // the fused kernel's counters are zero on entry and left zero
+    FusedArgs fa{f, q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
                  plan.groups, plan.stage_pages};
     const dim3 grid(static_cast<unsigned>(plan.groups), num_tokens);
     if (plan.waves == 12)
@@ -1572,6 +1609,10 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, 
     else
       hipLaunchKernelGGL(filter_verify_kernel<4>, grid, dim3(64 * 4), plan.smem, s, fa);
   } else if (max_len > 0) {
+    const int64_t nz = T * kHistBins + 2 * T;  // this call's hist, arrive, kbound
+    const int64_t zero_blocks = (nz + 255) / 256;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
+                       dim3(256), 0, s, ws.hist, nz);
     hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(plan.groups), num_tokens), dim3(256), 0, s, f);
     hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
   }

@@ -345,8 +345,11 @@ def topk_select(scores: torch.Tensor, lengths: torch.Tensor, k: int, out: torch.
 
 
 def indexer_topk_workspace(num_tokens: int, max_len: int, device) -> torch.Tensor:
+    """Zero-filled workspace for the indexer top-k calls of up to
+    ``num_tokens`` rows of ``max_len`` tokens (the calls keep its counters
+    zero, so it is reused as is)."""
     need = _lib.load().ekv_indexer_topk_workspace_size(int(num_tokens), int(max_len))
-    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    return torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
 
 
 def _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T):
