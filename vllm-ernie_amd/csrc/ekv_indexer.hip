@@ -687,13 +687,15 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
 // a workspace that was zero-filled once.
 constexpr int kCounterRow = kHistBins + 4;
 constexpr int kCounterRows = 1024;  // rows the fused path takes (at most 3 x CUs)
+constexpr int kHistRereads = 64;    // reads of a row histogram that does not yet sum to its tokens
 constexpr int64_t kCounterBytes = 256 + int64_t{kCounterRows} * kCounterRow * 4;
 
 struct FusedArgs {
   FilterArgs f;              // f.upper and f.hist are not used
   const int8_t* q_digits;    // [T, 3, 64, 128]
   uint32_t* counters;        // [kCounterRows, kCounterRow]
-  uint32_t* timeouts;        // waits that gave up (diagnostic, cumulative)
+  uint32_t* timeouts;        // [0] bound waits that gave up, [1] histograms that never summed to n
+                             // (diagnostic, cumulative)
   float* cand_score;         // [T, max_len] segment slices
   int32_t* cand_idx;
   int32_t* cand_count;       // [T, groups]
@@ -818,26 +820,38 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     constexpr int kBinsPer = (kHistBins + kThreads - 1) / kThreads;  // scanned from the top bin down
     const int r0 = kBinsPer * tid;
     int c[kBinsPer];
-    int sum = 0;
+    int excl = 0, total = 0;
+    // The row histogram counts each of the row's n tokens once.  Every
+    // workgroup's adds completed before it arrived, so the bins sum to n;
+    // the check makes the bound (and the clearing below) rely on that sum,
+    // not on the ordering: the bins are read again until they sum to n, and
+    // a histogram that never does gives bin 0 (every token a candidate).
+    for (int attempt = 0;; ++attempt) {
+      int sum = 0;
 #pragma unroll
-    for (int j = 0; j < kBinsPer; ++j) {
-      c[j] = (r0 + j < kHistBins) ? static_cast<int>(__hip_atomic_load(gh + (kHistBins - 1 - (r0 + j)), __ATOMIC_RELAXED,
-                                                                        __HIP_MEMORY_SCOPE_AGENT))
-                                  : 0;
-      sum += c[j];
+      for (int j = 0; j < kBinsPer; ++j) {
+        c[j] = (r0 + j < kHistBins) ? static_cast<int>(__hip_atomic_load(gh + (kHistBins - 1 - (r0 + j)),
+                                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                                    : 0;
+        sum += c[j];
+      }
+      excl = block_scan_excl<kThreads>(sum, s_misc, total);
+      if (total == n || attempt == kHistRereads) break;
+      __builtin_amdgcn_s_sleep(8);
     }
-    // every workgroup of the row has added its histogram (its adds completed
-    // before it arrived): leave the row histogram zero for the next call
+    // leave the row histogram zero for the next call
 #pragma unroll
     for (int j = 0; j < kBinsPer; ++j)
       if (r0 + j < kHistBins)
         __hip_atomic_store(gh + (kHistBins - 1 - (r0 + j)), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int total;
-    int excl = block_scan_excl<kThreads>(sum, s_misc, total);
+    if (total == n) {
 #pragma unroll
-    for (int j = 0; j < kBinsPer; ++j) {
-      if (excl < f.k && f.k <= excl + c[j]) s_misc[17] = kHistBins - 1 - (r0 + j);
-      excl += c[j];
+      for (int j = 0; j < kBinsPer; ++j) {
+        if (excl < f.k && f.k <= excl + c[j]) s_misc[17] = kHistBins - 1 - (r0 + j);
+        excl += c[j];
+      }
+    } else if (tid == 0) {
+      atomicAdd(a.timeouts + 1, 1u);  // bin 0 (s_misc[17] stays 0)
     }
     __syncthreads();
     if (tid == 0) {
