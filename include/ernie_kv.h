@@ -144,6 +144,21 @@ int ekv_hadamard_rows(const uint16_t* x, int64_t x_stride, uint16_t* y, int64_t 
                       int32_t dim, void* stream);
 
 /*
+ * Indexer prep: k_out = hadamard(rope(k_norm(k))), q_out = hadamard(rope(q))
+ * for q [T, heads, 128] and k [T, 128] bf16, with k_norm the LayerNorm
+ * (ln_w, ln_b fp32 [128], eps) and rope the NeoX rotation of dims 0..63 by
+ * row positions[t] of cos_sin [cos_sin_rows, 64] fp32 (cos 32 | sin 32;
+ * positions outside the table leave the row unrotated).  Outputs contiguous
+ * bf16.  Replaces the head of Ernie5_5Indexer.forward before the fp8
+ * quantization: k_norm, rotary_emb, hadamard_rows (nvidia/attention.py:
+ * 955-969; module setup :912-922).
+ */
+int ekv_indexer_prep(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const uint16_t* k,
+                     int64_t k_stride, int32_t num_tokens, int32_t heads, const float* ln_w, const float* ln_b,
+                     float eps, const float* cos_sin, int32_t cos_sin_rows, const int64_t* positions,
+                     uint16_t* q_out, uint16_t* k_out, void* stream);
+
+/*
  * Indexer q quant: q [T, heads, 128] bf16 -> fp8 with a per-(token, head)
  * UE8M0 scale folded into the head weights:
  *   w_out = (w * q_scale) * 128^-0.5 * 64^-0.5.

@@ -104,6 +104,53 @@ def neox_partial_rope(x: np.ndarray, cos_sin: np.ndarray, rot_dim: int) -> np.nd
     return out
 
 
+def _chunk_tree_sum(v: np.ndarray) -> np.ndarray:
+    """Sum of each 128-wide row in the kernel's fp32 order: per 8-element
+    chunk ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)), then a butterfly over the 16
+    chunks (partners at distance 1, 2, 4, 8), which leaves every chunk with
+    the same balanced-tree total."""
+    f32 = np.float32
+    c = v.reshape(*v.shape[:-1], 16, 8).astype(f32)
+    p = [(c[..., 2 * i] + c[..., 2 * i + 1]).astype(f32) for i in range(4)]
+    s = (((p[0] + p[1]).astype(f32)) + ((p[2] + p[3]).astype(f32))).astype(f32)
+    idx = np.arange(16)
+    for off in (1, 2, 4, 8):
+        s = (s + s[..., idx ^ off]).astype(f32)
+    return s[..., 0]
+
+
+def layer_norm_rows(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+    """LayerNorm of each 128-wide row (the indexer's ``k_norm``,
+    nvidia/attention.py:912, 962), in fp32 with the sums in
+    ``_chunk_tree_sum``'s order::
+
+        mean = fl32(S(x) / 128);  d = fl32(x - mean);  var = fl32(S(fl32(d*d)) / 128)
+        rstd = fl32(1 / sqrt_rn(fl32(var + eps)));  y = bf16(fl32(fl32(fl32(d * rstd) * w) + b))
+
+    Returns float32 values that are exactly bf16-representable."""
+    f32 = np.float32
+    x = np.asarray(x, f32)
+    n = f32(x.shape[-1])
+    mean = (_chunk_tree_sum(x) / n).astype(f32)
+    d = (x - mean[..., None]).astype(f32)
+    var = (_chunk_tree_sum((d * d).astype(f32)) / n).astype(f32)
+    rstd = (f32(1.0) / np.sqrt((var + f32(eps)).astype(f32))).astype(f32)
+    y = ((((d * rstd[..., None]).astype(f32)) * np.asarray(w, f32)).astype(f32) + np.asarray(b, f32)).astype(f32)
+    return bf16_round(y)
+
+
+def indexer_prep(q: np.ndarray, k: np.ndarray, ln_w: np.ndarray, ln_b: np.ndarray, eps: float,
+                 cos_sin: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """``Ernie5_5Indexer.forward`` up to the quantization (nvidia/attention.py:
+    955-969): ``k = hadamard(rope(k_norm(k)))``, ``q = hadamard(rope(q))``, the
+    NeoX rotation on dims 0..63.  ``q [T, 64, 128]``, ``k [T, 128]`` bf16 values,
+    ``cos_sin [T, 64]`` (the rows of the tokens' positions)."""
+    cs = np.asarray(cos_sin, np.float32)
+    k1 = neox_partial_rope(layer_norm_rows(k, ln_w, ln_b, eps), cs, 64)
+    q1 = neox_partial_rope(np.asarray(q, np.float32), cs[:, None, :], 64)
+    return hadamard_rows(q1), hadamard_rows(k1)
+
+
 WEIGHTS_SCALE = np.float32(INDEX_HEAD_DIM**-0.5 * INDEX_N_HEADS**-0.5)  # attention.py:925
 
 

@@ -36,6 +36,33 @@ def test_merge_swa_topk_known_answer(dev):
     assert np.array_equal(out.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("T", [1, 3, 33])
+def test_indexer_prep_exact(dev, T):
+    """k_norm + NeoX rope + Hadamard of q and k (attention.py:955-969),
+    bit-exact against the oracle; varied positions (one outside the table
+    stays unrotated), row scales and a constant k row."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(100 + T)
+    q = randn_bf16(rng, (T, 64, 128), scale=2.0)
+    k = (rng.standard_normal((T, 128)) * rng.uniform(0.05, 20, (T, 1)) + rng.uniform(-3, 3, (T, 1))).astype(np.float32)
+    k[0] = 0.75  # constant row: normalizes to the bias
+    k = bf16_values(bf16_tensor(k, "cpu"))
+    w = (1 + 0.2 * rng.standard_normal(128)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(128)).astype(np.float32)
+    table_rows = 70000
+    pos = rng.integers(0, table_rows, T).astype(np.int64)
+    pos[-1] = table_rows + 5 if T > 1 else pos[-1]
+    cs_table = oi.rope_cos_sin(np.arange(table_rows), 64, 8e6)
+    qo, ko = ops.indexer_prep(bf16_tensor(q, dev), bf16_tensor(k, dev), to_dev(w, dev), to_dev(b, dev), 1e-6,
+                              to_dev(cs_table, dev), to_dev(pos, dev))
+    cs = np.where((pos < table_rows)[:, None], cs_table[np.minimum(pos, table_rows - 1)],
+                  np.concatenate([np.ones(32), np.zeros(32)]).astype(np.float32))
+    rq, rk = oi.indexer_prep(q, k, w, b, 1e-6, cs.astype(np.float32))
+    assert np.array_equal(bf16_values(ko), rk)
+    assert np.array_equal(bf16_values(qo), rq)
+
+
 @pytest.mark.parametrize("num_rows", [1, 2, 5, 6, 7, 64, 129, 1026])
 def test_hadamard_rows_exact(dev, num_rows):
     from ernie_kv import ops

@@ -105,6 +105,57 @@ def test_partial_rope_split_cat_bit_exact():
     assert np.allclose(n0, n1, rtol=2e-2, atol=1e-2)
 
 
+def test_layer_norm_rows_against_fp64_torch():
+    """The k_norm restatement (attention.py:912, 962) against
+    torch.nn.functional.layer_norm in fp64: within one bf16 rounding."""
+    rng = np.random.default_rng(41)
+    x = bf16_round((rng.standard_normal((300, 128)) * rng.uniform(0.01, 30, (300, 1))
+                    + rng.uniform(-5, 5, (300, 1))).astype(np.float32))
+    w = (1 + 0.2 * rng.standard_normal(128)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(128)).astype(np.float32)
+    got = oi.layer_norm_rows(x, w, b, 1e-6)
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (128,), torch.from_numpy(w).double(),
+                                         torch.from_numpy(b).double(), 1e-6).numpy()
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-5)
+    assert np.array_equal(got, bf16_round(got))
+
+
+def test_layer_norm_rows_closed_forms():
+    """A constant row normalizes to the bias exactly; with eps = 0, scaling a
+    row by a power of two leaves every output bit unchanged; the reduction
+    order sums to the exact row sum within fp32 rounding."""
+    rng = np.random.default_rng(42)
+    w = (1 + 0.2 * rng.standard_normal(128)).astype(np.float32)
+    b = bf16_round((0.1 * rng.standard_normal(128)).astype(np.float32))
+    const = np.full((3, 128), 1.5, np.float32)
+    assert np.array_equal(oi.layer_norm_rows(const, w, b, 1e-6), np.broadcast_to(b, (3, 128)))
+    x = bf16_round(rng.standard_normal((50, 128)).astype(np.float32))
+    base = oi.layer_norm_rows(x, w, b, 0.0)
+    for k in (-3, 5, 11):
+        assert np.array_equal(oi.layer_norm_rows((x * np.float32(2.0 ** k)).astype(np.float32), w, b, 0.0), base)
+    s = oi._chunk_tree_sum(x)
+    np.testing.assert_allclose(s, x.astype(np.float64).sum(-1), rtol=0, atol=1e-4)
+    # unit weight, zero bias: every row has mean 0 and (biased) variance 1
+    # up to the bf16 rounding, which averages out over 128 entries
+    y = oi.layer_norm_rows(x, np.ones(128, np.float32), np.zeros(128, np.float32), 0.0).astype(np.float64)
+    assert np.abs(y.mean(-1)).max() < 2e-3
+    assert np.abs((y * y).mean(-1) - 1.0).max() < 2e-3
+
+
+def test_indexer_prep_at_position_zero_is_norm_then_hadamard():
+    """At position 0 the rotation is the identity (cos 1, sin 0), so the prep
+    reduces to hadamard(k_norm(k)) and hadamard(q), bit for bit."""
+    rng = np.random.default_rng(43)
+    q = bf16_round(rng.standard_normal((3, 64, 128)).astype(np.float32))
+    k = bf16_round(rng.standard_normal((3, 128)).astype(np.float32))
+    w = (1 + 0.2 * rng.standard_normal(128)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(128)).astype(np.float32)
+    cs = oi.rope_cos_sin(np.zeros(3, np.int64), 64, 8e6)
+    qh, kh = oi.indexer_prep(q, k, w, b, 1e-6, cs)
+    assert np.array_equal(kh, oi.hadamard_rows(oi.layer_norm_rows(k, w, b, 1e-6)))
+    assert np.array_equal(qh, oi.hadamard_rows(q))
+
+
 def test_q_quant_weight_fold():
     """attention.py:925, 980: w * q_scale * 128**-0.5 * 64**-0.5."""
     rng = np.random.default_rng(4)

@@ -94,6 +94,141 @@ __global__ void __launch_bounds__(256) hadamard_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// indexer prep (Ernie5_5Indexer.forward up to the quantization): k_norm
+// LayerNorm of k, NeoX RoPE on dims 0..63 of q and k, Hadamard.  One 16-lane
+// group per 128-wide row; lane j of the group holds elements 8j .. 8j+7 (fp32
+// copies of bf16 values).  Cross-lane partners are lane ^ 1, 2, 4, 8, inside
+// the group.
+// ---------------------------------------------------------------------------
+// Sum of the row: per lane ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)), then a
+// butterfly over the 16 lanes (partners 1, 2, 4, 8); every lane ends with the
+// same balanced-tree total.
+__device__ __forceinline__ float row_sum16(const float (&v)[8]) {
+  float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) s = s + __shfl_xor(s, off);
+  return s;
+}
+
+// y = bf16((d * rstd) * w + b), d = x - mean, over the 128-wide row.
+__device__ __forceinline__ void row_layer_norm(float (&v)[8], const float* w, const float* b, float eps, int j) {
+  const float mean = __fdiv_rn(row_sum16(v), 128.0f);
+  float d[8], sq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    d[e] = v[e] - mean;
+    sq[e] = d[e] * d[e];
+  }
+  const float var = __fdiv_rn(row_sum16(sq), 128.0f);
+  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
+  const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * j), w1 = *reinterpret_cast<const float4*>(w + 8 * j + 4);
+  const float4 b0 = *reinterpret_cast<const float4*>(b + 8 * j), b1 = *reinterpret_cast<const float4*>(b + 8 * j + 4);
+  const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16((d[e] * rstd) * ww[e] + bb[e]));
+}
+
+// NeoX rotation of dims 0..63 by (cos_i, sin_i) = (cs[i], cs[32 + i]): dim i
+// (lanes 0..3) pairs with dim i + 32 (lanes 4..7); cs == nullptr leaves the
+// row as it is.
+__device__ __forceinline__ void row_rope_neox64(float (&v)[8], const float* cs, int j) {
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], 4);
+  if (cs == nullptr || j >= 8) return;
+  const int i0 = 8 * (j & 3);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cs[i0 + e], sn = cs[32 + i0 + e];
+    const float r = (j < 4) ? (v[e] * c) - (p[e] * sn)   // x1 c - x2 s
+                            : (v[e] * c) + (p[e] * sn);  // x2 c + x1 s
+    v[e] = bf16_to_f32(f32_to_bf16(r));
+  }
+}
+
+// Orthonormal Walsh-Hadamard of the row: spans 1, 2, ..., 64 with
+// (a, b) -> (a + b, a - b), then times fl32(1/sqrt(128)), rounded to bf16.
+__device__ __forceinline__ void row_hadamard(float (&v)[8], int j) {
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if ((e & h) == 0) {
+        const float a = v[e], b = v[e + h];
+        v[e] = a + b;
+        v[e + h] = a - b;
+      }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    const bool lower = (j & m) == 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __shfl_xor(v[e], m);
+      v[e] = lower ? (v[e] + p) : (p - v[e]);
+    }
+  }
+  const float s = 0x1.6a09e6p-4f;  // fl32(1/sqrt(128))
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16(v[e] * s));
+}
+
+__device__ __forceinline__ void unpack_bf16x8(uint4 w, float (&v)[8]) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ww[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float (&v)[8]) {
+  uint32_t ww[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ww[i] = (__float_as_uint(v[2 * i]) >> 16) | (__float_as_uint(v[2 * i + 1]) & 0xffff0000u);
+  return make_uint4(ww[0], ww[1], ww[2], ww[3]);
+}
+
+struct PrepArgs {
+  const uint16_t* q;  // [T, heads, 128] bf16
+  int64_t q_tok_stride, q_head_stride;
+  const uint16_t* k;  // [T, 128] bf16
+  int64_t k_stride;
+  int32_t num_tokens, heads;
+  const float* ln_w;  // [128]
+  const float* ln_b;  // [128]
+  float eps;
+  const float* cos_sin;  // [cs_rows, 64]: cos 32 | sin 32
+  int32_t cs_rows;
+  const int64_t* positions;  // [T]
+  uint16_t* q_out;           // [T, heads, 128]
+  uint16_t* k_out;           // [T, 128]
+};
+
+// Rows of workgroup `block` (16 per workgroup): q rows (token, head) first,
+// then k rows.  Positions outside the cos/sin table leave the row unrotated.
+__device__ __forceinline__ void prep_rows(const PrepArgs& a, int block) {
+  const int j = threadIdx.x & 15;
+  const int64_t row = static_cast<int64_t>(block) * 16 + (threadIdx.x >> 4);
+  const int64_t q_rows = static_cast<int64_t>(a.num_tokens) * a.heads;
+  if (row >= q_rows + a.num_tokens) return;  // whole 16-lane group exits together
+  const bool is_q = row < q_rows;
+  const int64_t t = is_q ? row / a.heads : row - q_rows;
+  const uint16_t* src = is_q ? a.q + t * a.q_tok_stride + (row % a.heads) * a.q_head_stride : a.k + t * a.k_stride;
+  float v[8];
+  unpack_bf16x8(*reinterpret_cast<const uint4*>(src + 8 * j), v);
+  const int64_t pos = a.positions[t];
+  const float* cs = (pos >= 0 && pos < a.cs_rows) ? a.cos_sin + pos * 64 : nullptr;
+  if (!is_q) row_layer_norm(v, a.ln_w, a.ln_b, a.eps, j);
+  row_rope_neox64(v, cs, j);
+  row_hadamard(v, j);
+  uint16_t* dst = is_q ? a.q_out + row * 128 : a.k_out + t * 128;
+  *reinterpret_cast<uint4*>(dst + 8 * j) = pack_bf16x8(v);
+}
+
+__global__ void __launch_bounds__(256) indexer_prep_kernel(PrepArgs a) { prep_rows(a, blockIdx.x); }
+
+// ---------------------------------------------------------------------------
 // indexer_q_quant: one 16-lane group per (token, head) row of 128.
 // ---------------------------------------------------------------------------
 struct QQuantArgs {
@@ -367,6 +502,29 @@ extern "C" int ekv_hadamard_rows(const uint16_t* x, int64_t x_stride, uint16_t* 
   EKV_CHECK(aligned4(x) && aligned4(y), "rows must be 4-byte aligned");
   hipLaunchKernelGGL(hadamard_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, x_stride, y, y_stride, rows);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_prep(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride, const uint16_t* k,
+                                int64_t k_stride, int32_t num_tokens, int32_t heads, const float* ln_w,
+                                const float* ln_b, float eps, const float* cos_sin, int32_t cos_sin_rows,
+                                const int64_t* positions, uint16_t* q_out, uint16_t* k_out, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && heads >= 0, "sizes must be >= 0");
+  if (num_tokens == 0) return 0;
+  EKV_CHECK(q && k && ln_w && ln_b && cos_sin && positions && q_out && k_out, "null pointer");
+  EKV_CHECK(q_head_stride >= 128 && q_tok_stride >= heads * q_head_stride && k_stride >= 128 &&
+                q_head_stride % 8 == 0 && q_tok_stride % 8 == 0 && k_stride % 8 == 0,
+            "q [T, heads, 128] and k [T, 128] rows must be 16-byte aligned, 128 wide");
+  EKV_CHECK(aligned16(q) && aligned16(k) && aligned16(q_out) && aligned16(k_out) && aligned16(ln_w) &&
+                aligned16(ln_b) && aligned16(cos_sin),
+            "buffers must be 16-byte aligned");
+  EKV_CHECK(cos_sin_rows >= 0, "cos_sin_rows must be >= 0");
+  PrepArgs a{q, q_tok_stride, q_head_stride, k, k_stride, num_tokens, heads, ln_w, ln_b, eps, cos_sin, cos_sin_rows,
+             positions, q_out, k_out};
+  const int64_t rows = static_cast<int64_t>(num_tokens) * (heads + 1);
+  EKV_CHECK((rows + 15) / 16 < (int64_t{1} << 31), "too many rows");
+  hipLaunchKernelGGL(indexer_prep_kernel, dim3(static_cast<uint32_t>((rows + 15) / 16)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return ekv_launch_status();
 }
 

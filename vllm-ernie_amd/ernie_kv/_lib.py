@@ -38,6 +38,7 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_hca_decode_indices": (I32, [P, P, I32, P, I32, P, I32, I32, I32, P, I64, I32, P, P]),
     "ekv_merge_swa_topk": (I32, [P, I64, P, I64, P, I32, I32, I32, I32, P]),
     "ekv_hadamard_rows": (I32, [P, I64, P, I64, I32, I32, P]),
+    "ekv_indexer_prep": (I32, [P, I64, I64, P, I64, I32, I32, P, P, F32, P, I32, P, P, P, P]),
     "ekv_indexer_q_quant": (I32, [P, I64, I64, P, I32, I64, I32, I32, P, P, P, P]),
     "ekv_indexer_windowed_lengths": (I32, [P, I32, I32, P, P]),
     "ekv_dsa_decode_prologue": (I32, [P, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I32, P, I64, I64, P, I32,

@@ -229,6 +229,38 @@ def merge_swa_topk(topk_indices: torch.Tensor, out: torch.Tensor, positions: tor
     )
 
 
+def indexer_prep(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    ln_w: torch.Tensor,
+    ln_b: torch.Tensor,
+    eps: float,
+    cos_sin: torch.Tensor,
+    positions: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``Ernie5_5Indexer.forward`` before the quantization (attention.py:
+    955-969): ``(hadamard(rope(q)), hadamard(rope(k_norm(k))))`` for
+    ``q [T, H, 128]``, ``k [T, 128]`` bf16; NeoX rope on dims 0..63 by the rows
+    ``cos_sin[positions]`` of an fp32 ``[N, 64]`` table (cos | sin)."""
+    _check_dev(q, k, ln_w, ln_b, cos_sin, positions)
+    _bits16(q)
+    _bits16(k)
+    T, H, D = q.shape
+    _need(D == 128 and q.stride(2) == 1 and k.shape == (T, 128) and k.stride(1) == 1, "q [T, H, 128], k [T, 128]")
+    _need(ln_w.shape == (128,) and ln_b.shape == (128,) and ln_w.dtype == torch.float32 and ln_b.dtype == torch.float32,
+          "ln_w, ln_b fp32 [128]")
+    _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(), "cos_sin fp32 [N, 64]")
+    _need(positions.dtype == torch.int64 and positions.numel() == T, "positions int64 [T]")
+    q_out = torch.empty((T, H, 128), dtype=q.dtype, device=q.device)
+    k_out = torch.empty((T, 128), dtype=k.dtype, device=k.device)
+    _lib.call(
+        "ekv_indexer_prep", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), _rs(k), T, H,
+        ln_w.contiguous().data_ptr(), ln_b.contiguous().data_ptr(), float(eps), cos_sin.data_ptr(), cos_sin.shape[0],
+        positions.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), _stream(),
+    )
+    return q_out, k_out
+
+
 def hadamard_rows(x: torch.Tensor) -> torch.Tensor:
     """Reference semantics of ``hadamard_rows`` (attention.py:102-108)."""
     _check_dev(x)
