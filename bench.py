@@ -91,6 +91,13 @@ def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
         out=torch.empty((B, 64, 512), dtype=torch.bfloat16, device=dev),
         lse=torch.empty((B, 64), dtype=torch.float32, device=dev),
     )
+    # indexer prep: k_norm LayerNorm parameters and the rope table (theta
+    # 2.5e6, rope_theta of the config) for every position of the context
+    st["ln_w"] = (1.0 + 0.1 * torch.randn(128, device=dev, generator=g)).contiguous()
+    st["ln_b"] = (0.1 * torch.randn(128, device=dev, generator=g)).contiguous()
+    inv = 2.5e6 ** (-torch.arange(32, device=dev, dtype=torch.float64) * 2.0 / 64)
+    ang = torch.arange(ctx, device=dev, dtype=torch.float64)[:, None] * inv[None, :]
+    st["rope"] = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).contiguous()
     need = ops._lib.load().ekv_sparse_mla_decode_workspace_size(B, 64, 2176)
     st["dec_ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
     st["idx_ws"] = ops.indexer_topk_workspace(B, ctx, dev)
@@ -109,11 +116,12 @@ def dsa_step(ops, st, ev=None):
 
 
 def dsa_pre(ops, st):
-    """Cache appends of the new token, the indexer's q quantization and the
+    """From the raw indexer projections: k_norm, rope and Hadamard of q and k,
+    cache appends of the new token, the indexer's q quantization and the
     windowed lengths, in one launch."""
     st["q8"], st["wf"], st["digits"] = ops.dsa_decode_prologue(
         st["k_new"], st["kcache"], st["latent_new"], st["latent"], st["slots"], st["q_idx"], st["w_idx"],
-        st["positions"], 128, st["lengths"])
+        st["positions"], 128, st["lengths"], prep=(st["ln_w"], st["ln_b"], 1e-6, st["rope"]))
 
 
 def dsa_filter(ops, st):

@@ -175,11 +175,14 @@ int ekv_indexer_q_quant(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
  * DSA decode prologue in one launch, with the results of ekv_indexer_k_insert
  * (k rows into kcache), ekv_kv_append_quant (latent rows of width dim into
  * cache; both at slot_mapping), ekv_indexer_q_quant and
- * ekv_indexer_windowed_lengths with the same arguments.  No single reference
- * function does all four: it replaces, for a decode step, the indexer K
- * insert (nvidia/attention.py:942-953), the MLA latent append [vLLM
- * concat_and_cache_mla], the q quant of SparseAttnIndexer
- * (nvidia/attention.py:976-980) and the metadata lengths
+ * ekv_indexer_windowed_lengths with the same arguments.  With cos_sin
+ * non-null, q and k are the raw indexer projections and ekv_indexer_prep
+ * (ln_w, ln_b, eps, cos_sin, cos_sin_rows, positions) runs first on them, in
+ * the same launch.  No single reference function does all of this: it
+ * replaces, for a decode step, the head of Ernie5_5Indexer.forward
+ * (k_norm, rotary_emb, hadamard_rows, q quant; nvidia/attention.py:955-980),
+ * the indexer K insert (nvidia/attention.py:942-953), the MLA latent append
+ * [vLLM concat_and_cache_mla] and the metadata lengths
  * (nvidia/attention.py:669-675).
  */
 int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride,
@@ -188,7 +191,8 @@ int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint8_t* kcache
                             int32_t num_tokens, const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                             const void* weights, int32_t weights_is_bf16, int64_t w_stride, int32_t heads,
                             uint8_t* q_fp8, float* w_out, int8_t* q_digits, const int64_t* positions,
-                            int32_t window, int32_t* lengths, void* stream);
+                            int32_t window, int32_t* lengths, const float* ln_w, const float* ln_b, float eps,
+                            const float* cos_sin, int32_t cos_sin_rows, void* stream);
 
 /*
  * Windowed indexer lengths out[t] = max(positions[t] + 1 - window, 0).

@@ -99,3 +99,37 @@ def test_dsa_decode_prologue_matches_separate_calls(dev, dim):
     assert torch.equal(kc[0], kc[1]) and torch.equal(lc[0], lc[1]) and torch.equal(lens[0], lens[1])
     for a, b in zip(ref_q, got_q):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dim", [576, 512])
+def test_dsa_decode_prologue_with_indexer_prep(dev, dim):
+    """With the prep arguments the prologue takes the raw indexer projections:
+    it equals ekv_indexer_prep followed by the prologue without them."""
+    from ernie_kv import ops
+    from oracle import indexer as oi
+
+    rng = np.random.default_rng(dim + 7)
+    T, H, pages = 19, 64, 40
+    slots = rng.choice(pages * 64, T, replace=False).astype(np.int64)
+    slots[5] = -1
+    slots_t = to_dev(slots, dev)
+    pos_np = rng.integers(0, 9000, T).astype(np.int64)
+    pos_np[0] = 0
+    positions = to_dev(pos_np, dev)
+    k = bf16_tensor((rng.standard_normal((T, 128)) * 3 + 1).astype(np.float32), dev)
+    lat = bf16_tensor(randn_bf16(rng, (T, dim)), dev)
+    q = bf16_tensor(randn_bf16(rng, (T, H, 128), 2.0), dev)
+    w = bf16_tensor(randn_bf16(rng, (T, H)), dev)
+    ln_w = to_dev((1 + 0.2 * rng.standard_normal(128)).astype(np.float32), dev)
+    ln_b = to_dev((0.1 * rng.standard_normal(128)).astype(np.float32), dev)
+    cs = to_dev(oi.rope_cos_sin(np.arange(10000), 64, 8e6), dev)
+    kc = [torch.zeros((pages, 64 * 132), dtype=torch.uint8, device=dev) for _ in range(2)]
+    lc = [torch.zeros((pages, 64 * (dim + 4)), dtype=torch.uint8, device=dev) for _ in range(2)]
+    lens = [torch.full((T,), -5, dtype=torch.int32, device=dev) for _ in range(2)]
+    qh, kh = ops.indexer_prep(q, k, ln_w, ln_b, 1e-6, cs, positions)
+    ref_q = ops.dsa_decode_prologue(kh, kc[0], lat, lc[0], slots_t, qh, w, positions, 128, lens[0])
+    got_q = ops.dsa_decode_prologue(k, kc[1], lat, lc[1], slots_t, q, w, positions, 128, lens[1],
+                                    prep=(ln_w, ln_b, 1e-6, cs))
+    assert torch.equal(kc[0], kc[1]) and torch.equal(lc[0], lc[1]) and torch.equal(lens[0], lens[1])
+    for a, b in zip(ref_q, got_q):
+        assert torch.equal(a, b)

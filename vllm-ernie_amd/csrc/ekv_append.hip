@@ -100,95 +100,6 @@ __global__ void __launch_bounds__(256) hadamard_rows_kernel(
 // copies of bf16 values).  Cross-lane partners are lane ^ 1, 2, 4, 8, inside
 // the group.
 // ---------------------------------------------------------------------------
-// Sum of the row: per lane ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)), then a
-// butterfly over the 16 lanes (partners 1, 2, 4, 8); every lane ends with the
-// same balanced-tree total.
-__device__ __forceinline__ float row_sum16(const float (&v)[8]) {
-  float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) s = s + __shfl_xor(s, off);
-  return s;
-}
-
-// y = bf16((d * rstd) * w + b), d = x - mean, over the 128-wide row.
-__device__ __forceinline__ void row_layer_norm(float (&v)[8], const float* w, const float* b, float eps, int j) {
-  const float mean = __fdiv_rn(row_sum16(v), 128.0f);
-  float d[8], sq[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    d[e] = v[e] - mean;
-    sq[e] = d[e] * d[e];
-  }
-  const float var = __fdiv_rn(row_sum16(sq), 128.0f);
-  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
-  const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * j), w1 = *reinterpret_cast<const float4*>(w + 8 * j + 4);
-  const float4 b0 = *reinterpret_cast<const float4*>(b + 8 * j), b1 = *reinterpret_cast<const float4*>(b + 8 * j + 4);
-  const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-  const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16((d[e] * rstd) * ww[e] + bb[e]));
-}
-
-// NeoX rotation of dims 0..63 by (cos_i, sin_i) = (cs[i], cs[32 + i]): dim i
-// (lanes 0..3) pairs with dim i + 32 (lanes 4..7); cs == nullptr leaves the
-// row as it is.
-__device__ __forceinline__ void row_rope_neox64(float (&v)[8], const float* cs, int j) {
-  float p[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], 4);
-  if (cs == nullptr || j >= 8) return;
-  const int i0 = 8 * (j & 3);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float c = cs[i0 + e], sn = cs[32 + i0 + e];
-    const float r = (j < 4) ? (v[e] * c) - (p[e] * sn)   // x1 c - x2 s
-                            : (v[e] * c) + (p[e] * sn);  // x2 c + x1 s
-    v[e] = bf16_to_f32(f32_to_bf16(r));
-  }
-}
-
-// Orthonormal Walsh-Hadamard of the row: spans 1, 2, ..., 64 with
-// (a, b) -> (a + b, a - b), then times fl32(1/sqrt(128)), rounded to bf16.
-__device__ __forceinline__ void row_hadamard(float (&v)[8], int j) {
-#pragma unroll
-  for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if ((e & h) == 0) {
-        const float a = v[e], b = v[e + h];
-        v[e] = a + b;
-        v[e + h] = a - b;
-      }
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const bool lower = (j & m) == 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = __shfl_xor(v[e], m);
-      v[e] = lower ? (v[e] + p) : (p - v[e]);
-    }
-  }
-  const float s = 0x1.6a09e6p-4f;  // fl32(1/sqrt(128))
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16(v[e] * s));
-}
-
-__device__ __forceinline__ void unpack_bf16x8(uint4 w, float (&v)[8]) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float(ww[i] << 16);
-    v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
-  }
-}
-
-__device__ __forceinline__ uint4 pack_bf16x8(const float (&v)[8]) {
-  uint32_t ww[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ww[i] = (__float_as_uint(v[2 * i]) >> 16) | (__float_as_uint(v[2 * i + 1]) & 0xffff0000u);
-  return make_uint4(ww[0], ww[1], ww[2], ww[3]);
-}
-
 struct PrepArgs {
   const uint16_t* q;  // [T, heads, 128] bf16
   int64_t q_tok_stride, q_head_stride;
@@ -241,6 +152,11 @@ struct QQuantArgs {
   uint8_t* q_fp8;            // [T, heads, 128]
   float* w_out;              // [T, heads]
   int8_t* q_digits;          // [T, 3, heads, 128] or null
+  // indexer q prep before the quantization (optional): q is the raw
+  // projection, made hadamard(rope(q)) with cos_sin row positions[t]
+  const float* cos_sin;      // [cs_rows, 64]; nullptr = no prep
+  int32_t cs_rows;
+  const int64_t* positions;
 };
 
 // Rows (token, head) 16 * block .. +15, 16 lanes per row.
@@ -264,13 +180,19 @@ __device__ __forceinline__ void q_quant_rows(const QQuantArgs& qa, int block) {
   uint4 wv = *reinterpret_cast<const uint4*>(src + 8 * ln);
   uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
   float v[8];
-  float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     v[2 * i] = __uint_as_float(ww[i] << 16);
     v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
-    amax = fmaxf(amax, fmaxf(fabsf(v[2 * i]), fabsf(v[2 * i + 1])));
   }
+  if (qa.cos_sin != nullptr) {  // uniform over the launch
+    const int64_t pos = qa.positions[t];
+    row_rope_neox64(v, (pos >= 0 && pos < qa.cs_rows) ? qa.cos_sin + pos * 64 : nullptr, ln);
+    row_hadamard(v, ln);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   amax = wave_max_xor(amax, 16);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
@@ -551,8 +473,12 @@ extern "C" int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint
                                        int64_t q_tok_stride, int64_t q_head_stride, const void* weights,
                                        int32_t weights_is_bf16, int64_t w_stride, int32_t heads, uint8_t* q_fp8,
                                        float* w_out, int8_t* q_digits, const int64_t* positions, int32_t window,
-                                       int32_t* lengths, void* stream) {
+                                       int32_t* lengths, const float* ln_w, const float* ln_b, float eps,
+                                       const float* cos_sin, int32_t cos_sin_rows, void* stream) {
   EKV_CHECK(num_tokens >= 0 && window >= 0, "bad sizes");
+  EKV_CHECK(cos_sin == nullptr || (ln_w && ln_b && cos_sin_rows >= 0 && aligned16(ln_w) && aligned16(ln_b) &&
+                                   aligned16(cos_sin)),
+            "the indexer prep needs 16-byte aligned ln_w, ln_b and cos_sin");
   if (num_tokens == 0) return 0;
   EKV_CHECK(dim == 512 || dim == 576, "latent dim must be 512 or 576");
   int rc = check_append(k, k_stride, 128, slot_mapping, kcache, k_page_stride);
@@ -566,7 +492,15 @@ extern "C" int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint
   a.k_rows = append_args(k, k_stride, num_tokens, slot_mapping, kcache, k_page_stride, k_num_pages);
   a.latent = append_args(latent, latent_stride, num_tokens, slot_mapping, cache, page_stride, num_pages);
   a.q = QQuantArgs{q, q_tok_stride, q_head_stride, weights, weights_is_bf16, w_stride, num_tokens, heads,
-                   q_fp8, w_out, q_digits};
+                   q_fp8, w_out, q_digits, cos_sin, cos_sin_rows, positions};
+  if (cos_sin != nullptr) {
+    a.k_rows.positions = positions;
+    a.k_rows.ln_w = ln_w;
+    a.k_rows.ln_b = ln_b;
+    a.k_rows.eps = eps;
+    a.k_rows.cos_sin = cos_sin;
+    a.k_rows.cs_rows = cos_sin_rows;
+  }
   a.positions = positions;
   a.window = window;
   a.lengths = lengths;

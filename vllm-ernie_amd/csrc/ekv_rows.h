@@ -32,7 +32,110 @@ struct AppendArgs {
   uint16_t* state;           // [num_state, 256, 2*D] bf16
   const int32_t* state_slot; // [B]
   int32_t num_state;
+  // indexer K prep before the quantization (D = 128 only; optional): rows
+  // are the raw projection, made hadamard(rope(k_norm(row))) with the
+  // LayerNorm (ln_w, ln_b, eps) and cos_sin row positions[t]
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  const float* cos_sin;      // [cs_rows, 64]; nullptr = no prep
+  int32_t cs_rows;
 };
+
+// ---------------------------------------------------------------------------
+// Indexer prep on a 128-wide row held by a 16-lane group: lane j holds
+// elements 8j .. 8j+7 (fp32 copies of bf16 values); cross-lane partners are
+// lane ^ 1, 2, 4, 8, inside the group.  k_norm LayerNorm, NeoX RoPE on dims
+// 0..63 and the Hadamard of Ernie5_5Indexer.forward.
+// ---------------------------------------------------------------------------
+// Sum of the row: per lane ((v0+v1)+(v2+v3))+((v4+v5)+(v6+v7)), then a
+// butterfly over the 16 lanes (partners 1, 2, 4, 8); every lane ends with the
+// same balanced-tree total.
+__device__ __forceinline__ float row_sum16(const float (&v)[8]) {
+  float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) s = s + __shfl_xor(s, off);
+  return s;
+}
+
+// y = bf16((d * rstd) * w + b), d = x - mean, over the 128-wide row.
+__device__ __forceinline__ void row_layer_norm(float (&v)[8], const float* w, const float* b, float eps, int j) {
+  const float mean = __fdiv_rn(row_sum16(v), 128.0f);
+  float d[8], sq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    d[e] = v[e] - mean;
+    sq[e] = d[e] * d[e];
+  }
+  const float var = __fdiv_rn(row_sum16(sq), 128.0f);
+  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
+  const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * j), w1 = *reinterpret_cast<const float4*>(w + 8 * j + 4);
+  const float4 b0 = *reinterpret_cast<const float4*>(b + 8 * j), b1 = *reinterpret_cast<const float4*>(b + 8 * j + 4);
+  const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16((d[e] * rstd) * ww[e] + bb[e]));
+}
+
+// NeoX rotation of dims 0..63 by (cos_i, sin_i) = (cs[i], cs[32 + i]): dim i
+// (lanes 0..3) pairs with dim i + 32 (lanes 4..7); cs == nullptr leaves the
+// row as it is.
+__device__ __forceinline__ void row_rope_neox64(float (&v)[8], const float* cs, int j) {
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], 4);
+  if (cs == nullptr || j >= 8) return;
+  const int i0 = 8 * (j & 3);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cs[i0 + e], sn = cs[32 + i0 + e];
+    const float r = (j < 4) ? (v[e] * c) - (p[e] * sn)   // x1 c - x2 s
+                            : (v[e] * c) + (p[e] * sn);  // x2 c + x1 s
+    v[e] = bf16_to_f32(f32_to_bf16(r));
+  }
+}
+
+// Orthonormal Walsh-Hadamard of the row: spans 1, 2, ..., 64 with
+// (a, b) -> (a + b, a - b), then times fl32(1/sqrt(128)), rounded to bf16.
+__device__ __forceinline__ void row_hadamard(float (&v)[8], int j) {
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if ((e & h) == 0) {
+        const float a = v[e], b = v[e + h];
+        v[e] = a + b;
+        v[e + h] = a - b;
+      }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    const bool lower = (j & m) == 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __shfl_xor(v[e], m);
+      v[e] = lower ? (v[e] + p) : (p - v[e]);
+    }
+  }
+  const float s = 0x1.6a09e6p-4f;  // fl32(1/sqrt(128))
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16(v[e] * s));
+}
+
+__device__ __forceinline__ void unpack_bf16x8(uint4 w, float (&v)[8]) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ww[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float (&v)[8]) {
+  uint32_t ww[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ww[i] = (__float_as_uint(v[2 * i]) >> 16) | (__float_as_uint(v[2 * i + 1]) & 0xffff0000u);
+  return make_uint4(ww[0], ww[1], ww[2], ww[3]);
+}
 
 // One row's fp8 image: lane `ln` of the row's kLanes lanes holds the 8-byte
 // pieces ln, ln + kLanes, ... of the D fp8 codes, plus the row's scale.
@@ -127,6 +230,17 @@ __device__ __forceinline__ void append_rows(const AppendArgs& a, int block) {
     const int64_t tt = t < a.num_tokens ? t : 0;
     load_bf16_row<D, kLanes>(a.rows + tt * a.row_stride, ln, raw[r]);
     slot[r] = a.slot_mapping[tt];
+    if constexpr (D == 128) {
+      if (a.cos_sin != nullptr) {  // uniform: every row of the launch or none
+        float v[8];
+        unpack_bf16x8(raw[r][0], v);
+        const int64_t pos = a.positions[tt];
+        row_layer_norm(v, a.ln_w, a.ln_b, a.eps, ln);
+        row_rope_neox64(v, (pos >= 0 && pos < a.cs_rows) ? a.cos_sin + pos * 64 : nullptr, ln);
+        row_hadamard(v, ln);
+        raw[r][0] = pack_bf16x8(v);
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < kSeq; ++r) {

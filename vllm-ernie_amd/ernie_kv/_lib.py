@@ -42,7 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_indexer_q_quant": (I32, [P, I64, I64, P, I32, I64, I32, I32, P, P, P, P]),
     "ekv_indexer_windowed_lengths": (I32, [P, I32, I32, P, P]),
     "ekv_dsa_decode_prologue": (I32, [P, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I32, P, I64, I64, P, I32,
-                                      I64, I32, P, P, P, P, I32, P, P]),
+                                      I64, I32, P, P, P, P, I32, P, P, P, F32, P, I32, P]),
     "ekv_indexer_score": (I32, [P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, P]),
     "ekv_topk_select": (I32, [P, I64, P, I32, I32, P, I64, I32, P]),
     "ekv_indexer_topk_workspace_size": (I64, [I32, I32]),

@@ -304,12 +304,24 @@ def dsa_decode_prologue(
     positions: torch.Tensor,
     window: int,
     lengths: torch.Tensor,
+    prep: tuple | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """One launch doing ``indexer_k_insert(k, slot_mapping, kcache)``,
     ``kv_append_quant(latent, slot_mapping, cache)``, ``indexer_q_quant(q,
     weights)`` (returned) and ``indexer_windowed_lengths(positions, window,
-    lengths)``."""
+    lengths)``.  With ``prep = (ln_w, ln_b, eps, cos_sin)``, q and k are the
+    raw indexer projections and ``indexer_prep`` runs on them first, in the
+    same launch."""
     _check_dev(k, kcache, latent, cache, slot_mapping, q, weights, positions, lengths)
+    ln_w = ln_b = cos_sin = None
+    eps = 0.0
+    if prep is not None:
+        ln_w, ln_b, eps, cos_sin = prep
+        _check_dev(ln_w, ln_b, cos_sin)
+        _need(ln_w.shape == (128,) and ln_b.shape == (128,) and ln_w.dtype == torch.float32
+              and ln_b.dtype == torch.float32 and ln_w.is_contiguous() and ln_b.is_contiguous(), "ln_w, ln_b fp32 [128]")
+        _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(),
+              "cos_sin fp32 [N, 64]")
     _bits16(k)
     _bits16(latent)
     _bits16(q)
@@ -332,7 +344,8 @@ def dsa_decode_prologue(
         latent.data_ptr(), _rs(latent), latent.shape[1], cache.data_ptr(), _rs(cache), cache.shape[0],
         slot_mapping.data_ptr(), T, q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
         int(weights.dtype == torch.bfloat16), _rs(weights), H, q_fp8.data_ptr(), w_out.data_ptr(), digits.data_ptr(),
-        positions.data_ptr(), int(window), lengths.data_ptr(), _stream(),
+        positions.data_ptr(), int(window), lengths.data_ptr(), _ptr(ln_w), _ptr(ln_b), float(eps), _ptr(cos_sin),
+        0 if cos_sin is None else cos_sin.shape[0], _stream(),
     )
     return q_fp8, w_out, digits
 
