@@ -1055,19 +1055,26 @@ struct SelectSmem {
   uint32_t pmin, pmax;  // range of the current pass's keys
 };
 
-// LDS histogram increment: one atomic for the whole wave when every active
-// lane falls in the same bin (runs of equal keys), else one per lane.
+// LDS histogram increment: the lanes sharing a bin with the first remaining
+// lane add with one atomic, twice; the others one atomic per lane.  Runs of
+// equal keys (ties) then cost one or two atomics per wave instead of one per
+// lane on the same address.
 __device__ __forceinline__ void hist_add_ties(uint32_t* hist, int bin) {
-  const uint64_t act = __ballot(bin >= 0);
-  if (act == 0) return;
-  const int leader = static_cast<int>(__builtin_ctzll(act));
-  const int lb = __builtin_amdgcn_readlane(bin, leader);
-  const uint64_t same = __ballot(bin == lb);
-  if (same == act) {
-    if ((threadIdx.x & 63) == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(act)));
-  } else if (bin >= 0) {
-    atomicAdd(&hist[bin], 1u);
+  const int lane = threadIdx.x & 63;
+  uint64_t act = __ballot(bin >= 0);
+  // two rounds: the lanes sharing the first remaining lane's bin add with
+  // one atomic (a tie group, most of a wave in tie-heavy rows, is taken in
+  // one of them); the rest add one each
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (act == 0) return;
+    const int leader = static_cast<int>(__builtin_ctzll(act));
+    const int lb = __builtin_amdgcn_readlane(bin, leader);
+    const uint64_t same = __ballot(bin == lb) & act;
+    if (lane == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(same)));
+    act &= ~same;
   }
+  if ((act >> lane) & 1u) atomicAdd(&hist[bin], 1u);
 }
 
 __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) {
