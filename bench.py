@@ -31,10 +31,10 @@ sys.path.insert(0, str(ROOT / "vllm-ernie_amd"))
 METRIC = "KV gather+decode HBM GB/s (% of 8 TB/s); decode tok/s/GPU at 128K ctx"
 HBM_PEAK_GBS = 8000.0
 # HBM bytes one filter_verify_kernel launch moves on the default workload:
-# rocprofv3 FETCH_SIZE (588.8 MB) + WRITE_SIZE (7.56 MB) per dispatch, each
+# rocprofv3 FETCH_SIZE (590.2 MB) + WRITE_SIZE (10.8 MB) per dispatch, each
 # scaled by what the counter reads for a 512 MiB device copy (x2.0 fetch, x1.0
 # write; run bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
-FILTER_TRAFFIC_BYTES = 588_804_045 + 7_559_136
+FILTER_TRAFFIC_BYTES = 590_228_753 + 10_803_104
 FP8_PEAK_TFLOPS = 5000.0
 
 
