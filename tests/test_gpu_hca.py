@@ -104,3 +104,53 @@ def test_hca_decode_indices(dev):
     ref, rl = oh.hca_decode_indices(positions, req, case.comp_bt, case.ring_pages, case.ring, width)
     assert np.array_equal(out.cpu().numpy(), ref)
     assert np.array_equal(lens.cpu().numpy(), rl)
+
+
+@pytest.mark.parametrize("dim", [576, 512])
+def test_hca_decode_end_to_end(dev, dim):
+    """Config-2 shape, scaled down: sequences of random context length are
+    prefilled through ekv_hca_write (latent rows, compressed spans, window
+    ring), then one decode token per sequence attends over its compressed
+    entries and window ring: the index rows (ekv_hca_decode_indices) match
+    the oracle exactly and the decode output is within the bf16 tolerance
+    (|out - ref| <= 2e-3 + 2e-2 |ref|) of the fp64 oracle."""
+    from ernie_kv import ops
+    from oracle import decode as od
+
+    rng = np.random.default_rng(50 + dim)
+    B, H, ring = 5, 64, 192
+    ctx = rng.integers(300, 2600, B)
+    ctx[0] = 128  # exactly one compressed entry and a full window
+    case = HcaCase(rng, dim, num_seqs=B, max_pos=int(ctx.max()) + 8, ring=ring)
+    gpu = {
+        "pool": torch.zeros((case.pages, paged.fp8_page_bytes(dim)), dtype=torch.uint8, device=dev),
+        "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
+    }
+    _run_call(dev, case, rng, [0] * B, ctx.tolist(), gpu, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool)
+
+    positions = (ctx - 1).astype(np.int64)
+    req = np.arange(B, dtype=np.int32)
+    width = int(ctx.max()) // 128 + 128
+    idx = torch.full((B, width), -9, dtype=torch.int32, device=dev)
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    ops.hca_decode_indices(to_dev(positions, dev), to_dev(req, dev), to_dev(case.comp_bt, dev),
+                           to_dev(case.ring_pages, dev), ring, idx, lens)
+    ref_idx, ref_len = oh.hca_decode_indices(positions, req, case.comp_bt, case.ring_pages, ring, width)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx) and np.array_equal(lens.cpu().numpy(), ref_len)
+
+    q = randn_bf16(rng, (B, H, dim))
+    sinks = rng.standard_normal(H).astype(np.float32)
+    scale = 256 ** -0.5
+    out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev)
+    ops.sparse_mla_decode(bf16_tensor(q, dev), gpu["pool"], idx, scale, out, lse, sinks=to_dev(sinks, dev),
+                          lengths=lens)
+    ref_o, ref_l = od.sparse_mla_decode(q, lambda sl: od.gather_rows_fp8(case.st.pool, sl, dim), ref_idx, scale,
+                                        512, sinks)
+    got = bf16_values(out).astype(np.float64)
+    err = np.abs(got - ref_o)
+    assert np.all(err <= 2e-3 + 2e-2 * np.abs(ref_o)), f"max err {err.max()}"
+    gl = lse.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(gl - ref_l) <= 2e-3 * np.maximum(1.0, np.abs(ref_l)))

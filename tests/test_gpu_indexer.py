@@ -305,6 +305,13 @@ def test_indexer_topk_long_rows_match_exact_path(dev, kind):
     assert int(ws[256: 256 + T * 4100 * 4].view(torch.int32).abs().sum()) == 0
 
 
+def test_indexer_topk_million_token_row(dev):
+    """A 1,048,576-token row (config 5's longest context) beside shorter
+    ones, through the fused filter: same top-2048 as the exact path."""
+    ws = _topk_vs_exact_path(dev, [1048576, 262144, 4096, 2049], 4, 1048576, "normal", seed=61)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+
+
 def test_indexer_topk_workspace_reused_across_shapes(dev):
     """One zero-filled workspace for calls of different row counts and
     lengths (the fused kernel's counters sit at fixed offsets and are left

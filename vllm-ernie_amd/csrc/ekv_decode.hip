@@ -64,7 +64,7 @@ struct DecodeArgs {
   float scale;              // softmax scale
   int32_t heads;
   int32_t per_split;        // entries per split (multiple of kTile, <= kMaxSplitEntries)
-  uint16_t* ws_o;           // [T, NS, H, 512] bf16, O / l of the split
+  float* ws_o;              // [T, NS, H, 512] fp32, O / l of the split
   float* ws_ml;             // [T, NS, H, 2] (m in log2 units, l)
   int32_t splits;
 };
@@ -77,10 +77,7 @@ struct DecodeSmem {
   static constexpr int kKRowB = BF16 ? 2 * (D + 8) : D + 8;  // K row stride (bytes)
   static constexpr int kImgB = kTile * kKRowB;
   static constexpr int kPRow = kTile + 8;   // bf16 P row stride (elements)
-  static constexpr int kORow = kDv + 8;     // bf16 output staging row stride
-  static constexpr int kImgRegion =
-      kKImages * kImgB > 64 * kORow * 2 ? kKImages * kImgB : 64 * kORow * 2;  // images, then output staging
-  __align__(16) uint8_t img[kImgRegion];
+  __align__(16) uint8_t img[kKImages * kImgB];
   uint16_t p[2][64 * kPRow];                // P of tiles t (written) and t-1 (read)
   float alpha[2][64];                       // rescale factor per head (valid when grow[.][head / 16])
   int32_t grow[2][kScoreWaves];
@@ -500,37 +497,28 @@ sparse_decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  // Epilogue: O / l as bf16 through LDS (over the K images), then out.
-  uint16_t* ostage = reinterpret_cast<uint16_t*>(sm.img);
+  // Epilogue: O / l of the split in fp32 (the combine sums the splits'
+  // partials, which may cancel, so they keep fp32 precision): each store
+  // instruction writes 16 consecutive channels (64 bytes) of one head.
+  const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
 #pragma unroll
   for (int hf = 0; hf < 4; ++hf) {
     if (hf >= hgroups) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float l = sm.row_l[16 * hf + 4 * g + i];
+      const int h = 16 * hf + 4 * g + i;
+      const float l = sm.row_l[h];
       const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
-      uint16_t* orow = &ostage[(16 * hf + 4 * g + i) * SM::kORow + 64 * wave + col];
+      float* orow = a.ws_o + (base + h) * kDv + 64 * wave + col;
 #pragma unroll
-      for (int nt = 0; nt < 4; nt += 2) {
-        const uint32_t pk = bf16x2_bits(o[hf][nt][i] * inv, o[hf][nt + 1][i] * inv);
-        orow[16 * nt] = static_cast<uint16_t>(pk & 0xffffu);
-        orow[16 * nt + 16] = static_cast<uint16_t>(pk >> 16);
-      }
+      for (int nt = 0; nt < 4; ++nt) orow[16 * nt] = o[hf][nt][i] * inv;
     }
-  }
-  __syncthreads();
-  const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
-  const int chunks = a.heads * (kDv / 8);
-  for (int c = tid; c < chunks; c += kThreads) {
-    const int h = c / (kDv / 8), part = c % (kDv / 8);
-    const uint4 v = *reinterpret_cast<const uint4*>(&ostage[h * SM::kORow + 8 * part]);
-    *reinterpret_cast<uint4*>(a.ws_o + (base + h) * kDv + 8 * part) = v;
   }
 }
 
 // 256 threads per (t, 4 heads): wave = head, lane = 8 output channels.
 __global__ void __launch_bounds__(256) decode_combine_kernel(
-    const uint16_t* ws_o, const float* ws_ml, int32_t splits, int32_t heads, const float* sinks,
+    const float* ws_o, const float* ws_ml, int32_t splits, int32_t heads, const float* sinks,
     uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, float* lse, int64_t lse_stride) {
   const int t = blockIdx.y;
   const int h = 4 * blockIdx.x + (threadIdx.x >> 6);
@@ -544,7 +532,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < splits; s0 += kBatch) {
     float ms[kBatch], ls[kBatch];
-    uint4 v[kBatch];
+    float4 v[kBatch][2];
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
       const bool ok = s0 + b < splits;
@@ -552,7 +540,8 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
       const float2 ml = *reinterpret_cast<const float2*>(ws_ml + row * 2);
       ms[b] = ok ? ml.x : -INFINITY;
       ls[b] = ml.y;
-      v[b] = *reinterpret_cast<const uint4*>(ws_o + row * kDv + 8 * lane);
+      v[b][0] = *reinterpret_cast<const float4*>(ws_o + row * kDv + 8 * lane);
+      v[b][1] = *reinterpret_cast<const float4*>(ws_o + row * kDv + 8 * lane + 4);
     }
     float mb = M;
 #pragma unroll
@@ -570,12 +559,9 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
       if (ms[b] == -INFINITY) continue;
       const float f = exp2f(ms[b] - M) * ls[b];
       L += f;
-      const uint32_t w[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+      const float x[8] = {v[b][0].x, v[b][0].y, v[b][0].z, v[b][0].w, v[b][1].x, v[b][1].y, v[b][1].z, v[b][1].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * f;
-        acc[2 * i + 1] += bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * f;
-      }
+      for (int i = 0; i < 8; ++i) acc[i] += x[i] * f;
     }
   }
   float den = L;
@@ -617,7 +603,7 @@ static int decode_splits(int32_t num_tokens, int32_t width) {
 extern "C" int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int32_t heads, int32_t width) {
   if (num_tokens <= 0 || heads <= 0) return 0;
   const int64_t n = static_cast<int64_t>(num_tokens) * decode_splits(num_tokens, width) * heads;
-  return n * kDv * 2 + n * 2 * 4 + 256;
+  return n * kDv * 4 + n * 2 * 4 + 256;
 }
 
 template <int D, bool BF16>
@@ -659,8 +645,8 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   const int splits = decode_splits(num_tokens, width);
   const int tiles = (width + kTile - 1) / kTile;
   const int per_split = ((tiles + splits - 1) / splits) * kTile;
-  uint16_t* ws_o = static_cast<uint16_t*>(workspace);
-  float* ws_ml = reinterpret_cast<float*>(ws_o + static_cast<int64_t>(num_tokens) * splits * heads * kDv);
+  float* ws_o = static_cast<float*>(workspace);
+  float* ws_ml = ws_o + static_cast<int64_t>(num_tokens) * splits * heads * kDv;
   DecodeArgs a{q, q_tok_stride, q_head_stride, cache, page_stride, num_pages * kPageTokens, indices, idx_stride,
                width, lengths, block_table, bt_stride, req_ids, scale, heads, per_split, ws_o, ws_ml, splits};
   hipStream_t s = static_cast<hipStream_t>(stream);
