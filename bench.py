@@ -46,8 +46,11 @@ def parse():
     p.add_argument("--batch", type=int, default=32)
     p.add_argument("--ctx", type=int, default=131072)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-hca", action="store_true", help="skip the HCA chunked-prefill write measurement")
+    p.add_argument("--no-hca", action="store_true",
+                   help="skip the HCA measurements (chunked-prefill write, decode step)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--only", choices=["hca_write", "hca_decode"], default=None,
+                   help="run only this HCA measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -98,8 +101,7 @@ def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
     inv = 2.5e6 ** (-torch.arange(32, device=dev, dtype=torch.float64) * 2.0 / 64)
     ang = torch.arange(ctx, device=dev, dtype=torch.float64)[:, None] * inv[None, :]
     st["rope"] = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).contiguous()
-    need = ops._lib.load().ekv_sparse_mla_decode_workspace_size(B, 64, 2176)
-    st["dec_ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
+    st["dec_ws"] = ops.decode_workspace(B, 64, 2176, dev)
     st["idx_ws"] = ops.indexer_topk_workspace(B, ctx, dev)
     return st
 
@@ -217,6 +219,100 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
     }
 
 
+def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx_hi: int = 131072, D: int = 576,
+                     ring: int = 128):
+    """HCA-layer decode step state: B sequences with seeded contexts in
+    [ctx_lo, ctx_hi), their compressed entries and 128-row window rings as
+    random fp8 rows (fp32 scale 2^-8) in permuted pages, one new token each.
+    Synthetic inputs."""
+    dev = torch.device("cuda:0")
+    gc = torch.Generator().manual_seed(seed + 2)
+    gd = torch.Generator(device=dev).manual_seed(seed + 2)
+    ctx = torch.randint(ctx_lo, ctx_hi, (B,), generator=gc).to(torch.int64)
+    spans = ctx_hi // 128 + 1
+    comp_pages = (spans + 63) // 64
+    ring_pp = (ring + 63) // 64
+    pages = B * (comp_pages + ring_pp + 1)
+    perm = torch.randperm(pages, generator=gc).to(torch.int32)
+    comp_bt = perm[: B * comp_pages].view(B, comp_pages).to(dev)
+    ring_pages = perm[B * comp_pages: B * (comp_pages + ring_pp)].view(B, ring_pp).to(dev)
+    latent_page = perm[B * (comp_pages + ring_pp):].to(torch.int64)
+    positions = ctx - 1  # the new token; the context after its append is ctx
+    slots = (latent_page * 64 + positions % 64).to(dev)
+    codes = torch.randint(0, 256, (pages, 64 * D), device=dev, dtype=torch.uint8, generator=gd)
+    codes -= ((codes & 0x7F) == 0x7F).to(torch.uint8)  # no NaN codes
+    scales = torch.full((pages, 64), 2.0 ** -8, device=dev, dtype=torch.float32)
+    ang = (torch.arange(spans, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    width = (ctx_hi // 128) + ring
+    rnd = lambda *s: torch.randn(*s, device=dev, generator=gd).to(torch.bfloat16)  # noqa: E731
+    st = dict(
+        B=B, D=D, ring=ring, ctx=ctx, width=width,
+        pool=torch.cat([codes, scales.view(torch.uint8)], dim=1).contiguous(),
+        latent=rnd(B, D), kv_score=rnd(B, 2 * D), state=rnd(B + 2, 256, 2 * D),
+        state_slot=torch.randperm(B + 2, generator=gc)[:B].to(torch.int32).to(dev),
+        ape=(torch.randn(128, D, device=dev, generator=gd) * 0.5).contiguous(),
+        norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=gd)).contiguous(),
+        cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(dev),
+        comp_bt=comp_bt, ring_pages=ring_pages, slots=slots, positions=positions.to(dev),
+        token_seq=torch.arange(B, dtype=torch.int32, device=dev),
+        qsl=torch.arange(B + 1, dtype=torch.int32, device=dev),
+        req=torch.arange(B, dtype=torch.int32, device=dev),
+        q=rnd(B, 64, D), sinks=torch.randn(64, device=dev, generator=gd),
+        idx=torch.empty((B, width), dtype=torch.int32, device=dev),
+        lens=torch.empty(B, dtype=torch.int32, device=dev),
+        out=torch.empty((B, 64, 512), dtype=torch.bfloat16, device=dev),
+        lse=torch.empty((B, 64), dtype=torch.float32, device=dev),
+    )
+    st["dec_ws"] = ops.decode_workspace(B, 64, width, dev)
+    return st
+
+
+def hca_decode_step(ops, st):
+    """One HCA decode step: the new token's write (latent row, window ring,
+    state ring; the spans it completes are compressed), its index rows
+    (compressed entries, then the window), then the 64-head decode."""
+    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], 1,
+                  st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
+                  st["ring_pages"], st["ring"], st["pool"])
+    ops.hca_decode_indices(st["positions"], st["req"], st["comp_bt"], st["ring_pages"], st["ring"], st["idx"],
+                           st["lens"])
+    ops.sparse_mla_decode(st["q"], st["pool"], st["idx"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
+                          lengths=st["lens"], workspace=st["dec_ws"])
+
+
+def measure_hca_decode(torch, ops, seed: int, reps: int = 50) -> dict:
+    st = build_hca_decode(torch, ops, seed)
+    for _ in range(3):
+        hca_decode_step(ops, st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        hca_decode_step(ops, st)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    B, D = st["B"], st["D"]
+    ctx = st["ctx"]
+    rows = int((ctx // 128 + torch.clamp(ctx, max=st["ring"])).sum())
+    gather = rows * (D + 4)
+    q_out = B * 64 * D * 2 + B * 64 * 512 * 2 + B * 64 * 4
+    append = B * (D * 2 + 2 * (D + 4) + 2 * D * 2 * 2)  # latent in, row + ring row out, kv_score in + state out
+    total = gather + q_out + append
+    return {
+        "workload": f"hca_decode_b{B}_ctx8192-131072",
+        "kernels": "hca_compress_kernel<576> (spans completed by the new token) + hca_append_kernel<576> + "
+                   "hca_decode_indices_kernel + sparse_decode_kernel<576> + decode_combine_kernel",
+        "ms": round(ms, 4),
+        "rows_per_step": rows,
+        "bytes": {"gather": gather, "q_out": q_out, "append": append, "total": total},
+        "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
+        "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "tok_per_s": round(B / (ms * 1e-3), 1),
+    }
+
+
 def dsa_bytes(B: int, ctx: int) -> dict:
     n = max(ctx - 128, 0)
     k_read = B * n * 132
@@ -278,6 +374,10 @@ def main():
     from ernie_kv import ops
 
     torch.cuda.init()
+    if args.only is not None:
+        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode}[args.only]
+        print(json.dumps(leg(torch, ops, args.seed)), flush=True)
+        return
     st = build_dsa_decode(torch, ops, args.batch, args.ctx, args.seed)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device="cuda")
@@ -346,6 +446,8 @@ def main():
         del st
         torch.cuda.empty_cache()
         line["hca_write"] = measure_hca_write(torch, ops, args.seed)
+        torch.cuda.empty_cache()
+        line["hca_decode"] = measure_hca_decode(torch, ops, args.seed)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.batch, args.ctx, args.seed)
     print(json.dumps(line), flush=True)

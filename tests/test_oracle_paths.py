@@ -410,6 +410,35 @@ def test_decode_matches_softmax_with_sink_logit():
         np.testing.assert_allclose(lse[t], np.log(np.exp(s).sum(1)), rtol=1e-12)
 
 
+def test_decode_p_bound_covers_bf16_weights():
+    """The p_bound output bounds what rounding the softmax weights to bf16
+    (under any reference max at or above the row max, as the kernels'
+    online softmax does) moves the output; a bound of a quarter of it is
+    exceeded on the same rows (it is not loose by orders of magnitude)."""
+    import torch
+
+    rng = np.random.default_rng(31)
+    T, H, D = 6, 16, 576
+    q = rng.standard_normal((T, H, D))
+    rows = rng.standard_normal((300, D))
+    idx = rng.integers(0, 300, (T, 12)).astype(np.int32)
+    sinks = rng.standard_normal(H)
+    out, _, bound = od.sparse_mla_decode(q, lambda s: rows[s], idx, 0.0625, 512, sinks, p_bound=True)
+    worst = 0.0
+    for t in range(T):
+        kv = rows[idx[t]]
+        s = q[t] @ kv.T * 0.0625
+        for shift in (0.0, 3.7, 7.9):  # reference max above the row max
+            m = np.maximum(s.max(1), sinks) + shift
+            e = np.exp(s - m[:, None])
+            eb = torch.tensor(e).to(torch.bfloat16).double().numpy()
+            den = e.sum(1) + np.exp(sinks - m)
+            err = np.abs((eb @ kv[:, :512]) / den[:, None] - out[t])
+            assert np.all(err <= bound[t] * (1 + 1e-9))
+            worst = max(worst, float((err / bound[t]).max()))
+    assert worst > 0.25
+
+
 def test_decode_empty_row():
     out, lse = od.sparse_mla_decode(np.ones((1, 16, 576)), lambda s: None, np.full((1, 4), -1), 0.1, 512,
                                     np.zeros(16))

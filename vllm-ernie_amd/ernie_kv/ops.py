@@ -475,6 +475,13 @@ def indexer_topk(
 
 
 # --------------------------------------------------------------------------- decode
+def decode_workspace(num_tokens: int, heads: int, width: int, device) -> torch.Tensor:
+    """Workspace for ``sparse_mla_decode`` calls up to this shape (the split
+    partials: O / l and (m, l) in fp32 per row, split and head)."""
+    need = _lib.load().ekv_sparse_mla_decode_workspace_size(num_tokens, heads, width)
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+
 def sparse_mla_decode(
     q: torch.Tensor,
     cache: torch.Tensor,
@@ -508,7 +515,7 @@ def sparse_mla_decode(
         _need(sinks.dtype == torch.float32 and sinks.numel() >= H, "sinks fp32 [H]")
     need = _lib.load().ekv_sparse_mla_decode_workspace_size(T, H, idx.shape[1])
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        workspace = decode_workspace(T, H, idx.shape[1], q.device)
     _lib.call(
         "ekv_sparse_mla_decode", q.data_ptr(), _rs(q), q.stride(1), T, H, D, cache.data_ptr(),
         int(cache_bf16), page_stride, num_pages, idx.data_ptr(), _rs(idx), idx.shape[1], _ptr(lengths),
