@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-hca", action="store_true",
                    help="skip the HCA measurements (chunked-prefill write, decode step)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--only", choices=["hca_write", "hca_decode"], default=None,
+    p.add_argument("--no-mtp", action="store_true", help="skip the multi-token-prediction (1M-context) measurement")
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp"], default=None,
                    help="run only this HCA measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
@@ -57,13 +58,23 @@ def parse():
     return p.parse_args()
 
 
-def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
-    """Synthetic DSA-layer decode state at batch B x context ctx."""
+def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, spike_frac: float = 0.05):
+    """Synthetic DSA-layer decode state: sequence s holds ctxs[s] tokens, the
+    last rows_per_seq of them new this step (one query row each: the token
+    and its draft tokens), in permuted pages."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
-    pages_per_seq = ctx // 64
-    num_pages = B * pages_per_seq
-    block_table = torch.randperm(num_pages, device=dev, generator=g).to(torch.int32).view(B, pages_per_seq)
+    S, R = len(ctxs), rows_per_seq
+    ctx = max(ctxs)
+    B = S * R  # query rows
+    pps = [(c + 63) // 64 for c in ctxs]
+    num_pages = sum(pps)
+    perm = torch.randperm(num_pages, device=dev, generator=g).to(torch.int32)
+    block_table = torch.full((S, max(pps)), -1, dtype=torch.int32, device=dev)
+    o = 0
+    for s, n in enumerate(pps):
+        block_table[s, :n] = perm[o:o + n]
+        o += n
 
     def random_fp8_pages(dim: int, scale_exp: int):
         pages = torch.randint(0, 256, (num_pages, 64 * dim), device=dev, dtype=torch.uint8, generator=g)
@@ -72,23 +83,25 @@ def build_dsa_decode(torch, ops, B: int, ctx: int, seed: int):
         return torch.cat([pages, scales.view(torch.uint8)], dim=1).contiguous()
 
     kcache = random_fp8_pages(128, -8)
-    # 5% of tokens hold one identical "spike" key row: exact score ties
-    spike = kcache[0, :128].clone()
-    mask = torch.rand(num_pages, 64, device=dev, generator=g) < 0.05
-    vals = kcache[:, : 64 * 128].unflatten(1, (64, 128))
-    vals[mask] = spike
+    if spike_frac > 0:
+        # a fraction of tokens hold one identical "spike" key row: exact score ties
+        spike = kcache[0, :128].clone()
+        mask = torch.rand(num_pages, 64, device=dev, generator=g) < spike_frac
+        vals = kcache[:, : 64 * 128].unflatten(1, (64, 128))
+        vals[mask] = spike
     latent = random_fp8_pages(576, -8)
-    positions = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
-    req_ids = torch.arange(B, dtype=torch.int32, device=dev)
+    ctx_t = torch.tensor(ctxs, dtype=torch.int64, device=dev)
+    req_ids = torch.arange(S, dtype=torch.int32, device=dev).repeat_interleave(R)
+    positions = (ctx_t.repeat_interleave(R) - R + torch.arange(R, device=dev).repeat(S)).contiguous()
     pos = positions
-    slots = (block_table[torch.arange(B, device=dev), (pos // 64)].to(torch.int64) * 64 + pos % 64).contiguous()
+    slots = (block_table[req_ids.long(), (pos // 64)].to(torch.int64) * 64 + pos % 64).contiguous()
     rnd = lambda *s: torch.randn(*s, device=dev, generator=g).to(torch.bfloat16)  # noqa: E731
     st = dict(
-        B=B, ctx=ctx, block_table=block_table, kcache=kcache, latent=latent, positions=positions,
+        B=B, S=S, R=R, ctxs=list(ctxs), ctx=ctx, block_table=block_table, kcache=kcache, latent=latent,
+        positions=positions,
         req_ids=req_ids, slots=slots, k_new=rnd(B, 128), latent_new=rnd(B, 576), q_idx=rnd(B, 64, 128),
         w_idx=rnd(B, 64), q=rnd(B, 64, 576), sinks=torch.randn(64, device=dev, generator=g),
         lengths=torch.empty(B, dtype=torch.int32, device=dev),
-        scores=torch.empty((B, ctx), dtype=torch.float32, device=dev),
         topk=torch.empty((B, 2048), dtype=torch.int32, device=dev),
         merged=torch.empty((B, 2176), dtype=torch.int32, device=dev),
         out=torch.empty((B, 64, 512), dtype=torch.bfloat16, device=dev),
@@ -220,15 +233,23 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
 
 
 def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx_hi: int = 131072, D: int = 576,
-                     ring: int = 128):
+                     ring: int = 128, ctxs: list | None = None, rows_per_seq: int = 1):
     """HCA-layer decode step state: B sequences with seeded contexts in
-    [ctx_lo, ctx_hi), their compressed entries and 128-row window rings as
-    random fp8 rows (fp32 scale 2^-8) in permuted pages, one new token each.
-    Synthetic inputs."""
+    [ctx_lo, ctx_hi) (or the given ctxs), their compressed entries and window
+    rings as random fp8 rows (fp32 scale 2^-8) in permuted pages, and
+    rows_per_seq new tokens each (the token and its drafts, one query row
+    each).  Synthetic inputs."""
     dev = torch.device("cuda:0")
     gc = torch.Generator().manual_seed(seed + 2)
     gd = torch.Generator(device=dev).manual_seed(seed + 2)
-    ctx = torch.randint(ctx_lo, ctx_hi, (B,), generator=gc).to(torch.int64)
+    if ctxs is not None:
+        B = len(ctxs)
+        ctx = torch.tensor(ctxs, dtype=torch.int64)
+        ctx_hi = int(ctx.max()) + 1
+    else:
+        ctx = torch.randint(ctx_lo, ctx_hi, (B,), generator=gc).to(torch.int64)
+    R = rows_per_seq
+    T = B * R
     spans = ctx_hi // 128 + 1
     comp_pages = (spans + 63) // 64
     ring_pp = (ring + 63) // 64
@@ -237,8 +258,9 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
     comp_bt = perm[: B * comp_pages].view(B, comp_pages).to(dev)
     ring_pages = perm[B * comp_pages: B * (comp_pages + ring_pp)].view(B, ring_pp).to(dev)
     latent_page = perm[B * (comp_pages + ring_pp):].to(torch.int64)
-    positions = ctx - 1  # the new token; the context after its append is ctx
-    slots = (latent_page * 64 + positions % 64).to(dev)
+    # the new tokens: the last R positions of each context
+    positions = ctx.repeat_interleave(R) - R + torch.arange(R).repeat(B)
+    slots = (latent_page.repeat_interleave(R) * 64 + positions % 64).to(dev)
     codes = torch.randint(0, 256, (pages, 64 * D), device=dev, dtype=torch.uint8, generator=gd)
     codes -= ((codes & 0x7F) == 0x7F).to(torch.uint8)  # no NaN codes
     scales = torch.full((pages, 64), 2.0 ** -8, device=dev, dtype=torch.float32)
@@ -247,24 +269,24 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
     width = (ctx_hi // 128) + ring
     rnd = lambda *s: torch.randn(*s, device=dev, generator=gd).to(torch.bfloat16)  # noqa: E731
     st = dict(
-        B=B, D=D, ring=ring, ctx=ctx, width=width,
+        B=B, T=T, R=R, D=D, ring=ring, ctx=ctx, width=width,
         pool=torch.cat([codes, scales.view(torch.uint8)], dim=1).contiguous(),
-        latent=rnd(B, D), kv_score=rnd(B, 2 * D), state=rnd(B + 2, 256, 2 * D),
+        latent=rnd(T, D), kv_score=rnd(T, 2 * D), state=rnd(B + 2, 256, 2 * D),
         state_slot=torch.randperm(B + 2, generator=gc)[:B].to(torch.int32).to(dev),
         ape=(torch.randn(128, D, device=dev, generator=gd) * 0.5).contiguous(),
         norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=gd)).contiguous(),
         cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(dev),
         comp_bt=comp_bt, ring_pages=ring_pages, slots=slots, positions=positions.to(dev),
-        token_seq=torch.arange(B, dtype=torch.int32, device=dev),
-        qsl=torch.arange(B + 1, dtype=torch.int32, device=dev),
-        req=torch.arange(B, dtype=torch.int32, device=dev),
-        q=rnd(B, 64, D), sinks=torch.randn(64, device=dev, generator=gd),
-        idx=torch.empty((B, width), dtype=torch.int32, device=dev),
-        lens=torch.empty(B, dtype=torch.int32, device=dev),
-        out=torch.empty((B, 64, 512), dtype=torch.bfloat16, device=dev),
-        lse=torch.empty((B, 64), dtype=torch.float32, device=dev),
+        token_seq=torch.arange(B, dtype=torch.int32, device=dev).repeat_interleave(R),
+        qsl=(torch.arange(B + 1, dtype=torch.int32) * R).to(dev),
+        req=torch.arange(B, dtype=torch.int32, device=dev).repeat_interleave(R),
+        q=rnd(T, 64, D), sinks=torch.randn(64, device=dev, generator=gd),
+        idx=torch.empty((T, width), dtype=torch.int32, device=dev),
+        lens=torch.empty(T, dtype=torch.int32, device=dev),
+        out=torch.empty((T, 64, 512), dtype=torch.bfloat16, device=dev),
+        lse=torch.empty((T, 64), dtype=torch.float32, device=dev),
     )
-    st["dec_ws"] = ops.decode_workspace(B, 64, width, dev)
+    st["dec_ws"] = ops.decode_workspace(T, 64, width, dev)
     return st
 
 
@@ -272,7 +294,7 @@ def hca_decode_step(ops, st):
     """One HCA decode step: the new token's write (latent row, window ring,
     state ring; the spans it completes are compressed), its index rows
     (compressed entries, then the window), then the 64-head decode."""
-    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], 1,
+    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["R"],
                   st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
                   st["ring_pages"], st["ring"], st["pool"])
     ops.hca_decode_indices(st["positions"], st["req"], st["comp_bt"], st["ring_pages"], st["ring"], st["idx"],
@@ -281,35 +303,99 @@ def hca_decode_step(ops, st):
                           lengths=st["lens"], workspace=st["dec_ws"])
 
 
-def measure_hca_decode(torch, ops, seed: int, reps: int = 50) -> dict:
-    st = build_hca_decode(torch, ops, seed)
-    for _ in range(3):
-        hca_decode_step(ops, st)
+def time_ms(torch, step, reps: int, warmup: int = 3) -> float:
+    """Average milliseconds of step() over reps calls (events on the current stream)."""
+    for _ in range(warmup):
+        step()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
-        hca_decode_step(ops, st)
+        step()
     b.record()
     torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
-    B, D = st["B"], st["D"]
-    ctx = st["ctx"]
-    rows = int((ctx // 128 + torch.clamp(ctx, max=st["ring"])).sum())
+    return a.elapsed_time(b) / reps
+
+
+def hca_decode_bytes(st) -> dict:
+    """Algorithmic bytes of one HCA decode step: each query row's compressed
+    entries and window rows (580 B each), q / out / lse, and the new tokens'
+    appends (latent in, row and ring row out, kv || score in, state row out)."""
+    D, T = st["D"], st["T"]
+    seq = st["positions"].cpu() + 1
+    rows = int((seq // 128 + seq.clamp(max=128)).sum())
     gather = rows * (D + 4)
-    q_out = B * 64 * D * 2 + B * 64 * 512 * 2 + B * 64 * 4
-    append = B * (D * 2 + 2 * (D + 4) + 2 * D * 2 * 2)  # latent in, row + ring row out, kv_score in + state out
-    total = gather + q_out + append
+    q_out = T * 64 * D * 2 + T * 64 * 512 * 2 + T * 64 * 4
+    append = T * (D * 2 + 2 * (D + 4) + 2 * D * 2 * 2)
+    return {"rows": rows, "gather": gather, "q_out": q_out, "append": append, "total": gather + q_out + append}
+
+
+def measure_hca_decode(torch, ops, seed: int, reps: int = 50) -> dict:
+    st = build_hca_decode(torch, ops, seed)
+    ms = time_ms(torch, lambda: hca_decode_step(ops, st), reps)
+    by = hca_decode_bytes(st)
     return {
-        "workload": f"hca_decode_b{B}_ctx8192-131072",
+        "workload": f"hca_decode_b{st['B']}_ctx8192-131072",
         "kernels": "hca_compress_kernel<576> (spans completed by the new token) + hca_append_kernel<576> + "
                    "hca_decode_indices_kernel + sparse_decode_kernel<576> + decode_combine_kernel",
         "ms": round(ms, 4),
-        "rows_per_step": rows,
-        "bytes": {"gather": gather, "q_out": q_out, "append": append, "total": total},
-        "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
-        "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "tok_per_s": round(B / (ms * 1e-3), 1),
+        "rows_per_step": by.pop("rows"),
+        "bytes": by,
+        "GB/s": round(by["total"] / (ms * 1e-3) / 1e9, 1),
+        "frac": round(by["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "tok_per_s": round(st["T"] / (ms * 1e-3), 1),
+    }
+
+
+MTP_CTXS = [262144] * 8 + [1048576]
+MTP_ROWS = 3  # the token and its 2 draft tokens
+MTP_LAYERS = {"dsa": 6, "hca": 37}
+MTP_ACCEPT = 0.7
+
+
+def measure_mtp(torch, ops, seed: int, reps: int = 10) -> dict:
+    """Multi-token-prediction decode at 8 x 262,144 + 1 x 1,048,576 contexts,
+    3 query rows per sequence: one DSA layer step and one HCA layer step
+    measured, and the model step composed from them (6 DSA + 37 HCA layers)."""
+    S, R = len(MTP_CTXS), MTP_ROWS
+    st = build_dsa_decode(torch, ops, MTP_CTXS, seed, rows_per_seq=R, spike_frac=0.0)
+    dsa_ms = time_ms(torch, lambda: dsa_step(ops, st), reps)
+    pos = st["positions"].cpu()
+    n_row = (pos + 1 - 128).clamp(min=0)
+    k_once = sum(max(c - 128, 0) for c in MTP_CTXS) * 132  # each sequence's keys read once
+    k_rows = int(n_row.sum()) * 132                       # read per query row, as this build does
+    gather = int((n_row.clamp(max=2048) + (pos + 1).clamp(max=128)).sum()) * 580
+    T = S * R
+    qo = T * (64 * 576 * 2 + 64 * 512 * 2 + 64 * 128 * 2 + 64 * 2 + 64 * 4)
+    del st
+    torch.cuda.empty_cache()
+    # the window ring holds the 128-row window of every query row (128 + R - 1
+    # rows), in whole 64-row pages
+    sh = build_hca_decode(torch, ops, seed, ctxs=MTP_CTXS, rows_per_seq=R, ring=64 * ((128 + R - 1 + 63) // 64))
+    hca_ms = time_ms(torch, lambda: hca_decode_step(ops, sh), reps)
+    hb = hca_decode_bytes(sh)
+    del sh
+    torch.cuda.empty_cache()
+    step_ms = MTP_LAYERS["dsa"] * dsa_ms + MTP_LAYERS["hca"] * hca_ms
+    tok_step = S * sum(MTP_ACCEPT ** i for i in range(R))  # expected accepted tokens per step
+    dsa_total = k_once + gather + qo
+    return {
+        "workload": f"mtp_decode_{S}seq_{R}rows_8x262144_1x1048576",
+        "dsa_layer": {
+            "ms": round(dsa_ms, 4),
+            "bytes": {"indexer_k_once": k_once, "indexer_k_per_row": k_rows, "gather": gather, "q_out": qo,
+                      "total": dsa_total},
+            "GB/s": round(dsa_total / (dsa_ms * 1e-3) / 1e9, 1),
+            "GB/s_per_row_k": round((k_rows + gather + qo) / (dsa_ms * 1e-3) / 1e9, 1),
+        },
+        "hca_layer": {
+            "ms": round(hca_ms, 4), "rows_per_step": hb.pop("rows"), "bytes": hb,
+            "GB/s": round(hb["total"] / (hca_ms * 1e-3) / 1e9, 1),
+        },
+        "model_step_ms": round(step_ms, 3),
+        "model_step": "composed: 6 x dsa_layer.ms + 37 x hca_layer.ms (the attention KV path only)",
+        "query_rows_per_s": round(T / (step_ms * 1e-3), 1),
+        "tok_per_s_accept_0.7": round(tok_step / (step_ms * 1e-3), 1),
     }
 
 
@@ -375,10 +461,10 @@ def main():
 
     torch.cuda.init()
     if args.only is not None:
-        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode}[args.only]
+        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp}[args.only]
         print(json.dumps(leg(torch, ops, args.seed)), flush=True)
         return
-    st = build_dsa_decode(torch, ops, args.batch, args.ctx, args.seed)
+    st = build_dsa_decode(torch, ops, [args.ctx] * args.batch, args.seed)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -448,6 +534,9 @@ def main():
         line["hca_write"] = measure_hca_write(torch, ops, args.seed)
         torch.cuda.empty_cache()
         line["hca_decode"] = measure_hca_decode(torch, ops, args.seed)
+    if not args.no_mtp:
+        torch.cuda.empty_cache()
+        line["mtp"] = measure_mtp(torch, ops, args.seed)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.batch, args.ctx, args.seed)
     print(json.dumps(line), flush=True)

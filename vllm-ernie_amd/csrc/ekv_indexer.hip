@@ -228,6 +228,8 @@ struct FilterArgs {
   int32_t k;
   uint16_t* upper;           // [T, max_len] U_s rounded up to bf16
   uint32_t* hist;            // [T, kHistBins] counts of L_s key prefixes
+  int32_t rows;              // T (filter_kernel: 1-D grid of groups x T workgroups)
+  int32_t groups;            // workgroup slots per row, a multiple of 8
 };
 
 
@@ -280,9 +282,11 @@ __device__ __forceinline__ int find_bin(const uint32_t* hist, int nb, int remain
   return bin;
 }
 
-// Pages of each wave: the row's 64-token pages are split into contiguous
-// ranges, one per wave of the row (4 waves per workgroup, `groups`
-// workgroups per row), so workgroup x owns pages [4x, 4x + 4) * per_wave.
+// Pages of each wave: every row's 64-token pages are split into contiguous
+// ranges of the same length, one per wave (4 waves per workgroup), so
+// workgroup x of a row owns pages [4x, 4x + 4) * per_wave; per_wave is set by
+// the batch's longest row over `groups` workgroups, so a longer row uses
+// proportionally more workgroups and every wave streams about as many pages.
 __host__ __device__ inline int filter_per_wave(int n, int groups) {
   const int npages = (n + kPageTokens - 1) / kPageTokens;
   return (npages + 4 * groups - 1) / (4 * groups);
@@ -413,12 +417,28 @@ constexpr int kFilterStage = 32;  // pages of upper bounds staged per wave
 __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ __align__(16) uint16_t s_up[4][kFilterStage * kPageTokens];
+  __shared__ int s_maxn;
   const int tid = threadIdx.x;
-  const int t = blockIdx.y;
+  // Workgroup b runs on XCD b % 8 (round-robin dispatch).  Slot b / 8 of an
+  // XCD takes segment x = 8 (slot / T) + b % 8 of row slot % T: segments are
+  // spread over the XCDs, and the rows of one segment run back to back on one
+  // XCD, so rows of one sequence (draft-token rows) read the same pages there
+  // at about the same time and share them through its L2.
+  const int b = static_cast<int>(blockIdx.x);
+  const int slot = b >> 3;
+  const int x = 8 * (slot / a.rows) + (b & 7), t = slot % a.rows;
+  if (x >= a.groups) return;
+  if (tid == 0) s_maxn = 0;
+  __syncthreads();
+  int mx = 0;
+  for (int i = tid; i < a.rows; i += 256) mx = max(mx, min(a.lengths[i], a.max_len));
+  for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  if ((tid & 63) == 0) atomicMax(&s_maxn, mx);
+  __syncthreads();
   const int n = min(a.lengths[t], a.max_len);
   const int npages = (n + kPageTokens - 1) / kPageTokens;
-  const int per_wave = filter_per_wave(n, static_cast<int>(gridDim.x));
-  if (4 * static_cast<int>(blockIdx.x) * per_wave >= npages || n <= a.k) return;  // rows with n <= k need no filtering
+  const int per_wave = filter_per_wave(s_maxn, a.groups);
+  if (4 * x * per_wave >= npages || n <= a.k) return;  // rows with n <= k need no filtering
   for (int i = tid; i < kHistBins; i += 256) s_hist[i] = 0;
 
   const int lane = tid & 63, wave = tid >> 6;
@@ -429,7 +449,7 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   load_filter_operands(a, t, g, col, qa, wv, ebound);
   __syncthreads();
 
-  const int wr = __builtin_amdgcn_readfirstlane(4 * static_cast<int>(blockIdx.x) + wave);  // wave of the row
+  const int wr = __builtin_amdgcn_readfirstlane(4 * x + wave);  // wave of the row
   const int p_begin = min(wr * per_wave, npages), p_end = min(p_begin + per_wave, npages);
   uint16_t* up_row = a.upper + static_cast<int64_t>(t) * a.max_len;
   uint16_t* stage = s_up[wave];
@@ -1428,6 +1448,7 @@ int num_chunks(int32_t max_len) { return max_len > 0 ? (max_len + kChunk - 1) / 
 // Workgroups the filter targets in all: about three per CU, each wave
 // streaming many pages.
 constexpr int64_t kFilterTargetGroups = 768;
+constexpr int64_t kFilterMaxWavePages = 64;
 
 // Count slots [T, groups] of either path: chunks per row, or segments (at most
 // ceil(kFilterTargetGroups / T) per row).
@@ -1530,8 +1551,13 @@ bool plan_fused(int64_t T, int32_t max_len, int64_t pages, int cus, int64_t targ
 FilterPlan plan_filter(int64_t T, int32_t max_len) {
   const int64_t pages = (static_cast<int64_t>(max_len) + kPageTokens - 1) / kPageTokens;
   FilterPlan p{false, 4, 1, 0, 0};
-  p.groups = static_cast<int>(
-      std::max<int64_t>(1, std::min<int64_t>((pages + 3) / 4, (kFilterTargetGroups + T - 1) / T)));
+  // unfused: about kFilterTargetGroups workgroups over T equal rows, and at
+  // least enough that a max_len row takes at most kFilterMaxWavePages pages
+  // per wave (rows of mixed lengths use slots in proportion to their pages);
+  // a multiple of 8 (the segments are spread over the 8 XCDs)
+  const int64_t g = std::max<int64_t>((kFilterTargetGroups + T - 1) / T, (pages + 4 * kFilterMaxWavePages - 1) /
+                                                                             (4 * kFilterMaxWavePages));
+  p.groups = static_cast<int>((std::max<int64_t>(1, std::min<int64_t>((pages + 3) / 4, g)) + 7) & ~int64_t{7});
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
@@ -1617,9 +1643,9 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   TopkWorkspace ws = carve(workspace, T, L);
-  FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-               max_len, k, ws.upper, ws.hist};
   const FilterPlan plan = plan_filter(T, max_len);
+  FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+               max_len, k, ws.upper, ws.hist, num_tokens, plan.groups};
   if (plan.fused) {
     // the fused kernel's counters are zero on entry and left zero
     FusedArgs fa{f, q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
@@ -1634,7 +1660,7 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, 
     const int64_t zero_blocks = (nz + 255) / 256;
     hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
                        dim3(256), 0, s, ws.hist, nz);
-    hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(plan.groups), num_tokens), dim3(256), 0, s, f);
+    hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(plan.groups * T)), dim3(256), 0, s, f);
     hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
   }
   return ekv_launch_status();
