@@ -568,6 +568,10 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
   const int64_t row = static_cast<int64_t>(t) * a.max_len;
   const int c_begin = blockIdx.x * kVerifyChunks;
   int32_t* counts = a.cand_count + static_cast<int64_t>(t) * a.chunks;
+  if (c_begin * kChunk >= n) {  // every chunk past the row's end: empty lists
+    if (tid < kVerifyChunks && c_begin + tid < a.chunks) counts[c_begin + tid] = 0;
+    return;
+  }
   if (n <= a.k) {  // every token is selected: list them, no scores needed
     for (int c = c_begin; c < min(c_begin + kVerifyChunks, a.chunks); ++c) {
       const int chunk0 = c * kChunk;
