@@ -14,6 +14,13 @@ Prints ONE JSON line.  ``value`` = algorithmic HBM bytes per step / step time
 (GB/s), the metric's unit; ``tok_per_s`` = decode tokens per second.
 Algorithmic bytes per step: indexer K rows 132 B x sum of windowed lengths,
 gathered latent rows 580 B x 2176 per row, plus q / out tensors.
+
+The line also carries the other workloads, each measured on its own:
+``hca_write`` (chunked-prefill cache write, 16 x 8192 tokens), ``hca_decode``
+(HCA decode step, 64 sequences at 8K-128K contexts) and ``mtp`` (DSA and HCA
+layer decode steps at 8 x 256K + 1 x 1M contexts with 3 query rows per
+sequence, and the model step composed from them).  ``--only`` runs one of
+them alone.
 """
 
 from __future__ import annotations
