@@ -89,6 +89,32 @@ def test_hca_write_path_exact(dev, dim, fused):
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
+@pytest.mark.parametrize("dim", [576, 512])
+def test_hca_write_decode_completes_spans(dev, dim, fused):
+    """Calls of fewer than 128 rows per sequence (decode, drafts) that complete
+    spans whose first rows sit in the state ring (the compressor's straddle
+    path).  Spans start 125, 126, 127 and 1 rows before the call."""
+    rng = np.random.default_rng(40 + dim)
+    case = HcaCase(rng, dim, num_seqs=3, max_pos=600, ring=192)
+    gpu = {
+        "pool": torch.zeros((case.pages, paged.fp8_page_bytes(dim)), dtype=torch.uint8, device=dev),
+        "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
+    }
+    calls = [
+        ([0, 0, 0], [125, 255, 126]),     # prefill, partial spans left in the state ring
+        ([125, 255, 126], [3, 1, 3]),     # completes span 0, span 1 (one row), span 0 (two rows)
+        ([128, 256, 129], [127, 127, 127]),  # span 1 of sequence 2: one ring row, 127 new
+        ([255, 383, 256], [1, 1, 3]),     # span 1 and span 2 by their last row
+    ]
+    for starts, counts in calls:
+        _run_call(dev, case, rng, starts, counts, gpu, fused)
+        torch.cuda.synchronize()
+        assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool), f"pool mismatch after call {starts}"
+        got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
+        assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
+
+
 def test_hca_decode_indices(dev):
     from ernie_kv import ops
 
