@@ -10,7 +10,7 @@ import torch
 from helpers import bf16_tensor, bf16_values, permuted_block_table, randn_bf16, to_dev
 from oracle import decode as od
 from oracle import paged
-from oracle.fp8 import bf16_round, quantize_rows
+from oracle.fp8 import quantize_rows
 from oracle.merge import logical_to_global
 
 pytestmark = pytest.mark.gpu
