@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0
 # write; run bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
 FILTER_TRAFFIC_BYTES = 590_228_753 + 10_803_104
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -126,14 +127,15 @@ def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, s
 
 
 def dsa_step(ops, st, ev=None):
-    """One DSA decode step, eager; ``ev`` = (start, end) events around the scorer."""
+    """One DSA decode step, eager; ``ev`` = (start, end, start, end) events
+    around the scorer and around the sparse MLA decode."""
     dsa_pre(ops, st)
     if ev is not None:
         ev[0].record()
     dsa_filter(ops, st)
     if ev is not None:
         ev[1].record()
-    dsa_post(ops, st)
+    dsa_post(ops, st, ev)
 
 
 def dsa_pre(ops, st):
@@ -150,12 +152,16 @@ def dsa_filter(ops, st):
     ops.indexer_filter(st["q8"], st["digits"], st["wf"], *common, st["idx_ws"])
 
 
-def dsa_post(ops, st):
+def dsa_post(ops, st, ev=None):
     common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
     ops.indexer_select(st["digits"], st["wf"], *common, st["topk"], st["idx_ws"], merged=st["merged"],
                        positions=st["positions"], window=128)
+    if ev is not None:
+        ev[2].record()
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
                           block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
+    if ev is not None:
+        ev[3].record()
 
 
 def build_hca_write(torch, ops, seed: int, B: int = 16, chunk: int = 8192, max_off: int = 65536, D: int = 576):
@@ -480,7 +486,7 @@ def main():
     for _ in range(args.warmup):
         dsa_step(ops, st)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(4)) for _ in range(args.steps)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -490,12 +496,16 @@ def main():
     t_end.record()
     torch.cuda.synchronize()
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    filt_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    filt_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    dec_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
     by = dsa_bytes(args.batch, args.ctx)
     gbs = by["total"] / (ms_step * 1e-3) / 1e9
     n = max(args.ctx - 128, 0)
     filt_gbs = by["indexer_k"] / (filt_ms * 1e-3) / 1e9
     filt_tflops = args.batch * n * 64 * 128 * 2 / (filt_ms * 1e-3) / 1e12
+    # decode contractions: S = Q K^T over the 576-wide rows and O = P V over
+    # their first 512 columns, 64 heads x 2176 rows per query row
+    dec_flops = args.batch * 64 * (min(n, 2048) + min(args.ctx, 128)) * (576 + 512) * 2
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -532,6 +542,15 @@ def main():
             "bytes_per_launch": by["indexer_k"],
             "mfma_fp8_tflops": round(filt_tflops, 1),
             "mfma_frac": round(filt_tflops / FP8_PEAK_TFLOPS, 4),
+        },
+        "decode": {
+            "kernels": "sparse_decode_kernel<576> + decode_combine_kernel (ekv_sparse_mla_decode), timed by events "
+                       "around the call",
+            "ms": round(dec_ms, 4),
+            "bytes": by["gather"],
+            "GB/s_gather": round(by["gather"] / (dec_ms * 1e-3) / 1e9, 1),
+            "mfma_bf16_tflops": round(dec_flops / (dec_ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(dec_flops / (dec_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
     }
     if not args.no_hca:
