@@ -264,16 +264,21 @@ def _device_cache(dev, seed, num_seqs, pages_per_seq, kind):
     return bt, kcache
 
 
-def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed, ws=None):
+def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed, ws=None, rows_per_seq=1):
     """ekv_indexer_topk against ekv_topk_select over ekv_indexer_score's exact
     scores (both bit-exact against the oracle in the tests above); returns the
-    workspace of the top-k call (a new zero-filled one unless `ws` is given)."""
+    workspace of the top-k call (a new zero-filled one unless `ws` is given).
+    With rows_per_seq > 1, rows R*i .. R*i+R-1 belong to sequence i (a
+    sequence's token and draft rows), else row t to sequence t % num_seqs."""
     from ernie_kv import ops
 
     T = len(lengths)
     bt, kcache = _device_cache(dev, seed, num_seqs, max_len // 64 + 1, kind)
     lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
-    req = (torch.arange(T, dtype=torch.int32, device=dev) % num_seqs).contiguous()
+    if rows_per_seq > 1:
+        req = (torch.arange(T, dtype=torch.int32, device=dev) // rows_per_seq).contiguous()
+    else:
+        req = (torch.arange(T, dtype=torch.int32, device=dev) % num_seqs).contiguous()
     g = torch.Generator(device=dev).manual_seed(seed + 1)
     q = torch.randn(T, 64, 128, generator=g, device=dev).to(torch.bfloat16)
     w = torch.randn(T, 64, generator=g, device=dev).to(torch.bfloat16)
@@ -309,6 +314,22 @@ def test_indexer_topk_million_token_row(dev):
     """A 1,048,576-token row (config 5's longest context) beside shorter
     ones, through the fused filter: same top-2048 as the exact path."""
     ws = _topk_vs_exact_path(dev, [1048576, 262144, 4096, 2049], 4, 1048576, "normal", seed=61)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+
+
+@pytest.mark.parametrize("rows", [2, 3])
+def test_indexer_topk_draft_rows(dev, rows):
+    """Draft-token rows (the decode layout's next_n = rows): 24 rows, R per
+    sequence at consecutive positions, one sequence at 1M tokens -- too long
+    for the one-launch plan, so the filter / bound / verify launches run, with
+    a sequence's rows reading the same pages back to back.  Same top-2048 as
+    the exact path."""
+    S = 24 // rows
+    lengths = []
+    for s_ in range(S):
+        ctx = 1048576 if s_ == 0 else 65536 + 777 * s_
+        lengths += [ctx - rows + 1 + r for r in range(rows)]
+    ws = _topk_vs_exact_path(dev, lengths, S, 1048576, "normal", seed=70 + rows, rows_per_seq=rows)
     assert int(ws[:16].view(torch.int32).sum()) == 0
 
 
