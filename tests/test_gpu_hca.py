@@ -180,3 +180,82 @@ def test_hca_decode_end_to_end(dev, dim):
     assert np.all(err <= 2e-3 + 2e-2 * np.abs(ref_o)), f"max err {err.max()}"
     gl = lse.cpu().numpy().astype(np.float64)
     assert np.all(np.abs(gl - ref_l) <= 2e-3 * np.maximum(1.0, np.abs(ref_l)))
+
+
+def test_hca_decode_step_graph_replay(dev):
+    """The HCA decode step -- ekv_hca_write of one new token per sequence
+    (two of them complete a span), ekv_hca_decode_indices and
+    ekv_sparse_mla_decode -- captured in a HIP graph: nothing inside
+    synchronizes with the host or allocates, and each of three replays, with
+    eager work and synchronizations between them, equals the eager step bit
+    for bit (the step is idempotent: it rewrites the same slots)."""
+    from ernie_kv import ops
+
+    g = torch.Generator(device=dev).manual_seed(91)
+    B, D, ring, H = 8, 576, 128, 64
+    ctx = torch.tensor([300, 1024, 777, 2048, 1500, 129, 640, 2999], dtype=torch.int64)  # 1024, 2048: span ends
+    spans = int(ctx.max()) // 128 + 1
+    comp_pp, ring_pp = (spans + 63) // 64, ring // 64
+    pages = B * (comp_pp + ring_pp + 1)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+    comp_bt = perm[: B * comp_pp].view(B, comp_pp).to(dev)
+    ring_pages = perm[B * comp_pp: B * (comp_pp + ring_pp)].view(B, ring_pp).to(dev)
+    lat_page = perm[B * (comp_pp + ring_pp):].to(torch.int64)
+    pos = ctx - 1
+    codes = torch.randint(0, 256, (pages, 64 * D), device=dev, dtype=torch.uint8, generator=g)
+    codes -= ((codes & 0x7F) == 0x7F).to(torch.uint8)
+    scales = torch.full((pages, 64), 2.0 ** -8, device=dev, dtype=torch.float32)
+    pool = torch.cat([codes, scales.view(torch.uint8)], dim=1).contiguous()
+    ang = (torch.arange(spans, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    rnd = lambda *s: torch.randn(*s, device=dev, generator=g).to(torch.bfloat16)  # noqa: E731
+    st = dict(latent=rnd(B, D), kv_score=rnd(B, 2 * D), state=rnd(B, 256, 2 * D), q=rnd(B, H, D),
+              slots=(lat_page * 64 + pos % 64).to(dev), positions=pos.to(dev),
+              token_seq=torch.arange(B, dtype=torch.int32, device=dev),
+              qsl=torch.arange(B + 1, dtype=torch.int32, device=dev),
+              state_slot=torch.arange(B, dtype=torch.int32, device=dev),
+              ape=(0.5 * torch.randn(128, D, device=dev, generator=g)).contiguous(),
+              norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=g)).contiguous(),
+              cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], 1).to(torch.float32).to(dev),
+              sinks=torch.randn(H, device=dev, generator=g))
+    width = spans + ring
+    idx = torch.empty((B, width), dtype=torch.int32, device=dev)
+    lens = torch.empty(B, dtype=torch.int32, device=dev)
+    out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev)
+    ws = ops.decode_workspace(B, H, width, dev)
+
+    def step():
+        ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], 1,
+                      st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], comp_bt,
+                      ring_pages, ring, pool)
+        ops.hca_decode_indices(st["positions"], st["token_seq"], comp_bt, ring_pages, ring, idx, lens)
+        ops.sparse_mla_decode(st["q"], pool, idx, 256 ** -0.5, out, lse, sinks=st["sinks"], lengths=lens,
+                              workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    want = [x.clone() for x in (pool, st["state"], idx, lens, out, lse)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.fill_(0)
+        lse.fill_(0)
+        idx.fill_(-5)
+        lens.fill_(0)
+        _ = (st["q"][:, :, :64].float() @ st["q"][:, :, :64].float().transpose(1, 2).contiguous()).sum()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (pool, st["state"], idx, lens, out, lse)
+        for name, a_, b_ in zip(["pool", "state", "idx", "lens", "out", "lse"], got, want):
+            assert torch.equal(a_.view(torch.uint8) if a_.dtype == torch.bfloat16 else a_,
+                               b_.view(torch.uint8) if b_.dtype == torch.bfloat16 else b_), f"replay {rep}: {name}"
