@@ -909,7 +909,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // Phase 3: candidates of the segment in order, scored Lay::kList at a time.
   auto score_list = [&](int cnt, int base) {
     __syncthreads();
-    constexpr int kBatch = 3;  // blocks whose key rows are loaded together
+    constexpr int kBatch = 2;  // blocks whose key rows are loaded together
     for (int bb = wave * 16; bb < cnt; bb += 16 * kWaves * kBatch) {
       int tok[kBatch];
       int64_t page[kBatch];
