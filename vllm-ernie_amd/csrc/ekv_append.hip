@@ -25,23 +25,11 @@ __global__ void __launch_bounds__(256) kv_append_quant_kernel(AppendArgs a) {
   append_rows<D, kAppendSeq<D>>(a, blockIdx.x);
 }
 
-// HCA append: workgroups [0, main_blocks) store every row at its slot, the
-// rest write the window ring and state ring rows of each sequence's tail,
-// kTailBlockRows rows of one sequence each.
-constexpr int kTailBlockRows = 16;
-
+// HCA append over the grid of hca_append_grid.
 template <int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8)))
 hca_append_kernel(AppendArgs a, int main_blocks, int tail_rows) {
-  const int block = static_cast<int>(blockIdx.x);
-  if (block < main_blocks) {
-    append_rows<D, kAppendSeq<D>>(a, block);
-    return;
-  }
-  const int tb = block - main_blocks;
-  const int blocks_per_seq = tail_rows / kTailBlockRows;
-  const int k_lo = (tb % blocks_per_seq) * kTailBlockRows;
-  hca_tail_range<D, 4, 1>(a, tb / blocks_per_seq, k_lo, k_lo + kTailBlockRows);
+  hca_append_block<D>(a, static_cast<int>(blockIdx.x), main_blocks, tail_rows);
 }
 
 // ---------------------------------------------------------------------------
@@ -306,13 +294,8 @@ __global__ void __launch_bounds__(256) dsa_prologue_kernel(DsaPrologueArgs a) {
 }
 
 int launch_hca_append(const AppendArgs& a, int dim, int num_seqs, bool rows, bool tail, hipStream_t s) {
-  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>);
-  const int main_blocks = rows ? (a.num_tokens + rows_per_block - 1) / rows_per_block : 0;
-  // each sequence's last max(ring, 256) rows, in whole tail workgroups
-  const int tail_rows =
-      (hca_tail_span(a.ring_pages != nullptr, a.ring) + kTailBlockRows - 1) / kTailBlockRows * kTailBlockRows;
-  const bool any_tail = tail && (a.ring_pages != nullptr || a.state != nullptr);
-  const int64_t blocks = main_blocks + (any_tail ? static_cast<int64_t>(num_seqs) * (tail_rows / kTailBlockRows) : 0);
+  int main_blocks = 0, tail_rows = 0;
+  const int64_t blocks = hca_append_grid(a, dim, num_seqs, rows, tail, main_blocks, tail_rows);
   EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
   if (blocks == 0) return 0;
   dim3 grid(static_cast<uint32_t>(blocks));

@@ -353,6 +353,32 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
   compress_span<D>(a, ls, b, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
 }
 
+// Decode-sized HCA write (fewer than 128 new rows per sequence, so at most
+// one span per sequence completes: the one holding its first new position)
+// in one launch: workgroups [0, num_seqs) compress that span when the call
+// completes it, the rest run the append grid's blocks on their first 4
+// waves.  The two touch disjoint memory: the compressor reads this call's
+// inputs and state-ring rows of positions before the call, the append writes
+// this call's positions (rows, window ring, state ring).
+template <int D>
+__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5)))
+hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows) {
+  __shared__ CompressLds<D> ls;
+  const int block = static_cast<int>(blockIdx.x);
+  if (block < num_seqs) {
+    const int t0 = c.qsl[block];
+    const int n = c.qsl[block + 1] - t0;
+    if (n <= 0) return;
+    const int64_t p0 = c.positions[t0];
+    const int64_t j = p0 / kSpan;
+    if (j * kSpan + kSpan - 1 > p0 + n - 1 || j >= c.max_spans) return;  // no span completed by this call
+    compress_span<D>(c, ls, block, t0, p0, j, c.state_slot != nullptr ? c.state_slot[block] : -1);
+    return;
+  }
+  if (threadIdx.x >= 256) return;  // the append's blocks are 4-wave; they use no workgroup barrier
+  hca_append_block<D>(a, block - num_seqs, main_blocks, tail_rows);
+}
+
 }  // namespace ekv
 
 using namespace ekv;
@@ -425,6 +451,17 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
                        state_slot, num_state);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (max_query_len < kSpan) {  // decode-sized: compress and append in one launch
+    int main_blocks = 0, tail_rows = 0;
+    const int64_t blocks = num_seqs + hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
+    EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    if (dim == 512)
+      hipLaunchKernelGGL(hca_write_small_kernel<512>, grid, dim3(512), 0, s, c, ap, num_seqs, main_blocks, tail_rows);
+    else
+      hipLaunchKernelGGL(hca_write_small_kernel<576>, grid, dim3(576), 0, s, c, ap, num_seqs, main_blocks, tail_rows);
+    return ekv_launch_status();
+  }
   const dim3 grid(max_query_len / kSpan + 1, num_seqs);
   if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(512), 0, s, c);
   else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, c);

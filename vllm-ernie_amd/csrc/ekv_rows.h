@@ -327,6 +327,33 @@ constexpr int append_block_rows(int d, int seq, int waves = 4) { return waves * 
 template <int D>
 constexpr int kAppendSeq = (D == 128) ? 1 : 4;
 
+// HCA append grid: workgroups [0, main_blocks) store every row at its slot,
+// the rest write the window ring and state ring rows of each sequence's
+// tail, kTailBlockRows rows of one sequence each.  Returns the block count.
+constexpr int kTailBlockRows = 16;
+inline int64_t hca_append_grid(const AppendArgs& a, int dim, int num_seqs, bool rows, bool tail, int& main_blocks,
+                               int& tail_rows) {
+  const int rows_per_block = append_block_rows(dim, kAppendSeq<576>);
+  main_blocks = rows ? (a.num_tokens + rows_per_block - 1) / rows_per_block : 0;
+  // each sequence's last max(ring, 256) rows, in whole tail workgroups
+  tail_rows = (hca_tail_span(a.ring_pages != nullptr, a.ring) + kTailBlockRows - 1) / kTailBlockRows * kTailBlockRows;
+  const bool any_tail = tail && (a.ring_pages != nullptr || a.state != nullptr);
+  return main_blocks + (any_tail ? static_cast<int64_t>(num_seqs) * (tail_rows / kTailBlockRows) : 0);
+}
+
+// One append grid block: a row block or a tail block (256 threads).
+template <int D>
+__device__ __forceinline__ void hca_append_block(const AppendArgs& a, int block, int main_blocks, int tail_rows) {
+  if (block < main_blocks) {
+    append_rows<D, kAppendSeq<D>>(a, block);
+    return;
+  }
+  const int tb = block - main_blocks;
+  const int blocks_per_seq = tail_rows / kTailBlockRows;
+  const int k_lo = (tb % blocks_per_seq) * kTailBlockRows;
+  hca_tail_range<D, 4, 1>(a, tb / blocks_per_seq, k_lo, k_lo + kTailBlockRows);
+}
+
 
 // Argument checks and AppendArgs of an HCA append (the latent rows, the
 // window ring and the compressor state ring); 0 or an error status.
