@@ -308,6 +308,17 @@ int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                           int64_t out_tok_stride, int64_t out_head_stride, float* lse,
                           int64_t lse_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Diagnostic, no counterpart in the reference: the indexer filter's fp8-MFMA
+ * dot products out[s][h] = q[h] . k[s] of e4m3fn codes (q [64][128],
+ * k [num_keys][128], num_keys a multiple of 16, out [num_keys][64] fp32),
+ * computed by the same MFMA call and operand layout as ekv_indexer_filter.
+ * Lets a caller check, on the device at hand, the error bound the filter's
+ * candidate test assumes (|dot - exact| <= 2^-8 * 448^2 per head).
+ */
+int ekv_indexer_filter_dots(const uint8_t* q_codes, const uint8_t* k_codes, int32_t num_keys, float* out,
+                            void* stream);
+
 /* The 256-entry byte -> packed signed base-64 digit table the scorer uses. */
 int ekv_fp8_digit_table(uint32_t* table, void* stream);
 

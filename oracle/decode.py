@@ -48,19 +48,12 @@ def sparse_mla_decode(
     dv: int,
     sinks: np.ndarray | None = None,
     lengths: np.ndarray | None = None,
-    p_bound: bool = False,
 ):
-    """``q [T, H, D]``; ``rows_of(slots) -> [n, D]`` fp64; returns (out, lse).
-
-    With ``p_bound`` also returns ``2^-8 sum_j p_j |v_j| / den`` per output
-    element: a bound on what rounding the weights p_j to bf16 before the
-    P V product (as the kernels and FlashMLA do; relative error <= 2^-9 per
-    weight) moves ``out``.  It matters where few rows nearly cancel."""
+    """``q [T, H, D]``; ``rows_of(slots) -> [n, D]`` fp64; returns (out, lse)."""
     q = np.asarray(q, dtype=np.float64)
     T, H, _ = q.shape
     out = np.zeros((T, H, dv), dtype=np.float64)
     lse = np.full((T, H), -np.inf, dtype=np.float64)
-    bound = np.zeros((T, H, dv), dtype=np.float64)
     sink = None if sinks is None else np.asarray(sinks, dtype=np.float64)
     for t in range(T):
         idx = np.asarray(indices[t], dtype=np.int64)
@@ -80,5 +73,4 @@ def sparse_mla_decode(
         if sink is not None:
             den = den + np.exp(sink - m)
         out[t] = (e @ kv[:, :dv]) / den[:, None]
-        bound[t] = 2.0 ** -8 * (e @ np.abs(kv[:, :dv])) / den[:, None]
-    return (out, lse, bound) if p_bound else (out, lse)
+    return out, lse

@@ -83,6 +83,36 @@ def rope_cos_sin(positions: np.ndarray, rot_dim: int, theta: float) -> np.ndarra
     return np.concatenate([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
 
 
+def yarn_cos_sin(positions: np.ndarray, rot_dim: int, theta: float, factor: float = 16.0,
+                 original_max_position: int = 4096, beta_fast: float = 32.0, beta_slow: float = 1.0) -> np.ndarray:
+    """YaRN cos | sin table (Peng et al., "YaRN: Efficient Context Window
+    Extension of Large Language Models", 2023): per frequency, a linear ramp
+    between the original (extrapolated) and the 1/factor (interpolated) inverse
+    frequency over the dims whose wavelengths lie between the ones that turn
+    beta_fast and beta_slow times in the original context, and the attention
+    factor mscale = 0.1 ln(factor) + 1 multiplied into cos and sin.
+
+    The HCA layers' RoPE is YaRN at ``compress_rope_theta``
+    (src/vllm_ernie/models/ernie5_5/config.py:187-188); its parameters come
+    from the checkpoint's ``rope_scaling``, so the ones here are
+    representative.  The table is an input of the compressor (cos_sin), not
+    computed by the path itself."""
+    half = rot_dim // 2
+    inv_extra = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / rot_dim)
+    inv_inter = inv_extra / factor
+
+    def corr_dim(turns):
+        return rot_dim * math.log(original_max_position / (turns * 2 * math.pi)) / (2 * math.log(theta))
+
+    low = max(math.floor(corr_dim(beta_fast)), 0)
+    high = min(math.ceil(corr_dim(beta_slow)), rot_dim - 1)
+    ramp = np.clip((np.arange(half, dtype=np.float64) - low) / max(high - low, 1e-3), 0.0, 1.0)
+    inv = inv_inter * ramp + inv_extra * (1.0 - ramp)
+    mscale = 0.1 * math.log(factor) + 1.0
+    ang = np.asarray(positions, dtype=np.float64)[:, None] * inv[None, :]
+    return (np.concatenate([np.cos(ang), np.sin(ang)], axis=-1) * mscale).astype(np.float32)
+
+
 def neox_partial_rope(x: np.ndarray, cos_sin: np.ndarray, rot_dim: int) -> np.ndarray:
     """NeoX rotation of dims ``[0, rot_dim)`` of the last axis; the rest untouched.
 

@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 
 class HcaCase:
-    def __init__(self, rng, dim, num_seqs, max_pos, ring):
+    def __init__(self, rng, dim, num_seqs, max_pos, ring, rope="plain"):
         self.dim, self.B, self.ring = dim, num_seqs, ring
         lp = (max_pos + 63) // 64
         spans = max_pos // 128 + 1
@@ -27,7 +27,10 @@ class HcaCase:
         self.pages = len(perm)
         self.ape = (rng.standard_normal((128, dim)) * 0.5).astype(np.float32)
         self.norm_w = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
-        self.cos_sin = oi.rope_cos_sin(np.arange(spans) * 128, 64, 1.6e5)
+        # the compressor's RoPE table at position 128 j (compress_rope_theta);
+        # "yarn": YaRN frequencies and attention factor, as the HCA config uses
+        table = oi.yarn_cos_sin if rope == "yarn" else oi.rope_cos_sin
+        self.cos_sin = table(np.arange(spans) * 128, 64, 1.6e5)
         self.state_slot = rng.permutation(num_seqs + 2)[:num_seqs].astype(np.int32)
         self.st = oh.HcaState(self.pages, dim, num_seqs + 2)
 
@@ -63,11 +66,12 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
                    d(case.ring_pages), case.ring, gpu["state"], d(case.state_slot))
 
 
+@pytest.mark.parametrize("rope", ["plain", "yarn"])
 @pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
 @pytest.mark.parametrize("dim", [576, 512])
-def test_hca_write_path_exact(dev, dim, fused):
+def test_hca_write_path_exact(dev, dim, fused, rope):
     rng = np.random.default_rng(dim)
-    case = HcaCase(rng, dim, num_seqs=3, max_pos=1400, ring=192)
+    case = HcaCase(rng, dim, num_seqs=3, max_pos=1400, ring=192, rope=rope)
     gpu = {
         "pool": torch.zeros((case.pages, paged.fp8_page_bytes(dim)), dtype=torch.uint8, device=dev),
         "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
@@ -89,14 +93,15 @@ def test_hca_write_path_exact(dev, dim, fused):
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
 
 
+@pytest.mark.parametrize("rope", ["plain", "yarn"])
 @pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
 @pytest.mark.parametrize("dim", [576, 512])
-def test_hca_write_decode_completes_spans(dev, dim, fused):
+def test_hca_write_decode_completes_spans(dev, dim, fused, rope):
     """Calls of fewer than 128 rows per sequence (decode, drafts) that complete
     spans whose first rows sit in the state ring (the compressor's straddle
     path).  Spans start 125, 126, 127 and 1 rows before the call."""
     rng = np.random.default_rng(40 + dim)
-    case = HcaCase(rng, dim, num_seqs=3, max_pos=600, ring=192)
+    case = HcaCase(rng, dim, num_seqs=3, max_pos=600, ring=192, rope=rope)
     gpu = {
         "pool": torch.zeros((case.pages, paged.fp8_page_bytes(dim)), dtype=torch.uint8, device=dev),
         "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),

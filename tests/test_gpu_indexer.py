@@ -357,3 +357,58 @@ def test_indexer_topk_many_rows(dev):
     lengths = rng.integers(0, 6000, 1100).astype(np.int32).tolist()
     lengths[:4] = [0, 2048, 2049, 6000]
     _topk_vs_exact_path(dev, lengths, 16, 6000, "normal", seed=9)
+
+
+def _adversarial_fp8_operands(rng):
+    """q [64, 128] and keys [S, 128] (e4m3fn codes) built to stress the fp8
+    MFMA's accumulation: maximal products of alternating and block signs that
+    cancel to 0, maximal products beside subnormal ones, a few large terms
+    cancelled by many small ones, every code value, and random codes."""
+    from oracle.fp8 import decode_table, encode_e4m3
+
+    valid = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    big, tiny = 448.0, 2.0 ** -9
+    alt = np.where(np.arange(128) % 2 == 0, big, -big)
+    block = np.where(np.arange(128) < 64, big, -big)
+    mixed = np.where(np.arange(128) % 2 == 0, big, tiny)
+    mixed_neg = np.where(np.arange(128) % 2 == 0, big, -tiny)
+    few_big = np.concatenate([np.full(4, big), np.full(124, -big * 4 / 124)])
+    exps = 2.0 ** rng.integers(-9, 9, 128) * rng.choice([-1.0, 1.0], 128)
+    pats = [alt, block, mixed, mixed_neg, few_big, exps, np.full(128, big), np.full(128, tiny)]
+    q_rows = [np.full(128, big), alt, block, np.where(np.arange(128) % 4 < 2, big, -big), mixed, exps]
+    q = np.stack([encode_e4m3(np.asarray(r, np.float32)) for r in q_rows])
+    q = np.concatenate([q, rng.choice(valid, (64 - len(q), 128))]).astype(np.uint8)
+    keys = [encode_e4m3(np.asarray(p, np.float32)) for p in pats]
+    keys += [encode_e4m3(np.asarray(np.roll(p, r), np.float32)) for p in pats for r in (1, 17, 64)]
+    keys += [np.resize(valid, 128), np.resize(valid[::-1], 128)]
+    keys = np.stack(keys).astype(np.uint8)
+    rand = rng.choice(valid, (16384 - len(keys) % 16, 128)).astype(np.uint8)
+    # signs of a random key matched to q row 0 (all +448): dot = sum |k| * 448,
+    # and flipped halves (large partial sums that cancel)
+    flip = rand[:2048].copy()
+    flip[:, 64:] ^= 0x80
+    k = np.concatenate([keys, rand, flip])
+    k = k[: len(k) // 16 * 16]
+    assert np.isfinite(decode_table()[k]).all() and np.isfinite(decode_table()[q]).all()
+    return q, k
+
+
+def test_filter_mfma_error_bound(dev):
+    """The filter drops a token only when its upper bound U = a + e falls
+    below the k-th lower bound, with e built on the assumption that each
+    head's fp8-MFMA dot product is within 2^-8 * 448^2 of the exact one.
+    Pinned on this device with the filter's own MFMA call over adversarial
+    cancellation patterns (maximal alternating / block signs, maximal beside
+    subnormal products, every code) and 18K random keys."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(2718)
+    q, k = _adversarial_fp8_operands(rng)
+    got = ops.indexer_filter_dots(to_dev(q, dev), to_dev(k, dev)).cpu().numpy().astype(np.float64)
+    exact = (oi.int_repr(k) @ oi.int_repr(q).T).astype(np.float64) * 2.0 ** -18
+    err = np.abs(got - exact)
+    bound = 2.0 ** -8 * 448.0 ** 2
+    worst = float(err.max())
+    print(f"fp8 MFMA dot error: max {worst:.3f} = 2^{np.log2(max(worst, 1e-30)):.2f} * 1 "
+          f"(bound 2^{np.log2(bound):.2f}); {int((err > 0).sum())} of {err.size} inexact")
+    assert worst <= bound, f"fp8 MFMA error {worst} exceeds the filter's assumed bound {bound}"

@@ -7,21 +7,25 @@
 //   * score waves 0..3 (q for heads 16w .. 16w+15 held in registers) first
 //     finish tile t-1 (below), then compute S = Q K^T of tile t on
 //     v_mfma_f32_16x16x32_bf16 from a bf16 K image in LDS, run the online
-//     softmax and write P (bf16, row scale folded in) for their heads; fp8
-//     K fragments become bf16 in registers (exact conversion);
+//     softmax and write P (row scale folded in) for their heads as a pair of
+//     bf16 values hi = bf16(P), lo = bf16(P - hi); fp8 K fragments become
+//     bf16 in registers (exact conversion);
 //   * data waves 4..7 finish tile t-1, store tile t+1 (the rows as cached:
 //     e4m3fn bytes, or bf16) into the next of three K images, and issue the
 //     loads of tile t+3 (8 rows per wave, row addresses in scalar registers,
 //     256-byte coalesced loads into registers, two tiles in flight);
-//   * "finish tile t-1" = O[:, 64w .. 64w+63] += P V for all heads, every wave
-//     taking its 64 channels.  The B operand (V, entries x channels) is read
-//     straight from the row-major K image with a transposing LDS read
-//     (ds_read_b64_tr_b8 for fp8 rows, ds_read_b64_tr_b16 for bf16); no
-//     separate V^T image is built.
+//   * "finish tile t-1" = O[:, 64w .. 64w+63] += P_hi V + P_lo V for all
+//     heads, every wave taking its 64 channels.  The B operand (V, entries x
+//     channels) is read straight from the row-major K image with a
+//     transposing LDS read (ds_read_b64_tr_b8 for fp8 rows, ds_read_b64_tr_b16
+//     for bf16); no separate V^T image is built.
+// The hi/lo pair carries P to about 2^-16 relative (one bf16 alone is 2^-8,
+// which rows of a few entries that nearly cancel expose); V itself is exact
+// in bf16 for fp8 and bf16 caches.
 // A prologue resolves every index entry of the split to a cache slot (block
 // table lookup) and fp32 row scale once.  The softmax reference max only
 // moves when a score exceeds it by more than 8 (log2 units), so O is rescaled
-// rarely.  Each split leaves O / l in bf16 plus (m, l) in fp32; the combine
+// rarely.  Each split leaves O / l in fp32 plus (m, l) in fp32; the combine
 // kernel merges the splits, adds the sink and writes bf16 out and the
 // natural-log lse (log sum_j exp(s_j), sink excluded).
 #include "ekv_common.h"
@@ -39,7 +43,9 @@ constexpr int kThreads = 64 * (kScoreWaves + kDataWaves);
 constexpr int kRowsPerDataWave = kTile / kDataWaves;   // 8
 constexpr int kKImages = 3;                  // tile t-1 (P V), t (S), t+1 (being stored)
 constexpr int kMaxSplitEntries = 1024;       // index entries one workgroup resolves
+constexpr int kMaxSplitTiles = kMaxSplitEntries / kTile;
 constexpr int kTargetGroups = 256;           // one workgroup per CU
+constexpr int kXcds = 8;                     // workgroup b runs on XCD b % 8
 constexpr float kRescaleSlack = 8.0f;        // log2 units: P <= 2**8 between rescales
 constexpr float kLog2e = 0x1.715476p+0f;
 constexpr float kLn2 = 0x1.62e430p-1f;
@@ -63,11 +69,97 @@ struct DecodeArgs {
   const int32_t* req_ids;   // [T] with block_table
   float scale;              // softmax scale
   int32_t heads;
-  int32_t per_split;        // entries per split (multiple of kTile, <= kMaxSplitEntries)
-  float* ws_o;              // [T, NS, H, 512] fp32, O / l of the split
-  float* ws_ml;             // [T, NS, H, 2] (m in log2 units, l)
-  int32_t splits;
+  int32_t rows;             // T
+  int32_t groups;           // G workgroups (a multiple of 8), >= T + T * tiles(width) / 32
+  float* ws_o;              // [G, H, 512] fp32, O / l of workgroup g's split
+  float* ws_ml;             // [G, H, 2] (m in log2 units, l)
+  int2* ws_rows;            // [T] (first workgroup, splits) of each row
+  const float* sinks;       // [H] or null
+  uint16_t* out;            // [T, H, 512] bf16
+  int64_t out_tok_stride, out_head_stride;
+  float* lse;               // [T, H] or null
+  int64_t lse_stride;
 };
+
+// Work split.  Row t has tiles_t = ceil(len_t / 32) tiles and gets
+//   splits_t = max(1, min(tiles_t, 1 + floor((G - T) * tiles_t / total_tiles)))
+// workgroups (sum <= G), taking equal runs of its tiles: splits follow the
+// entries, so a long row gets proportionally more workgroups.  Since
+// G - T >= total_tiles / 32, every split holds at most 32 tiles
+// (kMaxSplitEntries entries).  Row t's splits are the logical workgroups
+// first_t .. first_t + splits_t - 1 (first_t = sum of the splits before it).
+__device__ __forceinline__ int row_len(const DecodeArgs& a, int t) {
+  return a.lengths ? min(max(a.lengths[t], 0), a.width) : a.width;
+}
+__device__ __forceinline__ int row_splits(int64_t extra, int tiles, int64_t total) {
+  const int ns = 1 + (total > 0 ? static_cast<int>((extra * tiles) / total) : 0);
+  return max(1, min(tiles, ns));  // never more splits than tiles
+}
+
+// Finds the row and split of logical workgroup l; t = -1 when l is past the
+// last split.  All threads of the workgroup call it.
+template <int kN>
+__device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int& split, int& nsplit, int& first) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kW = kN / 64;
+  const int T = a.rows;
+  const int64_t extra = a.groups - T;
+  if (a.lengths == nullptr) {  // every row has `width` entries: closed form
+    const int tiles = (a.width + kTile - 1) / kTile;
+    const int ns = row_splits(extra, tiles, static_cast<int64_t>(T) * tiles);
+    t = (l / ns < T) ? l / ns : -1;
+    split = l % ns;
+    nsplit = ns;
+    first = l - split;
+    return;
+  }
+  // total tiles
+  int64_t sum = 0;
+  for (int r = tid; r < T; r += kN) sum += (row_len(a, r) + kTile - 1) / kTile;
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0) reinterpret_cast<int64_t*>(s_red)[wave] = sum;
+  __syncthreads();
+  int64_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) total += reinterpret_cast<int64_t*>(s_red)[w];
+  __syncthreads();
+  // splits of a contiguous run of rows per thread, scanned across the block
+  const int per = (T + kN - 1) / kN;
+  const int r0 = min(tid * per, T), r1 = min(r0 + per, T);
+  int cnt = 0;
+  for (int r = r0; r < r1; ++r) cnt += row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+  int x = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_red[2 * kW + wave] = x;
+  if (tid == 0) s_red[3 * kW] = -1;
+  __syncthreads();
+  int before = 0;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) before += (w < wave) ? s_red[2 * kW + w] : 0;
+  int pos = before + x - cnt;  // logical workgroups before row r0
+  if (pos <= l && l < pos + cnt) {
+    for (int r = r0; r < r1; ++r) {
+      const int ns = row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+      if (l < pos + ns) {
+        s_red[3 * kW] = r;
+        s_red[3 * kW + 1] = l - pos;
+        s_red[3 * kW + 2] = ns;
+        break;
+      }
+      pos += ns;
+    }
+  }
+  __syncthreads();
+  t = s_red[3 * kW];
+  split = s_red[3 * kW + 1];
+  nsplit = s_red[3 * kW + 2];
+  first = l - split;
+  __syncthreads();
+}
 
 // K images hold the tile's rows as stored: raw e4m3fn bytes (fp8 cache) or
 // bf16.  The fp8 row stride D + 8 bytes is 8 (mod 16) words: the 16 rows a
@@ -78,10 +170,12 @@ struct DecodeSmem {
   static constexpr int kImgB = kTile * kKRowB;
   static constexpr int kPRow = kTile + 8;   // bf16 P row stride (elements)
   __align__(16) uint8_t img[kKImages * kImgB];
-  uint16_t p[2][64 * kPRow];                // P of tiles t (written) and t-1 (read)
+  uint16_t p[2][64 * kPRow];                // bf16(P) of tiles t (written) and t-1 (read)
+  uint16_t plo[2][64 * kPRow];              // bf16(P - bf16(P)), same layout
   float alpha[2][64];                       // rescale factor per head (valid when grow[.][head / 16])
   int32_t grow[2][kScoreWaves];
-  float row_l[64];
+  float row_f[64];                          // epilogue: per-head output factor
+  __align__(8) int32_t red[64];             // split location scratch
   int32_t slot[kMaxSplitEntries];
   float kscale[kMaxSplitEntries];
 };
@@ -253,6 +347,11 @@ __device__ __forceinline__ void accumulate_pv(const DecodeSmem<D, BF16>& sm, con
 #pragma unroll
   for (int hf = 0; hf < 4; ++hf)
     pa[hf] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.p[pb][(16 * hf + col) * SM::kPRow + 8 * g]));
+  // the lo parts one head group ahead of their products (register pressure)
+  auto p_lo = [&](int hf) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.plo[pb][(16 * hf + col) * SM::kPRow + 8 * g]));
+  };
+  bf16x8 pl = p_lo(0);
   const int4 gr = *reinterpret_cast<const int4*>(sm.grow[pb]);
   const int grow_any = (gr.x | (hgroups > 1 ? gr.y : 0) | (hgroups > 2 ? gr.z : 0) | (hgroups > 3 ? gr.w : 0));
   if (__builtin_amdgcn_readfirstlane(grow_any)) {
@@ -269,9 +368,15 @@ __device__ __forceinline__ void accumulate_pv(const DecodeSmem<D, BF16>& sm, con
     }
   }
 #pragma unroll
-  for (int hf = 0; hf < 4; ++hf)
+  for (int hf = 0; hf < 4; ++hf) {
+    const bf16x8 pl_next = p_lo(hf < 3 ? hf + 1 : 3);
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hf], vb[nt], o[hf][nt], 0, 0, 0);
+    for (int nt = 0; nt < 4; ++nt) {
+      o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb[nt], o[hf][nt], 0, 0, 0);
+      o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hf], vb[nt], o[hf][nt], 0, 0, 0);
+    }
+    pl = pl_next;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -342,10 +447,15 @@ __device__ __forceinline__ void score_tile(DecodeSmem<D, BF16>& sm, const uint8_
     const float p0 = live ? exp2f(x[0][i] - st.m2[i]) : 0.0f;
     const float p1 = live ? exp2f(x[1][i] - st.m2[i]) : 0.0f;
     st.lsum[i] += p0 + p1;
-    uint16_t* prow = &sm.p[pb][(16 * wave + 4 * g + i) * SM::kPRow];
-    const uint32_t pk = bf16x2_bits(p0 * ks0, p1 * ks1);
-    prow[col] = static_cast<uint16_t>(pk & 0xffffu);
-    prow[16 + col] = static_cast<uint16_t>(pk >> 16);
+    const int prow = (16 * wave + 4 * g + i) * SM::kPRow;
+    const float w0 = p0 * ks0, w1 = p1 * ks1;
+    const uint32_t pk = bf16x2_bits(w0, w1);
+    const float h0 = __uint_as_float(pk << 16), h1 = __uint_as_float(pk & 0xffff0000u);
+    const uint32_t pl = bf16x2_bits(w0 - h0, w1 - h1);  // exact differences
+    sm.p[pb][prow + col] = static_cast<uint16_t>(pk & 0xffffu);
+    sm.p[pb][prow + 16 + col] = static_cast<uint16_t>(pk >> 16);
+    sm.plo[pb][prow + col] = static_cast<uint16_t>(pl & 0xffffu);
+    sm.plo[pb][prow + 16 + col] = static_cast<uint16_t>(pl >> 16);
   }
 }
 
@@ -362,9 +472,16 @@ sparse_decode_kernel(DecodeArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
-  const int t = blockIdx.y, split = blockIdx.x;
   const int hgroups = a.heads / 16;
   const bool scorer = wave < kScoreWaves;
+  // Logical workgroup: consecutive ids share an XCD (hardware workgroup b
+  // runs on XCD b % 8), so a row's splits read its q through one L2.
+  const int b = blockIdx.x;
+  const int l = (b % kXcds) * (a.groups / kXcds) + b / kXcds;
+  int t, split, nsplit, first;
+  locate_split<kThreads>(a, l, sm.red, t, split, nsplit, first);
+  if (t < 0) return;
+  if (split == 0 && tid == 0) a.ws_rows[t] = make_int2(first, nsplit);
 
   // q operands of the score waves (A of S = Q K^T): head 16w + col, dims 32ks + 8g .. +8
   bf16x8 qa[KS];
@@ -378,10 +495,10 @@ sparse_decode_kernel(DecodeArgs a) {
   // Prologue: entries -> slots, two dependent gathers (index, block table;
   // one without a block table) each issued for all of the thread's entries
   // first.  The rows' scales come with the rows.
-  int len = a.width;
-  if (a.lengths) len = min(max(a.lengths[t], 0), a.width);
-  const int e_begin = split * a.per_split;
-  const int e_cnt = max(0, min(e_begin + a.per_split, len) - e_begin);
+  const int len = row_len(a, t);
+  const int per_split = ((len + kTile - 1) / kTile + nsplit - 1) / nsplit * kTile;
+  const int e_begin = split * per_split;
+  const int e_cnt = max(0, min(e_begin + per_split, len) - e_begin);
   const int ntiles = (e_cnt + kTile - 1) / kTile;
   const int e_pad = ntiles * kTile;
   // Steps of the main loop: step s finishes tile s-1 and scores tile s, so
@@ -480,35 +597,68 @@ sparse_decode_kernel(DecodeArgs a) {
       __syncthreads();
       for (int s = ntiles + 1; s < steps; ++s) __syncthreads();
     }
-    // final denominators and maxima of this wave's heads
+    // final denominators and maxima of this wave's heads: a row of one split
+    // is finished here (sink, lse), otherwise its partial goes to the combine
     if (wave < hgroups) {
-      const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
+      const int64_t base = static_cast<int64_t>(l) * a.heads;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float l = row16_sum(st.lsum[i]);
+        const float lsum = row16_sum(st.lsum[i]);
         if (col == 0) {
           const int h = 16 * wave + 4 * g + i;
-          sm.row_l[h] = l;
-          a.ws_ml[(base + h) * 2 + 0] = st.m2[i];
-          a.ws_ml[(base + h) * 2 + 1] = l;
+          const float m = st.m2[i];
+          if (nsplit == 1) {
+            float den = lsum, numf = 1.0f;
+            if (a.sinks != nullptr) {
+              const float sk = a.sinks[h] * kLog2e;
+              const float mp = fmaxf(m, sk);
+              if (mp != -INFINITY) {
+                numf = (m == -INFINITY) ? 0.0f : exp2f(m - mp);
+                den = lsum * numf + exp2f(sk - mp);
+              }
+            }
+            sm.row_f[h] = (den > 0.0f) ? numf / den : 0.0f;
+            if (a.lse != nullptr)
+              a.lse[static_cast<int64_t>(t) * a.lse_stride + h] = (lsum > 0.0f) ? (m + log2f(lsum)) * kLn2 : -INFINITY;
+          } else {
+            sm.row_f[h] = (lsum > 0.0f) ? 1.0f / lsum : 0.0f;
+            a.ws_ml[(base + h) * 2 + 0] = m;
+            a.ws_ml[(base + h) * 2 + 1] = lsum;
+          }
         }
       }
     }
   }
   __syncthreads();
 
-  // Epilogue: O / l of the split in fp32 (the combine sums the splits'
-  // partials, which may cancel, so they keep fp32 precision): each store
-  // instruction writes 16 consecutive channels (64 bytes) of one head.
-  const int64_t base = (static_cast<int64_t>(t) * a.splits + split) * a.heads;
+  if (nsplit == 1) {
+    // the finished row in bf16: 16 consecutive channels (32 bytes) of one head
+    // per store instruction
+#pragma unroll
+    for (int hf = 0; hf < 4; ++hf) {
+      if (hf >= hgroups) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 16 * hf + 4 * g + i;
+        const float f = sm.row_f[h];
+        uint16_t* orow = a.out + static_cast<int64_t>(t) * a.out_tok_stride + h * a.out_head_stride + 64 * wave + col;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) orow[16 * nt] = f32_to_bf16(o[hf][nt][i] * f);
+      }
+    }
+    return;
+  }
+  // O / l of the split in fp32 (the combine sums the splits' partials, which
+  // may cancel, so they keep fp32 precision): each store instruction writes
+  // 16 consecutive channels (64 bytes) of one head.
+  const int64_t base = static_cast<int64_t>(l) * a.heads;
 #pragma unroll
   for (int hf = 0; hf < 4; ++hf) {
     if (hf >= hgroups) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 16 * hf + 4 * g + i;
-      const float l = sm.row_l[h];
-      const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
+      const float inv = sm.row_f[h];
       float* orow = a.ws_o + (base + h) * kDv + 64 * wave + col;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) orow[16 * nt] = o[hf][nt][i] * inv;
@@ -516,15 +666,18 @@ sparse_decode_kernel(DecodeArgs a) {
   }
 }
 
-// 256 threads per (t, 4 heads): wave = head, lane = 8 output channels.
+// 256 threads per (t, 4 heads): wave = head, lane = 8 output channels.  Rows
+// finished by their only split are skipped.
 __global__ void __launch_bounds__(256) decode_combine_kernel(
-    const float* ws_o, const float* ws_ml, int32_t splits, int32_t heads, const float* sinks,
+    const float* ws_o, const float* ws_ml, const int2* ws_rows, int32_t heads, const float* sinks,
     uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, float* lse, int64_t lse_stride) {
   const int t = blockIdx.y;
   const int h = 4 * blockIdx.x + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (h >= heads) return;
-  const int64_t b0 = static_cast<int64_t>(t) * splits * heads + h;
+  const int2 rs = ws_rows[t];
+  const int splits = rs.y;
+  if (h >= heads || splits <= 1) return;
+  const int64_t b0 = static_cast<int64_t>(rs.x) * heads + h;
   // Splits in batches of 8 with every load of a batch issued before any is
   // used; a running max rescales the partial sums between batches.
   constexpr int kBatch = 8;
@@ -590,20 +743,21 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
 
 using namespace ekv;
 
-static int decode_splits(int32_t num_tokens, int32_t width) {
-  const int tiles = (width + kTile - 1) / kTile;
-  int splits = (kTargetGroups + num_tokens - 1) / (num_tokens > 0 ? num_tokens : 1);
-  const int need = (width + kMaxSplitEntries - 1) / kMaxSplitEntries;
-  if (splits < need) splits = need;
-  if (splits > tiles) splits = tiles;
-  if (splits < 1) splits = 1;
-  return splits;
+// Workgroups of a call: at least one per CU, and enough that every split
+// holds at most kMaxSplitTiles tiles (G - T >= T * tiles(width) / 32 bounds
+// total_tiles / 32); a multiple of the XCD count.  Monotone in T and width,
+// so a workspace sized for (T, H, width) serves every smaller call.
+static int64_t decode_groups(int32_t num_tokens, int32_t width) {
+  const int64_t tiles = (static_cast<int64_t>(width) + kTile - 1) / kTile;
+  int64_t g = num_tokens + (num_tokens * tiles + kMaxSplitTiles - 1) / kMaxSplitTiles;
+  if (g < kTargetGroups) g = kTargetGroups;
+  return (g + kXcds - 1) / kXcds * kXcds;
 }
 
 extern "C" int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int32_t heads, int32_t width) {
-  if (num_tokens <= 0 || heads <= 0) return 0;
-  const int64_t n = static_cast<int64_t>(num_tokens) * decode_splits(num_tokens, width) * heads;
-  return n * kDv * 4 + n * 2 * 4 + 256;
+  if (num_tokens <= 0 || heads <= 0 || width < 0) return 0;
+  const int64_t n = decode_groups(num_tokens, width) * heads;
+  return n * kDv * 4 + n * 2 * 4 + static_cast<int64_t>(num_tokens) * 8 + 256;
 }
 
 template <int D, bool BF16>
@@ -642,15 +796,17 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
     set_error("workspace too small (see ekv_sparse_mla_decode_workspace_size)");
     return kWorkspaceTooSmall;
   }
-  const int splits = decode_splits(num_tokens, width);
-  const int tiles = (width + kTile - 1) / kTile;
-  const int per_split = ((tiles + splits - 1) / splits) * kTile;
+  const int64_t groups = decode_groups(num_tokens, width);
+  EKV_CHECK(groups < (int64_t{1} << 31), "too many decode workgroups");
   float* ws_o = static_cast<float*>(workspace);
-  float* ws_ml = ws_o + static_cast<int64_t>(num_tokens) * splits * heads * kDv;
+  float* ws_ml = ws_o + groups * heads * kDv;
+  int2* ws_rows = reinterpret_cast<int2*>(ws_ml + groups * heads * 2);
   DecodeArgs a{q, q_tok_stride, q_head_stride, cache, page_stride, num_pages * kPageTokens, indices, idx_stride,
-               width, lengths, block_table, bt_stride, req_ids, scale, heads, per_split, ws_o, ws_ml, splits};
+               width, lengths, block_table, bt_stride, req_ids, scale, heads, num_tokens,
+               static_cast<int32_t>(groups), ws_o, ws_ml, ws_rows, sinks, out, out_tok_stride, out_head_stride,
+               lse, lse_stride};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(splits, num_tokens);
+  const dim3 grid(static_cast<uint32_t>(groups));
   if (dim == 576) {
     if (cache_bf16) launch_decode<576, true>(a, grid, s);
     else launch_decode<576, false>(a, grid, s);
@@ -660,7 +816,7 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   }
   int rc = ekv_launch_status();
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads / 4, num_tokens), dim3(256), 0, s, ws_o, ws_ml, splits,
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(heads / 4, num_tokens), dim3(256), 0, s, ws_o, ws_ml, ws_rows,
                      heads, sinks, out, out_tok_stride, out_head_stride, lse, lse_stride);
   return ekv_launch_status();
 }

@@ -233,6 +233,33 @@ struct FilterArgs {
 };
 
 
+// The filter's approximate dot products: 16 heads (A rows, q codes) x 16
+// tokens (B columns, key codes) over the 128 dims on the fp8 MFMA, as
+// e4m3fn values without scales.  Its error against the exact dot product is
+// what the filter's bound e_s covers (ekv_indexer_filter_dots exposes it).
+__device__ __forceinline__ f32x4 filter_mfma(const i32x8& q, const i32x8& k) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q, k, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+}
+
+// out[s][h] = the filter's MFMA dot product of q row h and key row s (one
+// wave per 16 keys; operands laid out as filter_stream loads them).
+__global__ void __launch_bounds__(64) filter_dots_kernel(const uint8_t* q, const uint8_t* k, float* out) {
+  const int lane = threadIdx.x, g = lane >> 4, col = lane & 15;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * 16;
+  auto load8 = [](const uint8_t* p) {
+    const uint4 v0 = reinterpret_cast<const uint4*>(p)[0], v1 = reinterpret_cast<const uint4*>(p)[1];
+    return i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
+                 static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
+  };
+  const i32x8 kv = load8(k + (s0 + col) * kIdxDim + 32 * g);
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    const f32x4 cc = filter_mfma(load8(q + (16 * hb + col) * kIdxDim + 32 * g), kv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[(s0 + col) * kIdxHeads + 16 * hb + 4 * g + i] = cc[i];
+  }
+}
+
 // Block-wide exclusive prefix sum of an int; writes the block total.
 template <int kThreads>
 __device__ __forceinline__ int block_scan_excl(int v, int* s_wave, int& total) {
@@ -383,8 +410,7 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
       float acc = 0.0f;
 #pragma unroll
       for (int hb = 0; hb < 4; ++hb) {
-        const f32x4 cc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[hb], kv, f32x4{0.f, 0.f, 0.f, 0.f},
-                                                                           0, 0, 0, 0, 0, 0);
+        const f32x4 cc = filter_mfma(qa[hb], kv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc += wv[hb][i] * fmaxf(cc[i], 0.0f);
       }
@@ -1442,7 +1468,7 @@ namespace {
 
 void launch_select(const SelectArgs& a, int32_t rows, hipStream_t s) {
   const int smem = static_cast<int>(sizeof(SelectSmem));
-  hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(topk_select_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                       smem);
   hipLaunchKernelGGL(topk_select_kernel, dim3(rows), dim3(kSelThreads), smem, s, a);
 }
@@ -1594,6 +1620,17 @@ extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const u
               scores, scores_stride, max_len};
   dim3 grid((max_len + kScoreChunk - 1) / kScoreChunk, num_tokens);
   hipLaunchKernelGGL(score_exact_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_filter_dots(const uint8_t* q_codes, const uint8_t* k_codes, int32_t num_keys,
+                                       float* out, void* stream) {
+  EKV_CHECK(num_keys >= 0 && num_keys % 16 == 0, "num_keys must be a multiple of 16");
+  if (num_keys == 0) return 0;
+  EKV_CHECK(q_codes && k_codes && out, "null pointer");
+  EKV_CHECK(aligned16(q_codes) && aligned16(k_codes), "misaligned buffers");
+  hipLaunchKernelGGL(filter_dots_kernel, dim3(num_keys / 16), dim3(64), 0, static_cast<hipStream_t>(stream), q_codes,
+                     k_codes, out);
   return ekv_launch_status();
 }
 

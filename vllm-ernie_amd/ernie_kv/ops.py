@@ -389,6 +389,21 @@ def topk_select(scores: torch.Tensor, lengths: torch.Tensor, k: int, out: torch.
     )
 
 
+def indexer_filter_dots(q_codes: torch.Tensor, k_codes: torch.Tensor) -> torch.Tensor:
+    """The indexer filter's fp8-MFMA dot products ``[S, 64]`` of e4m3fn codes
+    ``q_codes [64, 128]`` and ``k_codes [S, 128]`` (S a multiple of 16), by
+    the filter's own MFMA call (a diagnostic of its error bound)."""
+    _check_dev(q_codes, k_codes)
+    _need(q_codes.shape == (64, 128) and q_codes.dtype == torch.uint8 and q_codes.is_contiguous(), "q_codes [64, 128]")
+    _need(k_codes.dim() == 2 and k_codes.shape[1] == 128 and k_codes.dtype == torch.uint8 and k_codes.is_contiguous(),
+          "k_codes [S, 128] uint8")
+    _need(k_codes.shape[0] % 16 == 0, "S must be a multiple of 16")
+    out = torch.empty((k_codes.shape[0], 64), dtype=torch.float32, device=k_codes.device)
+    _lib.call("ekv_indexer_filter_dots", q_codes.data_ptr(), k_codes.data_ptr(), k_codes.shape[0], out.data_ptr(),
+              _stream())
+    return out
+
+
 def indexer_topk_workspace(num_tokens: int, max_len: int, device) -> torch.Tensor:
     """Zero-filled workspace for the indexer top-k calls of up to
     ``num_tokens`` rows of ``max_len`` tokens (the calls keep its counters
@@ -476,8 +491,10 @@ def indexer_topk(
 
 # --------------------------------------------------------------------------- decode
 def decode_workspace(num_tokens: int, heads: int, width: int, device) -> torch.Tensor:
-    """Workspace for ``sparse_mla_decode`` calls up to this shape (the split
-    partials: O / l and (m, l) in fp32 per row, split and head)."""
+    """Workspace for every ``sparse_mla_decode`` call of at most ``num_tokens``
+    rows, ``heads`` heads and ``width`` index entries (the split partials:
+    O / l and (m, l) in fp32 per split and head, and each row's split
+    range).  A call given a smaller workspace raises; none allocates."""
     need = _lib.load().ekv_sparse_mla_decode_workspace_size(num_tokens, heads, width)
     return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
 
@@ -513,9 +530,12 @@ def sparse_mla_decode(
         num_pages, page_stride = cache.shape[0], _rs(cache)
     if sinks is not None:
         _need(sinks.dtype == torch.float32 and sinks.numel() >= H, "sinks fp32 [H]")
-    need = _lib.load().ekv_sparse_mla_decode_workspace_size(T, H, idx.shape[1])
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:
         workspace = decode_workspace(T, H, idx.shape[1], q.device)
+    else:
+        need = _lib.load().ekv_sparse_mla_decode_workspace_size(T, H, idx.shape[1])
+        _need(workspace.dtype == torch.uint8 and workspace.is_contiguous() and workspace.numel() >= need,
+              f"decode workspace too small: {workspace.numel()} < {need} bytes")
     _lib.call(
         "ekv_sparse_mla_decode", q.data_ptr(), _rs(q), q.stride(1), T, H, D, cache.data_ptr(),
         int(cache_bf16), page_stride, num_pages, idx.data_ptr(), _rs(idx), idx.shape[1], _ptr(lengths),
