@@ -114,16 +114,20 @@ int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t*
                   int64_t num_pages, void* stream);
 
 /*
- * HCA decode index rows: [compressed slots 0..n_c-1 | ring slots of positions
- * p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window), and the row
- * lengths.  Replaces the compressed+window index construction inside
+ * HCA decode index rows: [compressed slots 0..n_c-1 | window slots of
+ * positions p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window),
+ * and the row lengths.  Window slots are ring slots; with query_start_loc
+ * [B+1] and slot_mapping [T] of the call (both or neither), positions at or
+ * after the first call position of the row's request take that token's
+ * slot_mapping slot instead (a prefill chunk longer than the ring reads its
+ * own rows).  Replaces the compressed+window index construction inside
  * DeepseekV4Attention (nvidia/attention.py:471-539).
  */
 int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
                            const int32_t* comp_block_table, int32_t comp_bt_stride,
                            const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window,
-                           int32_t* out, int64_t out_stride, int32_t width, int32_t* lengths,
-                           void* stream);
+                           const int32_t* query_start_loc, const int64_t* slot_mapping, int32_t* out,
+                           int64_t out_stride, int32_t width, int32_t* lengths, void* stream);
 
 /*
  * merge_swa_topk: out[t] = [topk[t][:n] | seq-w .. seq-1 | -1 ...] with

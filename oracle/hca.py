@@ -262,8 +262,13 @@ def hca_decode_indices(
     ring: int,
     width: int,
     window: int = WINDOW,
+    call_qsl: np.ndarray | None = None,
+    call_slots: np.ndarray | None = None,
 ) -> tuple[np.ndarray, np.ndarray]:
-    """Global slots ``[comp 0..n_c-1 | window p-w+1..p | -1...]`` and lengths."""
+    """Global slots ``[comp 0..n_c-1 | window p-w+1..p | -1...]`` and lengths.
+    With the call's ``call_qsl`` / ``call_slots``, window positions at or
+    after the first call position of the row's request are that token's
+    slot, older ones ring slots."""
     T = len(positions)
     out = np.full((T, width), -1, dtype=np.int32)
     lens = np.zeros(T, dtype=np.int32)
@@ -275,8 +280,14 @@ def hca_decode_indices(
         assert n_c + w <= width
         for j in range(n_c):
             out[t, j] = comp_slot(comp_block_table, b, j)
+        first = int(positions[int(call_qsl[b])]) if call_slots is not None else None
         for i in range(w):
-            out[t, n_c + i] = ring_slot(ring_pages, b, p - w + 1 + i, ring)
+            q = p - w + 1 + i
+            if first is not None and q >= first:
+                s = int(call_slots[int(call_qsl[b]) + q - first])
+                out[t, n_c + i] = s if s >= 0 else -1
+            else:
+                out[t, n_c + i] = ring_slot(ring_pages, b, q, ring)
         lens[t] = n_c + w
     return out, lens
 

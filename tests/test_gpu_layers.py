@@ -1,0 +1,327 @@
+"""GPU parity of the layer-level drop-in surface (ernie_kv/attention.py):
+Ernie5_5Indexer.forward, Ernie5_5DSAAttention._indexer_and_attn, the HCA
+layer's _prepare_and_attn_fn, the sparse impl's _fp8/_bf16 kernel methods
+and Ernie5_5IndexerMetadataBuilder.build, each against the oracle.
+
+The layers' projections are plain torch GEMMs outside the path: the tests
+recompute them with the same torch calls on the same inputs (bit-identical
+on one device) and start the oracle from their outputs."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_tensor, bf16_values, permuted_block_table, randn_bf16, to_dev
+from oracle import decode as od
+from oracle import hca as oh
+from oracle import indexer as oi
+from oracle import paged
+from oracle.fp8 import quantize_rows
+from oracle.merge import logical_to_global, merge_swa_topk
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 2e-2, 2e-3
+TOPK, WINDOW = 2048, 128
+
+
+def wc_decode(codes, scale):
+    from oracle.fp8 import decode_e4m3
+
+    return decode_e4m3(codes).astype(np.float64) * scale.astype(np.float64)[:, None]
+
+
+def _check_decode(got, ref_o, what):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref_o)
+    bad = err > ATOL + RTOL * np.abs(ref_o)
+    assert not bad.any(), f"{what}: max err {err.max()} at {np.argwhere(bad)[0]}"
+
+
+def _dsa_setup(dev, rng, ctxs, rows_per_req):
+    """Caches pre-filled up to each request's context, plus the step's query
+    rows (the last rows_per_req positions of each request)."""
+    from ernie_kv import attention as A
+
+    cfg = A.ernie5_5_config(hidden_size=256, hybrid_mla_q_lora_rank=128)
+    B = len(ctxs)
+    P = max((c + 63) // 64 for c in ctxs)
+    bt = permuted_block_table(rng, B, P)
+    pages = B * P
+    kc = oi.kcache_pages(pages)
+    lat = np.zeros((pages, paged.fp8_page_bytes(576)), np.uint8)
+    for b, c in enumerate(ctxs):
+        s = np.arange(c - rows_per_req[b])  # the step writes the last rows itself
+        slots = bt[b, s // 64].astype(np.int64) * 64 + s % 64
+        oi.k_insert(kc, randn_bf16(rng, (len(s), 128)), slots)
+        codes, scale = quantize_rows(randn_bf16(rng, (len(s), 576)))
+        paged.write_fp8_rows(lat, slots, codes, scale, 576)
+    req = np.concatenate([np.full(r, b, np.int32) for b, r in enumerate(rows_per_req)])
+    positions = np.concatenate([np.arange(c - r, c) for c, r in zip(ctxs, rows_per_req)]).astype(np.int64)
+    slot_mapping = paged.slots_from_block_table(bt, req, positions)
+    T = len(positions)
+    params = {
+        "indexer.wq_b": bf16_tensor(randn_bf16(rng, (64 * 128, 128), 128 ** -0.5), dev),
+        "indexer.wk_weights_proj": bf16_tensor(randn_bf16(rng, (128 + 64, 256), 256 ** -0.5), dev),
+        "indexer.k_norm.weight": to_dev((1 + 0.1 * rng.standard_normal(128)).astype(np.float32), dev),
+        "indexer.k_norm.bias": to_dev((0.1 * rng.standard_normal(128)).astype(np.float32), dev),
+        "kv_b_proj": bf16_tensor(randn_bf16(rng, (64 * (192 + 256), 512), 0.05), dev),
+        "attn_sink": to_dev(rng.standard_normal(64).astype(np.float32), dev),
+    }
+    md = A.DSAStepMetadata(slot_mapping=to_dev(slot_mapping, dev), block_table=to_dev(bt, dev),
+                           req_ids=to_dev(req, dev), max_seq_len=int(max(ctxs)))
+    inputs = dict(hidden=randn_bf16(rng, (T, 256)), q_c=randn_bf16(rng, (T, 128)), q=randn_bf16(rng, (T, 64, 256)),
+                  kv_c=randn_bf16(rng, (T, 512)), k_pe=randn_bf16(rng, (T, 1, 64)))
+    return SimpleNamespace(cfg=cfg, bt=bt, kc=kc, lat=lat, req=req, positions=positions, slot_mapping=slot_mapping,
+                           T=T, params=params, md=md, inputs=inputs)
+
+
+def _oracle_indexer(case, layer, dev):
+    """The oracle's indexer from the layer's projection outputs: returns the
+    K cache after the insert, the top-k and the windowed lengths."""
+    hid = bf16_tensor(case.inputs["hidden"], dev)
+    qc = bf16_tensor(case.inputs["q_c"], dev)
+    iq, ik, iw = layer._project(hid, qc)
+    table = layer._prep_args(dev)[3]
+    pos = case.positions
+    rq, rk = oi.indexer_prep(bf16_values(iq), bf16_values(ik), layer.k_norm_weight.cpu().numpy(),
+                             layer.k_norm_bias.cpu().numpy(), 1e-6, table[to_dev(pos, dev)].cpu().numpy())
+    codes, wf = oi.quantize_q(rq, bf16_values(iw))
+    kc = case.kc.copy()
+    oi.k_insert(kc, rk, case.slot_mapping)
+    lens = oi.windowed_lengths(pos, WINDOW)
+    top, _ = oi.indexer_topk(codes, wf, kc, case.bt, case.req, lens, TOPK)
+    return kc, top
+
+
+def test_indexer_forward_vs_oracle(dev):
+    """Ernie5_5Indexer.forward (attention.py:955-984): projections, prep,
+    quant, K insert and the exact top-k into indexer_op.topk_indices_buffer."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(61)
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
+    swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
+    p = case.params
+    ix = A.Ernie5_5Indexer(case.cfg, topk_buf, swa_buf, prefix="model.layers.3.attn.indexer",
+                           wq_b=p["indexer.wq_b"], wk_weights_proj=p["indexer.wk_weights_proj"],
+                           k_norm_weight=p["indexer.k_norm.weight"], k_norm_bias=p["indexer.k_norm.bias"])
+    ix.k_cache.kv_cache = to_dev(case.kc, dev)
+    with A.set_forward_context({ix.k_cache.prefix: case.md}):
+        got = ix.forward(bf16_tensor(case.inputs["hidden"], dev), bf16_tensor(case.inputs["q_c"], dev),
+                         to_dev(case.positions, dev))
+    torch.cuda.synchronize()
+    kc_ref, top_ref = _oracle_indexer(case, ix, dev)
+    assert np.array_equal(ix.k_cache.kv_cache.cpu().numpy(), kc_ref), "indexer K cache bytes differ"
+    assert np.array_equal(got.cpu().numpy(), top_ref), "top-k differs"
+    assert (swa_buf == -7).all(), "forward alone must not touch the merged (swa) buffer"
+
+
+def test_dsa_indexer_and_attn_vs_oracle(dev):
+    """Ernie5_5DSAAttention._indexer_and_attn (attention.py:1205-1226): top-k,
+    merged rows, both caches' bytes, the sparse decode's latent output and
+    the up-projected out."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(62)
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    T = case.T
+    topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
+    swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
+    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params)
+    layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
+    layer.mla_attn.kv_cache = to_dev(case.lat, dev)
+    captured = {}
+    orig = layer.mla_attn.impl._fp8_flash_mla_kernel
+
+    def spy(*args, **kwargs):
+        captured["out"] = orig(*args, **kwargs)
+        return captured["out"]
+
+    layer.mla_attn.impl._fp8_flash_mla_kernel = spy
+    inp = case.inputs
+    out = torch.zeros((T, 64 * 256), dtype=torch.bfloat16, device=dev)
+    meta = {layer.mla_attn.prefix: case.md, layer.indexer.k_cache.prefix: case.md}
+    pos_t = to_dev(case.positions, dev)
+    with A.set_forward_context(meta):
+        layer._indexer_and_attn(bf16_tensor(inp["hidden"], dev), bf16_tensor(inp["q_c"], dev), pos_t,
+                                bf16_tensor(inp["q"], dev), bf16_tensor(inp["kv_c"], dev),
+                                bf16_tensor(inp["k_pe"], dev), out)
+    torch.cuda.synchronize()
+    kc_ref, top_ref = _oracle_indexer(case, layer.indexer, dev)
+    assert np.array_equal(layer.indexer.k_cache.kv_cache.cpu().numpy(), kc_ref), "indexer K cache bytes differ"
+    assert np.array_equal(topk_buf[:T].cpu().numpy(), top_ref), "top-k differs"
+    merged_ref = merge_swa_topk(top_ref, case.positions, TOPK + WINDOW, WINDOW)
+    assert np.array_equal(swa_buf[:T].cpu().numpy(), merged_ref), "merged rows differ"
+    lat = case.lat.copy()
+    rows = np.concatenate([inp["kv_c"], inp["k_pe"].reshape(T, 64)], axis=1)
+    codes, scale = quantize_rows(rows)
+    paged.write_fp8_rows(lat, case.slot_mapping, codes, scale, 576)
+    assert np.array_equal(layer.mla_attn.kv_cache.cpu().numpy(), lat), "latent cache bytes differ"
+    q_abs = bf16_values(layer.mla_attn.absorb_q(bf16_tensor(inp["q"], dev)))
+    glob = logical_to_global(merged_ref, case.req, case.bt)
+    ref_o, ref_l = od.sparse_mla_decode(q_abs, lambda s: od.gather_rows_fp8(lat, s, 576), glob, 256 ** -0.5, 512,
+                                        case.params["attn_sink"].cpu().numpy())
+    o_lat, lse = captured["out"]
+    o_lat = bf16_values(o_lat[:, 0])
+    _check_decode(o_lat, ref_o, "latent decode output")
+    fin = np.isfinite(ref_l)
+    assert np.all(np.abs(lse[:, 0].cpu().numpy()[fin] - ref_l[fin]) <= 2e-3 * np.maximum(1, np.abs(ref_l[fin])))
+    w_uv = layer.mla_attn.W_UV_T.float().cpu().numpy().astype(np.float64)  # [H, 512, 256]
+    ref_out = np.einsum("thc,hcv->thv", o_lat.astype(np.float64), w_uv).reshape(T, -1)
+    mag = np.einsum("thc,hcv->thv", np.abs(o_lat.astype(np.float64)), np.abs(w_uv)).reshape(T, -1)
+    got = bf16_values(out).astype(np.float64)
+    assert np.all(np.abs(got - ref_out) <= 8e-3 * mag + 1e-6), "up-projected out differs"
+
+
+def test_hca_prepare_and_attn_vs_oracle(dev):
+    """The HCA layer's cache write + decode (attention.py:471-539): a
+    prefill chunk then a decode step with one and three query rows; pool
+    and state bytes exact, o_padded within tolerance."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(63)
+    D, H, B, ring = 512, 64, 2, 192
+    cfg = A.ernie5_5_config()
+    lp, cp, rp = 8, 1, ring // 64
+    perm = rng.permutation(B * (lp + cp + rp)).astype(np.int32)
+    bt = perm[: B * lp].reshape(B, lp)
+    comp_bt = perm[B * lp: B * (lp + cp)].reshape(B, cp)
+    ring_pages = perm[B * (lp + cp):].reshape(B, rp)
+    pages = len(perm)
+    params = {"attn_sink": to_dev(rng.standard_normal(H).astype(np.float32), dev),
+              "compressor.ape": to_dev((rng.standard_normal((128, D)) * 0.5).astype(np.float32), dev),
+              "compressor.norm.weight": to_dev((1 + 0.1 * rng.standard_normal(D)).astype(np.float32), dev)}
+    cos_sin = oi.yarn_cos_sin(np.arange(8) * 128, 64, cfg.compress_rope_theta)
+    layer = A.select_ernie5_5_hca_cls("fp8")(cfg, "model.layers.0.attn", params=params, ring=ring,
+                                             compress_cos_sin=to_dev(cos_sin, dev))
+    layer.kv_cache = torch.zeros((pages, paged.fp8_page_bytes(D)), dtype=torch.uint8, device=dev)
+    layer.state_cache = torch.zeros((B, 256, 2 * D), dtype=torch.bfloat16, device=dev)
+    st = oh.HcaState(pages, D, B)
+    state_slot = np.arange(B, dtype=np.int32)
+    sinks = params["attn_sink"].cpu().numpy()
+    pos0 = [0, 0]
+    hist = {0: [], 1: []}  # latent rows by position, per request
+    for counts in ([300, 257], [1, 3], [70, 2]):
+        positions = np.concatenate([np.arange(p, p + n) for p, n in zip(pos0, counts)]).astype(np.int64)
+        token_seq = np.concatenate([np.full(n, b, np.int32) for b, n in enumerate(counts)])
+        qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        T = len(positions)
+        slots = paged.slots_from_block_table(bt, token_seq, positions)
+        kv = randn_bf16(rng, (T, D))
+        kv_score = randn_bf16(rng, (T, 2 * D))
+        q = randn_bf16(rng, (T, H, D))
+        md = A.HCAStepMetadata(slot_mapping=to_dev(slots, dev), query_start_loc=to_dev(qsl, dev),
+                               token_seq=to_dev(token_seq, dev), max_query_len=int(max(counts)),
+                               comp_block_table=to_dev(comp_bt, dev), ring_pages=to_dev(ring_pages, dev),
+                               state_slot=to_dev(state_slot, dev), max_seq_len=int(positions.max()) + 1)
+        o_padded = torch.zeros((T, 64, D), dtype=torch.bfloat16, device=dev)
+        with A.set_forward_context({layer.prefix: md}):
+            layer._prepare_and_attn_fn(bf16_tensor(q, dev), bf16_tensor(kv, dev), bf16_tensor(kv_score, dev),
+                                       to_dev(positions, dev), o_padded)
+        torch.cuda.synchronize()
+        oh.hca_write(st, kv, kv_score, positions, token_seq, qsl, slots, ring_pages, ring, comp_bt, state_slot,
+                     params["compressor.ape"].cpu().numpy(), params["compressor.norm.weight"].cpu().numpy(),
+                     cfg.rms_norm_eps, cos_sin)
+        assert np.array_equal(layer.kv_cache.cpu().numpy(), st.pool), f"pool bytes differ after {counts}"
+        assert np.array_equal(bf16_values(layer.state_cache).reshape(st.state.shape), st.state)
+        for t in range(T):
+            hist[int(token_seq[t])].append(kv[t])
+        # each row attends its request's compressed entries 0..n_c-1 (as the
+        # pool holds them) and the latent rows of its last w positions (by
+        # content: the quantized rows written at those positions)
+        ref_o = np.zeros((T, H, 512))
+        for t in range(T):
+            p, b = int(positions[t]), int(token_seq[t])
+            n_c, w = (p + 1) // 128, min(p + 1, WINDOW)
+            comp = od.gather_rows_fp8(st.pool, np.array([oh.comp_slot(comp_bt, b, j) for j in range(n_c)], np.int64),
+                                      D) if n_c else np.zeros((0, D))
+            wc, ws_ = quantize_rows(np.stack(hist[b][p - w + 1: p + 1]))
+            kv_rows = np.concatenate([comp, wc_decode(wc, ws_)])
+            ref_o[t] = od.sparse_mla_decode(q[t:t + 1], lambda s: kv_rows[s], np.arange(len(kv_rows))[None],
+                                            D ** -0.5, 512, sinks)[0][0]
+        _check_decode(bf16_values(o_padded), ref_o, f"o_padded after {counts}")
+        pos0 = [p + n for p, n in zip(pos0, counts)]
+
+
+@pytest.mark.parametrize("heads,padded", [(64, 64), (16, 64)])
+def test_fp8_flash_mla_kernel_method(dev, heads, padded):
+    """Ernie5_5FlashMLASparseImpl._fp8_flash_mla_kernel (attention.py:723-749):
+    q [batch, seq, heads, 576], global indices, heads padded with -inf sinks."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(64 + heads)
+    pages = 30
+    rows = randn_bf16(rng, (pages * 64, 576))
+    pool = np.zeros((pages, paged.fp8_page_bytes(576)), np.uint8)
+    codes, scale = quantize_rows(rows)
+    paged.write_fp8_rows(pool, np.arange(pages * 64), codes, scale, 576)
+    b, s, W = 3, 1, 2176
+    idx = rng.integers(0, pages * 64, (b, s, W)).astype(np.int32)
+    idx[1, 0, 1000:] = -1
+    q = randn_bf16(rng, (b, s, heads, 576))
+    sinks = rng.standard_normal(heads).astype(np.float32)
+    impl = A.Ernie5_5FlashMLASparseImpl(heads, 576, 256 ** -0.5, sinks=to_dev(sinks, dev),
+                                        fp8_decode_padded_heads=padded)
+    out, lse = impl._fp8_flash_mla_kernel(bf16_tensor(q, dev), to_dev(pool, dev), to_dev(idx, dev), None)
+    assert out.shape == (b, s, heads, 512) and lse.shape == (b, s, heads)
+    ref_o, ref_l = od.sparse_mla_decode(q.reshape(b * s, heads, 576), lambda sl: od.gather_rows_fp8(pool, sl, 576),
+                                        idx.reshape(b * s, W), 256 ** -0.5, 512, sinks)
+    _check_decode(bf16_values(out).reshape(b * s, heads, 512), ref_o, "fp8 kernel method")
+    assert np.all(np.abs(lse.cpu().numpy().reshape(b * s, heads) - ref_l) <= 2e-3 * np.maximum(1, np.abs(ref_l)))
+
+
+def test_bf16_flash_mla_kernel_method(dev):
+    """_bf16_flash_mla_kernel (attention.py:751-789): flat bf16 rows viewed as
+    [-1, 1, 576], topk_length, actual_num_heads padded to 16, caller's out."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(65)
+    N, T, W, H = 64 * 12, 5, 300, 12
+    cache = randn_bf16(rng, (N, 576))
+    idx = rng.integers(0, N, (T, W)).astype(np.int32)
+    lens = np.array([300, 1, 0, 150, 299], np.int32)
+    q = randn_bf16(rng, (T, H, 576))
+    sinks = rng.standard_normal(16).astype(np.float32)
+    impl = A.Ernie5_5FlashMLASparseImpl(16, 576, 256 ** -0.5, sinks=to_dev(sinks, dev), prefill_padding=16)
+    out = torch.zeros((T, 16, 512), dtype=torch.bfloat16, device=dev)
+    o, lse = impl._bf16_flash_mla_kernel(bf16_tensor(q, dev), bf16_tensor(cache, dev).view(N, 1, 576),
+                                         to_dev(idx, dev), topk_length=to_dev(lens, dev), actual_num_heads=H, out=out)
+    assert o.shape == (T, H, 512)
+    ref_o, _ = od.sparse_mla_decode(q, lambda sl: od.gather_rows_bf16(cache, sl), idx, 256 ** -0.5, 512, sinks[:H],
+                                    lens)
+    _check_decode(bf16_values(o), ref_o, "bf16 kernel method")
+
+
+def test_indexer_metadata_builder_build(dev):
+    """Ernie5_5IndexerMetadataBuilder.build (attention.py:652-691) with a stub
+    parent build: prefill chunk ends pulled in by the window (never below
+    the chunk start), decode seq_lens [num_reqs] and [num_reqs, next_n]
+    windowed to max(seq_len - 128, 0), compared with the reference's torch
+    expressions; too many decode entries are refused."""
+    from ernie_kv import attention as A
+
+    ks = torch.tensor([0, 0, 500, 1000], dtype=torch.int32, device=dev)
+    ke = torch.tensor([1, 129, 700, 5000], dtype=torch.int32, device=dev)
+    cases = [torch.tensor([0, 1, 127, 128, 129, 5000, 131072], dtype=torch.int32, device=dev),
+             torch.tensor([[126, 127], [128, 129], [4000, 4001]], dtype=torch.int32, device=dev)]
+    for seq_lens in cases:
+        def base_build(prefix_len, common, fast_build, seq_lens=seq_lens):
+            return A.IndexerMetadata(prefill=A.IndexerPrefill(chunks=[A.IndexerPrefillChunk(ks.clone(), ke.clone())]),
+                                     decode=A.IndexerDecode(seq_lens=seq_lens.clone()))
+        builder = A.Ernie5_5IndexerMetadataBuilder(WINDOW, max_num_reqs=8, device=dev, base_build=base_build,
+                                                   max_query_len=3)
+        md = builder.build(0, None)
+        torch.cuda.synchronize()
+        ref = torch.sub(seq_lens, WINDOW)
+        ref.clamp_min_(0)
+        assert md.decode.seq_lens.shape == seq_lens.shape
+        assert torch.equal(md.decode.seq_lens, ref)
+        assert torch.equal(md.prefill.chunks[0].cu_seqlen_ke, torch.maximum(ke - WINDOW, ks))
+    small = A.Ernie5_5IndexerMetadataBuilder(
+        WINDOW, max_num_reqs=2, device=dev,
+        base_build=lambda *a: A.IndexerMetadata(decode=A.IndexerDecode(seq_lens=cases[0].clone())))
+    with pytest.raises(ValueError):
+        small.build(0, None)

@@ -230,13 +230,18 @@ __global__ void windowed_lengths_kernel(const int64_t* positions, int32_t n, int
   if (i < n) out[i] = static_cast<int32_t>(max(positions[i] + 1 - window, static_cast<int64_t>(0)));
 }
 
+// Window entries of positions at or after the first position of the row's
+// request in this call come from the call's own slots (call_slots, by the
+// request's qsl range) when call_slots is given, others from the ring.
 __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
     const int64_t* positions, const int32_t* req_ids, const int32_t* comp_bt, int32_t comp_bt_stride,
-    const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window, int32_t* out,
-    int64_t out_stride, int32_t width, int32_t* lengths) {
+    const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window, const int32_t* qsl,
+    const int64_t* call_slots, int32_t* out, int64_t out_stride, int32_t width, int32_t* lengths) {
   const int64_t t = blockIdx.x;
   const int64_t p = positions[t];
   const int64_t b = req_ids[t];
+  const int64_t t0 = call_slots ? qsl[b] : 0;
+  const int64_t call_first = call_slots ? positions[t0] : INT64_MAX;
   const int64_t nc = (p + 1) / kSpan;
   const int64_t w = min(p + 1, static_cast<int64_t>(window));
   const int64_t len = min(nc + w, static_cast<int64_t>(width));
@@ -246,8 +251,13 @@ __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
       v = static_cast<int64_t>(comp_bt[b * comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
     } else if (c < len) {
       const int64_t pos = p - w + 1 + (c - nc);
-      const int64_t r = pos % ring;
-      v = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
+      if (pos >= call_first) {
+        v = call_slots[t0 + (pos - call_first)];
+        v = v < 0 ? -1 : v;
+      } else {
+        const int64_t r = pos % ring;
+        v = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
+      }
     }
     out[t * out_stride + c] = static_cast<int32_t>(v);
   }
@@ -511,15 +521,18 @@ extern "C" int ekv_indexer_windowed_lengths(const int64_t* positions, int32_t nu
 extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
                                       const int32_t* comp_block_table, int32_t comp_bt_stride,
                                       const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
-                                      int32_t window, int32_t* out, int64_t out_stride, int32_t width,
-                                      int32_t* lengths, void* stream) {
+                                      int32_t window, const int32_t* query_start_loc,
+                                      const int64_t* slot_mapping, int32_t* out, int64_t out_stride,
+                                      int32_t width, int32_t* lengths, void* stream) {
   EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
   if (num_tokens == 0) return 0;
   EKV_CHECK(positions && req_ids && comp_block_table && ring_pages && out && lengths, "null pointer");
   EKV_CHECK(ring >= window && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
+  EKV_CHECK((query_start_loc == nullptr) == (slot_mapping == nullptr),
+            "query_start_loc and slot_mapping go together");
   hipLaunchKernelGGL(hca_decode_indices_kernel, dim3(num_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
                      positions, req_ids, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
-                     window, out, out_stride, width, lengths);
+                     window, query_start_loc, slot_mapping, out, out_stride, width, lengths);
   return ekv_launch_status();
 }
 

@@ -11,6 +11,7 @@ with the fields the path reads.
 
 from __future__ import annotations
 
+import contextlib
 import dataclasses
 import enum
 import math
@@ -136,19 +137,33 @@ class Ernie5_5FlashMLASparseImpl(FlashMLASparseImplBase):
         self, q: torch.Tensor, kv_c_and_k_pe_cache: torch.Tensor, topk_indices: torch.Tensor,
         kernel_metadata: Any = None,
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """q [batch, seq_len, heads, 576]; cache uint8 pages; global indices
-        [batch, seq_len, width] (the reference passes a dummy block table)."""
+        """q [batch, seq_len, heads, 576]; cache uint8 pages; indices
+        [batch, seq_len, width].  As in the reference (dummy block table),
+        the indices are global cache slots; a ``kernel_metadata`` carrying
+        ``block_table`` and ``req_ids`` instead marks them request-local, and
+        the kernel converts them through the block table.  Heads are padded
+        with zero q rows and -inf sinks to ``fp8_decode_padded_heads``."""
         b, s, h, d = q.shape
+        padded = max(self.fp8_decode_padded_heads, h)
+        padded = (padded + 15) // 16 * 16
         flat_q = q.reshape(b * s, h, d)
-        idx = topk_indices.reshape(b * s, -1).to(torch.int32)
-        out = torch.empty((b * s, h, 512), dtype=q.dtype, device=q.device)
-        lse = torch.empty((b * s, h), dtype=torch.float32, device=q.device)
+        if padded > h:
+            qp = q.new_zeros((b * s, padded, d))
+            qp[:, :h] = flat_q
+            flat_q = qp
+        idx = topk_indices.reshape(b * s, -1)
+        if idx.dtype != torch.int32:
+            idx = idx.to(torch.int32)
+        out = torch.empty((b * s, padded, 512), dtype=q.dtype, device=q.device)
+        lse = torch.empty((b * s, padded), dtype=torch.float32, device=q.device)
         cache = kv_c_and_k_pe_cache.view(torch.uint8)
         cache = cache.reshape(cache.shape[0], -1)
-        ws = self._ws(ops._lib.load().ekv_sparse_mla_decode_workspace_size(b * s, h, idx.shape[1]), q.device)
-        ops.sparse_mla_decode(flat_q, cache, idx, self.softmax_scale, out, lse,
-                              sinks=self._padded_sinks(h), workspace=ws)
-        return out.view(b, s, h, 512), lse.view(b, s, h)
+        ws = self._ws(ops._lib.load().ekv_sparse_mla_decode_workspace_size(b * s, padded, idx.shape[1]), q.device)
+        bt = getattr(kernel_metadata, "block_table", None)
+        req = getattr(kernel_metadata, "req_ids", None)
+        ops.sparse_mla_decode(flat_q, cache, idx, self.softmax_scale, out, lse, sinks=self._padded_sinks(padded),
+                              block_table=bt, req_ids=req, workspace=ws)
+        return out[:, :h].reshape(b, s, h, 512), lse[:, :h].reshape(b, s, h)
 
     def _bf16_flash_mla_kernel(
         self, q: torch.Tensor, kv_c_and_k_pe_cache: torch.Tensor, topk_indices: torch.Tensor,
@@ -222,14 +237,17 @@ class IndexerMetadata:
 class Ernie5_5IndexerMetadataBuilder:
     """Excludes the trailing sliding window from the indexer KV range
     (attention.py:644-691).  ``base_build`` stands in for the vLLM parent's
-    ``build`` and must return an ``IndexerMetadata``."""
+    ``build`` and must return an ``IndexerMetadata``.  The decode seq_lens
+    buffers hold ``max_num_reqs * max_query_len`` entries: decode seq_lens
+    are ``[num_reqs]``, or ``[num_reqs, next_n]`` with draft tokens."""
 
-    def __init__(self, window: int, max_num_reqs: int, device, base_build=None) -> None:
+    def __init__(self, window: int, max_num_reqs: int, device, base_build=None, max_query_len: int = 1) -> None:
         self.window = window
         self.base_build = base_build
-        self.decode_seq_lens_buffer = torch.zeros(max_num_reqs, dtype=torch.int32, device=device)
+        n = max_num_reqs * max(1, max_query_len)
+        self.decode_seq_lens_buffer = torch.zeros(n, dtype=torch.int32, device=device)
         self.windowed_seq_lens_buffer = torch.zeros_like(self.decode_seq_lens_buffer)
-        self._positions = torch.zeros(max_num_reqs, dtype=torch.int64, device=device)
+        self._positions = torch.zeros(n, dtype=torch.int64, device=device)
 
     def build(self, common_prefix_len: int, common_attn_metadata, fast_build: bool = False) -> IndexerMetadata:
         metadata = self.base_build(common_prefix_len, common_attn_metadata, fast_build)
@@ -243,6 +261,9 @@ class Ernie5_5IndexerMetadataBuilder:
         if metadata.decode is not None:
             seq_lens = metadata.decode.seq_lens
             n = seq_lens.numel()
+            if n > self.windowed_seq_lens_buffer.numel():
+                raise ValueError(f"decode seq_lens has {n} entries; the builder holds "
+                                 f"{self.windowed_seq_lens_buffer.numel()} (max_num_reqs * max_query_len)")
             windowed = self.windowed_seq_lens_buffer[:n].view(seq_lens.shape)
             # max(seq_len - window, 0) == max((seq_len - 1) + 1 - window, 0)
             pos = self._positions[:n]
@@ -287,18 +308,6 @@ class Ernie5_5IndexerCache:
         return Ernie5_5IndexerBackend
 
 
-class Ernie5_5MLAAttention:
-    """Sparse MLA layer whose KV cache uses the DSA page size (attention.py:1028-1032)."""
-
-    def __init__(self, head_size: int = 576, cache_block_size: int = 64) -> None:
-        self.head_size = head_size
-        self.cache_block_size = cache_block_size
-
-    def get_kv_cache_spec(self, vllm_config) -> KVCacheSpec:
-        base = KVCacheSpec(block_size=vllm_config.cache_config.block_size, head_size=self.head_size)
-        return _dsa_page_spec(base, vllm_config)
-
-
 def _check_sink_backend(head_size: int, kv_cache_dtype: str) -> None:
     """Validates the sink-capable sparse backend (attention.py:1035-1057)."""
     reasons = []
@@ -310,14 +319,386 @@ def _check_sink_backend(head_size: int, kv_cache_dtype: str) -> None:
         raise RuntimeError("ERNIE 5.5 DSA needs the sink-capable FLASHMLA_SPARSE backend: " + ", ".join(reasons))
 
 
+# --------------------------------------------------------------------------- forward context
+@dataclass
+class ForwardContext:
+    """Stand-in for vLLM's forward context: the per-layer attention
+    metadata of the step, keyed by layer (cache) prefix."""
+
+    attn_metadata: dict = field(default_factory=dict)
+
+
+_forward_context: ForwardContext | None = None
+
+
+@contextlib.contextmanager
+def set_forward_context(attn_metadata: dict):
+    """Makes ``attn_metadata`` the step's metadata for the layers' forwards."""
+    global _forward_context
+    prev = _forward_context
+    _forward_context = ForwardContext(attn_metadata)
+    try:
+        yield _forward_context
+    finally:
+        _forward_context = prev
+
+
+def get_forward_context() -> ForwardContext:
+    if _forward_context is None:
+        raise RuntimeError("no forward context: run the layer inside set_forward_context(...)")
+    return _forward_context
+
+
+@dataclass
+class DSAStepMetadata:
+    """What a DSA layer reads from the step's metadata: both of its caches
+    (indexer K and latent) use 64-token pages named by one block table."""
+
+    slot_mapping: torch.Tensor  # [T] int64, negative = skip
+    block_table: torch.Tensor   # [B, P] int32
+    req_ids: torch.Tensor       # [T] int32, query row -> request (row of block_table)
+    max_seq_len: int            # tokens of the longest request
+
+
+@dataclass
+class HCAStepMetadata:
+    """What an HCA layer reads from the step's metadata: the latent rows'
+    slots, each request's query rows, and the compressed / window-ring /
+    compressor-state placement of each request."""
+
+    slot_mapping: torch.Tensor      # [T] int64
+    query_start_loc: torch.Tensor   # [B + 1] int32
+    token_seq: torch.Tensor         # [T] int32, query row -> request
+    max_query_len: int
+    comp_block_table: torch.Tensor  # [B, CP] int32 pages of the compressed entries
+    ring_pages: torch.Tensor        # [B, R / 64] int32 pages of the window ring
+    state_slot: torch.Tensor        # [B] int32 row of the compressor state ring
+    max_seq_len: int
+
+
+_rope_tables: dict = {}
+
+
+def rope_cos_sin_table(rot_dim: int, theta: float, max_position: int, device) -> torch.Tensor:
+    """fp32 ``[max_position, rot_dim]`` cos | sin table (plain RoPE,
+    ``inv_freq_i = theta ** (-2i / rot_dim)``), shared per (theta, size,
+    device) across layers."""
+    key = (rot_dim, float(theta), int(max_position), str(device))
+    t = _rope_tables.get(key)
+    if t is None:
+        inv = theta ** (-torch.arange(rot_dim // 2, dtype=torch.float64) * 2.0 / rot_dim)
+        ang = torch.arange(max_position, dtype=torch.float64)[:, None] * inv[None, :]
+        t = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(device).contiguous()
+        _rope_tables[key] = t
+    return t
+
+
+_topk_workspaces: dict = {}
+
+
+def _indexer_workspace(rows: int, max_len: int, device) -> torch.Tensor:
+    """A zero-filled indexer top-k workspace per device, grown on demand
+    (calls leave its counters zero, so layers share it on one stream)."""
+    key = str(device)
+    need = ops._lib.load().ekv_indexer_topk_workspace_size(int(rows), int(max_len))
+    ws = _topk_workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+        _topk_workspaces[key] = ws
+    return ws
+
+
+# Query rows scored per indexer call: one call's workspace holds
+# rows x max_len x 20 bytes, so long prefill chunks run in pieces.
+_INDEXER_WORKSPACE_BYTES = 1 << 30
+
+
+# --------------------------------------------------------------------------- layers
+class Ernie5_5Indexer:
+    """Lightning indexer scoring the tokens older than the sliding window
+    (attention.py:863-984).
+
+    ``forward(hidden_states, qr, positions)`` runs the reference's order:
+    the two projections (``wq_b`` on ``qr``, ``wk_weights_proj`` on
+    ``hidden_states``; plain library GEMMs), then on the HIP library
+    ``k_norm`` LayerNorm, NeoX RoPE of dims 0..63, Hadamard, the fp8
+    UE8M0 q quant with the weight fold, the K-cache insert and the exact
+    top-k of each query row over its first ``position + 1 - window``
+    tokens, written to ``indexer_op.topk_indices_buffer[:T]``.
+    ``topk_indices_buffer`` (the layer attribute) is the swa buffer the
+    sparse MLA reads: the merged rows.  FP8 K cache only (132-byte rows)."""
+
+    def __init__(self, config, topk_indices_buffer: torch.Tensor | None, swa_topk_buffer: torch.Tensor | None,
+                 prefix: str = "", *, wq_b: torch.Tensor, wk_weights_proj: torch.Tensor,
+                 k_norm_weight: torch.Tensor, k_norm_bias: torch.Tensor, use_fp4_kv: bool = False) -> None:
+        if use_fp4_kv:
+            raise NotImplementedError("the MXFP4 indexer cache is not built; use the FP8 (132-byte) cache")
+        self.n_head = config.index_n_heads
+        self.head_dim = config.index_head_dim
+        self.rope_dim = config.mla_qk_rope_head_dim
+        if (self.n_head, self.head_dim, self.rope_dim) != (64, 128, 64):
+            raise NotImplementedError("the indexer kernels take 64 heads x 128 dims with a 64-dim rope")
+        self.topk = config.index_topk
+        self.window = config.sliding_window
+        self.rope_theta = config.rope_theta
+        self.max_position = config.max_position_embeddings
+        self.wq_b = wq_b
+        self.wk_weights_proj = wk_weights_proj
+        self.k_norm_weight = k_norm_weight.float().contiguous()
+        self.k_norm_bias = k_norm_bias.float().contiguous()
+        self.k_norm_eps = 1e-6
+        self.weights_scale = self.head_dim ** -0.5 * self.n_head ** -0.5
+        self.topk_indices_buffer = swa_topk_buffer
+        self.k_cache = Ernie5_5IndexerCache(head_dim=self.head_dim + self.head_dim // INDEXER_QUANT_BLOCK * 4,
+                                            dtype=torch.uint8, prefix=f"{prefix}.k_cache")
+        self.indexer_op = SimpleNamespace(topk_indices_buffer=topk_indices_buffer, topk_tokens=self.topk)
+        self._lengths: torch.Tensor | None = None
+
+    def _project(self, hidden_states: torch.Tensor, qr: torch.Tensor):
+        q = (qr @ self.wq_b.t()).view(-1, self.n_head, self.head_dim)
+        kw = hidden_states @ self.wk_weights_proj.t()
+        k, weights = kw.split([self.head_dim, self.n_head], dim=-1)
+        return q, k.contiguous(), weights.contiguous()
+
+    def _prep_args(self, device):
+        return (self.k_norm_weight, self.k_norm_bias, self.k_norm_eps,
+                rope_cos_sin_table(self.rope_dim, self.rope_theta, self.max_position, device))
+
+    def _lengths_buf(self, T: int, device) -> torch.Tensor:
+        if self._lengths is None or self._lengths.numel() < T:
+            self._lengths = torch.empty(max(T, 1), dtype=torch.int32, device=device)
+        return self._lengths[:T]
+
+    def _topk(self, q8, digits, wf, md: DSAStepMetadata, lengths, positions, merged=None) -> None:
+        """Exact top-k of every query row (filter + select), in row pieces
+        whose workspace fits _INDEXER_WORKSPACE_BYTES; with ``merged`` the
+        select also writes merge_swa_topk's rows."""
+        T = q8.shape[0]
+        kcache = self.k_cache.kv_cache
+        out = self.indexer_op.topk_indices_buffer
+        L = max(int(md.max_seq_len), 1)
+        step = max(1, min(T, _INDEXER_WORKSPACE_BYTES // (20 * L)))
+        for r0 in range(0, T, step):
+            r1 = min(T, r0 + step)
+            ws = _indexer_workspace(r1 - r0, L, q8.device)
+            args = (kcache, md.block_table, md.req_ids[r0:r1], lengths[r0:r1], L)
+            ops.indexer_filter(q8[r0:r1], digits[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
+            ops.indexer_select(digits[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws,
+                               merged=None if merged is None else merged[r0:r1],
+                               positions=positions[r0:r1], window=self.window)
+
+    def forward(self, hidden_states: torch.Tensor, qr: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        md: DSAStepMetadata = get_forward_context().attn_metadata[self.k_cache.prefix]
+        T = hidden_states.shape[0]
+        q, k, weights = self._project(hidden_states, qr)
+        qp, kp = ops.indexer_prep(q, k, *self._prep_args(q.device), positions)
+        ops.indexer_k_insert(kp, md.slot_mapping, self.k_cache.kv_cache)
+        q8, wf, digits = ops.indexer_q_quant(qp, weights)
+        lengths = self._lengths_buf(T, q.device)
+        ops.indexer_windowed_lengths(positions, self.window, lengths)
+        self._topk(q8, digits, wf, md, lengths, positions)
+        return self.indexer_op.topk_indices_buffer[:T]
+
+    __call__ = forward
+
+
+class Ernie5_5MLAAttention:
+    """Sparse MLA over the DSA latent cache (attention.py:1028-1032 for the
+    KV spec; the layer vLLM's MLAAttention provides around the impl).
+
+    Holds the impl (sink-capable sparse decode), the bound latent cache
+    (``kv_cache``, fp8 pages of 576-byte rows + fp32 scales) and the
+    absorbed-MLA projections split from ``kv_b_proj``: W_UK maps the
+    nope part of q into the 512-d latent space, W_UV maps the decode's
+    latent output to the v heads (plain batched GEMMs)."""
+
+    def __init__(self, num_heads: int = 64, scale: float = 256 ** -0.5, qk_nope_head_dim: int = 192,
+                 qk_rope_head_dim: int = 64, v_head_dim: int = 256, kv_lora_rank: int = 512,
+                 kv_b_proj: torch.Tensor | None = None, prefix: str = "", sinks: torch.Tensor | None = None,
+                 head_size: int = 576, cache_block_size: int = 64) -> None:
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.cache_block_size = cache_block_size
+        self.qk_nope_head_dim = qk_nope_head_dim
+        self.qk_rope_head_dim = qk_rope_head_dim
+        self.v_head_dim = v_head_dim
+        self.kv_lora_rank = kv_lora_rank
+        self.prefix = prefix
+        self.kv_cache: torch.Tensor | None = None
+        self.impl = None
+        if sinks is not None:
+            self.impl = Ernie5_5FlashMLASparseImpl(num_heads, head_size, scale, sinks=sinks)
+        if kv_b_proj is not None:
+            w = kv_b_proj.view(num_heads, qk_nope_head_dim + v_head_dim, kv_lora_rank)
+            self.W_UK = w[:, :qk_nope_head_dim].contiguous()                   # [H, 192, 512]
+            self.W_UV_T = w[:, qk_nope_head_dim:].transpose(1, 2).contiguous()  # [H, 512, 256]
+
+    def get_kv_cache_spec(self, vllm_config) -> KVCacheSpec:
+        base = KVCacheSpec(block_size=vllm_config.cache_config.block_size, head_size=self.head_size)
+        return _dsa_page_spec(base, vllm_config)
+
+    def absorb_q(self, q: torch.Tensor) -> torch.Tensor:
+        """q [T, H, 192 + 64] -> [T, H, 512 + 64]: the nope part through W_UK."""
+        T = q.shape[0]
+        q_nope = q[..., : self.qk_nope_head_dim].transpose(0, 1).contiguous()  # [H, T, 192]
+        q_lat = torch.bmm(q_nope, self.W_UK)                                    # [H, T, 512]
+        return torch.cat([q_lat.transpose(0, 1), q[..., self.qk_nope_head_dim:]], dim=-1).contiguous().view(
+            T, self.num_heads, self.kv_lora_rank + self.qk_rope_head_dim)
+
+    def up_proj(self, o_latent: torch.Tensor) -> torch.Tensor:
+        """[T, H, 512] -> [T, H * 256] through W_UV."""
+        T = o_latent.shape[0]
+        o = torch.bmm(o_latent.transpose(0, 1).contiguous(), self.W_UV_T)  # [H, T, 256]
+        return o.transpose(0, 1).reshape(T, self.num_heads * self.v_head_dim)
+
+
+class Ernie5_5DSAAttention:
+    """The KV-cache part of the MLA + DSA layer (attention.py:1059-1226).
+
+    ``_indexer_and_attn(hidden_states, q_c, positions, q, kv_c_normed, k_pe,
+    out)`` keeps the reference's signature and order -- indexer (K insert,
+    scores, top-k), window merge, latent append, sparse MLA decode with the
+    sink -- with the decode step's launches fused: one prologue (indexer
+    prep, K insert, latent append, q quant, lengths), the filter, the select
+    (top-k and merged rows), the decode (block-table conversion in-kernel).
+    The projections around it (fused_qkv_a_proj, norms, rope, q_b_proj,
+    o_gate, VHA, wo_b) are the layer's plain GEMMs and stay outside this
+    path; the absorbed-MLA W_UK / W_UV products run as batched GEMMs."""
+
+    def __init__(self, config, prefix: str, topk_indices_buffer: torch.Tensor | None = None,
+                 swa_topk_buffer: torch.Tensor | None = None, *, params: dict, kv_cache_dtype: str = "fp8") -> None:
+        _check_attn_tp(config)
+        self.num_heads = config.hybrid_mla_num_attention_heads
+        self.num_local_heads = self.num_heads
+        self.kv_lora_rank = config.hybrid_mla_kv_lora_rank
+        self.qk_nope_head_dim = config.hybrid_mla_qk_nope_head_dim
+        self.qk_rope_head_dim = config.hybrid_mla_qk_rope_head_dim
+        self.qk_head_dim = self.qk_nope_head_dim + self.qk_rope_head_dim
+        self.v_head_dim = config.hybrid_mla_v_head_dim
+        self.window = config.sliding_window
+        _check_sink_backend(self.kv_lora_rank + self.qk_rope_head_dim, kv_cache_dtype)
+        if not kv_cache_dtype.startswith("fp8"):
+            raise NotImplementedError("the DSA latent append writes the fp8 page rows; use an fp8 KV cache")
+        self.attn_sink = params["attn_sink"].float().contiguous()
+        self.indexer = Ernie5_5Indexer(config, topk_indices_buffer, swa_topk_buffer, prefix=f"{prefix}.indexer",
+                                       wq_b=params["indexer.wq_b"], wk_weights_proj=params["indexer.wk_weights_proj"],
+                                       k_norm_weight=params["indexer.k_norm.weight"],
+                                       k_norm_bias=params["indexer.k_norm.bias"])
+        self.mla_attn = Ernie5_5MLAAttention(
+            num_heads=self.num_local_heads, scale=self.qk_head_dim ** -0.5, qk_nope_head_dim=self.qk_nope_head_dim,
+            qk_rope_head_dim=self.qk_rope_head_dim, v_head_dim=self.v_head_dim, kv_lora_rank=self.kv_lora_rank,
+            kv_b_proj=params["kv_b_proj"], prefix=f"{prefix}.attn", sinks=self.attn_sink)
+
+    def _indexer_and_attn(self, hidden_states: torch.Tensor, q_c: torch.Tensor, positions: torch.Tensor,
+                          q: torch.Tensor, kv_c_normed: torch.Tensor, k_pe: torch.Tensor, out: torch.Tensor) -> None:
+        """Indexer, window merge and sparse MLA in one eager segment
+        (attention.py:1205-1226): ``out [T, H * v_head_dim]`` in place."""
+        num_tokens = hidden_states.shape[0]
+        md: DSAStepMetadata = get_forward_context().attn_metadata[self.mla_attn.prefix]
+        ix = self.indexer
+        iq, ik, iw = ix._project(hidden_states, q_c)
+        latent = torch.cat([kv_c_normed, k_pe.reshape(num_tokens, -1)], dim=-1).contiguous()
+        lengths = ix._lengths_buf(num_tokens, q.device)
+        q8, wf, digits = ops.dsa_decode_prologue(
+            ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions, self.window,
+            lengths, prep=ix._prep_args(q.device))
+        merged = ix.topk_indices_buffer[:num_tokens]
+        ix._topk(q8, digits, wf, md, lengths, positions, merged=merged)
+        q_abs = self.mla_attn.absorb_q(q)
+        o_latent, _ = self.mla_attn.impl._fp8_flash_mla_kernel(
+            q_abs[:, None], self.mla_attn.kv_cache, merged[:, None],
+            SimpleNamespace(block_table=md.block_table, req_ids=md.req_ids))
+        out.copy_(self.mla_attn.up_proj(o_latent[:, 0]))
+
+
+class Ernie5_5HCAAttentionMixin:
+    """The KV-cache half of the HCA layer's forward (attention.py:471-539):
+    the cache write and the sparse attention into ``o_padded`` that upstream
+    ``DeepseekV4Attention._prepare_and_attn_fn`` performs.
+
+    ``_prepare_and_attn_fn(q, kv, kv_score, positions, o_padded)`` takes the
+    layer's projected, roped operands -- q ``[T, heads, D]``, the latent
+    rows kv ``[T, D]`` and the compressor input kv_score ``[T, 2D]`` (the
+    ``compressor.fused_wkv_wgate`` output, model.py:684-685) -- and on the
+    HIP library appends kv (fp8 rows, window ring, compressor state ring),
+    compresses every 128-token span that completes, builds each query row's
+    index row (its compressed entries, then its window) and runs the
+    64-head sparse decode with the sink into ``o_padded[:, :heads]``.
+    VHA, inverse RoPE and the output projections stay outside this path."""
+
+    def __init__(self, config, prefix: str, *, params: dict, ring: int = 192, padded_heads: int = 64,
+                 compress_cos_sin: torch.Tensor, scale: float | None = None) -> None:
+        _check_attn_tp(config)
+        self.prefix = prefix
+        self.n_local_heads = config.num_attention_heads
+        self.padded_heads = max(padded_heads, self.n_local_heads)
+        self.head_dim = config.head_dim
+        self.window = config.sliding_window
+        self.ring = ring
+        if ring % DSA_BLOCK_SIZE or ring < self.window:
+            raise ValueError("the window ring must be whole 64-row pages holding at least the window")
+        self.softmax_scale = self.head_dim ** -0.5 if scale is None else scale
+        self.attn_sink = params["attn_sink"].float().contiguous()
+        self.ape = params["compressor.ape"].float().contiguous()
+        self.norm_w = params["compressor.norm.weight"].float().contiguous()
+        self.norm_eps = config.rms_norm_eps
+        self.compress_cos_sin = compress_cos_sin
+        self.kv_cache: torch.Tensor | None = None     # fp8 pages [num_pages, 64 * (D + 4)]
+        self.state_cache: torch.Tensor | None = None  # bf16 [num_state, 256, 2 D]
+        self._idx: torch.Tensor | None = None
+        self._ws: torch.Tensor | None = None
+
+    def _buffers(self, T: int, width: int, device):
+        if self._idx is None or self._idx.shape[0] < T or self._idx.shape[1] < width:
+            self._idx = torch.empty((T, width), dtype=torch.int32, device=device)
+            self._lens = torch.empty(T, dtype=torch.int32, device=device)
+            self._lse = torch.empty((T, self.padded_heads), dtype=torch.float32, device=device)
+            self._ws = ops.decode_workspace(T, self.padded_heads, width, device)
+        return self._idx[:T, :width], self._lens[:T], self._lse[:T], self._ws
+
+    def _prepare_and_attn_fn(self, q: torch.Tensor, kv: torch.Tensor, kv_score: torch.Tensor,
+                             positions: torch.Tensor, o_padded: torch.Tensor) -> None:
+        md: HCAStepMetadata = get_forward_context().attn_metadata[self.prefix]
+        T, H, D = q.shape
+        # A request with more than ring - window rows in the call would
+        # overwrite ring rows that its own first rows' windows still read:
+        # such calls update the ring after the decode.
+        late_ring = md.max_query_len > self.ring - self.window
+        ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc, md.max_query_len,
+                      self.state_cache, md.state_slot, self.ape, self.norm_w, self.norm_eps, self.compress_cos_sin,
+                      md.comp_block_table, None if late_ring else md.ring_pages, self.ring, self.kv_cache)
+        width = md.max_seq_len // 128 + self.window
+        idx, lens, lse, ws = self._buffers(T, width, q.device)
+        ops.hca_decode_indices(positions, md.token_seq, md.comp_block_table, md.ring_pages, self.ring, idx, lens,
+                               self.window, query_start_loc=md.query_start_loc, slot_mapping=md.slot_mapping)
+        if H < self.padded_heads:
+            qp = q.new_zeros((T, self.padded_heads, D))
+            qp[:, :H] = q
+            q = qp
+        sinks = self.attn_sink
+        if sinks.numel() < self.padded_heads:
+            sinks = torch.cat([sinks, sinks.new_full((self.padded_heads - sinks.numel(),), float("-inf"))])
+        ops.sparse_mla_decode(q, self.kv_cache, idx, self.softmax_scale, o_padded, lse, sinks=sinks, lengths=lens,
+                              workspace=ws)
+        if late_ring:  # the window ring rows only (pool rows skipped, state ring already written)
+            skip = torch.full((T,), -1, dtype=torch.int64, device=q.device)
+            ops.hca_append(kv, None, skip, positions, md.token_seq, md.query_start_loc, self.kv_cache, md.ring_pages,
+                           self.ring, None, None)
+
+
 # --------------------------------------------------------------------------- HCA layer class choice
 class Ernie5_5HCAFlashInferAttention:
-    """HCA layer on a bf16 KV row (attention.py:542-545)."""
+    """HCA layer on a bf16 KV row (attention.py:542-545).  The write path
+    here stores fp8 page rows, so this class is named for the choice only
+    and refuses to run."""
 
     kv_cache_dtype = "bfloat16"
 
+    def __init__(self, *args, **kwargs) -> None:
+        raise NotImplementedError("bf16 HCA cache rows are not built; select an fp8 KV cache")
 
-class Ernie5_5HCAFlashMLAAttention:
+
+class Ernie5_5HCAFlashMLAAttention(Ernie5_5HCAAttentionMixin):
     """HCA layer on an fp8 KV row (attention.py:548-551)."""
 
     kv_cache_dtype = "fp8"
@@ -336,3 +717,20 @@ def simple_vllm_config(head_dim=512, mla_kv_lora_rank=512, mla_qk_rope_head_dim=
                          mla_qk_rope_head_dim=mla_qk_rope_head_dim)
     return SimpleNamespace(model_config=SimpleNamespace(hf_config=hf),
                            cache_config=SimpleNamespace(block_size=block_size))
+
+
+def ernie5_5_config(**overrides) -> SimpleNamespace:
+    """The Ernie5_5Config fields this path reads, at their defaults
+    (src/vllm_ernie/models/ernie5_5/config.py:13-62)."""
+    cfg = dict(hidden_size=4096, num_attention_heads=64, head_dim=512, q_lora_rank=1024, o_groups=8,
+               sliding_window=128, hybrid_mla_num_attention_heads=64, hybrid_mla_q_lora_rank=1024,
+               hybrid_mla_kv_lora_rank=512, hybrid_mla_qk_nope_head_dim=192, hybrid_mla_qk_rope_head_dim=64,
+               hybrid_mla_v_head_dim=256, index_n_heads=64, index_head_dim=128, index_topk=2048,
+               max_position_embeddings=200192, rope_theta=2500000.0, compress_rope_theta=160000.0,
+               rms_norm_eps=1e-6)
+    cfg.update(overrides)
+    ns = SimpleNamespace(**cfg)
+    ns.mla_qk_rope_head_dim = ns.hybrid_mla_qk_rope_head_dim
+    ns.mla_kv_lora_rank = ns.hybrid_mla_kv_lora_rank
+    ns.mla_q_lora_rank = ns.hybrid_mla_q_lora_rank
+    return ns

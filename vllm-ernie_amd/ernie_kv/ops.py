@@ -201,13 +201,23 @@ def hca_decode_indices(
     out: torch.Tensor,
     lengths: torch.Tensor,
     window: int = 128,
+    query_start_loc: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
 ) -> None:
-    _check_dev(positions, req_ids, comp_block_table, ring_pages, out, lengths)
+    """Index rows [compressed entries | window | -1 ...] and their lengths.
+    With ``query_start_loc`` and ``slot_mapping`` (the call's), window
+    positions inside the call use the call's slots, older ones the ring."""
+    _check_dev(positions, req_ids, comp_block_table, ring_pages, out, lengths, query_start_loc, slot_mapping)
     _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32 [T, W]")
+    _need((query_start_loc is None) == (slot_mapping is None), "query_start_loc and slot_mapping go together")
+    if slot_mapping is not None:
+        _need(slot_mapping.dtype == torch.int64 and query_start_loc.dtype == torch.int32,
+              "slot_mapping int64, query_start_loc int32")
     _lib.call(
         "ekv_hca_decode_indices", positions.data_ptr(), req_ids.data_ptr(), positions.numel(),
         comp_block_table.data_ptr(), _rs(comp_block_table), ring_pages.data_ptr(), _rs(ring_pages),
-        int(ring), int(window), out.data_ptr(), _rs(out), out.shape[1], lengths.data_ptr(), _stream(),
+        int(ring), int(window), _ptr(query_start_loc), _ptr(slot_mapping), out.data_ptr(), _rs(out), out.shape[1],
+        lengths.data_ptr(), _stream(),
     )
 
 
