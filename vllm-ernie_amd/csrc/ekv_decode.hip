@@ -2,32 +2,32 @@
 // compressed + window), with the per-head attention sink in the softmax
 // denominator.
 //
-// Workgroup = (query row t, split s of its index row), 512 threads in two
-// roles, one barrier per tile of 32 index entries.  Between two barriers:
-//   * score waves 0..3 (q for heads 16w .. 16w+15 held in registers) first
-//     finish tile t-1 (below), then compute S = Q K^T of tile t on
-//     v_mfma_f32_16x16x32_bf16 from a bf16 K image in LDS, run the online
-//     softmax and write P (row scale folded in) for their heads as a pair of
-//     bf16 values hi = bf16(P), lo = bf16(P - hi); fp8 K fragments become
-//     bf16 in registers (exact conversion);
-//   * data waves 4..7 finish tile t-1, store tile t+1 (the rows as cached:
-//     e4m3fn bytes, or bf16) into the next of three K images, and issue the
-//     loads of tile t+3 (8 rows per wave, row addresses in scalar registers,
-//     256-byte coalesced loads into registers, two tiles in flight);
-//   * "finish tile t-1" = O[:, 64w .. 64w+63] += P_hi V + P_lo V for all
-//     heads, every wave taking its 64 channels.  The B operand (V, entries x
-//     channels) is read straight from the row-major K image with a
-//     transposing LDS read (ds_read_b64_tr_b8 for fp8 rows, ds_read_b64_tr_b16
-//     for bf16); no separate V^T image is built.
-// The hi/lo pair carries P to about 2^-16 relative (one bf16 alone is 2^-8,
-// which rows of a few entries that nearly cancel expose); V itself is exact
-// in bf16 for fp8 and bf16 caches.
+// Workgroup = (query row t, split s of its index row): 8 waves, a scorer and
+// a data wave per group of 16 heads, the two waves of a group on one SIMD
+// (wave w and w + 4).  The split's entries go through in tiles of 32, one
+// barrier per tile.  At step s:
+//   * the scorer wave of a group computes S^T = K Q^T for tile s
+//     (v_mfma_f32_16x16x32_bf16, A = the tile's rows from LDS, fp8 converted
+//     exactly to bf16, B = its 16 heads of q held in registers), runs the
+//     online softmax (a lane holds one head's scores of 8 entries; the
+//     reference max only moves when a score exceeds it by more than 8 log2
+//     units), turns the weights P (row scale folded in) into a pair of bf16
+//     B operands hi = bf16(P), lo = bf16(P - hi), publishes them for the data
+//     wave and accumulates O^T[0, 128) += V^T P^T of tile s;
+//   * the data wave of a group accumulates O^T[128, 512) += V^T P^T of tile
+//     s - 1 from the published operands, and issues the direct global->LDS
+//     loads of a later tile (coalesced 16-byte loads of whole rows).
+// V^T (channels x entries) is read straight from the row-major tile image
+// with transposing LDS reads (ds_read_b64_tr_b8 / _b16); S^T's accumulator
+// layout is the B-operand layout of P^T, so P never leaves the registers of
+// the wave that computed it except for the data wave's copy.  The hi/lo pair
+// carries P to about 2^-16 relative (one bf16 alone is 2^-8, which rows of a
+// few entries that nearly cancel expose); V is exact in bf16.
 // A prologue resolves every index entry of the split to a cache slot (block
-// table lookup) and fp32 row scale once.  The softmax reference max only
-// moves when a score exceeds it by more than 8 (log2 units), so O is rescaled
-// rarely.  Each split leaves O / l in fp32 plus (m, l) in fp32; the combine
-// kernel merges the splits, adds the sink and writes bf16 out and the
-// natural-log lse (log sum_j exp(s_j), sink excluded).
+// table lookup) and loads the rows' fp32 scales once.  Each split leaves
+// O / l in fp32 plus (m, l); the combine kernel merges the splits, adds the
+// sink and writes bf16 out and the natural-log lse (log sum_j exp(s_j), sink
+// excluded).  A row of one split is finished in place.
 #include "ekv_common.h"
 #include "ekv_internal.h"
 
@@ -37,11 +37,8 @@ namespace ekv {
 
 constexpr int kDv = 512;
 constexpr int kTile = 32;
-constexpr int kScoreWaves = 4;               // up to 64 heads (one wave per 16)
-constexpr int kDataWaves = 4;
-constexpr int kThreads = 64 * (kScoreWaves + kDataWaves);
-constexpr int kRowsPerDataWave = kTile / kDataWaves;   // 8
-constexpr int kKImages = 3;                  // tile t-1 (P V), t (S), t+1 (being stored)
+constexpr int kGroups = 4;                   // head groups of 16 (up to 64 heads)
+constexpr int kThreads = 64 * 2 * kGroups;   // a scorer and a data wave per head group
 constexpr int kMaxSplitEntries = 1024;       // index entries one workgroup resolves
 constexpr int kMaxSplitTiles = kMaxSplitEntries / kTile;
 constexpr int kTargetGroups = 256;           // one workgroup per CU
@@ -161,24 +158,50 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
   __syncthreads();
 }
 
-// K images hold the tile's rows as stored: raw e4m3fn bytes (fp8 cache) or
-// bf16.  The fp8 row stride D + 8 bytes is 8 (mod 16) words: the 16 rows a
-// QK fragment read touches land on distinct bank pairs.
+// K tile images hold 32 rows as cached (e4m3fn bytes, or bf16), unpadded,
+// with each row's 16-byte chunks permuted (chunk j of row r is stored at
+// chunk swz(j, r), an XOR within runs of 8 chunks, of 4 for the last 4 of a
+// 36-chunk row) so that the 16 rows a fragment read touches spread over the
+// LDS banks.  Rows arrive by direct global->LDS loads: lane i of a load
+// instruction writes bytes [16 i, 16 i + 16) of the instruction's 1 KB.
 template <int D, bool BF16>
 struct DecodeSmem {
-  static constexpr int kKRowB = BF16 ? 2 * (D + 8) : D + 8;  // K row stride (bytes)
-  static constexpr int kImgB = kTile * kKRowB;
-  static constexpr int kPRow = kTile + 8;   // bf16 P row stride (elements)
-  __align__(16) uint8_t img[kKImages * kImgB];
-  uint16_t p[2][64 * kPRow];                // bf16(P) of tiles t (written) and t-1 (read)
-  uint16_t plo[2][64 * kPRow];              // bf16(P - bf16(P)), same layout
-  float alpha[2][64];                       // rescale factor per head (valid when grow[.][head / 16])
-  int32_t grow[2][kScoreWaves];
-  float row_f[64];                          // epilogue: per-head output factor
-  __align__(8) int32_t red[64];             // split location scratch
+  // Tile images: fp8 tiles are loaded two steps ahead into 4 images; bf16
+  // tiles (twice the bytes) one step ahead into 3.
+  static constexpr int kBufs = BF16 ? 3 : 4;
+  static constexpr int kAhead = kBufs - 2;
+  static constexpr int kRowB = BF16 ? 2 * D : D;     // row bytes
+  static constexpr int kChunks = kRowB / 16;          // 16-byte chunks per row
+  static constexpr int kImgB = kTile * kRowB;         // bytes of one tile image
+  static constexpr int kLoads = kImgB / 1024;         // 1 KB load instructions per tile
+  static constexpr int kLoadsPerWave = (kLoads + kGroups - 1) / kGroups;
+  __align__(16) uint8_t img[kBufs][kImgB];
+  __align__(16) uint8_t spill[1024];                  // target of the padding load instructions
+  __align__(16) uint4 p[2][kGroups][2][64];           // P hi / lo B operands of a head group, per lane
+  float alpha[2][kGroups][16];                        // O rescale factor per head (when grow)
+  int32_t grow[2][kGroups];
+  float fin[kGroups][16];                             // epilogue: per-head output factor
+  __align__(8) int32_t red[64];                       // split location scratch
   int32_t slot[kMaxSplitEntries];
-  float kscale[kMaxSplitEntries];
+  __align__(16) float kscale[kMaxSplitEntries];       // row scale, 0 for masked entries
 };
+
+template <int D, bool BF16>
+__device__ __forceinline__ int swz_chunk(int j, int r) {
+  using SM = DecodeSmem<D, BF16>;
+  if constexpr (SM::kChunks % 8 == 0) {
+    return j ^ (r & 7);
+  } else {  // 36 chunks: rows 2 apart start on the same banks, so permute by r / 2
+    const int x = r >> 1;
+    return j < 32 ? (j ^ (x & 7)) : (32 + ((j - 32) ^ (x & 3)));
+  }
+}
+
+// Byte offset in a tile image of bytes [8 h, 8 h + 8) of 16-byte chunk c of row r.
+template <int D, bool BF16>
+__device__ __forceinline__ int img_off(int r, int c, int h) {
+  return r * DecodeSmem<D, BF16>::kRowB + 16 * swz_chunk<D, BF16>(c, r) + 8 * h;
+}
 
 // Four e4m3fn bytes -> four bf16 (exact: every e4m3fn value is a bf16 value).
 __device__ __forceinline__ uint2 fp8x4_bf16(uint32_t w) {
@@ -186,119 +209,14 @@ __device__ __forceinline__ uint2 fp8x4_bf16(uint32_t w) {
   const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
   return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
 }
-
-// Max / sum over each row of 16 lanes, every lane receiving the result:
-// DPP row rotations by 8, 4, 2, 1 (VALU only, no LDS round trip).
-template <int kCtrl>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f32<0x128>(v));  // row_ror:8
-  v = fmaxf(v, dpp_f32<0x124>(v));  // row_ror:4
-  v = fmaxf(v, dpp_f32<0x122>(v));  // row_ror:2
-  return fmaxf(v, dpp_f32<0x121>(v));  // row_ror:1
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_f32<0x128>(v);
-  v += dpp_f32<0x124>(v);
-  v += dpp_f32<0x122>(v);
-  return v + dpp_f32<0x121>(v);
+__device__ __forceinline__ bf16x8 fp8x8_bf16(uint2 w) {
+  const uint2 lo = fp8x4_bf16(w.x), hi = fp8x4_bf16(w.y);
+  return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 __device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
   const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};  // round to nearest even
   return __builtin_bit_cast(uint32_t, v);
-}
-
-// ds_read_b64_tr_b16: in each row of 16 lanes, lane j receives 16-bit element
-// j % 4 of the 8 bytes addressed by lanes j / 4 + 4m (m = 0..3).
-__device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_i16x4*)((__attribute__((address_space(3))) uint16_t*)(p)));
-}
-
-// ---------------------------------------------------------------------------
-// Data role: rows 8u .. 8u+7 of a tile, 4-channel units lane + 64 j.
-template <int D, bool BF16>
-struct RowRegs {
-  using Unit = typename std::conditional<BF16, uint2, uint32_t>::type;
-  static constexpr int kUnits = D / 4;                   // 4-channel units per row
-  static constexpr int kJ = (kUnits + 63) / 64;
-  Unit v[kRowsPerDataWave][kJ];
-  float ks;                                              // lane r < 8: fp32 scale of row r
-  uint32_t valid;                                        // bit rr: row rr holds data (wave-uniform)
-  bool live;                                             // the tile exists
-};
-
-// Issue every load of tile `tile` for this data wave.  Masked rows and tiles
-// past the end read the first cache row and stay flagged invalid, so that the
-// wait before each store to LDS counts exactly the loads issued after it.
-template <int D, bool BF16>
-__device__ __forceinline__ void fetch_rows(const DecodeArgs& a, const DecodeSmem<D, BF16>& sm, int u, int tile, int ntiles,
-                                           RowRegs<D, BF16>& rr) {
-  using RR = RowRegs<D, BF16>;
-  const bool live = tile < ntiles;
-  const int tb = (live ? tile : 0) * kTile + kRowsPerDataWave * u;
-  const int lane = threadIdx.x & 63;
-  uint32_t valid = 0;
-  // One LDS read gives lane r the slot of row r; rows then become uniform.
-  const int my_slot = sm.slot[tb + (lane & (kRowsPerDataWave - 1))];
-  const int ks_slot = (live && my_slot >= 0) ? my_slot : 0;
-  // Keep each tile's loads in issue order relative to the other tiles' loads
-  // (the register buffers are consumed oldest first).
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int r = 0; r < kRowsPerDataWave; ++r) {
-    const int slot = __builtin_amdgcn_readlane(my_slot, r);
-    const bool ok = live && slot >= 0;
-    const int s = ok ? slot : 0;
-    const uint8_t* row = BF16 ? a.cache + static_cast<int64_t>(s) * (2 * D)
-                              : a.cache + static_cast<int64_t>(s >> 6) * a.page_stride + (s & 63) * D;
-    valid |= static_cast<uint32_t>(ok) << r;
-#pragma unroll
-    for (int j = 0; j < RR::kJ; ++j) {
-      const int unit = (RR::kUnits % 64 == 0 || lane + 64 * j < RR::kUnits) ? lane + 64 * j : RR::kUnits - 1;
-      rr.v[r][j] = *reinterpret_cast<const typename RR::Unit*>(row + unit * sizeof(typename RR::Unit));
-    }
-  }
-  // the rows' fp32 scales, lane r for row r (after the values of the page)
-  if constexpr (BF16) rr.ks = 1.0f;
-  else rr.ks = *reinterpret_cast<const float*>(a.cache + static_cast<int64_t>(ks_slot >> 6) * a.page_stride +
-                                                kPageTokens * D + (ks_slot & 63) * 4);
-  __builtin_amdgcn_sched_barrier(0);
-  rr.valid = valid;
-  rr.live = live;
-}
-
-// Store the wave's 8 rows into a K image as they are (masked rows become
-// zero, so that P = 0 never meets a non-finite value in P V).  Lanes past the
-// end of a row repeat its last unit: a duplicate store of equal data.
-template <int D, bool BF16>
-__device__ __forceinline__ void store_rows(const RowRegs<D, BF16>& rr, int u, int tile, DecodeSmem<D, BF16>& sm,
-                                           uint8_t* k) {
-  using RR = RowRegs<D, BF16>;
-  using SM = DecodeSmem<D, BF16>;
-  const int lane = threadIdx.x & 63;
-  if (rr.live && lane < kRowsPerDataWave)
-    sm.kscale[tile * kTile + kRowsPerDataWave * u + lane] = ((rr.valid >> lane) & 1u) ? rr.ks : 0.0f;
-#pragma unroll
-  for (int r = 0; r < kRowsPerDataWave; ++r) {
-    const bool ok = (rr.valid >> r) & 1u;
-    uint8_t* row = k + (kRowsPerDataWave * u + r) * SM::kKRowB;
-#pragma unroll
-    for (int j = 0; j < RR::kJ; ++j) {
-      const int unit = (RR::kUnits % 64 == 0 || lane + 64 * j < RR::kUnits) ? lane + 64 * j : RR::kUnits - 1;
-      if constexpr (BF16) *reinterpret_cast<uint2*>(row + 8 * unit) = ok ? rr.v[r][j] : make_uint2(0u, 0u);
-      else *reinterpret_cast<uint32_t*>(row + 4 * unit) = ok ? rr.v[r][j] : 0u;
-    }
-  }
-}
-
-// Eight e4m3fn bytes -> bf16x8 (exact).
-__device__ __forceinline__ bf16x8 fp8x8_bf16(uint2 w) {
-  const uint2 lo = fp8x4_bf16(w.x), hi = fp8x4_bf16(w.y);
-  return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 // ds_read_b64_tr_b8: in each row of 16 lanes, lane j receives byte j % 8 of
@@ -309,153 +227,131 @@ __device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
       (__attribute__((address_space(3))) i32x2*)((__attribute__((address_space(3))) uint8_t*)(p)));
   return make_uint2(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y));
 }
+// ds_read_b64_tr_b16: lane j receives 16-bit element j % 4 of the 8 bytes
+// addressed by lanes j / 4 + 4m (m = 0..3), as element m.
+__device__ __forceinline__ i16x4 lds_read_tr16(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)((__attribute__((address_space(3))) uint8_t*)(p)));
+}
+
+// s_waitcnt vmcnt(N), other counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Data waves: wait until at most n tiles' loads (n < kAhead) are in flight.
+template <int D, bool BF16>
+__device__ __forceinline__ void wait_tiles(int n) {
+  constexpr int L = DecodeSmem<D, BF16>::kLoadsPerWave;
+  if (n <= 0) wait_vm<0>();
+  else if (n == 1) wait_vm<L>();
+  else wait_vm<2 * L>();
+}
+
+// Entry of k-slot m (0..7) of lane group kg in the S^T accumulators / the
+// P V operands: S^T rows 4 kg + i of entry halves 0 and 1.
+__device__ __forceinline__ int slot_entry(int kg, int m) { return m < 4 ? 4 * kg + m : 16 + 4 * kg + (m - 4); }
 
 // ---------------------------------------------------------------------------
-// O[:, 64w .. 64w+63] += P V for every head group (all waves).  o[hf][nt]
-// holds heads 16hf + 4g + i, channels 64w + 16nt + col.
+// Tile loads (data waves).  Instruction k of a tile covers image bytes
+// [1024 k, 1024 k + 1024); lane i its 16-byte chunk 64 k + i, i.e. row
+// (64 k + i) / kChunks, stored chunk j = (64 k + i) % kChunks, which holds
+// row chunk swz(j, r).  Masked rows load the first cache row (their image
+// rows are zeroed once the tile has landed).  Padding instructions (when the
+// tile has fewer than kLoadsPerWave * 4) write the spill area.
 template <int D, bool BF16>
-__device__ __forceinline__ void accumulate_pv(const DecodeSmem<D, BF16>& sm, const uint8_t* kimg, int pb, int hgroups,
-                                              f32x4 (&o)[4][4]) {
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, DecodeSmem<D, BF16>& sm, int u, int tile) {
   using SM = DecodeSmem<D, BF16>;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int g = lane >> 4, col = lane & 15;
-  // B operand: entries 8g .. 8g+7 at channel 64w + 16nt + col.
-  bf16x8 vb[4];
-  if constexpr (BF16) {
-    // two 16-bit transposed reads of rows 8g + 4h + col/4, channels
-    // 64w + 16nt + 4 (col % 4) .. +3
-    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(kimg + (8 * g + (col >> 2)) * SM::kKRowB) + 64 * wave +
-                            4 * (col & 3);
+  int slots[SM::kLoadsPerWave];  // every slot read issued before the first use
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const i16x4 lo = lds_read_tr16(vbase + 16 * nt);
-      const i16x4 hi = lds_read_tr16(vbase + 2 * SM::kKRowB + 16 * nt);
-      const i16x4 both[2] = {lo, hi};
-      vb[nt] = __builtin_bit_cast(bf16x8, both);
-    }
-  } else {
-    // one 8-bit transposed read: lane col of row block g addresses row
-    // 8g + col/2, channels 64w + 16nt + 8 (col % 2) .. +7
-    const uint8_t* vbase = kimg + (8 * g + (col >> 1)) * SM::kKRowB + 64 * wave + 8 * (col & 1);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) vb[nt] = fp8x8_bf16(lds_read_tr8(vbase + 16 * nt));
-  }
-  // All operands are read before the first product; the rescale (rare) and
-  // the products of head groups past `hgroups` (unused) need no branches.
-  bf16x8 pa[4];
-#pragma unroll
-  for (int hf = 0; hf < 4; ++hf)
-    pa[hf] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.p[pb][(16 * hf + col) * SM::kPRow + 8 * g]));
-  // the lo parts one head group ahead of their products (register pressure)
-  auto p_lo = [&](int hf) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&sm.plo[pb][(16 * hf + col) * SM::kPRow + 8 * g]));
-  };
-  bf16x8 pl = p_lo(0);
-  const int4 gr = *reinterpret_cast<const int4*>(sm.grow[pb]);
-  const int grow_any = (gr.x | (hgroups > 1 ? gr.y : 0) | (hgroups > 2 ? gr.z : 0) | (hgroups > 3 ? gr.w : 0));
-  if (__builtin_amdgcn_readfirstlane(grow_any)) {
-    const int grs[4] = {gr.x, gr.y, gr.z, gr.w};
-#pragma unroll
-    for (int hf = 0; hf < 4; ++hf) {
-      if (!grs[hf]) continue;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float al = sm.alpha[pb][16 * hf + 4 * g + i];
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) o[hf][nt][i] *= al;
-      }
-    }
+  for (int j = 0; j < SM::kLoadsPerWave; ++j) {
+    const int k = j * kGroups + u;
+    const int pos = (k < SM::kLoads ? k : 0) * 64 + lane;
+    slots[j] = sm.slot[tile * kTile + pos / SM::kChunks];
   }
 #pragma unroll
-  for (int hf = 0; hf < 4; ++hf) {
-    const bf16x8 pl_next = p_lo(hf < 3 ? hf + 1 : 3);
+  for (int j = 0; j < SM::kLoadsPerWave; ++j) {
+    const int k = j * kGroups + u;
+    const bool real = k < SM::kLoads;
+    const int pos = (real ? k : 0) * 64 + lane;
+    const int r = pos / SM::kChunks, jj = pos % SM::kChunks;
+    const int s = slots[j];
+    const uint8_t* row;
+    if constexpr (BF16) row = a.cache + static_cast<int64_t>(s < 0 ? 0 : s) * (2 * D);
+    else row = a.cache + static_cast<int64_t>(s < 0 ? 0 : s >> 6) * a.page_stride + (s < 0 ? 0 : (s & 63) * D);
+    const uint8_t* src = row + 16 * swz_chunk<D, BF16>(jj, r);
+    uint8_t* dst = real ? sm.img[tile % SM::kBufs] + 1024 * k : sm.spill;
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  }
+}
+
+// Zero the image rows of masked entries of a tile that has landed.
+template <int D, bool BF16>
+__device__ __forceinline__ void zero_masked(DecodeSmem<D, BF16>& sm, int u, int tile) {
+  using SM = DecodeSmem<D, BF16>;
+  const int lane = threadIdx.x & 63;
+  const bool any = __any(lane < kTile && sm.slot[tile * kTile + lane] < 0);
+  if (!any) return;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb[nt], o[hf][nt], 0, 0, 0);
-      o[hf][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hf], vb[nt], o[hf][nt], 0, 0, 0);
-    }
-    pl = pl_next;
+  for (int j = 0; j < SM::kLoadsPerWave; ++j) {
+    const int k = j * kGroups + u;
+    if (k >= SM::kLoads) break;
+    const int pos = k * 64 + lane;
+    if (sm.slot[tile * kTile + pos / SM::kChunks] < 0)
+      *reinterpret_cast<uint4*>(sm.img[tile % SM::kBufs] + 16 * pos) = make_uint4(0, 0, 0, 0);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Score role: S = Q K^T for heads 16w .. 16w+15 over one tile, online softmax,
-// P (times the row scale, bf16) and the rescale factors to LDS buffer pb.
-struct SoftmaxState {
-  float m2[4];    // reference max (log2 units) of heads 4g + i
-  float lsum[4];  // this lane's share of the denominator relative to m2
-};
-
-template <int D, bool BF16>
-__device__ __forceinline__ void score_tile(DecodeSmem<D, BF16>& sm, const uint8_t* kimg, int pb, int tb, float sc2,
-                                           const bf16x8 (&qa)[D / 32], SoftmaxState& st) {
-  using SM = DecodeSmem<D, BF16>;
-  constexpr int KS = D / 32;
+// O^T[16 cb + 4 kg + i][head col] += V^T P^T over the tile's 32 entries for
+// the channel blocks [cb0, cb1): A = V^T from the image (transposing reads),
+// B = the P hi / lo operands.
+template <int D, bool BF16, int kCb0, int kCb1>
+__device__ __forceinline__ void pv_tile(const uint8_t* img, const bf16x8& phi, const bf16x8& plo,
+                                        f32x4 (&o)[kCb1 - kCb0]) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int g = lane >> 4, col = lane & 15;
-  // Four independent accumulation chains (entry half x even/odd k-step).
-  f32x4 s2[2][2];
+  const int kg = lane >> 4, col = lane & 15;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) s2[nt][0] = s2[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // B operand: entry 16nt + col, dims 32ks + 8g .. +7.
-  const uint8_t* kbase = kimg + col * SM::kKRowB + (BF16 ? 16 : 8) * g;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const uint8_t* src = kbase + 16 * nt * SM::kKRowB + (BF16 ? 64 : 32) * ks;
-      bf16x8 kb;
-      if constexpr (BF16) kb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src));
-      else kb = fp8x8_bf16(*reinterpret_cast<const uint2*>(src));
-      s2[nt][ks & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s2[nt][ks & 1], 0, 0, 0);
+  for (int cb = kCb0; cb < kCb1; ++cb) {
+    bf16x8 v;
+    if constexpr (BF16) {
+      // element m of read h: row slot_entry(kg, 4h + col / 4), channel 16 cb + 4 (col % 4)
+      const int ch = 16 * cb + 4 * (col & 3);
+      const int r0 = slot_entry(kg, col >> 2), r1 = slot_entry(kg, 4 + (col >> 2));
+      const i16x4 lo = lds_read_tr16(img + img_off<D, BF16>(r0, ch >> 3, (ch >> 2) & 1));
+      const i16x4 hi = lds_read_tr16(img + img_off<D, BF16>(r1, ch >> 3, (ch >> 2) & 1));
+      const i16x4 both[2] = {lo, hi};
+      v = __builtin_bit_cast(bf16x8, both);
+    } else {
+      // byte m: row slot_entry(kg, m) at channel 16 cb + (lane j of the row group)
+      const int r = slot_entry(kg, col >> 1);
+      v = fp8x8_bf16(lds_read_tr8(img + img_off<D, BF16>(r, cb, col & 1)));
     }
+    o[cb - kCb0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, plo, o[cb - kCb0], 0, 0, 0);
+    o[cb - kCb0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, phi, o[cb - kCb0], 0, 0, 0);
   }
-  const f32x4 s[2] = {s2[0][0] + s2[0][1], s2[1][0] + s2[1][1]};
-  // lane owns heads 4g+i, entries 16nt+col
-  const bool ok0 = sm.slot[tb + col] >= 0, ok1 = sm.slot[tb + 16 + col] >= 0;
-  const float ks0 = sm.kscale[tb + col], ks1 = sm.kscale[tb + 16 + col];
-  float x[2][4], mx[4];
-  bool grow = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[0][i] = ok0 ? s[0][i] * (sc2 * ks0) : -INFINITY;
-    x[1][i] = ok1 ? s[1][i] * (sc2 * ks1) : -INFINITY;
-    const float m = row16_max(fmaxf(x[0][i], x[1][i]));
-    mx[i] = m;
-    grow |= m > st.m2[i] + kRescaleSlack || (st.m2[i] == -INFINITY && m != -INFINITY);
-  }
-  const bool any = __any(grow);
-  if (any) {  // wave-uniform: move every head's reference to its max so far
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float mnew = fmaxf(st.m2[i], mx[i]);
-      float al = 1.0f;
-      if (mnew != -INFINITY) {
-        al = (st.m2[i] == -INFINITY) ? 0.0f : exp2f(st.m2[i] - mnew);
-        st.lsum[i] *= al;
-        st.m2[i] = mnew;
-      }
-      if (col == 0) sm.alpha[pb][16 * wave + 4 * g + i] = al;
-    }
-  }
-  if (lane == 0) sm.grow[pb][wave] = any ? 1 : 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool live = st.m2[i] != -INFINITY;
-    const float p0 = live ? exp2f(x[0][i] - st.m2[i]) : 0.0f;
-    const float p1 = live ? exp2f(x[1][i] - st.m2[i]) : 0.0f;
-    st.lsum[i] += p0 + p1;
-    const int prow = (16 * wave + 4 * g + i) * SM::kPRow;
-    const float w0 = p0 * ks0, w1 = p1 * ks1;
-    const uint32_t pk = bf16x2_bits(w0, w1);
-    const float h0 = __uint_as_float(pk << 16), h1 = __uint_as_float(pk & 0xffff0000u);
-    const uint32_t pl = bf16x2_bits(w0 - h0, w1 - h1);  // exact differences
-    sm.p[pb][prow + col] = static_cast<uint16_t>(pk & 0xffffu);
-    sm.p[pb][prow + 16 + col] = static_cast<uint16_t>(pk >> 16);
-    sm.plo[pb][prow + col] = static_cast<uint16_t>(pl & 0xffffu);
-    sm.plo[pb][prow + 16 + col] = static_cast<uint16_t>(pl >> 16);
+}
+
+// Channels 16 cb + 4 kg .. +3 of head 16 grp + col (this lane's O^T
+// values) times f: bf16 output of a row finished in place, else the split's
+// fp32 partial.
+template <bool kUnused>
+__device__ __forceinline__ void store_o(const DecodeArgs& a, int t, int l, int nsplit, int grp, int cb, float f,
+                                        const f32x4& v) {
+  const int lane = threadIdx.x & 63;
+  const int kg = lane >> 4, col = lane & 15;
+  const int h = 16 * grp + col;
+  const int c0 = 16 * cb + 4 * kg;
+  if (nsplit == 1) {
+    uint16_t* o = a.out + static_cast<int64_t>(t) * a.out_tok_stride + h * a.out_head_stride + c0;
+    *reinterpret_cast<uint2*>(o) = make_uint2(
+        static_cast<uint32_t>(f32_to_bf16(v[0] * f)) | (static_cast<uint32_t>(f32_to_bf16(v[1] * f)) << 16),
+        static_cast<uint32_t>(f32_to_bf16(v[2] * f)) | (static_cast<uint32_t>(f32_to_bf16(v[3] * f)) << 16));
+  } else {
+    float* o = a.ws_o + (static_cast<int64_t>(l) * a.heads + h) * kDv + c0;
+    *reinterpret_cast<float4*>(o) = make_float4(v[0] * f, v[1] * f, v[2] * f, v[3] * f);
   }
 }
 
@@ -466,16 +362,16 @@ sparse_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   using SM = DecodeSmem<D, BF16>;
   SM& sm = *reinterpret_cast<SM*>(smem_raw);
-  auto kimg = [&](int i) -> uint8_t* { return sm.img + i * SM::kImgB; };
   constexpr int KS = D / 32;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, col = lane & 15;
+  const int kg = lane >> 4, col = lane & 15;
   const int hgroups = a.heads / 16;
-  const bool scorer = wave < kScoreWaves;
-  // Logical workgroup: consecutive ids share an XCD (hardware workgroup b
-  // runs on XCD b % 8), so a row's splits read its q through one L2.
+  const bool scorer = wave < kGroups;
+  const int grp = scorer ? wave : wave - kGroups;   // head group; waves w and w + 4 share SIMD w
+  const bool active = grp < hgroups;
+
   const int b = blockIdx.x;
   const int l = (b % kXcds) * (a.groups / kXcds) + b / kXcds;
   int t, split, nsplit, first;
@@ -483,27 +379,15 @@ sparse_decode_kernel(DecodeArgs a) {
   if (t < 0) return;
   if (split == 0 && tid == 0) a.ws_rows[t] = make_int2(first, nsplit);
 
-  // q operands of the score waves (A of S = Q K^T): head 16w + col, dims 32ks + 8g .. +8
-  bf16x8 qa[KS];
-  if (scorer && wave < hgroups) {
-    const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (16 * wave + col) * a.q_head_stride;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qa[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * g));
-  }
-
-  // Prologue: entries -> slots, two dependent gathers (index, block table;
-  // one without a block table) each issued for all of the thread's entries
-  // first.  The rows' scales come with the rows.
   const int len = row_len(a, t);
   const int per_split = ((len + kTile - 1) / kTile + nsplit - 1) / nsplit * kTile;
   const int e_begin = split * per_split;
   const int e_cnt = max(0, min(e_begin + per_split, len) - e_begin);
   const int ntiles = (e_cnt + kTile - 1) / kTile;
   const int e_pad = ntiles * kTile;
-  // Steps of the main loop: step s finishes tile s-1 and scores tile s, so
-  // ntiles + 1 steps, rounded up to even (the data waves take steps in pairs).
-  const int steps = (ntiles + 2) & ~1;
+
+  // Prologue: entries -> slots (index, then block table), each gather issued
+  // for all of the thread's entries before the next.
   constexpr int kPrologue = kMaxSplitEntries / kThreads;
   int64_t sv[kPrologue];
 #pragma unroll
@@ -527,141 +411,199 @@ sparse_decode_kernel(DecodeArgs a) {
     const int64_t slot = (sv[j] >= 0 && sv[j] < a.num_rows) ? sv[j] : -1;
     if (e < e_pad) sm.slot[e] = static_cast<int32_t>(slot);
   }
-  if (tid < 2 * kScoreWaves) sm.grow[tid / kScoreWaves][tid % kScoreWaves] = 0;
+  __syncthreads();
+  // Data waves: the first kAhead tiles in flight (the only vector memory
+  // operations they issue, so their load counter counts tiles).  Scorer
+  // waves: the row scales and the q operands.
+  bf16x8 qb[KS];  // B operand of S^T = K Q^T: head 16 grp + col, dims 32 ks + 8 kg .. +7
+  if (!scorer) {
+    for (int i = 0; i < SM::kAhead && i < ntiles; ++i) issue_tile<D, BF16>(a, sm, grp, i);
+    wait_tiles<D, BF16>(min(SM::kAhead, ntiles) - 1);  // tile 0 landed
+    if (0 < ntiles) zero_masked<D, BF16>(sm, grp, 0);
+  } else {
+    constexpr int kPer = kMaxSplitEntries / (64 * kGroups);
+    float ksv[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 64 * kGroups * j;
+      const int s = (e < e_pad) ? sm.slot[e] : -1;
+      if constexpr (BF16) ksv[j] = s >= 0 ? 1.0f : 0.0f;
+      else ksv[j] = s >= 0 ? *reinterpret_cast<const float*>(a.cache + static_cast<int64_t>(s >> 6) * a.page_stride +
+                                                              kPageTokens * D + (s & 63) * 4)
+                           : 0.0f;
+    }
+    if (active) {
+      const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (16 * grp + col) * a.q_head_stride;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * kg));
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 64 * kGroups * j;
+      if (e < e_pad) sm.kscale[e] = ksv[j];
+    }
+  }
   __syncthreads();
 
-  f32x4 o[4][4];
+  // O^T accumulators: the scorer wave of a group holds channels [0, 128), the
+  // data wave [128, 512).  The two roles run separate loops with the same
+  // barriers (one per step, ntiles + 1 steps).
+  constexpr int kCbA = 8;
+  constexpr int kChains = 4;  // QK accumulation chains per entry half
+  if (scorer) {
+    f32x4 oa[kCbA];
 #pragma unroll
-  for (int hf = 0; hf < 4; ++hf)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) o[hf][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  if (!scorer) {
-    // ---------------- data waves ----------------
-    const int u = wave - kScoreWaves;
-    RowRegs<D, BF16> bufA, bufB;  // even tiles in A, odd tiles in B
-    fetch_rows<D, BF16>(a, sm, u, 0, ntiles, bufA);
-    fetch_rows<D, BF16>(a, sm, u, 1, ntiles, bufB);
-    store_rows<D, BF16>(bufA, u, 0, sm, kimg(0));
-    fetch_rows<D, BF16>(a, sm, u, 2, ntiles, bufA);
-    __syncthreads();  // tile 0 stored
-    // Step s finishes tile s-1 (P V from image (s-1) % 3), stores tile s+1 into
-    // image (s+1) % 3 and issues the loads of tile s+3.  Every load and
-    // store is unconditional (tiles past the end are zero rows nobody
-    // reads), so each wait leaves the newer tile in flight.
-    store_rows<D, BF16>(bufB, u, 1, sm, kimg(1));  // step 0
-    fetch_rows<D, BF16>(a, sm, u, 3, ntiles, bufB);
-    __syncthreads();
-    int s = 1, kp = 0;  // kp: image of tile s-1
-    for (; s + 1 <= ntiles; s += 2) {
-      const int k1 = (kp == 2) ? 0 : kp + 1, k2 = (k1 == 2) ? 0 : k1 + 1;
-      accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
-      store_rows<D, BF16>(bufA, u, s + 1, sm, kimg(k2));
-      fetch_rows<D, BF16>(a, sm, u, s + 3, ntiles, bufA);
-      __syncthreads();
-      accumulate_pv<D, BF16>(sm, kimg(k1), s & 1, hgroups, o);
-      store_rows<D, BF16>(bufB, u, s + 2, sm, kimg(kp));
-      fetch_rows<D, BF16>(a, sm, u, s + 4, ntiles, bufB);
-      __syncthreads();
-      kp = k2;
-    }
-    // the last (odd) step
-    if (s - 1 < ntiles) accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
-    __syncthreads();
-  } else {
-    // ---------------- score waves ----------------
-    SoftmaxState st;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      st.m2[i] = -INFINITY;
-      st.lsum[i] = 0.0f;
-    }
+    for (int i = 0; i < kCbA; ++i) oa[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m2 = -INFINITY, lsum = 0.0f;  // reference max (log2 units) and this lane's share of l, head col
     const float sc2 = a.scale * kLog2e;
-    __syncthreads();  // tile 0 stored
-    // Step s finishes tile s-1 and scores tile s (image s % 3, P buffer s & 1).
-    // Score waves past `hgroups` run on unused heads rather than branching.
-    if (ntiles == 0) {
-      for (int s = 0; s < steps; ++s) __syncthreads();
-    } else {
-      score_tile<D, BF16>(sm, kimg(0), 0, 0, sc2, qa, st);
-      __syncthreads();
-      int kp = 0;  // image of tile s-1
-      for (int s = 1; s < ntiles; ++s) {
-        const int kr = (kp == 2) ? 0 : kp + 1;
-        accumulate_pv<D, BF16>(sm, kimg(kp), (s - 1) & 1, hgroups, o);
-        score_tile<D, BF16>(sm, kimg(kr), s & 1, s * kTile, sc2, qa, st);
-        __syncthreads();
-        kp = kr;
-      }
-      accumulate_pv<D, BF16>(sm, kimg(kp), (ntiles - 1) & 1, hgroups, o);
-      __syncthreads();
-      for (int s = ntiles + 1; s < steps; ++s) __syncthreads();
-    }
-    // final denominators and maxima of this wave's heads: a row of one split
-    // is finished here (sink, lse), otherwise its partial goes to the combine
-    if (wave < hgroups) {
-      const int64_t base = static_cast<int64_t>(l) * a.heads;
+    for (int s = 0; s <= ntiles; ++s) {
+      if (s < ntiles && active) {
+        const uint8_t* img = sm.img[s % SM::kBufs];
+        const int tb = s * kTile;
+        // S^T = K Q^T for entries [16 nt, 16 nt + 16): eight accumulation
+        // chains (an MFMA's result is ready ~4 issues later)
+        f32x4 st[2][kChains];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lsum = row16_sum(st.lsum[i]);
-        if (col == 0) {
-          const int h = 16 * wave + 4 * g + i;
-          const float m = st.m2[i];
-          if (nsplit == 1) {
-            float den = lsum, numf = 1.0f;
-            if (a.sinks != nullptr) {
-              const float sk = a.sinks[h] * kLog2e;
-              const float mp = fmaxf(m, sk);
-              if (mp != -INFINITY) {
-                numf = (m == -INFINITY) ? 0.0f : exp2f(m - mp);
-                den = lsum * numf + exp2f(sk - mp);
-              }
-            }
-            sm.row_f[h] = (den > 0.0f) ? numf / den : 0.0f;
-            if (a.lse != nullptr)
-              a.lse[static_cast<int64_t>(t) * a.lse_stride + h] = (lsum > 0.0f) ? (m + log2f(lsum)) * kLn2 : -INFINITY;
-          } else {
-            sm.row_f[h] = (lsum > 0.0f) ? 1.0f / lsum : 0.0f;
-            a.ws_ml[(base + h) * 2 + 0] = m;
-            a.ws_ml[(base + h) * 2 + 1] = lsum;
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int c = 0; c < kChains; ++c) st[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const int e = 16 * nt + col;
+            bf16x8 kf;
+            if constexpr (BF16)
+              kf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(img + img_off<D, BF16>(e, 4 * ks + kg, 0)));
+            else
+              kf = fp8x8_bf16(*reinterpret_cast<const uint2*>(img + img_off<D, BF16>(e, 2 * ks + (kg >> 1), kg & 1)));
+            st[nt][ks % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[ks], st[nt][ks % kChains], 0, 0, 0);
           }
         }
+        // this lane: head col, entries slot_entry(kg, m)
+        const float4 k0 = *reinterpret_cast<const float4*>(&sm.kscale[tb + 4 * kg]);
+        const float4 k1 = *reinterpret_cast<const float4*>(&sm.kscale[tb + 16 + 4 * kg]);
+        const float ks8[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        f32x4 s0 = st[0][0], s1 = st[1][0];
+#pragma unroll
+        for (int c = 1; c < kChains; ++c) {
+          s0 += st[0][c];
+          s1 += st[1][c];
+        }
+        const float sv8[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        float x[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          x[m] = ks8[m] > 0.0f ? sv8[m] * (sc2 * ks8[m]) : -INFINITY;
+          mx = fmaxf(mx, x[m]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool grow = mx > m2 + kRescaleSlack || (m2 == -INFINITY && mx != -INFINITY);
+        const bool any = __any(grow);
+        if (any) {  // wave-uniform: move every head's reference to its max so far
+          const float mnew = fmaxf(m2, mx);
+          float al = 1.0f;
+          if (mnew != -INFINITY) {
+            al = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - mnew);
+            lsum *= al;
+            m2 = mnew;
+          }
+#pragma unroll
+          for (int i = 0; i < kCbA; ++i) oa[i] *= al;
+          if (kg == 0) sm.alpha[s & 1][grp][col] = al;
+        }
+        if (lane == 0) sm.grow[s & 1][grp] = any ? 1 : 0;
+        const bool live = m2 != -INFINITY;
+        float w[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const float p = live ? exp2f(x[m] - m2) : 0.0f;
+          lsum += p;
+          w[m] = p * ks8[m];
+        }
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          hi[m] = bf16x2_bits(w[2 * m], w[2 * m + 1]);
+          const float h0 = __uint_as_float(hi[m] << 16), h1 = __uint_as_float(hi[m] & 0xffff0000u);
+          lo[m] = bf16x2_bits(w[2 * m] - h0, w[2 * m + 1] - h1);  // exact differences
+        }
+        const uint4 phu = make_uint4(hi[0], hi[1], hi[2], hi[3]), plu = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        sm.p[s & 1][grp][0][lane] = phu;
+        sm.p[s & 1][grp][1][lane] = plu;
+        pv_tile<D, BF16, 0, kCbA>(img, __builtin_bit_cast(bf16x8, phu), __builtin_bit_cast(bf16x8, plu), oa);
       }
+      __syncthreads();
     }
-  }
-  __syncthreads();
-
-  if (nsplit == 1) {
-    // the finished row in bf16: 16 consecutive channels (32 bytes) of one head
-    // per store instruction
-#pragma unroll
-    for (int hf = 0; hf < 4; ++hf) {
-      if (hf >= hgroups) break;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = 16 * hf + 4 * g + i;
-        const float f = sm.row_f[h];
-        uint16_t* orow = a.out + static_cast<int64_t>(t) * a.out_tok_stride + h * a.out_head_stride + 64 * wave + col;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) orow[16 * nt] = f32_to_bf16(o[hf][nt][i] * f);
+    // Epilogue: finish the heads' softmax (a row of one split gets the sink
+    // and its lse here, otherwise (m, l) go to the combine), publish the
+    // factor for the data wave, scale and store channels [0, 128).
+    float f = 0.0f;
+    if (active) {
+      float lt = lsum + __shfl_xor(lsum, 16);
+      lt += __shfl_xor(lt, 32);
+      const int h = 16 * grp + col;
+      if (nsplit == 1) {
+        float den = lt, numf = 1.0f;
+        if (a.sinks != nullptr) {
+          const float sk = a.sinks[h] * kLog2e;
+          const float mp = fmaxf(m2, sk);
+          if (mp != -INFINITY) {
+            numf = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - mp);
+            den = lt * numf + exp2f(sk - mp);
+          }
+        }
+        f = (den > 0.0f) ? numf / den : 0.0f;
+        if (kg == 0 && a.lse != nullptr)
+          a.lse[static_cast<int64_t>(t) * a.lse_stride + h] = (lt > 0.0f) ? (m2 + log2f(lt)) * kLn2 : -INFINITY;
+      } else {
+        f = (lt > 0.0f) ? 1.0f / lt : 0.0f;
+        if (kg == 0) {
+          const int64_t row = static_cast<int64_t>(l) * a.heads + h;
+          a.ws_ml[row * 2 + 0] = m2;
+          a.ws_ml[row * 2 + 1] = lt;
+        }
       }
+      if (kg == 0) sm.fin[grp][col] = f;
     }
-    return;
-  }
-  // O / l of the split in fp32 (the combine sums the splits' partials, which
-  // may cancel, so they keep fp32 precision): each store instruction writes
-  // 16 consecutive channels (64 bytes) of one head.
-  const int64_t base = static_cast<int64_t>(l) * a.heads;
+    __syncthreads();
+    if (active) {
 #pragma unroll
-  for (int hf = 0; hf < 4; ++hf) {
-    if (hf >= hgroups) break;
+      for (int i = 0; i < kCbA; ++i) store_o<false>(a, t, l, nsplit, grp, i, f, oa[i]);
+    }
+  } else {
+    constexpr int kCbB = kDv / 16 - kCbA;
+    f32x4 ob[kCbB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 16 * hf + 4 * g + i;
-      const float inv = sm.row_f[h];
-      float* orow = a.ws_o + (base + h) * kDv + 64 * wave + col;
+    for (int i = 0; i < kCbB; ++i) ob[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s <= ntiles; ++s) {
+      if (s + SM::kAhead < ntiles) issue_tile<D, BF16>(a, sm, grp, s + SM::kAhead);
+      if (s >= 1 && active) {
+        const uint8_t* img = sm.img[(s - 1) % SM::kBufs];
+        const int pb = (s - 1) & 1;
+        if (sm.grow[pb][grp]) {
+          const float al = sm.alpha[pb][grp][col];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) orow[16 * nt] = o[hf][nt][i] * inv;
+          for (int i = 0; i < kCbB; ++i) ob[i] *= al;
+        }
+        const bf16x8 phi = __builtin_bit_cast(bf16x8, sm.p[pb][grp][0][lane]);
+        const bf16x8 plo = __builtin_bit_cast(bf16x8, sm.p[pb][grp][1][lane]);
+        pv_tile<D, BF16, kCbA, kDv / 16>(img, phi, plo, ob);
+      }
+      // tile s + 1 must have landed when the step ends; tiles s + 2 ..
+      // s + kAhead may stay in flight
+      wait_tiles<D, BF16>(min(ntiles - 1, s + SM::kAhead) - (s + 1));
+      if (s + 1 < ntiles) zero_masked<D, BF16>(sm, grp, s + 1);
+      __syncthreads();
+    }
+    __syncthreads();  // the scorer wave's factor
+    if (active) {
+      const float f = sm.fin[grp][col];
+#pragma unroll
+      for (int i = 0; i < kCbB; ++i) store_o<false>(a, t, l, nsplit, grp, kCbA + i, f, ob[i]);
     }
   }
 }
@@ -780,7 +722,7 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   EKV_CHECK(num_tokens >= 0 && width >= 0, "sizes must be >= 0");
   if (num_tokens == 0) return 0;
   EKV_CHECK(dim == 512 || dim == 576, "dim must be 512 or 576");
-  EKV_CHECK(heads > 0 && heads % 16 == 0 && heads <= 16 * kScoreWaves, "heads must be a multiple of 16, <= 64");
+  EKV_CHECK(heads > 0 && heads % 16 == 0 && heads <= 16 * kGroups, "heads must be a multiple of 16, <= 64");
   EKV_CHECK(q && cache && indices && out, "null pointer");
   EKV_CHECK(block_table == nullptr || req_ids != nullptr, "block_table needs req_ids");
   EKV_CHECK(q_tok_stride % 8 == 0 && q_head_stride % 8 == 0 && aligned16(q), "q must be 16-byte aligned rows");
