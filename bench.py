@@ -7,26 +7,35 @@ quantize the indexer queries, score every non-window token exactly, select the
 top-2048 (lowest index on ties), append the 128-token window, gather the 2176
 rows and run 64-head sparse MLA decode with a sink.  Inputs are synthetic
 (seeded) and resident in HBM before the timed region.  The step is issued
-eagerly on one stream (the GPU, not the host, is the bottleneck: HIP graph
-replay and a forked stream for the cache appends both measured slower).
+eagerly on one stream.
 
-Prints ONE JSON line.  ``value`` = algorithmic HBM bytes per step / step time
-(GB/s), the metric's unit; ``tok_per_s`` = decode tokens per second.
-Algorithmic bytes per step: indexer K rows 132 B x sum of windowed lengths,
-gathered latent rows 580 B x 2176 per row, plus q / out tensors.
+Prints ONE JSON line.  ``value`` = algorithmic HBM bytes of the DSA step /
+step time (GB/s), the metric's unit.  Algorithmic bytes per step: indexer K
+rows 132 B x sum of windowed lengths, gathered latent rows 580 B x 2176 per
+row, plus q / out tensors.  ``tok_per_s`` = decode tokens per second of the
+model's whole attention KV path at this shape: 6 DSA layer steps + 37 HCA
+layer steps (the HCA decode measured at the same 32 x 131,072 contexts);
+``tok_per_s_dsa_layer`` is one DSA layer alone.
 
 The line also carries the other workloads, each measured on its own:
 ``hca_write`` (chunked-prefill cache write, 16 x 8192 tokens), ``hca_decode``
 (HCA decode step, 64 sequences at 8K-128K contexts) and ``mtp`` (DSA and HCA
 layer decode steps at 8 x 256K + 1 x 1M contexts with 3 query rows per
-sequence, and the model step composed from them).  ``--only`` runs one of
-them alone.
+sequence, drafts accepted with p = 0.7 and rejected ones re-appended at the
+next step, and the model step composed from them).  ``--only`` runs one of
+them alone.  ``roofline.traffic`` (and each leg's ``traffic``) is the HBM
+traffic per launch of the leg's dominant kernel from the committed rocprofv3
+counter summary profiles/hbm_traffic.json, or null when that file holds no
+reading for the workload.  ``cpu_baseline`` (and each leg's) is the numpy
+oracle on a process pool over the host's cores, timed before the GPU is
+touched.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import os
 import sys
 import time
 from pathlib import Path
@@ -36,13 +45,10 @@ sys.path.insert(0, str(ROOT / "vllm-ernie_amd"))
 
 METRIC = "KV gather+decode HBM GB/s (% of 8 TB/s); decode tok/s/GPU at 128K ctx"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes one filter_verify_kernel launch moves on the default workload:
-# rocprofv3 FETCH_SIZE (590.2 MB) + WRITE_SIZE (10.8 MB) per dispatch, each
-# scaled by what the counter reads for a 512 MiB device copy (x2.0 fetch, x1.0
-# write; run bench.py --copy-mb 512 under rocprofv3 --pmc to reproduce).
-FILTER_TRAFFIC_BYTES = 590_228_753 + 10_803_104
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
+MODEL_LAYERS = {"dsa": 6, "hca": 37}  # ERNIE 5.5: 37 HCA : 6 DSA attention layers
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 
 
 def parse():
@@ -57,24 +63,40 @@ def parse():
                    help="skip the HCA measurements (chunked-prefill write, decode step)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-mtp", action="store_true", help="skip the multi-token-prediction (1M-context) measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp"], default=None,
-                   help="run only this HCA measurement and print its JSON object (for profiling one workload)")
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa"], default=None,
+                   help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return p.parse_args()
 
 
-def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, spike_frac: float = 0.05):
+def traffic_of(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    counter summary, or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    rec = data.get("workloads", {}).get(workload)
+    if not rec or rec.get("kernel") != kernel:
+        return None
+    return rec.get("bytes")
+
+
+# --------------------------------------------------------------------------- DSA step
+def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, spike_frac: float = 0.05,
+                     extra_tokens: int = 0):
     """Synthetic DSA-layer decode state: sequence s holds ctxs[s] tokens, the
     last rows_per_seq of them new this step (one query row each: the token
-    and its draft tokens), in permuted pages."""
+    and its draft tokens), in permuted pages (extra_tokens more positions
+    are mapped for steps that grow the sequences)."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
     S, R = len(ctxs), rows_per_seq
-    ctx = max(ctxs)
+    ctx = max(ctxs) + extra_tokens
     B = S * R  # query rows
-    pps = [(c + 63) // 64 for c in ctxs]
+    pps = [(c + extra_tokens + 63) // 64 for c in ctxs]
     num_pages = sum(pps)
     perm = torch.randperm(num_pages, device=dev, generator=g).to(torch.int32)
     block_table = torch.full((S, max(pps)), -1, dtype=torch.int32, device=dev)
@@ -164,6 +186,15 @@ def dsa_post(ops, st, ev=None):
         ev[3].record()
 
 
+def dsa_bytes(B: int, ctx: int) -> dict:
+    n = max(ctx - 128, 0)
+    k_read = B * n * 132
+    gather = B * (min(n, 2048) + min(ctx, 128)) * 580
+    qo = B * 64 * 576 * 2 + B * 64 * 512 * 2 + B * 64 * 128 * 2 + B * 64 * 2 + B * 64 * 4
+    return {"indexer_k": k_read, "gather": gather, "q_out": qo, "total": k_read + gather + qo}
+
+
+# --------------------------------------------------------------------------- HCA write (config 4)
 def build_hca_write(torch, ops, seed: int, B: int = 16, chunk: int = 8192, max_off: int = 65536, D: int = 576):
     """Chunked-prefill cache write: B sequences each appending a `chunk`-token
     chunk at a random offset in [0, max_off), scattered by a random slot
@@ -212,40 +243,39 @@ def hca_write_step(ops, st):
                   st["ring_pages"], 128, st["pool"])
 
 
-def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
-    st = build_hca_write(torch, ops, seed)
-    for _ in range(2):
-        hca_write_step(ops, st)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
-        hca_write_step(ops, st)
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
-    T, D, B = st["T"], st["D"], st["B"]
+def hca_write_bytes(T: int, D: int, B: int, spans_done: int) -> dict:
     # the survey's algorithmic bytes: latent rows read (bf16) and written
     # (fp8 + scale), compressed entries and window-ring rows written
-    surveyed = T * D * 2 + T * (D + 4) + st["spans_done"] * (D + 4) + B * 128 * (D + 4)
+    surveyed = T * D * 2 + T * (D + 4) + spans_done * (D + 4) + B * 128 * (D + 4)
     # plus the compressor's kv || score rows (bf16, 2D per token) read once and
     # the state-ring rows (last 256 positions per sequence) copied
     full = surveyed + T * 2 * D * 2 + 2 * B * 256 * 2 * D * 2
+    return {"latent_rows": surveyed, "with_kv_score": full}
+
+
+def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
+    st = build_hca_write(torch, ops, seed)
+    ms = time_ms(torch, lambda: hca_write_step(ops, st), reps, warmup=2)
+    by = hca_write_bytes(st["T"], st["D"], st["B"], st["spans_done"])
+    workload = f"hca_chunked_prefill_b{st['B']}_chunk{st['chunk']}"
     return {
-        "workload": f"hca_chunked_prefill_b{B}_chunk{st['chunk']}",
+        "workload": workload,
         "kernels": "hca_compress_kernel<576> + hca_append_kernel<576> (rows, window ring, state ring)",
         "ms": round(ms, 4),
-        "bytes_latent_rows": surveyed,
-        "GB/s_latent_rows": round(surveyed / (ms * 1e-3) / 1e9, 1),
-        "frac_latent_rows": round(surveyed / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "bytes_with_kv_score": full,
-        "GB/s_with_kv_score": round(full / (ms * 1e-3) / 1e9, 1),
-        "frac_with_kv_score": round(full / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_latent_rows": by["latent_rows"],
+        "GB/s_latent_rows": round(by["latent_rows"] / (ms * 1e-3) / 1e9, 1),
+        "frac_latent_rows": round(by["latent_rows"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_with_kv_score": by["with_kv_score"],
+        "GB/s_with_kv_score": round(by["with_kv_score"] / (ms * 1e-3) / 1e9, 1),
+        "frac_with_kv_score": round(by["with_kv_score"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": {"kernel": "hca_compress_kernel<576>",
+                    "bytes": traffic_of(workload, "hca_compress_kernel<576>")},
     }
 
 
+# --------------------------------------------------------------------------- HCA decode (config 2)
 def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx_hi: int = 131072, D: int = 576,
-                     ring: int = 128, ctxs: list | None = None, rows_per_seq: int = 1):
+                     ring: int = 128, ctxs: list | None = None, rows_per_seq: int = 1, extra_tokens: int = 0):
     """HCA-layer decode step state: B sequences with seeded contexts in
     [ctx_lo, ctx_hi) (or the given ctxs), their compressed entries and window
     rings as random fp8 rows (fp32 scale 2^-8) in permuted pages, and
@@ -260,19 +290,23 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
         ctx_hi = int(ctx.max()) + 1
     else:
         ctx = torch.randint(ctx_lo, ctx_hi, (B,), generator=gc).to(torch.int64)
+    ctx_hi += extra_tokens
     R = rows_per_seq
     T = B * R
     spans = ctx_hi // 128 + 1
     comp_pages = (spans + 63) // 64
     ring_pp = (ring + 63) // 64
-    pages = B * (comp_pages + ring_pp + 1)
+    lat_pp = 1 + (extra_tokens + R + 63) // 64  # pages for the new tokens' own rows
+    pages = B * (comp_pages + ring_pp + lat_pp)
     perm = torch.randperm(pages, generator=gc).to(torch.int32)
     comp_bt = perm[: B * comp_pages].view(B, comp_pages).to(dev)
     ring_pages = perm[B * comp_pages: B * (comp_pages + ring_pp)].view(B, ring_pp).to(dev)
-    latent_page = perm[B * (comp_pages + ring_pp):].to(torch.int64)
+    lat_bt = perm[B * (comp_pages + ring_pp):].view(B, lat_pp).to(torch.int64)
     # the new tokens: the last R positions of each context
     positions = ctx.repeat_interleave(R) - R + torch.arange(R).repeat(B)
-    slots = (latent_page.repeat_interleave(R) * 64 + positions % 64).to(dev)
+    base = (ctx - R)  # first new position per sequence; its rows go to the sequence's own pages
+    rel = positions - base.repeat_interleave(R)
+    slots = (lat_bt[torch.arange(B).repeat_interleave(R), rel // 64] * 64 + rel % 64).to(dev)
     codes = torch.randint(0, 256, (pages, 64 * D), device=dev, dtype=torch.uint8, generator=gd)
     codes -= ((codes & 0x7F) == 0x7F).to(torch.uint8)  # no NaN codes
     scales = torch.full((pages, 64), 2.0 ** -8, device=dev, dtype=torch.float32)
@@ -281,7 +315,7 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
     width = (ctx_hi // 128) + ring
     rnd = lambda *s: torch.randn(*s, device=dev, generator=gd).to(torch.bfloat16)  # noqa: E731
     st = dict(
-        B=B, T=T, R=R, D=D, ring=ring, ctx=ctx, width=width,
+        B=B, T=T, R=R, D=D, ring=ring, ctx=ctx, width=width, base=base, lat_bt=lat_bt,
         pool=torch.cat([codes, scales.view(torch.uint8)], dim=1).contiguous(),
         latent=rnd(T, D), kv_score=rnd(T, 2 * D), state=rnd(B + 2, 256, 2 * D),
         state_slot=torch.randperm(B + 2, generator=gc)[:B].to(torch.int32).to(dev),
@@ -342,13 +376,14 @@ def hca_decode_bytes(st) -> dict:
     return {"rows": rows, "gather": gather, "q_out": q_out, "append": append, "total": gather + q_out + append}
 
 
-def measure_hca_decode(torch, ops, seed: int, reps: int = 50) -> dict:
-    st = build_hca_decode(torch, ops, seed)
+def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None = None, label: str | None = None) -> dict:
+    st = build_hca_decode(torch, ops, seed, ctxs=ctxs)
     ms = time_ms(torch, lambda: hca_decode_step(ops, st), reps)
     by = hca_decode_bytes(st)
+    workload = label or f"hca_decode_b{st['B']}_ctx8192-131072"
     return {
-        "workload": f"hca_decode_b{st['B']}_ctx8192-131072",
-        "kernels": "hca_compress_kernel<576> (spans completed by the new token) + hca_append_kernel<576> + "
+        "workload": workload,
+        "kernels": "hca_write_small_kernel<576> (the new tokens' rows, ring, state; spans they complete) + "
                    "hca_decode_indices_kernel + sparse_decode_kernel<576> + decode_combine_kernel",
         "ms": round(ms, 4),
         "rows_per_step": by.pop("rows"),
@@ -356,43 +391,96 @@ def measure_hca_decode(torch, ops, seed: int, reps: int = 50) -> dict:
         "GB/s": round(by["total"] / (ms * 1e-3) / 1e9, 1),
         "frac": round(by["total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "tok_per_s": round(st["T"] / (ms * 1e-3), 1),
+        "traffic": {"kernel": "sparse_decode_kernel<576>", "bytes": traffic_of(workload, "sparse_decode_kernel<576>")},
     }
 
 
+# --------------------------------------------------------------------------- MTP (config 5)
 MTP_CTXS = [262144] * 8 + [1048576]
 MTP_ROWS = 3  # the token and its 2 draft tokens
-MTP_LAYERS = {"dsa": 6, "hca": 37}
 MTP_ACCEPT = 0.7
+MTP_STEPS = 13  # 3 warmup + 10 timed
 
 
-def measure_mtp(torch, ops, seed: int, reps: int = 10) -> dict:
+def mtp_schedule(ctxs: list, steps: int, seed: int):
+    """Per step, the first query position of each sequence: the step's rows
+    are that position and the next two (token + 2 drafts).  Draft 1 is
+    accepted with p = 0.7, draft 2 (if draft 1 was) with p = 0.7; the next
+    step starts after the last accepted row, so the rejected drafts'
+    positions are written again (re-appended).  Returns (first positions
+    [steps, S], accepted tokens per step)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed + 5)
+    first = np.array(ctxs, np.int64) - MTP_ROWS
+    firsts, accepted = [], []
+    for _ in range(steps):
+        firsts.append(first.copy())
+        a1 = rng.random(len(ctxs)) < MTP_ACCEPT
+        a2 = a1 & (rng.random(len(ctxs)) < MTP_ACCEPT)
+        acc = 1 + a1.astype(np.int64) + a2.astype(np.int64)
+        accepted.append(int(acc.sum()))
+        first = first + acc
+    return np.stack(firsts), accepted
+
+
+def measure_mtp(torch, ops, seed: int, steps: int = MTP_STEPS, warm: int = 3) -> dict:
     """Multi-token-prediction decode at 8 x 262,144 + 1 x 1,048,576 contexts,
-    3 query rows per sequence: one DSA layer step and one HCA layer step
-    measured, and the model step composed from them (6 DSA + 37 HCA layers)."""
+    3 query rows per sequence, drafts accepted with p = 0.7 and the rejected
+    ones re-appended at the next step: a DSA layer's and an HCA layer's
+    steps measured over the same accept/reject schedule, and the model step
+    composed from them (6 DSA + 37 HCA layers)."""
     S, R = len(MTP_CTXS), MTP_ROWS
-    st = build_dsa_decode(torch, ops, MTP_CTXS, seed, rows_per_seq=R, spike_frac=0.0)
-    dsa_ms = time_ms(torch, lambda: dsa_step(ops, st), reps)
-    pos = st["positions"].cpu()
-    n_row = (pos + 1 - 128).clamp(min=0)
+    firsts, accepted = mtp_schedule(MTP_CTXS, steps, seed)
+    grow = int(firsts[-1].max() - (max(MTP_CTXS) - R)) + 64
+    dev = torch.device("cuda:0")
+    offs = torch.arange(R, device=dev).repeat(S)
+    pos_steps = [torch.from_numpy(f).to(dev).repeat_interleave(R) + offs for f in firsts]
+
+    st = build_dsa_decode(torch, ops, MTP_CTXS, seed, rows_per_seq=R, spike_frac=0.0, extra_tokens=grow)
+    req = st["req_ids"].long()
+    dsa_pos = [p.contiguous() for p in pos_steps]
+    dsa_slots = [(st["block_table"][req, p // 64].to(torch.int64) * 64 + p % 64).contiguous() for p in pos_steps]
+
+    def dsa_at(i):
+        st["positions"], st["slots"] = dsa_pos[i], dsa_slots[i]
+        dsa_step(ops, st)
+
+    dsa_ms = sequence_ms(torch, dsa_at, steps, warm)
+    pos0 = pos_steps[0].cpu()
+    n_row = (pos0 + 1 - 128).clamp(min=0)
     k_once = sum(max(c - 128, 0) for c in MTP_CTXS) * 132  # each sequence's keys read once
     k_rows = int(n_row.sum()) * 132                       # read per query row, as this build does
-    gather = int((n_row.clamp(max=2048) + (pos + 1).clamp(max=128)).sum()) * 580
+    gather = int((n_row.clamp(max=2048) + (pos0 + 1).clamp(max=128)).sum()) * 580
     T = S * R
     qo = T * (64 * 576 * 2 + 64 * 512 * 2 + 64 * 128 * 2 + 64 * 2 + 64 * 4)
     del st
     torch.cuda.empty_cache()
     # the window ring holds the 128-row window of every query row (128 + R - 1
     # rows), in whole 64-row pages
-    sh = build_hca_decode(torch, ops, seed, ctxs=MTP_CTXS, rows_per_seq=R, ring=64 * ((128 + R - 1 + 63) // 64))
-    hca_ms = time_ms(torch, lambda: hca_decode_step(ops, sh), reps)
+    sh = build_hca_decode(torch, ops, seed, ctxs=MTP_CTXS, rows_per_seq=R, ring=64 * ((128 + R - 1 + 63) // 64),
+                          extra_tokens=grow)
+    base = sh["base"].to(dev).repeat_interleave(R)
+    lat_bt = sh["lat_bt"].to(dev)
+    sreq = torch.arange(S, device=dev).repeat_interleave(R)
+    hca_slots = [(lat_bt[sreq, (p - base) // 64] * 64 + (p - base) % 64).contiguous() for p in pos_steps]
+
+    def hca_at(i):
+        sh["positions"], sh["slots"] = dsa_pos[i], hca_slots[i]
+        hca_decode_step(ops, sh)
+
+    hca_ms = sequence_ms(torch, hca_at, steps, warm)
+    sh["positions"] = dsa_pos[0]
     hb = hca_decode_bytes(sh)
     del sh
     torch.cuda.empty_cache()
-    step_ms = MTP_LAYERS["dsa"] * dsa_ms + MTP_LAYERS["hca"] * hca_ms
-    tok_step = S * sum(MTP_ACCEPT ** i for i in range(R))  # expected accepted tokens per step
+    step_ms = MODEL_LAYERS["dsa"] * dsa_ms + MODEL_LAYERS["hca"] * hca_ms
+    tok_step = sum(accepted[warm:]) / (steps - warm)  # accepted tokens per step, drawn
     dsa_total = k_once + gather + qo
     return {
         "workload": f"mtp_decode_{S}seq_{R}rows_8x262144_1x1048576",
+        "accept": f"drafts accepted with p={MTP_ACCEPT} (draft 2 only after draft 1); rejected drafts re-appended "
+                  f"at the next step; {tok_step:.2f} tokens accepted per step over the timed steps",
         "dsa_layer": {
             "ms": round(dsa_ms, 4),
             "bytes": {"indexer_k_once": k_once, "indexer_k_per_row": k_rows, "gather": gather, "q_out": qo,
@@ -407,28 +495,42 @@ def measure_mtp(torch, ops, seed: int, reps: int = 10) -> dict:
         "model_step_ms": round(step_ms, 3),
         "model_step": "composed: 6 x dsa_layer.ms + 37 x hca_layer.ms (the attention KV path only)",
         "query_rows_per_s": round(T / (step_ms * 1e-3), 1),
-        "tok_per_s_accept_0.7": round(tok_step / (step_ms * 1e-3), 1),
+        "tok_per_s": round(tok_step / (step_ms * 1e-3), 1),
     }
 
 
-def dsa_bytes(B: int, ctx: int) -> dict:
-    n = max(ctx - 128, 0)
-    k_read = B * n * 132
-    gather = B * (min(n, 2048) + min(ctx, 128)) * 580
-    qo = B * 64 * 576 * 2 + B * 64 * 512 * 2 + B * 64 * 128 * 2 + B * 64 * 2 + B * 64 * 4
-    return {"indexer_k": k_read, "gather": gather, "q_out": qo, "total": k_read + gather + qo}
+def sequence_ms(torch, step_at, steps: int, warm: int) -> float:
+    """Average milliseconds of step_at(i) for i in [warm, steps) after running
+    steps 0 .. warm-1 untimed (events on the current stream)."""
+    for i in range(warm):
+        step_at(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(warm, steps):
+        step_at(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (steps - warm)
 
 
-def cpu_baseline(B: int, ctx: int, seed: int) -> dict:
-    """Oracle (numpy, this build's CPU restatement) on a bounded sample: one
-    query row of the same workload (scoring all its tokens, top-2048, decode)."""
+# --------------------------------------------------------------------------- CPU baselines
+def _cpu_workers() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def _cpu_dsa_row(args):
+    """Oracle of one DSA query row: exact scores of its n keys, top-2048,
+    64-head decode over 2176 gathered rows.  Synthetic inputs of the
+    headline's shape (seeded per row)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT))
     from oracle import decode as od
     from oracle import indexer as oi
-    from oracle.fp8 import bf16_round
+    from oracle.fp8 import bf16_round, decode_e4m3
 
+    ctx, seed = args
     rng = np.random.default_rng(seed)
     n = max(ctx - 128, 0)
     codes = rng.integers(0, 256, (n, 128)).astype(np.uint8)
@@ -436,46 +538,126 @@ def cpu_baseline(B: int, ctx: int, seed: int) -> dict:
     kscale = np.full(n, 2.0 ** -8, np.float32)
     q = bf16_round(rng.standard_normal((64, 128)).astype(np.float32))
     w = bf16_round(rng.standard_normal(64).astype(np.float32))
-    qc, wf = oi.quantize_q(q[None], w[None])
     lat_codes = rng.integers(0, 256, (2176, 576)).astype(np.uint8)
     lat_codes[(lat_codes & 0x7F) == 0x7F] ^= 1
-    from oracle.fp8 import decode_e4m3
-
     rows = decode_e4m3(lat_codes).astype(np.float64) * 2.0 ** -8
     qm = bf16_round(rng.standard_normal((1, 64, 576)).astype(np.float32))
     sinks = rng.standard_normal(64).astype(np.float32)
     t0 = time.perf_counter()
+    qc, wf = oi.quantize_q(q[None], w[None])
     sc = oi.exact_scores(qc[0], wf[0], codes, kscale)
     top = oi.topk_ascending(sc, 2048)
-    idx = np.concatenate([np.arange(2176)])[None].astype(np.int32)
+    idx = np.concatenate([top, np.arange(n, n + 128)])[None]
+    idx = np.where(idx >= 0, idx % 2176, -1)
     od.sparse_mla_decode(qm, lambda s: rows[s], idx, 256 ** -0.5, 512, sinks)
-    dt = time.perf_counter() - t0
-    row_bytes = dsa_bytes(1, ctx)["total"]
-    return {
-        "value": round(row_bytes / dt / 1e9, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"1 query row of the same step (ctx {ctx}: exact scores of {n} keys, top-2048, "
-                  f"64-head decode over 2176 rows); numpy oracle, {dt:.2f} s; {1.0 / dt:.4f} tok/s",
-        "tok_per_s": round(1.0 / dt, 5),
+    return time.perf_counter() - t0
+
+
+def _cpu_hca_write_seq(args):
+    """Oracle of one sequence's chunked-prefill write: quantize its rows,
+    compress every span the chunk completes, the window ring."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import hca as oh
+    from oracle import indexer as oi
+    from oracle.fp8 import bf16_round, quantize_rows
+
+    chunk, off, D, seed = args
+    rng = np.random.default_rng(seed)
+    lat = bf16_round(rng.standard_normal((chunk, D)).astype(np.float32))
+    kvs = bf16_round(rng.standard_normal((chunk + 128, 2 * D)).astype(np.float32))
+    ape = (rng.standard_normal((128, D)) * 0.5).astype(np.float32)
+    norm_w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    t0 = time.perf_counter()
+    quantize_rows(lat)
+    first, last = off // 128, (off + chunk) // 128
+    for j in range(first, last):
+        r0 = 128 * j - off + 128  # kvs row of position 128 j (state rows before the chunk start at row 0..127)
+        cs = oi.rope_cos_sin(np.array([128 * j]), 64, 1.6e5)[0]
+        y = oh.compress_span(kvs[r0:r0 + 128, :D], kvs[r0:r0 + 128, D:], ape, norm_w, 1e-6, cs)
+        quantize_rows(y[None])
+    return time.perf_counter() - t0
+
+
+def _cpu_hca_decode_row(args):
+    """Oracle of one HCA decode row: 64-head decode over its compressed
+    entries and 128-row window, plus the new row's quantization."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import decode as od
+    from oracle.fp8 import bf16_round, decode_e4m3, quantize_rows
+
+    ctx, seed = args
+    rng = np.random.default_rng(seed)
+    n = ctx // 128 + 128
+    codes = rng.integers(0, 256, (n, 576)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] ^= 1
+    q = bf16_round(rng.standard_normal((1, 64, 576)).astype(np.float32))
+    sinks = rng.standard_normal(64).astype(np.float32)
+    new = bf16_round(rng.standard_normal((1, 576)).astype(np.float32))
+    t0 = time.perf_counter()
+    quantize_rows(new)
+    rows = decode_e4m3(codes).astype(np.float64) * 2.0 ** -8
+    od.sparse_mla_decode(q, lambda s: rows[s], np.arange(n)[None], 256 ** -0.5, 512, sinks)
+    return time.perf_counter() - t0
+
+
+def _pool_run(fn, jobs):
+    import multiprocessing as mp
+
+    workers = min(_cpu_workers(), len(jobs))
+    t0 = time.perf_counter()
+    with mp.get_context("fork").Pool(workers) as pool:
+        busy = pool.map(fn, jobs, chunksize=1)
+    return time.perf_counter() - t0, sum(busy), workers
+
+
+def cpu_baselines(B: int, ctx: int, seed: int) -> dict:
+    """The numpy oracle on the host's cores (a process pool, one job per
+    query row or sequence), each on the full workload of its leg.  Run
+    before the GPU is initialized."""
+    import numpy as np
+
+    out = {}
+    wall, busy, workers = _pool_run(_cpu_dsa_row, [(ctx, seed * 1000 + r) for r in range(B)])
+    by = dsa_bytes(B, ctx)["total"]
+    out["dsa"] = {
+        "value": round(by / wall / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+        "sample": f"the whole headline step on the CPU: {B} query rows at ctx {ctx} (exact scores of "
+                  f"{max(ctx - 128, 0)} keys each, top-2048, 64-head decode over 2176 rows), numpy oracle, one "
+                  f"row per job on {workers} processes: {wall:.2f} s wall, {busy:.1f} core-s",
+        "tok_per_s": round(B / wall, 3), "ms_per_step": round(wall * 1e3, 1),
     }
+    rng = np.random.default_rng(seed + 1)
+    offs = rng.integers(0, 65536, 16)
+    wall, busy, workers = _pool_run(_cpu_hca_write_seq, [(8192, int(o), 576, seed * 1000 + i) for i, o in
+                                                         enumerate(offs)])
+    spans = int(((offs + 8192) // 128 - offs // 128).sum())
+    by = hca_write_bytes(16 * 8192, 576, 16, spans)
+    out["hca_write"] = {
+        "value": round(by["with_kv_score"] / wall / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+        "sample": f"the whole chunked-prefill write on the CPU: 16 sequences x 8192 rows quantized and {spans} spans "
+                  f"compressed, numpy oracle, one sequence per job on {workers} processes: {wall:.2f} s wall, "
+                  f"{busy:.1f} core-s",
+        "ms": round(wall * 1e3, 1),
+    }
+    ctxs = rng.integers(8192, 131072, 64)
+    wall, busy, workers = _pool_run(_cpu_hca_decode_row, [(int(c), seed * 1000 + i) for i, c in enumerate(ctxs)])
+    rows = int((ctxs // 128 + 128).sum())
+    byd = rows * 580 + 64 * (64 * 576 * 2 + 64 * 512 * 2 + 64 * 4)
+    out["hca_decode"] = {
+        "value": round(byd / wall / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
+        "sample": f"the whole 64-row HCA decode step on the CPU ({rows} index entries), numpy oracle, one row per "
+                  f"job on {workers} processes: {wall:.2f} s wall, {busy:.1f} core-s",
+        "tok_per_s": round(64 / wall, 3),
+    }
+    return out
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU (one DP rank's share of the attention "
-                                   "work); --gpus must be 1", "n_gpus": args.gpus}))
-        sys.exit(2)
-    import torch
-    from ernie_kv import ops
-
-    torch.cuda.init()
-    if args.only is not None:
-        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp}[args.only]
-        print(json.dumps(leg(torch, ops, args.seed)), flush=True)
-        return
+# --------------------------------------------------------------------------- main
+def measure_dsa(torch, ops, args, line: dict) -> None:
     st = build_dsa_decode(torch, ops, [args.ctx] * args.batch, args.seed)
     if args.copy_mb > 0:
         src = torch.ones(args.copy_mb << 20, dtype=torch.uint8, device="cuda")
@@ -504,25 +686,19 @@ def main():
     filt_gbs = by["indexer_k"] / (filt_ms * 1e-3) / 1e9
     filt_tflops = args.batch * n * 64 * 128 * 2 / (filt_ms * 1e-3) / 1e12
     # decode contractions: S = Q K^T over the 576-wide rows and O = P V over
-    # their first 512 columns, 64 heads x 2176 rows per query row
-    dec_flops = args.batch * 64 * (min(n, 2048) + min(args.ctx, 128)) * (576 + 512) * 2
-    line = {
-        "metric": METRIC,
+    # their first 512 columns (twice: the hi and lo bf16 parts of P), 64 heads
+    # x 2176 rows per query row
+    dec_flops = args.batch * 64 * (min(n, 2048) + min(args.ctx, 128)) * (576 + 2 * 512) * 2
+    workload = f"dsa_decode_b{args.batch}_ctx{args.ctx}"
+    traffic = traffic_of(workload, "filter_verify_kernel<12>")
+    line.update({
         "value": round(gbs, 2),
         "unit": "GB/s",
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "tok_per_s": round(args.batch / (ms_step * 1e-3), 1),
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp8",
-        "data": "synthetic",
+        "tok_per_s_dsa_layer": round(args.batch / (ms_step * 1e-3), 1),
         "config": {
-            "workload": f"dsa_decode_b{args.batch}_ctx{args.ctx}",
+            "workload": workload,
             "batch": args.batch, "ctx": args.ctx, "index_topk": 2048, "window": 128, "heads": 64,
             "latent_dim": 576, "indexer": "64x128 fp8", "kv_cache": "fp8 e4m3 + fp32 per-token scale",
             "bytes_per_step": by,
@@ -535,9 +711,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(filt_gbs / HBM_PEAK_GBS, 4),
-            "traffic": FILTER_TRAFFIC_BYTES if (args.batch, args.ctx) == (32, 131072) else None,
-            "traffic_vs_algorithmic": round(FILTER_TRAFFIC_BYTES / by["indexer_k"], 4)
-            if (args.batch, args.ctx) == (32, 131072) else None,
+            "traffic": traffic,
+            "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this "
+                              "workload, scaled by a plain copy's readings)" if traffic else None,
+            "traffic_vs_algorithmic": round(traffic / by["indexer_k"], 4) if traffic else None,
             "ms": round(filt_ms, 4),
             "bytes_per_launch": by["indexer_k"],
             "mfma_fp8_tflops": round(filt_tflops, 1),
@@ -552,18 +729,62 @@ def main():
             "mfma_bf16_tflops": round(dec_flops / (dec_ms * 1e-3) / 1e12, 1),
             "mfma_frac": round(dec_flops / (dec_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
-    }
+    })
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU (one DP rank's share of the attention "
+                                   "work); --gpus must be 1", "n_gpus": args.gpus}))
+        sys.exit(2)
+    # CPU baselines first: the process pool forks before the GPU is touched
+    cpu = None
+    if not args.no_cpu_baseline and args.only is None:
+        cpu = cpu_baselines(args.batch, args.ctx, args.seed)
+    import torch
+    from ernie_kv import ops
+
+    torch.cuda.init()
+    if args.only is not None:
+        if args.only == "dsa":
+            line = {}
+            measure_dsa(torch, ops, args, line)
+            print(json.dumps(line), flush=True)
+            return
+        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp}[args.only]
+        print(json.dumps(leg(torch, ops, args.seed)), flush=True)
+        return
+    line = {"metric": METRIC}
+    measure_dsa(torch, ops, args, line)
+    torch.cuda.empty_cache()
+    # the HCA layers' decode step at the headline shape, for the model step
+    hca_head = measure_hca_decode(torch, ops, args.seed, ctxs=[args.ctx] * args.batch,
+                                  label=f"hca_decode_b{args.batch}_ctx{args.ctx}")
+    torch.cuda.empty_cache()
+    model_ms = MODEL_LAYERS["dsa"] * line["ms_per_step"] + MODEL_LAYERS["hca"] * hca_head["ms"]
+    line.update({
+        "tok_per_s": round(args.batch / (model_ms * 1e-3), 1),
+        "model_step": {"ms": round(model_ms, 4),
+                       "composed": "6 x the DSA step (ms_per_step) + 37 x the HCA decode step (hca_layer.ms) at "
+                                   "the same batch and context: the model's attention KV path per decode step",
+                       "hca_layer": hca_head},
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
+    })
     if not args.no_hca:
-        del st
-        torch.cuda.empty_cache()
         line["hca_write"] = measure_hca_write(torch, ops, args.seed)
         torch.cuda.empty_cache()
         line["hca_decode"] = measure_hca_decode(torch, ops, args.seed)
     if not args.no_mtp:
         torch.cuda.empty_cache()
         line["mtp"] = measure_mtp(torch, ops, args.seed)
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.batch, args.ctx, args.seed)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu["dsa"]
+        if "hca_write" in line:
+            line["hca_write"]["cpu_baseline"] = cpu["hca_write"]
+        if "hca_decode" in line:
+            line["hca_decode"]["cpu_baseline"] = cpu["hca_decode"]
     print(json.dumps(line), flush=True)
 
 
