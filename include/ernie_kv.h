@@ -313,6 +313,37 @@ int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                           int64_t lse_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * x * sigmoid(gate) (bf16 roundings of torch's `x * torch.sigmoid(gate)`)
+ * quantized to fp8 e4m3 in 1 x 128 groups with UE8M0 scales: x, gate
+ * [num_rows, hidden] bf16 (hidden a multiple of 512), out [num_rows,
+ * out_stride] fp8, scale int32 at scale[pack * scale_stride + row] holding
+ * the biased exponents (e + 127) of groups 4 pack .. 4 pack + 3 in bytes
+ * 0..3 (DeepGEMM's packed column-major layout; scale_stride >= num_rows).
+ * Replaces sigmoid_mul_quant_fp8 / _sigmoid_mul_quant_kernel
+ * (nvidia/attention.py:288-361).
+ */
+int ekv_sigmoid_mul_quant_fp8(const uint16_t* x, int64_t x_stride, const uint16_t* gate, int64_t gate_stride,
+                              int32_t num_rows, int32_t hidden, uint8_t* out, int64_t out_stride, int32_t* scale,
+                              int64_t scale_stride, void* stream);
+
+/*
+ * VHA head mixing + inverse RoPE + fp8 quant of the HCA attention output:
+ * y = mix @ o[t] (o [T, heads >= 64 padded, 512] bf16 with the given
+ * strides, mix [64, 64] bf16, fp32 accumulation), the interleaved pairs of
+ * channels nope_dim .. 511 rotated back by the row positions[t] of cos_sin
+ * ([P, cs_stride] fp32: cos rope_dim/2 | sin rope_dim/2), then a UE8M0
+ * fp8 quant per (head, 128 channels).  out fp8 [n_groups, T, (64 /
+ * n_groups) * 512]; scale int32 [n_groups, 64 / n_groups, aligned_tokens]
+ * with the biased exponent of channel chunk c in byte c; scale rows
+ * T .. aligned_tokens - 1 are zeroed.  Replaces vha_inv_rope_fp8_quant /
+ * _vha_inv_rope_quant_kernel (nvidia/attention.py:166-285).
+ */
+int ekv_vha_inv_rope_fp8_quant(const uint16_t* o, int64_t o_tok_stride, int64_t o_head_stride, int32_t num_tokens,
+                               int32_t heads, const uint16_t* mix, const int64_t* positions, const float* cos_sin,
+                               int64_t cs_stride, int32_t n_groups, int32_t nope_dim, int32_t rope_dim, uint8_t* out,
+                               int32_t* scale, int32_t aligned_tokens, void* stream);
+
+/*
  * Diagnostic, no counterpart in the reference: the indexer filter's fp8-MFMA
  * dot products out[s][h] = q[h] . k[s] of e4m3fn codes (q [64][128],
  * k [num_keys][128], num_keys a multiple of 16, out [num_keys][64] fp32),

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "ekv_fp8_digit_table": (I32, [P, P]),
     "ekv_indexer_filter_dots": (I32, [P, P, I32, P, P]),
+    "ekv_sigmoid_mul_quant_fp8": (I32, [P, I64, P, I64, I32, I32, P, I64, P, I64, P]),
+    "ekv_vha_inv_rope_fp8_quant": (I32, [P, I64, I64, I32, I32, P, P, P, I64, I32, I32, I32, P, P, I32, P]),
 }
 
 _lib = None

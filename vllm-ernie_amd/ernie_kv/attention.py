@@ -686,6 +686,56 @@ class Ernie5_5HCAAttentionMixin:
                            self.ring, None, None)
 
 
+# --------------------------------------------------------------------------- post-attention quant
+VHA_RANK = 16
+
+
+@dataclass
+class QuantizedActivation:
+    """Stand-in for vLLM's QuantizedActivation: the fields the fp8 o-proj reads."""
+
+    data: torch.Tensor
+    scale: torch.Tensor
+    orig_dtype: Any
+    orig_shape: tuple
+    quant_key: str = "fp8_dynamic_128_sym"
+
+
+class VHAPostMix:
+    """Head mixing ``o[h] <- sum_g m[h, g] o[g]`` with ``m = I + V U^T``
+    (attention.py:120-157, TP = 1): a plain batched product outside this
+    path; ``m`` is what vha_inv_rope_fp8_quant fuses."""
+
+    def __init__(self, num_heads: int, rank: int = VHA_RANK, device=None, dtype=torch.bfloat16) -> None:
+        self.U = torch.zeros(num_heads, rank, dtype=dtype, device=device)
+        self.V = torch.zeros(num_heads, rank, dtype=dtype, device=device)
+        self.m = torch.eye(num_heads, dtype=dtype, device=device)
+
+    def fold(self) -> None:
+        eye = torch.eye(self.U.shape[0], dtype=self.U.dtype, device=self.U.device)
+        self.m.copy_(torch.addmm(eye, self.V, self.U.t()))
+
+    def forward(self, o: torch.Tensor) -> torch.Tensor:
+        return torch.matmul(self.m, o)
+
+    __call__ = forward
+
+
+def vha_inv_rope_fp8_quant(o: torch.Tensor, mix: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor,
+                           n_groups: int, nope_dim: int, rope_dim: int) -> QuantizedActivation:
+    """VHA head mixing + inverse RoPE + fp8 quant in one kernel
+    (attention.py:232-285): data [T, n_groups, hpg * 512] fp8, scale
+    [T, n_groups, hpg] int32 (byte c = biased exponent of channel chunk c)."""
+    data, scale = ops.vha_inv_rope_fp8_quant(o, mix, positions, cos_sin_cache, n_groups, nope_dim, rope_dim)
+    return QuantizedActivation(data=data, scale=scale, orig_dtype=o.dtype, orig_shape=tuple(data.shape))
+
+
+def sigmoid_mul_quant_fp8(x: torch.Tensor, gate: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``x * sigmoid(gate)`` as 1x128 UE8M0 fp8 with DeepGEMM-packed scales
+    (attention.py:340-361)."""
+    return ops.sigmoid_mul_quant_fp8(x, gate)
+
+
 # --------------------------------------------------------------------------- HCA layer class choice
 class Ernie5_5HCAFlashInferAttention:
     """HCA layer on a bf16 KV row (attention.py:542-545).  The write path

@@ -43,6 +43,7 @@ SOURCES = {
     "ekv_hca.hip": EXACT,
     "ekv_indexer.hip": EXACT,
     "ekv_decode.hip": [],
+    "ekv_quant.hip": EXACT,
 }
 
 

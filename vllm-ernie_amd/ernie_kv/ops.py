@@ -553,3 +553,57 @@ def sparse_mla_decode(
         float(scale), out.data_ptr(), _rs(out), out.stride(1), _ptr(lse),
         0 if lse is None else _rs(lse), workspace.data_ptr(), workspace.numel(), _stream(),
     )
+
+
+# --------------------------------------------------------------------------- post-attention quant
+def tma_aligned_rows(n: int) -> int:
+    """Rows of a 4-byte scale buffer padded to 16 bytes (the TMA alignment
+    the reference's packed scale buffers use)."""
+    return (n + 3) // 4 * 4
+
+
+def sigmoid_mul_quant_fp8(x: torch.Tensor, gate: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``x * sigmoid(gate)`` as 1x128 UE8M0 fp8 with packed scales
+    (attention.py:340-361): returns (out fp8 [N, hidden], scale int32
+    [N, hidden / 512] with strides (1, tma_aligned_rows(N)))."""
+    _check_dev(x, gate)
+    _bits16(x)
+    _bits16(gate)
+    N, hidden = x.shape
+    _need(gate.shape == x.shape and hidden % 512 == 0, "gate like x, hidden a multiple of 512")
+    _need(x.stride(-1) == 1 and gate.stride(-1) == 1, "rows must be contiguous")
+    out = torch.empty((N, hidden), dtype=torch.float8_e4m3fn, device=x.device)
+    packs = hidden // 512
+    aligned = tma_aligned_rows(N)
+    scale = torch.empty_strided((N, packs), (1, aligned), dtype=torch.int32, device=x.device)
+    if N:
+        _lib.call("ekv_sigmoid_mul_quant_fp8", x.data_ptr(), _rs(x), gate.data_ptr(), _rs(gate), N, hidden,
+                  out.data_ptr(), hidden, scale.data_ptr(), aligned, _stream())
+    return out, scale
+
+
+def vha_inv_rope_fp8_quant(o: torch.Tensor, mix: torch.Tensor, positions: torch.Tensor,
+                           cos_sin_cache: torch.Tensor, n_groups: int, nope_dim: int,
+                           rope_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """VHA head mixing + inverse RoPE + fp8 quant (attention.py:232-285).
+    Returns (data fp8 [T, n_groups, hpg * 512] -- a transposed view of a
+    [n_groups, T, hpg * 512] buffer -- and scale int32 [T, n_groups, hpg] --
+    a view of [n_groups, hpg, tma_aligned_rows(T)] -- with chunk c's biased
+    exponent in byte c), the layouts of the reference."""
+    _check_dev(o, mix, positions, cos_sin_cache)
+    _bits16(o)
+    _bits16(mix)
+    T, H, D = o.shape
+    _need(H == 64 and D == 512 and o.stride(-1) == 1, "o [T, 64, 512] with unit channel stride")
+    _need(mix.shape == (64, 64) and mix.is_contiguous(), "mix [64, 64] contiguous")
+    _need(positions.dtype == torch.int64 and positions.numel() >= T, "positions int64 [T]")
+    _need(cos_sin_cache.dtype == torch.float32 and cos_sin_cache.stride(-1) == 1, "cos_sin_cache fp32 rows")
+    hpg = H // n_groups
+    out = torch.empty((n_groups, T, hpg * D), dtype=torch.float8_e4m3fn, device=o.device)
+    aligned = tma_aligned_rows(T)
+    scale = torch.empty((n_groups, hpg, aligned), dtype=torch.int32, device=o.device)
+    if aligned:
+        _lib.call("ekv_vha_inv_rope_fp8_quant", o.data_ptr(), o.stride(0), o.stride(1), T, H,
+                  mix.data_ptr(), positions.data_ptr(), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0),
+                  int(n_groups), int(nope_dim), int(rope_dim), out.data_ptr(), scale.data_ptr(), aligned, _stream())
+    return out.transpose(0, 1), scale.permute(2, 0, 1)[:T]
