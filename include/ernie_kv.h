@@ -354,6 +354,25 @@ int ekv_vha_inv_rope_fp8_quant(const uint16_t* o, int64_t o_tok_stride, int64_t 
 int ekv_indexer_filter_dots(const uint8_t* q_codes, const uint8_t* k_codes, int32_t num_keys, float* out,
                             void* stream);
 
+/*
+ * ekv_sparse_mla_decode without a workspace argument: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split partials go to a 64 MiB device array inside the library (one per
+ * GPU, held until the process ends); a call needing more
+ * (ekv_sparse_mla_decode_workspace_size > 64 MiB, e.g. beyond ~150 query
+ * rows of 2176 entries at 64 heads) fails with status 1.  Calls that overlap
+ * on one GPU (different streams) race on that array.  Allocates nothing.
+ */
+int ekv_sparse_mla_decode_noalloc(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                  int32_t num_tokens, int32_t heads, int32_t dim, const uint8_t* cache,
+                                  int32_t cache_bf16, int64_t page_stride /*bytes*/, int64_t num_pages,
+                                  const int32_t* indices, int64_t idx_stride, int32_t width,
+                                  const int32_t* lengths, const int32_t* block_table, int64_t bt_stride,
+                                  const int32_t* req_ids, const float* sinks, float scale, uint16_t* out,
+                                  int64_t out_tok_stride, int64_t out_head_stride, float* lse,
+                                  int64_t lse_stride, void* stream);
+
 /* The 256-entry byte -> packed signed base-64 digit table the scorer uses. */
 int ekv_fp8_digit_table(uint32_t* table, void* stream);
 

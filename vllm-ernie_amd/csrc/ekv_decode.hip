@@ -31,6 +31,8 @@
 #include "ekv_common.h"
 #include "ekv_internal.h"
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace ekv {
@@ -761,4 +763,57 @@ extern "C" int ekv_sparse_mla_decode(const uint16_t* q, int64_t q_tok_stride, in
   hipLaunchKernelGGL(decode_combine_kernel, dim3(heads / 4, num_tokens), dim3(256), 0, s, ws_o, ws_ml, ws_rows,
                      heads, sinks, out, out_tok_stride, out_head_stride, lse, lse_stride);
   return ekv_launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the split partials live in `scratch`, a
+// file-scope device array (one per GPU the library runs on, held until the
+// process ends).  Its device address is looked up once per device, with that
+// device current, on the first call there; host code passes that address to
+// the kernels, never the array's name.  Calls on one GPU share the array, so
+// calls that overlap on one GPU (different streams) race; the decode writes
+// every partial it reads within the call, so nothing needs clearing.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = int64_t{64} << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+static void* scratch_address(int device) {
+  void* p = g_scratch_ptr[device].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  p = g_scratch_ptr[device].load(std::memory_order_relaxed);
+  if (p == nullptr) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[device].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+extern "C" int ekv_sparse_mla_decode_noalloc(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                             int32_t num_tokens, int32_t heads, int32_t dim, const uint8_t* cache,
+                                             int32_t cache_bf16, int64_t page_stride, int64_t num_pages,
+                                             const int32_t* indices, int64_t idx_stride, int32_t width,
+                                             const int32_t* lengths, const int32_t* block_table, int64_t bt_stride,
+                                             const int32_t* req_ids, const float* sinks, float scale, uint16_t* out,
+                                             int64_t out_tok_stride, int64_t out_head_stride, float* lse,
+                                             int64_t lse_stride, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && width >= 0, "sizes must be >= 0");
+  if (num_tokens == 0) return 0;
+  const int64_t need = ekv_sparse_mla_decode_workspace_size(num_tokens, heads, width);
+  if (need > kNoAllocScratchBytes) {
+    set_error("ekv_sparse_mla_decode_noalloc: the call needs more scratch than the 64 MiB the library holds "
+              "(see ekv_sparse_mla_decode_workspace_size); use ekv_sparse_mla_decode with a workspace");
+    return kInvalidArgument;
+  }
+  int device = 0;
+  EKV_CHECK(hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices, "no current device");
+  void* ws = scratch_address(device);
+  EKV_CHECK(ws != nullptr, "hipGetSymbolAddress of the decode scratch failed");
+  return ekv_sparse_mla_decode(q, q_tok_stride, q_head_stride, num_tokens, heads, dim, cache, cache_bf16, page_stride,
+                               num_pages, indices, idx_stride, width, lengths, block_table, bt_stride, req_ids, sinks,
+                               scale, out, out_tok_stride, out_head_stride, lse, lse_stride, ws, kNoAllocScratchBytes,
+                               stream);
 }

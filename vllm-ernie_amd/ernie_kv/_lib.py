@@ -55,6 +55,10 @@ SIGNATURES: dict[str, tuple] = {
         [P, I64, I64, I32, I32, I32, P, I32, I64, I64, P, I64, I32, P, P, I64, P, P, F32, P, I64, I64, P, I64, P, I64, P],
     ),
     "ekv_fp8_digit_table": (I32, [P, P]),
+    "ekv_sparse_mla_decode_noalloc": (
+        I32,
+        [P, I64, I64, I32, I32, I32, P, I32, I64, I64, P, I64, I32, P, P, I64, P, P, F32, P, I64, I64, P, I64, P],
+    ),
     "ekv_indexer_filter_dots": (I32, [P, P, I32, P, P]),
     "ekv_sigmoid_mul_quant_fp8": (I32, [P, I64, P, I64, I32, I32, P, I64, P, I64, P]),
     "ekv_vha_inv_rope_fp8_quant": (I32, [P, I64, I64, I32, I32, P, P, P, I64, I32, I32, I32, P, P, I32, P]),
