@@ -376,6 +376,110 @@ int ekv_sparse_mla_decode_noalloc(const uint16_t* q, int64_t q_tok_stride, int64
 /* The 256-entry byte -> packed signed base-64 digit table the scorer uses. */
 int ekv_fp8_digit_table(uint32_t* table, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * MXFP4 indexer (use_fp4_kv).  Key rows are 68 bytes: 64 bytes of packed
+ * e2m1 values (even element in the low nibble) and 4 E8M0 scale bytes, one
+ * per 32 values; a 64-token page holds all values first (row r at 64 r), then
+ * all scale bytes (row r at 64 * 64 + 4 r).  Quantization per 32-value group:
+ * scale = 2^ceil(log2(amax / 6)), values to the nearest e2m1 with ties to the
+ * larger magnitude.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * MXFP4 quantization of rows r = tok * heads + h of x (bf16 at
+ * x + tok * x_tok_stride + h * x_head_stride, dim values, dim % 32 == 0):
+ * dim / 2 packed bytes at values + r * values_stride, dim / 32 scale bytes at
+ * scales + r * scales_stride.  Replaces downcast_to_mxfp(x, axis=-1) as
+ * _quantize_fp4 calls it (nvidia/attention.py:990-1008).
+ */
+int ekv_mxfp4_quant(const uint16_t* x, int64_t x_tok_stride, int64_t x_head_stride, int32_t num_tokens,
+                    int32_t heads, int32_t dim, uint8_t* values, int64_t values_stride, uint8_t* scales,
+                    int64_t scales_stride, void* stream);
+
+/*
+ * Indexer q for the MXFP4 path: q [T, heads, 128] bf16 -> q_values
+ * [T, heads, 64] and q_scales [T, heads] (the four scale bytes of a head as
+ * one int32), and w_out [T, heads] = fl32(weights * fl32(128^-0.5 * 64^-0.5))
+ * (no q scale is folded on this path).  Replaces the q half of
+ * _quantize_fp4 and the weight scaling (nvidia/attention.py:969-974,
+ * 990-995, 1022-1025).
+ */
+int ekv_indexer_q_quant_fp4(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                            const void* weights, int32_t weights_is_bf16, int64_t w_stride, int32_t num_tokens,
+                            int32_t heads, uint8_t* q_values, int32_t* q_scales, float* w_out, void* stream);
+
+/*
+ * MXFP4 indexer K insert: k [num_tokens, k_stride] bf16 (128 wide) quantized
+ * and written to the page row of slot_mapping[t] (negative slots skipped).
+ * Replaces the k half of _quantize_fp4: downcast_to_mxfp then
+ * _store_indexer_fp4 (nvidia/attention.py:999-1021, 831-860).
+ */
+int ekv_indexer_k_insert_fp4(const uint16_t* k, int64_t k_stride, int32_t num_tokens,
+                             const int64_t* slot_mapping, uint8_t* kcache, int64_t page_stride /*bytes*/,
+                             int64_t num_pages, void* stream);
+
+/*
+ * Store of already quantized MXFP4 rows (64 value bytes at
+ * values + t * values_stride, 4 scale bytes at scales + t * scales_stride)
+ * into the page row of slot_mapping[t]; negative slots skipped.  Replaces
+ * _store_indexer_fp4 (nvidia/attention.py:831-860).
+ */
+int ekv_indexer_store_fp4(const uint8_t* values, int64_t values_stride, const uint8_t* scales,
+                          int64_t scales_stride, int32_t num_tokens, const int64_t* slot_mapping,
+                          uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages, void* stream);
+
+/*
+ * Exact MXFP4 indexer scores, as ekv_indexer_score for 68-byte key rows: per
+ * head, block sums D_b of the integers 2 * e2m1 (exact), T_b =
+ * fl32(D_b * 2^(sq_b + sk_b - 256)), dot = ((T_0 + T_1) + T_2) + T_3 in fp32,
+ * score = sum_h fl32(w_h * relu(dot)) in the fixed head order, + 0.
+ * Replaces the FP4 paged MQA logits of SparseAttnIndexer(use_fp4_cache=True)
+ * (nvidia/attention.py:942-953, 982-984).
+ */
+int ekv_indexer_score_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                          const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                          const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                          const int32_t* lengths, int32_t num_tokens, int32_t max_len, float* scores,
+                          int64_t scores_stride, void* stream);
+
+/*
+ * MXFP4 counterparts of ekv_indexer_filter / _select / _topk (same workspace,
+ * ekv_indexer_topk_workspace_size): the filter runs the scaled fp4 MFMA over
+ * every token with an error bound, the candidates are scored exactly as
+ * ekv_indexer_score_fp4, and the select writes the exact top-k (lowest index
+ * first on ties), optionally merged as ekv_indexer_select describes.
+ * Replaces SparseAttnIndexer with use_fp4_cache=True (nvidia/attention.py:
+ * 942-953, 982-984).
+ */
+int ekv_indexer_filter_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                           const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                           const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                           const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t k,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+int ekv_indexer_select_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                           const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                           const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                           const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                           int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                           int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
+                           const int64_t* positions, int32_t window, int32_t merged_slots, void* stream);
+int ekv_indexer_topk_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                         const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                         const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                         const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                         int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Diagnostic, no counterpart in the reference: the MXFP4 filter's MFMA dot
+ * products out[s][h] = q[h] . k[s] of dequantized e2m1 rows (q_values
+ * [64][64], q_scales [64] words, k_values [num_keys][64], k_scales [num_keys]
+ * words, num_keys a multiple of 16), by the same MFMA call and operand layout
+ * as ekv_indexer_filter_fp4, to check the error bound its candidate test
+ * assumes on the device at hand.
+ */
+int ekv_indexer_filter_dots_fp4(const uint8_t* q_values, const int32_t* q_scales, const uint8_t* k_values,
+                                const int32_t* k_scales, int32_t num_keys, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

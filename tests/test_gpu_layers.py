@@ -17,6 +17,7 @@ from helpers import bf16_tensor, bf16_values, permuted_block_table, randn_bf16, 
 from oracle import decode as od
 from oracle import hca as oh
 from oracle import indexer as oi
+from oracle import mxfp4 as om
 from oracle import paged
 from oracle.fp8 import quantize_rows
 from oracle.merge import logical_to_global, merge_swa_topk
@@ -39,9 +40,11 @@ def _check_decode(got, ref_o, what):
     assert not bad.any(), f"{what}: max err {err.max()} at {np.argwhere(bad)[0]}"
 
 
-def _dsa_setup(dev, rng, ctxs, rows_per_req):
+def _dsa_setup(dev, rng, ctxs, rows_per_req, fp4=False):
     """Caches pre-filled up to each request's context, plus the step's query
-    rows (the last rows_per_req positions of each request)."""
+    rows (the last rows_per_req positions of each request).  With fp4 the
+    indexer K cache holds MXFP4 rows in 9216-byte pages (the packed-block
+    stride)."""
     from ernie_kv import attention as A
 
     cfg = A.ernie5_5_config(hidden_size=256, hybrid_mla_q_lora_rank=128)
@@ -49,12 +52,12 @@ def _dsa_setup(dev, rng, ctxs, rows_per_req):
     P = max((c + 63) // 64 for c in ctxs)
     bt = permuted_block_table(rng, B, P)
     pages = B * P
-    kc = oi.kcache_pages(pages)
+    kc = np.zeros((pages, 9216), np.uint8) if fp4 else oi.kcache_pages(pages)
     lat = np.zeros((pages, paged.fp8_page_bytes(576)), np.uint8)
     for b, c in enumerate(ctxs):
         s = np.arange(c - rows_per_req[b])  # the step writes the last rows itself
         slots = bt[b, s // 64].astype(np.int64) * 64 + s % 64
-        oi.k_insert(kc, randn_bf16(rng, (len(s), 128)), slots)
+        (om.k_insert if fp4 else oi.k_insert)(kc, randn_bf16(rng, (len(s), 128)), slots)
         codes, scale = quantize_rows(randn_bf16(rng, (len(s), 576)))
         paged.write_fp8_rows(lat, slots, codes, scale, 576)
     req = np.concatenate([np.full(r, b, np.int32) for b, r in enumerate(rows_per_req)])
@@ -87,27 +90,36 @@ def _oracle_indexer(case, layer, dev):
     pos = case.positions
     rq, rk = oi.indexer_prep(bf16_values(iq), bf16_values(ik), layer.k_norm_weight.cpu().numpy(),
                              layer.k_norm_bias.cpu().numpy(), 1e-6, table[to_dev(pos, dev)].cpu().numpy())
-    codes, wf = oi.quantize_q(rq, bf16_values(iw))
     kc = case.kc.copy()
-    oi.k_insert(kc, rk, case.slot_mapping)
     lens = oi.windowed_lengths(pos, WINDOW)
-    top, _ = oi.indexer_topk(codes, wf, kc, case.bt, case.req, lens, TOPK)
+    if layer.use_fp4_kv:
+        qv, qs, wf = om.quantize_q(rq, bf16_values(iw))
+        om.k_insert(kc, rk, case.slot_mapping)
+        top, _ = om.indexer_topk(qv, qs, wf, kc, case.bt, case.req, lens, TOPK)
+    else:
+        codes, wf = oi.quantize_q(rq, bf16_values(iw))
+        oi.k_insert(kc, rk, case.slot_mapping)
+        top, _ = oi.indexer_topk(codes, wf, kc, case.bt, case.req, lens, TOPK)
     return kc, top
 
 
-def test_indexer_forward_vs_oracle(dev):
+@pytest.mark.parametrize("fp4", [False, True], ids=["fp8", "mxfp4"])
+def test_indexer_forward_vs_oracle(dev, fp4):
     """Ernie5_5Indexer.forward (attention.py:955-984): projections, prep,
-    quant, K insert and the exact top-k into indexer_op.topk_indices_buffer."""
+    quant, K insert and the exact top-k into indexer_op.topk_indices_buffer;
+    fp8 (132-byte) or MXFP4 (68-byte, _quantize_fp4 :986-1025) K rows."""
     from ernie_kv import attention as A
 
     rng = np.random.default_rng(61)
-    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3], fp4=fp4)
     topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
     p = case.params
     ix = A.Ernie5_5Indexer(case.cfg, topk_buf, swa_buf, prefix="model.layers.3.attn.indexer",
                            wq_b=p["indexer.wq_b"], wk_weights_proj=p["indexer.wk_weights_proj"],
-                           k_norm_weight=p["indexer.k_norm.weight"], k_norm_bias=p["indexer.k_norm.bias"])
+                           k_norm_weight=p["indexer.k_norm.weight"], k_norm_bias=p["indexer.k_norm.bias"],
+                           use_fp4_kv=fp4)
+    assert ix.k_cache.head_dim == (68 if fp4 else 132)
     ix.k_cache.kv_cache = to_dev(case.kc, dev)
     with A.set_forward_context({ix.k_cache.prefix: case.md}):
         got = ix.forward(bf16_tensor(case.inputs["hidden"], dev), bf16_tensor(case.inputs["q_c"], dev),
@@ -119,18 +131,20 @@ def test_indexer_forward_vs_oracle(dev):
     assert (swa_buf == -7).all(), "forward alone must not touch the merged (swa) buffer"
 
 
-def test_dsa_indexer_and_attn_vs_oracle(dev):
+@pytest.mark.parametrize("fp4", [False, True], ids=["fp8", "mxfp4"])
+def test_dsa_indexer_and_attn_vs_oracle(dev, fp4):
     """Ernie5_5DSAAttention._indexer_and_attn (attention.py:1205-1226): top-k,
     merged rows, both caches' bytes, the sparse decode's latent output and
-    the up-projected out."""
+    the up-projected out (fp8 or MXFP4 indexer K cache)."""
     from ernie_kv import attention as A
 
     rng = np.random.default_rng(62)
-    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3], fp4=fp4)
     T = case.T
     topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
-    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params)
+    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params,
+                                   use_fp4_kv=fp4)
     layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
     layer.mla_attn.kv_cache = to_dev(case.lat, dev)
     captured = {}

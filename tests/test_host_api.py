@@ -123,3 +123,32 @@ def test_attn_tp_and_sink_backend_errors():
         _check_attn_tp(cfg, 3)
     with pytest.raises(RuntimeError, match="sink-capable"):
         _check_sink_backend(384, "fp8")
+
+
+def _indexer(use_fp4_kv, pcp=1, dcp=1):
+    import torch
+
+    from ernie_kv import attention as A
+
+    cfg = A.ernie5_5_config(hidden_size=256, hybrid_mla_q_lora_rank=128)
+    return A.Ernie5_5Indexer(cfg, None, None, prefix="model.layers.0.self_attn.indexer",
+                             wq_b=torch.zeros(64 * 128, 128), wk_weights_proj=torch.zeros(192, 256),
+                             k_norm_weight=torch.ones(128), k_norm_bias=torch.zeros(128), use_fp4_kv=use_fp4_kv,
+                             prefill_context_parallel_size=pcp, decode_context_parallel_size=dcp)
+
+
+@pytest.mark.parametrize("pcp,dcp", [(2, 1), (1, 2), (2, 2)])
+def test_mxfp4_requires_single_context_parallel(pcp, dcp):
+    """test_indexer_fp4.py:59-70 (attention.py:881-892): the MXFP4 indexer
+    refuses context parallelism with the reference's message."""
+    with pytest.raises(NotImplementedError, match="PCP=DCP=1") as error:
+        _indexer(True, pcp, dcp)
+    assert f"PCP={pcp}, DCP={dcp}" in str(error.value)
+    _indexer(False, pcp, dcp)  # the fp8 cache has no such limit
+
+
+def test_indexer_k_cache_row_bytes():
+    """68-byte MXFP4 rows (64 packed values + 4 UE8M0) vs 132-byte fp8 rows
+    (attention.py:929-935)."""
+    assert _indexer(True).k_cache.head_dim == 68
+    assert _indexer(False).k_cache.head_dim == 132

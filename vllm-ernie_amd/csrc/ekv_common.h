@@ -98,6 +98,58 @@ __device__ __forceinline__ uint32_t fp8_digit_pack(uint32_t code) {
   return d0 | (d1 << 8) | (d2 << 16);
 }
 
+// ---------------------------------------------------------------------------
+// MXFP4 (OCP MX e2m1 values, one E8M0 scale byte per 32 values).
+// ---------------------------------------------------------------------------
+constexpr int kMxBlock = 32;
+
+// E8M0 byte of a 32-value group with max |x| = amax: the exponent field of
+// fl32(amax / 6) rounded up to a power of two (0 when the quotient is 0).
+__device__ __forceinline__ uint32_t mxfp4_scale_byte(float amax) {
+  const uint32_t bits = __float_as_uint(__fdiv_rn(amax, 6.0f));
+  return ((bits + 0x7fffffu) & 0x7f800000u) >> 23;
+}
+
+// e2m1 code of y (|y| <= 6 after scaling): nearest, a tie going to the larger
+// magnitude (one is added below the two kept bits, then they are shifted
+// out), saturating at 6, sign kept (a small negative y gives code 8, -0).
+__device__ __forceinline__ uint32_t e2m1_code(float y) {
+  const uint32_t u = __float_as_uint(y);
+  const uint32_t sign = u >> 31, e = (u >> 23) & 0xffu, m = u & 0x7fffffu;
+  uint32_t m2 = m;
+  if (e < 127u) {
+    const uint32_t adj = 126u - e;  // aligns a value below 1 to the e2m1 subnormal
+    m2 = adj < 32u ? (0x400000u | (m >> 1)) >> adj : 0u;
+  }
+  const uint32_t e2 = (e > 126u ? e : 126u) - 126u;
+  const uint32_t c = min((((e2 << 2) | (m2 >> 21)) + 1u) >> 1, 7u);
+  return (sign << 3) | c;
+}
+
+// 2**(byte - 127), the value of an E8M0 byte (byte 0 is 2**-127).
+__device__ __forceinline__ float e8m0_value(uint32_t byte) {
+  return byte ? __uint_as_float(byte << 23) : 0x1p-127f;
+}
+
+// Four e2m1 codes (one per byte, low nibble) -> the int8 values 2 * e2m1
+// (0, +-1, 2, 3, 4, 6, 8, 12), byte for byte.
+__device__ __forceinline__ uint32_t e2m1x4_to_i8(uint32_t n) {
+  const uint32_t m = n & 0x07070707u;
+  const uint32_t pos = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, m);
+  const uint32_t neg = __builtin_amdgcn_perm(0xf4f8fafcu, 0xfdfeff00u, m);
+  const uint32_t s = ((n >> 3) & 0x01010101u) * 0xffu;
+  return (pos & ~s) | (neg & s);
+}
+
+// Four packed e2m1 bytes (eight values) -> eight int8 2 * e2m1 values: the
+// low nibbles (even elements) in the low word, the high nibbles in the high
+// word.  Dot products over all eight are unchanged by this element order as
+// long as both operands use it.
+__device__ __forceinline__ int64_t fp4x8_to_i8(uint32_t w) {
+  const uint32_t lo = e2m1x4_to_i8(w & 0x0f0f0f0fu), hi = e2m1x4_to_i8((w >> 4) & 0x0f0f0f0fu);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max_xor(T v, int width) {
   for (int m = width >> 1; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, width));

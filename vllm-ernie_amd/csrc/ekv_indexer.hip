@@ -166,6 +166,112 @@ __device__ __forceinline__ float exact_block(const ExactOperands& op, const uint
 }
 
 // ---------------------------------------------------------------------------
+// MXFP4 keys (the use_fp4_kv indexer): 64 packed e2m1 bytes per token, then
+// the four E8M0 scale bytes of every token of the page.  Exact scores, with
+// I = 2 * e2m1 value (|I| <= 12) and sq, sk the scale bytes of block b (32
+// dims):
+//   D_b = sum_{d in b} Iq[h, d] * Ik[s, d]     (v_mfma_i32_16x16x32_i8, exact)
+//   T_b = fl32(D_b * 2^(sq_b + sk_b - 256))    (exact in double, one rounding)
+//   dot = ((T_0 + T_1) + T_2) + T_3            (fp32)
+// then p_h = fl32(w_h * max(dot, 0)), the fp8 path's head-sum order and
+// score = acc + 0 (no per-token factor).
+// The filter runs all four blocks in one v_mfma_scale_f32_16x16x128_f8f6f4
+// with both operands e2m1 and their E8M0 scales.  Each block sum is exact
+// there (at most 32 * 36 in quarter units); adding the four scaled sums is
+// aligned to the scales, so its error is bounded by M = sum_b 1152 *
+// 2^(sq_b + sk_b - 254), the largest magnitude the scales allow, not by the
+// actual block sums (a large-scale block that sums to zero still costs
+// precision).  The error term
+//   e_s = 1152 * 2^-16 * sum_b 2^(sk_b - 127) * sum_h |w_h| 2^(sq_hb - 127)
+//       = 2^-16 * sum_h |w_h| M_h
+// covers the MFMA (measured at most 2^-25.2 M on the device), the
+// contract's three additions and the two head sums (2 * 18 * 2^-24 of
+// sum_h |w_h| |dot_h| <= 2^-18.8 sum_h |w_h| M_h).
+// Layouts: i8 16x16x32: lane l: row/col l%16, K bytes [8(l/16), +8) -- lane
+// group g takes elements [8g, +8) of block b, the packed bytes
+// [16b + 4g, +4) of a row; fp4 16x16x128: lane l: row/col l%16, K values
+// [32(l/16), +32), the packed bytes [16g, +16) (block g), with block g's scale
+// byte in the lane's scale operand.
+// ---------------------------------------------------------------------------
+constexpr int kFp4Row = 64;                           // packed bytes per key row
+constexpr int kFp4PageBytes = kPageTokens * kFp4Row;  // scales follow the values
+constexpr float kFp4BoundFactor = 1152.0f * 0x1p-16f;
+
+struct Fp4Key {
+  int64_t kq[4];  // block b: eight int8 values (elements 32b + 8g ...) of the lane's token
+  uint32_t ks;    // the token's four scale bytes
+};
+
+// This lane's part of key row r of the page at `base` (zeros unless ok; the
+// loads themselves are unconditional).
+__device__ __forceinline__ void load_key_fp4(const uint8_t* base, int r, int g, bool ok, Fp4Key& key) {
+  const uint8_t* row = base + r * kFp4Row + 4 * g;
+  uint32_t w[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) w[b] = *reinterpret_cast<const uint32_t*>(row + 16 * b);
+  const uint32_t s = *reinterpret_cast<const uint32_t*>(base + kFp4PageBytes + r * 4);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) key.kq[b] = ok ? fp4x8_to_i8(w[b]) : int64_t{0};
+  key.ks = ok ? s : 0u;
+}
+
+// q operand of head row (16 hb + col) for block b, as load_key_fp4 lays keys out.
+__device__ __forceinline__ int64_t load_q_fp4(const uint8_t* q_values, int64_t t, int hb, int b, int g, int col) {
+  const uint8_t* row = q_values + (t * kIdxHeads + 16 * hb + col) * kFp4Row;
+  return fp4x8_to_i8(*reinterpret_cast<const uint32_t*>(row + 16 * b + 4 * g));
+}
+
+// Exact fp4 scores of the 16 tokens of a block (token = lane % 16); every lane
+// of the column returns the same value.  qop(hb, b) yields this lane's q
+// operand, qsc(h) the four scale bytes of head h.
+template <bool kStaged = false, class QOp, class QSc>
+__device__ __forceinline__ float exact_block_fp4(QOp qop, QSc qsc, const float (&wv)[4][4], const Fp4Key& key) {
+  const int g = (threadIdx.x & 63) >> 4;
+  float acc = 0.0f;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    if (kStaged) __builtin_amdgcn_sched_barrier(0);
+    i32x4 c[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      c[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(qop(hb, b), key.kq[b], i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t qs = qsc(16 * hb + 4 * g + i);
+      float tb[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int e = static_cast<int>(((qs >> (8 * b)) & 0xffu) + ((key.ks >> (8 * b)) & 0xffu)) - 256;
+        tb[b] = static_cast<float>(__builtin_ldexp(static_cast<double>(c[b][i]), e));
+      }
+      const float dot = ((tb[0] + tb[1]) + tb[2]) + tb[3];
+      acc = acc + wv[hb][i] * fmaxf(dot, 0.0f);
+    }
+  }
+  const float a01 = acc + __shfl_xor(acc, 16);
+  const float tot = a01 + __shfl_xor(a01, 32);
+  return tot + 0.0f;
+}
+
+// Exact-path operands of query row t in registers (fp4 keys).
+struct Fp4Operands {
+  int64_t q[4][4];  // [hb][block]
+  float wv[4][4];
+};
+
+__device__ __forceinline__ void load_fp4_operands(Fp4Operands& op, const uint8_t* q_values, const float* w, int64_t t,
+                                                  int g, int col) {
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) op.q[hb][b] = load_q_fp4(q_values, t, hb, b, g, col);
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) op.wv[hb][i] = w[t * kIdxHeads + 16 * hb + 4 * g + i];
+}
+
+// ---------------------------------------------------------------------------
 // Exact scores of every token s < lengths[t] (ekv_indexer_score).
 // ---------------------------------------------------------------------------
 struct ScoreArgs {
@@ -181,16 +287,23 @@ struct ScoreArgs {
   float* scores;             // [T, scores_stride]
   int64_t scores_stride;
   int32_t max_len;
+  const uint8_t* q_fp4;      // fp4 keys: q values [T, 64, 64] (q_digits unused)
+  const int32_t* q_scales;   // fp4 keys: [T, 64], four E8M0 bytes per head
 };
 
 constexpr int kScoreIters = 8;                        // 16-token blocks per wave
 constexpr int kScoreChunk = 4 * 16 * kScoreIters;     // tokens per workgroup
 
+template <bool kFp4>
 __global__ void __launch_bounds__(256) score_exact_kernel(ScoreArgs a) {
-  __shared__ uint32_t s_table[256];
+  __shared__ uint32_t s_table[256];  // fp8: digit table; fp4: q scale words
   const int tid = threadIdx.x;
-  s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
   const int t = blockIdx.y;
+  if constexpr (kFp4) {
+    if (tid < kIdxHeads) s_table[tid] = static_cast<uint32_t>(a.q_scales[static_cast<int64_t>(t) * kIdxHeads + tid]);
+  } else {
+    s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  }
   const int n = min(a.lengths[t], a.max_len);
   __syncthreads();
   const int64_t chunk0 = static_cast<int64_t>(blockIdx.x) * kScoreChunk;
@@ -198,15 +311,31 @@ __global__ void __launch_bounds__(256) score_exact_kernel(ScoreArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, col = lane & 15;
   const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
-  ExactOperands op;
-  load_exact_operands(op, a.q_digits, a.w, t, g, col);
-  for (int it = 0; it < kScoreIters; ++it) {
-    const int64_t s = chunk0 + (static_cast<int64_t>(wave) * kScoreIters + it) * 16 + col;
-    uint4 kb[2];
-    float ks;
-    load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, s < n ? s : -1, g, kb, ks);
-    const float sc = exact_block(op, s_table, kb, ks);
-    if (s < n && g == 0) a.scores[static_cast<int64_t>(t) * a.scores_stride + s] = sc;
+  if constexpr (kFp4) {
+    Fp4Operands op;
+    load_fp4_operands(op, a.q_fp4, a.w, t, g, col);
+    for (int it = 0; it < kScoreIters; ++it) {
+      const int64_t s = chunk0 + (static_cast<int64_t>(wave) * kScoreIters + it) * 16 + col;
+      int64_t page = -1;
+      if (s < n && (s >> 6) < a.bt_stride) page = bt[s >> 6];
+      const bool ok = page >= 0 && page < a.num_pages;
+      Fp4Key key;
+      load_key_fp4(a.kcache + (ok ? page : 0) * a.page_stride, static_cast<int>(s & 63), g, ok, key);
+      const float sc = exact_block_fp4([&](int hb, int b) { return op.q[hb][b]; },
+                                       [&](int h) { return s_table[h]; }, op.wv, key);
+      if (s < n && g == 0) a.scores[static_cast<int64_t>(t) * a.scores_stride + s] = sc;
+    }
+  } else {
+    ExactOperands op;
+    load_exact_operands(op, a.q_digits, a.w, t, g, col);
+    for (int it = 0; it < kScoreIters; ++it) {
+      const int64_t s = chunk0 + (static_cast<int64_t>(wave) * kScoreIters + it) * 16 + col;
+      uint4 kb[2];
+      float ks;
+      load_key_i8(a.kcache, a.page_stride, a.num_pages, bt, a.bt_stride, s < n ? s : -1, g, kb, ks);
+      const float sc = exact_block(op, s_table, kb, ks);
+      if (s < n && g == 0) a.scores[static_cast<int64_t>(t) * a.scores_stride + s] = sc;
+    }
   }
 }
 
@@ -230,6 +359,7 @@ struct FilterArgs {
   uint32_t* hist;            // [T, kHistBins] counts of L_s key prefixes
   int32_t rows;              // T (filter_kernel: 1-D grid of groups x T workgroups)
   int32_t groups;            // workgroup slots per row, a multiple of 8
+  const int32_t* q_scales;   // fp4 keys: [T, 64] E8M0 bytes (q_fp8 is then q values [T, 64, 64])
 };
 
 
@@ -239,6 +369,34 @@ struct FilterArgs {
 // what the filter's bound e_s covers (ekv_indexer_filter_dots exposes it).
 __device__ __forceinline__ f32x4 filter_mfma(const i32x8& q, const i32x8& k) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q, k, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+}
+
+// The fp4 filter's dot products: both operands e2m1 (the first four words of
+// each operand) with this lane's block scale byte in bits 0..7 of qs / ks.
+__device__ __forceinline__ f32x4 filter_mfma_fp4(const i32x8& q, uint32_t qs, const i32x8& k, uint32_t ks) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q, k, f32x4{0.f, 0.f, 0.f, 0.f}, 4, 4, 0,
+                                                          static_cast<int>(qs), 0, static_cast<int>(ks));
+}
+
+// out[s][h] = the fp4 filter's MFMA dot product of q row h (q values [64, 64],
+// q scales [64] words) and key row s (k values [N, 64], k scales [N] words).
+__global__ void __launch_bounds__(64) filter_dots_fp4_kernel(const uint8_t* q, const int32_t* qs, const uint8_t* k,
+                                                             const int32_t* ks, float* out) {
+  const int lane = threadIdx.x, g = lane >> 4, col = lane & 15;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * 16;
+  auto load4 = [](const uint8_t* p) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    return i32x8{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w), 0, 0, 0, 0};
+  };
+  const i32x8 kv = load4(k + (s0 + col) * kFp4Row + 16 * g);
+  const uint32_t kb = (static_cast<uint32_t>(ks[s0 + col]) >> (8 * g)) & 0xffu;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    const uint32_t qb = (static_cast<uint32_t>(qs[16 * hb + col]) >> (8 * g)) & 0xffu;
+    const f32x4 cc = filter_mfma_fp4(load4(q + (16 * hb + col) * kFp4Row + 16 * g), qb, kv, kb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[(s0 + col) * kIdxHeads + 16 * hb + 4 * g + i] = cc[i];
+  }
 }
 
 // out[s][h] = the filter's MFMA dot product of q row h and key row s (one
@@ -319,30 +477,58 @@ __host__ __device__ inline int filter_per_wave(int n, int groups) {
   return (npages + 4 * groups - 1) / (4 * groups);
 }
 
-// Filter operands of row t for this lane: the fp8 q rows in f8f6f4 A layout,
-// the 16 head weights wv[hb][i] = w[16hb + 4g + i] and the error bound
-// factor 448^2 (2^-8 + 2^-9) sum_h |w_h| (scaled by a token's kscale).
-__device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t, int g, int col, i32x8 (&qa)[4],
-                                                     float (&wv)[4][4], float& ebound) {
+// Filter operands of row t for this lane: the q rows in f8f6f4 A layout (fp8:
+// 32 codes; fp4: 16 packed bytes of block g, and qsc[hb] = that block's scale
+// byte of head 16hb + col), the 16 head weights wv[hb][i] = w[16hb + 4g + i]
+// and the error-bound factors: fp8 eb[0] = 448^2 (2^-8 + 2^-9) sum_h |w_h|
+// (times a token's kscale); fp4 eb[b] = 1152 * 2^-16 * sum_h |w_h|
+// 2^(sq_hb - 127) (times 2^(sk_b - 127), summed over b).
+struct FilterOps {
+  i32x8 qa[4];
+  uint32_t qsc[4];
+  float wv[4][4];
+  float eb[4];
+};
+
+template <bool kFp4>
+__device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t, int g, int col, FilterOps& op) {
+  const int64_t th = static_cast<int64_t>(t) * kIdxHeads;
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) {
-    const uint4* src = reinterpret_cast<const uint4*>(a.q_fp8 + (static_cast<int64_t>(t) * kIdxHeads + 16 * hb + col) * kIdxDim +
-                                                      32 * g);
-    const uint4 v0 = src[0], v1 = src[1];
-    qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
-                   static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
+    if constexpr (kFp4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(a.q_fp8 + (th + 16 * hb + col) * kFp4Row + 16 * g);
+      op.qa[hb] = i32x8{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w),
+                        0, 0, 0, 0};
+      op.qsc[hb] = (static_cast<uint32_t>(a.q_scales[th + 16 * hb + col]) >> (8 * g)) & 0xffu;
+    } else {
+      const uint4* src = reinterpret_cast<const uint4*>(a.q_fp8 + (th + 16 * hb + col) * kIdxDim + 32 * g);
+      const uint4 v0 = src[0], v1 = src[1];
+      op.qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
+                        static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
+      op.qsc[hb] = 0u;
+    }
   }
-  float wabs = 0.0f;
+  float wabs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      wv[hb][i] = a.w[static_cast<int64_t>(t) * kIdxHeads + 16 * hb + 4 * g + i];
-      wabs += fabsf(wv[hb][i]);
+      const float wi = a.w[th + 16 * hb + 4 * g + i];
+      op.wv[hb][i] = wi;
+      if constexpr (kFp4) {
+        const uint32_t qs = static_cast<uint32_t>(a.q_scales[th + 16 * hb + 4 * g + i]);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wabs[b] += fabsf(wi) * e8m0_value((qs >> (8 * b)) & 0xffu);
+      } else {
+        wabs[0] += fabsf(wi);
+      }
     }
-  float ws = (col == 0) ? wabs : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
-  for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
-  ebound = ws * (448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float ws = (col == 0) ? wabs[b] : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
+    for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
+    op.eb[b] = ws * (kFp4 ? kFp4BoundFactor : 448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+  }
 }
 
 // Streams logical pages of row t: `first`, then the pages next() returns (an
@@ -354,10 +540,9 @@ __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t,
 // calls emit(lp, page, sc, e) with page = the block-table entry, or -1 when the
 // page is unmapped; the lower bound sc - e of every token s < n goes into the
 // LDS histogram.
-template <class Next, class Emit>
+template <bool kFp4, class Next, class Emit>
 __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
-                                              uint32_t* s_hist, const i32x8 (&qa)[4], const float (&wv)[4][4],
-                                              float ebound, Emit emit) {
+                                              uint32_t* s_hist, const FilterOps& op, Emit emit) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, col = lane & 15;
   const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
@@ -367,22 +552,28 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
     const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : -1;
     return (p >= 0 && p < a.num_pages) ? p : -1;
   };
-  // One page = 4 blocks of 16 tokens; this lane's 32 bytes of each block row,
-  // and the scale of row `lane` (one coalesced 256-byte load per page).
-  // Loads are unconditional so the compiler keeps them in flight.
-  auto load_page = [&](int64_t page, uint4 (&kb)[4][2], float& ks) {
+  // One page = 4 blocks of 16 tokens; this lane's 32 bytes (fp4: 16) of each
+  // block row, and the scale (fp4: four scale bytes) of row `lane` (one
+  // coalesced 256-byte load per page).  Loads are unconditional so the
+  // compiler keeps them in flight.
+  auto load_page = [&](int64_t page, uint4 (&kb)[4][2], uint32_t& ks) {
     const uint8_t* pbase = a.kcache + (page >= 0 ? page : 0) * a.page_stride;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int row = 16 * b + col;
-      const uint4* src = reinterpret_cast<const uint4*>(pbase + row * kIdxDim + 32 * g);
-      kb[b][0] = src[0];
-      kb[b][1] = src[1];
+      if constexpr (kFp4) {
+        kb[b][0] = *reinterpret_cast<const uint4*>(pbase + row * kFp4Row + 16 * g);
+        kb[b][1] = make_uint4(0, 0, 0, 0);
+      } else {
+        const uint4* src = reinterpret_cast<const uint4*>(pbase + row * kIdxDim + 32 * g);
+        kb[b][0] = src[0];
+        kb[b][1] = src[1];
+      }
     }
-    ks = *reinterpret_cast<const float*>(pbase + kIdxPageBytes + lane * 4);
+    ks = *reinterpret_cast<const uint32_t*>(pbase + (kFp4 ? kFp4PageBytes : kIdxPageBytes) + lane * 4);
   };
   uint4 nxt[4][2];
-  float nks;
+  uint32_t nks;
   int lp = first;
   int lp1 = next();
   int64_t cur_page = page_of(lp);
@@ -396,7 +587,7 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
       kb[b][1] = nxt[b][1];
     }
     const int64_t page = cur_page;
-    const float page_scale = page >= 0 ? nks : 0.0f;  // scale of page row `lane`
+    const uint32_t row_scale = nks;  // scale word of page row `lane`
     load_page(page1, nxt, nks);  // in flight while this page is scored
     cur_page = page1;
     const int lp2 = next();
@@ -407,20 +598,33 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
       const i32x8 kv = i32x8{static_cast<int>(kb[b][0].x), static_cast<int>(kb[b][0].y), static_cast<int>(kb[b][0].z),
                              static_cast<int>(kb[b][0].w), static_cast<int>(kb[b][1].x), static_cast<int>(kb[b][1].y),
                              static_cast<int>(kb[b][1].z), static_cast<int>(kb[b][1].w)};
+      // fp4: block g's scale byte of token 16b + col (page row 16b + col)
+      const uint32_t kscb =
+          kFp4 ? (static_cast<uint32_t>(__shfl(static_cast<int>(row_scale), 16 * b + col)) >> (8 * g)) & 0xffu : 0u;
       float acc = 0.0f;
 #pragma unroll
       for (int hb = 0; hb < 4; ++hb) {
-        const f32x4 cc = filter_mfma(qa[hb], kv);
+        const f32x4 cc = kFp4 ? filter_mfma_fp4(op.qa[hb], op.qsc[hb], kv, kscb) : filter_mfma(op.qa[hb], kv);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += wv[hb][i] * fmaxf(cc[i], 0.0f);
+        for (int i = 0; i < 4; ++i) acc += op.wv[hb][i] * fmaxf(cc[i], 0.0f);
       }
       acc += __shfl_xor(acc, 16);
       acc += __shfl_xor(acc, 32);
       if (g == b) mine = acc;  // block b's token col is page row 16b + col = this lane
     }
     const int64_t s = static_cast<int64_t>(lp) * kPageTokens + lane;
-    const float sc = mine * page_scale;
-    const float e = page_scale * ebound;
+    float sc, e;
+    if constexpr (kFp4) {
+      float eb = 0.0f;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) eb += op.eb[b] * e8m0_value((row_scale >> (8 * b)) & 0xffu);
+      sc = page >= 0 ? mine : 0.0f;
+      e = page >= 0 ? eb : 0.0f;
+    } else {
+      const float page_scale = page >= 0 ? __uint_as_float(row_scale) : 0.0f;
+      sc = mine * page_scale;
+      e = page_scale * op.eb[0];
+    }
     if (s < n) atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
     emit(lp, page, sc, e);
     lp = lp1;
@@ -440,6 +644,7 @@ __device__ __forceinline__ uint16_t upper_prefix(float sc, float e) {
 // also wait for the store (vector memory counts retire in order).
 constexpr int kFilterStage = 32;  // pages of upper bounds staged per wave
 
+template <bool kFp4>
 __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   __shared__ uint32_t s_hist[kHistBins];
   __shared__ __align__(16) uint16_t s_up[4][kFilterStage * kPageTokens];
@@ -469,10 +674,8 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
 
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, col = lane & 15;
-  i32x8 qa[4];
-  float wv[4][4];
-  float ebound;
-  load_filter_operands(a, t, g, col, qa, wv, ebound);
+  FilterOps op;
+  load_filter_operands<kFp4>(a, t, g, col, op);
   __syncthreads();
 
   const int wr = __builtin_amdgcn_readfirstlane(4 * x + wave);  // wave of the row
@@ -495,8 +698,8 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   };
   int staged = 0, stage_first = p_begin;
   int seq = p_begin;
-  filter_stream(a, t, n, p_begin, p_end, [&] { return ++seq; }, s_hist, qa, wv, ebound,
-                [&](int lp, int64_t, float sc, float e) {
+  filter_stream<kFp4>(a, t, n, p_begin, p_end, [&] { return ++seq; }, s_hist, op,
+                      [&](int lp, int64_t, float sc, float e) {
     stage[staged * kPageTokens + lane] = bf16_round_up(sc + e);
     if (++staged == kFilterStage) {  // wave-uniform
       __builtin_amdgcn_wave_barrier();
@@ -576,20 +779,27 @@ struct VerifyArgs {
   int32_t* cand_idx;         // [T, max_len]
   int32_t* cand_count;       // [T, chunks]
   int32_t chunks;
+  const uint8_t* q_fp4;      // fp4 keys: q values [T, 64, 64] (q_digits unused)
+  const int32_t* q_scales;   // fp4 keys: [T, 64]
 };
 
 constexpr int kVerifyChunks = 4;  // chunks per verify workgroup
 constexpr int kVerifyPages = kVerifyChunks * kChunk / kPageTokens;
 
+template <bool kFp4>
 __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
-  __shared__ uint32_t s_table[256];
+  __shared__ uint32_t s_table[256];  // fp8: digit table; fp4: q scale words
   __shared__ int16_t s_list[kVerifyChunks * kChunk];  // candidate token offsets in the group, ascending
   __shared__ int16_t s_meta[kVerifyChunks * kChunk];  // chunk (bits 11..12) and position in its chunk list
   __shared__ int32_t s_pages[kVerifyPages];           // block-table entries of the group's pages
   __shared__ int s_wave[4];
   const int tid = threadIdx.x;
-  s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
   const int t = blockIdx.y;
+  if constexpr (kFp4) {
+    if (tid < kIdxHeads) s_table[tid] = static_cast<uint32_t>(a.q_scales[static_cast<int64_t>(t) * kIdxHeads + tid]);
+  } else {
+    s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  }
   const int n = min(a.lengths[t], a.max_len);
   const int64_t row = static_cast<int64_t>(t) * a.max_len;
   const int c_begin = blockIdx.x * kVerifyChunks;
@@ -617,8 +827,14 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
     const int64_t blk = (tok0 >> 6) + tid;
     s_pages[tid] = (blk < a.bt_stride) ? bt[blk] : -1;
   }
+  // fp8: digit operands; fp4: packed-value operands (the other is unused)
   ExactOperands op;
-  load_exact_operands(op, a.q_digits, a.w, t, g, col);
+  Fp4Operands op4;
+  if constexpr (kFp4) {
+    load_fp4_operands(op4, a.q_fp4, a.w, t, g, col);
+  } else {
+    load_exact_operands(op, a.q_digits, a.w, t, g, col);
+  }
   // Candidates of each chunk (ascending), appended to one list.  The upper
   // bounds of all the workgroup's chunks are loaded before any is tested.
   const uint32_t kbound = a.kbound[t];
@@ -685,23 +901,34 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
     }
     uint4 kb[kVerifyBatch][2];
     float ks[kVerifyBatch];
+    Fp4Key k4[kFp4 ? kVerifyBatch : 1];
 #pragma unroll
     for (int j = 0; j < kVerifyBatch; ++j) {
       const bool ok = page[j] >= 0 && page[j] < a.num_pages;
       const uint8_t* base = a.kcache + (ok ? page[j] : 0) * a.page_stride;
       const int r = static_cast<int>(tok[j] & 63);
-      const uint4 k0 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 16 * g);
-      const uint4 k1 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 64 + 16 * g);
-      const float sc = *reinterpret_cast<const float*>(base + kIdxPageBytes + r * 4);
-      kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
-      kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
-      ks[j] = ok ? sc : 0.0f;
+      if constexpr (kFp4) {
+        load_key_fp4(base, r, g, ok, k4[j]);
+      } else {
+        const uint4 k0 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 16 * g);
+        const uint4 k1 = *reinterpret_cast<const uint4*>(base + r * kIdxDim + 64 + 16 * g);
+        const float sc = *reinterpret_cast<const float*>(base + kIdxPageBytes + r * 4);
+        kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
+        kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
+        ks[j] = ok ? sc : 0.0f;
+      }
     }
 #pragma unroll
     for (int j = 0; j < kVerifyBatch; ++j) {
       const int b0 = bb + 64 * j;
       if (b0 >= total) break;
-      const float sc = exact_block(op, s_table, kb[j], ks[j]);
+      float sc;
+      if constexpr (kFp4) {
+        sc = exact_block_fp4([&](int hb, int b) { return op4.q[hb][b]; }, [&](int h) { return s_table[h]; }, op4.wv,
+                             k4[j]);
+      } else {
+        sc = exact_block(op, s_table, kb[j], ks[j]);
+      }
       const int li = b0 + col;
       if (li < total && g == 0) {
         const int meta = s_meta[li];
@@ -771,14 +998,19 @@ struct FusedLayout {
   static constexpr int bytes(int stage_pages) { return kFixed + stage_pages * (4 + 2 * kPageTokens); }
 };
 
-template <int kWaves>
+// fp4 keys: the q operands of the exact path, [hb][block][lane] 8-byte words.
+constexpr int kFusedQ4Words = 4 * 4 * 64;
+static_assert(kFusedQ4Words * 8 <= kFusedQdBytes, "fp4 q operands share the digit operands' LDS");
+
+template <int kWaves, bool kFp4>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) filter_verify_kernel(FusedArgs a) {
   using Lay = FusedLayout<kWaves>;
   constexpr int kThreads = Lay::kThreads;
   extern __shared__ __align__(16) uint8_t fused_smem[];
   uint32_t* s_hist = reinterpret_cast<uint32_t*>(fused_smem);     // phase 1
   const uint4* s_qd = reinterpret_cast<const uint4*>(fused_smem);  // phases 2-3 (same bytes)
-  uint32_t* s_table = reinterpret_cast<uint32_t*>(fused_smem + kFusedQdBytes);
+  const uint2* s_q4 = reinterpret_cast<const uint2*>(fused_smem);  // fp4: phases 2-3 (same bytes)
+  uint32_t* s_table = reinterpret_cast<uint32_t*>(fused_smem + kFusedQdBytes);  // fp4: q scale words
   int32_t* s_list = reinterpret_cast<int32_t*>(s_table + 256);
   int* s_misc = reinterpret_cast<int*>(s_list + Lay::kList);  // [0..15] scans, [16] last, [17] bin, [18] next page
   int32_t* s_pages = reinterpret_cast<int32_t*>(s_misc + 32);
@@ -805,14 +1037,16 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     return;
   }
   for (int i = tid; i < kHistBins; i += kThreads) s_hist[i] = 0;
-  if (tid < 256) s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  if constexpr (kFp4) {
+    if (tid < kIdxHeads) s_table[tid] = static_cast<uint32_t>(f.q_scales[static_cast<int64_t>(t) * kIdxHeads + tid]);
+  } else {
+    if (tid < 256) s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
+  }
   if (tid == 0) s_misc[18] = wg_p0 + kWaves;  // wave w starts at page wg_p0 + w
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, col = lane & 15;
-  i32x8 qa[4];
-  float wv[4][4];
-  float ebound;
-  load_filter_operands(f, t, g, col, qa, wv, ebound);
+  FilterOps op;
+  load_filter_operands<kFp4>(f, t, g, col, op);
   __syncthreads();
 
   // Phase 1: stream the pages; upper-bound prefixes and page entries to LDS.
@@ -821,11 +1055,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     if (lane == 0) v = atomicAdd(&s_misc[18], 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  filter_stream(f, t, n, wg_p0 + wave, wg_p1, grab, s_hist, qa, wv, ebound,
-                [&](int lp, int64_t page, float sc, float e) {
-                  s_pref[(lp - wg_p0) * kPageTokens + lane] = upper_prefix(sc, e);
-                  if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
-                });
+  filter_stream<kFp4>(f, t, n, wg_p0 + wave, wg_p1, grab, s_hist, op,
+                      [&](int lp, int64_t page, float sc, float e) {
+                        s_pref[(lp - wg_p0) * kPageTokens + lane] = upper_prefix(sc, e);
+                        if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
+                      });
   __syncthreads();
   uint32_t* gh = a.counters + static_cast<int64_t>(t) * kCounterRow;
   uint32_t* const arrive = gh + kHistBins;
@@ -834,18 +1068,32 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t v = s_hist[i];
     if (v) atomicAdd(&gh[i], v);
   }
-  // q digit operands, into the histogram's LDS once every lane is past it.
+  // q exact operands, into the histogram's LDS once every lane is past it
+  // (fp8: digit planes; fp4: the 2 * e2m1 values, [hb][block][lane]).
   constexpr int kQdPer = (kFusedQdBytes / 16) / kThreads;
   static_assert(kQdPer * kThreads * 16 == kFusedQdBytes, "q digit staging must divide evenly");
-  uint4 qd_regs[kQdPer];
+  constexpr int kQ4Per = (kFusedQ4Words + kThreads - 1) / kThreads;
+  uint4 qd_regs[kFp4 ? 1 : kQdPer];
+  uint2 q4_regs[kFp4 ? kQ4Per : 1];
+  if constexpr (kFp4) {
 #pragma unroll
-  for (int j = 0; j < kQdPer; ++j) {
-    const int idx = tid + kThreads * j;  // entry e = (hb * 3 + d) * 2 + kh, lane ln
-    const int e = idx >> 6, ln = idx & 63;
-    const int hb = e / 6, d = (e / 2) % 3, kh = e & 1;
-    const int lg = ln >> 4, lc = ln & 15;
-    qd_regs[j] = *reinterpret_cast<const uint4*>(a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + lc) *
-                                                                  kIdxDim + 64 * kh + 16 * lg);
+    for (int j = 0; j < kQ4Per; ++j) {
+      const int idx = tid + kThreads * j;  // entry e = hb * 4 + b, lane ln
+      const int e = idx >> 6, ln = idx & 63;
+      int64_t v = 0;
+      if (idx < kFusedQ4Words) v = load_q_fp4(f.q_fp8, t, e >> 2, e & 3, ln >> 4, ln & 15);
+      q4_regs[j] = make_uint2(static_cast<uint32_t>(v), static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kQdPer; ++j) {
+      const int idx = tid + kThreads * j;  // entry e = (hb * 3 + d) * 2 + kh, lane ln
+      const int e = idx >> 6, ln = idx & 63;
+      const int hb = e / 6, d = (e / 2) % 3, kh = e & 1;
+      const int lg = ln >> 4, lc = ln & 15;
+      qd_regs[j] = *reinterpret_cast<const uint4*>(
+          a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + lc) * kIdxDim + 64 * kh + 16 * lg);
+    }
   }
   // Every histogram atomic of the workgroup has completed before it arrives.
   // No cache maintenance is needed: device-scope atomics and the agent-scope
@@ -862,9 +1110,16 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     s_misc[16] = ((before & 0xffffu) + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
     s_misc[17] = 0;
   }
-  uint4* s_qd_w = reinterpret_cast<uint4*>(fused_smem);
+  if constexpr (kFp4) {
+    uint2* s_q4_w = reinterpret_cast<uint2*>(fused_smem);
 #pragma unroll
-  for (int j = 0; j < kQdPer; ++j) s_qd_w[tid + kThreads * j] = qd_regs[j];
+    for (int j = 0; j < kQ4Per; ++j)
+      if (tid + kThreads * j < kFusedQ4Words) s_q4_w[tid + kThreads * j] = q4_regs[j];
+  } else {
+    uint4* s_qd_w = reinterpret_cast<uint4*>(fused_smem);
+#pragma unroll
+    for (int j = 0; j < kQdPer; ++j) s_qd_w[tid + kThreads * j] = qd_regs[j];
+  }
   __syncthreads();
   if (s_misc[16]) {
     constexpr int kBinsPer = (kHistBins + kThreads - 1) / kThreads;  // scanned from the top bin down
@@ -947,28 +1202,43 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       }
       uint4 kb[kBatch][2];
       float ks[kBatch];
+      Fp4Key k4[kFp4 ? kBatch : 1];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         const bool ok = page[j] >= 0;  // mapped pages only (checked when streamed)
         const uint8_t* base_p = f.kcache + (ok ? page[j] : 0) * f.page_stride;
         const int r = tok[j] & 63;
-        const uint4 k0 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 16 * g);
-        const uint4 k1 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 64 + 16 * g);
-        const float sc = *reinterpret_cast<const float*>(base_p + kIdxPageBytes + r * 4);
-        kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
-        kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
-        ks[j] = ok ? sc : 0.0f;
+        if constexpr (kFp4) {
+          load_key_fp4(base_p, r, g, ok, k4[j]);
+        } else {
+          const uint4 k0 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 16 * g);
+          const uint4 k1 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 64 + 16 * g);
+          const float sc = *reinterpret_cast<const float*>(base_p + kIdxPageBytes + r * 4);
+          kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
+          kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
+          ks[j] = ok ? sc : 0.0f;
+        }
       }
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         const int b0 = bb + 16 * kWaves * j;
         if (b0 >= cnt) break;
-        const float sc = exact_block_with<true>(
-            [&](int hb, int d, int kh) {
-              const uint4 v = s_qd[((hb * 3 + d) * 2 + kh) * 64 + lane];
-              return i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-            },
-            wv, s_table, kb[j], ks[j]);
+        float sc;
+        if constexpr (kFp4) {
+          sc = exact_block_fp4<true>(
+              [&](int hb, int b) {
+                const uint2 v = s_q4[(hb * 4 + b) * 64 + lane];
+                return static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
+              },
+              [&](int h) { return s_table[h]; }, op.wv, k4[j]);
+        } else {
+          sc = exact_block_with<true>(
+              [&](int hb, int d, int kh) {
+                const uint4 v = s_qd[((hb * 3 + d) * 2 + kh) * 64 + lane];
+                return i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+              },
+              op.wv, s_table, kb[j], ks[j]);
+        }
         const int li = b0 + col;
         if (li < cnt && g == 0) {
           a.cand_score[out0 + base + li] = sc;
@@ -1558,10 +1828,10 @@ int occupancy(const void* kernel, int threads, int smem) {
   return occ;
 }
 
-template <int kWaves>
+template <int kWaves, bool kFp4>
 bool plan_fused(int64_t T, int32_t max_len, int64_t pages, int cus, int64_t target_groups, FilterPlan& p) {
   if (T > kCounterRows) return false;
-  const void* kernel = reinterpret_cast<const void*>(filter_verify_kernel<kWaves>);
+  const void* kernel = reinterpret_cast<const void*>(filter_verify_kernel<kWaves, kFp4>);
   int64_t groups = std::max<int64_t>(1, std::min<int64_t>((pages + kWaves - 1) / kWaves, (target_groups + T - 1) / T));
   for (int attempt = 0; attempt < 4 && groups >= 1; ++attempt) {
     const int per_group = fused_group_pages(max_len, static_cast<int>(groups));
@@ -1578,6 +1848,7 @@ bool plan_fused(int64_t T, int32_t max_len, int64_t pages, int cus, int64_t targ
   return false;
 }
 
+template <bool kFp4>
 FilterPlan plan_filter(int64_t T, int32_t max_len) {
   const int64_t pages = (static_cast<int64_t>(max_len) + kPageTokens - 1) / kPageTokens;
   FilterPlan p{false, 4, 1, 0, 0};
@@ -1592,8 +1863,8 @@ FilterPlan plan_filter(int64_t T, int32_t max_len) {
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     return p;
-  if (T <= cus && plan_fused<12>(T, max_len, pages, cus, cus, p)) return p;
-  if (plan_fused<4>(T, max_len, pages, cus, kFilterTargetGroups, p)) return p;
+  if (T <= cus && plan_fused<12, kFp4>(T, max_len, pages, cus, cus, p)) return p;
+  if (plan_fused<4, kFp4>(T, max_len, pages, cus, kFilterTargetGroups, p)) return p;
   return p;
 }
 
@@ -1617,9 +1888,27 @@ extern "C" int ekv_indexer_score(const int8_t* q_digits, const float* w, const u
   EKV_CHECK(scores_stride >= max_len, "scores_stride must be >= max_len");
   EKV_CHECK(aligned16(q_digits) && aligned16(kcache), "misaligned buffers");
   ScoreArgs a{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-              scores, scores_stride, max_len};
+              scores, scores_stride, max_len, nullptr, nullptr};
   dim3 grid((max_len + kScoreChunk - 1) / kScoreChunk, num_tokens);
-  hipLaunchKernelGGL(score_exact_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(score_exact_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_score_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                     const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                     const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                     const int32_t* lengths, int32_t num_tokens, int32_t max_len, float* scores,
+                                     int64_t scores_stride, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && max_len >= 0, "sizes must be >= 0");
+  if (num_tokens == 0 || max_len == 0) return 0;
+  EKV_CHECK(q_values && q_scales && w && kcache && block_table && req_ids && lengths && scores, "null pointer");
+  EKV_CHECK(page_stride >= kPageTokens * (kFp4Row + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(scores_stride >= max_len, "scores_stride must be >= max_len");
+  EKV_CHECK(aligned16(q_values) && aligned16(kcache), "misaligned buffers");
+  ScoreArgs a{nullptr, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+              scores, scores_stride, max_len, q_values, q_scales};
+  dim3 grid((max_len + kScoreChunk - 1) / kScoreChunk, num_tokens);
+  hipLaunchKernelGGL(score_exact_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return ekv_launch_status();
 }
 
@@ -1631,6 +1920,17 @@ extern "C" int ekv_indexer_filter_dots(const uint8_t* q_codes, const uint8_t* k_
   EKV_CHECK(aligned16(q_codes) && aligned16(k_codes), "misaligned buffers");
   hipLaunchKernelGGL(filter_dots_kernel, dim3(num_keys / 16), dim3(64), 0, static_cast<hipStream_t>(stream), q_codes,
                      k_codes, out);
+  return ekv_launch_status();
+}
+
+extern "C" int ekv_indexer_filter_dots_fp4(const uint8_t* q_values, const int32_t* q_scales, const uint8_t* k_values,
+                                           const int32_t* k_scales, int32_t num_keys, float* out, void* stream) {
+  EKV_CHECK(num_keys >= 0 && num_keys % 16 == 0, "num_keys must be a multiple of 16");
+  if (num_keys == 0) return 0;
+  EKV_CHECK(q_values && q_scales && k_values && k_scales && out, "null pointer");
+  EKV_CHECK(aligned16(q_values) && aligned16(k_values), "misaligned buffers");
+  hipLaunchKernelGGL(filter_dots_fp4_kernel, dim3(num_keys / 16), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     q_values, q_scales, k_values, k_scales, out);
   return ekv_launch_status();
 }
 
@@ -1652,10 +1952,10 @@ namespace {
 
 int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_t page_stride,
                     const int32_t* block_table, const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
-                    int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes) {
+                    int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes, bool fp4) {
   EKV_CHECK(num_tokens >= 0 && max_len >= 0 && k > 0, "bad sizes");
   EKV_CHECK(q && w && kcache && block_table && req_ids && lengths, "null pointer");
-  EKV_CHECK(page_stride >= kPageTokens * (kIdxDim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(page_stride >= kPageTokens * ((fp4 ? kFp4Row : kIdxDim) + 4) && page_stride % 16 == 0, "bad page_stride");
   EKV_CHECK(aligned16(q) && aligned16(kcache), "misaligned buffers");
   const int64_t need = ekv_indexer_topk_workspace_size(num_tokens, max_len);
   EKV_CHECK(workspace != nullptr || need == 0, "workspace is null");
@@ -1666,42 +1966,54 @@ int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_
   return 0;
 }
 
-}  // namespace
+// Query-side operands of one top-k call: fp8 keys take q codes, their digit
+// planes and the folded weights; fp4 keys take q values, q scale words and
+// the weights.
+struct TopkQuery {
+  const uint8_t* q;         // fp8: codes [T, 64, 128]; fp4: packed values [T, 64, 64]
+  const int8_t* q_digits;   // fp8 only
+  const int32_t* q_scales;  // fp4 only
+  const float* w;
+};
 
-// Stage 1: fp8-MFMA filter.  Fused plan: filter, bound and exact scoring of
-// the candidates in one launch.  Otherwise: upper bounds, lower-bound
-// histogram and key bound; the candidates are scored in stage 2.
-extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
-                                  const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
-                                  const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
-                                  const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t k,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  int rc = check_topk_args(q_fp8, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
-                           workspace, workspace_bytes);
+// Stage 1: MFMA filter.  Fused plan: filter, bound and exact scoring of the
+// candidates in one launch.  Otherwise: upper bounds, lower-bound histogram
+// and key bound; the candidates are scored in stage 2.
+template <bool kFp4>
+int run_filter(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+               const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
+               int32_t num_tokens, int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes,
+               void* stream) {
+  int rc = check_topk_args(q.q, q.w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
+                           workspace, workspace_bytes, kFp4);
   if (rc) return rc;
-  EKV_CHECK(q_digits != nullptr && aligned16(q_digits), "q_digits must be a 16-byte aligned [T, 3, 64, 128]");
+  if constexpr (kFp4) {
+    EKV_CHECK(q.q_scales != nullptr, "q_scales must be a [T, 64] int32");
+  } else {
+    EKV_CHECK(q.q_digits != nullptr && aligned16(q.q_digits), "q_digits must be a 16-byte aligned [T, 3, 64, 128]");
+  }
   if (num_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   TopkWorkspace ws = carve(workspace, T, L);
-  const FilterPlan plan = plan_filter(T, max_len);
-  FilterArgs f{q_fp8, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-               max_len, k, ws.upper, ws.hist, num_tokens, plan.groups};
+  const FilterPlan plan = plan_filter<kFp4>(T, max_len);
+  FilterArgs f{q.q, q.w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+               max_len, k, ws.upper, ws.hist, num_tokens, plan.groups, q.q_scales};
   if (plan.fused) {
     // the fused kernel's counters are zero on entry and left zero
-    FusedArgs fa{f, q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
+    FusedArgs fa{f, q.q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
                  plan.groups, plan.stage_pages};
     const dim3 grid(static_cast<unsigned>(plan.groups), num_tokens);
     if (plan.waves == 12)
-      hipLaunchKernelGGL(filter_verify_kernel<12>, grid, dim3(64 * 12), plan.smem, s, fa);
+      hipLaunchKernelGGL((filter_verify_kernel<12, kFp4>), grid, dim3(64 * 12), plan.smem, s, fa);
     else
-      hipLaunchKernelGGL(filter_verify_kernel<4>, grid, dim3(64 * 4), plan.smem, s, fa);
+      hipLaunchKernelGGL((filter_verify_kernel<4, kFp4>), grid, dim3(64 * 4), plan.smem, s, fa);
   } else if (max_len > 0) {
     const int64_t nz = T * kHistBins + 2 * T;  // this call's hist, arrive, kbound
     const int64_t zero_blocks = (nz + 255) / 256;
     hipLaunchKernelGGL(zero_u32_kernel, dim3(static_cast<unsigned>(zero_blocks < 1024 ? zero_blocks : 1024)),
                        dim3(256), 0, s, ws.hist, nz);
-    hipLaunchKernelGGL(filter_kernel, dim3(static_cast<unsigned>(plan.groups * T)), dim3(256), 0, s, f);
+    hipLaunchKernelGGL(filter_kernel<kFp4>, dim3(static_cast<unsigned>(plan.groups * T)), dim3(256), 0, s, f);
     hipLaunchKernelGGL(bound_kernel, dim3(num_tokens), dim3(256), 0, s, ws.hist, lengths, max_len, k, ws.kbound);
   }
   return ekv_launch_status();
@@ -1709,16 +2021,17 @@ extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, 
 
 // Stage 2: (unfused plan) exact scores of the candidates of each chunk; then
 // the exact select over the candidate lists.
-extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache, int64_t page_stride,
-                                  int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
-                                  const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
-                                  int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
-                                  void* workspace, int64_t workspace_bytes, int32_t* merged_out,
-                                  int64_t merged_stride, int32_t merged_width, const int64_t* positions,
-                                  int32_t window, int32_t merged_slots, void* stream) {
-  int rc = check_topk_args(q_digits, w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
-                           workspace, workspace_bytes);
+template <bool kFp4>
+int run_select(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+               const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
+               int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
+               void* workspace, int64_t workspace_bytes, int32_t* merged_out, int64_t merged_stride,
+               int32_t merged_width, const int64_t* positions, int32_t window, int32_t merged_slots, void* stream) {
+  int rc = check_topk_args(kFp4 ? static_cast<const void*>(q.q) : static_cast<const void*>(q.q_digits), q.w, kcache,
+                           page_stride, block_table, req_ids, lengths, num_tokens, max_len, k, workspace,
+                           workspace_bytes, kFp4);
   if (rc) return rc;
+  if constexpr (kFp4) EKV_CHECK(q.q_scales != nullptr, "q_scales must be a [T, 64] int32");
   EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
   EKV_CHECK(merged_out == nullptr || (positions != nullptr && window >= 0 && merged_width >= 0 &&
                                       merged_stride >= merged_width),
@@ -1729,12 +2042,13 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
   const int chunks = num_chunks(max_len);
   EKV_CHECK(chunks <= kSelMaxChunks, "max_len too large for the select stage");
   TopkWorkspace ws = carve(workspace, T, L);
-  const FilterPlan plan = plan_filter(T, max_len);
+  const FilterPlan plan = plan_filter<kFp4>(T, max_len);
   if (!plan.fused) {
-    VerifyArgs v{q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-                 max_len, k, ws.upper, ws.kbound, ws.cand_score, ws.cand_idx, ws.counts, chunks};
-    hipLaunchKernelGGL(verify_kernel, dim3((chunks + kVerifyChunks - 1) / kVerifyChunks, num_tokens), dim3(256), 0,
-                       s, v);
+    VerifyArgs v{q.q_digits, q.w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
+                 max_len, k, ws.upper, ws.kbound, ws.cand_score, ws.cand_idx, ws.counts, chunks,
+                 kFp4 ? q.q : nullptr, q.q_scales};
+    hipLaunchKernelGGL(verify_kernel<kFp4>, dim3((chunks + kVerifyChunks - 1) / kVerifyChunks, num_tokens),
+                       dim3(256), 0, s, v);
   }
   SelectArgs sel{nullptr, 0, lengths, ws.cand_score, ws.cand_idx, ws.counts, plan.fused ? plan.groups : chunks,
                  ws.stage_score, ws.stage_idx, topk_out, out_stride, k, static_cast<int32_t>(L),
@@ -1742,6 +2056,30 @@ extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const 
                  merged_slots ? block_table : nullptr, bt_stride, req_ids, num_pages};
   launch_select(sel, num_tokens, s);
   return ekv_launch_status();
+}
+
+}  // namespace
+
+extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
+                                  const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                  const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                  const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t k,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  return run_filter<false>(TopkQuery{q_fp8, q_digits, nullptr, w}, kcache, page_stride, num_pages, block_table,
+                           bt_stride, req_ids, lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kcache, int64_t page_stride,
+                                  int64_t num_pages, const int32_t* block_table, int64_t bt_stride,
+                                  const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
+                                  int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k,
+                                  void* workspace, int64_t workspace_bytes, int32_t* merged_out,
+                                  int64_t merged_stride, int32_t merged_width, const int64_t* positions,
+                                  int32_t window, int32_t merged_slots, void* stream) {
+  return run_select<false>(TopkQuery{nullptr, q_digits, nullptr, w}, kcache, page_stride, num_pages, block_table,
+                           bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                           workspace_bytes, merged_out, merged_stride, merged_width, positions, window,
+                           merged_slots, stream);
 }
 
 extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
@@ -1756,4 +2094,40 @@ extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, co
   return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
                             num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, nullptr, 0, 0,
                             nullptr, 0, 0, stream);
+}
+
+extern "C" int ekv_indexer_filter_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                      const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                      const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                      const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t k,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
+  return run_filter<true>(TopkQuery{q_values, nullptr, q_scales, w}, kcache, page_stride, num_pages, block_table,
+                          bt_stride, req_ids, lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ekv_indexer_select_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                      const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                      const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                      const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                                      int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                                      int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
+                                      const int64_t* positions, int32_t window, int32_t merged_slots, void* stream) {
+  return run_select<true>(TopkQuery{q_values, nullptr, q_scales, w}, kcache, page_stride, num_pages, block_table,
+                          bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                          workspace_bytes, merged_out, merged_stride, merged_width, positions, window, merged_slots,
+                          stream);
+}
+
+extern "C" int ekv_indexer_topk_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                    const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                    const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                    const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                                    int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  int rc = ekv_indexer_filter_fp4(q_values, q_scales, w, kcache, page_stride, num_pages, block_table, bt_stride,
+                                  req_ids, lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return ekv_indexer_select_fp4(q_values, q_scales, w, kcache, page_stride, num_pages, block_table, bt_stride,
+                                req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                                workspace_bytes, nullptr, 0, 0, nullptr, 0, 0, stream);
 }

@@ -62,6 +62,18 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_indexer_filter_dots": (I32, [P, P, I32, P, P]),
     "ekv_sigmoid_mul_quant_fp8": (I32, [P, I64, P, I64, I32, I32, P, I64, P, I64, P]),
     "ekv_vha_inv_rope_fp8_quant": (I32, [P, I64, I64, I32, I32, P, P, P, I64, I32, I32, I32, P, P, I32, P]),
+    "ekv_mxfp4_quant": (I32, [P, I64, I64, I32, I32, I32, P, I64, P, I64, P]),
+    "ekv_indexer_q_quant_fp4": (I32, [P, I64, I64, P, I32, I64, I32, I32, P, P, P, P]),
+    "ekv_indexer_k_insert_fp4": (I32, [P, I64, I32, P, P, I64, I64, P]),
+    "ekv_indexer_store_fp4": (I32, [P, I64, P, I64, I32, P, P, I64, I64, P]),
+    "ekv_indexer_score_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, P]),
+    "ekv_indexer_filter_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, I32, P, I64, P]),
+    "ekv_indexer_select_fp4": (
+        I32,
+        [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P],
+    ),
+    "ekv_indexer_topk_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P]),
+    "ekv_indexer_filter_dots_fp4": (I32, [P, P, P, P, I32, P, P]),
 }
 
 _lib = None

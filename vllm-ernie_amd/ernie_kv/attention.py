@@ -25,6 +25,7 @@ from . import ops
 
 DSA_BLOCK_SIZE = 64  # attention.py:97-98
 INDEXER_QUANT_BLOCK = 128  # attention.py:99
+MXFP4_BLOCK_SIZE = 32  # values per UE8M0 scale of the MXFP4 indexer cache (attention.py:47, 932)
 
 
 # --------------------------------------------------------------------------- vLLM stand-ins
@@ -426,13 +427,23 @@ class Ernie5_5Indexer:
     top-k of each query row over its first ``position + 1 - window``
     tokens, written to ``indexer_op.topk_indices_buffer[:T]``.
     ``topk_indices_buffer`` (the layer attribute) is the swa buffer the
-    sparse MLA reads: the merged rows.  FP8 K cache only (132-byte rows)."""
+    sparse MLA reads: the merged rows.  K cache rows are 132 bytes (fp8
+    values + fp32 scale) or, with ``use_fp4_kv``, 68 bytes (MXFP4 values +
+    four E8M0 scales; ``_quantize_fp4``, attention.py:986-1025), which the
+    reference allows only without context parallelism (:881-892)."""
 
     def __init__(self, config, topk_indices_buffer: torch.Tensor | None, swa_topk_buffer: torch.Tensor | None,
                  prefix: str = "", *, wq_b: torch.Tensor, wk_weights_proj: torch.Tensor,
-                 k_norm_weight: torch.Tensor, k_norm_bias: torch.Tensor, use_fp4_kv: bool = False) -> None:
-        if use_fp4_kv:
-            raise NotImplementedError("the MXFP4 indexer cache is not built; use the FP8 (132-byte) cache")
+                 k_norm_weight: torch.Tensor, k_norm_bias: torch.Tensor, use_fp4_kv: bool = False,
+                 prefill_context_parallel_size: int = 1, decode_context_parallel_size: int = 1) -> None:
+        self.use_fp4_kv = bool(use_fp4_kv)
+        if self.use_fp4_kv:
+            pcp_size, dcp_size = prefill_context_parallel_size, decode_context_parallel_size
+            if pcp_size != 1 or dcp_size != 1:
+                raise NotImplementedError(
+                    "ERNIE 5.5 MXFP4 indexer currently requires PCP=DCP=1 "
+                    "(prefill_context_parallel_size=1 and decode_context_parallel_size=1). "
+                    f"Got PCP={pcp_size}, DCP={dcp_size}.")
         self.n_head = config.index_n_heads
         self.head_dim = config.index_head_dim
         self.rope_dim = config.mla_qk_rope_head_dim
@@ -449,8 +460,11 @@ class Ernie5_5Indexer:
         self.k_norm_eps = 1e-6
         self.weights_scale = self.head_dim ** -0.5 * self.n_head ** -0.5
         self.topk_indices_buffer = swa_topk_buffer
-        self.k_cache = Ernie5_5IndexerCache(head_dim=self.head_dim + self.head_dim // INDEXER_QUANT_BLOCK * 4,
-                                            dtype=torch.uint8, prefix=f"{prefix}.k_cache")
+        if self.use_fp4_kv:  # 64 packed values + 4 UE8M0 scales = 68 bytes
+            k_cache_head_dim = self.head_dim // 2 + self.head_dim // MXFP4_BLOCK_SIZE
+        else:  # 128 fp8 + 4-byte fp32 scale = 132 bytes
+            k_cache_head_dim = self.head_dim + self.head_dim // INDEXER_QUANT_BLOCK * 4
+        self.k_cache = Ernie5_5IndexerCache(head_dim=k_cache_head_dim, dtype=torch.uint8, prefix=f"{prefix}.k_cache")
         self.indexer_op = SimpleNamespace(topk_indices_buffer=topk_indices_buffer, topk_tokens=self.topk)
         self._lengths: torch.Tensor | None = None
 
@@ -469,34 +483,52 @@ class Ernie5_5Indexer:
             self._lengths = torch.empty(max(T, 1), dtype=torch.int32, device=device)
         return self._lengths[:T]
 
-    def _topk(self, q8, digits, wf, md: DSAStepMetadata, lengths, positions, merged=None) -> None:
+    def _topk(self, qa, qb, wf, md: DSAStepMetadata, lengths, positions, merged=None) -> None:
         """Exact top-k of every query row (filter + select), in row pieces
         whose workspace fits _INDEXER_WORKSPACE_BYTES; with ``merged`` the
-        select also writes merge_swa_topk's rows."""
-        T = q8.shape[0]
+        select also writes merge_swa_topk's rows.  ``(qa, qb)`` are the fp8
+        codes and digit planes, or the MXFP4 values and scale words."""
+        T = qa.shape[0]
         kcache = self.k_cache.kv_cache
         out = self.indexer_op.topk_indices_buffer
         L = max(int(md.max_seq_len), 1)
         step = max(1, min(T, _INDEXER_WORKSPACE_BYTES // (20 * L)))
         for r0 in range(0, T, step):
             r1 = min(T, r0 + step)
-            ws = _indexer_workspace(r1 - r0, L, q8.device)
+            ws = _indexer_workspace(r1 - r0, L, qa.device)
             args = (kcache, md.block_table, md.req_ids[r0:r1], lengths[r0:r1], L)
-            ops.indexer_filter(q8[r0:r1], digits[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
-            ops.indexer_select(digits[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws,
-                               merged=None if merged is None else merged[r0:r1],
-                               positions=positions[r0:r1], window=self.window)
+            sel = dict(merged=None if merged is None else merged[r0:r1], positions=positions[r0:r1],
+                       window=self.window)
+            if self.use_fp4_kv:
+                ops.indexer_filter_fp4(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
+                ops.indexer_select_fp4(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws, **sel)
+            else:
+                ops.indexer_filter(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
+                ops.indexer_select(qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws, **sel)
+
+    def _quantize_fp4(self, q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, slot_mapping: torch.Tensor):
+        """MXFP4 q (values [T, 64, 64], scale words [T, 64]) and the K insert
+        of k at ``slot_mapping`` (attention.py:986-1025), plus the fp32 weights
+        ``weights * weights_scale`` (:973)."""
+        T = q.shape[0]
+        num_tokens = min(k.shape[0], slot_mapping.numel())
+        if num_tokens:
+            ops.indexer_k_insert_fp4(k[:num_tokens], slot_mapping[:num_tokens], self.k_cache.kv_cache)
+        return ops.indexer_q_quant_fp4(q.view(T, self.n_head, self.head_dim), weights)
 
     def forward(self, hidden_states: torch.Tensor, qr: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         md: DSAStepMetadata = get_forward_context().attn_metadata[self.k_cache.prefix]
         T = hidden_states.shape[0]
         q, k, weights = self._project(hidden_states, qr)
         qp, kp = ops.indexer_prep(q, k, *self._prep_args(q.device), positions)
-        ops.indexer_k_insert(kp, md.slot_mapping, self.k_cache.kv_cache)
-        q8, wf, digits = ops.indexer_q_quant(qp, weights)
+        if self.use_fp4_kv:
+            qa, qb, wf = self._quantize_fp4(qp, kp, weights, md.slot_mapping)
+        else:
+            ops.indexer_k_insert(kp, md.slot_mapping, self.k_cache.kv_cache)
+            qa, wf, qb = ops.indexer_q_quant(qp, weights)
         lengths = self._lengths_buf(T, q.device)
         ops.indexer_windowed_lengths(positions, self.window, lengths)
-        self._topk(q8, digits, wf, md, lengths, positions)
+        self._topk(qa, qb, wf, md, lengths, positions)
         return self.indexer_op.topk_indices_buffer[:T]
 
     __call__ = forward
@@ -566,7 +598,8 @@ class Ernie5_5DSAAttention:
     path; the absorbed-MLA W_UK / W_UV products run as batched GEMMs."""
 
     def __init__(self, config, prefix: str, topk_indices_buffer: torch.Tensor | None = None,
-                 swa_topk_buffer: torch.Tensor | None = None, *, params: dict, kv_cache_dtype: str = "fp8") -> None:
+                 swa_topk_buffer: torch.Tensor | None = None, *, params: dict, kv_cache_dtype: str = "fp8",
+                 use_fp4_kv: bool = False) -> None:
         _check_attn_tp(config)
         self.num_heads = config.hybrid_mla_num_attention_heads
         self.num_local_heads = self.num_heads
@@ -583,7 +616,7 @@ class Ernie5_5DSAAttention:
         self.indexer = Ernie5_5Indexer(config, topk_indices_buffer, swa_topk_buffer, prefix=f"{prefix}.indexer",
                                        wq_b=params["indexer.wq_b"], wk_weights_proj=params["indexer.wk_weights_proj"],
                                        k_norm_weight=params["indexer.k_norm.weight"],
-                                       k_norm_bias=params["indexer.k_norm.bias"])
+                                       k_norm_bias=params["indexer.k_norm.bias"], use_fp4_kv=use_fp4_kv)
         self.mla_attn = Ernie5_5MLAAttention(
             num_heads=self.num_local_heads, scale=self.qk_head_dim ** -0.5, qk_nope_head_dim=self.qk_nope_head_dim,
             qk_rope_head_dim=self.qk_rope_head_dim, v_head_dim=self.v_head_dim, kv_lora_rank=self.kv_lora_rank,
@@ -599,11 +632,17 @@ class Ernie5_5DSAAttention:
         iq, ik, iw = ix._project(hidden_states, q_c)
         latent = torch.cat([kv_c_normed, k_pe.reshape(num_tokens, -1)], dim=-1).contiguous()
         lengths = ix._lengths_buf(num_tokens, q.device)
-        q8, wf, digits = ops.dsa_decode_prologue(
-            ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions, self.window,
-            lengths, prep=ix._prep_args(q.device))
+        if ix.use_fp4_kv:  # prep, MXFP4 K insert and q, latent append, lengths
+            qp, kp = ops.indexer_prep(iq, ik, *ix._prep_args(q.device), positions)
+            qa, qb, wf = ix._quantize_fp4(qp, kp, iw, md.slot_mapping)
+            ops.kv_append_quant(latent, md.slot_mapping, self.mla_attn.kv_cache)
+            ops.indexer_windowed_lengths(positions, self.window, lengths)
+        else:  # one prologue launch
+            qa, wf, qb = ops.dsa_decode_prologue(
+                ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions,
+                self.window, lengths, prep=ix._prep_args(q.device))
         merged = ix.topk_indices_buffer[:num_tokens]
-        ix._topk(q8, digits, wf, md, lengths, positions, merged=merged)
+        ix._topk(qa, qb, wf, md, lengths, positions, merged=merged)
         q_abs = self.mla_attn.absorb_q(q)
         o_latent, _ = self.mla_attn.impl._fp8_flash_mla_kernel(
             q_abs[:, None], self.mla_attn.kv_cache, merged[:, None],

@@ -44,6 +44,7 @@ SOURCES = {
     "ekv_indexer.hip": EXACT,
     "ekv_decode.hip": [],
     "ekv_quant.hip": EXACT,
+    "ekv_mxfp4.hip": EXACT,
 }
 
 

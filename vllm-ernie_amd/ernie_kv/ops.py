@@ -499,6 +499,169 @@ def indexer_topk(
     )
 
 
+# --------------------------------------------------------------------------- MXFP4 indexer
+FP4_ROW_BYTES = INDEX_HEAD_DIM // 2 + INDEX_HEAD_DIM // 32  # 68 (attention.py:929-932)
+
+
+def fp4_page_bytes() -> int:
+    return PAGE_TOKENS * FP4_ROW_BYTES
+
+
+def mxfp4_quant(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``downcast_to_mxfp(x, axis=-1)`` of bf16 ``x [..., D]`` (D a multiple of
+    32): ``(values uint8 [..., D/2], scales uint8 [..., D/32])``."""
+    _check_dev(x)
+    _bits16(x)
+    D = x.shape[-1]
+    _need(D % 32 == 0, "last dim must be a multiple of 32")
+    x2 = x.reshape(-1, D)
+    _need(x2.stride(1) == 1, "x must have a unit last stride")
+    rows = x2.shape[0]
+    values = torch.empty((rows, D // 2), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((rows, D // 32), dtype=torch.uint8, device=x.device)
+    _lib.call("ekv_mxfp4_quant", x2.data_ptr(), _rs(x2), 0, rows, 1, D, values.data_ptr(), _rs(values),
+              scales.data_ptr(), _rs(scales), _stream())
+    return values.view(*x.shape[:-1], D // 2), scales.view(*x.shape[:-1], D // 32)
+
+
+def indexer_q_quant_fp4(q: torch.Tensor, weights: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``q [T, H, 128]`` bf16 -> (values uint8 [T, H, 64], scales int32 [T, H],
+    w fp32 [T, H] = weights * 128**-0.5 * 64**-0.5)."""
+    _check_dev(q, weights)
+    _bits16(q)
+    T, H, Dh = q.shape
+    _need(Dh == 128 and q.stride(2) == 1, "q must be [T, H, 128] with unit last stride")
+    _need(weights.shape[:2] == (T, H) and weights.stride(1) == 1, "weights [T, H]")
+    _need(weights.dtype in (torch.bfloat16, torch.float32), "weights bf16 or fp32")
+    values = torch.empty((T, H, 64), dtype=torch.uint8, device=q.device)
+    scales = torch.empty((T, H), dtype=torch.int32, device=q.device)
+    w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
+    _lib.call(
+        "ekv_indexer_q_quant_fp4", q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), _rs(weights), T, H, values.data_ptr(), scales.data_ptr(),
+        w_out.data_ptr(), _stream(),
+    )
+    return values, scales, w_out
+
+
+def indexer_k_insert_fp4(k: torch.Tensor, slot_mapping: torch.Tensor, kcache: torch.Tensor) -> None:
+    """Indexer K rows ``[T, 128]`` bf16 -> 68-byte MXFP4 rows in ``kcache``."""
+    _check_dev(k, slot_mapping, kcache)
+    _bits16(k)
+    _need(k.shape[1] == INDEX_HEAD_DIM and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
+    _need(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
+    _lib.call(
+        "ekv_indexer_k_insert_fp4", k.data_ptr(), _rs(k), k.shape[0], slot_mapping.data_ptr(),
+        kcache.data_ptr(), _rs(kcache), kcache.shape[0], _stream(),
+    )
+
+
+def indexer_store_fp4(values: torch.Tensor, scales: torch.Tensor, slot_mapping: torch.Tensor,
+                      kcache: torch.Tensor) -> None:
+    """``_store_indexer_fp4``: quantized rows (values ``[T, 64]``, scales
+    ``[T, 4]`` uint8) to their slots in ``kcache``."""
+    _check_dev(values, scales, slot_mapping, kcache)
+    _need(values.dtype == torch.uint8 and values.shape[1] == 64 and values.stride(1) == 1, "values uint8 [T, 64]")
+    _need(scales.dtype == torch.uint8 and scales.shape[1] == 4 and scales.stride(1) == 1, "scales uint8 [T, 4]")
+    _need(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
+    _lib.call(
+        "ekv_indexer_store_fp4", values.data_ptr(), _rs(values), scales.data_ptr(), _rs(scales), values.shape[0],
+        slot_mapping.data_ptr(), kcache.data_ptr(), _rs(kcache), kcache.shape[0], _stream(),
+    )
+
+
+def _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths):
+    _check_dev(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    T = q_values.shape[0]
+    _need(q_values.shape == (T, 64, 64) and q_values.dtype == torch.uint8 and q_values.is_contiguous(),
+          "q_values uint8 [T, 64, 64]")
+    _need(q_scales.shape == (T, 64) and q_scales.dtype == torch.int32 and q_scales.is_contiguous(),
+          "q_scales int32 [T, 64]")
+    _need(w.shape == (T, 64) and w.dtype == torch.float32 and w.is_contiguous(), "w fp32 [T, 64]")
+    _need(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table int32")
+    _need(lengths.dtype == torch.int32 and req_ids.dtype == torch.int32, "lengths/req_ids int32")
+    return T
+
+
+def indexer_score_fp4(q_values, q_scales, w, kcache, block_table, req_ids, lengths, max_len: int,
+                      scores: torch.Tensor) -> None:
+    """Exact MXFP4 indexer scores of every token ``s < lengths[t]``."""
+    T = _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    _check_dev(scores)
+    _need(scores.dtype == torch.float32 and scores.stride(1) == 1 and scores.shape[1] >= max_len, "scores")
+    _lib.call(
+        "ekv_indexer_score_fp4", q_values.data_ptr(), q_scales.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), scores.data_ptr(), _rs(scores), _stream(),
+    )
+
+
+def indexer_filter_fp4(q_values, q_scales, w, kcache, block_table, req_ids, lengths, max_len: int,
+                       workspace: torch.Tensor, k: int = 2048) -> None:
+    """Stage 1 of the MXFP4 top-k (as ``indexer_filter``)."""
+    T = _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    _lib.call(
+        "ekv_indexer_filter_fp4", q_values.data_ptr(), q_scales.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), int(k), workspace.data_ptr(), workspace.numel(), _stream(),
+    )
+
+
+def indexer_select_fp4(q_values, q_scales, w, kcache, block_table, req_ids, lengths, max_len: int,
+                       topk_out: torch.Tensor, workspace: torch.Tensor, merged: torch.Tensor | None = None,
+                       positions: torch.Tensor | None = None, window: int = 128, merged_slots: bool = False) -> None:
+    """Stage 2 of the MXFP4 top-k (as ``indexer_select``)."""
+    T = _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    m_ptr, m_stride, m_width, p_ptr = 0, 0, 0, 0
+    if merged is not None:
+        _need(positions is not None, "merged output needs positions")
+        _check_dev(merged, positions)
+        _need(merged.dtype == torch.int32 and merged.stride(1) == 1 and merged.shape[0] == T, "merged int32 [T, W]")
+        _need(positions.dtype == torch.int64 and positions.shape[0] == T, "positions int64 [T]")
+        _need(merged.shape[1] >= topk_out.shape[1] + window, "merged width must be >= k + window")
+        m_ptr, m_stride, m_width, p_ptr = merged.data_ptr(), _rs(merged), merged.shape[1], positions.data_ptr()
+    _lib.call(
+        "ekv_indexer_select_fp4", q_values.data_ptr(), q_scales.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1],
+        workspace.data_ptr(), workspace.numel(), m_ptr, m_stride, m_width, p_ptr, int(window),
+        int(bool(merged_slots)), _stream(),
+    )
+
+
+def indexer_topk_fp4(q_values, q_scales, w, kcache, block_table, req_ids, lengths, max_len: int,
+                     topk_out: torch.Tensor, workspace: torch.Tensor | None = None) -> None:
+    """Exact MXFP4 top-k over ``s < lengths[t]``, ascending, -1 padded."""
+    T = _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    if workspace is None:
+        workspace = indexer_topk_workspace(T, max_len, q_values.device)
+    _lib.call(
+        "ekv_indexer_topk_fp4", q_values.data_ptr(), q_scales.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1],
+        workspace.data_ptr(), workspace.numel(), _stream(),
+    )
+
+
+def indexer_filter_dots_fp4(q_values: torch.Tensor, q_scales: torch.Tensor, k_values: torch.Tensor,
+                            k_scales: torch.Tensor) -> torch.Tensor:
+    """The MXFP4 filter's MFMA dot products ``[S, 64]`` (a diagnostic of its
+    error bound): q ``[64, 64]`` uint8 + ``[64]`` int32, k ``[S, 64]`` + ``[S]``."""
+    _check_dev(q_values, q_scales, k_values, k_scales)
+    _need(q_values.shape == (64, 64) and q_values.dtype == torch.uint8 and q_values.is_contiguous(), "q_values [64, 64]")
+    _need(q_scales.shape == (64,) and q_scales.dtype == torch.int32, "q_scales int32 [64]")
+    S = k_values.shape[0]
+    _need(k_values.shape == (S, 64) and k_values.dtype == torch.uint8 and k_values.is_contiguous(), "k_values [S, 64]")
+    _need(k_scales.shape == (S,) and k_scales.dtype == torch.int32, "k_scales int32 [S]")
+    _need(S % 16 == 0, "S must be a multiple of 16")
+    out = torch.empty((S, 64), dtype=torch.float32, device=k_values.device)
+    _lib.call("ekv_indexer_filter_dots_fp4", q_values.data_ptr(), q_scales.data_ptr(), k_values.data_ptr(),
+              k_scales.data_ptr(), S, out.data_ptr(), _stream())
+    return out
+
+
 # --------------------------------------------------------------------------- decode
 def decode_workspace(num_tokens: int, heads: int, width: int, device) -> torch.Tensor:
     """Workspace for every ``sparse_mla_decode`` call of at most ``num_tokens``
