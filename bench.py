@@ -63,7 +63,10 @@ def parse():
                    help="skip the HCA measurements (chunked-prefill write, decode step)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-mtp", action="store_true", help="skip the multi-token-prediction (1M-context) measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa"], default=None,
+    p.add_argument("--no-fp4", action="store_true", help="skip the MXFP4 indexer measurement")
+    p.add_argument("--no-prefill", action="store_true", help="skip the DSA prefill-chunk measurement")
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa", "indexer_fp4", "dsa_prefill"],
+                   default=None,
                    help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one plain device copy of this many MiB (a known-size kernel that calibrates "
@@ -192,6 +195,116 @@ def dsa_bytes(B: int, ctx: int) -> dict:
     gather = B * (min(n, 2048) + min(ctx, 128)) * 580
     qo = B * 64 * 576 * 2 + B * 64 * 512 * 2 + B * 64 * 128 * 2 + B * 64 * 2 + B * 64 * 4
     return {"indexer_k": k_read, "gather": gather, "q_out": qo, "total": k_read + gather + qo}
+
+
+# --------------------------------------------------------------------------- DSA prefill chunk
+def measure_dsa_prefill(torch, ops, seed: int, chunk: int = 4096, ctx: int = 32768, reps: int = 5) -> dict:
+    """A DSA layer's chunked-prefill step: `chunk` new tokens of one request
+    ending at `ctx`, each a query row -- prologue (indexer prep, K insert,
+    latent append, q quant, lengths), indexer top-k of every row (the
+    many-row filter / bound / verify kernels), select with merged rows, and
+    the sparse MLA over the rows' 2176 entries.  The indexer's work is
+    quadratic in the chunk: row t scores pos_t + 1 - 128 keys."""
+    st = build_dsa_decode(torch, ops, [ctx], seed, rows_per_seq=chunk, spike_frac=0.0)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for _ in range(2):
+        dsa_step(ops, st)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    filt = dec = 0.0
+    t0.record()
+    for _ in range(reps):
+        dsa_step(ops, st, ev)
+        torch.cuda.synchronize()
+        filt += ev[0].elapsed_time(ev[1])
+        dec += ev[2].elapsed_time(ev[3])
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    n = [max(p + 1 - 128, 0) for p in range(ctx - chunk, ctx)]
+    keys = sum(n)
+    flops = keys * 64 * 128 * 2
+    filt_ms = filt / reps
+    return {
+        "workload": f"dsa_prefill_chunk{chunk}_ctx{ctx}",
+        "ms": round(ms, 3), "tok_per_s": round(chunk / (ms * 1e-3), 1),
+        "indexer_filter_ms": round(filt_ms, 3), "decode_ms": round(dec / reps, 3),
+        "indexer_keys_scored": keys, "indexer_key_bytes": keys * 132,
+        "indexer_fp8_tflops": round(flops / (filt_ms * 1e-3) / 1e12, 1),
+        "indexer_mfma_frac": round(flops / (filt_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+        "what": "one request's prefill chunk as query rows through the DSA step (prologue, indexer filter, "
+                "select with merged rows, sparse MLA); the indexer filter is timed by events around its call",
+    }
+
+
+# --------------------------------------------------------------------------- MXFP4 indexer (use_fp4_kv)
+def measure_indexer_fp4(torch, ops, seed: int, B: int = 32, ctx: int = 131072, reps: int = 20,
+                        spike_frac: float = 0.05) -> dict:
+    """The indexer top-k with 68-byte MXFP4 key rows at the headline shape:
+    filter (scaled fp4 MFMA over every key row) + exact select with the
+    merged rows, from q already quantized; key bytes random e2m1 with scale
+    bytes 2^-8..2^-1 and 5% identical spike rows (exact ties)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + 4)
+    pps = (ctx + 63) // 64
+    num_pages = B * pps
+    block_table = torch.randperm(num_pages, device=dev, generator=g).to(torch.int32).view(B, pps)
+    vals = torch.randint(0, 256, (num_pages, 64 * 64), device=dev, dtype=torch.uint8, generator=g)
+    scl = torch.randint(119, 127, (num_pages, 64 * 4), device=dev, dtype=torch.uint8, generator=g)
+    if spike_frac > 0:
+        mask = torch.rand(num_pages, 64, device=dev, generator=g) < spike_frac
+        v3 = vals.view(num_pages, 64, 64)
+        v3[mask] = v3[0, 0].clone()
+        s3 = scl.view(num_pages, 64, 4)
+        s3[mask] = s3[0, 0].clone()
+    kcache = torch.cat([vals, scl], dim=1).contiguous()
+    del vals, scl
+    q = torch.randn(B, 64, 128, device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn(B, 64, device=dev, generator=g).to(torch.bfloat16)
+    qv, qs, wf = ops.indexer_q_quant_fp4(q, w)
+    req = torch.arange(B, dtype=torch.int32, device=dev)
+    positions = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
+    lengths = torch.full((B,), max(ctx - 128, 0), dtype=torch.int32, device=dev)
+    ws = ops.indexer_topk_workspace(B, ctx, dev)
+    topk = torch.empty((B, 2048), dtype=torch.int32, device=dev)
+    merged = torch.empty((B, 2176), dtype=torch.int32, device=dev)
+    common = (kcache, block_table, req, lengths, ctx)
+
+    def step(ev=None):
+        ops.indexer_filter_fp4(qv, qs, wf, *common, ws)
+        if ev is not None:
+            ev.record()
+        ops.indexer_select_fp4(qv, qs, wf, *common, topk, ws, merged=merged, positions=positions, window=128)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    mids = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    t0.record()
+    for i in range(reps):
+        starts[i].record()
+        step(mids[i])
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    filt_ms = sum(starts[i].elapsed_time(mids[i]) for i in range(reps)) / reps
+    n = max(ctx - 128, 0)
+    k_bytes = B * n * 68
+    timeouts = int(ws[:8].view(torch.int32).sum())
+    del kcache
+    return {
+        "workload": f"indexer_fp4_b{B}_ctx{ctx}",
+        "ms": round(ms, 4), "filter_ms": round(filt_ms, 4), "select_ms": round(ms - filt_ms, 4),
+        "key_bytes": k_bytes, "filter_GB/s": round(k_bytes / (filt_ms * 1e-3) / 1e9, 1),
+        "filter_frac": round(k_bytes / (filt_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "bound_timeouts": timeouts,
+        "what": "ekv_indexer_filter_fp4 + ekv_indexer_select_fp4 (merged rows) over 68-byte MXFP4 key rows, "
+                "q pre-quantized; filter_frac = key bytes / filter time / 8 TB/s",
+    }
 
 
 # --------------------------------------------------------------------------- HCA write (config 4)
@@ -752,7 +865,8 @@ def main():
             measure_dsa(torch, ops, args, line)
             print(json.dumps(line), flush=True)
             return
-        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp}[args.only]
+        leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp,
+               "indexer_fp4": measure_indexer_fp4, "dsa_prefill": measure_dsa_prefill}[args.only]
         print(json.dumps(leg(torch, ops, args.seed)), flush=True)
         return
     line = {"metric": METRIC}
@@ -779,6 +893,12 @@ def main():
     if not args.no_mtp:
         torch.cuda.empty_cache()
         line["mtp"] = measure_mtp(torch, ops, args.seed)
+    if not args.no_fp4:
+        torch.cuda.empty_cache()
+        line["indexer_fp4"] = measure_indexer_fp4(torch, ops, args.seed, B=args.batch, ctx=args.ctx)
+    if not args.no_prefill:
+        torch.cuda.empty_cache()
+        line["dsa_prefill"] = measure_dsa_prefill(torch, ops, args.seed)
     if cpu is not None:
         line["cpu_baseline"] = cpu["dsa"]
         if "hca_write" in line:

@@ -339,3 +339,103 @@ def test_indexer_metadata_builder_build(dev):
         base_build=lambda *a: A.IndexerMetadata(decode=A.IndexerDecode(seq_lens=cases[0].clone())))
     with pytest.raises(ValueError):
         small.build(0, None)
+
+
+@pytest.mark.parametrize("fp4", [False, True], ids=["fp8", "mxfp4"])
+def test_dsa_prefill_chunk_vs_oracle(dev, fp4):
+    """A chunked-prefill step through Ernie5_5DSAAttention._indexer_and_attn:
+    1100 prefill rows of one request (positions 2500..3599) beside a decode
+    row, so the indexer runs its many-row kernels (more rows than the fused
+    filter takes) in workspace pieces.  Every row's top-k equals the exact
+    path's (ekv_indexer_score[_fp4] + ekv_topk_select over the cache after
+    the step); sampled rows equal the oracle's top-k and decode output; the
+    per-row candidate counts equal the prefill chunk form of the metadata
+    (cu_seqlen_ke - cu_seqlen_ks after the builder's window rewrite,
+    attention.py:659-668); both caches' bytes equal the oracle's."""
+    from ernie_kv import attention as A
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(66)
+    case = _dsa_setup(dev, rng, [3600, 5000], [1100, 1], fp4=fp4)
+    T = case.T
+    topk_buf = torch.full((T, TOPK), -7, dtype=torch.int32, device=dev)
+    swa_buf = torch.full((T, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
+    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params,
+                                   use_fp4_kv=fp4)
+    layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
+    layer.mla_attn.kv_cache = to_dev(case.lat, dev)
+    captured = {}
+    orig = layer.mla_attn.impl._fp8_flash_mla_kernel
+
+    def spy(*args, **kwargs):
+        captured["out"] = orig(*args, **kwargs)
+        return captured["out"]
+
+    layer.mla_attn.impl._fp8_flash_mla_kernel = spy
+    inp = case.inputs
+    out = torch.zeros((T, 64 * 256), dtype=torch.bfloat16, device=dev)
+    meta = {layer.mla_attn.prefix: case.md, layer.indexer.k_cache.prefix: case.md}
+    pos_t = to_dev(case.positions, dev)
+    with A.set_forward_context(meta):
+        layer._indexer_and_attn(bf16_tensor(inp["hidden"], dev), bf16_tensor(inp["q_c"], dev), pos_t,
+                                bf16_tensor(inp["q"], dev), bf16_tensor(inp["kv_c"], dev),
+                                bf16_tensor(inp["k_pe"], dev), out)
+    torch.cuda.synchronize()
+    # the prefill chunk's metadata form: cu_seqlen_ks = start of each row's
+    # request in the flattened K, cu_seqlen_ke = ks + pos + 1, windowed by the builder
+    starts = np.array([0, 3600], np.int64)[case.req]
+    ks = torch.tensor(starts, dtype=torch.int32, device=dev)
+    ke = torch.tensor(starts + case.positions + 1, dtype=torch.int32, device=dev)
+    builder = A.Ernie5_5IndexerMetadataBuilder(
+        WINDOW, max_num_reqs=2, device=dev,
+        base_build=lambda *a: A.IndexerMetadata(prefill=A.IndexerPrefill(chunks=[A.IndexerPrefillChunk(ks, ke)])))
+    chunk = builder.build(0, None).prefill.chunks[0]
+    lengths = layer.indexer._lengths_buf(T, dev)
+    assert torch.equal((chunk.cu_seqlen_ke - chunk.cu_seqlen_ks).to(torch.int32), lengths)
+    # all rows: the exact path over the cache after the step
+    hid, qc = bf16_tensor(inp["hidden"], dev), bf16_tensor(inp["q_c"], dev)
+    iq, ik, iw = layer.indexer._project(hid, qc)
+    qp, kp = ops.indexer_prep(iq, ik, *layer.indexer._prep_args(dev), pos_t)
+    L = int(case.md.max_seq_len)
+    scores = torch.zeros((T, L), device=dev)
+    args = (layer.indexer.k_cache.kv_cache, case.md.block_table, case.md.req_ids, lengths, L)
+    if fp4:
+        qv, qs, wf = ops.indexer_q_quant_fp4(qp, iw)
+        ops.indexer_score_fp4(qv, qs, wf, *args, scores)
+    else:
+        q8, wf, dig = ops.indexer_q_quant(qp, iw)
+        ops.indexer_score(dig, wf, *args, scores)
+    ref_top = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    ops.topk_select(scores, lengths, TOPK, ref_top)
+    assert torch.equal(topk_buf[:T], ref_top), "top-k differs from the exact path"
+    top = topk_buf[:T].cpu().numpy()
+    merged_ref = merge_swa_topk(top, case.positions, TOPK + WINDOW, WINDOW)
+    assert np.array_equal(swa_buf[:T].cpu().numpy(), merged_ref), "merged rows differ"
+    # caches: the oracle's inserts and appends of all T rows
+    rq, rk = oi.indexer_prep(bf16_values(iq), bf16_values(ik), layer.indexer.k_norm_weight.cpu().numpy(),
+                             layer.indexer.k_norm_bias.cpu().numpy(), 1e-6,
+                             layer.indexer._prep_args(dev)[3][pos_t].cpu().numpy())
+    kc = case.kc.copy()
+    (om.k_insert if fp4 else oi.k_insert)(kc, rk, case.slot_mapping)
+    assert np.array_equal(layer.indexer.k_cache.kv_cache.cpu().numpy(), kc), "indexer K cache bytes differ"
+    lat = case.lat.copy()
+    rows = np.concatenate([inp["kv_c"], inp["k_pe"].reshape(T, 64)], axis=1)
+    codes, scale = quantize_rows(rows)
+    paged.write_fp8_rows(lat, case.slot_mapping, codes, scale, 576)
+    assert np.array_equal(layer.mla_attn.kv_cache.cpu().numpy(), lat), "latent cache bytes differ"
+    # sampled rows against the oracle: top-k and the sparse decode
+    sample = np.array([0, 1, 129, 700, 1098, 1099, 1100])
+    lens = oi.windowed_lengths(case.positions, WINDOW)
+    if fp4:
+        rv, rs, rw = om.quantize_q(rq[sample], bf16_values(iw)[sample])
+        otop, _ = om.indexer_topk(rv, rs, rw, kc, case.bt, case.req[sample], lens[sample], TOPK)
+    else:
+        codes_q, rw = oi.quantize_q(rq[sample], bf16_values(iw)[sample])
+        otop, _ = oi.indexer_topk(codes_q, rw, kc, case.bt, case.req[sample], lens[sample], TOPK)
+    assert np.array_equal(top[sample], otop), "sampled top-k rows differ from the oracle"
+    q_abs = bf16_values(layer.mla_attn.absorb_q(bf16_tensor(inp["q"], dev)))[sample]
+    glob = logical_to_global(merged_ref[sample], case.req[sample], case.bt)
+    ref_o, _ = od.sparse_mla_decode(q_abs, lambda s: od.gather_rows_fp8(lat, s, 576), glob, 256 ** -0.5, 512,
+                                    case.params["attn_sink"].cpu().numpy())
+    o_lat = bf16_values(captured["out"][0][:, 0])[sample]
+    _check_decode(o_lat, ref_o, "prefill rows' latent decode output")
