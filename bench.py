@@ -65,7 +65,9 @@ def parse():
     p.add_argument("--no-mtp", action="store_true", help="skip the multi-token-prediction (1M-context) measurement")
     p.add_argument("--no-fp4", action="store_true", help="skip the MXFP4 indexer measurement")
     p.add_argument("--no-prefill", action="store_true", help="skip the DSA prefill-chunk measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa", "indexer_fp4", "dsa_prefill"],
+    p.add_argument("--no-pages", action="store_true", help="skip the page-format transcoder measurement")
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa", "indexer_fp4", "dsa_prefill",
+                                      "pages"],
                    default=None,
                    help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -236,6 +238,36 @@ def measure_dsa_prefill(torch, ops, seed: int, chunk: int = 4096, ctx: int = 327
         "what": "one request's prefill chunk as query rows through the DSA step (prologue, indexer filter, "
                 "select with merged rows, sparse MLA); the indexer filter is timed by events around its call",
     }
+
+
+# --------------------------------------------------------------------------- upstream page format
+def measure_pages(torch, ops, seed: int, num_pages: int = 4096, reps: int = 20) -> dict:
+    """Export of `num_pages` latent pages (576-wide, 64 rows) to fp8_ds_mla
+    pages and import back: bytes read + written per call over its time."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + 5)
+    own = torch.randint(0, 126, (num_pages, 64 * 580), device=dev, dtype=torch.uint8, generator=g)
+    own[:, 64 * 576:] = torch.full((num_pages, 64), 2.0 ** -6, device=dev).view(torch.uint8)
+    ds = torch.zeros((num_pages, ops.ds_mla_page_stride()), dtype=torch.uint8, device=dev)
+    ids = torch.arange(num_pages, dtype=torch.int32, device=dev)
+    res = {}
+    for name, fn in (("export", lambda: ops.export_fp8_ds_mla_pages(own, ids, ds)),
+                     ("import", lambda: ops.import_fp8_ds_mla_pages(ds, ids, own))):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        nbytes = num_pages * 64 * (580 + 656)
+        res[name] = {"ms": round(ms, 4), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    res["workload"] = f"fp8_ds_mla_pages_{num_pages}"
+    res["what"] = "this library's 580-byte latent rows <-> fp8_ds_mla 656-byte rows, 64 rows per page"
+    return res
 
 
 # --------------------------------------------------------------------------- MXFP4 indexer (use_fp4_kv)
@@ -866,7 +898,8 @@ def main():
             print(json.dumps(line), flush=True)
             return
         leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp,
-               "indexer_fp4": measure_indexer_fp4, "dsa_prefill": measure_dsa_prefill}[args.only]
+               "indexer_fp4": measure_indexer_fp4, "dsa_prefill": measure_dsa_prefill,
+               "pages": measure_pages}[args.only]
         print(json.dumps(leg(torch, ops, args.seed)), flush=True)
         return
     line = {"metric": METRIC}
@@ -899,6 +932,9 @@ def main():
     if not args.no_prefill:
         torch.cuda.empty_cache()
         line["dsa_prefill"] = measure_dsa_prefill(torch, ops, args.seed)
+    if not args.no_pages:
+        torch.cuda.empty_cache()
+        line["pages"] = measure_pages(torch, ops, args.seed)
     if cpu is not None:
         line["cpu_baseline"] = cpu["dsa"]
         if "hca_write" in line:

@@ -480,6 +480,45 @@ int ekv_indexer_topk_fp4(const uint8_t* q_values, const int32_t* q_scales, const
 int ekv_indexer_filter_dots_fp4(const uint8_t* q_values, const int32_t* q_scales, const uint8_t* k_values,
                                 const int32_t* k_scales, int32_t num_keys, float* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Upstream page format at the KV-connector boundary.  fp8_ds_mla is the fp8
+ * KV dtype of vLLM's FlashMLA sparse backend, on which the reference's DSA
+ * layers run (nvidia/attention.py:551-558, 792-795): a 576-wide latent row is
+ * 656 bytes -- 512 e4m3fn codes (dims 0..511), 4 fp32 scales (scale t for
+ * dims 128t..128t+127), 64 bf16 values (dims 512..575) -- 64 token-major rows
+ * per page, page stride a multiple of the packed block alignment 9216
+ * (nvidia/attention.py:561-571), e.g. 46080.  This library's latent page is
+ * 64 rows of 576 codes, then 64 fp32 power-of-two row scales.  The indexer
+ * pages already have DeepGEMM's layout (values, then scales) and need no
+ * transcoding.  No reference function corresponds: the reference moves
+ * fp8_ds_mla blocks as they are; these let a connector move this library's
+ * pages in that format.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * Export: page src_pages[i] of `cache` (this library's 576-wide latent pages)
+ * -> page dst_pages[i] (i when dst_pages is NULL) of `out` in fp8_ds_mla.
+ * Lossless: codes 0..511 copied, the row scale in the four tile slots, dims
+ * 512..575 as exact bf16.  Page ids out of range are skipped.
+ */
+int ekv_export_fp8_ds_mla_pages(const uint8_t* cache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                                const int32_t* src_pages, int32_t n, uint8_t* out,
+                                int64_t out_page_stride /*bytes*/, int64_t out_num_pages,
+                                const int32_t* dst_pages, void* stream);
+
+/*
+ * Import: fp8_ds_mla page src_pages[i] of `src` -> page dst_pages[i] (i when
+ * NULL) of `cache`: each row dequantized in fp32 (code * tile scale, bf16 as
+ * is), then quantized as ekv_kv_append_quant does (one UE8M0 scale per row,
+ * round to nearest even).  Pages that ekv_export_fp8_ds_mla_pages wrote come
+ * back with the same values (the same bytes, except rows whose largest code is
+ * 224: half the scale, doubled codes).  Page ids out of range are skipped.
+ */
+int ekv_import_fp8_ds_mla_pages(const uint8_t* src, int64_t src_page_stride /*bytes*/, int64_t src_num_pages,
+                                const int32_t* src_pages, int32_t n, uint8_t* cache,
+                                int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* dst_pages,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "ekv_indexer_topk_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P]),
     "ekv_indexer_filter_dots_fp4": (I32, [P, P, P, P, I32, P, P]),
+    "ekv_export_fp8_ds_mla_pages": (I32, [P, I64, I64, P, I32, P, I64, I64, P, P]),
+    "ekv_import_fp8_ds_mla_pages": (I32, [P, I64, I64, P, I32, P, I64, I64, P, P]),
 }
 
 _lib = None

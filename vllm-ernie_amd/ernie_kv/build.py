@@ -45,6 +45,7 @@ SOURCES = {
     "ekv_decode.hip": [],
     "ekv_quant.hip": EXACT,
     "ekv_mxfp4.hip": EXACT,
+    "ekv_pages.hip": EXACT,
 }
 
 

@@ -662,6 +662,39 @@ def indexer_filter_dots_fp4(q_values: torch.Tensor, q_scales: torch.Tensor, k_va
     return out
 
 
+# --------------------------------------------------------------------------- upstream page format
+DS_MLA_ROW_BYTES = 656  # 512 fp8 + 4 fp32 tile scales + 64 bf16
+
+
+def ds_mla_page_stride() -> int:
+    """64 fp8_ds_mla rows rounded up to the packed block alignment (9216 B)."""
+    return -(-PAGE_TOKENS * DS_MLA_ROW_BYTES // 9216) * 9216
+
+
+def export_fp8_ds_mla_pages(cache: torch.Tensor, src_pages: torch.Tensor, out: torch.Tensor,
+                            dst_pages: torch.Tensor | None = None) -> None:
+    """This library's 576-wide latent pages ``src_pages`` of ``cache`` ->
+    fp8_ds_mla pages of ``out`` (``dst_pages``, default 0..n-1); lossless."""
+    _check_dev(cache, src_pages, out, dst_pages)
+    _need(src_pages.dtype == torch.int32 and (dst_pages is None or dst_pages.dtype == torch.int32),
+          "page ids must be int32")
+    _need(dst_pages is None or dst_pages.numel() == src_pages.numel(), "dst_pages must match src_pages")
+    _lib.call("ekv_export_fp8_ds_mla_pages", cache.data_ptr(), _rs(cache), cache.shape[0], src_pages.data_ptr(),
+              src_pages.numel(), out.data_ptr(), _rs(out), out.shape[0], _ptr(dst_pages), _stream())
+
+
+def import_fp8_ds_mla_pages(src: torch.Tensor, src_pages: torch.Tensor, cache: torch.Tensor,
+                            dst_pages: torch.Tensor | None = None) -> None:
+    """fp8_ds_mla pages ``src_pages`` of ``src`` -> this library's latent
+    pages of ``cache`` (``dst_pages``, default 0..n-1), requantized per row."""
+    _check_dev(src, src_pages, cache, dst_pages)
+    _need(src_pages.dtype == torch.int32 and (dst_pages is None or dst_pages.dtype == torch.int32),
+          "page ids must be int32")
+    _need(dst_pages is None or dst_pages.numel() == src_pages.numel(), "dst_pages must match src_pages")
+    _lib.call("ekv_import_fp8_ds_mla_pages", src.data_ptr(), _rs(src), src.shape[0], src_pages.data_ptr(),
+              src_pages.numel(), cache.data_ptr(), _rs(cache), cache.shape[0], _ptr(dst_pages), _stream())
+
+
 # --------------------------------------------------------------------------- decode
 def decode_workspace(num_tokens: int, heads: int, width: int, device) -> torch.Tensor:
     """Workspace for every ``sparse_mla_decode`` call of at most ``num_tokens``
