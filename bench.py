@@ -66,8 +66,8 @@ def parse():
     p.add_argument("--no-fp4", action="store_true", help="skip the MXFP4 indexer measurement")
     p.add_argument("--no-prefill", action="store_true", help="skip the DSA prefill-chunk measurement")
     p.add_argument("--no-pages", action="store_true", help="skip the page-format transcoder measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "mtp", "dsa", "indexer_fp4", "dsa_prefill",
-                                      "pages"],
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "hca_layer", "mtp", "dsa", "indexer_fp4",
+                                      "dsa_prefill", "pages"],
                    default=None,
                    help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -896,6 +896,10 @@ def main():
             line = {}
             measure_dsa(torch, ops, args, line)
             print(json.dumps(line), flush=True)
+            return
+        if args.only == "hca_layer":  # the HCA decode step at the headline batch and context
+            print(json.dumps(measure_hca_decode(torch, ops, args.seed, ctxs=[args.ctx] * args.batch,
+                                                label=f"hca_decode_b{args.batch}_ctx{args.ctx}")), flush=True)
             return
         leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp,
                "indexer_fp4": measure_indexer_fp4, "dsa_prefill": measure_dsa_prefill,

@@ -29,7 +29,9 @@ def _fp8_pool(rng, pages, dim, scale=1.0):
 def _check(out_t, lse_t, ref_o, ref_l, H):
     got = bf16_values(out_t)[:, :H].astype(np.float64)
     err = np.abs(got - ref_o)
-    bad = err > ATOL + RTOL * np.abs(ref_o)
+    allow = ATOL + RTOL * np.abs(ref_o)
+    print(f"decode worst error: {float((err / allow).max()):.3f} of the allowance, max abs {float(err.max()):.2e}")
+    bad = err > allow
     assert not bad.any(), f"max err {err.max()}; first miss at {np.argwhere(bad)[0]}"
     if lse_t is not None:
         gl = lse_t.cpu().numpy().astype(np.float64)
