@@ -439,3 +439,57 @@ def test_dsa_prefill_chunk_vs_oracle(dev, fp4):
                                     case.params["attn_sink"].cpu().numpy())
     o_lat = bf16_values(captured["out"][0][:, 0])[sample]
     _check_decode(o_lat, ref_o, "prefill rows' latent decode output")
+
+
+def test_dsa_indexer_and_attn_graph_replay(dev):
+    """Ernie5_5DSAAttention._indexer_and_attn captured in a HIP graph: the
+    layer's launches take fixed workspaces and never synchronize the host, so
+    each of three replays, with eager work and synchronizations between
+    them, equals the eager call bit for bit (the step rewrites the same
+    slots with the same rows, so it is idempotent)."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(67)
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    T = case.T
+    topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
+    swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
+    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params)
+    layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
+    layer.mla_attn.kv_cache = to_dev(case.lat, dev)
+    inp = {k: bf16_tensor(v, dev) for k, v in case.inputs.items()}
+    out = torch.zeros((T, 64 * 256), dtype=torch.bfloat16, device=dev)
+    meta = {layer.mla_attn.prefix: case.md, layer.indexer.k_cache.prefix: case.md}
+    pos_t = to_dev(case.positions, dev)
+
+    def step():
+        with A.set_forward_context(meta):
+            layer._indexer_and_attn(inp["hidden"], inp["q_c"], pos_t, inp["q"], inp["kv_c"], inp["k_pe"], out)
+
+    def state():
+        return [topk_buf[:T].clone(), swa_buf[:T].clone(), out.clone(), layer.indexer.k_cache.kv_cache.clone(),
+                layer.mla_attn.kv_cache.clone()]
+
+    step()
+    torch.cuda.synchronize()
+    ref = state()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for i in range(3):
+        topk_buf.fill_(-1)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        got = state()
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b), f"replay {i} differs from the eager call"
+        step()  # eager work between replays
+        torch.cuda.synchronize()

@@ -16,6 +16,8 @@
 // CPU oracle, so no multiply-add may be fused behind its back.
 #include "ekv_common.h"
 #include "ekv_internal.h"
+
+#include <algorithm>
 #include "ekv_rows.h"
 
 namespace ekv {
@@ -233,6 +235,9 @@ __global__ void windowed_lengths_kernel(const int64_t* positions, int32_t n, int
 // Window entries of positions at or after the first position of the row's
 // request in this call come from the call's own slots (call_slots, by the
 // request's qsl range) when call_slots is given, others from the ring.
+constexpr int kIdxPerThread = 4;
+constexpr int kIdxPerBlock = 256 * kIdxPerThread;
+
 __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
     const int64_t* positions, const int32_t* req_ids, const int32_t* comp_bt, int32_t comp_bt_stride,
     const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window, const int32_t* qsl,
@@ -245,23 +250,32 @@ __global__ void __launch_bounds__(256) hca_decode_indices_kernel(
   const int64_t nc = (p + 1) / kSpan;
   const int64_t w = min(p + 1, static_cast<int64_t>(window));
   const int64_t len = min(nc + w, static_cast<int64_t>(width));
-  for (int c = threadIdx.x; c < width; c += blockDim.x) {
-    int64_t v = -1;
+  // Workgroup (t, y) writes entries [kIdxPerBlock y, kIdxPerBlock (y + 1)) of
+  // row t, kIdxPerThread per thread with their table loads issued together.
+  int64_t v[kIdxPerThread];
+#pragma unroll
+  for (int j = 0; j < kIdxPerThread; ++j) {
+    const int c = static_cast<int>(blockIdx.y) * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
+    v[j] = -1;
     if (c < nc) {
-      v = static_cast<int64_t>(comp_bt[b * comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
+      v[j] = static_cast<int64_t>(comp_bt[b * comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
     } else if (c < len) {
       const int64_t pos = p - w + 1 + (c - nc);
       if (pos >= call_first) {
-        v = call_slots[t0 + (pos - call_first)];
-        v = v < 0 ? -1 : v;
+        const int64_t sv = call_slots[t0 + (pos - call_first)];
+        v[j] = sv < 0 ? -1 : sv;
       } else {
         const int64_t r = pos % ring;
-        v = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
+        v[j] = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
       }
     }
-    out[t * out_stride + c] = static_cast<int32_t>(v);
   }
-  if (threadIdx.x == 0) lengths[t] = static_cast<int32_t>(len);
+#pragma unroll
+  for (int j = 0; j < kIdxPerThread; ++j) {
+    const int c = static_cast<int>(blockIdx.y) * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
+    if (c < width) out[t * out_stride + c] = static_cast<int32_t>(v[j]);
+  }
+  if (blockIdx.y == 0 && threadIdx.x == 0) lengths[t] = static_cast<int32_t>(len);
 }
 
 // ---------------------------------------------------------------------------
@@ -530,7 +544,10 @@ extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* r
   EKV_CHECK(ring >= window && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
   EKV_CHECK((query_start_loc == nullptr) == (slot_mapping == nullptr),
             "query_start_loc and slot_mapping go together");
-  hipLaunchKernelGGL(hca_decode_indices_kernel, dim3(num_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
+  EKV_CHECK(width >= 0 && out_stride >= width, "out_stride must be >= width >= 0");
+  const dim3 grid(static_cast<unsigned>(num_tokens),
+                  static_cast<unsigned>(std::max(1, (width + kIdxPerBlock - 1) / kIdxPerBlock)));
+  hipLaunchKernelGGL(hca_decode_indices_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
                      positions, req_ids, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
                      window, query_start_loc, slot_mapping, out, out_stride, width, lengths);
   return ekv_launch_status();
