@@ -310,29 +310,65 @@ __device__ __forceinline__ void zero_masked(DecodeSmem<D, BF16>& sm, int u, int 
 // O^T[16 cb + 4 kg + i][head col] += V^T P^T over the tile's 32 entries for
 // the channel blocks [cb0, cb1): A = V^T from the image (transposing reads),
 // B = the P hi / lo operands.
+// This lane's V^T fragment of channel block cb (16 channels x the tile's 32
+// entries), read transposed from the row-major image: 8 fp8 bytes (in .x,
+// .y) or 8 bf16 values.
+template <int D, bool BF16>
+__device__ __forceinline__ uint4 pv_read(const uint8_t* img, int cb) {
+  const int lane = threadIdx.x & 63;
+  const int kg = lane >> 4, col = lane & 15;
+  if constexpr (BF16) {
+    // element m of read h: row slot_entry(kg, 4h + col / 4), channel 16 cb + 4 (col % 4)
+    const int ch = 16 * cb + 4 * (col & 3);
+    const int r0 = slot_entry(kg, col >> 2), r1 = slot_entry(kg, 4 + (col >> 2));
+    const i16x4 lo = lds_read_tr16(img + img_off<D, BF16>(r0, ch >> 3, (ch >> 2) & 1));
+    const i16x4 hi = lds_read_tr16(img + img_off<D, BF16>(r1, ch >> 3, (ch >> 2) & 1));
+    const i16x4 both[2] = {lo, hi};
+    return __builtin_bit_cast(uint4, both);
+  } else {
+    // byte m: row slot_entry(kg, m) at channel 16 cb + (lane j of the row group)
+    const int r = slot_entry(kg, col >> 1);
+    const uint2 w = lds_read_tr8(img + img_off<D, BF16>(r, cb, col & 1));
+    return make_uint4(w.x, w.y, 0u, 0u);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ bf16x8 pv_frag(const uint4& raw) {
+  if constexpr (BF16) return __builtin_bit_cast(bf16x8, raw);
+  else return fp8x8_bf16(make_uint2(raw.x, raw.y));
+}
+
+// O^T[16 cb .. ] += V^T P^T over channel blocks [kCb0, kCb1): the V^T
+// fragments of a group of kPvGroup blocks are read while the previous group
+// multiplies, and a group issues its lo products, then its hi products, so
+// the two MFMAs into one accumulator are kPvGroup issues apart.
+constexpr int kPvGroup = 4;
+
 template <int D, bool BF16, int kCb0, int kCb1>
 __device__ __forceinline__ void pv_tile(const uint8_t* img, const bf16x8& phi, const bf16x8& plo,
                                         f32x4 (&o)[kCb1 - kCb0]) {
-  const int lane = threadIdx.x & 63;
-  const int kg = lane >> 4, col = lane & 15;
+  constexpr int kN = kCb1 - kCb0, kG = kPvGroup;
+  static_assert(kN % kG == 0, "channel blocks must fill whole groups");
+  uint4 raw[2][kG];
 #pragma unroll
-  for (int cb = kCb0; cb < kCb1; ++cb) {
-    bf16x8 v;
-    if constexpr (BF16) {
-      // element m of read h: row slot_entry(kg, 4h + col / 4), channel 16 cb + 4 (col % 4)
-      const int ch = 16 * cb + 4 * (col & 3);
-      const int r0 = slot_entry(kg, col >> 2), r1 = slot_entry(kg, 4 + (col >> 2));
-      const i16x4 lo = lds_read_tr16(img + img_off<D, BF16>(r0, ch >> 3, (ch >> 2) & 1));
-      const i16x4 hi = lds_read_tr16(img + img_off<D, BF16>(r1, ch >> 3, (ch >> 2) & 1));
-      const i16x4 both[2] = {lo, hi};
-      v = __builtin_bit_cast(bf16x8, both);
-    } else {
-      // byte m: row slot_entry(kg, m) at channel 16 cb + (lane j of the row group)
-      const int r = slot_entry(kg, col >> 1);
-      v = fp8x8_bf16(lds_read_tr8(img + img_off<D, BF16>(r, cb, col & 1)));
+  for (int j = 0; j < kG; ++j) raw[0][j] = pv_read<D, BF16>(img, kCb0 + j);
+#pragma unroll
+  for (int g = 0; g < kN / kG; ++g) {
+    if (g + 1 < kN / kG) {
+#pragma unroll
+      for (int j = 0; j < kG; ++j) raw[(g + 1) & 1][j] = pv_read<D, BF16>(img, kCb0 + (g + 1) * kG + j);
     }
-    o[cb - kCb0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, plo, o[cb - kCb0], 0, 0, 0);
-    o[cb - kCb0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, phi, o[cb - kCb0], 0, 0, 0);
+    bf16x8 v[kG];
+#pragma unroll
+    for (int j = 0; j < kG; ++j) v[j] = pv_frag<BF16>(raw[g & 1][j]);
+#pragma unroll
+    for (int j = 0; j < kG; ++j)
+      o[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v[j], plo, o[g * kG + j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < kG; ++j)
+      o[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v[j], phi, o[g * kG + j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -470,18 +506,40 @@ sparse_decode_kernel(DecodeArgs a) {
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
           for (int c = 0; c < kChains; ++c) st[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // K fragments of entries col and 16 + col at K step ks, read kKPre
+        // steps ahead of their MFMAs; the steps are issued in order so an
+        // accumulator's consecutive MFMAs are 2 kChains issues apart
+        constexpr int kKPre = BF16 ? 2 : 4;  // bf16 fragments take twice the registers
+        uint4 kr[kKPre][BF16 ? 2 : 1];
+        auto k_read = [&](int ks, uint4 (&dst)[BF16 ? 2 : 1]) {
+          if constexpr (BF16) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+              dst[nt] = *reinterpret_cast<const uint4*>(img + img_off<D, BF16>(16 * nt + col, 4 * ks + kg, 0));
+          } else {
+            const uint2 a0 = *reinterpret_cast<const uint2*>(img + img_off<D, BF16>(col, 2 * ks + (kg >> 1), kg & 1));
+            const uint2 a1 =
+                *reinterpret_cast<const uint2*>(img + img_off<D, BF16>(16 + col, 2 * ks + (kg >> 1), kg & 1));
+            dst[0] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          }
+        };
+#pragma unroll
+        for (int p = 0; p < kKPre; ++p) k_read(p, kr[p]);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const int e = 16 * nt + col;
-            bf16x8 kf;
-            if constexpr (BF16)
-              kf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(img + img_off<D, BF16>(e, 4 * ks + kg, 0)));
-            else
-              kf = fp8x8_bf16(*reinterpret_cast<const uint2*>(img + img_off<D, BF16>(e, 2 * ks + (kg >> 1), kg & 1)));
-            st[nt][ks % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb[ks], st[nt][ks % kChains], 0, 0, 0);
+          bf16x8 kf[2];
+          if constexpr (BF16) {
+            kf[0] = __builtin_bit_cast(bf16x8, kr[ks % kKPre][0]);
+            kf[1] = __builtin_bit_cast(bf16x8, kr[ks % kKPre][1]);
+          } else {
+            kf[0] = fp8x8_bf16(make_uint2(kr[ks % kKPre][0].x, kr[ks % kKPre][0].y));
+            kf[1] = fp8x8_bf16(make_uint2(kr[ks % kKPre][0].z, kr[ks % kKPre][0].w));
           }
+          if (ks + kKPre < KS) k_read(ks + kKPre, kr[ks % kKPre]);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            st[nt][ks % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[nt], qb[ks], st[nt][ks % kChains], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
         }
         // this lane: head col, entries slot_entry(kg, m)
         const float4 k0 = *reinterpret_cast<const float4*>(&sm.kscale[tb + 4 * kg]);
