@@ -4,7 +4,8 @@
 lines 582-641: each output row is ``[topk[:n] | seq-w .. seq-1 | -1 ...]`` with
 ``seq = pos + 1``, ``n = min(max(seq - window, 0), topk)``, ``w = min(seq,
 window)``.  Pinned by the known-answer test ``test_dsa_backend.py:18-37``
-(transcribed in ``tests/test_oracle_merge.py``).
+(transcribed in ``tests/test_oracle_paths.py::test_merge_swa_topk_known_answer``
+and, on the GPU, ``tests/test_gpu_indexer.py::test_merge_swa_topk_known_answer``).
 
 The logical->global conversion is the paged-slot closed form applied to a
 request-local index (the FlashMLA fp8 path receives global indices and a dummy

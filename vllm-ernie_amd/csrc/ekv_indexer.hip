@@ -651,13 +651,17 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   __shared__ int s_maxn;
   const int tid = threadIdx.x;
   // Workgroup b runs on XCD b % 8 (round-robin dispatch).  Slot b / 8 of an
-  // XCD takes segment x = 8 (slot / T) + b % 8 of row slot % T: segments are
-  // spread over the XCDs, and the rows of one segment run back to back on one
-  // XCD, so rows of one sequence (draft-token rows) read the same pages there
-  // at about the same time and share them through its L2.
+  // XCD takes segment x = 8 (slot / T) + (b % 8 + seq) % 8 of row t = slot % T
+  // (seq its request): segments are spread over the XCDs, and the rows of one
+  // segment of a sequence run back to back on one XCD, so its draft-token rows
+  // read the same pages there at about the same time and share them through
+  // its L2.  The rotation by sequence spreads the last, partly active groups
+  // of segments of rows of equal length over the XCDs instead of piling them
+  // on the first ones.
   const int b = static_cast<int>(blockIdx.x);
   const int slot = b >> 3;
-  const int x = 8 * (slot / a.rows) + (b & 7), t = slot % a.rows;
+  const int t = slot % a.rows;
+  const int x = 8 * (slot / a.rows) + (((b & 7) + a.req_ids[t]) & 7);
   if (x >= a.groups) return;
   if (tid == 0) s_maxn = 0;
   __syncthreads();
