@@ -159,8 +159,10 @@ struct CompressLds {
 // lane l of it owns the 4 channels 64w + 4 (l % 16) + 0..3 of row group
 // l / 16.  Every kv_score element is read from memory once: the softmax is
 // an online one per (row group, channel), merged over the groups in order.
-// Every thread of the workgroup must call it (it synchronizes).
-template <int D>
+// Every thread of the workgroup must call it (it synchronizes).  kRingPipe:
+// spans that start in the state ring get the input path's load pipeline too
+// (at the cost of more registers).
+template <int D, bool kRingPipe>
 __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds<D>& ls, int b, int t0, int64_t p0,
                                               int64_t j, int st) {
   constexpr int kWaves = D / 64;
@@ -232,6 +234,58 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
       gate_chunk(sc, ap, g);
       __builtin_amdgcn_sched_barrier(0);
       if (step + 1 < kSteps) issue_gate(step + 1);  // into the score / ape registers just consumed
+      __builtin_amdgcn_sched_barrier(0);
+      if (step == 0) softmax_terms<true>(sm, g, kv[cur]);
+      else softmax_terms<false>(sm, g, kv[cur]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else if constexpr (kRingPipe) {
+    // The span's first rows precede this call: rows i < split64 come from
+    // the state ring, the others from the input.  Same arithmetic and the
+    // same pipeline as above (next chunk's kv rows in flight while a chunk is
+    // consumed, its score and ape rows issued once the gate values are
+    // formed), with per-lane row addresses: lane bases of row group grp in
+    // the ring (row i at ring + i * 2D) and in the input (row i at input +
+    // (i - split) * stride); a row before the call without a ring reads the
+    // call's first row and counts as 0.
+    const int split = static_cast<int>(split64);
+    const bool has_state = st >= 0 && st < a.num_state;
+    const uint16_t* ring = (has_state ? a.state + (static_cast<int64_t>(st) * kStateRing + (j & 1) * kSpan) * (2 * D)
+                                      : a.kv_score + t0 * a.kvs_stride - grp * (2 * D)) +
+                           grp * (2 * D) + c0;
+    const uint16_t* input = a.kv_score + (t0 - split + grp) * a.kvs_stride + c0;
+    auto load_row = [&](int i0, int col) -> uint2 {  // row i0 + grp, channels col + c0 ..
+      const bool from_ring = i0 + grp < split;
+      const uint16_t* r = from_ring ? ring + (has_state ? i0 * (2 * D) : 0) : input + i0 * a.kvs_stride;
+      const uint2 v = *reinterpret_cast<const uint2*>(r + col);
+      return (from_ring && !has_state) ? make_uint2(0, 0) : v;
+    };
+    constexpr int kSteps = kGroupRows / kChunk;
+    uint2 sc[kChunk], kv[2][kChunk];
+    float4 ap[kChunk];
+    auto issue_kv = [&](int step, uint2 (&k_)[kChunk]) {
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) k_[u] = load_row(kRowGroups * (step * kChunk + u), 0);
+    };
+    auto issue_gate = [&](int step) {
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int i0 = kRowGroups * (step * kChunk + u);
+        sc[u] = load_row(i0, D);
+        ap[u] = load_ape(i0);
+      }
+    };
+    issue_kv(0, kv[0]);
+    issue_gate(0);
+#pragma unroll
+    for (int step = 0; step < kSteps; ++step) {
+      const int cur = step & 1;
+      if (step + 1 < kSteps) issue_kv(step + 1, kv[cur ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      float g[kChunk][4];
+      gate_chunk(sc, ap, g);
+      __builtin_amdgcn_sched_barrier(0);
+      if (step + 1 < kSteps) issue_gate(step + 1);
       __builtin_amdgcn_sched_barrier(0);
       if (step == 0) softmax_terms<true>(sm, g, kv[cur]);
       else softmax_terms<false>(sm, g, kv[cur]);
@@ -350,7 +404,7 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
   const int64_t j = p0 / kSpan + blockIdx.x;
   if (j * kSpan + kSpan - 1 > p0 + n - 1) return;  // span not completed by this call
   if (j >= a.max_spans) return;
-  compress_span<D>(a, ls, b, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
+  compress_span<D, false>(a, ls, b, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
 }
 
 // Decode-sized HCA write (fewer than 128 new rows per sequence, so at most
@@ -359,9 +413,13 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
 // completes it, the rest run the append grid's blocks on their first 4
 // waves.  The two touch disjoint memory: the compressor reads this call's
 // inputs and state-ring rows of positions before the call, the append writes
-// this call's positions (rows, window ring, state ring).
+// this call's positions (rows, window ring, state ring).  Every span such a
+// call compresses starts in the state ring (all but its last rows precede the
+// call), so the ring path is pipelined here; one span per sequence leaves the
+// CUs lightly loaded, so the registers that takes cost no occupancy that
+// matters.
 template <int D>
-__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5)))
+__global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(4)))
 hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows) {
   __shared__ CompressLds<D> ls;
   const int block = static_cast<int>(blockIdx.x);
@@ -372,7 +430,7 @@ hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_bloc
     const int64_t p0 = c.positions[t0];
     const int64_t j = p0 / kSpan;
     if (j * kSpan + kSpan - 1 > p0 + n - 1 || j >= c.max_spans) return;  // no span completed by this call
-    compress_span<D>(c, ls, block, t0, p0, j, c.state_slot != nullptr ? c.state_slot[block] : -1);
+    compress_span<D, true>(c, ls, block, t0, p0, j, c.state_slot != nullptr ? c.state_slot[block] : -1);
     return;
   }
   if (threadIdx.x >= 256) return;  // the append's blocks are 4-wave; they use no workgroup barrier
