@@ -478,6 +478,7 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
         lse=torch.empty((T, 64), dtype=torch.float32, device=dev),
     )
     st["dec_ws"] = ops.decode_workspace(T, 64, width, dev)
+    st["write_ws"] = ops.hca_write_workspace(B, D, dev)
     return st
 
 
@@ -487,7 +488,7 @@ def hca_decode_step(ops, st):
     (compressed entries, then the window), then the 64-head decode."""
     ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["R"],
                   st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
-                  st["ring_pages"], st["ring"], st["pool"])
+                  st["ring_pages"], st["ring"], st["pool"], workspace=st["write_ws"])
     ops.hca_decode_indices(st["positions"], st["req"], st["comp_bt"], st["ring_pages"], st["ring"], st["idx"],
                            st["lens"])
     ops.sparse_mla_decode(st["q"], st["pool"], st["idx"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],

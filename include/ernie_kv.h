@@ -100,7 +100,12 @@ int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t
  * The whole HCA write of one step in one call: ekv_hca_compress followed by
  * ekv_hca_append with the same arguments, both on `stream` (same bytes in the
  * pool and the state ring).  comp_block_table must not be NULL; ring_pages /
- * state may be.  Replaces the cache-write half of
+ * state may be.  workspace (16-byte aligned, at least
+ * ekv_hca_write_workspace_size(num_seqs, dim) bytes, zero-filled once before
+ * its first use and left zero by every call) may be NULL; with it,
+ * decode-sized calls (max_query_len < 128) compress each completed span with
+ * four workgroups instead of one -- same bytes.  Calls that share a workspace
+ * must not overlap.  Replaces the cache-write half of
  * DeepseekV4Attention._prepare_and_attn_fn (nvidia/attention.py:494-505) with
  * its compressor call (Ernie5_5Compressor.forward, nvidia/attention.py:398-408).
  */
@@ -111,7 +116,11 @@ int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t*
                   const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
                   const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
                   int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride /*bytes*/,
-                  int64_t num_pages, void* stream);
+                  int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of ekv_hca_write's workspace for up to num_seqs sequences of width
+ * dim (no counterpart in the reference, whose compressor is unfused). */
+int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim);
 
 /*
  * HCA decode index rows: [compressed slots 0..n_c-1 | window slots of

@@ -56,9 +56,11 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
     d = lambda a: to_dev(a, dev)  # noqa: E731
     kvs_t = bf16_tensor(kv_score, dev)
     if fused:
+        if fused == "ws" and "ws" not in gpu:  # decode-sized calls split each span over four workgroups
+            gpu["ws"] = ops.hca_write_workspace(case.B, D, dev)
         ops.hca_write(bf16_tensor(latent, dev), kvs_t, d(slots), d(positions), d(token_seq), d(qsl), int(max(counts)),
                       gpu["state"], d(case.state_slot), d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin),
-                      d(case.comp_bt), d(case.ring_pages), case.ring, gpu["pool"])
+                      d(case.comp_bt), d(case.ring_pages), case.ring, gpu["pool"], workspace=gpu.get("ws"))
         return
     ops.hca_compress(kvs_t, d(positions), d(qsl), int(max(counts)), gpu["state"], d(case.state_slot),
                      d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin), d(case.comp_bt), gpu["pool"])
@@ -67,7 +69,7 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
 
 
 @pytest.mark.parametrize("rope", ["plain", "yarn"])
-@pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
+@pytest.mark.parametrize("fused", [False, True, "ws"], ids=["compress+append", "hca_write", "hca_write+ws"])
 @pytest.mark.parametrize("dim", [576, 512])
 def test_hca_write_path_exact(dev, dim, fused, rope):
     rng = np.random.default_rng(dim)
@@ -91,10 +93,12 @@ def test_hca_write_path_exact(dev, dim, fused, rope):
         assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool), f"pool mismatch after call {starts}"
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
+        if "ws" in gpu:  # the arrival counters are left zero
+            assert int(gpu["ws"][:256].sum()) == 0
 
 
 @pytest.mark.parametrize("rope", ["plain", "yarn"])
-@pytest.mark.parametrize("fused", [False, True], ids=["compress+append", "hca_write"])
+@pytest.mark.parametrize("fused", [False, True, "ws"], ids=["compress+append", "hca_write", "hca_write+ws"])
 @pytest.mark.parametrize("dim", [576, 512])
 def test_hca_write_decode_completes_spans(dev, dim, fused, rope):
     """Calls of fewer than 128 rows per sequence (decode, drafts) that complete
@@ -118,6 +122,8 @@ def test_hca_write_decode_completes_spans(dev, dim, fused, rope):
         assert np.array_equal(gpu["pool"].cpu().numpy(), case.st.pool), f"pool mismatch after call {starts}"
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
+        if "ws" in gpu:  # the arrival counters are left zero
+            assert int(gpu["ws"][:256].sum()) == 0
 
 
 def test_hca_decode_indices(dev):
@@ -229,11 +235,12 @@ def test_hca_decode_step_graph_replay(dev):
     out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
     lse = torch.empty((B, H), dtype=torch.float32, device=dev)
     ws = ops.decode_workspace(B, H, width, dev)
+    write_ws = ops.hca_write_workspace(B, D, dev)
 
     def step():
         ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], 1,
                       st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], comp_bt,
-                      ring_pages, ring, pool)
+                      ring_pages, ring, pool, workspace=write_ws)
         ops.hca_decode_indices(st["positions"], st["token_seq"], comp_bt, ring_pages, ring, idx, lens)
         ops.sparse_mla_decode(st["q"], pool, idx, 256 ** -0.5, out, lse, sinks=st["sinks"], lengths=lens,
                               workspace=ws)

@@ -68,6 +68,11 @@ struct CompressArgs {
   uint8_t* pool;             // [num_pages, page_stride]
   int64_t page_stride;
   int64_t num_pages;
+  // Decode-sized writes with a workspace: a span's four channel quarters are
+  // compressed by four workgroups (null: one workgroup per span).
+  uint32_t* span_count;      // [B] arrivals per span (zero between calls)
+  float* span_x;             // [B, D] softmax results
+  float* span_part;          // [B, D/4] sums of squares per channel quad
 };
 
 // Third descriptor word of a raw (unswizzled, unformatted) buffer resource.
@@ -146,12 +151,39 @@ __device__ __forceinline__ void softmax_terms(SoftmaxState& s, const float (&g)[
   }
 }
 
+// softmax_terms for one channel (the same operations in the same order).
+template <bool kFirst>
+__device__ __forceinline__ void softmax_terms1(float& m, float& Z, float& N, const float (&g)[kChunk],
+                                               const float (&kv)[kChunk]) {
+  float mc = m;
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) mc = fmaxf(mc, g[u]);
+  if (kFirst) {
+    m = mc;
+  } else {
+    const bool mv = mc > m + kShiftSlack;
+    if (__builtin_amdgcn_ballot_w64(mv) != 0) {
+      const float r = exp_ekv(m - mc);
+      Z = mv ? Z * r : Z;
+      N = mv ? N * r : N;
+      m = mv ? mc : m;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kChunk; ++u) {
+    const float e = exp_ekv(g[u] - m);
+    Z = Z + e;
+    N = __builtin_fmaf(e, kv[u], N);
+  }
+}
+
 // Workgroup-shared scratch of compress_span.
 template <int D>
 struct CompressLds {
   __align__(16) float part[D / 4];
   float wmax[D / 64];
   float rn;
+  int last;
 };
 
 // Compress span j of sequence b (first row t0 at position p0, state slot st)
@@ -391,6 +423,164 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
+// compress_span split over four workgroups (decode-sized calls with a
+// workspace): workgroup k takes channels [k D/4, (k+1) D/4), one per lane --
+// wave w channels 16w .. 16w+15 of the quarter, lane l of row group l / 16 --
+// so each lane runs one channel's online softmax over its group's 32 rows
+// instead of four.  It writes its softmax results and its channel quads'
+// sums of squares to the workspace; the last of the four to arrive reads all
+// of them and finishes the row (RMSNorm with the sum in quad order, RoPE,
+// quant) as compress_span does: every operation on a channel, and the order
+// of the sums, is the same, so the bytes are too.  Every thread of the
+// workgroup must call it (it synchronizes).
+constexpr int kQuarters = 4;
+
+template <int D>
+__device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, CompressLds<D>& ls, int b, int k,
+                                                      int t0, int64_t p0, int64_t j, int st) {
+  constexpr int kCh = D / kQuarters;
+  static_assert(kCh == 16 * (D / 64), "a quarter is 16 channels per wave");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int grp = lane >> 4;
+  const int c = k * kCh + 16 * wave + (lane & 15);  // this lane's channel
+
+  // Row i of the span, as in compress_span: the input for i >= split, else
+  // the state ring (a row without one reads the call's first row and counts
+  // as 0).  Lane bases of row group grp; rows i0 + grp.
+  const int64_t split64 = p0 - j * kSpan;
+  const int split = static_cast<int>(split64 < 0 ? 0 : split64);
+  const bool has_state = st >= 0 && st < a.num_state;
+  const uint16_t* ring = (has_state ? a.state + (static_cast<int64_t>(st) * kStateRing + (j & 1) * kSpan) * (2 * D)
+                                    : a.kv_score + t0 * a.kvs_stride - grp * (2 * D)) +
+                         grp * (2 * D) + c;
+  const uint16_t* input = a.kv_score + (t0 - split64 + grp) * a.kvs_stride + c;
+  auto load_row = [&](int i0, int col) -> float {
+    const bool from_ring = i0 + grp < split;
+    const uint16_t* r = from_ring ? ring + (has_state ? i0 * (2 * D) : 0) : input + i0 * a.kvs_stride;
+    const uint32_t v = r[col];
+    return (from_ring && !has_state) ? 0.0f : __uint_as_float(v << 16);
+  };
+  const float* ape = a.ape + grp * D + c;
+  constexpr int kSteps = kGroupRows / kChunk;
+  float sc[kChunk], ap[kChunk], kv[2][kChunk];
+  auto issue_kv = [&](int step, float (&k_)[kChunk]) {
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) k_[u] = load_row(kRowGroups * (step * kChunk + u), 0);
+  };
+  auto issue_gate = [&](int step) {
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int i0 = kRowGroups * (step * kChunk + u);
+      sc[u] = load_row(i0, D);
+      ap[u] = ape[i0 * D];
+    }
+  };
+  float m = -INFINITY, Z = 0.0f, N = 0.0f;
+  issue_kv(0, kv[0]);
+  issue_gate(0);
+#pragma unroll
+  for (int step = 0; step < kSteps; ++step) {
+    const int cur = step & 1;
+    if (step + 1 < kSteps) issue_kv(step + 1, kv[cur ^ 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    float g[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) g[u] = sc[u] + ap[u];
+    __builtin_amdgcn_sched_barrier(0);
+    if (step + 1 < kSteps) issue_gate(step + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (step == 0) softmax_terms1<true>(m, Z, N, g, kv[cur]);
+    else softmax_terms1<false>(m, Z, N, g, kv[cur]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Merge the 4 row groups in order (lanes l, l+16, l+32, l+48).
+  float m_g[kRowGroups];
+#pragma unroll
+  for (int r = 0; r < kRowGroups; ++r) m_g[r] = __shfl(m, (lane & 15) + 16 * r);
+  float M = m_g[0];
+#pragma unroll
+  for (int r = 1; r < kRowGroups; ++r) M = fmaxf(M, m_g[r]);
+  float Zs = 0.0f, Ns = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kRowGroups; ++r) {
+    const float s = exp_ekv(m_g[r] - M);
+    Zs = __builtin_fmaf(__shfl(Z, (lane & 15) + 16 * r), s, Zs);
+    Ns = __builtin_fmaf(__shfl(N, (lane & 15) + 16 * r), s, Ns);
+  }
+  const float x = __fdiv_rn(Ns, Zs);
+  // the quad's sum of squares, channel 4q first (lanes 4q' .. 4q'+3 hold it)
+  const float x1 = __shfl_down(x, 1), x2 = __shfl_down(x, 2), x3 = __shfl_down(x, 3);
+  float part = 0.0f;
+  part = part + x * x;
+  part = part + x1 * x1;
+  part = part + x2 * x2;
+  part = part + x3 * x3;
+  if (grp == 0) {
+    __hip_atomic_store(a.span_x + static_cast<int64_t>(b) * D + c, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((c & 3) == 0)
+      __hip_atomic_store(a.span_part + static_cast<int64_t>(b) * (D / 4) + c / 4, part, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's results are out before it arrives
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(a.span_count + b, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    ls.last = (before + 1u == static_cast<uint32_t>(kQuarters)) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!ls.last) return;
+
+  // Last arriver: the row from all quarters, thread tid = channel tid.
+  if (tid == 0) __hip_atomic_store(a.span_count + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float xc = __hip_atomic_load(a.span_x + static_cast<int64_t>(b) * D + tid, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+  if (tid < D / 4)
+    ls.part[tid] = __hip_atomic_load(a.span_part + static_cast<int64_t>(b) * (D / 4) + tid, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (tid == 0) {
+    float S = 0.0f;
+    for (int q = 0; q < D / 4; q += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&ls.part[q]);
+      S = S + v.x; S = S + v.y; S = S + v.z; S = S + v.w;
+    }
+    const float ms = __fdiv_rn(S, static_cast<float>(D));
+    ls.rn = __fdiv_rn(1.0f, __fsqrt_rn(ms + a.eps));
+  }
+  __syncthreads();
+  const float rn = ls.rn;
+  float y = (xc * rn) * a.norm_w[tid];
+  const float yp = __shfl_xor(y, 1);  // the RoPE pair (channels 2i, 2i+1)
+  if (tid >= D - 64) {
+    const int pi = (tid - (D - 64)) / 2;
+    const float cz = a.cos_sin[j * 64 + pi], sz = a.cos_sin[j * 64 + 32 + pi];
+    const float x0 = (tid & 1) ? yp : y, x1v = (tid & 1) ? y : yp;
+    y = (tid & 1) ? x0 * sz + x1v * cz : x0 * cz - x1v * sz;
+  }
+  float amax = wave_max_xor(fabsf(y), 64);
+  if (lane == 0) ls.wmax[wave] = amax;
+  __syncthreads();
+  amax = ls.wmax[0];
+#pragma unroll
+  for (int wv = 1; wv < D / 64; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
+  const int e = ue8m0_exponent(amax);
+  const float inv = exp2i(-e);
+  const int64_t slot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
+                           kPageTokens + j % kPageTokens;
+  const float y1 = __shfl_down(y, 1), y2 = __shfl_down(y, 2), y3 = __shfl_down(y, 3);
+  if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
+  uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
+  const int64_t off = slot % kPageTokens;
+  if ((tid & 3) == 0) {
+    const uint32_t lo = f32x2_to_fp8(y * inv, y1 * inv);
+    const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
+    *reinterpret_cast<uint32_t*>(page + off * D + tid) = lo | (hi << 16);
+  }
+  if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
+}
+
 // One workgroup per (span slot, sequence): span p0 / 128 + blockIdx.x of
 // sequence blockIdx.y, when this call completes it.
 template <int D>
@@ -423,18 +613,23 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(4)))
 hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows) {
   __shared__ CompressLds<D> ls;
   const int block = static_cast<int>(blockIdx.x);
-  if (block < num_seqs) {
-    const int t0 = c.qsl[block];
-    const int n = c.qsl[block + 1] - t0;
+  const bool quarters = c.span_count != nullptr;
+  const int compress_blocks = quarters ? kQuarters * num_seqs : num_seqs;
+  if (block < compress_blocks) {
+    const int seq = quarters ? block / kQuarters : block;
+    const int t0 = c.qsl[seq];
+    const int n = c.qsl[seq + 1] - t0;
     if (n <= 0) return;
     const int64_t p0 = c.positions[t0];
     const int64_t j = p0 / kSpan;
     if (j * kSpan + kSpan - 1 > p0 + n - 1 || j >= c.max_spans) return;  // no span completed by this call
-    compress_span<D, true>(c, ls, block, t0, p0, j, c.state_slot != nullptr ? c.state_slot[block] : -1);
+    const int st = c.state_slot != nullptr ? c.state_slot[seq] : -1;
+    if (quarters) compress_span_quarter<D>(c, ls, seq, block % kQuarters, t0, p0, j, st);
+    else compress_span<D, true>(c, ls, seq, t0, p0, j, st);
     return;
   }
   if (threadIdx.x >= 256) return;  // the append's blocks are 4-wave; they use no workgroup barrier
-  hca_append_block<D>(a, block - num_seqs, main_blocks, tail_rows);
+  hca_append_block<D>(a, block - compress_blocks, main_blocks, tail_rows);
 }
 
 }  // namespace ekv
@@ -459,8 +654,15 @@ int hca_compress_args(CompressArgs& a, const uint16_t* kv_score, int64_t kvs_str
                 (state == nullptr || aligned8(state)),
             "misaligned buffers");
   a = CompressArgs{kv_score, kvs_stride, positions, qsl, state, state_slot, num_state, ape, norm_w, eps,
-                   cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride, num_pages};
+                   cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride, num_pages,
+                   nullptr, nullptr, nullptr};
   return 0;
+}
+
+// ekv_hca_write workspace: arrival counters u32 [B] (zero between calls),
+// padded to 256 bytes | softmax results f32 [B, D] | quad sums f32 [B, D/4].
+int64_t hca_write_ws_bytes(int64_t num_seqs, int64_t dim) {
+  return ((num_seqs * 4 + 255) / 256) * 256 + num_seqs * (dim + dim / 4) * 4;
 }
 
 }  // namespace
@@ -487,6 +689,10 @@ extern "C" int ekv_hca_compress(const uint16_t* kv_score, int64_t kvs_stride, co
   return ekv_launch_status();
 }
 
+extern "C" int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim) {
+  return num_seqs > 0 && dim > 0 ? hca_write_ws_bytes(num_seqs, dim) : 0;
+}
+
 extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
                              int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
                              const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
@@ -495,7 +701,7 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
                              const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
                              const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
                              int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride,
-                             int64_t num_pages, void* stream) {
+                             int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream) {
   EKV_CHECK(num_tokens >= 0 && num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
   if (num_tokens == 0 || num_seqs == 0) return 0;
   CompressArgs c;
@@ -503,6 +709,14 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
                              norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride,
                              num_pages);
   if (rc) return rc;
+  if (workspace != nullptr) {
+    EKV_CHECK(workspace_bytes >= hca_write_ws_bytes(num_seqs, dim) && aligned16(workspace),
+              "workspace too small (ekv_hca_write_workspace_size) or misaligned");
+    uint8_t* w = static_cast<uint8_t*>(workspace);
+    c.span_count = reinterpret_cast<uint32_t*>(w);
+    c.span_x = reinterpret_cast<float*>(w + ((int64_t{num_seqs} * 4 + 255) / 256) * 256);
+    c.span_part = c.span_x + int64_t{num_seqs} * dim;
+  }
   AppendArgs ap;
   rc = hca_append_args(ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
                        token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages, ring_stride, ring, state,
@@ -511,7 +725,8 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (max_query_len < kSpan) {  // decode-sized: compress and append in one launch
     int main_blocks = 0, tail_rows = 0;
-    const int64_t blocks = num_seqs + hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
+    const int64_t compress_blocks = (c.span_count ? int64_t{kQuarters} : int64_t{1}) * num_seqs;
+    const int64_t blocks = compress_blocks + hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
     EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
     const dim3 grid(static_cast<uint32_t>(blocks));
     if (dim == 512)

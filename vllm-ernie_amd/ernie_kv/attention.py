@@ -686,6 +686,16 @@ class Ernie5_5HCAAttentionMixin:
         self.state_cache: torch.Tensor | None = None  # bf16 [num_state, 256, 2 D]
         self._idx: torch.Tensor | None = None
         self._ws: torch.Tensor | None = None
+        self._write_ws: torch.Tensor | None = None
+        self._write_seqs = 0
+
+    def _write_workspace(self, num_seqs: int, D: int, device) -> torch.Tensor:
+        """The cache write's workspace (decode-sized calls compress a span
+        with four workgroups), grown to the widest batch seen."""
+        if self._write_ws is None or self._write_seqs < num_seqs:
+            self._write_seqs = max(num_seqs, 2 * self._write_seqs)
+            self._write_ws = ops.hca_write_workspace(self._write_seqs, D, device)
+        return self._write_ws
 
     def _buffers(self, T: int, width: int, device):
         if self._idx is None or self._idx.shape[0] < T or self._idx.shape[1] < width:
@@ -705,7 +715,8 @@ class Ernie5_5HCAAttentionMixin:
         late_ring = md.max_query_len > self.ring - self.window
         ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc, md.max_query_len,
                       self.state_cache, md.state_slot, self.ape, self.norm_w, self.norm_eps, self.compress_cos_sin,
-                      md.comp_block_table, None if late_ring else md.ring_pages, self.ring, self.kv_cache)
+                      md.comp_block_table, None if late_ring else md.ring_pages, self.ring, self.kv_cache,
+                      workspace=self._write_workspace(md.query_start_loc.numel() - 1, D, q.device))
         width = md.max_seq_len // 128 + self.window
         idx, lens, lse, ws = self._buffers(T, width, q.device)
         ops.hca_decode_indices(positions, md.token_seq, md.comp_block_table, md.ring_pages, self.ring, idx, lens,

@@ -160,11 +160,13 @@ def hca_write(
     ring_pages: torch.Tensor | None,
     ring: int,
     pool: torch.Tensor,
+    workspace: torch.Tensor | None = None,
 ) -> None:
     """``hca_compress`` then ``hca_append`` (same arguments, same result) in
-    one call."""
+    one call.  With ``workspace`` (``hca_write_workspace``) decode-sized calls
+    compress each completed span with four workgroups (same bytes)."""
     _check_dev(latent, kv_score, slot_mapping, positions, token_seq, qsl, state, state_slot, ape, norm_w, cos_sin,
-               comp_block_table, ring_pages, pool)
+               comp_block_table, ring_pages, pool, workspace)
     _bits16(latent)
     _bits16(kv_score)
     T, D = latent.shape
@@ -181,6 +183,8 @@ def hca_write(
     if state is not None:
         _bits16(state)
         _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
+    if workspace is not None:
+        _need(workspace.dtype == torch.uint8 and workspace.is_contiguous(), "workspace: a uint8 hca_write_workspace")
     _lib.call(
         "ekv_hca_write", latent.data_ptr(), _rs(latent), kv_score.data_ptr(), _rs(kv_score), T, D,
         slot_mapping.data_ptr(), positions.data_ptr(), token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1,
@@ -188,8 +192,15 @@ def hca_write(
         ape.data_ptr(), norm_w.data_ptr(), float(eps), cos_sin.data_ptr(), cos_sin.shape[0],
         comp_block_table.data_ptr(), _rs(comp_block_table), _ptr(ring_pages),
         0 if ring_pages is None else _rs(ring_pages), int(ring), pool.data_ptr(), _rs(pool), pool.shape[0],
-        _stream(),
+        _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream(),
     )
+
+
+def hca_write_workspace(num_seqs: int, dim: int, device) -> torch.Tensor:
+    """Zero-filled workspace of ``hca_write`` for up to ``num_seqs`` sequences
+    of width ``dim`` (every call leaves it zero again)."""
+    n = int(_lib.load().ekv_hca_write_workspace_size(int(num_seqs), int(dim)))
+    return torch.zeros(max(n, 16), dtype=torch.uint8, device=device)
 
 
 def hca_decode_indices(
