@@ -484,13 +484,13 @@ def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx
 
 def hca_decode_step(ops, st):
     """One HCA decode step: the new token's write (latent row, window ring,
-    state ring; the spans it completes are compressed), its index rows
-    (compressed entries, then the window), then the 64-head decode."""
-    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["R"],
-                  st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
-                  st["ring_pages"], st["ring"], st["pool"], workspace=st["write_ws"])
-    ops.hca_decode_indices(st["positions"], st["req"], st["comp_bt"], st["ring_pages"], st["ring"], st["idx"],
-                           st["lens"])
+    state ring; the spans it completes are compressed) and its index rows
+    (compressed entries, then the window) in one launch, then the 64-head
+    decode."""
+    ops.hca_write_step(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"],
+                       st["R"], st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"],
+                       st["comp_bt"], st["ring_pages"], st["ring"], st["pool"], 128, st["idx"], st["lens"],
+                       workspace=st["write_ws"])
     ops.sparse_mla_decode(st["q"], st["pool"], st["idx"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
                           lengths=st["lens"], workspace=st["dec_ws"])
 
@@ -551,8 +551,8 @@ def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None 
     workload = label or f"hca_decode_b{st['B']}_ctx8192-131072"
     return {
         "workload": workload,
-        "kernels": "hca_write_small_kernel<576> (the new tokens' rows, ring, state; spans they complete) + "
-                   "hca_decode_indices_kernel + sparse_decode_kernel<576> + decode_combine_kernel",
+        "kernels": "hca_write_small_kernel<576> (the new tokens' rows, ring, state; spans they complete; the "
+                   "index rows) + sparse_decode_kernel<576> + decode_combine_kernel",
         "ms": round(ms, 4),
         "ms_eager": round(ms_eager, 4),
         "launch": "hip_graph: one captured step replayed (ms); ms_eager = the same step launched eagerly",

@@ -123,6 +123,24 @@ int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t*
 int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim);
 
 /*
+ * ekv_hca_write followed by ekv_hca_decode_indices of the same tokens
+ * (req_ids = token_seq, query_start_loc = qsl, slot_mapping = the call's
+ * slots, the given ring_pages) with the same results; decode-sized calls
+ * (max_query_len < 128) build the index rows in the write's launch.  The
+ * cache-write and index halves of DeepseekV4Attention._prepare_and_attn_fn
+ * (nvidia/attention.py:471-539) in one call.
+ */
+int ekv_hca_write_step(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score, int64_t kvs_stride,
+                       int32_t num_tokens, int32_t dim, const int64_t* slot_mapping, const int64_t* positions,
+                       const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs, int32_t max_query_len,
+                       uint16_t* state, const int32_t* state_slot, int32_t num_state, const float* ape,
+                       const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                       const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                       int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride /*bytes*/,
+                       int64_t num_pages, void* workspace, int64_t workspace_bytes, int32_t window,
+                       int32_t* idx_out, int64_t idx_stride, int32_t width, int32_t* lengths, void* stream);
+
+/*
  * HCA decode index rows: [compressed slots 0..n_c-1 | window slots of
  * positions p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window),
  * and the row lengths.  Window slots are ring slots; with query_start_loc

@@ -271,3 +271,61 @@ def test_hca_decode_step_graph_replay(dev):
         for name, a_, b_ in zip(["pool", "state", "idx", "lens", "out", "lse"], got, want):
             assert torch.equal(a_.view(torch.uint8) if a_.dtype == torch.bfloat16 else a_,
                                b_.view(torch.uint8) if b_.dtype == torch.bfloat16 else b_), f"replay {rep}: {name}"
+
+
+@pytest.mark.parametrize("rows", [1, 3, 130], ids=["decode", "drafts", "prefill-sized"])
+@pytest.mark.parametrize("use_ws", [False, True], ids=["no-ws", "ws"])
+def test_hca_write_step_matches_separate_calls(dev, rows, use_ws):
+    """ekv_hca_write_step (the write and the step's index rows, one launch for
+    decode-sized calls) leaves the same pool, state ring, index rows and
+    lengths as ekv_hca_write followed by ekv_hca_decode_indices with the
+    call's slots."""
+    from ernie_kv import ops
+
+    g = torch.Generator(device=dev).manual_seed(17 + rows)
+    B, D, ring, window = 4, 576, 192, 128
+    ctx = torch.tensor([300, 1024, 777, 2048], dtype=torch.int64)  # the call's last positions are ctx - 1
+    spans = int(ctx.max()) // 128 + 2
+    comp_pp, ring_pp = (spans + 63) // 64, ring // 64
+    lat_pp = (int(ctx.max()) + 63) // 64
+    pages = B * (comp_pp + ring_pp + lat_pp)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    comp_bt = perm[: B * comp_pp].view(B, comp_pp).to(dev)
+    ring_pages = perm[B * comp_pp: B * (comp_pp + ring_pp)].view(B, ring_pp).to(dev)
+    lat_bt = perm[B * (comp_pp + ring_pp):].view(B, lat_pp).to(torch.int64)
+    pos = torch.cat([torch.arange(int(c) - rows, int(c)) for c in ctx])
+    seq = torch.arange(B).repeat_interleave(rows)
+    slots = lat_bt[seq, pos // 64] * 64 + pos % 64
+    T = B * rows
+    rnd = lambda *s: torch.randn(*s, device=dev, generator=g).to(torch.bfloat16)  # noqa: E731
+    ang = (torch.arange(spans, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    args = dict(latent=rnd(T, D), kv_score=rnd(T, 2 * D), slot_mapping=slots.to(dev), positions=pos.to(dev),
+                token_seq=seq.to(torch.int32).to(dev),
+                qsl=(torch.arange(B + 1, dtype=torch.int32) * rows).to(dev), max_query_len=rows,
+                state_slot=torch.arange(B, dtype=torch.int32, device=dev),
+                ape=(0.5 * torch.randn(128, D, device=dev, generator=g)).contiguous(),
+                norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=g)).contiguous(), eps=1e-6,
+                cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], 1).to(torch.float32).to(dev),
+                comp_block_table=comp_bt, ring_pages=ring_pages, ring=ring)
+    state0 = rnd(B, 256, 2 * D)
+    pool0 = torch.randint(0, 256, (pages, paged.fp8_page_bytes(D)), device=dev, dtype=torch.uint8, generator=g)
+    width = int(ctx.max()) // 128 + window
+    outs = []
+    for fused in (False, True):
+        pool, state = pool0.clone(), state0.clone()
+        idx = torch.full((T, width), -7, dtype=torch.int32, device=dev)
+        lens = torch.zeros(T, dtype=torch.int32, device=dev)
+        ws = ops.hca_write_workspace(B, D, dev) if use_ws else None
+        if fused:
+            ops.hca_write_step(pool=pool, state=state, window=window, out=idx, lengths=lens, workspace=ws, **args)
+        else:
+            ops.hca_write(pool=pool, state=state, workspace=ws, **args)
+            ops.hca_decode_indices(args["positions"], args["token_seq"], comp_bt, ring_pages, ring, idx, lens, window,
+                                   query_start_loc=args["qsl"], slot_mapping=args["slot_mapping"])
+        torch.cuda.synchronize()
+        outs.append((pool, state.view(torch.int16), idx, lens))
+        if ws is not None:
+            assert int(ws[:256].sum()) == 0
+    for name, a_, b_ in zip(["pool", "state", "idx", "lens"], *outs):
+        assert torch.equal(a_, b_), name

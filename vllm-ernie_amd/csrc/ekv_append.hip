@@ -232,50 +232,8 @@ __global__ void windowed_lengths_kernel(const int64_t* positions, int32_t n, int
   if (i < n) out[i] = static_cast<int32_t>(max(positions[i] + 1 - window, static_cast<int64_t>(0)));
 }
 
-// Window entries of positions at or after the first position of the row's
-// request in this call come from the call's own slots (call_slots, by the
-// request's qsl range) when call_slots is given, others from the ring.
-constexpr int kIdxPerThread = 4;
-constexpr int kIdxPerBlock = 256 * kIdxPerThread;
-
-__global__ void __launch_bounds__(256) hca_decode_indices_kernel(
-    const int64_t* positions, const int32_t* req_ids, const int32_t* comp_bt, int32_t comp_bt_stride,
-    const int32_t* ring_pages, int32_t ring_stride, int32_t ring, int32_t window, const int32_t* qsl,
-    const int64_t* call_slots, int32_t* out, int64_t out_stride, int32_t width, int32_t* lengths) {
-  const int64_t t = blockIdx.x;
-  const int64_t p = positions[t];
-  const int64_t b = req_ids[t];
-  const int64_t t0 = call_slots ? qsl[b] : 0;
-  const int64_t call_first = call_slots ? positions[t0] : INT64_MAX;
-  const int64_t nc = (p + 1) / kSpan;
-  const int64_t w = min(p + 1, static_cast<int64_t>(window));
-  const int64_t len = min(nc + w, static_cast<int64_t>(width));
-  // Workgroup (t, y) writes entries [kIdxPerBlock y, kIdxPerBlock (y + 1)) of
-  // row t, kIdxPerThread per thread with their table loads issued together.
-  int64_t v[kIdxPerThread];
-#pragma unroll
-  for (int j = 0; j < kIdxPerThread; ++j) {
-    const int c = static_cast<int>(blockIdx.y) * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
-    v[j] = -1;
-    if (c < nc) {
-      v[j] = static_cast<int64_t>(comp_bt[b * comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
-    } else if (c < len) {
-      const int64_t pos = p - w + 1 + (c - nc);
-      if (pos >= call_first) {
-        const int64_t sv = call_slots[t0 + (pos - call_first)];
-        v[j] = sv < 0 ? -1 : sv;
-      } else {
-        const int64_t r = pos % ring;
-        v[j] = static_cast<int64_t>(ring_pages[b * ring_stride + r / kPageTokens]) * kPageTokens + r % kPageTokens;
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < kIdxPerThread; ++j) {
-    const int c = static_cast<int>(blockIdx.y) * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
-    if (c < width) out[t * out_stride + c] = static_cast<int32_t>(v[j]);
-  }
-  if (blockIdx.y == 0 && threadIdx.x == 0) lengths[t] = static_cast<int32_t>(len);
+__global__ void __launch_bounds__(256) hca_decode_indices_kernel(HcaIndexArgs a) {
+  hca_index_block(a, blockIdx.x, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -545,11 +503,10 @@ extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* r
   EKV_CHECK((query_start_loc == nullptr) == (slot_mapping == nullptr),
             "query_start_loc and slot_mapping go together");
   EKV_CHECK(width >= 0 && out_stride >= width, "out_stride must be >= width >= 0");
-  const dim3 grid(static_cast<unsigned>(num_tokens),
-                  static_cast<unsigned>(std::max(1, (width + kIdxPerBlock - 1) / kIdxPerBlock)));
-  hipLaunchKernelGGL(hca_decode_indices_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
-                     positions, req_ids, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
-                     window, query_start_loc, slot_mapping, out, out_stride, width, lengths);
+  const HcaIndexArgs a{positions, req_ids, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                       window, query_start_loc, slot_mapping, out, out_stride, width, lengths};
+  const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(hca_index_blocks_per_row(width)));
+  hipLaunchKernelGGL(hca_decode_indices_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return ekv_launch_status();
 }
 

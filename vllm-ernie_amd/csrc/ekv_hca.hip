@@ -610,7 +610,8 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
 // matters.
 template <int D>
 __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(4)))
-hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows) {
+hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows,
+                       HcaIndexArgs ix, int append_blocks, int index_y) {
   __shared__ CompressLds<D> ls;
   const int block = static_cast<int>(blockIdx.x);
   const bool quarters = c.span_count != nullptr;
@@ -628,8 +629,14 @@ hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_bloc
     else compress_span<D, true>(c, ls, seq, t0, p0, j, st);
     return;
   }
-  if (threadIdx.x >= 256) return;  // the append's blocks are 4-wave; they use no workgroup barrier
-  hca_append_block<D>(a, block - compress_blocks, main_blocks, tail_rows);
+  if (threadIdx.x >= 256) return;  // the append's and index rows' blocks are 4-wave, with no workgroup barrier
+  const int ab = block - compress_blocks;
+  if (ab < append_blocks) {
+    hca_append_block<D>(a, ab, main_blocks, tail_rows);
+    return;
+  }
+  const int ib = ab - append_blocks;  // index rows (the step's decode reads them after this launch)
+  hca_index_block(ix, ib / index_y, ib % index_y);
 }
 
 }  // namespace ekv
@@ -693,15 +700,25 @@ extern "C" int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim) {
   return num_seqs > 0 && dim > 0 ? hca_write_ws_bytes(num_seqs, dim) : 0;
 }
 
-extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
-                             int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
-                             const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
-                             int32_t num_seqs, int32_t max_query_len, uint16_t* state,
-                             const int32_t* state_slot, int32_t num_state, const float* ape,
-                             const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
-                             const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
-                             int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride,
-                             int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
+                                      const int32_t* comp_block_table, int32_t comp_bt_stride,
+                                      const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
+                                      int32_t window, const int32_t* query_start_loc,
+                                      const int64_t* slot_mapping, int32_t* out, int64_t out_stride,
+                                      int32_t width, int32_t* lengths, void* stream);
+
+namespace {
+
+// ekv_hca_write, and with ix the step's decode index rows in the same launch
+// (decode-sized calls) or right after it.
+int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score, int64_t kvs_stride,
+                   int32_t num_tokens, int32_t dim, const int64_t* slot_mapping, const int64_t* positions,
+                   const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs, int32_t max_query_len,
+                   uint16_t* state, const int32_t* state_slot, int32_t num_state, const float* ape,
+                   const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                   const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                   int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride, int64_t num_pages,
+                   void* workspace, int64_t workspace_bytes, const HcaIndexArgs* ix, void* stream) {
   EKV_CHECK(num_tokens >= 0 && num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
   if (num_tokens == 0 || num_seqs == 0) return 0;
   CompressArgs c;
@@ -723,16 +740,24 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
                        state_slot, num_state);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (max_query_len < kSpan) {  // decode-sized: compress and append in one launch
+  if (max_query_len < kSpan) {  // decode-sized: compress, append (and index rows) in one launch
     int main_blocks = 0, tail_rows = 0;
     const int64_t compress_blocks = (c.span_count ? int64_t{kQuarters} : int64_t{1}) * num_seqs;
-    const int64_t blocks = compress_blocks + hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
+    const int64_t append_blocks = hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
+    const int index_y = ix ? hca_index_blocks_per_row(ix->width) : 1;
+    const int64_t index_blocks = ix ? int64_t{num_tokens} * index_y : 0;
+    const int64_t blocks = compress_blocks + append_blocks + index_blocks;
     EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
+    const HcaIndexArgs none{};
+    const HcaIndexArgs& ia = ix ? *ix : none;
     const dim3 grid(static_cast<uint32_t>(blocks));
+    const int ab = static_cast<int>(append_blocks);
     if (dim == 512)
-      hipLaunchKernelGGL(hca_write_small_kernel<512>, grid, dim3(512), 0, s, c, ap, num_seqs, main_blocks, tail_rows);
+      hipLaunchKernelGGL(hca_write_small_kernel<512>, grid, dim3(512), 0, s, c, ap, num_seqs, main_blocks, tail_rows,
+                         ia, ab, index_y);
     else
-      hipLaunchKernelGGL(hca_write_small_kernel<576>, grid, dim3(576), 0, s, c, ap, num_seqs, main_blocks, tail_rows);
+      hipLaunchKernelGGL(hca_write_small_kernel<576>, grid, dim3(576), 0, s, c, ap, num_seqs, main_blocks, tail_rows,
+                         ia, ab, index_y);
     return ekv_launch_status();
   }
   const dim3 grid(max_query_len / kSpan + 1, num_seqs);
@@ -740,5 +765,48 @@ extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, cons
   else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, c);
   rc = ekv_launch_status();
   if (rc) return rc;
-  return launch_hca_append(ap, dim, num_seqs, true, true, s);
+  rc = launch_hca_append(ap, dim, num_seqs, true, true, s);
+  if (rc || ix == nullptr) return rc;
+  return ekv_hca_decode_indices(ix->positions, ix->req_ids, num_tokens, ix->comp_bt, ix->comp_bt_stride,
+                                ix->ring_pages, ix->ring_stride, ix->ring, ix->window, ix->qsl, ix->call_slots,
+                                ix->out, ix->out_stride, ix->width, ix->lengths, stream);
+}
+
+}  // namespace
+
+extern "C" int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                             int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                             const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                             int32_t num_seqs, int32_t max_query_len, uint16_t* state,
+                             const int32_t* state_slot, int32_t num_state, const float* ape,
+                             const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                             const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                             int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride,
+                             int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream) {
+  return hca_write_impl(latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+                        token_seq, qsl, num_seqs, max_query_len, state, state_slot, num_state, ape, norm_w, eps,
+                        cos_sin, max_spans, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring, pool,
+                        page_stride, num_pages, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int ekv_hca_write_step(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                                  int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                                  const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                                  int32_t num_seqs, int32_t max_query_len, uint16_t* state,
+                                  const int32_t* state_slot, int32_t num_state, const float* ape,
+                                  const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                                  const int32_t* comp_block_table, int32_t comp_bt_stride,
+                                  const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint8_t* pool,
+                                  int64_t page_stride, int64_t num_pages, void* workspace, int64_t workspace_bytes,
+                                  int32_t window, int32_t* idx_out, int64_t idx_stride, int32_t width,
+                                  int32_t* lengths, void* stream) {
+  EKV_CHECK(ring_pages && idx_out && lengths, "null pointer");
+  EKV_CHECK(ring >= window && window >= 0 && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
+  EKV_CHECK(width >= 0 && idx_stride >= width, "idx_stride must be >= width >= 0");
+  const HcaIndexArgs ix{positions, token_seq, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                        window, qsl, slot_mapping, idx_out, idx_stride, width, lengths};
+  return hca_write_impl(latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+                        token_seq, qsl, num_seqs, max_query_len, state, state_slot, num_state, ape, norm_w, eps,
+                        cos_sin, max_spans, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring, pool,
+                        page_stride, num_pages, workspace, workspace_bytes, &ix, stream);
 }

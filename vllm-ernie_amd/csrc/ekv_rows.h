@@ -389,4 +389,73 @@ inline int hca_append_args(AppendArgs& a, const uint16_t* latent, int64_t latent
 // status.  Defined with the append kernels.
 int launch_hca_append(const AppendArgs& a, int dim, int num_seqs, bool rows, bool tail, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// HCA decode index rows: [compressed slots 0..n_c-1 | window slots of
+// positions p-w+1..p | -1 ...], n_c = (p+1)/128, w = min(p+1, window), and
+// the row lengths.  Window entries of positions at or after the first
+// position of the row's request in this call come from the call's own slots
+// (call_slots, by the request's qsl range) when call_slots is given, others
+// from the ring.  Block (t, y) of 256 threads writes entries
+// [kIdxPerBlock y, kIdxPerBlock (y + 1)) of row t, kIdxPerThread per thread
+// with their table loads issued together.
+// ---------------------------------------------------------------------------
+struct HcaIndexArgs {
+  const int64_t* positions;
+  const int32_t* req_ids;
+  const int32_t* comp_bt;
+  int32_t comp_bt_stride;
+  const int32_t* ring_pages;
+  int32_t ring_stride;
+  int32_t ring;
+  int32_t window;
+  const int32_t* qsl;
+  const int64_t* call_slots;
+  int32_t* out;
+  int64_t out_stride;
+  int32_t width;
+  int32_t* lengths;
+};
+
+constexpr int kIdxPerThread = 4;
+constexpr int kIdxPerBlock = 256 * kIdxPerThread;
+
+__host__ __device__ inline int hca_index_blocks_per_row(int width) {
+  return width > kIdxPerBlock ? (width + kIdxPerBlock - 1) / kIdxPerBlock : 1;
+}
+
+__device__ __forceinline__ void hca_index_block(const HcaIndexArgs& a, int64_t t, int y) {
+  const int64_t p = a.positions[t];
+  const int64_t b = a.req_ids[t];
+  const int64_t t0 = a.call_slots ? a.qsl[b] : 0;
+  const int64_t call_first = a.call_slots ? a.positions[t0] : INT64_MAX;
+  const int64_t nc = (p + 1) / kSpan;
+  const int64_t w = min(p + 1, static_cast<int64_t>(a.window));
+  const int64_t len = min(nc + w, static_cast<int64_t>(a.width));
+  int64_t v[kIdxPerThread];
+#pragma unroll
+  for (int j = 0; j < kIdxPerThread; ++j) {
+    const int c = y * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
+    v[j] = -1;
+    if (c < nc) {
+      v[j] = static_cast<int64_t>(a.comp_bt[b * a.comp_bt_stride + c / kPageTokens]) * kPageTokens + c % kPageTokens;
+    } else if (c < len) {
+      const int64_t pos = p - w + 1 + (c - nc);
+      if (pos >= call_first) {
+        const int64_t sv = a.call_slots[t0 + (pos - call_first)];
+        v[j] = sv < 0 ? -1 : sv;
+      } else {
+        const int64_t r = pos % a.ring;
+        v[j] = static_cast<int64_t>(a.ring_pages[b * a.ring_stride + r / kPageTokens]) * kPageTokens +
+               r % kPageTokens;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kIdxPerThread; ++j) {
+    const int c = y * kIdxPerBlock + j * 256 + static_cast<int>(threadIdx.x);
+    if (c < a.width) a.out[t * a.out_stride + c] = static_cast<int32_t>(v[j]);
+  }
+  if (y == 0 && threadIdx.x == 0) a.lengths[t] = static_cast<int32_t>(len);
+}
+
 }  // namespace ekv

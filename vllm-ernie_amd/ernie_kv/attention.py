@@ -713,14 +713,21 @@ class Ernie5_5HCAAttentionMixin:
         # overwrite ring rows that its own first rows' windows still read:
         # such calls update the ring after the decode.
         late_ring = md.max_query_len > self.ring - self.window
-        ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc, md.max_query_len,
-                      self.state_cache, md.state_slot, self.ape, self.norm_w, self.norm_eps, self.compress_cos_sin,
-                      md.comp_block_table, None if late_ring else md.ring_pages, self.ring, self.kv_cache,
-                      workspace=self._write_workspace(md.query_start_loc.numel() - 1, D, q.device))
         width = md.max_seq_len // 128 + self.window
         idx, lens, lse, ws = self._buffers(T, width, q.device)
-        ops.hca_decode_indices(positions, md.token_seq, md.comp_block_table, md.ring_pages, self.ring, idx, lens,
-                               self.window, query_start_loc=md.query_start_loc, slot_mapping=md.slot_mapping)
+        write_ws = self._write_workspace(md.query_start_loc.numel() - 1, D, q.device)
+        if late_ring:
+            ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc,
+                          md.max_query_len, self.state_cache, md.state_slot, self.ape, self.norm_w, self.norm_eps,
+                          self.compress_cos_sin, md.comp_block_table, None, self.ring, self.kv_cache,
+                          workspace=write_ws)
+            ops.hca_decode_indices(positions, md.token_seq, md.comp_block_table, md.ring_pages, self.ring, idx, lens,
+                                   self.window, query_start_loc=md.query_start_loc, slot_mapping=md.slot_mapping)
+        else:  # the write and the index rows (one launch for decode-sized calls)
+            ops.hca_write_step(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc,
+                               md.max_query_len, self.state_cache, md.state_slot, self.ape, self.norm_w,
+                               self.norm_eps, self.compress_cos_sin, md.comp_block_table, md.ring_pages, self.ring,
+                               self.kv_cache, self.window, idx, lens, workspace=write_ws)
         if H < self.padded_heads:
             qp = q.new_zeros((T, self.padded_heads, D))
             qp[:, :H] = q

@@ -142,6 +142,39 @@ def hca_append(
     )
 
 
+def _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
+                    ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace) -> list:
+    _check_dev(latent, kv_score, slot_mapping, positions, token_seq, qsl, state, state_slot, ape, norm_w, cos_sin,
+               comp_block_table, ring_pages, pool, workspace)
+    _bits16(latent)
+    _bits16(kv_score)
+    T, D = latent.shape
+    _need(latent.stride(1) == 1, "latent must be row-contiguous")
+    _need(kv_score.shape[1] >= 2 * D and kv_score.stride(1) == 1, "kv_score must be [T, 2D]")
+    _need(ape.shape == (128, D) and ape.dtype == torch.float32 and ape.is_contiguous(), "ape fp32 [128, D]")
+    _need(norm_w.shape == (D,) and norm_w.dtype == torch.float32, "norm_w fp32 [D]")
+    _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(), "cos_sin fp32 [S, 64]")
+    _need(comp_block_table.dtype == torch.int32 and comp_block_table.stride(1) == 1, "comp_block_table int32")
+    _need(slot_mapping.dtype == torch.int64 and positions.dtype == torch.int64, "slot_mapping/positions int64")
+    _need(token_seq.dtype == torch.int32 and qsl.dtype == torch.int32, "token_seq/qsl int32")
+    if ring_pages is not None:
+        _need(ring_pages.dtype == torch.int32 and ring_pages.stride(1) == 1, "ring_pages int32 [B, R/64]")
+    if state is not None:
+        _bits16(state)
+        _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
+    if workspace is not None:
+        _need(workspace.dtype == torch.uint8 and workspace.is_contiguous(), "workspace: a uint8 hca_write_workspace")
+    return [
+        latent.data_ptr(), _rs(latent), kv_score.data_ptr(), _rs(kv_score), T, D,
+        slot_mapping.data_ptr(), positions.data_ptr(), token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1,
+        int(max_query_len), _ptr(state), _ptr(state_slot), 0 if state is None else state.shape[0],
+        ape.data_ptr(), norm_w.data_ptr(), float(eps), cos_sin.data_ptr(), cos_sin.shape[0],
+        comp_block_table.data_ptr(), _rs(comp_block_table), _ptr(ring_pages),
+        0 if ring_pages is None else _rs(ring_pages), int(ring), pool.data_ptr(), _rs(pool), pool.shape[0],
+        _ptr(workspace), 0 if workspace is None else workspace.numel(),
+    ]
+
+
 def hca_write(
     latent: torch.Tensor,
     kv_score: torch.Tensor,
@@ -165,35 +198,46 @@ def hca_write(
     """``hca_compress`` then ``hca_append`` (same arguments, same result) in
     one call.  With ``workspace`` (``hca_write_workspace``) decode-sized calls
     compress each completed span with four workgroups (same bytes)."""
-    _check_dev(latent, kv_score, slot_mapping, positions, token_seq, qsl, state, state_slot, ape, norm_w, cos_sin,
-               comp_block_table, ring_pages, pool, workspace)
-    _bits16(latent)
-    _bits16(kv_score)
-    T, D = latent.shape
-    _need(latent.stride(1) == 1, "latent must be row-contiguous")
-    _need(kv_score.shape[1] >= 2 * D and kv_score.stride(1) == 1, "kv_score must be [T, 2D]")
-    _need(ape.shape == (128, D) and ape.dtype == torch.float32 and ape.is_contiguous(), "ape fp32 [128, D]")
-    _need(norm_w.shape == (D,) and norm_w.dtype == torch.float32, "norm_w fp32 [D]")
-    _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(), "cos_sin fp32 [S, 64]")
-    _need(comp_block_table.dtype == torch.int32 and comp_block_table.stride(1) == 1, "comp_block_table int32")
-    _need(slot_mapping.dtype == torch.int64 and positions.dtype == torch.int64, "slot_mapping/positions int64")
-    _need(token_seq.dtype == torch.int32 and qsl.dtype == torch.int32, "token_seq/qsl int32")
-    if ring_pages is not None:
-        _need(ring_pages.dtype == torch.int32 and ring_pages.stride(1) == 1, "ring_pages int32 [B, R/64]")
-    if state is not None:
-        _bits16(state)
-        _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
-    if workspace is not None:
-        _need(workspace.dtype == torch.uint8 and workspace.is_contiguous(), "workspace: a uint8 hca_write_workspace")
-    _lib.call(
-        "ekv_hca_write", latent.data_ptr(), _rs(latent), kv_score.data_ptr(), _rs(kv_score), T, D,
-        slot_mapping.data_ptr(), positions.data_ptr(), token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1,
-        int(max_query_len), _ptr(state), _ptr(state_slot), 0 if state is None else state.shape[0],
-        ape.data_ptr(), norm_w.data_ptr(), float(eps), cos_sin.data_ptr(), cos_sin.shape[0],
-        comp_block_table.data_ptr(), _rs(comp_block_table), _ptr(ring_pages),
-        0 if ring_pages is None else _rs(ring_pages), int(ring), pool.data_ptr(), _rs(pool), pool.shape[0],
-        _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream(),
-    )
+    args = _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
+                           ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace)
+    _lib.call("ekv_hca_write", *args, _stream())
+
+
+def hca_write_step(
+    latent: torch.Tensor,
+    kv_score: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    positions: torch.Tensor,
+    token_seq: torch.Tensor,
+    qsl: torch.Tensor,
+    max_query_len: int,
+    state: torch.Tensor | None,
+    state_slot: torch.Tensor | None,
+    ape: torch.Tensor,
+    norm_w: torch.Tensor,
+    eps: float,
+    cos_sin: torch.Tensor,
+    comp_block_table: torch.Tensor,
+    ring_pages: torch.Tensor,
+    ring: int,
+    pool: torch.Tensor,
+    window: int,
+    out: torch.Tensor,
+    lengths: torch.Tensor,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """``hca_write`` then ``hca_decode_indices(positions, token_seq, ...,
+    query_start_loc=qsl, slot_mapping=slot_mapping)`` into ``out`` /
+    ``lengths``, same results; decode-sized calls build the index rows in the
+    write's launch."""
+    _need(ring_pages is not None, "ring_pages is needed for the index rows")
+    _check_dev(out, lengths)
+    _need(out.dtype == torch.int32 and out.dim() == 2 and out.stride(1) == 1, "out must be int32 [T, width]")
+    _need(lengths.dtype == torch.int32 and lengths.numel() >= latent.shape[0], "lengths must be int32 [T]")
+    args = _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
+                           ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace)
+    _lib.call("ekv_hca_write_step", *args, int(window), out.data_ptr(), out.stride(0), out.shape[1],
+              lengths.data_ptr(), _stream())
 
 
 def hca_write_workspace(num_seqs: int, dim: int, device) -> torch.Tensor:
