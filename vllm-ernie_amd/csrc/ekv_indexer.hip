@@ -998,7 +998,8 @@ template <int kWaves>
 struct FusedLayout {
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kList = 8 * kThreads;  // candidates scored per pass (>= one compaction round)
-  static constexpr int kFixed = kFusedQdBytes + 256 * 4 + kList * 4 + 32 * 4;
+  // q operands / histogram | table | list | list scores | misc
+  static constexpr int kFixed = kFusedQdBytes + 256 * 4 + 2 * kList * 4 + 32 * 4;
   static constexpr int bytes(int stage_pages) { return kFixed + stage_pages * (4 + 2 * kPageTokens); }
 };
 
@@ -1016,7 +1017,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const uint2* s_q4 = reinterpret_cast<const uint2*>(fused_smem);  // fp4: phases 2-3 (same bytes)
   uint32_t* s_table = reinterpret_cast<uint32_t*>(fused_smem + kFusedQdBytes);  // fp4: q scale words
   int32_t* s_list = reinterpret_cast<int32_t*>(s_table + 256);
-  int* s_misc = reinterpret_cast<int*>(s_list + Lay::kList);  // [0..15] scans, [16] last, [17] bin, [18] next page
+  float* s_score = reinterpret_cast<float*>(s_list + Lay::kList);  // exact scores of the list
+  int* s_misc = reinterpret_cast<int*>(s_score + Lay::kList);  // [0..15] scans, [16] last, [17] bin, [18] next page
   int32_t* s_pages = reinterpret_cast<int32_t*>(s_misc + 32);
   uint16_t* s_pref = reinterpret_cast<uint16_t*>(s_pages + a.stage_pages);
 
@@ -1108,6 +1110,23 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   __syncthreads();
 
   // Phase 2: arrive; the last workgroup of the row publishes the bound.
+  // Every workgroup reads the row histogram as it arrives (the last one to
+  // arrive then has it without a second round trip; the others ignore it).
+  constexpr int kBinsPer = (kHistBins + kThreads - 1) / kThreads;  // scanned from the top bin down
+  const int r0 = kBinsPer * tid;
+  int c[kBinsPer];
+  auto read_hist = [&]() -> int {
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j) {
+      c[j] = (r0 + j < kHistBins) ? static_cast<int>(__hip_atomic_load(gh + (kHistBins - 1 - (r0 + j)),
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                                  : 0;
+      sum += c[j];
+    }
+    return sum;
+  };
+  int first_sum = read_hist();
   const int groups_row = (npages + per_group - 1) / per_group;
   if (tid == 0) {
     const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1126,33 +1145,19 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   }
   __syncthreads();
   if (s_misc[16]) {
-    constexpr int kBinsPer = (kHistBins + kThreads - 1) / kThreads;  // scanned from the top bin down
-    const int r0 = kBinsPer * tid;
-    int c[kBinsPer];
     int excl = 0, total = 0;
     // The row histogram counts each of the row's n tokens once.  Every
     // workgroup's adds completed before it arrived, so the bins sum to n;
     // the check makes the bound (and the clearing below) rely on that sum,
-    // not on the ordering: the bins are read again until they sum to n, and
+    // not on the ordering: the bins are read again until they sum to n (the
+    // read made on arrival may predate the other workgroups' arrivals), and
     // a histogram that never does gives bin 0 (every token a candidate).
     for (int attempt = 0;; ++attempt) {
-      int sum = 0;
-#pragma unroll
-      for (int j = 0; j < kBinsPer; ++j) {
-        c[j] = (r0 + j < kHistBins) ? static_cast<int>(__hip_atomic_load(gh + (kHistBins - 1 - (r0 + j)),
-                                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-                                    : 0;
-        sum += c[j];
-      }
+      const int sum = attempt == 0 ? first_sum : read_hist();
       excl = block_scan_excl<kThreads>(sum, s_misc, total);
       if (total == n || attempt == kHistRereads) break;
       __builtin_amdgcn_s_sleep(8);
     }
-    // leave the row histogram zero for the next call
-#pragma unroll
-    for (int j = 0; j < kBinsPer; ++j)
-      if (r0 + j < kHistBins)
-        __hip_atomic_store(gh + (kHistBins - 1 - (r0 + j)), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (total == n) {
 #pragma unroll
       for (int j = 0; j < kBinsPer; ++j) {
@@ -1163,11 +1168,16 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       atomicAdd(a.timeouts + 1, 1u);  // bin 0 (s_misc[17] stays 0)
     }
     __syncthreads();
-    if (tid == 0) {
-      __builtin_amdgcn_s_waitcnt(0);  // the histogram is zero before the bound is out
+    if (tid == 0)
       __hip_atomic_store(kword, (static_cast<uint32_t>(s_misc[17]) << (32 - kHistBits)) | 1u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // then leave the row histogram zero for the next call (every workgroup
+    // of the row has arrived, so nothing in this call reads it again, and
+    // the stores complete before the kernel does)
+#pragma unroll
+    for (int j = 0; j < kBinsPer; ++j)
+      if (r0 + j < kHistBins)
+        __hip_atomic_store(gh + (kHistBins - 1 - (r0 + j)), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else if (tid == 0) {
     uint32_t v = 0;
     for (int spins = 0; spins < kFusedSpinLimit; ++spins) {
@@ -1194,35 +1204,40 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // Phase 3: candidates of the segment in order, scored Lay::kList at a time.
   auto score_list = [&](int cnt, int base) {
     __syncthreads();
-    constexpr int kBatch = 2;  // blocks whose key rows are loaded together
-    for (int bb = wave * 16; bb < cnt; bb += 16 * kWaves * kBatch) {
+    // Passes of kBatch blocks per wave; the next pass's key rows are loaded
+    // (into the other buffer) while a pass is scored.
+    constexpr int kBatch = 2;
+    constexpr int kStride = 16 * kWaves * kBatch;
+    struct Keys {
       int tok[kBatch];
-      int64_t page[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int li = bb + 16 * kWaves * j + col;
-        tok[j] = (li < cnt) ? s_list[li] : -1;  // offset in the segment
-        page[j] = (tok[j] >= 0) ? static_cast<int64_t>(s_pages[tok[j] >> 6]) : -1;
-      }
+      bool ok[kBatch];
       uint4 kb[kBatch][2];
       float ks[kBatch];
       Fp4Key k4[kFp4 ? kBatch : 1];
+    };
+    auto load = [&](int bb, Keys& p) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const bool ok = page[j] >= 0;  // mapped pages only (checked when streamed)
-        const uint8_t* base_p = f.kcache + (ok ? page[j] : 0) * f.page_stride;
-        const int r = tok[j] & 63;
+        const int li = bb + 16 * kWaves * j + col;
+        p.tok[j] = (li < cnt) ? s_list[li] : -1;  // offset in the segment
+        const int64_t page = (p.tok[j] >= 0) ? static_cast<int64_t>(s_pages[p.tok[j] >> 6]) : -1;
+        const bool ok = page >= 0;  // mapped pages only (checked when streamed)
+        p.ok[j] = ok;
+        const uint8_t* base_p = f.kcache + (ok ? page : 0) * f.page_stride;
+        const int r = p.tok[j] & 63;
         if constexpr (kFp4) {
-          load_key_fp4(base_p, r, g, ok, k4[j]);
+          load_key_fp4(base_p, r, g, ok, p.k4[j]);
         } else {
-          const uint4 k0 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 16 * g);
-          const uint4 k1 = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 64 + 16 * g);
-          const float sc = *reinterpret_cast<const float*>(base_p + kIdxPageBytes + r * 4);
-          kb[j][0] = ok ? k0 : make_uint4(0, 0, 0, 0);
-          kb[j][1] = ok ? k1 : make_uint4(0, 0, 0, 0);
-          ks[j] = ok ? sc : 0.0f;
+          // used as loaded (a missing entry reads a row of page 0 and its
+          // score is zeroed after): values selected on `ok` here would let
+          // the compiler put the loads under a branch
+          p.kb[j][0] = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 16 * g);
+          p.kb[j][1] = *reinterpret_cast<const uint4*>(base_p + r * kIdxDim + 64 + 16 * g);
+          p.ks[j] = *reinterpret_cast<const float*>(base_p + kIdxPageBytes + r * 4);
         }
       }
+    };
+    auto run = [&](int bb, const Keys& p) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         const int b0 = bb + 16 * kWaves * j;
@@ -1234,23 +1249,47 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                 const uint2 v = s_q4[(hb * 4 + b) * 64 + lane];
                 return static_cast<int64_t>((static_cast<uint64_t>(v.y) << 32) | v.x);
               },
-              [&](int h) { return s_table[h]; }, op.wv, k4[j]);
+              [&](int h) { return s_table[h]; }, op.wv, p.k4[j]);
         } else {
           sc = exact_block_with<true>(
               [&](int hb, int d, int kh) {
                 const uint4 v = s_qd[((hb * 3 + d) * 2 + kh) * 64 + lane];
                 return i32x4{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
               },
-              op.wv, s_table, kb[j], ks[j]);
+              op.wv, s_table, p.kb[j], p.ks[j]);
+          sc = p.ok[j] ? sc : 0.0f;  // an unmapped page's tokens score 0
         }
         const int li = b0 + col;
-        if (li < cnt && g == 0) {
-          a.cand_score[out0 + base + li] = sc;
-          a.cand_idx[out0 + base + li] = seg0 + tok[j];
-        }
+        if (li < cnt && g == 0) s_score[li] = sc;
       }
+    };
+    // (the loads are unconditional -- past the list they read a row of page
+    // 0 and give zeros -- and the scores go to LDS, so only loads are in
+    // flight and the waits for one buffer leave the other's loads going)
+    Keys ka, kb2;
+    int bb = wave * 16;
+    load(bb, ka);
+    __builtin_amdgcn_sched_barrier(0);
+    for (;;) {
+      if (bb >= cnt) break;
+      load(bb + kStride, kb2);
+      __builtin_amdgcn_sched_barrier(0);
+      run(bb, ka);
+      bb += kStride;
+      if (bb >= cnt) break;
+      load(bb + kStride, ka);
+      __builtin_amdgcn_sched_barrier(0);
+      run(bb, kb2);
+      bb += kStride;
     }
     __syncthreads();
+    for (int i = tid; i < cnt; i += kThreads) {
+      a.cand_score[out0 + base + i] = s_score[i];
+      a.cand_idx[out0 + base + i] = seg0 + s_list[i];
+    }
+    // the list's LDS may be refilled after this; the stores need not have
+    // completed (a barrier with a fence would wait for them)
+    __builtin_amdgcn_s_barrier();
   };
   // One scan over the whole segment (kOnePass groups of 8 tokens per thread)
   // when it is short enough and its candidates fit the list.
