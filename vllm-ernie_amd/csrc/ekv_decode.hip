@@ -112,9 +112,12 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
     first = l - split;
     return;
   }
-  // total tiles
+  // total tiles (with T <= kN thread r reads row r's length once, here)
+  const int mine = (T <= kN && tid < T) ? (row_len(a, tid) + kTile - 1) / kTile : 0;
   int64_t sum = 0;
-  for (int r = tid; r < T; r += kN) sum += (row_len(a, r) + kTile - 1) / kTile;
+  if (T <= kN) sum = mine;
+  else
+    for (int r = tid; r < T; r += kN) sum += (row_len(a, r) + kTile - 1) / kTile;
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (lane == 0) reinterpret_cast<int64_t*>(s_red)[wave] = sum;
   __syncthreads();
@@ -126,7 +129,11 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
   const int per = (T + kN - 1) / kN;
   const int r0 = min(tid * per, T), r1 = min(r0 + per, T);
   int cnt = 0;
-  for (int r = r0; r < r1; ++r) cnt += row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+  if (T <= kN) {
+    if (r0 < r1) cnt = row_splits(extra, mine, total);  // r0 = tid
+  } else {
+    for (int r = r0; r < r1; ++r) cnt += row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+  }
   int x = cnt;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -142,7 +149,7 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
   int pos = before + x - cnt;  // logical workgroups before row r0
   if (pos <= l && l < pos + cnt) {
     for (int r = r0; r < r1; ++r) {
-      const int ns = row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+      const int ns = T <= kN ? cnt : row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
       if (l < pos + ns) {
         s_red[3 * kW] = r;
         s_red[3 * kW + 1] = l - pos;
