@@ -175,14 +175,14 @@ def dsa_pre(ops, st):
 
 
 def dsa_filter(ops, st):
+    """The indexer: filter, exact scoring of the candidates, exact top-2048
+    and its merge with the window (one launch when the filter fits one)."""
     common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
-    ops.indexer_filter(st["q8"], st["digits"], st["wf"], *common, st["idx_ws"])
+    ops.indexer_topk_merged(st["q8"], st["digits"], st["wf"], *common, st["topk"], st["idx_ws"],
+                            merged=st["merged"], positions=st["positions"], window=128)
 
 
 def dsa_post(ops, st, ev=None):
-    common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
-    ops.indexer_select(st["digits"], st["wf"], *common, st["topk"], st["idx_ws"], merged=st["merged"],
-                       positions=st["positions"], window=128)
     if ev is not None:
         ev[2].record()
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
@@ -204,7 +204,7 @@ def measure_dsa_prefill(torch, ops, seed: int, chunk: int = 4096, ctx: int = 327
     """A DSA layer's chunked-prefill step: `chunk` new tokens of one request
     ending at `ctx`, each a query row -- prologue (indexer prep, K insert,
     latent append, q quant, lengths), indexer top-k of every row (the
-    many-row filter / bound / verify kernels), select with merged rows, and
+    many-row filter / bound / verify kernels and the select, with merged rows), and
     the sparse MLA over the rows' 2176 entries.  The indexer's work is
     quadratic in the chunk: row t scores pos_t + 1 - 128 keys."""
     st = build_dsa_decode(torch, ops, [ctx], seed, rows_per_seq=chunk, spike_frac=0.0)
@@ -235,8 +235,9 @@ def measure_dsa_prefill(torch, ops, seed: int, chunk: int = 4096, ctx: int = 327
         "indexer_keys_scored": keys, "indexer_key_bytes": keys * 132,
         "indexer_fp8_tflops": round(flops / (filt_ms * 1e-3) / 1e12, 1),
         "indexer_mfma_frac": round(flops / (filt_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
-        "what": "one request's prefill chunk as query rows through the DSA step (prologue, indexer filter, "
-                "select with merged rows, sparse MLA); the indexer filter is timed by events around its call",
+        "what": "one request's prefill chunk as query rows through the DSA step (prologue, indexer top-k with "
+                "merged rows, sparse MLA); the indexer top-k (filter, bound, verify and select launches) is timed "
+                "by events around its call",
     }
 
 
@@ -303,39 +304,22 @@ def measure_indexer_fp4(torch, ops, seed: int, B: int = 32, ctx: int = 131072, r
     merged = torch.empty((B, 2176), dtype=torch.int32, device=dev)
     common = (kcache, block_table, req, lengths, ctx)
 
-    def step(ev=None):
-        ops.indexer_filter_fp4(qv, qs, wf, *common, ws)
-        if ev is not None:
-            ev.record()
-        ops.indexer_select_fp4(qv, qs, wf, *common, topk, ws, merged=merged, positions=positions, window=128)
+    def step():
+        ops.indexer_topk_merged_fp4(qv, qs, wf, *common, topk, ws, merged=merged, positions=positions, window=128)
 
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    t0.record()
-    for i in range(reps):
-        starts[i].record()
-        step(mids[i])
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / reps
-    filt_ms = sum(starts[i].elapsed_time(mids[i]) for i in range(reps)) / reps
+    ms = time_ms(torch, step, reps)
     n = max(ctx - 128, 0)
     k_bytes = B * n * 68
-    timeouts = int(ws[:8].view(torch.int32).sum())
+    timeouts = int(ws[:16].view(torch.int32).sum())
     del kcache
     return {
         "workload": f"indexer_fp4_b{B}_ctx{ctx}",
-        "ms": round(ms, 4), "filter_ms": round(filt_ms, 4), "select_ms": round(ms - filt_ms, 4),
-        "key_bytes": k_bytes, "filter_GB/s": round(k_bytes / (filt_ms * 1e-3) / 1e9, 1),
-        "filter_frac": round(k_bytes / (filt_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "bound_timeouts": timeouts,
-        "what": "ekv_indexer_filter_fp4 + ekv_indexer_select_fp4 (merged rows) over 68-byte MXFP4 key rows, "
-                "q pre-quantized; filter_frac = key bytes / filter time / 8 TB/s",
+        "ms": round(ms, 4), "key_bytes": k_bytes, "GB/s_keys": round(k_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac_keys": round(k_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "wait_timeouts": timeouts,
+        "what": "ekv_indexer_topk_merged_fp4 (filter, exact scoring of the candidates, exact top-2048 and the "
+                "merged rows in one launch) over 68-byte MXFP4 key rows, q pre-quantized; frac_keys = key bytes "
+                "/ call time / 8 TB/s",
     }
 
 
@@ -870,8 +854,8 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_eager": round(ms_eager, 4),
-        "launch": "hip_graph: the timed steps replay one captured DSA step (prologue, filter, select, decode, "
-                  "combine); ms_per_step_eager = the same steps launched eagerly",
+        "launch": "hip_graph: the timed steps replay one captured DSA step (prologue, indexer top-k with the "
+                  "merged rows, decode, combine); ms_per_step_eager = the same steps launched eagerly",
         "tok_per_s_dsa_layer": round(args.batch / (ms_step * 1e-3), 1),
         "config": {
             "workload": workload,
@@ -880,8 +864,9 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
             "bytes_per_step": by,
         },
         "roofline": {
-            "kernel": "ekv_indexer_filter = filter_verify_kernel<12> (fp8-MFMA filter over every key row, "
-                      "candidate bound, exact scoring of the candidates), timed by events around the call",
+            "kernel": "ekv_indexer_topk_merged = filter_verify_kernel<12> (fp8-MFMA filter over every key row, "
+                      "candidate bound, exact scoring of the candidates, exact top-2048 and the merged rows, in "
+                      "one launch), timed by events around the call",
             "bound": "hbm",
             "achieved": round(filt_gbs, 1),
             "peak": HBM_PEAK_GBS,

@@ -305,14 +305,48 @@ int ekv_indexer_select(const int8_t* q_digits, const float* w, const uint8_t* kc
                        int32_t window, int32_t merged_slots, void* stream);
 
 /*
- * ekv_indexer_filter followed by ekv_indexer_select: the SparseAttnIndexer
- * decode path (nvidia/attention.py:942-953, 982-984) in one call.
+ * Both stages in one call: the SparseAttnIndexer decode path
+ * (nvidia/attention.py:942-953, 982-984).  When the filter runs as one launch
+ * the exact select runs inside that launch too: the workgroups of each row
+ * agree on the top-k threshold through counters in `workspace` and write the
+ * output directly.  Same results as ekv_indexer_filter + ekv_indexer_select.
  */
 int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, const float* w, const uint8_t* kcache,
                      int64_t page_stride /*bytes*/, int64_t num_pages, const int32_t* block_table,
                      int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
                      int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride,
                      int32_t k, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * ekv_indexer_topk with ekv_indexer_select's merged output (merge_swa_topk
+ * of the result, optionally as cache slots): the indexer half of
+ * Ernie5_5DSAAttention._indexer_and_attn (nvidia/attention.py:1205-1226:
+ * SparseAttnIndexer filling topk_indices_buffer, then merge_swa_topk at
+ * :582-641), one launch when the filter plan allows it.
+ */
+int ekv_indexer_topk_merged(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
+                            const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                            const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                            const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                            int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                            int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
+                            const int64_t* positions, int32_t window, int32_t merged_slots, void* stream);
+
+/*
+ * Diagnostic, no counterpart in the reference: bytes at the front of a
+ * top-k workspace that hold the one-launch path's per-row counters (zero
+ * between calls).
+ */
+int64_t ekv_indexer_topk_counter_bytes(void);
+
+/*
+ * Test hook, no counterpart in the reference: polls a one-launch top-k
+ * workgroup makes while it waits for the rest of its row before it gives up
+ * (the row is then selected by its last workgroup alone; still exact).
+ * polls < 0 restores the default.  Returns the previous value.  Process-wide;
+ * not for concurrent use with top-k calls.
+ */
+int32_t ekv_indexer_set_spin_limit(int32_t polls);
 
 /* Workspace bytes ekv_sparse_mla_decode needs. */
 int64_t ekv_sparse_mla_decode_workspace_size(int32_t num_tokens, int32_t heads, int32_t width);
@@ -470,7 +504,7 @@ int ekv_indexer_score_fp4(const uint8_t* q_values, const int32_t* q_scales, cons
                           int64_t scores_stride, void* stream);
 
 /*
- * MXFP4 counterparts of ekv_indexer_filter / _select / _topk (same workspace,
+ * MXFP4 counterparts of ekv_indexer_filter / _select / _topk / _topk_merged (same workspace,
  * ekv_indexer_topk_workspace_size): the filter runs the scaled fp4 MFMA over
  * every token with an error bound, the candidates are scored exactly as
  * ekv_indexer_score_fp4, and the select writes the exact top-k (lowest index
@@ -495,6 +529,13 @@ int ekv_indexer_topk_fp4(const uint8_t* q_values, const int32_t* q_scales, const
                          const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
                          const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
                          int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes, void* stream);
+int ekv_indexer_topk_merged_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                const uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages,
+                                const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
+                                int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
+                                int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
+                                const int64_t* positions, int32_t window, int32_t merged_slots, void* stream);
 
 /*
  * Diagnostic, no counterpart in the reference: the MXFP4 filter's MFMA dot

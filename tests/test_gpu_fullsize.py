@@ -1,8 +1,8 @@
 """GPU parity of the timed workloads at full size.
 
 The DSA decode step exactly as ``bench.py`` times it (``build_dsa_decode`` +
-``dsa_step``: prologue with indexer prep -> fused filter -> select with the
-merged output -> decode through the block table) at 32 x 131,072 tokens with
+``dsa_step``: prologue with indexer prep -> one-launch filter, exact scoring
+and select with the merged output -> decode through the block table) at 32 x 131,072 tokens with
 5% identical spike keys, and the multi-token step at 8 x 262,144 + 1 x
 1,048,576 tokens with 3 query rows per sequence, are checked against:
 
@@ -13,8 +13,8 @@ merged output -> decode through the block table) at 32 x 131,072 tokens with
   top-k, merged rows, and the decode output within
   |err| <= 2e-3 + 2e-2 |ref| (lse within 2e-3);
 * the cache bytes the step appended, and the indexer workspace's diagnostic
-  counters (bound waits that timed out, histograms that never summed), which
-  must stay 0.
+  counters (waits that gave up, histograms that never summed, rows selected
+  alone), which must stay 0.
 """
 
 import numpy as np
@@ -71,8 +71,8 @@ def _run_and_check(st, rows_to_check_extra, label):
     _say(f"[{label}] step")
     bench.dsa_step(ops, st)
     torch.cuda.synchronize()
-    counters = st["idx_ws"][:8].view(torch.int32).cpu().numpy()
-    assert counters[0] == 0 and counters[1] == 0, f"indexer counters {counters}"
+    counters = st["idx_ws"][:16].view(torch.int32).cpu().numpy()
+    assert not counters.any(), f"indexer counters {counters}"
     topk = st["topk"].cpu().numpy()
     merged = st["merged"].cpu().numpy()
     positions = st["positions"].cpu().numpy()

@@ -241,6 +241,17 @@ def test_indexer_topk_stages_match_one_call(dev):
     for t in range(T):
         row = got[t][got[t] >= 0]
         assert len(row) == min(lengths[t], TOPK) and np.all(row < lengths[t]) and np.all(np.diff(row) > 0)
+    # the one-call path (select inside the filter launch) writes the same
+    # top-k, merged rows and slots
+    for slots_mode, ref in ((False, ref_merged), (True, torch.from_numpy(ref_slots.astype(np.int32)).to(dev))):
+        d = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+        m = torch.full((T, TOPK + WINDOW + 5), -9, dtype=torch.int32, device=dev)
+        ops.indexer_topk_merged(q8, dig, wf, *args, st["max_len"], d, ws, merged=m, positions=positions,
+                                window=WINDOW, merged_slots=slots_mode)
+        assert torch.equal(a, d)
+        assert torch.equal(m, ref)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+    assert int(ws[256: ops.indexer_topk_counter_bytes()].view(torch.int32).abs().sum()) == 0
 
 
 def _device_cache(dev, seed, num_seqs, pages_per_seq, kind):
@@ -300,6 +311,8 @@ def _topk_vs_exact_path(dev, lengths, num_seqs, max_len, kind, seed, ws=None, ro
 def test_indexer_topk_long_rows_match_exact_path(dev, kind):
     """Rows long enough that one filter workgroup owns more than 2048 tokens
     (constant keys: all of them candidates, scored over several passes)."""
+    from ernie_kv import ops
+
     lengths = [262144, 200000, 131072, 70000, 2049, 5000, 0, 180000]
     T, max_len = len(lengths), 262144
     ws = _topk_vs_exact_path(dev, lengths, T, max_len, kind, seed=5)
@@ -307,7 +320,7 @@ def test_indexer_topk_long_rows_match_exact_path(dev, kind):
     # gave up, then (from byte 256) the fused kernel's per-row counters,
     # which every call leaves zero
     assert int(ws[:16].view(torch.int32).sum()) == 0
-    assert int(ws[256: 256 + T * 4100 * 4].view(torch.int32).abs().sum()) == 0
+    assert int(ws[256: ops.indexer_topk_counter_bytes()].view(torch.int32).abs().sum()) == 0
 
 
 def test_indexer_topk_million_token_row(dev):
@@ -347,7 +360,49 @@ def test_indexer_topk_workspace_reused_across_shapes(dev):
                         ws=ws)
     _topk_vs_exact_path(dev, [60000, 4000], 2, 60000, "constant", seed=35, ws=ws)
     assert int(ws[:16].view(torch.int32).sum()) == 0
-    assert int(ws[256: 256 + 1024 * 4100 * 4].view(torch.int32).abs().sum()) == 0
+    assert int(ws[256: ops.indexer_topk_counter_bytes()].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("kind", ["normal", "constant"])
+def test_indexer_topk_rows_select_alone_when_waits_give_up(dev, kind):
+    """With the waits' poll limit at 0 every workgroup that waits for the
+    rest of its row gives up at once: its bound is bin 0 (every token a
+    candidate) and the row's last workgroup to leave selects over the lists
+    alone.  The top-k still equals the exact path's, the row count of those
+    selects is counted, and the counters are left zero."""
+    from ernie_kv import ops
+
+    lengths = [70000, 2049, 0, 30000, 5000, 131072, 12345, 2048]
+    T, max_len = len(lengths), 131072
+    prev = ops.indexer_set_spin_limit(0)
+    try:
+        ws = _topk_vs_exact_path(dev, lengths, 4, max_len, kind, seed=81)
+    finally:
+        ops.indexer_set_spin_limit(prev)
+    counts = ws[:16].view(torch.int32).cpu().numpy()
+    long_rows = sum(1 for n in lengths if n > TOPK)
+    assert counts[2] == long_rows, f"counters {counts}"  # every row with waits selected alone
+    assert int(ws[256: ops.indexer_topk_counter_bytes()].view(torch.int32).abs().sum()) == 0
+    # and with the default limit again, nothing gives up
+    ws2 = _topk_vs_exact_path(dev, lengths, 4, max_len, kind, seed=82)
+    assert int(ws2[:16].view(torch.int32).sum()) == 0
+
+
+def test_indexer_topk_four_wave_plan(dev):
+    """300 query rows: more than one per CU, so the one-launch plan takes
+    4-wave workgroups (about three per CU, a row over one or two of them),
+    with the select in the same launch; rows long enough that some lists
+    exceed what the local select holds take the rounds over workgroups."""
+    from ernie_kv import ops
+
+    rng = np.random.default_rng(41)
+    lengths = rng.integers(0, 9000, 300).astype(np.int32).tolist()
+    lengths[:5] = [0, 2048, 2049, 9000, 6000]
+    ws = _topk_vs_exact_path(dev, lengths, 12, 9000, "normal", seed=43)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+    ws = _topk_vs_exact_path(dev, lengths[:40], 12, 9000, "constant", seed=44)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
+    assert int(ws[256: ops.indexer_topk_counter_bytes()].view(torch.int32).abs().sum()) == 0
 
 
 def test_indexer_topk_many_rows(dev):

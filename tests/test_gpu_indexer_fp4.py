@@ -224,7 +224,7 @@ def test_indexer_topk_fp4_end_to_end(dev, kind, spikes):
     rv, rs, rw = om.quantize_q(st["q"], st["w"])
     ref, _ = om.indexer_topk(rv, rs, rw, st["kcache"], st["bt"], st["req"], lengths, TOPK)
     assert np.array_equal(out.cpu().numpy(), ref)
-    assert int(ws[:8].view(torch.int32).sum()) == 0  # no bound wait gave up
+    assert int(ws[:16].view(torch.int32).sum()) == 0  # no wait gave up
 
 
 def test_indexer_topk_fp4_stages_and_merge(dev):
@@ -251,6 +251,14 @@ def test_indexer_topk_fp4_stages_and_merge(dev):
     ref_merged = torch.full_like(merged, -9)
     ops.merge_swa_topk(a, ref_merged, positions, WINDOW)
     assert torch.equal(merged, ref_merged)
+    # the one-call path (select inside the filter launch)
+    c = torch.full((T, TOPK), -9, dtype=torch.int32, device=dev)
+    m2 = torch.full_like(merged, -9)
+    ops.indexer_topk_merged_fp4(qv, qs, wf, *args, st["max_len"], c, ws, merged=m2, positions=positions,
+                                window=WINDOW)
+    assert torch.equal(a, c)
+    assert torch.equal(m2, ref_merged)
+    assert int(ws[:16].view(torch.int32).sum()) == 0
 
 
 def test_indexer_topk_fp4_many_rows(dev):

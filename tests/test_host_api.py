@@ -16,7 +16,7 @@ def _header_functions() -> dict[str, int]:
     """name -> number of parameters, parsed from include/ernie_kv.h."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(ekv_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|int32_t|int64_t|const char\*)\s+(ekv_\w+)\s*\(([^)]*)\)\s*;", text):
         params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
         out[m.group(1)] = len(params)
     return out

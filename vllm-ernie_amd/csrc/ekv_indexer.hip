@@ -957,16 +957,62 @@ __global__ void __launch_bounds__(256) verify_kernel(VerifyArgs a) {
 // the youngest waves finishing last.
 // The wait for the bound is bounded: a workgroup that gives up takes bin 0,
 // which makes every token of its segment a candidate -- slower, still exact.
+//
+// In-launch select (FusedArgs::sel_out set): the row's workgroups then also
+// agree on the exact top-k threshold and each writes its own selected tokens,
+// at offset (greater keys in earlier segments) + min(tied keys in earlier
+// segments, ties to take): segments are in token order, so the lowest
+// indices take the ties.
+//   * Exchange: each workgroup writes its candidate list (token, exact score)
+//     and count, arrives, and once the whole row has arrived reads the
+//     counts.  At least k tokens have a lower bound L in the bound bin b* or
+//     above, so the k-th largest exact key is >= lo = b* << 20.
+//   * Local select (the row's candidates fit a workgroup's LDS, 2 kList
+//     keys): every workgroup loads all of the row's keys and finds the
+//     threshold with histogram passes in LDS -- first [lo, lo + 2^22) in 4096
+//     bins of 2^10 keys (keys above in one more counter); a threshold bin
+//     whose keys are all needed ends the search, else the next pass splits
+//     its low 10 bits; if the window misses the threshold, passes of 12, 12
+//     and 8 bits over the whole key range follow (radix select).  The keys of
+//     the earlier segments give its offsets.
+//   * Otherwise the same passes run as rounds over the workgroups, each
+//     closed by the last to arrive, which publishes the decision the others
+//     wait for, and a records round exchanges each workgroup's (greater,
+//     tied) counts.
+// Every wait is bounded.  A workgroup that gives up marks the row; each
+// workgroup has written its candidate list before the exchange, and the last
+// to depart from a marked row selects over those lists alone (exact, slower)
+// and counts it in timeouts[2].
+// Outputs, lists and counters of this path are written with agent-scope
+// stores and read back with agent-scope loads, so they are coherent across
+// the XCDs' L2s within the launch.
 // ---------------------------------------------------------------------------
-// Per-row counters of the fused kernel, kCounterRow words per row at fixed
-// offsets at the front of the workspace: the row histogram, the arrival word
-// (arrivals in bits 0..15, departures in bits 16..31) and the bound word
-// ((bin << 20) | 1 once published).  They are zero when a call starts and the
-// call leaves them zero: the last workgroup to arrive zeroes the histogram
-// after reading it, the last to depart (after reading the bound) clears the
-// arrival and bound words.  So the fused path needs no clearing launch, only
-// a workspace that was zero-filled once.
-constexpr int kCounterRow = kHistBins + 4;
+// Per-row control block of the fused kernel, kCounterRow words per row at
+// fixed offsets at the front of the workspace:
+//   [0, kHistSlot)              histogram A: kHistBins bins, then [kHistBins]
+//                               keys above the bins, [kHistBins + 1] keys counted
+//   [kHistSlot, 2 kHistSlot)    histogram B (the rounds alternate A and B;
+//                               the bound uses A)
+//   kArriveWord                 arrivals (bits 0..15, cumulative over the
+//                               rounds) and departures (bits 16..31)
+//   kFailWord                   set when a wait of the row gave up
+//   kDecWords + 8 r             decision of round r (r = 0: the bound word,
+//                               (bin << 20) | 1 once published; r = 1, the
+//                               exchange, has none)
+//   kRecWords + 2 x             workgroup x's (greater, tied) counts
+// All of it is zero when a call starts and the call leaves it zero: a round's
+// last arriver zeroes its histogram after reading it, the last workgroup to
+// depart clears the arrival, fail and decision words and the records (and,
+// for a marked row, both histograms).  So the fused path needs no clearing
+// launch, only a workspace that was zero-filled once.
+constexpr int kHistSlot = kHistBins + 2;
+constexpr int kArriveWord = 2 * kHistSlot;
+constexpr int kFailWord = kArriveWord + 1;
+constexpr int kDecWords = kArriveWord + 4;
+constexpr int kSelRounds = 6;  // the bound, the exchange and at most four histogram rounds
+constexpr int kRecWords = kDecWords + 8 * kSelRounds;
+constexpr int kSelMaxGroups = 256;  // workgroups per row the in-launch select takes
+constexpr int kCounterRow = kRecWords + 2 * kSelMaxGroups;
 constexpr int kCounterRows = 1024;  // rows the fused path takes (at most 3 x CUs)
 constexpr int kHistRereads = 64;    // reads of a row histogram that does not yet sum to its tokens
 constexpr int64_t kCounterBytes = 256 + int64_t{kCounterRows} * kCounterRow * 4;
@@ -975,14 +1021,54 @@ struct FusedArgs {
   FilterArgs f;              // f.upper and f.hist are not used
   const int8_t* q_digits;    // [T, 3, 64, 128]
   uint32_t* counters;        // [kCounterRows, kCounterRow]
-  uint32_t* timeouts;        // [0] bound waits that gave up, [1] histograms that never summed to n
+  uint32_t* timeouts;        // [0] bound waits that gave up, [1] histograms that never summed,
+                             // [2] rows whose select ran alone after a wait gave up
                              // (diagnostic, cumulative)
   float* cand_score;         // [T, max_len] segment slices
   int32_t* cand_idx;
   int32_t* cand_count;       // [T, groups]
   int32_t groups;
   int32_t stage_pages;       // LDS capacity in pages (>= pages per workgroup of every row)
+  int32_t spin_limit;        // polls of a wait before it gives up
+  // In-launch select (null: the candidate lists are left for topk_select_kernel)
+  int32_t* sel_out;          // [T, sel_stride] top-k, ascending, -1 padded
+  int64_t sel_stride;
+  int32_t* merged;           // optional [T, merged_stride] rows of merge_swa_topk (see SelectArgs)
+  int64_t merged_stride;
+  int32_t merged_width;
+  const int64_t* positions;
+  int32_t window;
+  int32_t merged_slots;      // merged entries as cache slots through the block table
 };
+
+__device__ __forceinline__ uint32_t ld_agent(const void* p) {
+  return __hip_atomic_load(static_cast<const uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(void* p, uint32_t v) {
+  __hip_atomic_store(static_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS histogram increment: the lanes sharing a bin with the first remaining
+// lane add with one atomic, twice; the others one atomic per lane.  Runs of
+// equal keys (ties) then cost one or two atomics per wave instead of one per
+// lane on the same address.
+__device__ __forceinline__ void hist_add_ties(uint32_t* hist, int bin) {
+  const int lane = threadIdx.x & 63;
+  uint64_t act = __ballot(bin >= 0);
+  // two rounds: the lanes sharing the first remaining lane's bin add with
+  // one atomic (a tie group, most of a wave in tie-heavy rows, is taken in
+  // one of them); the rest add one each
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (act == 0) return;
+    const int leader = static_cast<int>(__builtin_ctzll(act));
+    const int lb = __builtin_amdgcn_readlane(bin, leader);
+    const uint64_t same = __ballot(bin == lb) & act;
+    if (lane == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(same)));
+    act &= ~same;
+  }
+  if ((act >> lane) & 1u) atomicAdd(&hist[bin], 1u);
+}
 
 // Pages of each workgroup's segment: workgroup x of a row owns logical pages
 // [x, x + 1) * fused_group_pages.
@@ -992,7 +1078,8 @@ __host__ __device__ inline int fused_group_pages(int n, int groups) {
 }
 
 constexpr int kFusedQdBytes = 4 * 3 * 2 * 64 * 16;  // q digit operands [hb][digit][K half][lane]
-constexpr int kFusedSpinLimit = 1 << 14;
+constexpr int kFusedSpinLimit = 1 << 14;            // default FusedArgs::spin_limit
+static_assert(kHistSlot * 4 <= kFusedQdBytes, "a select round's LDS histogram shares the q operands' LDS");
 
 template <int kWaves>
 struct FusedLayout {
@@ -1001,6 +1088,128 @@ struct FusedLayout {
   // q operands / histogram | table | list | list scores | misc
   static constexpr int kFixed = kFusedQdBytes + 256 * 4 + 2 * kList * 4 + 32 * 4;
   static constexpr int bytes(int stage_pages) { return kFixed + stage_pages * (4 + 2 * kPageTokens); }
+};
+
+// The bin of an nbins-bin histogram (read(b) = count of bin b, `above` keys
+// past the bins) holding the k-th largest key: (keys above bin fb) < k <=
+// (keys above fb) + h.  fb = -1 when the bins and `above` cannot hold it.
+template <int kThreads, class Read>
+__device__ __forceinline__ void find_threshold_bin(Read read, int nbins, int above, int k, int* s_misc, int& fb,
+                                                   int& above_f, int& h) {
+  constexpr int kPer = (kHistBins + kThreads - 1) / kThreads;  // bins per thread, from the top down
+  const int rb0 = kPer * static_cast<int>(threadIdx.x);
+  int hc[kPer];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    hc[j] = (rb0 + j < nbins) ? read(nbins - 1 - (rb0 + j)) : 0;
+    sum += hc[j];
+  }
+  if (threadIdx.x == 0) s_misc[28] = -1;
+  int total;
+  int e = above + block_scan_excl<kThreads>(sum, s_misc, total);  // keys above this thread's first bin
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (rb0 + j < nbins && e < k && k <= e + hc[j]) {
+      s_misc[28] = nbins - 1 - (rb0 + j);
+      s_misc[29] = e;
+      s_misc[30] = hc[j];
+    }
+    e += hc[j];
+  }
+  __syncthreads();
+  fb = s_misc[28];
+  above_f = s_misc[29];
+  h = s_misc[30];
+  __syncthreads();
+}
+
+// What a histogram pass over keys >= lo (bins of 2^shift keys) decides, from
+// its threshold bin fb (above_f keys above it, h in it):
+//   1: another pass: p = (lo, shift, nbins, keys >= lo) -- the bin's low
+//      bits split 12 at a time, or, when the first pass's window missed
+//      (fb < 0), 12 bits of the whole key range;
+//   2: final: p = (thr_lo, thr_hi, ties to take): keys >= thr_hi are taken,
+//      then `need` keys of [thr_lo, thr_hi) -- the bin's lower edge when all
+//      its keys are needed, else its single key;
+//   3: no decision (a pass after the first whose window misses).
+__device__ inline int select_decision(bool first, uint32_t lo, int shift, int k, int fb, int above_f, int h,
+                                      uint32_t (&p)[5]) {
+  p[0] = p[1] = p[2] = p[3] = p[4] = 0u;
+  if (fb < 0) {
+    if (!first) return 3;
+    p[1] = 20u;
+    p[2] = static_cast<uint32_t>(kHistBins);
+    p[3] = 0xffffffffu;
+    return 1;
+  }
+  const int nd = k - above_f;
+  const uint32_t base = lo + (static_cast<uint32_t>(fb) << shift);
+  if (nd == h) {
+    p[0] = p[1] = base;
+    return 2;
+  }
+  if (shift == 0) {
+    p[0] = base;
+    p[1] = base + 1u;
+    p[2] = static_cast<uint32_t>(nd);
+    return 2;
+  }
+  const int next = shift > kHistBits ? shift - kHistBits : 0;  // split the bin's low bits, 12 at a time
+  p[0] = base;
+  p[1] = static_cast<uint32_t>(next);
+  p[2] = 1u << (shift - next);
+  p[3] = static_cast<uint32_t>(above_f + h);
+  return 1;
+}
+
+// The in-launch select's outputs of row t: the top-k row and the optional
+// merged row, whose entry for token i is i or, with merged_slots, its cache
+// slot through the block table (-1 when unmapped).  Built where it is used,
+// so none of it stays live across the page stream.
+struct SelRow {
+  int32_t* out;
+  int32_t* merged;
+  int64_t seq, m_topk, width, window;
+  const int32_t* bt;  // null unless merged_slots
+  int64_t bt_stride, num_pages;
+  __device__ SelRow(const FusedArgs& a, int t)
+      : out(a.sel_out + static_cast<int64_t>(t) * a.sel_stride),
+        merged(a.merged ? a.merged + static_cast<int64_t>(t) * a.merged_stride : nullptr),
+        seq(0), m_topk(0), width(a.merged_width), window(a.window), bt(nullptr), bt_stride(a.f.bt_stride),
+        num_pages(a.f.num_pages) {
+    if (merged) {
+      seq = a.positions[t] + 1;
+      m_topk = min(min(max(seq - window, int64_t{0}), static_cast<int64_t>(a.f.k)), width);
+      if (a.merged_slots) bt = a.f.block_table + static_cast<int64_t>(a.f.req_ids[t]) * a.f.bt_stride;
+    }
+  }
+  __device__ uint32_t entry(int64_t i) const {
+    if (bt == nullptr || i < 0) return static_cast<uint32_t>(i);
+    if ((i >> 6) >= bt_stride) return 0xffffffffu;
+    const int64_t p = bt[i >> 6];
+    return (p >= 0 && p < num_pages) ? static_cast<uint32_t>(p * kPageTokens + (i & 63)) : 0xffffffffu;
+  }
+  // output entry pos = token tok (or -1); the merged entry from the block table
+  __device__ void emit(int64_t pos, int64_t tok) const {
+    st_agent(out + pos, static_cast<uint32_t>(tok));
+    if (merged && pos < m_topk) st_agent(merged + pos, entry(tok));
+  }
+  // the same with the token's page known (-1: unmapped)
+  __device__ void emit_paged(int64_t pos, int64_t tok, int64_t page) const {
+    st_agent(out + pos, static_cast<uint32_t>(tok));
+    if (merged && pos < m_topk)
+      st_agent(merged + pos, bt == nullptr ? static_cast<uint32_t>(tok)
+                                           : (page >= 0 ? static_cast<uint32_t>(page * kPageTokens + (tok & 63))
+                                                        : 0xffffffffu));
+  }
+  // entries [m_topk, width) of the merged row: the window, then -1
+  __device__ void window_part(int tid, int nthreads) const {
+    if (!merged) return;
+    const int64_t w = min(seq, window);
+    for (int64_t c = m_topk + tid; c < width; c += nthreads)
+      st_agent(merged + c, (c < m_topk + w) ? entry(seq - w + (c - m_topk)) : 0xffffffffu);
+  }
 };
 
 // fp4 keys: the q operands of the exact path, [hb][block][lane] 8-byte words.
@@ -1033,12 +1242,27 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const int seg_len = min(per_group * kPageTokens, n - seg0);
   const int64_t out0 = static_cast<int64_t>(t) * f.max_len + seg0;
   int32_t* count = a.cand_count + static_cast<int64_t>(t) * a.groups + x;
+
+  const bool sel = a.sel_out != nullptr;
+  if (sel && x == 0) {
+    // the window part of the merged row, and the -1 fill past n when every
+    // token is selected (also for rows without tokens)
+    const SelRow so(a, t);
+    so.window_part(tid, kThreads);
+    if (n <= f.k)
+      for (int i = n + tid; i < f.k; i += kThreads) so.emit(i, -1);
+  }
   if (seg_len <= 0) {  // no pages in this segment
     if (tid == 0) *count = 0;
     return;
   }
   if (n <= f.k) {  // every token is selected: list them, no scores needed
-    for (int i = tid; i < seg_len; i += kThreads) a.cand_idx[out0 + i] = seg0 + i;
+    if (sel) {
+      const SelRow so(a, t);
+      for (int i = tid; i < seg_len; i += kThreads) so.emit(seg0 + i, seg0 + i);
+    } else {
+      for (int i = tid; i < seg_len; i += kThreads) a.cand_idx[out0 + i] = seg0 + i;
+    }
     if (tid == 0) *count = seg_len;
     return;
   }
@@ -1067,20 +1291,23 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                         if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
                       });
   __syncthreads();
-  uint32_t* gh = a.counters + static_cast<int64_t>(t) * kCounterRow;
-  uint32_t* const arrive = gh + kHistBins;
-  uint32_t* const kword = gh + kHistBins + 1;
+  uint32_t* const rowc = a.counters + static_cast<int64_t>(t) * kCounterRow;
+  uint32_t* const gh = rowc;  // histogram A
+  uint32_t* const arrive = rowc + kArriveWord;
+  uint32_t* const kword = rowc + kDecWords;
   for (int i = tid; i < kHistBins; i += kThreads) {
     const uint32_t v = s_hist[i];
     if (v) atomicAdd(&gh[i], v);
   }
-  // q exact operands, into the histogram's LDS once every lane is past it
-  // (fp8: digit planes; fp4: the 2 * e2m1 values, [hb][block][lane]).
+  // q exact operands, loaded now and stored into the histogram's LDS once
+  // every lane is past it (fp8: digit planes; fp4: the 2 * e2m1 values,
+  // [hb][block][lane]).
   constexpr int kQdPer = (kFusedQdBytes / 16) / kThreads;
   static_assert(kQdPer * kThreads * 16 == kFusedQdBytes, "q digit staging must divide evenly");
   constexpr int kQ4Per = (kFusedQ4Words + kThreads - 1) / kThreads;
-  uint4 qd_regs[kFp4 ? 1 : kQdPer];
-  uint2 q4_regs[kFp4 ? kQ4Per : 1];
+  // (native vectors: kept in registers)
+  i32x4 qd_regs[kFp4 ? 1 : kQdPer];
+  i32x2 q4_regs[kFp4 ? kQ4Per : 1];
   if constexpr (kFp4) {
 #pragma unroll
     for (int j = 0; j < kQ4Per; ++j) {
@@ -1088,7 +1315,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       const int e = idx >> 6, ln = idx & 63;
       int64_t v = 0;
       if (idx < kFusedQ4Words) v = load_q_fp4(f.q_fp8, t, e >> 2, e & 3, ln >> 4, ln & 15);
-      q4_regs[j] = make_uint2(static_cast<uint32_t>(v), static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+      q4_regs[j] = i32x2{static_cast<int>(v), static_cast<int>(static_cast<uint64_t>(v) >> 32)};
     }
   } else {
 #pragma unroll
@@ -1097,7 +1324,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       const int e = idx >> 6, ln = idx & 63;
       const int hb = e / 6, d = (e / 2) % 3, kh = e & 1;
       const int lg = ln >> 4, lc = ln & 15;
-      qd_regs[j] = *reinterpret_cast<const uint4*>(
+      qd_regs[j] = *reinterpret_cast<const i32x4*>(
           a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + lc) * kIdxDim + 64 * kh + 16 * lg);
     }
   }
@@ -1108,6 +1335,18 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // candidates, still exact).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // (every lane is past the histogram: the q operands take its LDS now, so
+  // they are not held in registers across the wait below)
+  if constexpr (kFp4) {
+    i32x2* s_q4_w = reinterpret_cast<i32x2*>(fused_smem);
+#pragma unroll
+    for (int j = 0; j < kQ4Per; ++j)
+      if (tid + kThreads * j < kFusedQ4Words) s_q4_w[tid + kThreads * j] = q4_regs[j];
+  } else {
+    i32x4* s_qd_w = reinterpret_cast<i32x4*>(fused_smem);
+#pragma unroll
+    for (int j = 0; j < kQdPer; ++j) s_qd_w[tid + kThreads * j] = qd_regs[j];
+  }
 
   // Phase 2: arrive; the last workgroup of the row publishes the bound.
   // Every workgroup reads the row histogram as it arrives (the last one to
@@ -1132,16 +1371,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_misc[16] = ((before & 0xffffu) + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
     s_misc[17] = 0;
-  }
-  if constexpr (kFp4) {
-    uint2* s_q4_w = reinterpret_cast<uint2*>(fused_smem);
-#pragma unroll
-    for (int j = 0; j < kQ4Per; ++j)
-      if (tid + kThreads * j < kFusedQ4Words) s_q4_w[tid + kThreads * j] = q4_regs[j];
-  } else {
-    uint4* s_qd_w = reinterpret_cast<uint4*>(fused_smem);
-#pragma unroll
-    for (int j = 0; j < kQdPer; ++j) s_qd_w[tid + kThreads * j] = qd_regs[j];
+    s_misc[19] = 0;  // a wait of this workgroup gave up
   }
   __syncthreads();
   if (s_misc[16]) {
@@ -1180,17 +1410,21 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         __hip_atomic_store(gh + (kHistBins - 1 - (r0 + j)), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else if (tid == 0) {
     uint32_t v = 0;
-    for (int spins = 0; spins < kFusedSpinLimit; ++spins) {
+    for (int spins = 0; spins < a.spin_limit; ++spins) {
       v = __hip_atomic_load(kword, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (v != 0) break;
       __builtin_amdgcn_s_sleep(4);
     }
-    if (v == 0) atomicAdd(a.timeouts, 1u);  // bin 0: every token is a candidate
+    if (v == 0) {  // bin 0: every token is a candidate
+      atomicAdd(a.timeouts, 1u);
+      s_misc[19] = 1;
+    }
     s_misc[17] = static_cast<int>(v >> (32 - kHistBits));
   }
   // depart: the last workgroup of the row to hold the bound clears the
-  // bound and arrival words (the last arriver departs after publishing)
-  if (tid == 0) {
+  // bound and arrival words (the last arriver departs after publishing).
+  // With the in-launch select the workgroups depart after the select.
+  if (tid == 0 && !sel) {
     __builtin_amdgcn_s_waitcnt(0);
     const uint32_t before = __hip_atomic_fetch_add(arrive, 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((before >> 16) + 1u == static_cast<uint32_t>(groups_row)) {
@@ -1200,6 +1434,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   }
   __syncthreads();
   const uint32_t bin = static_cast<uint32_t>(s_misc[17]);
+  const bool bound_gave_up = s_misc[19] != 0;
 
   // Phase 3: candidates of the segment in order, scored Lay::kList at a time.
   auto score_list = [&](int cnt, int base) {
@@ -1284,8 +1519,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     __syncthreads();
     for (int i = tid; i < cnt; i += kThreads) {
-      a.cand_score[out0 + base + i] = s_score[i];
-      a.cand_idx[out0 + base + i] = seg0 + s_list[i];
+      st_agent(a.cand_score + out0 + base + i, __float_as_uint(s_score[i]));
+      st_agent(a.cand_idx + out0 + base + i, static_cast<uint32_t>(seg0 + s_list[i]));
     }
     // the list's LDS may be refilled after this; the stores need not have
     // completed (a barrier with a fence would wait for them)
@@ -1294,6 +1529,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // One scan over the whole segment (kOnePass groups of 8 tokens per thread)
   // when it is short enough and its candidates fit the list.
   constexpr int kOnePass = 3;
+  int out_n = 0, lds_n = 0;  // candidates listed; the last lds_n of them are still in LDS
+  bool listed = false;
   if (seg_len <= 8 * kOnePass * kThreads) {
     const int o0 = 8 * kOnePass * tid;
     uint32_t flags = 0;
@@ -1321,45 +1558,521 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       for (int b = 0; b < 8 * kOnePass; ++b)
         if (flags & (1u << b)) s_list[pos++] = o0 + b;
       if (tot > 0) score_list(tot, 0);
-      if (tid == 0) *count = tot;
-      return;
+      out_n = lds_n = tot;
+      listed = true;
     }
   }
-  int out_n = 0, list_n = 0;
-  for (int r0 = 0; r0 < seg_len; r0 += 8 * kThreads) {
-    const int o0 = r0 + 8 * tid;
-    uint32_t flags = 0;
-    int cnt = 0;
-    if (o0 < seg_len) {
-      const uint4 v = *reinterpret_cast<const uint4*>(s_pref + o0);
-      const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+  if (!listed) {
+    int list_n = 0;
+    for (int r0 = 0; r0 < seg_len; r0 += 8 * kThreads) {
+      const int o0 = r0 + 8 * tid;
+      uint32_t flags = 0;
+      int cnt = 0;
+      if (o0 < seg_len) {
+        const uint4 v = *reinterpret_cast<const uint4*>(s_pref + o0);
+        const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t pref = (wds[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-        if (o0 + j < seg_len && pref >= bin) {
-          flags |= 1u << j;
-          ++cnt;
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t pref = (wds[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+          if (o0 + j < seg_len && pref >= bin) {
+            flags |= 1u << j;
+            ++cnt;
+          }
+        }
+      }
+      int rtot;
+      const int ex = block_scan_excl<kThreads>(cnt, s_misc, rtot);
+      if (list_n + rtot > Lay::kList) {  // uniform
+        score_list(list_n, out_n);
+        out_n += list_n;
+        lds_n = list_n;
+        list_n = 0;
+      }
+      int pos = list_n + ex;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (flags & (1u << j)) s_list[pos++] = o0 + j;
+      list_n += rtot;
+    }
+    if (list_n > 0) {
+      score_list(list_n, out_n);
+      out_n += list_n;
+      lds_n = list_n;
+    }
+  }
+  if (tid == 0) st_agent(count, static_cast<uint32_t>(out_n));
+  if (!sel) return;
+
+  // ---- In-launch select (see the comment above FusedArgs) ----
+  const int G = groups_row;
+  const int lds_base = out_n - lds_n;
+  uint32_t* const s_lh = reinterpret_cast<uint32_t*>(fused_smem);  // pass histogram (q operands are done)
+  int* const s_off = reinterpret_cast<int*>(s_table);              // [G] offsets of the row's lists
+  int* const s_dec = s_misc + 20;  // [20..25] a round's decision; s_misc[26..31] scratch
+  uint32_t* const failw = rowc + kFailWord;
+  auto key_at = [&](int i) -> uint32_t {  // exact score key of entry i of this workgroup's list
+    const float sc = (i >= lds_base) ? s_score[i - lds_base] : __uint_as_float(ld_agent(a.cand_score + out0 + i));
+    return score_key(sc + 0.0f);
+  };
+  auto tok_at = [&](int i) -> int64_t {  // its token
+    return (i >= lds_base) ? static_cast<int64_t>(seg0 + s_list[i - lds_base])
+                           : static_cast<int64_t>(static_cast<int32_t>(ld_agent(a.cand_idx + out0 + i)));
+  };
+  bool failed = bound_gave_up;
+
+  // Exchange: once every workgroup of the row has written its list and count
+  // (agent-scope stores, completed before it arrives), each reads the counts.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    bool all_in = false;
+    if (!failed) {
+      const uint32_t target = 2u * static_cast<uint32_t>(G);
+      const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      all_in = (before & 0xffffu) + 1u >= target;
+      for (int spins = 0; !all_in && spins < a.spin_limit; ++spins) {
+        __builtin_amdgcn_s_sleep(4);
+        all_in = (ld_agent(arrive) & 0xffffu) >= target;
+        if (!all_in && ld_agent(failw) != 0) break;
+      }
+    }
+    s_misc[16] = all_in ? 1 : 0;
+    s_misc[17] = 0;
+  }
+  __syncthreads();
+  failed = s_misc[16] == 0;
+  int n_row = 0, max_list = 0;
+  if (!failed) {
+    const int cy = (tid < G) ? static_cast<int>(ld_agent(a.cand_count + static_cast<int64_t>(t) * a.groups + tid)) : 0;
+    if (tid == 0) s_misc[27] = 0;
+    const int ex = block_scan_excl<kThreads>(cy, s_misc, n_row);
+    if (tid < G) s_off[tid] = ex;
+    if (tid == x && cy != out_n) s_misc[17] = 1;  // (a count that is not this call's)
+    int cm = cy;
+    for (int off = 32; off > 0; off >>= 1) cm = max(cm, __shfl_xor(cm, off));
+    if ((tid & 63) == 0 && cm > 0) atomicMax(s_misc + 27, cm);
+    __syncthreads();
+    failed = s_misc[17] != 0;
+    max_list = s_misc[27];
+  }
+
+  const SelRow so(a, t);  // (its loads in flight during the select)
+
+  // Local select: with the row's candidates fitting LDS beside this
+  // workgroup's list, every workgroup loads all their keys (in list order, so
+  // segment by segment) and finds the threshold itself, histogram passes over
+  // LDS; its offsets count the keys of the segments before its own.  No
+  // further exchange.
+  // (the keys go after this workgroup's list tokens, over its scores; the
+  // choice is the same in every workgroup of the row: from the counts, every
+  // list in LDS and the longest beside all the keys)
+  const bool local = !failed && max_list <= Lay::kList && max_list + n_row <= 2 * Lay::kList;
+  uint32_t* const s_key = reinterpret_cast<uint32_t*>(s_list + out_n);  // [n_row]
+  uint32_t thr_lo = 0, thr_hi = 0;  // selected: keys >= thr_hi, then ties in [thr_lo, thr_hi)
+  int need = 0, gt_before = 0, eq_before = 0, my0 = 0;
+  const int64_t row0 = static_cast<int64_t>(t) * f.max_len;
+  const int64_t seg_tokens = static_cast<int64_t>(per_group) * kPageTokens;
+  if (local) {
+    my0 = s_off[x];
+    __syncthreads();  // the scores' LDS becomes the keys
+    constexpr int kKeys = 8;  // loads in flight per thread
+    uint32_t kmax = 0u;       // the row's largest key
+    if (tid == 0) s_misc[26] = 0;
+    for (int p0 = 0; p0 < n_row; p0 += kKeys * kThreads) {
+      float v[kKeys];
+#pragma unroll
+      for (int j = 0; j < kKeys; ++j) {
+        const int p = p0 + tid + j * kThreads;
+        v[j] = 0.0f;
+        if (p < n_row) {
+          int y = 0, hi = G - 1;  // the last list with s_off[y] <= p (empty lists are skipped)
+          while (y < hi) {
+            const int mid = (y + hi + 1) >> 1;
+            if (s_off[mid] <= p) y = mid;
+            else hi = mid - 1;
+          }
+          v[j] = __uint_as_float(ld_agent(a.cand_score + row0 + y * seg_tokens + (p - s_off[y])));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kKeys; ++j) {
+        const int p = p0 + tid + j * kThreads;
+        if (p < n_row) {
+          const uint32_t key = score_key(v[j] + 0.0f);
+          s_key[p] = key;
+          kmax = max(kmax, key);
         }
       }
     }
-    int rtot;
-    const int ex = block_scan_excl<kThreads>(cnt, s_misc, rtot);
-    if (list_n + rtot > Lay::kList) {  // uniform
-      score_list(list_n, out_n);
-      out_n += list_n;
-      list_n = 0;
+    for (int off = 32; off > 0; off >>= 1) kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), off)));
+    if ((tid & 63) == 0) atomicMax(reinterpret_cast<uint32_t*>(s_misc + 26), kmax);
+    __syncthreads();
+    kmax = static_cast<uint32_t>(s_misc[26]);
+    uint32_t lo = bin << (32 - kHistBits);  // the k-th largest exact key is >= lo
+    // first pass: [lo, lo + 2^22) in bins of 2^10 keys, or wider bins when
+    // the keys reach beyond that (so the pass always holds the threshold)
+    int shift = 10, nbins = kHistBins;
+    if (kmax >= lo) {
+      const uint32_t span = (kmax - lo) >> 10;
+      if (span >= static_cast<uint32_t>(kHistBins)) shift = 10 + (32 - __clz(static_cast<int>(span))) - kHistBits;
     }
-    int pos = list_n + ex;
+    for (bool first = true;; first = false) {
+      for (int i = tid; i <= kHistBins; i += kThreads) s_lh[i] = 0;
+      __syncthreads();
+      for (int p0 = 0; p0 < n_row; p0 += kThreads) {
+        const int p = p0 + tid;
+        int b = -1;
+        if (p < n_row) {
+          const uint32_t key = s_key[p];
+          if (key >= lo) {
+            const uint32_t d = (key - lo) >> shift;
+            b = (d >= static_cast<uint32_t>(nbins)) ? kHistBins : static_cast<int>(d);
+          }
+        }
+        hist_add_ties(s_lh, b);
+      }
+      __syncthreads();
+      int fb, above_f, h;
+      find_threshold_bin<kThreads>([&](int bb) { return static_cast<int>(s_lh[bb]); }, nbins,
+                                   static_cast<int>(s_lh[kHistBins]), f.k, s_misc, fb, above_f, h);
+      uint32_t pd[5];
+      const int kind = select_decision(first, lo, shift, f.k, fb, above_f, h, pd);
+      if (kind == 2) {
+        thr_lo = pd[0];
+        thr_hi = pd[1];
+        need = static_cast<int>(pd[2]);
+        break;
+      }
+      if (kind != 1) {  // (cannot happen: the keys are the row's candidates, all exact)
+        failed = true;
+        break;
+      }
+      lo = pd[0];
+      shift = static_cast<int>(pd[1]);
+      nbins = static_cast<int>(pd[2]);
+    }
+    int gtc = 0, eqc = 0;
+    for (int p = tid; p < my0; p += kThreads) {
+      const uint32_t key = s_key[p];
+      gtc += key >= thr_hi;
+      eqc += (key >= thr_lo) && (key < thr_hi);
+    }
+    (void)block_scan_excl<kThreads>(gtc, s_misc, gt_before);
+    (void)block_scan_excl<kThreads>(eqc, s_misc, eq_before);
+  }
+
+  // Rows with more candidates than LDS holds: rounds over the workgroups,
+  // each closed by its last arriver, which publishes the decision.
+  int rnd = 2;  // round 0 was the bound, round 1 the exchange
+  if (!failed && !local) {
+    uint32_t lo = bin << (32 - kHistBits);
+    int shift = 10, nbins = kHistBins;
+    int expect = -1;  // keys >= lo in the row, when known
+    int gt_total = 0, eq_total = 0;
+    constexpr int kPer = (kHistBins + kThreads - 1) / kThreads;  // bins per thread, scanned from the top down
+    while (!failed) {
+      uint32_t* const hr = rowc + (rnd & 1) * kHistSlot;
+      uint32_t* const dec = rowc + kDecWords + 8 * rnd;
+      for (int i = tid; i <= kHistBins; i += kThreads) s_lh[i] = 0;
+      __syncthreads();
+      int mine = 0;
+      for (int i0 = 0; i0 < out_n; i0 += kThreads) {
+        const int i = i0 + tid;
+        int b = -1;
+        if (i < out_n) {
+          const uint32_t key = key_at(i);
+          if (key >= lo) {
+            const uint32_t d = (key - lo) >> shift;
+            b = (d >= static_cast<uint32_t>(nbins)) ? kHistBins : static_cast<int>(d);  // kHistBins: above
+            ++mine;
+          }
+        }
+        hist_add_ties(s_lh, b);
+      }
+      int counted;
+      (void)block_scan_excl<kThreads>(mine, s_misc, counted);  // (its barriers also complete s_lh)
+      for (int i = tid; i <= kHistBins; i += kThreads) {
+        const uint32_t v = s_lh[i];
+        if (v) atomicAdd(hr + i, v);
+      }
+      if (tid == 0 && counted) atomicAdd(hr + kHistBins + 1, static_cast<uint32_t>(counted));
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_misc[16] = ((before & 0xffffu) + 1u == static_cast<uint32_t>((rnd + 1) * G)) ? 1 : 0;
+      }
+      __syncthreads();
+      if (s_misc[16]) {
+        // Last to arrive: every workgroup's adds completed before it arrived.
+        // The bins and the above counter must sum to the keys counted (and to
+        // the keys the previous decision expects at or above lo).
+        bool ok = false;
+        int above = 0;
+        for (int attempt = 0;; ++attempt) {
+          if (tid == 0) {
+            s_misc[26] = static_cast<int>(ld_agent(hr + kHistBins));
+            s_misc[27] = static_cast<int>(ld_agent(hr + kHistBins + 1));
+          }
+          const int rb0 = kPer * tid;
+          int sum = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (flags & (1u << j)) s_list[pos++] = o0 + j;
-    list_n += rtot;
+          for (int j = 0; j < kPer; ++j)
+            sum += (rb0 + j < nbins) ? static_cast<int>(ld_agent(hr + (nbins - 1 - (rb0 + j)))) : 0;
+          int total;
+          (void)block_scan_excl<kThreads>(sum, s_misc, total);
+          above = s_misc[26];
+          ok = (total + above == s_misc[27]) && (expect < 0 || s_misc[27] == expect);
+          __syncthreads();  // before s_misc[26..27] are written again
+          if (ok || attempt == kHistRereads) break;
+          __builtin_amdgcn_s_sleep(8);
+        }
+        int fb = -1, above_f = 0, h = 0;
+        if (ok)
+          find_threshold_bin<kThreads>([&](int bb) { return static_cast<int>(ld_agent(hr + bb)); }, nbins, above,
+                                       f.k, s_misc, fb, above_f, h);
+        if (tid == 0) {
+          uint32_t pd[5] = {0u, 0u, 0u, 0u, 0u};
+          int kind = 3;
+          if (!ok) atomicAdd(a.timeouts + 1, 1u);
+          else kind = select_decision(rnd == 2, lo, shift, f.k, fb, above_f, h, pd);
+          if (kind == 2) {  // the final decision carries the row's totals of greater and tied keys
+            pd[3] = static_cast<uint32_t>(pd[0] == pd[1] ? f.k : above_f);
+            pd[4] = static_cast<uint32_t>(pd[0] == pd[1] ? 0 : h);
+          }
+          s_dec[0] = kind;
+#pragma unroll
+          for (int w = 0; w < 5; ++w) {
+            s_dec[1 + w] = static_cast<int>(pd[w]);
+            st_agent(dec + 1 + w, pd[w]);
+          }
+          __builtin_amdgcn_s_waitcnt(0);  // the payload before the word that announces it
+          st_agent(dec, static_cast<uint32_t>(kind));
+        }
+        // leave the histogram zero (everyone has arrived; nobody reads it again)
+        for (int i = tid; i < nbins; i += kThreads) st_agent(hr + i, 0u);
+        if (tid == 0) {
+          st_agent(hr + kHistBins, 0u);
+          st_agent(hr + kHistBins + 1, 0u);
+        }
+      } else if (tid == 0) {
+        uint32_t v = 0;
+        for (int spins = 0; spins < a.spin_limit; ++spins) {
+          v = ld_agent(dec);
+          if (v != 0 || ld_agent(failw) != 0) break;
+          __builtin_amdgcn_s_sleep(4);
+        }
+        s_dec[0] = (v != 0) ? static_cast<int>(v) : 3;
+        if (v != 0)
+#pragma unroll
+          for (int w = 0; w < 5; ++w) s_dec[1 + w] = static_cast<int>(ld_agent(dec + 1 + w));
+      }
+      __syncthreads();
+      const int kind = s_dec[0];
+      if (kind == 2) {
+        thr_lo = static_cast<uint32_t>(s_dec[1]);
+        thr_hi = static_cast<uint32_t>(s_dec[2]);
+        need = s_dec[3];
+        gt_total = s_dec[4];
+        eq_total = s_dec[5];
+      } else if (kind == 1) {
+        lo = static_cast<uint32_t>(s_dec[1]);
+        shift = s_dec[2];
+        nbins = s_dec[3];
+        expect = s_dec[4];
+      } else {
+        failed = true;
+      }
+      __syncthreads();  // s_dec and s_misc are reused
+      if (kind != 1) break;
+      if (++rnd >= kSelRounds) failed = true;  // (at most four histogram rounds are ever decided)
+    }
+
+    // Records round: this workgroup's (greater, tied) counts; its offsets
+    // are the sums over the row's earlier workgroups.
+    uint32_t* const rec = rowc + kRecWords;
+    if (!failed) {
+      int gt = 0, eq = 0;
+      for (int i = tid; i < out_n; i += kThreads) {
+        const uint32_t key = key_at(i);
+        gt += key >= thr_hi;
+        eq += (key >= thr_lo) && (key < thr_hi);
+      }
+      int gt_x, eq_x;
+      (void)block_scan_excl<kThreads>(gt, s_misc, gt_x);
+      (void)block_scan_excl<kThreads>(eq, s_misc, eq_x);
+      if (tid == 0) {
+        st_agent(rec + 2 * x, static_cast<uint32_t>(gt_x));
+        st_agent(rec + 2 * x + 1, static_cast<uint32_t>(eq_x));
+        __builtin_amdgcn_s_waitcnt(0);
+        const uint32_t target = static_cast<uint32_t>((rnd + 2) * G);
+        const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool all_in = (before & 0xffffu) + 1u >= target;
+        for (int spins = 0; !all_in && spins < a.spin_limit; ++spins) {
+          __builtin_amdgcn_s_sleep(4);
+          all_in = (ld_agent(arrive) & 0xffffu) >= target;
+          if (!all_in && ld_agent(failw) != 0) break;
+        }
+        s_misc[16] = all_in ? 1 : 0;
+      }
+      __syncthreads();
+      if (!s_misc[16]) failed = true;
+      for (int attempt = 0; !failed; ++attempt) {
+        int gy = 0, ey = 0;
+        if (tid < G) {
+          gy = static_cast<int>(ld_agent(rec + 2 * tid));
+          ey = static_cast<int>(ld_agent(rec + 2 * tid + 1));
+        }
+        int gsum, esum;
+        const int gex = block_scan_excl<kThreads>(gy, s_misc, gsum);
+        const int eex = block_scan_excl<kThreads>(ey, s_misc, esum);
+        if (tid == x) {
+          s_misc[28] = gex;
+          s_misc[29] = eex;
+        }
+        __syncthreads();
+        gt_before = s_misc[28];
+        eq_before = s_misc[29];
+        __syncthreads();
+        if (gsum == gt_total && esum == eq_total) break;
+        if (attempt == kHistRereads) failed = true;
+        __builtin_amdgcn_s_sleep(8);
+      }
+    }
   }
-  if (list_n > 0) {
-    score_list(list_n, out_n);
-    out_n += list_n;
+
+  // Ordered output of this segment's selected tokens: a selected key's
+  // position is (greater keys before it) + min(tied keys before it, need).
+  if (!failed) {
+    auto okey = [&](int i) -> uint32_t { return local ? s_key[my0 + i] : key_at(i); };
+    auto otok = [&](int i) -> int64_t { return local ? static_cast<int64_t>(seg0 + s_list[i]) : tok_at(i); };
+    auto emit = [&](int pos, int64_t tok) { so.emit_paged(pos, tok, s_pages[(tok - seg0) >> 6]); };
+    int gt_base = gt_before, eq_base = eq_before;
+    for (int i0 = 0; i0 < out_n; i0 += kThreads * 8) {
+      const int start = i0 + tid * 8;
+      uint32_t gtm = 0, eqm = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (start + j < out_n) {
+          const uint32_t key = okey(start + j);
+          if (key >= thr_hi) gtm |= 1u << j;
+          else if (key >= thr_lo) eqm |= 1u << j;
+        }
+      }
+      int packed_total;
+      const int packed = block_scan_excl<kThreads>(__popc(gtm) | (__popc(eqm) << 16), s_misc, packed_total);
+      int gb = gt_base + (packed & 0xffff), eb = eq_base + (packed >> 16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (gtm & (1u << j)) {
+          const int pos = gb + min(eb, need);
+          if (pos < f.k) emit(pos, otok(start + j));
+          ++gb;
+        } else if (eqm & (1u << j)) {
+          if (eb < need && gb + eb < f.k) emit(gb + eb, otok(start + j));
+          ++eb;
+        }
+      }
+      gt_base += packed_total & 0xffff;
+      eq_base += packed_total >> 16;
+    }
   }
-  if (tid == 0) *count = out_n;
+
+  // Depart.  The last workgroup of the row to depart clears the row's words
+  // and, if any wait of the row gave up, selects over the row's lists alone.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    if (failed) {
+      st_agent(failw, 1u);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    const uint32_t before = __hip_atomic_fetch_add(arrive, 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_misc[16] = ((before >> 16) + 1u == static_cast<uint32_t>(G)) ? 1 : 0;
+    s_misc[17] = (s_misc[16] && ld_agent(failw) != 0) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_misc[16]) return;
+  if (s_misc[17]) {
+    if (tid == 0) atomicAdd(a.timeouts + 2, 1u);
+    // Every workgroup wrote its list and count before it departed.  Radix
+    // select (4 passes of 8 bits) over the lists, then the ordered output.
+    int* const s_cnt = s_off;
+    for (int y = tid; y < G; y += kThreads)
+      s_cnt[y] = static_cast<int>(ld_agent(a.cand_count + static_cast<int64_t>(t) * a.groups + y));
+    __syncthreads();
+    int ncand = 0;
+    for (int y = 0; y < G; ++y) ncand += s_cnt[y];
+    auto gkey = [&](int y, int i) -> uint32_t {
+      return score_key(__uint_as_float(ld_agent(a.cand_score + row0 + y * seg_tokens + i)) + 0.0f);
+    };
+    uint32_t prefix = 0u, mask = 0u;
+    int remaining = f.k;
+    const bool all = ncand <= f.k;
+    if (!all) {
+      for (int sh = 24; sh >= 0; sh -= 8) {
+        for (int b = tid; b < 256; b += kThreads) s_lh[b] = 0;
+        __syncthreads();
+        for (int y = 0; y < G; ++y)
+          for (int i = tid; i < s_cnt[y]; i += kThreads) {
+            const uint32_t key = gkey(y, i);
+            if ((key & mask) == prefix) atomicAdd(&s_lh[(key >> sh) & 255u], 1u);
+          }
+        __syncthreads();
+        int above;
+        const int b = find_bin<kThreads>(s_lh, 256, remaining, s_misc, s_misc + 28, above);
+        remaining -= above;
+        prefix |= static_cast<uint32_t>(b) << sh;
+        mask |= 255u << sh;
+      }
+    }
+    int gt_base = 0, eq_base = 0;
+    for (int y = 0; y < G; ++y)
+      for (int i0 = 0; i0 < s_cnt[y]; i0 += kThreads * 4) {
+        const int start = i0 + tid * 4;
+        uint32_t gtm = 0, eqm = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (start + j < s_cnt[y]) {
+            if (all) {
+              gtm |= 1u << j;
+            } else {
+              const uint32_t key = gkey(y, start + j);
+              if (key > prefix) gtm |= 1u << j;
+              else if (key == prefix) eqm |= 1u << j;
+            }
+          }
+        }
+        int packed_total;
+        const int packed = block_scan_excl<kThreads>(__popc(gtm) | (__popc(eqm) << 16), s_misc, packed_total);
+        int gb = gt_base + (packed & 0xffff), eb = eq_base + (packed >> 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool g_ = gtm & (1u << j), e_ = eqm & (1u << j);
+          if (!g_ && !e_) continue;
+          const int64_t tok = static_cast<int32_t>(ld_agent(a.cand_idx + row0 + y * seg_tokens + start + j));
+          if (g_) {
+            const int pos = gb + min(eb, remaining);
+            if (pos < f.k) so.emit(pos, tok);
+            ++gb;
+          } else {
+            if (eb < remaining && gb + eb < f.k) so.emit(gb + eb, tok);
+            ++eb;
+          }
+        }
+        gt_base += packed_total & 0xffff;
+        eq_base += packed_total >> 16;
+      }
+    for (int i = gt_base + min(eq_base, all ? 0 : remaining) + tid; i < f.k; i += kThreads) so.emit(i, -1);
+    // both histograms may hold adds of rounds that were never closed
+    for (int i = tid; i < 2 * kHistSlot; i += kThreads) st_agent(rowc + i, 0u);
+  }
+  for (int i = tid; i < 8 * kSelRounds; i += kThreads) st_agent(rowc + kDecWords + i, 0u);
+  for (int i = tid; i < 2 * G; i += kThreads) st_agent(rowc + kRecWords + i, 0u);
+  if (tid == 0) {
+    st_agent(failw, 0u);
+    st_agent(arrive, 0u);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1418,28 +2131,6 @@ struct SelectSmem {
   uint32_t pmin, pmax;  // range of the current pass's keys
 };
 
-// LDS histogram increment: the lanes sharing a bin with the first remaining
-// lane add with one atomic, twice; the others one atomic per lane.  Runs of
-// equal keys (ties) then cost one or two atomics per wave instead of one per
-// lane on the same address.
-__device__ __forceinline__ void hist_add_ties(uint32_t* hist, int bin) {
-  const int lane = threadIdx.x & 63;
-  uint64_t act = __ballot(bin >= 0);
-  // two rounds: the lanes sharing the first remaining lane's bin add with
-  // one atomic (a tie group, most of a wave in tie-heavy rows, is taken in
-  // one of them); the rest add one each
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    if (act == 0) return;
-    const int leader = static_cast<int>(__builtin_ctzll(act));
-    const int lb = __builtin_amdgcn_readlane(bin, leader);
-    const uint64_t same = __ballot(bin == lb) & act;
-    if (lane == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(same)));
-    act &= ~same;
-  }
-  if ((act >> lane) & 1u) atomicAdd(&hist[bin], 1u);
-}
-
 __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) {
   extern __shared__ __align__(16) uint8_t smem_raw[];
   SelectSmem& sm = *reinterpret_cast<SelectSmem*>(smem_raw);
@@ -1457,7 +2148,8 @@ __global__ void __launch_bounds__(kSelThreads) topk_select_kernel(SelectArgs a) 
   const int32_t* mbt = nullptr;
   if (merged) {
     seq = a.positions[t] + 1;
-    m_topk = min(max(seq - a.window, static_cast<int64_t>(0)), static_cast<int64_t>(k));
+    m_topk = min(min(max(seq - a.window, static_cast<int64_t>(0)), static_cast<int64_t>(k)),
+                 static_cast<int64_t>(a.merged_width));
     if (a.slot_bt) mbt = a.slot_bt + static_cast<int64_t>(a.slot_req[t]) * a.slot_bt_stride;
   }
   // Slot conversion reads the row's first kSelBtPages block-table entries
@@ -1993,6 +2685,21 @@ extern "C" int ekv_topk_select(const float* scores, int64_t scores_stride, const
 
 namespace {
 
+// Outputs of a top-k call that selects: top-k rows and the optional merged rows.
+struct SelOutputs {
+  int32_t* topk_out;
+  int64_t out_stride;
+  int32_t* merged;
+  int64_t merged_stride;
+  int32_t merged_width;
+  const int64_t* positions;
+  int32_t window;
+  int32_t merged_slots;
+};
+
+// Polls of a fused-kernel wait before it gives up (ekv_indexer_set_spin_limit).
+int g_spin_limit = kFusedSpinLimit;
+
 int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_t page_stride,
                     const int32_t* block_table, const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
                     int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes, bool fp4) {
@@ -2021,12 +2728,15 @@ struct TopkQuery {
 
 // Stage 1: MFMA filter.  Fused plan: filter, bound and exact scoring of the
 // candidates in one launch.  Otherwise: upper bounds, lower-bound histogram
-// and key bound; the candidates are scored in stage 2.
+// and key bound; the candidates are scored in stage 2.  With `so` the fused
+// plan also selects (when a row's workgroups fit the control block) and
+// *selected says whether it did.
 template <bool kFp4>
 int run_filter(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
                const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
                int32_t num_tokens, int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes,
-               void* stream) {
+               void* stream, const SelOutputs* so = nullptr, bool* selected = nullptr) {
+  if (selected) *selected = false;
   int rc = check_topk_args(q.q, q.w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
                            workspace, workspace_bytes, kFp4);
   if (rc) return rc;
@@ -2044,8 +2754,14 @@ int run_filter(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, i
                max_len, k, ws.upper, ws.hist, num_tokens, plan.groups, q.q_scales};
   if (plan.fused) {
     // the fused kernel's counters are zero on entry and left zero
+    const bool in_launch = so != nullptr && plan.groups <= kSelMaxGroups;
     FusedArgs fa{f, q.q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts,
-                 plan.groups, plan.stage_pages};
+                 plan.groups, plan.stage_pages, g_spin_limit,
+                 in_launch ? so->topk_out : nullptr, in_launch ? so->out_stride : 0,
+                 in_launch ? so->merged : nullptr, in_launch ? so->merged_stride : 0,
+                 in_launch ? so->merged_width : 0, in_launch ? so->positions : nullptr,
+                 in_launch ? so->window : 0, in_launch ? so->merged_slots : 0};
+    if (selected) *selected = in_launch;
     const dim3 grid(static_cast<unsigned>(plan.groups), num_tokens);
     if (plan.waves == 12)
       hipLaunchKernelGGL((filter_verify_kernel<12, kFp4>), grid, dim3(64 * 12), plan.smem, s, fa);
@@ -2101,7 +2817,38 @@ int run_select(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, i
   return ekv_launch_status();
 }
 
+// Both stages in one call: with the fused plan the filter launch also
+// selects (and merges), otherwise stage 2 runs after it.
+template <bool kFp4>
+int run_topk(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+             const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, const int32_t* lengths,
+             int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k, void* workspace,
+             int64_t workspace_bytes, int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
+             const int64_t* positions, int32_t window, int32_t merged_slots, void* stream) {
+  EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
+  EKV_CHECK(merged_out == nullptr || (positions != nullptr && window >= 0 && merged_width >= 0 &&
+                                      merged_stride >= merged_width),
+            "merged_out needs positions, window >= 0 and merged_stride >= merged_width");
+  const SelOutputs so{topk_out, out_stride, merged_out, merged_stride, merged_width, positions, window,
+                      merged_slots ? 1 : 0};
+  bool selected = false;
+  int rc = run_filter<kFp4>(q, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths, num_tokens,
+                            max_len, k, workspace, workspace_bytes, stream, &so, &selected);
+  if (rc || selected) return rc;
+  return run_select<kFp4>(q, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths, num_tokens,
+                          max_len, topk_out, out_stride, k, workspace, workspace_bytes, merged_out, merged_stride,
+                          merged_width, positions, window, merged_slots, stream);
+}
+
 }  // namespace
+
+extern "C" int64_t ekv_indexer_topk_counter_bytes(void) { return kCounterBytes; }
+
+extern "C" int32_t ekv_indexer_set_spin_limit(int32_t polls) {
+  const int32_t prev = g_spin_limit;
+  g_spin_limit = polls < 0 ? kFusedSpinLimit : polls;
+  return prev;
+}
 
 extern "C" int ekv_indexer_filter(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
                                   const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
@@ -2131,12 +2878,23 @@ extern "C" int ekv_indexer_topk(const uint8_t* q_fp8, const int8_t* q_digits, co
                                 const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
                                 int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
                                 void* stream) {
-  int rc = ekv_indexer_filter(q_fp8, q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids,
-                              lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
-  if (rc) return rc;
-  return ekv_indexer_select(q_digits, w, kcache, page_stride, num_pages, block_table, bt_stride, req_ids, lengths,
-                            num_tokens, max_len, topk_out, out_stride, k, workspace, workspace_bytes, nullptr, 0, 0,
-                            nullptr, 0, 0, stream);
+  return run_topk<false>(TopkQuery{q_fp8, q_digits, nullptr, w}, kcache, page_stride, num_pages, block_table,
+                         bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                         workspace_bytes, nullptr, 0, 0, nullptr, 0, 0, stream);
+}
+
+extern "C" int ekv_indexer_topk_merged(const uint8_t* q_fp8, const int8_t* q_digits, const float* w,
+                                       const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                       const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                       const int32_t* lengths, int32_t num_tokens, int32_t max_len,
+                                       int32_t* topk_out, int64_t out_stride, int32_t k, void* workspace,
+                                       int64_t workspace_bytes, int32_t* merged_out, int64_t merged_stride,
+                                       int32_t merged_width, const int64_t* positions, int32_t window,
+                                       int32_t merged_slots, void* stream) {
+  return run_topk<false>(TopkQuery{q_fp8, q_digits, nullptr, w}, kcache, page_stride, num_pages, block_table,
+                         bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                         workspace_bytes, merged_out, merged_stride, merged_width, positions, window, merged_slots,
+                         stream);
 }
 
 extern "C" int ekv_indexer_filter_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
@@ -2167,10 +2925,21 @@ extern "C" int ekv_indexer_topk_fp4(const uint8_t* q_values, const int32_t* q_sc
                                     const int32_t* lengths, int32_t num_tokens, int32_t max_len, int32_t* topk_out,
                                     int64_t out_stride, int32_t k, void* workspace, int64_t workspace_bytes,
                                     void* stream) {
-  int rc = ekv_indexer_filter_fp4(q_values, q_scales, w, kcache, page_stride, num_pages, block_table, bt_stride,
-                                  req_ids, lengths, num_tokens, max_len, k, workspace, workspace_bytes, stream);
-  if (rc) return rc;
-  return ekv_indexer_select_fp4(q_values, q_scales, w, kcache, page_stride, num_pages, block_table, bt_stride,
-                                req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
-                                workspace_bytes, nullptr, 0, 0, nullptr, 0, 0, stream);
+  return run_topk<true>(TopkQuery{q_values, nullptr, q_scales, w}, kcache, page_stride, num_pages, block_table,
+                        bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                        workspace_bytes, nullptr, 0, 0, nullptr, 0, 0, stream);
+}
+
+extern "C" int ekv_indexer_topk_merged_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,
+                                           const uint8_t* kcache, int64_t page_stride, int64_t num_pages,
+                                           const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids,
+                                           const int32_t* lengths, int32_t num_tokens, int32_t max_len,
+                                           int32_t* topk_out, int64_t out_stride, int32_t k, void* workspace,
+                                           int64_t workspace_bytes, int32_t* merged_out, int64_t merged_stride,
+                                           int32_t merged_width, const int64_t* positions, int32_t window,
+                                           int32_t merged_slots, void* stream) {
+  return run_topk<true>(TopkQuery{q_values, nullptr, q_scales, w}, kcache, page_stride, num_pages, block_table,
+                        bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
+                        workspace_bytes, merged_out, merged_stride, merged_width, positions, window, merged_slots,
+                        stream);
 }

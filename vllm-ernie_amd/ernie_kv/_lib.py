@@ -55,6 +55,12 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_indexer_filter": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, I32, P, I64, P]),
     "ekv_indexer_select": (I32, [P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P]),
     "ekv_indexer_topk": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P]),
+    "ekv_indexer_topk_merged": (
+        I32,
+        [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P],
+    ),
+    "ekv_indexer_topk_counter_bytes": (I64, []),
+    "ekv_indexer_set_spin_limit": (I32, [I32]),
     "ekv_sparse_mla_decode_workspace_size": (I64, [I32, I32, I32]),
     "ekv_sparse_mla_decode": (
         I32,
@@ -79,6 +85,10 @@ SIGNATURES: dict[str, tuple] = {
         [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P],
     ),
     "ekv_indexer_topk_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P]),
+    "ekv_indexer_topk_merged_fp4": (
+        I32,
+        [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P],
+    ),
     "ekv_indexer_filter_dots_fp4": (I32, [P, P, P, P, I32, P, P]),
     "ekv_export_fp8_ds_mla_pages": (I32, [P, I64, I64, P, I32, P, I64, I64, P, P]),
     "ekv_import_fp8_ds_mla_pages": (I32, [P, I64, I64, P, I32, P, I64, I64, P, P]),

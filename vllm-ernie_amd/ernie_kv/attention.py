@@ -484,7 +484,8 @@ class Ernie5_5Indexer:
         return self._lengths[:T]
 
     def _topk(self, qa, qb, wf, md: DSAStepMetadata, lengths, positions, merged=None) -> None:
-        """Exact top-k of every query row (filter + select), in row pieces
+        """Exact top-k of every query row (filter + select, one launch when the
+        filter fits one), in row pieces
         whose workspace fits _INDEXER_WORKSPACE_BYTES; with ``merged`` the
         select also writes merge_swa_topk's rows.  ``(qa, qb)`` are the fp8
         codes and digit planes, or the MXFP4 values and scale words."""
@@ -500,11 +501,10 @@ class Ernie5_5Indexer:
             sel = dict(merged=None if merged is None else merged[r0:r1], positions=positions[r0:r1],
                        window=self.window)
             if self.use_fp4_kv:
-                ops.indexer_filter_fp4(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
-                ops.indexer_select_fp4(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws, **sel)
+                ops.indexer_topk_merged_fp4(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws,
+                                            **sel)
             else:
-                ops.indexer_filter(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, ws, k=self.topk)
-                ops.indexer_select(qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws, **sel)
+                ops.indexer_topk_merged(qa[r0:r1], qb[r0:r1], wf[r0:r1], *args, out[r0:r1, : self.topk], ws, **sel)
 
     def _quantize_fp4(self, q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, slot_mapping: torch.Tensor):
         """MXFP4 q (values [T, 64, 64], scale words [T, 64]) and the K insert

@@ -501,6 +501,18 @@ def indexer_filter(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, ma
     )
 
 
+def _merged_args(merged, positions, window, topk_out, T):
+    """(pointer, row stride, width, positions pointer) of an optional merged output."""
+    if merged is None:
+        return 0, 0, 0, 0
+    _need(positions is not None, "merged output needs positions")
+    _check_dev(merged, positions)
+    _need(merged.dtype == torch.int32 and merged.stride(1) == 1 and merged.shape[0] == T, "merged int32 [T, W]")
+    _need(positions.dtype == torch.int64 and positions.shape[0] == T, "positions int64 [T]")
+    _need(merged.shape[1] >= topk_out.shape[1] + window, "merged width must be >= k + window")
+    return merged.data_ptr(), _rs(merged), merged.shape[1], positions.data_ptr()
+
+
 def indexer_select(q_digits, w, kcache, block_table, req_ids, lengths, max_len: int, topk_out: torch.Tensor,
                    workspace: torch.Tensor, merged: torch.Tensor | None = None,
                    positions: torch.Tensor | None = None, window: int = 128, merged_slots: bool = False) -> None:
@@ -552,6 +564,38 @@ def indexer_topk(
         T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(),
         workspace.numel(), _stream(),
     )
+
+
+def indexer_topk_merged(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, max_len: int,
+                        topk_out: torch.Tensor, workspace: torch.Tensor, merged: torch.Tensor | None = None,
+                        positions: torch.Tensor | None = None, window: int = 128,
+                        merged_slots: bool = False) -> None:
+    """``indexer_topk`` with ``indexer_select``'s merged output, in one call
+    (one launch when the filter fits one: its workgroups then also select)."""
+    T = q_fp8.shape[0]
+    _topk_common(q_fp8, q_digits, w, kcache, block_table, req_ids, lengths, T)
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    m_ptr, m_stride, m_width, p_ptr = _merged_args(merged, positions, window, topk_out, T)
+    _lib.call(
+        "ekv_indexer_topk_merged", q_fp8.data_ptr(), q_digits.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1],
+        workspace.data_ptr(), workspace.numel(), m_ptr, m_stride, m_width, p_ptr, int(window),
+        int(bool(merged_slots)), _stream(),
+    )
+
+
+def indexer_topk_counter_bytes() -> int:
+    """Bytes at the front of a top-k workspace holding the one-launch path's
+    per-row counters (zero between calls)."""
+    return int(_lib.load().ekv_indexer_topk_counter_bytes())
+
+
+def indexer_set_spin_limit(polls: int) -> int:
+    """Test hook: polls a one-launch top-k workgroup waits for the rest of its
+    row before it gives up (the row's last workgroup then selects alone);
+    ``polls < 0`` restores the default.  Returns the previous value."""
+    return int(_lib.load().ekv_indexer_set_spin_limit(int(polls)))
 
 
 # --------------------------------------------------------------------------- MXFP4 indexer
@@ -697,6 +741,23 @@ def indexer_topk_fp4(q_values, q_scales, w, kcache, block_table, req_ids, length
         _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
         lengths.data_ptr(), T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1],
         workspace.data_ptr(), workspace.numel(), _stream(),
+    )
+
+
+def indexer_topk_merged_fp4(q_values, q_scales, w, kcache, block_table, req_ids, lengths, max_len: int,
+                            topk_out: torch.Tensor, workspace: torch.Tensor, merged: torch.Tensor | None = None,
+                            positions: torch.Tensor | None = None, window: int = 128,
+                            merged_slots: bool = False) -> None:
+    """MXFP4 ``indexer_topk_merged``."""
+    T = _fp4_common(q_values, q_scales, w, kcache, block_table, req_ids, lengths)
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    m_ptr, m_stride, m_width, p_ptr = _merged_args(merged, positions, window, topk_out, T)
+    _lib.call(
+        "ekv_indexer_topk_merged_fp4", q_values.data_ptr(), q_scales.data_ptr(), w.data_ptr(), kcache.data_ptr(),
+        _rs(kcache), kcache.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        lengths.data_ptr(), T, int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1],
+        workspace.data_ptr(), workspace.numel(), m_ptr, m_stride, m_width, p_ptr, int(window),
+        int(bool(merged_slots)), _stream(),
     )
 
 
