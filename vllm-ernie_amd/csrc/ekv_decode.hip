@@ -243,6 +243,19 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint8_t* p) {
       (lds_i16x4*)((__attribute__((address_space(3))) uint8_t*)(p)));
 }
 
+// Max of v over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows),
+// with VALU lane swaps instead of LDS permutes: after a swap of rows r and
+// r ^ 1 (or halves) between two copies of v, the max of the two results is
+// the pairwise max in every lane.
+__device__ __forceinline__ float max_rows(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // s_waitcnt vmcnt(N), other counters untouched.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -566,8 +579,7 @@ sparse_decode_kernel(DecodeArgs a) {
           x[m] = ks8[m] > 0.0f ? sv8[m] * (sc2 * ks8[m]) : -INFINITY;
           mx = fmaxf(mx, x[m]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_rows(mx);
         const bool grow = mx > m2 + kRescaleSlack || (m2 == -INFINITY && mx != -INFINITY);
         const bool any = __any(grow);
         if (any) {  // wave-uniform: move every head's reference to its max so far
@@ -587,7 +599,7 @@ sparse_decode_kernel(DecodeArgs a) {
         float w[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-          const float p = live ? exp2f(x[m] - m2) : 0.0f;
+          const float p = live ? __builtin_amdgcn_exp2f(x[m] - m2) : 0.0f;  // (x - m2 <= 8; tiny weights flush to 0)
           lsum += p;
           w[m] = p * ks8[m];
         }
