@@ -360,6 +360,8 @@ def build_hca_write(torch, ops, seed: int, B: int = 16, chunk: int = 8192, max_o
         norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=gd)).contiguous(),
         cos_sin=cos_sin, comp_bt=comp_bt, ring_pages=ring_pages.to(dev), slots=slots, positions=positions,
         token_seq=token_seq, qsl=qsl,
+        # a workspace slot per (sequence, span slot): each span compressed by D / 64 one-wave workgroups
+        ws=ops.hca_write_workspace(B, D, dev, max_query_len=chunk),
     )
     return st
 
@@ -369,7 +371,7 @@ def hca_write_step(ops, st):
     rows, window ring, state ring)."""
     ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["chunk"],
                   st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
-                  st["ring_pages"], 128, st["pool"])
+                  st["ring_pages"], 128, st["pool"], workspace=st["ws"])
 
 
 def hca_write_bytes(T: int, D: int, B: int, spans_done: int) -> dict:
@@ -389,7 +391,8 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
     workload = f"hca_chunked_prefill_b{st['B']}_chunk{st['chunk']}"
     return {
         "workload": workload,
-        "kernels": "hca_compress_kernel<576> + hca_append_kernel<576> (rows, window ring, state ring)",
+        "kernels": "hca_compress_slab_kernel<576> (9 one-wave workgroups per span) + hca_append_kernel<576> "
+                   "(rows, window ring, state ring)",
         "ms": round(ms, 4),
         "bytes_latent_rows": by["latent_rows"],
         "GB/s_latent_rows": round(by["latent_rows"] / (ms * 1e-3) / 1e9, 1),
@@ -397,8 +400,8 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
         "bytes_with_kv_score": by["with_kv_score"],
         "GB/s_with_kv_score": round(by["with_kv_score"] / (ms * 1e-3) / 1e9, 1),
         "frac_with_kv_score": round(by["with_kv_score"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "traffic": {"kernel": "hca_compress_kernel<576>",
-                    "bytes": traffic_of(workload, "hca_compress_kernel<576>")},
+        "traffic": {"kernel": "hca_compress_slab_kernel<576>",
+                    "bytes": traffic_of(workload, "hca_compress_slab_kernel<576>")},
     }
 
 

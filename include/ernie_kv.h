@@ -102,10 +102,13 @@ int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t
  * pool and the state ring).  comp_block_table must not be NULL; ring_pages /
  * state may be.  workspace (16-byte aligned, at least
  * ekv_hca_write_workspace_size(num_seqs, dim) bytes, zero-filled once before
- * its first use and left zero by every call) may be NULL; with it,
- * decode-sized calls (max_query_len < 128) compress each completed span with
- * four workgroups instead of one -- same bytes.  Calls that share a workspace
- * must not overlap.  Replaces the cache-write half of
+ * its first use and left zero by every call; pass the same workspace_bytes on
+ * every call that shares it) may be NULL; with it, decode-sized calls
+ * (max_query_len < 128) compress each completed span with four workgroups
+ * instead of one, and longer calls whose workspace holds
+ * num_seqs * (max_query_len / 128 + 1) spans compress each span with D / 64
+ * one-wave workgroups -- same bytes either way.  Calls that share a
+ * workspace must not overlap.  Replaces the cache-write half of
  * DeepseekV4Attention._prepare_and_attn_fn (nvidia/attention.py:494-505) with
  * its compressor call (Ernie5_5Compressor.forward, nvidia/attention.py:398-408).
  */
@@ -118,9 +121,11 @@ int ekv_hca_write(const uint16_t* latent, int64_t latent_stride, const uint16_t*
                   int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride /*bytes*/,
                   int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Bytes of ekv_hca_write's workspace for up to num_seqs sequences of width
- * dim (no counterpart in the reference, whose compressor is unfused). */
-int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim);
+/* Bytes of an ekv_hca_write workspace that holds num_spans spans of width
+ * dim (<= 576): a call needs one per sequence, and one per sequence and span
+ * slot (num_seqs * (max_query_len / 128 + 1)) for the prefill split (no
+ * counterpart in the reference, whose compressor is unfused). */
+int64_t ekv_hca_write_workspace_size(int32_t num_spans, int32_t dim);
 
 /*
  * ekv_hca_write followed by ekv_hca_decode_indices of the same tokens

@@ -58,6 +58,8 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
     if fused:
         if fused == "ws" and "ws" not in gpu:  # decode-sized calls split each span over four workgroups
             gpu["ws"] = ops.hca_write_workspace(case.B, D, dev)
+        if fused == "ws-spans" and "ws" not in gpu:  # and prefill calls over D / 64 one-wave workgroups
+            gpu["ws"] = ops.hca_write_workspace(case.B, D, dev, max_query_len=1000)
         ops.hca_write(bf16_tensor(latent, dev), kvs_t, d(slots), d(positions), d(token_seq), d(qsl), int(max(counts)),
                       gpu["state"], d(case.state_slot), d(case.ape), d(case.norm_w), 1e-6, d(case.cos_sin),
                       d(case.comp_bt), d(case.ring_pages), case.ring, gpu["pool"], workspace=gpu.get("ws"))
@@ -68,8 +70,16 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
                    d(case.ring_pages), case.ring, gpu["state"], d(case.state_slot))
 
 
+def _counters_zero(ws) -> bool:
+    """The workspace's arrival counters (one u32 per span slot it holds, at
+    its start) are all zero."""
+    record = 4 + (576 + 144) * 4
+    return int(ws[: 4 * (ws.numel() // record)].sum()) == 0
+
+
 @pytest.mark.parametrize("rope", ["plain", "yarn"])
-@pytest.mark.parametrize("fused", [False, True, "ws"], ids=["compress+append", "hca_write", "hca_write+ws"])
+@pytest.mark.parametrize("fused", [False, True, "ws", "ws-spans"],
+                         ids=["compress+append", "hca_write", "hca_write+ws", "hca_write+ws-spans"])
 @pytest.mark.parametrize("dim", [576, 512])
 def test_hca_write_path_exact(dev, dim, fused, rope):
     rng = np.random.default_rng(dim)
@@ -94,7 +104,7 @@ def test_hca_write_path_exact(dev, dim, fused, rope):
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
         if "ws" in gpu:  # the arrival counters are left zero
-            assert int(gpu["ws"][:256].sum()) == 0
+            assert _counters_zero(gpu["ws"])
 
 
 @pytest.mark.parametrize("rope", ["plain", "yarn"])
@@ -123,7 +133,7 @@ def test_hca_write_decode_completes_spans(dev, dim, fused, rope):
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
         if "ws" in gpu:  # the arrival counters are left zero
-            assert int(gpu["ws"][:256].sum()) == 0
+            assert _counters_zero(gpu["ws"])
 
 
 def test_hca_decode_indices(dev):
@@ -316,7 +326,7 @@ def test_hca_write_step_matches_separate_calls(dev, rows, use_ws):
         pool, state = pool0.clone(), state0.clone()
         idx = torch.full((T, width), -7, dtype=torch.int32, device=dev)
         lens = torch.zeros(T, dtype=torch.int32, device=dev)
-        ws = ops.hca_write_workspace(B, D, dev) if use_ws else None
+        ws = ops.hca_write_workspace(B, D, dev, max_query_len=rows) if use_ws else None
         if fused:
             ops.hca_write_step(pool=pool, state=state, window=window, out=idx, lengths=lens, workspace=ws, **args)
         else:
@@ -326,6 +336,6 @@ def test_hca_write_step_matches_separate_calls(dev, rows, use_ws):
         torch.cuda.synchronize()
         outs.append((pool, state.view(torch.int16), idx, lens))
         if ws is not None:
-            assert int(ws[:256].sum()) == 0
+            assert _counters_zero(ws)
     for name, a_, b_ in zip(["pool", "state", "idx", "lens"], *outs):
         assert torch.equal(a_, b_), name

@@ -186,23 +186,19 @@ struct CompressLds {
   int last;
 };
 
-// Compress span j of sequence b (first row t0 at position p0, state slot st)
-// with one workgroup of D threads.  Wave w owns channels 64w .. 64w+63;
-// lane l of it owns the 4 channels 64w + 4 (l % 16) + 0..3 of row group
-// l / 16.  Every kv_score element is read from memory once: the softmax is
-// an online one per (row group, channel), merged over the groups in order.
-// Every thread of the workgroup must call it (it synchronizes).  kRingPipe:
-// spans that start in the state ring get the input path's load pipeline too
-// (at the cost of more registers).
+// The softmax of span j of a sequence (first row t0 at position p0, state
+// slot st) for the 4 channels 4 quad .. 4 quad + 3, row group lane / 16 of
+// this lane, merged over the 4 row groups in order: every lane of a column
+// (lanes l, l+16, l+32, l+48 of the wave, which must share quad) ends with the
+// same x, and part = their sum of squares in channel order.  Every
+// kv_score element is read from memory once: the softmax is an online one per
+// (row group, channel).  kRingPipe: spans that start in the state ring get
+// the input path's load pipeline too (at the cost of more registers).
 template <int D, bool kRingPipe>
-__device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds<D>& ls, int b, int t0, int64_t p0,
-                                              int64_t j, int st) {
-  constexpr int kWaves = D / 64;
-  constexpr int kQuads = D / 4;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int grp = lane >> 4;                            // row group r
-  const int quad = (tid >> 6) * 16 + (lane & 15);       // channel quad
+__device__ __forceinline__ void span_softmax(const CompressArgs& a, int quad, int t0, int64_t p0, int64_t j, int st,
+                                             float (&x)[4], float& part) {
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4;  // row group r
   const int c0 = 4 * quad;
 
   SoftmaxState sm;
@@ -353,8 +349,7 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   }
 
   // Merge the 4 row groups in order (lanes l, l+16, l+32, l+48 of a wave).
-  float x[4];
-  float part = 0.0f;
+  part = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     float m_g[kRowGroups];
@@ -373,6 +368,26 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
     x[k] = __fdiv_rn(N, Z);
     part = part + x[k] * x[k];
   }
+}
+
+// Compress span j of sequence b (first row t0 at position p0, state slot st)
+// with one workgroup of D threads.  Wave w owns channels 64w .. 64w+63;
+// lane l of it owns the 4 channels 64w + 4 (l % 16) + 0..3 of row group
+// l / 16 (span_softmax), then the row is finished: RMSNorm (the quads' sums
+// of squares added in quad order by one thread), RoPE, quant.  Every thread
+// of the workgroup must call it (it synchronizes).
+template <int D, bool kRingPipe>
+__device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds<D>& ls, int b, int t0, int64_t p0,
+                                              int64_t j, int st) {
+  constexpr int kWaves = D / 64;
+  constexpr int kQuads = D / 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int grp = lane >> 4;                            // row group r
+  const int quad = (tid >> 6) * 16 + (lane & 15);       // channel quad
+  const int c0 = 4 * quad;
+  float x[4], part;
+  span_softmax<D, kRingPipe>(a, quad, t0, p0, j, st, x, part);
   // From here on the lanes of row group 0 carry the row: quad q's channels.
   const bool owner = grp == 0;
   if (owner) ls.part[quad] = part;
@@ -523,10 +538,10 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
       __hip_atomic_store(a.span_part + static_cast<int64_t>(b) * (D / 4) + c / 4, part, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's results are out before it arrives
+  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's results are complete before it arrives (as in compress_span_slab)
   __syncthreads();
   if (tid == 0) {
-    const uint32_t before = __hip_atomic_fetch_add(a.span_count + b, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t before = __hip_atomic_fetch_add(a.span_count + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ls.last = (before + 1u == static_cast<uint32_t>(kQuarters)) ? 1 : 0;
   }
   __syncthreads();
@@ -579,6 +594,127 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
     *reinterpret_cast<uint32_t*>(page + off * D + tid) = lo | (hi << 16);
   }
   if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
+}
+
+// The row of span j (workspace slot `slot`, compressed slot through
+// sequence b's comp_block_table row) from the softmax results and quad sums
+// in the workspace, finished by one wave as compress_span finishes it:
+// RMSNorm with the quad sums added in quad order by lane 0, RoPE on the last
+// 64 channels, the per-token quant.  Lane l takes channels 64 i + l.  Clears
+// the slot's arrival counter.  part_lds holds D / 4 floats.
+template <int D>
+__device__ __forceinline__ void finish_span_wave(const CompressArgs& a, float* part_lds, int64_t slot, int b,
+                                                 int64_t j) {
+  constexpr int kSlabs = D / 64;
+  const int lane = threadIdx.x & 63;
+  if (lane == 0) __hip_atomic_store(a.span_count + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float* sx = a.span_x + slot * D;
+  const float* sp = a.span_part + slot * (D / 4);
+  for (int q = lane; q < D / 4; q += 64)
+    part_lds[q] = __hip_atomic_load(sp + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float xs[kSlabs];
+#pragma unroll
+  for (int i = 0; i < kSlabs; ++i) xs[i] = __hip_atomic_load(sx + 64 * i + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  float rn = 0.0f;
+  if (lane == 0) {
+    float S = 0.0f;
+    for (int q = 0; q < D / 4; q += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&part_lds[q]);
+      S = S + v.x; S = S + v.y; S = S + v.z; S = S + v.w;
+    }
+    const float ms = __fdiv_rn(S, static_cast<float>(D));
+    rn = __fdiv_rn(1.0f, __fsqrt_rn(ms + a.eps));
+  }
+  rn = __shfl(rn, 0);
+  float y[kSlabs];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kSlabs; ++i) {
+    const int c = 64 * i + lane;
+    float v = (xs[i] * rn) * a.norm_w[c];
+    if (i == kSlabs - 1) {  // channels D - 64 .. D - 1: RoPE on the pairs (2i, 2i+1)
+      const float vp = __shfl_xor(v, 1);
+      const int pi = lane / 2;
+      const float cz = a.cos_sin[j * 64 + pi], sz = a.cos_sin[j * 64 + 32 + pi];
+      const float x0 = (lane & 1) ? vp : v, x1 = (lane & 1) ? v : vp;
+      v = (lane & 1) ? x0 * sz + x1 * cz : x0 * cz - x1 * sz;
+    }
+    y[i] = v;
+    amax = i == 0 ? fabsf(v) : fmaxf(amax, fabsf(v));
+  }
+  amax = wave_max_xor(amax, 64);
+  const int e = ue8m0_exponent(amax);
+  const float inv = exp2i(-e);
+  const int64_t cslot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
+                            kPageTokens + j % kPageTokens;
+  if (cslot < 0 || cslot >= a.num_pages * kPageTokens) return;
+  uint8_t* page = a.pool + (cslot / kPageTokens) * a.page_stride;
+  const int64_t off = cslot % kPageTokens;
+#pragma unroll
+  for (int i = 0; i < kSlabs; ++i) {
+    const float y1 = __shfl_down(y[i], 1), y2 = __shfl_down(y[i], 2), y3 = __shfl_down(y[i], 3);
+    if ((lane & 3) == 0) {
+      const uint32_t lo = f32x2_to_fp8(y[i] * inv, y1 * inv);
+      const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
+      *reinterpret_cast<uint32_t*>(page + off * D + 64 * i + lane) = lo | (hi << 16);
+    }
+  }
+  if (lane == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
+}
+
+// Span j of sequence b compressed by D / 64 one-wave workgroups (prefill
+// calls with a workspace): workgroup `slab` runs compress_span's wave `slab`
+// -- channels 64 slab .. 64 slab + 63, 4 per lane of row group lane / 16 --
+// and writes its softmax results and quad sums to workspace slot `slot`; the
+// last of the span's workgroups to arrive finishes the row (finish_span_wave).
+// The operations on a channel and the order of the sums are compress_span's,
+// so the bytes are too.  Spans that start in the state ring take the plain
+// per-row path (one per sequence at most).
+template <int D>
+__device__ __forceinline__ void compress_span_slab(const CompressArgs& a, float* part_lds, int64_t slot, int b,
+                                                   int slab, int t0, int64_t p0, int64_t j, int st) {
+  const int lane = threadIdx.x & 63;
+  const int quad = 16 * slab + (lane & 15);
+  float x[4], part;
+  span_softmax<D, false>(a, quad, t0, p0, j, st, x, part);
+  if (lane < 16) {
+    float* sx = a.span_x + slot * D + 4 * quad;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) __hip_atomic_store(sx + k, x[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.span_part + slot * (D / 4) + quad, part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // This wave's results are complete (agent-coherent stores) before it
+  // arrives; the last arriver's loads are agent-coherent and issued after its
+  // add returns.  No acquire / release: their L2 write-back and invalidate on
+  // every arrival would cost more than the span.
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t before = 0;
+  if (lane == 0) before = __hip_atomic_fetch_add(a.span_count + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  before = __shfl(before, 0);
+  if (before + 1u != static_cast<uint32_t>(D / 64)) return;
+  finish_span_wave<D>(a, part_lds, slot, b, j);
+}
+
+// One one-wave workgroup per (channel slab, span slot, sequence), slab
+// fastest: span slot x of sequence b is span p0 / 128 + x, compressed when
+// this call completes it, into workspace slot b * slots + x.
+template <int D>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(5)))
+hca_compress_slab_kernel(CompressArgs a, int slots) {
+  __shared__ __align__(16) float part_lds[D / 4];
+  constexpr int kSlabs = D / 64;
+  const int span_id = static_cast<int>(blockIdx.x) / kSlabs;
+  const int slab = static_cast<int>(blockIdx.x) - span_id * kSlabs;
+  const int b = span_id / slots;
+  const int t0 = a.qsl[b];
+  const int n = a.qsl[b + 1] - t0;
+  if (n <= 0) return;
+  const int64_t p0 = a.positions[t0];
+  const int64_t j = p0 / kSpan + (span_id - b * slots);
+  if (j * kSpan + kSpan - 1 > p0 + n - 1) return;  // span not completed by this call
+  if (j >= a.max_spans) return;
+  compress_span_slab<D>(a, part_lds, span_id, b, slab, t0, p0, j, a.state_slot != nullptr ? a.state_slot[b] : -1);
 }
 
 // One workgroup per (span slot, sequence): span p0 / 128 + blockIdx.x of
@@ -666,10 +802,21 @@ int hca_compress_args(CompressArgs& a, const uint16_t* kv_score, int64_t kvs_str
   return 0;
 }
 
-// ekv_hca_write workspace: arrival counters u32 [B] (zero between calls),
-// padded to 256 bytes | softmax results f32 [B, D] | quad sums f32 [B, D/4].
-int64_t hca_write_ws_bytes(int64_t num_seqs, int64_t dim) {
-  return ((num_seqs * 4 + 255) / 256) * 256 + num_seqs * (dim + dim / 4) * 4;
+// ekv_hca_write workspace holding S spans: arrival counters u32 [S] (zero
+// between calls), padded to 256 bytes | softmax results f32 [S, 576] | quad
+// sums f32 [S, 144] (a span of width D uses the first D, D / 4 of its row).
+// S is the most spans the byte size holds, so the layout depends on the size
+// alone and one buffer serves calls of either width.
+constexpr int64_t kWsWidth = 576;
+
+int64_t hca_write_ws_bytes(int64_t spans) {
+  return ((spans * 4 + 255) / 256) * 256 + spans * (kWsWidth + kWsWidth / 4) * 4;
+}
+
+int64_t hca_write_ws_capacity(int64_t bytes) {
+  int64_t spans = bytes / (4 + (kWsWidth + kWsWidth / 4) * 4);
+  while (spans > 0 && hca_write_ws_bytes(spans) > bytes) --spans;
+  return spans;
 }
 
 }  // namespace
@@ -696,8 +843,8 @@ extern "C" int ekv_hca_compress(const uint16_t* kv_score, int64_t kvs_stride, co
   return ekv_launch_status();
 }
 
-extern "C" int64_t ekv_hca_write_workspace_size(int32_t num_seqs, int32_t dim) {
-  return num_seqs > 0 && dim > 0 ? hca_write_ws_bytes(num_seqs, dim) : 0;
+extern "C" int64_t ekv_hca_write_workspace_size(int32_t num_spans, int32_t dim) {
+  return num_spans > 0 && dim > 0 && dim <= kWsWidth ? hca_write_ws_bytes(num_spans) : 0;
 }
 
 extern "C" int ekv_hca_decode_indices(const int64_t* positions, const int32_t* req_ids, int32_t num_tokens,
@@ -726,13 +873,15 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
                              norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride,
                              num_pages);
   if (rc) return rc;
+  int64_t ws_spans = 0;
   if (workspace != nullptr) {
-    EKV_CHECK(workspace_bytes >= hca_write_ws_bytes(num_seqs, dim) && aligned16(workspace),
+    ws_spans = hca_write_ws_capacity(workspace_bytes);
+    EKV_CHECK(ws_spans >= num_seqs && aligned16(workspace),
               "workspace too small (ekv_hca_write_workspace_size) or misaligned");
     uint8_t* w = static_cast<uint8_t*>(workspace);
     c.span_count = reinterpret_cast<uint32_t*>(w);
-    c.span_x = reinterpret_cast<float*>(w + ((int64_t{num_seqs} * 4 + 255) / 256) * 256);
-    c.span_part = c.span_x + int64_t{num_seqs} * dim;
+    c.span_x = reinterpret_cast<float*>(w + ((ws_spans * 4 + 255) / 256) * 256);
+    c.span_part = c.span_x + ws_spans * kWsWidth;
   }
   AppendArgs ap;
   rc = hca_append_args(ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
@@ -760,9 +909,19 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
                          ia, ab, index_y);
     return ekv_launch_status();
   }
-  const dim3 grid(max_query_len / kSpan + 1, num_seqs);
-  if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(512), 0, s, c);
-  else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, c);
+  const int slots = max_query_len / kSpan + 1;  // spans that can complete per sequence
+  if (c.span_count != nullptr && ws_spans >= int64_t{num_seqs} * slots) {
+    // a workspace slot per (sequence, span slot): D / 64 one-wave workgroups per span
+    const int64_t blocks = int64_t{num_seqs} * slots * (dim / 64);
+    EKV_CHECK(blocks < (int64_t{1} << 31), "too many rows");
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    if (dim == 512) hipLaunchKernelGGL(hca_compress_slab_kernel<512>, grid, dim3(64), 0, s, c, slots);
+    else hipLaunchKernelGGL(hca_compress_slab_kernel<576>, grid, dim3(64), 0, s, c, slots);
+  } else {
+    const dim3 grid(slots, num_seqs);
+    if (dim == 512) hipLaunchKernelGGL(hca_compress_kernel<512>, grid, dim3(512), 0, s, c);
+    else hipLaunchKernelGGL(hca_compress_kernel<576>, grid, dim3(576), 0, s, c);
+  }
   rc = ekv_launch_status();
   if (rc) return rc;
   rc = launch_hca_append(ap, dim, num_seqs, true, true, s);

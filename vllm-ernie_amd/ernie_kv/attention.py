@@ -687,14 +687,17 @@ class Ernie5_5HCAAttentionMixin:
         self._idx: torch.Tensor | None = None
         self._ws: torch.Tensor | None = None
         self._write_ws: torch.Tensor | None = None
-        self._write_seqs = 0
+        self._write_spans = 0
 
-    def _write_workspace(self, num_seqs: int, D: int, device) -> torch.Tensor:
-        """The cache write's workspace (decode-sized calls compress a span
-        with four workgroups), grown to the widest batch seen."""
-        if self._write_ws is None or self._write_seqs < num_seqs:
-            self._write_seqs = max(num_seqs, 2 * self._write_seqs)
-            self._write_ws = ops.hca_write_workspace(self._write_seqs, D, device)
+    def _write_workspace(self, num_seqs: int, max_query_len: int, D: int, device) -> torch.Tensor:
+        """The cache write's workspace, grown to the most span slots a call
+        has had (one per sequence and 128 rows of its longest query, plus
+        one): decode-sized calls compress a span with four workgroups, longer
+        ones with D / 64."""
+        spans = num_seqs * (max_query_len // 128 + 1)
+        if self._write_ws is None or self._write_spans < spans:
+            self._write_spans = max(spans, 2 * self._write_spans)
+            self._write_ws = ops.hca_write_workspace(self._write_spans, D, device)
         return self._write_ws
 
     def _buffers(self, T: int, width: int, device):
@@ -715,7 +718,7 @@ class Ernie5_5HCAAttentionMixin:
         late_ring = md.max_query_len > self.ring - self.window
         width = md.max_seq_len // 128 + self.window
         idx, lens, lse, ws = self._buffers(T, width, q.device)
-        write_ws = self._write_workspace(md.query_start_loc.numel() - 1, D, q.device)
+        write_ws = self._write_workspace(md.query_start_loc.numel() - 1, md.max_query_len, D, q.device)
         if late_ring:
             ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc,
                           md.max_query_len, self.state_cache, md.state_slot, self.ape, self.norm_w, self.norm_eps,

@@ -197,7 +197,9 @@ def hca_write(
 ) -> None:
     """``hca_compress`` then ``hca_append`` (same arguments, same result) in
     one call.  With ``workspace`` (``hca_write_workspace``) decode-sized calls
-    compress each completed span with four workgroups (same bytes)."""
+    compress each completed span with four workgroups, and longer calls whose
+    workspace was sized for their ``max_query_len`` with ``dim / 64`` (same
+    bytes)."""
     args = _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
                            ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace)
     _lib.call("ekv_hca_write", *args, _stream())
@@ -240,10 +242,13 @@ def hca_write_step(
               lengths.data_ptr(), _stream())
 
 
-def hca_write_workspace(num_seqs: int, dim: int, device) -> torch.Tensor:
-    """Zero-filled workspace of ``hca_write`` for up to ``num_seqs`` sequences
-    of width ``dim`` (every call leaves it zero again)."""
-    n = int(_lib.load().ekv_hca_write_workspace_size(int(num_seqs), int(dim)))
+def hca_write_workspace(num_seqs: int, dim: int, device, max_query_len: int = 0) -> torch.Tensor:
+    """Zero-filled workspace of ``hca_write`` for calls of up to ``num_seqs``
+    sequences of width ``dim`` (every call leaves it zero again).  Sized for
+    ``max_query_len`` rows per sequence it also holds a slot per span of
+    such calls, which then compress each span with ``dim / 64`` workgroups."""
+    spans = int(num_seqs) * (max(int(max_query_len), 0) // 128 + 1)
+    n = int(_lib.load().ekv_hca_write_workspace_size(spans, int(dim)))
     return torch.zeros(max(n, 16), dtype=torch.uint8, device=device)
 
 
