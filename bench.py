@@ -176,17 +176,20 @@ def dsa_pre(ops, st):
 
 def dsa_filter(ops, st):
     """The indexer: filter, exact scoring of the candidates, exact top-2048
-    and its merge with the window (one launch when the filter fits one)."""
+    and its merge with the window as cache slots (one launch when the
+    filter fits one)."""
     common = (st["kcache"], st["block_table"], st["req_ids"], st["lengths"], st["ctx"])
     ops.indexer_topk_merged(st["q8"], st["digits"], st["wf"], *common, st["topk"], st["idx_ws"],
-                            merged=st["merged"], positions=st["positions"], window=128)
+                            merged=st["merged"], positions=st["positions"], window=128, merged_slots=True)
 
 
 def dsa_post(ops, st, ev=None):
+    """The sparse MLA decode over the merged rows, which hold cache slots (the
+    indexer and the latent cache share the block table)."""
     if ev is not None:
         ev[2].record()
     ops.sparse_mla_decode(st["q"], st["latent"], st["merged"], 256 ** -0.5, st["out"], st["lse"], sinks=st["sinks"],
-                          block_table=st["block_table"], req_ids=st["req_ids"], workspace=st["dec_ws"])
+                          workspace=st["dec_ws"])
     if ev is not None:
         ev[3].record()
 

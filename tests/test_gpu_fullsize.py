@@ -2,7 +2,7 @@
 
 The DSA decode step exactly as ``bench.py`` times it (``build_dsa_decode`` +
 ``dsa_step``: prologue with indexer prep -> one-launch filter, exact scoring
-and select with the merged output -> decode through the block table) at 32 x 131,072 tokens with
+and select with the merged output as cache slots -> decode) at 32 x 131,072 tokens with
 5% identical spike keys, and the multi-token step at 8 x 262,144 + 1 x
 1,048,576 tokens with 3 query rows per sequence, are checked against:
 
@@ -10,7 +10,8 @@ and select with the merged output -> decode through the block table) at 32 x 131
   full score rows) for every query row, bit-exact;
 * the numpy oracle for the rows whose top-k threshold is a tie among the
   spike keys and for further sampled rows: exact scores (as uint32 bits),
-  top-k, merged rows, and the decode output within
+  top-k, merged rows (the window merge through the block table), and the
+  decode output within
   |err| <= 2e-3 + 2e-2 |ref| (lse within 2e-3);
 * the cache bytes the step appended, and the indexer workspace's diagnostic
   counters (waits that gave up, histograms that never summed, rows selected
@@ -92,7 +93,9 @@ def _run_and_check(st, rows_to_check_extra, label):
     top2 = top2.cpu().numpy()
     bad = [t for t in range(B) if not np.array_equal(topk[t], top2[t])]
     assert not bad, f"fused top-k differs from the exact path on rows {bad}"
-    assert np.array_equal(merged, merge_swa_topk(topk, positions, merged.shape[1], WINDOW))
+    # the merged rows are cache slots: the window merge, then the block table
+    want = logical_to_global(merge_swa_topk(topk, positions, merged.shape[1], WINDOW), req, bt)
+    assert np.array_equal(merged, want)
 
     # the prologue's q / weights against the oracle's prep and quant
     _say(f"[{label}] prologue vs oracle")
@@ -135,8 +138,7 @@ def _run_and_check(st, rows_to_check_extra, label):
         ref = _oracle_scores(kcache_np, bt[req[t]], n, codes_q[t], wf[t])
         assert np.array_equal(ref.view(np.uint32), sc_gpu[t, :n].view(np.uint32)), f"row {t}: scores differ"
         assert np.array_equal(oi.topk_ascending(ref, TOPK), topk[t]), f"row {t}: top-k differs"
-        glob = logical_to_global(merged[t:t + 1], req[t:t + 1], bt)[0]
-        valid = glob[glob >= 0]
+        valid = merged[t][merged[t] >= 0]
         kv = _gather_latent(st["latent"], valid)
         ref_o, ref_l = od.sparse_mla_decode(q_dec[t:t + 1], lambda s: kv[s], np.arange(len(valid))[None],
                                             256 ** -0.5, 512, sinks)

@@ -193,6 +193,7 @@ struct DecodeSmem {
   __align__(8) int32_t red[64];                       // split location scratch
   int32_t slot[kMaxSplitEntries];
   __align__(16) float kscale[kMaxSplitEntries];       // row scale, 0 for masked entries
+  __align__(8) int64_t roff[kMaxSplitEntries];        // byte offset of the entry's row in the cache (masked: 0)
 };
 
 template <int D, bool BF16>
@@ -282,29 +283,51 @@ __device__ __forceinline__ int slot_entry(int kg, int m) { return m < 4 ? 4 * kg
 // row chunk swz(j, r).  Masked rows load the first cache row (their image
 // rows are zeroed once the tile has landed).  Padding instructions (when the
 // tile has fewer than kLoadsPerWave * 4) write the spill area.
+// A data wave's share of every tile's loads, fixed for the kernel: load j is
+// instruction k = j * kGroups + u, and this lane copies the tile's entry
+// `row` from byte `col` of its cached row.
 template <int D, bool BF16>
-__device__ __forceinline__ void issue_tile(const DecodeArgs& a, DecodeSmem<D, BF16>& sm, int u, int tile) {
+struct TileLanes {
+  static constexpr int kN = DecodeSmem<D, BF16>::kLoadsPerWave;
+  int row[kN], col[kN];
+};
+
+template <int D, bool BF16>
+__device__ __forceinline__ TileLanes<D, BF16> tile_lanes(int u) {
   using SM = DecodeSmem<D, BF16>;
   const int lane = threadIdx.x & 63;
-  int slots[SM::kLoadsPerWave];  // every slot read issued before the first use
+  TileLanes<D, BF16> tl;
 #pragma unroll
   for (int j = 0; j < SM::kLoadsPerWave; ++j) {
     const int k = j * kGroups + u;
     const int pos = (k < SM::kLoads ? k : 0) * 64 + lane;
-    slots[j] = sm.slot[tile * kTile + pos / SM::kChunks];
+    const int r = pos / SM::kChunks, jj = pos % SM::kChunks;
+    tl.row[j] = r;
+    tl.col[j] = 16 * swz_chunk<D, BF16>(jj, r);
   }
+  return tl;
+}
+
+// Byte offset of the cached row of a slot (-1: masked, read as row 0).
+template <int D, bool BF16>
+__device__ __forceinline__ int64_t row_offset(const DecodeArgs& a, int64_t s) {
+  if (s < 0) return 0;
+  if constexpr (BF16) return s * (2 * D);
+  else return (s >> 6) * a.page_stride + (s & 63) * D;
+}
+
+template <int D, bool BF16>
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, DecodeSmem<D, BF16>& sm, const TileLanes<D, BF16>& tl,
+                                           int u, int tile) {
+  using SM = DecodeSmem<D, BF16>;
+  int64_t ro[SM::kLoadsPerWave];  // every row offset read issued before the first use
+#pragma unroll
+  for (int j = 0; j < SM::kLoadsPerWave; ++j) ro[j] = sm.roff[tile * kTile + tl.row[j]];
 #pragma unroll
   for (int j = 0; j < SM::kLoadsPerWave; ++j) {
     const int k = j * kGroups + u;
-    const bool real = k < SM::kLoads;
-    const int pos = (real ? k : 0) * 64 + lane;
-    const int r = pos / SM::kChunks, jj = pos % SM::kChunks;
-    const int s = slots[j];
-    const uint8_t* row;
-    if constexpr (BF16) row = a.cache + static_cast<int64_t>(s < 0 ? 0 : s) * (2 * D);
-    else row = a.cache + static_cast<int64_t>(s < 0 ? 0 : s >> 6) * a.page_stride + (s < 0 ? 0 : (s & 63) * D);
-    const uint8_t* src = row + 16 * swz_chunk<D, BF16>(jj, r);
-    uint8_t* dst = real ? sm.img[tile % SM::kBufs] + 1024 * k : sm.spill;
+    const uint8_t* src = a.cache + ro[j] + tl.col[j];
+    uint8_t* dst = k < SM::kLoads ? sm.img[tile % SM::kBufs] + 1024 * k : sm.spill;
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
   }
 }
@@ -467,15 +490,19 @@ sparse_decode_kernel(DecodeArgs a) {
   for (int j = 0; j < kPrologue; ++j) {
     const int e = tid + kThreads * j;
     const int64_t slot = (sv[j] >= 0 && sv[j] < a.num_rows) ? sv[j] : -1;
-    if (e < e_pad) sm.slot[e] = static_cast<int32_t>(slot);
+    if (e < e_pad) {
+      sm.slot[e] = static_cast<int32_t>(slot);
+      sm.roff[e] = row_offset<D, BF16>(a, slot);
+    }
   }
   __syncthreads();
   // Data waves: the first kAhead tiles in flight (the only vector memory
   // operations they issue, so their load counter counts tiles).  Scorer
   // waves: the row scales and the q operands.
   bf16x8 qb[KS];  // B operand of S^T = K Q^T: head 16 grp + col, dims 32 ks + 8 kg .. +7
+  const TileLanes<D, BF16> tl = tile_lanes<D, BF16>(grp);
   if (!scorer) {
-    for (int i = 0; i < SM::kAhead && i < ntiles; ++i) issue_tile<D, BF16>(a, sm, grp, i);
+    for (int i = 0; i < SM::kAhead && i < ntiles; ++i) issue_tile<D, BF16>(a, sm, tl, grp, i);
     wait_tiles<D, BF16>(min(SM::kAhead, ntiles) - 1);  // tile 0 landed
     if (0 < ntiles) zero_masked<D, BF16>(sm, grp, 0);
   } else {
@@ -659,7 +686,7 @@ sparse_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < kCbB; ++i) ob[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s <= ntiles; ++s) {
-      if (s + SM::kAhead < ntiles) issue_tile<D, BF16>(a, sm, grp, s + SM::kAhead);
+      if (s + SM::kAhead < ntiles) issue_tile<D, BF16>(a, sm, tl, grp, s + SM::kAhead);
       if (s >= 1 && active) {
         const uint8_t* img = sm.img[(s - 1) % SM::kBufs];
         const int pb = (s - 1) & 1;
