@@ -13,8 +13,8 @@
 //     reference max only moves when a score exceeds it by more than 8 log2
 //     units), turns the weights P (row scale folded in) into a pair of bf16
 //     B operands hi = bf16(P), lo = bf16(P - hi), publishes them for the data
-//     wave and accumulates O^T[0, 128) += V^T P^T of tile s;
-//   * the data wave of a group accumulates O^T[128, 512) += V^T P^T of tile
+//     wave and accumulates O^T[0, 256) += V^T P^T of tile s;
+//   * the data wave of a group accumulates O^T[256, 512) += V^T P^T of tile
 //     s - 1 from the published operands, and issues the direct global->LDS
 //     loads of a later tile (coalesced 16-byte loads of whole rows).
 // V^T (channels x entries) is read straight from the row-major tile image
@@ -531,10 +531,11 @@ sparse_decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  // O^T accumulators: the scorer wave of a group holds channels [0, 128), the
-  // data wave [128, 512).  The two roles run separate loops with the same
-  // barriers (one per step, ntiles + 1 steps).
-  constexpr int kCbA = 8;
+  // O^T accumulators: the scorer wave of a group holds channels [0, 256), the
+  // data wave [256, 512) (an even split: the scorer's QK and softmax and the
+  // data wave's tile loads take about the same time).  The two roles run
+  // separate loops with the same barriers (one per step, ntiles + 1 steps).
+  constexpr int kCbA = 16;
   constexpr int kChains = 4;  // QK accumulation chains per entry half
   if (scorer) {
     f32x4 oa[kCbA];
@@ -646,7 +647,7 @@ sparse_decode_kernel(DecodeArgs a) {
     }
     // Epilogue: finish the heads' softmax (a row of one split gets the sink
     // and its lse here, otherwise (m, l) go to the combine), publish the
-    // factor for the data wave, scale and store channels [0, 128).
+    // factor for the data wave, scale and store channels [0, 256).
     float f = 0.0f;
     if (active) {
       float lt = lsum + __shfl_xor(lsum, 16);
