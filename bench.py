@@ -234,13 +234,14 @@ def measure_dsa_prefill(torch, ops, seed: int, chunk: int = 4096, ctx: int = 327
     return {
         "workload": f"dsa_prefill_chunk{chunk}_ctx{ctx}",
         "ms": round(ms, 3), "tok_per_s": round(chunk / (ms * 1e-3), 1),
-        "indexer_filter_ms": round(filt_ms, 3), "decode_ms": round(dec / reps, 3),
+        "indexer_topk_ms": round(filt_ms, 3), "decode_ms": round(dec / reps, 3),
         "indexer_keys_scored": keys, "indexer_key_bytes": keys * 132,
         "indexer_fp8_tflops": round(flops / (filt_ms * 1e-3) / 1e12, 1),
         "indexer_mfma_frac": round(flops / (filt_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
         "what": "one request's prefill chunk as query rows through the DSA step (prologue, indexer top-k with "
-                "merged rows, sparse MLA); the indexer top-k (filter, bound, verify and select launches) is timed "
-                "by events around its call",
+                "merged rows, sparse MLA); indexer_topk_ms = the indexer top-k call (filter, bound, verify and "
+                "select launches, merged rows as cache slots) timed by events around it; indexer_mfma_frac = its "
+                "fp8 filter flops over that time",
     }
 
 
