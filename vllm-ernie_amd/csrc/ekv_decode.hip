@@ -171,7 +171,11 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
 // with each row's 16-byte chunks permuted (chunk j of row r is stored at
 // chunk swz(j, r), an XOR within runs of 8 chunks, of 4 for the last 4 of a
 // 36-chunk row) so that the 16 rows a fragment read touches spread over the
-// LDS banks.  Rows arrive by direct global->LDS loads: lane i of a load
+// LDS banks.  For 576-byte rows (144 dwords, so rows 4 apart start on the
+// same bank) the XOR value is parity(r & 6) | parity(r & 9) << 1 |
+// parity(r & 16) << 2, which leaves both the QK fragment reads (rows
+// 0..15 or 16..31 at one chunk) and the transposed P·V reads (rows
+// 4 kg .. 4 kg + 3 and 16 + 4 kg .. at one chunk) free of bank conflicts.  Rows arrive by direct global->LDS loads: lane i of a load
 // instruction writes bytes [16 i, 16 i + 16) of the instruction's 1 KB.
 template <int D, bool BF16>
 struct DecodeSmem {
@@ -201,9 +205,10 @@ __device__ __forceinline__ int swz_chunk(int j, int r) {
   using SM = DecodeSmem<D, BF16>;
   if constexpr (SM::kChunks % 8 == 0) {
     return j ^ (r & 7);
-  } else {  // 36 chunks: rows 2 apart start on the same banks, so permute by r / 2
-    const int x = r >> 1;
-    return j < 32 ? (j ^ (x & 7)) : (32 + ((j - 32) ^ (x & 3)));
+  } else {
+    const int f = (__builtin_popcount(r & 6) & 1) | ((__builtin_popcount(r & 9) & 1) << 1) |
+                  ((__builtin_popcount(r & 16) & 1) << 2);
+    return j < 32 ? (j ^ f) : (32 + ((j - 32) ^ (f & 3)));
   }
 }
 
