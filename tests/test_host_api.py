@@ -152,3 +152,26 @@ def test_indexer_k_cache_row_bytes():
     (attention.py:929-935)."""
     assert _indexer(True).k_cache.head_dim == 68
     assert _indexer(False).k_cache.head_dim == 132
+
+
+def test_hca_write_workspace_size_in_span_slots():
+    """ekv_hca_write_workspace_size(num_spans, dim) (host arithmetic only):
+    monotone in the span count, independent of the width (the layout holds
+    576-wide slots so one buffer serves both widths), zero for an invalid
+    width, and Python's hca_write_workspace sizes prefill calls by their span
+    slots: num_seqs * (max_query_len // 128 + 1)."""
+    from ernie_kv import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libernie_kv.so not built (run __graft_entry__.build())")
+    lib = _lib.load()
+    size = lib.ekv_hca_write_workspace_size
+    sizes = [size(n, 576) for n in range(1, 3000, 7)]
+    assert all(b > a for a, b in zip(sizes, sizes[1:]))
+    for n in (1, 16, 1040, 4096):
+        assert size(n, 512) == size(n, 576)
+        # counters (u32, padded to 256 B) then 576 + 144 floats per slot
+        assert size(n, 576) == (n * 4 + 255) // 256 * 256 + n * (576 + 144) * 4
+    assert size(0, 576) == 0 and size(16, 0) == 0 and size(16, 1024) == 0
+    # 16 sequences of 8192-row chunks complete at most 16 * 65 spans
+    assert size(16 * (8192 // 128 + 1), 576) > size(16, 576)
