@@ -89,13 +89,15 @@ def test_hca_write_path_exact(dev, dim, fused, rope):
         "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
     }
     # chunked prefill, partial spans carried in the state ring, then MTP-style
-    # 3-token steps, a rollback re-append, and a long chunk.
+    # 3-token steps, a rollback re-append, a long chunk, and a prefill call in
+    # which one sequence has no rows.
     calls = [
         ([0, 0, 0], [300, 100, 128]),
         ([300, 100, 128], [3, 200, 2]),
         ([303, 300, 130], [3, 3, 3]),
         ([304, 301, 131], [3, 3, 3]),  # rollback: re-append from one position back
         ([307, 304, 134], [900, 1, 700]),
+        ([1207, 305, 834], [0, 260, 130]),  # spans 2 and 3 of sequence 1, span 6 of sequence 2 (from the ring)
     ]
     for starts, counts in calls:
         _run_call(dev, case, rng, starts, counts, gpu, fused)
