@@ -285,6 +285,92 @@ def test_hca_decode_step_graph_replay(dev):
                                b_.view(torch.uint8) if b_.dtype == torch.bfloat16 else b_), f"replay {rep}: {name}"
 
 
+def test_hca_write_graph_keeps_compression_the_capture_batch_skipped(dev):
+    """A captured graph keeps the 128-span compression even when the batch it
+    was captured with completes no span (the reference's
+    test_compressor_skip_not_baked_into_cuda_graph,
+    test_dsa_backend.py:92-127): ekv_hca_write_step is captured with
+    positions that complete nothing, then replayed with positions of which two
+    complete a span; the pool, state ring, index rows and lengths equal an
+    eager call on the replay's inputs from the same starting state."""
+    from ernie_kv import ops
+
+    g = torch.Generator(device=dev).manual_seed(23)
+    B, D, ring, window = 6, 576, 192, 128
+    ctx_capture = torch.tensor([300, 1000, 777, 2000, 1500, 130], dtype=torch.int64)  # no span ends
+    ctx_replay = torch.tensor([301, 1024, 778, 2048, 1501, 131], dtype=torch.int64)   # 1024, 2048 end spans
+    spans = int(ctx_replay.max()) // 128 + 1
+    comp_pp, ring_pp = (spans + 63) // 64, ring // 64
+    lat_pp = (int(ctx_replay.max()) + 63) // 64
+    pages = B * (comp_pp + ring_pp + lat_pp)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(6)).to(torch.int32)
+    comp_bt = perm[: B * comp_pp].view(B, comp_pp).to(dev)
+    ring_pages = perm[B * comp_pp: B * (comp_pp + ring_pp)].view(B, ring_pp).to(dev)
+    lat_bt = perm[B * (comp_pp + ring_pp):].view(B, lat_pp).to(torch.int64)
+    rnd = lambda *s_: torch.randn(*s_, device=dev, generator=g).to(torch.bfloat16)  # noqa: E731
+    ang = (torch.arange(spans, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    seq = torch.arange(B)
+
+    def inputs(ctx):
+        pos = ctx - 1
+        return pos.to(dev), (lat_bt[seq, pos // 64] * 64 + pos % 64).to(dev)
+
+    pos_c, slots_c = inputs(ctx_capture)
+    pos_r, slots_r = inputs(ctx_replay)
+    args = dict(latent=rnd(B, D), kv_score=rnd(B, 2 * D), slot_mapping=slots_c.clone(), positions=pos_c.clone(),
+                token_seq=seq.to(torch.int32).to(dev), qsl=torch.arange(B + 1, dtype=torch.int32, device=dev),
+                max_query_len=1, state_slot=torch.arange(B, dtype=torch.int32, device=dev),
+                ape=(0.5 * torch.randn(128, D, device=dev, generator=g)).contiguous(),
+                norm_w=(1.0 + 0.1 * torch.randn(D, device=dev, generator=g)).contiguous(), eps=1e-6,
+                cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], 1).to(torch.float32).to(dev),
+                comp_block_table=comp_bt, ring_pages=ring_pages, ring=ring)
+    state0 = rnd(B, 256, 2 * D)
+    pool0 = torch.randint(0, 126, (pages, paged.fp8_page_bytes(D)), device=dev, dtype=torch.uint8, generator=g)
+    width = int(ctx_replay.max()) // 128 + window
+    pool, state = pool0.clone(), state0.clone()
+    idx = torch.full((B, width), -7, dtype=torch.int32, device=dev)
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    ws = ops.hca_write_workspace(B, D, dev)
+
+    def step():
+        ops.hca_write_step(pool=pool, state=state, window=window, out=idx, lengths=lens, workspace=ws, **args)
+
+    step()  # warm-up with the capture batch
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    def reset(pos, slots):
+        pool.copy_(pool0)
+        state.copy_(state0)
+        idx.fill_(-7)
+        lens.zero_()
+        args["positions"].copy_(pos)
+        args["slot_mapping"].copy_(slots)
+        torch.cuda.synchronize()
+
+    reset(pos_r, slots_r)
+    step()  # eager on the replay's inputs
+    torch.cuda.synchronize()
+    want = [x.clone() for x in (pool, state, idx, lens)]
+    assert not torch.equal(want[0], pool0), "the replay batch must write"
+    for rep in range(2):
+        reset(pos_r, slots_r)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a_, b_ in zip(["pool", "state", "idx", "lens"], (pool, state, idx, lens), want):
+            assert torch.equal(a_.view(torch.uint8) if a_.dtype == torch.bfloat16 else a_,
+                               b_.view(torch.uint8) if b_.dtype == torch.bfloat16 else b_), f"replay {rep}: {name}"
+    # the two completed spans were written: their compressed slots differ from the starting pool
+    for b_, j in ((1, 1023 // 128), (3, 2047 // 128)):
+        page = int(comp_bt[b_, j // 64])
+        off = (j % 64) * D
+        assert not torch.equal(pool[page, off:off + D], pool0[page, off:off + D]), f"span {j} of sequence {b_}"
+
+
 @pytest.mark.parametrize("rows", [1, 3, 130], ids=["decode", "drafts", "prefill-sized"])
 @pytest.mark.parametrize("use_ws", [False, True], ids=["no-ws", "ws"])
 def test_hca_write_step_matches_separate_calls(dev, rows, use_ws):
