@@ -537,7 +537,8 @@ def hca_decode_bytes(st) -> dict:
 def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None = None, label: str | None = None) -> dict:
     st = build_hca_decode(torch, ops, seed, ctxs=ctxs)
     ms_eager = time_ms(torch, lambda: hca_decode_step(ops, st), reps)
-    ms = graph_ms(torch, lambda: hca_decode_step(ops, st), reps)
+    ms_graph = graph_ms(torch, lambda: hca_decode_step(ops, st), reps)
+    ms = min(ms_eager, ms_graph)
     by = hca_decode_bytes(st)
     workload = label or f"hca_decode_b{st['B']}_ctx8192-131072"
     return {
@@ -545,8 +546,10 @@ def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None 
         "kernels": "hca_write_small_kernel<576> (the new tokens' rows, ring, state; spans they complete; the "
                    "index rows) + sparse_decode_kernel<576> + decode_combine_kernel",
         "ms": round(ms, 4),
+        "ms_graph": round(ms_graph, 4),
         "ms_eager": round(ms_eager, 4),
-        "launch": "hip_graph: one captured step replayed (ms); ms_eager = the same step launched eagerly",
+        "launch": "ms = the faster of a HIP graph replaying one captured step (ms_graph) and the same step "
+                  "launched eagerly (ms_eager)",
         "rows_per_step": by.pop("rows"),
         "bytes": by,
         "GB/s": round(by["total"] / (ms * 1e-3) / 1e9, 1),
@@ -938,7 +941,7 @@ def main():
     torch.cuda.empty_cache()
     # each layer type in its faster launch mode (graph replay or eager)
     dsa_ms = min(line["ms_per_step"], line["ms_per_step_eager"])
-    hca_ms = min(hca_head["ms"], hca_head["ms_eager"])
+    hca_ms = hca_head["ms"]  # (already the faster mode)
     model_ms = MODEL_LAYERS["dsa"] * dsa_ms + MODEL_LAYERS["hca"] * hca_ms
     line.update({
         "tok_per_s": round(args.batch / (model_ms * 1e-3), 1),
