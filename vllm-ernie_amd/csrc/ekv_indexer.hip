@@ -1678,6 +1678,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     constexpr int kKeys = 8;  // loads in flight per thread
     uint32_t kmax = 0u;       // the row's largest key
     if (tid == 0) s_misc[26] = 0;
+    // the lists' offsets in scalar registers when the row has at most
+    // kRegLists workgroups (past G: no key is that far)
+    constexpr int kRegLists = 8;
+    int offr[kRegLists];
+#pragma unroll
+    for (int i = 0; i < kRegLists; ++i) offr[i] = __builtin_amdgcn_readfirstlane(i < G ? s_off[i] : INT_MAX);
     for (int p0 = 0; p0 < n_row; p0 += kKeys * kThreads) {
       float v[kKeys];
 #pragma unroll
@@ -1685,13 +1691,25 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         const int p = p0 + tid + j * kThreads;
         v[j] = 0.0f;
         if (p < n_row) {
-          int y = 0, hi = G - 1;  // the last list with s_off[y] <= p (empty lists are skipped)
-          while (y < hi) {
-            const int mid = (y + hi + 1) >> 1;
-            if (s_off[mid] <= p) y = mid;
-            else hi = mid - 1;
+          // the last list with its offset <= p (empty lists are skipped)
+          int y = 0, off = offr[0];
+          if (G <= kRegLists) {
+#pragma unroll
+            for (int i = 1; i < kRegLists; ++i)
+              if (offr[i] <= p) {
+                y = i;
+                off = offr[i];
+              }
+          } else {
+            int hi = G - 1;
+            while (y < hi) {
+              const int mid = (y + hi + 1) >> 1;
+              if (s_off[mid] <= p) y = mid;
+              else hi = mid - 1;
+            }
+            off = s_off[y];
           }
-          v[j] = __uint_as_float(ld_agent(a.cand_score + row0 + y * seg_tokens + (p - s_off[y])));
+          v[j] = __uint_as_float(ld_agent(a.cand_score + row0 + y * seg_tokens + (p - off)));
         }
       }
 #pragma unroll
