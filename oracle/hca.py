@@ -9,7 +9,11 @@ which appends the latent by ``slot_mapping`` and runs ``DeepseekCompressor``
 below is a restatement of the DeepSeek-V4 compressor as described by its call
 sites -- **parity unpinned** against upstream; it is pinned against closed
 forms (constant gate -> mean, one-hot gate -> copy, permutation invariance) and
-an fp64 brute force in ``tests/test_oracle_hca.py``.
+an fp64 brute force in ``tests/test_oracle_paths.py``.  Its RoPE pairing
+(interleaved pairs of the last 64 channels, rotated forward) is pinned by the
+reference's own inverse rotation of these rows (``_vha_inv_rope_quant_kernel``,
+``attention.py:166-229``, restated in ``oracle.quant``), which undoes it; the
+rotation position 128 j of compressed entry j stays parity unpinned.
 
 Compressor of span j (positions 128j .. 128j+127), per channel c < D: the
 softmax over the span of g_i = fl32(score_i[c] + ape[i, c]) weights kv_i[c].
@@ -62,9 +66,11 @@ STATE_RING = 256
 WINDOW = 128
 
 LOG2E = np.float32(1.0 / math.log(2.0))
-# P(f) ~ 2**f on [-1/2, 1/2]: degree 5, coefficients from a Remez exchange on
-# the relative error (then rounded to fp32, P(0) = 1 exactly); evaluated in
-# fp32 Horner with fused multiply-adds its relative error is below 2.2e-7.
+# P(f) ~ 2**f on [-1/2, 1/2]: degree 5, P(0) = 1 exactly, fp32 coefficients
+# fit to the relative error of the fp32 evaluation; within 2x of the exact
+# minimax error (9.1e-8) and, evaluated in fp32 Horner with fused
+# multiply-adds, below 2.2e-7 relative error.  tests/test_oracle_paths.py
+# re-derives the minimax fit by a Remez exchange and checks these bounds.
 EXP_C = [np.float32(float.fromhex(h)) for h in (
     "0x1.0p+0", "0x1.62e428p-1", "0x1.ebf918p-3", "0x1.c6b6e4p-5", "0x1.3d0c52p-7", "0x1.5c08e6p-10")]
 

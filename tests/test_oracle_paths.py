@@ -305,6 +305,56 @@ def test_compressor_permutation_invariance():
     np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("D", [512, 576])
+def test_compressor_rope_is_undone_by_the_reference_inverse_rope(D):
+    """The compressor's rotation of the last 64 channels is the one the
+    reference's own post-attention kernel inverts: ``_vha_inv_rope_quant_kernel``
+    (attention.py:166-229) maps each interleaved pair (2i, 2i+1) of the rope
+    dims to ``(e cos + o sin, o cos - e sin)`` with ``cos | sin`` from the same
+    table row (``:208-219``), restated as ``oracle.quant.vha_inv_rope_quant``.
+    Applied at the same position to a compressed row it must give back the
+    row before its rotation (the compressor run with cos = 1, sin = 0), within
+    fp32 rounding.  A compressor that rotated NeoX halves (i, i + 32), or
+    rotated the other way, fails this."""
+    from oracle import quant as oq
+
+    rng = np.random.default_rng(21)
+    kv, sc = _span(rng, D)
+    ape = (rng.standard_normal((128, D)) * 0.5).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    pos = 128 * 500
+    cs = oi.rope_cos_sin(np.array([pos]), 64, 1.6e5)[0]
+    ident = np.concatenate([np.ones(32, np.float32), np.zeros(32, np.float32)])
+    rotated = oh.compress_span(kv, sc, ape, w, 1e-6, cs)
+    plain = oh.compress_span(kv, sc, ape, w, 1e-6, ident)
+    assert np.array_equal(rotated[: D - 64], plain[: D - 64])
+
+    def inverse(row):
+        # the last 512 channels as head 0 of an identity head mix, nope 448
+        o = np.zeros((1, 64, 512), np.float32)
+        o[0, 0] = row[D - 512:]
+        table = np.zeros((pos + 1, 64), np.float32)
+        table[pos] = cs
+        y = oq.vha_inv_rope_quant(o, np.eye(64, dtype=np.float32), np.array([pos]), table, 1, 448, 64,
+                                  quantize=False)
+        return y[0, 0, 448:]
+
+    tol = 4e-6 * np.abs(plain[D - 64:]).max()
+    assert np.abs(inverse(rotated) - plain[D - 64:]).max() <= tol
+
+    # planted mistakes in the rotation: NeoX halves, and the opposite direction
+    c, s = cs[:32], cs[32:]
+    r = plain[D - 64:].copy()
+    neox = np.concatenate([r[:32] * c - r[32:] * s, r[:32] * s + r[32:] * c]).astype(np.float32)
+    backwards = r.copy()
+    backwards[0::2] = r[0::2] * c + r[1::2] * s
+    backwards[1::2] = r[1::2] * c - r[0::2] * s
+    for wrong in (neox, backwards):
+        row = plain.copy()
+        row[D - 64:] = wrong
+        assert np.abs(inverse(row) - plain[D - 64:]).max() > 100 * tol
+
+
 def _fma32_exact(a, b, c):
     """Correctly rounded fp32 a*b + c by exact rational arithmetic: the
     nearest of the fp32 values around the fp64 approximation, ties to the
@@ -354,6 +404,63 @@ def test_exp_ekv_accuracy():
     x = np.linspace(-60, 0, 200001).astype(np.float32)
     np.testing.assert_allclose(oh.exp_ekv(x), np.exp(x.astype(np.float64)), rtol=5e-6)
     assert oh.exp_ekv(np.float32(0.0)) == 1.0 and oh.exp_ekv(np.float32(-200.0)) == 0.0
+
+
+def _remez_exp2_rel(deg=5, iters=40):
+    """Minimax relative-error polynomial P of degree ``deg`` with P(0) = 1 for
+    2**f on [-1/2, 1/2], by a Remez exchange: with P(f) = 1 + f Q(f) the
+    relative error is |f| 2**-f (Q(f) - g(f)) up to sign, g(f) = (2**f - 1)/f,
+    so Q is the weighted minimax fit of the smooth g with weight |f| 2**-f.
+    Returns (coefficients [1, q0, .., q_{deg-1}], minimax error)."""
+    grid = np.linspace(-0.5, 0.5, 400001)
+    grid = grid[grid != 0]
+    g = np.expm1(grid * math.log(2.0)) / grid
+    wt = np.abs(grid) * np.exp2(-grid)
+    n = deg + 1
+    x = 0.5 * np.cos(np.pi * (np.arange(n)[::-1] + 0.5) / n)
+    for _ in range(iters):
+        wx = np.abs(x) * np.exp2(-x)
+        A = np.concatenate([wx[:, None] * x[:, None] ** np.arange(deg)[None, :],
+                            -((-1.0) ** np.arange(n))[:, None]], axis=1)
+        sol = np.linalg.solve(A, wx * np.expm1(x * math.log(2.0)) / x)
+        q, E = sol[:deg], abs(sol[deg])
+        e = wt * (np.polyval(q[::-1], grid) - g)
+        # one extremum per run of equal sign, then the n largest alternating
+        edges = np.flatnonzero(np.diff(np.sign(e)) != 0) + 1
+        idx = np.array([s[np.argmax(np.abs(e[s]))] for s in np.split(np.arange(len(grid)), edges)])
+        while len(idx) > n:
+            idx = idx[1:] if abs(e[idx[0]]) < abs(e[idx[-1]]) else idx[:-1]
+        x = grid[idx]
+        if np.abs(e).max() <= E * (1 + 1e-9):
+            break
+    return np.concatenate([[1.0], q]), np.abs(e).max()
+
+
+def test_exp_polynomial_is_a_near_minimax_fit():
+    """Provenance of EXP_C, the compressor's degree-5 polynomial for 2**f on
+    [-1/2, 1/2]: re-derive the minimax relative-error fit (with P(0) = 1) by a
+    Remez exchange and bound EXP_C against it.  EXP_C is within 2x of the
+    optimum in exact arithmetic (it was fit to the fp32-rounded evaluation),
+    its coefficients within 1e-3 of the optimum's, and its fp32 Horner-with-FMA
+    evaluation -- the kernel's -- stays below the 2.2e-7 relative error the
+    oracle states."""
+    coef, emin = _remez_exp2_rel()
+    assert 8e-8 < emin < 1e-7  # degree 5 on a unit interval: ~9.1e-8
+    f = np.linspace(-0.5, 0.5, 400001)
+    c = np.array([float(v) for v in oh.EXP_C])
+    assert c[0] == 1.0
+    rel = np.abs(np.polyval(c[::-1], f) * np.exp2(-f) - 1.0).max()
+    assert emin <= rel <= 2.0 * emin
+    assert np.all(np.abs(c / coef - 1.0) < 1e-3)
+    # the fp32 evaluation the kernel performs
+    f32 = f.astype(np.float32)
+    p = np.broadcast_to(oh.EXP_C[5], f32.shape).astype(np.float32)
+    for k in range(4, -1, -1):
+        p = oh.fma32(p, f32, oh.EXP_C[k])
+    assert np.abs(p.astype(np.float64) / np.exp2(f32.astype(np.float64)) - 1.0).max() < 2.2e-7
+    # a dropped term: the best degree-4 fit is ~12x worse than the stated bound
+    c4, e4 = _remez_exp2_rel(deg=4)
+    assert e4 > 10 * 2.2e-7
 
 
 def test_hca_rollback_recompresses_from_latest_rows():
