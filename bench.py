@@ -66,8 +66,8 @@ def parse():
     p.add_argument("--no-fp4", action="store_true", help="skip the MXFP4 indexer measurement")
     p.add_argument("--no-prefill", action="store_true", help="skip the DSA prefill-chunk measurement")
     p.add_argument("--no-pages", action="store_true", help="skip the page-format transcoder measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "hca_layer", "mtp", "dsa", "indexer_fp4",
-                                      "dsa_prefill", "pages"],
+    p.add_argument("--only", choices=["hca_write", "hca_decode", "hca_layer", "mtp", "dsa", "dsa_random_row",
+                                      "indexer_fp4", "dsa_prefill", "pages"],
                    default=None,
                    help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -90,12 +90,32 @@ def traffic_of(workload: str, kernel: str):
 
 
 # --------------------------------------------------------------------------- DSA step
+SPIKE_SIGMA = 4.0
+
+
 def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, spike_frac: float = 0.05,
-                     extra_tokens: int = 0):
+                     extra_tokens: int = 0, spikes: str = "sigma4"):
     """Synthetic DSA-layer decode state: sequence s holds ctxs[s] tokens, the
     last rows_per_seq of them new this step (one query row each: the token
     and its draft tokens), in permuted pages (extra_tokens more positions
-    are mapped for steps that grow the sequences)."""
+    are mapped for steps that grow the sequences).
+
+    Indexer keys (``spike_frac`` of the scored positions are spikes):
+
+    * ``spikes="sigma4"`` (the DSA decode workload at 5% spikes): every key is
+      an N(0,1) bf16 row written by the library's K insert (fp8 codes + UE8M0
+      scale); each sequence then gets its own spike key row whose exact score
+      for the sequence's query row is the smallest reachable at or above
+      mean + 4 sigma of the row's ordinary scores, written at a seeded
+      ``spike_frac`` of its scored positions.  The spikes score identically,
+      so a row's top-2048 is the few ordinary tokens above +4 sigma and then
+      the lowest-index spikes: every row's threshold is a tie.
+    * ``spikes="random_row"``: uniformly random fp8 codes (scale 2^-8) and
+      one random code row copied into ``spike_frac`` of all positions; its
+      score is random, so it ties the threshold of only some rows.
+    """
+    if spike_frac <= 0:
+        spikes = "none"
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
     S, R = len(ctxs), rows_per_seq
@@ -116,8 +136,17 @@ def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, s
         scales = torch.full((num_pages, 64), 2.0 ** scale_exp, device=dev, dtype=torch.float32)
         return torch.cat([pages, scales.view(torch.uint8)], dim=1).contiguous()
 
-    kcache = random_fp8_pages(128, -8)
-    if spike_frac > 0:
+    if spikes == "sigma4":
+        kcache = torch.zeros((num_pages, 64 * 132), dtype=torch.uint8, device=dev)
+        rows = num_pages * 64
+        for r0 in range(0, rows, 1 << 20):
+            n = min(1 << 20, rows - r0)
+            k = torch.randn(n, 128, device=dev, generator=g).to(torch.bfloat16)
+            ops.indexer_k_insert(k, torch.arange(r0, r0 + n, device=dev, dtype=torch.int64), kcache)
+        del k
+    else:
+        kcache = random_fp8_pages(128, -8)
+    if spikes == "random_row":
         # a fraction of tokens hold one identical "spike" key row: exact score ties
         spike = kcache[0, :128].clone()
         mask = torch.rand(num_pages, 64, device=dev, generator=g) < spike_frac
@@ -150,7 +179,58 @@ def build_dsa_decode(torch, ops, ctxs: list, seed: int, rows_per_seq: int = 1, s
     st["rope"] = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).contiguous()
     st["dec_ws"] = ops.decode_workspace(B, 64, 2176, dev)
     st["idx_ws"] = ops.indexer_topk_workspace(B, ctx, dev)
+    if spikes == "sigma4":
+        _place_sigma_spikes(torch, ops, st, g, spike_frac)
     return st
+
+
+def _place_sigma_spikes(torch, ops, st, g, spike_frac: float, sigma: float = SPIKE_SIGMA) -> None:
+    """Per sequence, a spike key row scoring mean + `sigma` standard
+    deviations of its query row's ordinary exact scores (the smallest such
+    score the row's fp8 quantization reaches), written by the K insert at a
+    seeded `spike_frac` of the sequence's scored positions."""
+    dev = st["kcache"].device
+    S, R = st["S"], st["R"]
+    dsa_pre(ops, st)  # q codes and folded weights of the step's query rows
+    scores = torch.empty((st["B"], st["ctx"]), dtype=torch.float32, device=dev)
+    ops.indexer_score(st["digits"], st["wf"], st["kcache"], st["block_table"], st["req_ids"], st["lengths"],
+                      st["ctx"], scores)
+    lut = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).to(torch.float64).to(dev)
+    lengths = st["lengths"].cpu()
+    # candidate spike rows beta * v / rms(v), beta = 2^-8 .. 2^8 in steps of 2^(1/256)
+    betas = torch.exp2(torch.arange(-2048, 2048, device=dev, dtype=torch.float64) / 256.0)
+    J = betas.numel()
+    scratch = torch.zeros((J // 64, 64 * 132), dtype=torch.uint8, device=dev)
+    spike_rows, spike_slots, achieved = [], [], []
+    for s in range(S):
+        t = s * R  # the sequence's first query row
+        n = int(lengths[t])
+        ordinary = scores[t, :n].double()
+        mu, sd = float(ordinary.mean()), float(ordinary.std())
+        target = mu + sigma * sd
+        qd = lut[st["q8"][t].long()]  # [64, 128]
+        w = st["wf"][t].double()
+        v = (w.clamp(min=0)[:, None] * qd).sum(0)
+        v = v / v.pow(2).mean().sqrt()
+        cand = (betas[:, None] * v[None, :]).to(torch.bfloat16)
+        ops.indexer_k_insert(cand, torch.arange(J, device=dev, dtype=torch.int64), scratch)
+        codes = scratch[:, : 64 * 128].reshape(J, 128)
+        scale = scratch[:, 64 * 128:].contiguous().view(torch.float32).reshape(J).double()
+        est = ((lut[codes.long()] @ qd.T).clamp(min=0) * w[None, :]).sum(1) * scale
+        ok = torch.nonzero(est >= target).flatten()
+        if ok.numel() == 0:
+            raise RuntimeError(f"no spike row reaches +{sigma} sigma for sequence {s}")
+        j = int(ok[0])
+        achieved.append((float(est[j]) - mu) / sd)
+        mask = torch.rand(n, device=dev, generator=g) < spike_frac
+        pos = torch.nonzero(mask).flatten()
+        bt = st["block_table"][s]
+        spike_slots.append(bt[pos // 64].to(torch.int64) * 64 + pos % 64)
+        spike_rows.append(cand[j:j + 1].expand(pos.numel(), 128))
+    ops.indexer_k_insert(torch.cat(spike_rows).contiguous(), torch.cat(spike_slots).contiguous(), st["kcache"])
+    torch.cuda.synchronize()
+    st["spikes"] = {"sigma": [round(a, 3) for a in achieved],
+                    "per_row": [int(x.numel()) for x in spike_slots]}
 
 
 def dsa_step(ops, st, ev=None):
@@ -538,7 +618,7 @@ def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None 
     st = build_hca_decode(torch, ops, seed, ctxs=ctxs)
     ms_eager = time_ms(torch, lambda: hca_decode_step(ops, st), reps)
     ms_graph = graph_ms(torch, lambda: hca_decode_step(ops, st), reps)
-    ms = min(ms_eager, ms_graph)
+    ms = ms_graph  # the serving mode: the step captured once and replayed
     by = hca_decode_bytes(st)
     workload = label or f"hca_decode_b{st['B']}_ctx8192-131072"
     return {
@@ -548,8 +628,8 @@ def measure_hca_decode(torch, ops, seed: int, reps: int = 50, ctxs: list | None 
         "ms": round(ms, 4),
         "ms_graph": round(ms_graph, 4),
         "ms_eager": round(ms_eager, 4),
-        "launch": "ms = the faster of a HIP graph replaying one captured step (ms_graph) and the same step "
-                  "launched eagerly (ms_eager)",
+        "launch": "ms = a HIP graph replaying one captured step (ms_graph, the serving mode); ms_eager = the "
+                  "same step launched eagerly",
         "rows_per_step": by.pop("rows"),
         "bytes": by,
         "GB/s": round(by["total"] / (ms * 1e-3) / 1e9, 1),
@@ -694,12 +774,15 @@ def _cpu_dsa_row(args):
     from oracle import indexer as oi
     from oracle.fp8 import bf16_round, decode_e4m3
 
+    from oracle.fp8 import quantize_rows
+
     ctx, seed = args
     rng = np.random.default_rng(seed)
     n = max(ctx - 128, 0)
-    codes = rng.integers(0, 256, (n, 128)).astype(np.uint8)
-    codes[(codes & 0x7F) == 0x7F] ^= 1
-    kscale = np.full(n, 2.0 ** -8, np.float32)
+    # N(0,1) key rows quantized as the K insert does; 5% of them one spike row
+    codes, kscale = quantize_rows(bf16_round(rng.standard_normal((n, 128)).astype(np.float32)))
+    spike = rng.random(n) < 0.05
+    codes[spike], kscale[spike] = codes[0], kscale[0]
     q = bf16_round(rng.standard_normal((64, 128)).astype(np.float32))
     w = bf16_round(rng.standard_normal(64).astype(np.float32))
     lat_codes = rng.integers(0, 256, (2176, 576)).astype(np.uint8)
@@ -790,8 +873,9 @@ def cpu_baselines(B: int, ctx: int, seed: int) -> dict:
     out["dsa"] = {
         "value": round(by / wall / 1e9, 4), "unit": "GB/s", "cores": workers, "kind": "port",
         "sample": f"the whole headline step on the CPU: {B} query rows at ctx {ctx} (exact scores of "
-                  f"{max(ctx - 128, 0)} keys each, top-2048, 64-head decode over 2176 rows), numpy oracle, one "
-                  f"row per job on {workers} processes: {wall:.2f} s wall, {busy:.1f} core-s",
+                  f"{max(ctx - 128, 0)} N(0,1) keys each with 5% identical spike rows, top-2048, 64-head decode "
+                  f"over 2176 rows), numpy oracle, one row per job on {workers} processes (the GPU box's CPU share "
+                  f"is 16 cores): {wall:.2f} s wall, {busy:.1f} core-s",
         "tok_per_s": round(B / wall, 3), "ms_per_step": round(wall * 1e3, 1),
     }
     rng = np.random.default_rng(seed + 1)
@@ -821,6 +905,51 @@ def cpu_baselines(B: int, ctx: int, seed: int) -> dict:
 
 
 # --------------------------------------------------------------------------- main
+def time_dsa(torch, ops, st, steps: int, warmup: int):
+    """(graph-replay ms, eager ms, indexer top-k call ms, decode call ms) of the
+    DSA step on `st`: `steps` eager steps with events around the top-k and
+    decode calls, then `steps` replays of one captured step."""
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        dsa_step(ops, st)
+    torch.cuda.synchronize()
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(4)) for _ in range(steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(steps):
+        dsa_step(ops, st, evs[i])
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_eager = t_start.elapsed_time(t_end) / steps
+    # the timed steps: replays of one captured step (the whole DSA step is
+    # graph-capturable: fixed workspaces, no host synchronization)
+    ms_step = graph_ms(torch, lambda: dsa_step(ops, st), steps)
+    filt_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    dec_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / steps
+    return ms_step, ms_eager, filt_ms, dec_ms
+
+
+def measure_dsa_random_row(torch, ops, args) -> dict:
+    """The DSA step at the headline shape on uniformly random key codes with
+    one random spike row in 5% of the positions (its score is random, so it
+    ties the threshold of only some rows)."""
+    st = build_dsa_decode(torch, ops, [args.ctx] * args.batch, args.seed, spikes="random_row")
+    ms_step, ms_eager, filt_ms, dec_ms = time_dsa(torch, ops, st, args.steps, args.warmup)
+    by = dsa_bytes(args.batch, args.ctx)
+    del st
+    return {
+        "workload": f"dsa_decode_b{args.batch}_ctx{args.ctx}_random_spike_row",
+        "ms": round(ms_step, 4), "ms_eager": round(ms_eager, 4),
+        "GB/s": round(by["total"] / (ms_step * 1e-3) / 1e9, 1),
+        "frac": round(by["total"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "indexer_topk_ms": round(filt_ms, 4), "decode_ms": round(dec_ms, 4),
+        "what": "the headline DSA step (graph replays) on uniformly random fp8 key codes at scale 2^-8 with one "
+                "random key row copied into 5% of the positions",
+    }
+
+
 def measure_dsa(torch, ops, args, line: dict) -> None:
     st = build_dsa_decode(torch, ops, [args.ctx] * args.batch, args.seed)
     if args.copy_mb > 0:
@@ -828,25 +957,7 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
         dst = torch.empty_like(src)
         dst.copy_(src)
         del src, dst
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        dsa_step(ops, st)
-    torch.cuda.synchronize()
-    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(4)) for _ in range(args.steps)]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record()
-    for i in range(args.steps):
-        dsa_step(ops, st, evs[i])
-    t_end.record()
-    torch.cuda.synchronize()
-    ms_eager = t_start.elapsed_time(t_end) / args.steps
-    # the timed steps: replays of one captured step (the whole DSA step is
-    # graph-capturable: fixed workspaces, no host synchronization)
-    ms_step = graph_ms(torch, lambda: dsa_step(ops, st), args.steps)
-    filt_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    dec_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+    ms_step, ms_eager, filt_ms, dec_ms = time_dsa(torch, ops, st, args.steps, args.warmup)
     by = dsa_bytes(args.batch, args.ctx)
     gbs = by["total"] / (ms_step * 1e-3) / 1e9
     n = max(args.ctx - 128, 0)
@@ -871,6 +982,11 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
             "workload": workload,
             "batch": args.batch, "ctx": args.ctx, "index_topk": 2048, "window": 128, "heads": 64,
             "latent_dim": 576, "indexer": "64x128 fp8", "kv_cache": "fp8 e4m3 + fp32 per-token scale",
+            "keys": "N(0,1) rows through the K insert; per sequence 5% of the scored positions hold a spike row "
+                    "whose exact score is mean + 4 sigma of the row's ordinary scores (every row's top-2048 ends in "
+                    "a lowest-index tie among its spikes)",
+            "spike_sigma": [min(st["spikes"]["sigma"]), max(st["spikes"]["sigma"])],
+            "spikes_per_row": round(sum(st["spikes"]["per_row"]) / len(st["spikes"]["per_row"]), 1),
             "bytes_per_step": by,
         },
         "roofline": {
@@ -923,6 +1039,9 @@ def main():
             measure_dsa(torch, ops, args, line)
             print(json.dumps(line), flush=True)
             return
+        if args.only == "dsa_random_row":
+            print(json.dumps(measure_dsa_random_row(torch, ops, args)), flush=True)
+            return
         if args.only == "hca_layer":  # the HCA decode step at the headline batch and context
             print(json.dumps(measure_hca_decode(torch, ops, args.seed, ctxs=[args.ctx] * args.batch,
                                                 label=f"hca_decode_b{args.batch}_ctx{args.ctx}")), flush=True)
@@ -939,21 +1058,23 @@ def main():
     hca_head = measure_hca_decode(torch, ops, args.seed, ctxs=[args.ctx] * args.batch,
                                   label=f"hca_decode_b{args.batch}_ctx{args.ctx}")
     torch.cuda.empty_cache()
-    # each layer type in its faster launch mode (graph replay or eager)
-    dsa_ms = min(line["ms_per_step"], line["ms_per_step_eager"])
-    hca_ms = hca_head["ms"]  # (already the faster mode)
+    # both layer types as graph replays (the serving mode)
+    dsa_ms = line["ms_per_step"]
+    hca_ms = hca_head["ms_graph"]
     model_ms = MODEL_LAYERS["dsa"] * dsa_ms + MODEL_LAYERS["hca"] * hca_ms
     line.update({
         "tok_per_s": round(args.batch / (model_ms * 1e-3), 1),
         "model_step": {"ms": round(model_ms, 4),
                        "composed": "6 x the DSA step + 37 x the HCA decode step (hca_layer) at the same batch and "
-                                   "context, each in its faster launch mode (graph replay or eager): the model's "
+                                   "context, both as HIP graph replays: the model's "
                                    "attention KV path per decode step",
                        "dsa_ms": round(dsa_ms, 4), "hca_ms": round(hca_ms, 4),
                        "hca_layer": hca_head},
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
     })
+    line["dsa_random_spike_row"] = measure_dsa_random_row(torch, ops, args)
+    torch.cuda.empty_cache()
     if not args.no_hca:
         line["hca_write"] = measure_hca_write(torch, ops, args.seed)
         torch.cuda.empty_cache()

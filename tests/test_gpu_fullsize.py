@@ -2,9 +2,12 @@
 
 The DSA decode step exactly as ``bench.py`` times it (``build_dsa_decode`` +
 ``dsa_step``: prologue with indexer prep -> one-launch filter, exact scoring
-and select with the merged output as cache slots -> decode) at 32 x 131,072 tokens with
-5% identical spike keys, and the multi-token step at 8 x 262,144 + 1 x
-1,048,576 tokens with 3 query rows per sequence, are checked against:
+and select with the merged output as cache slots -> decode) at 32 x 131,072
+tokens with 5% spike keys at +4 sigma of each row's scores (every row's
+top-2048 ends in a lowest-index tie among its spikes), the same step with one
+random spike row in 5% of the positions, and the multi-token step at 8 x
+262,144 + 1 x 1,048,576 tokens with 3 query rows per sequence, are checked
+against:
 
 * the GPU's exact path (``ekv_indexer_score`` + ``ekv_topk_select`` over the
   full score rows) for every query row, bit-exact;
@@ -64,7 +67,7 @@ def _gather_latent(latent, slots, dim=576):
     return decode_e4m3(codes).astype(np.float64) * scale.astype(np.float64)[:, None]
 
 
-def _run_and_check(st, rows_to_check_extra, label):
+def _run_and_check(st, rows_to_check_extra, label, oracle_tie_rows=True):
     import bench
     from ernie_kv import ops
 
@@ -127,7 +130,7 @@ def _run_and_check(st, rows_to_check_extra, label):
         thr = sc_gpu[t, sel].min()
         if (sc_gpu[t, :n] == thr).sum() > (sc_gpu[t, sel] == thr).sum():
             tie_rows.append(t)
-    rows = sorted(set(tie_rows) | set(rows_to_check_extra))
+    rows = sorted((set(tie_rows) if oracle_tie_rows else set()) | set(rows_to_check_extra))
     _say(f"[{label}] tie rows {tie_rows}; oracle rows {rows}")
     q_dec = bf16_values(st["q"])
     sinks = st["sinks"].cpu().numpy()
@@ -150,13 +153,36 @@ def _run_and_check(st, rows_to_check_extra, label):
 
 
 def test_headline_step_fullsize(dev):
-    """The timed headline step: 32 x 131,072, 5% identical +spike keys."""
+    """The timed headline step: 32 x 131,072, N(0,1) keys, 5% spike keys per
+    sequence at +4 sigma of its row's ordinary scores.  Every row's threshold
+    is a tie among its spikes, broken by the lowest index: fused == the exact
+    path on all 32 rows, the oracle on five of them."""
     import bench
     from ernie_kv import ops
 
     st = bench.build_dsa_decode(torch, ops, [131072] * 32, 0)
-    ties = _run_and_check(st, [0, 5, 11, 20, 31], "b32_ctx131072")
-    assert len(ties) >= 1  # the workload does put spike ties on the threshold of some rows
+    sig = st["spikes"]["sigma"]
+    assert min(sig) >= bench.SPIKE_SIGMA and max(sig) < bench.SPIKE_SIGMA + 0.05, sig
+    ties = _run_and_check(st, [0, 5, 11, 20, 31], "b32_ctx131072", oracle_tie_rows=False)
+    assert ties == list(range(32)), f"rows without a tie at the threshold: {sorted(set(range(32)) - set(ties))}"
+    # the spikes are the threshold group: each row selects every ordinary
+    # token above the spike score and then its lowest-index spikes
+    topk = st["topk"].cpu().numpy()
+    for t, cnt in enumerate(st["spikes"]["per_row"]):
+        assert 2048 < cnt and (topk[t] >= 0).all()
+
+
+def test_headline_random_spike_row_fullsize(dev):
+    """The headline shape with uniformly random key codes and one random
+    spike row copied into 5% of the positions (the random-row leg): every
+    row against the exact path, the tie rows and three others against the
+    oracle."""
+    import bench
+    from ernie_kv import ops
+
+    st = bench.build_dsa_decode(torch, ops, [131072] * 32, 0, spikes="random_row")
+    ties = _run_and_check(st, [0, 17, 31], "b32_ctx131072_random_row")
+    assert len(ties) >= 1  # the random spike row ties the threshold of some rows
 
 
 def test_mtp_step_fullsize(dev):
