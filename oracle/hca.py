@@ -121,32 +121,33 @@ SLACK = np.float32(8.0)  # a chunk max above shift + SLACK moves the shift
 
 def span_softmax_sum(g: np.ndarray, kv: np.ndarray) -> np.ndarray:
     """sum_i softmax_i(g) * kv_i per channel, in the one-pass order above
-    (``g, kv [128, D]`` fp32; returns ``x [D]``)."""
+    (``g, kv [..., 128, D]`` fp32, any leading span dimensions; returns
+    ``x [..., D]``)."""
     f32 = np.float32
-    D = g.shape[1]
+    shape = g.shape[:-2] + g.shape[-1:]
     ms, Zs, Ns = [], [], []
     with np.errstate(invalid="ignore", over="ignore"):
         for r in range(ROW_GROUPS):
-            m = np.full(D, -np.inf, f32)
-            Z = np.zeros(D, f32)
-            N = np.zeros(D, f32)
+            m = np.full(shape, -np.inf, f32)
+            Z = np.zeros(shape, f32)
+            N = np.zeros(shape, f32)
             rows = np.arange(r, SPAN, ROW_GROUPS)
             for k0 in range(0, len(rows), CHUNK):
                 chunk = rows[k0 : k0 + CHUNK]
-                mc = np.maximum(m, g[chunk].max(axis=0))
+                mc = np.maximum(m, g[..., chunk, :].max(axis=-2))
                 move = mc > (m + SLACK).astype(f32)
                 s = exp_ekv((m - mc).astype(f32))
                 Z = np.where(move, (Z * s).astype(f32), Z)
                 N = np.where(move, (N * s).astype(f32), N)
                 m = np.where(move, mc, m)
                 for i in chunk:
-                    e = exp_ekv((g[i] - m).astype(f32))
+                    e = exp_ekv((g[..., i, :] - m).astype(f32))
                     Z = (Z + e).astype(f32)
-                    N = fma32(e, kv[i], N)
+                    N = fma32(e, kv[..., i, :], N)
             ms.append(m), Zs.append(Z), Ns.append(N)
         M = np.max(np.stack(ms), axis=0)
-        Z = np.zeros(D, f32)
-        N = np.zeros(D, f32)
+        Z = np.zeros(shape, f32)
+        N = np.zeros(shape, f32)
         for r in range(ROW_GROUPS):
             s = exp_ekv((ms[r] - M).astype(f32))
             Z = fma32(Zs[r], s, Z)
@@ -162,27 +163,30 @@ def compress_span(
     eps: float,
     cos_sin: np.ndarray,
 ) -> np.ndarray:
-    """One compressed row (fp32 before quant) from ``kv, score [128, D]`` (bf16 values)."""
-    kv = np.asarray(kv, np.float32)
-    D = kv.shape[1]
-    g = (np.asarray(score, np.float32) + np.asarray(ape, np.float32)).astype(np.float32)
+    """The compressed row (fp32 before quant) of each span: ``kv, score
+    [..., 128, D]`` (bf16 values) and ``cos_sin [..., 64]`` with the same
+    leading span dimensions (none for one span); returns ``[..., D]``."""
+    f32 = np.float32
+    kv = np.asarray(kv, f32)
+    D = kv.shape[-1]
+    g = (np.asarray(score, f32) + np.asarray(ape, f32)).astype(f32)
     x = span_softmax_sum(g, kv)
-    sq = (x * x).astype(np.float32).reshape(D // 4, 4)
-    part = np.zeros(D // 4, np.float32)
+    sq = (x * x).astype(f32).reshape(x.shape[:-1] + (D // 4, 4))
+    part = np.zeros(sq.shape[:-1], f32)
     for k in range(4):
-        part = (part + sq[:, k]).astype(np.float32)
-    S = np.float32(0.0)
-    for v in part:
-        S = np.float32(S + v)
-    ms = np.float32(S / np.float32(D))
-    r = np.float32(np.float32(1.0) / np.sqrt(np.float32(ms + np.float32(eps))))
-    y = ((x * r).astype(np.float32) * np.asarray(norm_w, np.float32)).astype(np.float32)
-    cs = np.asarray(cos_sin, np.float32)
-    x0 = y[D - 64 :: 2].copy()
-    x1 = y[D - 63 :: 2].copy()
-    c, s = cs[:32], cs[32:64]
-    y[D - 64 :: 2] = ((x0 * c).astype(np.float32) - (x1 * s).astype(np.float32)).astype(np.float32)
-    y[D - 63 :: 2] = ((x0 * s).astype(np.float32) + (x1 * c).astype(np.float32)).astype(np.float32)
+        part = (part + sq[..., k]).astype(f32)
+    S = np.zeros(x.shape[:-1], f32)
+    for q in range(D // 4):
+        S = (S + part[..., q]).astype(f32)
+    ms = (S / f32(D)).astype(f32)
+    r = (f32(1.0) / np.sqrt((ms + f32(eps)).astype(f32))).astype(f32)
+    y = ((x * r[..., None]).astype(f32) * np.asarray(norm_w, f32)).astype(f32)
+    cs = np.asarray(cos_sin, f32)
+    x0 = y[..., D - 64 :: 2].copy()
+    x1 = y[..., D - 63 :: 2].copy()
+    c, s = cs[..., :32], cs[..., 32:64]
+    y[..., D - 64 :: 2] = ((x0 * c).astype(f32) - (x1 * s).astype(f32)).astype(f32)
+    y[..., D - 63 :: 2] = ((x0 * s).astype(f32) + (x1 * c).astype(f32)).astype(f32)
     return y
 
 
@@ -228,6 +232,7 @@ def hca_write(
     positions = np.asarray(positions, np.int64)
     B = len(qsl) - 1
     if comp_block_table is not None:
+        spans, js, slots = [], [], []
         for b in range(B):
             t0, t1 = int(qsl[b]), int(qsl[b + 1])
             if t1 <= t0:
@@ -241,9 +246,14 @@ def hca_write(
                         rows[i] = kv_score[t0 + p - p0]
                     else:
                         rows[i] = st.state[int(state_slot[b]), p % STATE_RING]
-                y = compress_span(rows[:, :D], rows[:, D:], ape, norm_w, eps, comp_cos_sin[j])
-                codes, scale = quantize_rows(y[None, :])
-                write_fp8_rows(st.pool, [comp_slot(comp_block_table, b, j)], codes, scale, D)
+                spans.append(rows)
+                js.append(j)
+                slots.append(comp_slot(comp_block_table, b, j))
+        if spans:
+            rows = np.stack(spans)
+            y = compress_span(rows[..., :D], rows[..., D:], ape, norm_w, eps, np.asarray(comp_cos_sin)[js])
+            codes, scale = quantize_rows(y)
+            write_fp8_rows(st.pool, slots, codes, scale, D)
     codes, scale = quantize_rows(latent)
     write_fp8_rows(st.pool, slot_mapping, codes, scale, D)
     for b in range(B):

@@ -114,6 +114,23 @@ def test_padded_sinks_are_noop_minus_inf():
     assert impl._padded_sinks(16) is impl.sinks
 
 
+def test_fp8_kernel_refuses_fp8_ds_mla_pages():
+    """Upstream fp8_ds_mla pages share this library's 46,080-byte page
+    stride, so the fp8 sparse kernel takes the format from kv_cache_dtype and
+    refuses such a cache (before any device work) instead of reading its
+    656-byte rows as 580-byte ones."""
+    import torch
+
+    from ernie_kv.attention import Ernie5_5FlashMLASparseImpl
+
+    impl = Ernie5_5FlashMLASparseImpl(num_heads=64, head_size=576, scale=0.0625, kv_cache_dtype="fp8_ds_mla",
+                                      sinks=torch.zeros(64))
+    q = torch.zeros((1, 1, 64, 576), dtype=torch.bfloat16)
+    cache = torch.zeros((4, 46080), dtype=torch.uint8)
+    with pytest.raises(ValueError, match="fp8_ds_mla"):
+        impl._fp8_flash_mla_kernel(q, cache, torch.zeros((1, 1, 2176), dtype=torch.int32))
+
+
 def test_attn_tp_and_sink_backend_errors():
     from ernie_kv.attention import _check_attn_tp, _check_sink_backend
 

@@ -143,7 +143,17 @@ class Ernie5_5FlashMLASparseImpl(FlashMLASparseImplBase):
         the indices are global cache slots; a ``kernel_metadata`` carrying
         ``block_table`` and ``req_ids`` instead marks them request-local, and
         the kernel converts them through the block table.  Heads are padded
-        with zero q rows and -inf sinks to ``fp8_decode_padded_heads``."""
+        with zero q rows and -inf sinks to ``fp8_decode_padded_heads``.
+
+        The cache must hold this library's rows (d fp8 codes per row, then
+        the page's fp32 scales).  Upstream's ``fp8_ds_mla`` pages (656-byte
+        rows) have the same 46,080-byte page stride, so the format is taken
+        from ``kv_cache_dtype`` and an ``fp8_ds_mla`` cache is refused rather
+        than misread: ``ops.import_fp8_ds_mla_pages`` converts its pages."""
+        if self.kv_cache_dtype == "fp8_ds_mla":
+            raise ValueError("_fp8_flash_mla_kernel reads 580-byte fp8 rows with per-token fp32 scales; this cache "
+                             "holds fp8_ds_mla pages (656-byte rows): convert them with "
+                             "ops.import_fp8_ds_mla_pages")
         b, s, h, d = q.shape
         padded = max(self.fp8_decode_padded_heads, h)
         padded = (padded + 15) // 16 * 16
