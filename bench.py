@@ -66,8 +66,8 @@ def parse():
     p.add_argument("--no-fp4", action="store_true", help="skip the MXFP4 indexer measurement")
     p.add_argument("--no-prefill", action="store_true", help="skip the DSA prefill-chunk measurement")
     p.add_argument("--no-pages", action="store_true", help="skip the page-format transcoder measurement")
-    p.add_argument("--only", choices=["hca_write", "hca_decode", "hca_layer", "mtp", "dsa", "dsa_random_row",
-                                      "indexer_fp4", "dsa_prefill", "pages"],
+    p.add_argument("--only", choices=["hca_small", "hca_write", "hca_decode", "hca_layer", "mtp", "dsa",
+                                      "dsa_random_row", "indexer_fp4", "dsa_prefill", "pages"],
                    default=None,
                    help="run only this measurement and print its JSON object (for profiling one workload)")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -489,6 +489,93 @@ def measure_hca_write(torch, ops, seed: int, reps: int = 10) -> dict:
     }
 
 
+# --------------------------------------------------------------------------- HCA layer in bf16 (config 1)
+def build_hca_small(torch, ops, seed: int, B: int = 4, ctx: int = 4096, D: int = 576, heads: int = 16,
+                    hidden: int = 4096):
+    """The small HCA layer workload: B sequences of ctx tokens written into a
+    bf16 paged cache (block size 64, permuted block table) in one prefill
+    call -- every row appended, every 128-token span compressed (compressor
+    input = hidden N(0,1) x fused_wkv_wgate N(0, 0.02), ape N(0, 0.02),
+    RMSNorm weight 1, RoPE at compress_rope_theta 1.6e5), the 128-row window
+    ring written -- then one decode query per sequence (its last token, 16
+    heads, q N(0,1)) over its ctx/128 compressed entries and 128 window rows.
+    Latents N(0,1).  Synthetic inputs, seeded."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed + 6)
+    gc = torch.Generator().manual_seed(seed + 6)
+    lat_pp, spans, ring = ctx // 64, ctx // 128, 128
+    comp_pp, ring_pp = (spans + 1 + 63) // 64, ring // 64
+    pages = B * (lat_pp + comp_pp + ring_pp)
+    perm = torch.randperm(pages, generator=gc).to(torch.int32)
+    bt = perm[: B * lat_pp].view(B, lat_pp)
+    comp_bt = perm[B * lat_pp: B * (lat_pp + comp_pp)].view(B, comp_pp).to(dev)
+    ring_pages = perm[B * (lat_pp + comp_pp):].view(B, ring_pp).to(dev)
+    T = B * ctx
+    positions = torch.arange(ctx, dtype=torch.int64).repeat(B)
+    token_seq = torch.arange(B, dtype=torch.int32).repeat_interleave(ctx)
+    slots = bt[token_seq.long(), positions // 64].to(torch.int64) * 64 + positions % 64
+    h = torch.randn(T, hidden, device=dev, generator=g)
+    w = torch.randn(hidden, 2 * D, device=dev, generator=g) * 0.02
+    kv_score = (h @ w).to(torch.bfloat16)
+    del h, w
+    ang = (torch.arange(spans + 1, dtype=torch.float64)[:, None] * 128.0) * (
+        1.6e5 ** (-torch.arange(32, dtype=torch.float64) * 2.0 / 64))[None, :]
+    width = spans + ring
+    st = dict(
+        B=B, T=T, ctx=ctx, D=D, heads=heads, ring=ring, width=width, scale=D ** -0.5,
+        latent=torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16), kv_score=kv_score,
+        slots=slots.to(dev), positions=positions.to(dev), token_seq=token_seq.to(dev),
+        qsl=(torch.arange(B + 1, dtype=torch.int32) * ctx).to(dev),
+        state=torch.zeros((B, 256, 2 * D), dtype=torch.bfloat16, device=dev),
+        state_slot=torch.arange(B, dtype=torch.int32, device=dev),
+        ape=(0.02 * torch.randn(128, D, device=dev, generator=g)).contiguous(),
+        norm_w=torch.ones(D, device=dev), comp_bt=comp_bt, ring_pages=ring_pages,
+        cos_sin=torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(dev),
+        pool=torch.zeros((pages * 64, D), dtype=torch.bfloat16, device=dev),
+        q=torch.randn(B, heads, D, device=dev, generator=g).to(torch.bfloat16),
+        sinks=torch.randn(heads, device=dev, generator=g),
+        q_pos=torch.full((B,), ctx - 1, dtype=torch.int64, device=dev),
+        req=torch.arange(B, dtype=torch.int32, device=dev),
+        idx=torch.empty((B, width), dtype=torch.int32, device=dev),
+        lens=torch.empty(B, dtype=torch.int32, device=dev),
+        out=torch.empty((B, heads, 512), dtype=torch.bfloat16, device=dev),
+        lse=torch.empty((B, heads), dtype=torch.float32, device=dev),
+        ws=ops.hca_write_workspace(B, D, dev, max_query_len=ctx),
+    )
+    st["dec_ws"] = ops.decode_workspace(B, heads, width, dev)
+    return st
+
+
+def hca_small_step(ops, st):
+    """The bf16 HCA write of every token (rows, compressed spans, window
+    ring), the decode rows' indices and the 16-head decode."""
+    ops.hca_write(st["latent"], st["kv_score"], st["slots"], st["positions"], st["token_seq"], st["qsl"], st["ctx"],
+                  st["state"], st["state_slot"], st["ape"], st["norm_w"], 1e-6, st["cos_sin"], st["comp_bt"],
+                  st["ring_pages"], st["ring"], st["pool"], workspace=st["ws"])
+    ops.hca_decode_indices(st["q_pos"], st["req"], st["comp_bt"], st["ring_pages"], st["ring"], st["idx"], st["lens"])
+    ops.sparse_mla_decode(st["q"], st["pool"], st["idx"], st["scale"], st["out"], st["lse"], sinks=st["sinks"],
+                          lengths=st["lens"], cache_bf16=True, workspace=st["dec_ws"])
+
+
+def measure_hca_small(torch, ops, seed: int, reps: int = 20) -> dict:
+    st = build_hca_small(torch, ops, seed)
+    ms = time_ms(torch, lambda: hca_small_step(ops, st), reps)
+    T, D, B = st["T"], st["D"], st["B"]
+    spans = B * (st["ctx"] // 128)
+    # rows in (bf16) and out (bf16), kv || score in, compressed and ring rows
+    # out, the state ring's last 256 rows, then the decode's rows and q / out
+    write = T * D * 2 * 2 + T * 2 * D * 2 + spans * D * 2 + B * st["ring"] * D * 2 + B * 256 * 2 * D * 2
+    dec = B * st["width"] * D * 2 + B * st["heads"] * (D * 2 + 512 * 2 + 4)
+    return {
+        "workload": f"hca_layer_bf16_b{B}_ctx{st['ctx']}_h{st['heads']}",
+        "ms": round(ms, 4), "bytes": write + dec,
+        "GB/s": round((write + dec) / (ms * 1e-3) / 1e9, 1),
+        "frac": round((write + dec) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "what": "ekv_hca_write_bf16 of 4 x 4096 tokens (rows, 128 compressed spans, window ring) + index rows + "
+                "16-head sparse decode over 32 + 128 bf16 rows per sequence, events around the three calls",
+    }
+
+
 # --------------------------------------------------------------------------- HCA decode (config 2)
 def build_hca_decode(torch, ops, seed: int, B: int = 64, ctx_lo: int = 8192, ctx_hi: int = 131072, D: int = 576,
                      ring: int = 128, ctxs: list | None = None, rows_per_seq: int = 1, extra_tokens: int = 0):
@@ -851,6 +938,42 @@ def _cpu_hca_decode_row(args):
     return time.perf_counter() - t0
 
 
+def _cpu_hca_small_seq(args):
+    """Oracle of one sequence of the small bf16 HCA layer workload: its 4096
+    rows into a bf16 pool, its 32 spans compressed, the window ring, then
+    its 16-head decode over 32 + 128 rows."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import decode as od
+    from oracle import hca as oh
+    from oracle import indexer as oi
+    from oracle.fp8 import bf16_from_bits, bf16_round
+
+    ctx, D, heads, seed = args
+    rng = np.random.default_rng(seed)
+    lat = bf16_round(rng.standard_normal((ctx, D)).astype(np.float32))
+    kvs = bf16_round((rng.standard_normal((ctx, 2 * D)) * 1.28).astype(np.float32))
+    ape = (rng.standard_normal((128, D)) * 0.02).astype(np.float32)
+    q = bf16_round(rng.standard_normal((1, heads, D)).astype(np.float32))
+    sinks = rng.standard_normal(heads).astype(np.float32)
+    pages = ctx // 64 + 3
+    bt = rng.permutation(pages).astype(np.int32)
+    comp_bt, ring_pages = bt[None, -3:-2], bt[None, -2:]
+    pos = np.arange(ctx, dtype=np.int64)
+    slots = bt[pos // 64].astype(np.int64) * 64 + pos % 64
+    cs = oi.rope_cos_sin(np.arange(ctx // 128 + 1) * 128, 64, 1.6e5)
+    t0 = time.perf_counter()
+    st = oh.HcaState(pages, D, 1, bf16=True)
+    oh.hca_write(st, lat, kvs, pos, np.zeros(ctx, np.int32), np.array([0, ctx], np.int32), slots, ring_pages, 128,
+                 comp_bt, np.zeros(1, np.int32), ape, np.ones(D, np.float32), 1e-6, cs)
+    idx, lens = oh.hca_decode_indices(np.array([ctx - 1]), np.zeros(1, np.int32), comp_bt, ring_pages, 128,
+                                      ctx // 128 + 128)
+    vals = bf16_from_bits(st.pool.view(np.uint16).reshape(-1, D))
+    od.sparse_mla_decode(q, lambda s: od.gather_rows_bf16(vals, s), idx, D ** -0.5, 512, sinks, lengths=lens)
+    return time.perf_counter() - t0
+
+
 def _pool_run(fn, jobs):
     import multiprocessing as mp
 
@@ -889,6 +1012,14 @@ def cpu_baselines(B: int, ctx: int, seed: int) -> dict:
         "sample": f"the whole chunked-prefill write on the CPU: 16 sequences x 8192 rows quantized and {spans} spans "
                   f"compressed, numpy oracle, one sequence per job on {workers} processes: {wall:.2f} s wall, "
                   f"{busy:.1f} core-s",
+        "ms": round(wall * 1e3, 1),
+    }
+    wall, busy, workers = _pool_run(_cpu_hca_small_seq, [(4096, 576, 16, seed * 1000 + 7 + i) for i in range(4)])
+    out["hca_small"] = {
+        "value": round(4 / wall, 3), "unit": "sequences/s", "cores": workers, "kind": "port",
+        "sample": f"the whole small bf16 HCA layer step on the CPU: 4 sequences x 4096 rows into a bf16 pool, 128 "
+                  f"spans compressed, window ring, 16-head decode over 32 + 128 rows, numpy oracle, one sequence per "
+                  f"job on {workers} processes: {wall:.2f} s wall, {busy:.1f} core-s",
         "ms": round(wall * 1e3, 1),
     }
     ctxs = rng.integers(8192, 131072, 64)
@@ -1047,6 +1178,7 @@ def main():
                                                 label=f"hca_decode_b{args.batch}_ctx{args.ctx}")), flush=True)
             return
         leg = {"hca_write": measure_hca_write, "hca_decode": measure_hca_decode, "mtp": measure_mtp,
+               "hca_small": measure_hca_small,
                "indexer_fp4": measure_indexer_fp4, "dsa_prefill": measure_dsa_prefill,
                "pages": measure_pages}[args.only]
         print(json.dumps(leg(torch, ops, args.seed)), flush=True)
@@ -1076,6 +1208,8 @@ def main():
     line["dsa_random_spike_row"] = measure_dsa_random_row(torch, ops, args)
     torch.cuda.empty_cache()
     if not args.no_hca:
+        line["hca_small"] = measure_hca_small(torch, ops, args.seed)
+        torch.cuda.empty_cache()
         line["hca_write"] = measure_hca_write(torch, ops, args.seed)
         torch.cuda.empty_cache()
         line["hca_decode"] = measure_hca_decode(torch, ops, args.seed)
@@ -1097,6 +1231,8 @@ def main():
             line["hca_write"]["cpu_baseline"] = cpu["hca_write"]
         if "hca_decode" in line:
             line["hca_decode"]["cpu_baseline"] = cpu["hca_decode"]
+        if "hca_small" in line:
+            line["hca_small"]["cpu_baseline"] = cpu["hca_small"]
     print(json.dumps(line), flush=True)
 
 

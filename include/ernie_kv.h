@@ -146,6 +146,36 @@ int ekv_hca_write_step(const uint16_t* latent, int64_t latent_stride, const uint
                        int32_t* idx_out, int64_t idx_stride, int32_t width, int32_t* lengths, void* stream);
 
 /*
+ * ekv_hca_write / ekv_hca_write_step for a pool of bf16 rows (the plain KV
+ * row of the non-fp8 HCA class, Ernie5_5HCAFlashInferAttention, which
+ * select_ernie5_5_hca_cls picks for a non-fp8 kv_cache_dtype,
+ * nvidia/attention.py:542-558): a page is 64 rows of dim bf16 values
+ * (page_stride >= 128 * dim bytes; exactly that for the flat-row view the
+ * sparse decode reads, nvidia/attention.py:761-763).  Latent and window-ring
+ * rows are stored as given; a compressed row is the fp32 result rounded to
+ * bf16 (nearest even) instead of quantized.  Everything else as the fp8
+ * entry points.
+ */
+int ekv_hca_write_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                       int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                       const int64_t* positions, const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs,
+                       int32_t max_query_len, uint16_t* state, const int32_t* state_slot, int32_t num_state,
+                       const float* ape, const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                       const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
+                       int32_t ring_stride, int32_t ring, uint16_t* pool, int64_t page_stride /*bytes*/,
+                       int64_t num_pages, void* workspace, int64_t workspace_bytes, void* stream);
+int ekv_hca_write_step_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                            int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                            const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                            int32_t num_seqs, int32_t max_query_len, uint16_t* state, const int32_t* state_slot,
+                            int32_t num_state, const float* ape, const float* norm_w, float eps,
+                            const float* cos_sin, int32_t max_spans, const int32_t* comp_block_table,
+                            int32_t comp_bt_stride, const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
+                            uint16_t* pool, int64_t page_stride /*bytes*/, int64_t num_pages, void* workspace,
+                            int64_t workspace_bytes, int32_t window, int32_t* idx_out, int64_t idx_stride,
+                            int32_t width, int32_t* lengths, void* stream);
+
+/*
  * HCA decode index rows: [compressed slots 0..n_c-1 | window slots of
  * positions p-w+1..p | -1 ...] with n_c = (p+1)/128, w = min(p+1, window),
  * and the row lengths.  Window slots are ring slots; with query_start_loc

@@ -58,7 +58,7 @@ import math
 
 import numpy as np
 
-from .fp8 import bf16_round, quantize_rows
+from .fp8 import bf16_bits, bf16_round, quantize_rows
 from .paged import PAGE_TOKENS, write_fp8_rows
 
 SPAN = 128
@@ -202,11 +202,31 @@ def comp_slot(comp_block_table: np.ndarray, seq: int, j: int) -> int:
 class HcaState:
     """Numpy model of every buffer the HCA write path touches."""
 
-    def __init__(self, num_pages: int, dim: int, num_state: int, stride: int | None = None):
+    def __init__(self, num_pages: int, dim: int, num_state: int, stride: int | None = None, bf16: bool = False):
+        """``bf16``: a pool of bf16 rows (64 rows of ``dim`` bf16 values a
+        page, no scales; the non-fp8 HCA cache) instead of fp8 rows with
+        per-token scales."""
         self.dim = dim
-        stride = PAGE_TOKENS * (dim + 4) if stride is None else stride
+        self.bf16 = bf16
+        if stride is None:
+            stride = PAGE_TOKENS * (2 * dim if bf16 else dim + 4)
         self.pool = np.zeros((num_pages, stride), dtype=np.uint8)
         self.state = np.zeros((num_state, STATE_RING, 2 * dim), dtype=np.float32)
+
+    def store(self, slots, rows: np.ndarray) -> None:
+        """Rows ``[n, dim]`` (fp32 values) into their slots: UE8M0 fp8 with
+        per-token scales, or rounded to bf16 (nearest even) in a bf16 pool;
+        negative slots are skipped."""
+        rows = np.asarray(rows, np.float32)
+        if not self.bf16:
+            codes, scale = quantize_rows(rows)
+            write_fp8_rows(self.pool, slots, codes, scale, self.dim)
+            return
+        bits = bf16_bits(rows).view(np.uint8).reshape(len(rows), 2 * self.dim)
+        for i, slot in enumerate(np.asarray(slots, np.int64)):
+            if slot >= 0:
+                off = (slot % PAGE_TOKENS) * 2 * self.dim
+                self.pool[slot // PAGE_TOKENS, off:off + 2 * self.dim] = bits[i]
 
 
 def hca_write(
@@ -252,10 +272,9 @@ def hca_write(
         if spans:
             rows = np.stack(spans)
             y = compress_span(rows[..., :D], rows[..., D:], ape, norm_w, eps, np.asarray(comp_cos_sin)[js])
-            codes, scale = quantize_rows(y)
-            write_fp8_rows(st.pool, slots, codes, scale, D)
-    codes, scale = quantize_rows(latent)
-    write_fp8_rows(st.pool, slot_mapping, codes, scale, D)
+            st.store(slots, y)
+    latent = np.asarray(latent, np.float32)
+    st.store(slot_mapping, latent)
     for b in range(B):
         t0, t1 = int(qsl[b]), int(qsl[b + 1])
         if t1 <= t0:
@@ -265,7 +284,7 @@ def hca_write(
         for t in range(t0, t1):
             p = p0 + (t - t0)
             if ring_pages is not None and p > pl - ring:
-                write_fp8_rows(st.pool, [ring_slot(ring_pages, b, p, ring)], codes[t : t + 1], scale[t : t + 1], D)
+                st.store([ring_slot(ring_pages, b, p, ring)], latent[t : t + 1])
             if comp_block_table is not None and p > pl - STATE_RING:
                 st.state[int(state_slot[b]), p % STATE_RING] = kv_score[t]
 

@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 
 class HcaCase:
-    def __init__(self, rng, dim, num_seqs, max_pos, ring, rope="plain"):
+    def __init__(self, rng, dim, num_seqs, max_pos, ring, rope="plain", bf16=False):
         self.dim, self.B, self.ring = dim, num_seqs, ring
         lp = (max_pos + 63) // 64
         spans = max_pos // 128 + 1
@@ -32,7 +32,7 @@ class HcaCase:
         table = oi.yarn_cos_sin if rope == "yarn" else oi.rope_cos_sin
         self.cos_sin = table(np.arange(spans) * 128, 64, 1.6e5)
         self.state_slot = rng.permutation(num_seqs + 2)[:num_seqs].astype(np.int32)
-        self.st = oh.HcaState(self.pages, dim, num_seqs + 2)
+        self.st = oh.HcaState(self.pages, dim, num_seqs + 2, bf16=bf16)
 
 
 def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
@@ -106,6 +106,37 @@ def test_hca_write_path_exact(dev, dim, fused, rope):
         got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
         assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
         if "ws" in gpu:  # the arrival counters are left zero
+            assert _counters_zero(gpu["ws"])
+
+
+@pytest.mark.parametrize("fused", [True, "ws", "ws-spans"], ids=["hca_write", "hca_write+ws", "hca_write+ws-spans"])
+@pytest.mark.parametrize("dim", [576, 512])
+def test_hca_write_path_exact_bf16(dev, dim, fused):
+    """The bf16 pool (ekv_hca_write_bf16: rows stored as given, compressed
+    rows rounded to bf16) over the same call sequence as the fp8 test:
+    chunked prefill, 3-token steps, a rollback re-append, long chunks."""
+    rng = np.random.default_rng(dim + 7)
+    case = HcaCase(rng, dim, num_seqs=3, max_pos=1400, ring=192, rope="yarn", bf16=True)
+    gpu = {
+        "pool": torch.zeros((case.pages * 64, dim), dtype=torch.bfloat16, device=dev),
+        "state": torch.zeros((case.B + 2, 256, 2 * dim), dtype=torch.bfloat16, device=dev),
+    }
+    calls = [
+        ([0, 0, 0], [300, 100, 128]),
+        ([300, 100, 128], [3, 200, 2]),
+        ([303, 300, 130], [3, 3, 3]),
+        ([304, 301, 131], [3, 3, 3]),
+        ([307, 304, 134], [900, 1, 700]),
+        ([1207, 305, 834], [0, 260, 130]),
+    ]
+    for starts, counts in calls:
+        _run_call(dev, case, rng, starts, counts, gpu, fused)
+        torch.cuda.synchronize()
+        got = gpu["pool"].view(torch.uint8).reshape(case.pages, -1).cpu().numpy()
+        assert np.array_equal(got, case.st.pool), f"pool mismatch after call {starts}"
+        got_state = bf16_values(gpu["state"]).reshape(case.st.state.shape)
+        assert np.array_equal(got_state, case.st.state), f"state mismatch after call {starts}"
+        if "ws" in gpu:
             assert _counters_zero(gpu["ws"])
 
 

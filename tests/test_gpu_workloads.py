@@ -160,3 +160,42 @@ def test_mtp_accept_reject_steps(dev):
         ref_o, _ = od.sparse_mla_decode(qh, lambda sl: od.gather_rows_fp8(ost.pool, sl, D), ref_idx, 256 ** -0.5, 512,
                                         cpu("sinks"), lengths=ref_len)
         _close(bf16_values(sh["out"]).astype(np.float64), ref_o, f"step {i}: HCA decode")
+
+
+def test_hca_layer_bf16_small(dev):
+    """The small bf16 HCA layer workload (bench.build_hca_small: 4 sequences
+    x 4096 tokens written in one prefill call into a bf16 paged cache with
+    N(0, 0.02) compressor weights, then a 16-head decode of each sequence's
+    last token over its 32 compressed entries and 128 window rows) against
+    the oracle: the bf16 pool and state ring bit-exact, the index rows exact,
+    the decode within |err| <= 2e-3 + 2e-2 |ref|."""
+    import bench
+    from ernie_kv import ops
+    from oracle import decode as od
+    from oracle.fp8 import bf16_from_bits
+
+    st = bench.build_hca_small(torch, ops, 0)
+    B, D, ctx = st["B"], st["D"], st["ctx"]
+    _say("[hca_small] GPU step")
+    bench.hca_small_step(ops, st)
+    torch.cuda.synchronize()
+    cpu = lambda k: st[k].cpu().numpy()  # noqa: E731
+    pages = st["pool"].shape[0] // 64
+    ost = oh.HcaState(pages, D, B, bf16=True)
+    oh.hca_write(ost, bf16_values(st["latent"]), bf16_values(st["kv_score"]), cpu("positions"), cpu("token_seq"),
+                 cpu("qsl"), cpu("slots"), cpu("ring_pages"), st["ring"], cpu("comp_bt"), cpu("state_slot"),
+                 cpu("ape"), cpu("norm_w"), 1e-6, cpu("cos_sin"))
+    got = st["pool"].view(torch.uint8).reshape(pages, -1).cpu().numpy()
+    bad = np.flatnonzero((got != ost.pool).any(axis=1))
+    assert bad.size == 0, f"{bad.size} pages differ"
+    assert np.array_equal(bf16_values(st["state"]), ost.state)
+    ref_idx, ref_len = oh.hca_decode_indices(cpu("q_pos"), cpu("req"), cpu("comp_bt"), cpu("ring_pages"), st["ring"],
+                                             st["width"])
+    assert np.array_equal(cpu("idx"), ref_idx) and np.array_equal(cpu("lens"), ref_len)
+    assert (ref_len == ctx // 128 + 128).all()
+    vals = bf16_from_bits(ost.pool.view(np.uint16).reshape(-1, D))
+    ref_o, ref_l = od.sparse_mla_decode(bf16_values(st["q"]), lambda s: od.gather_rows_bf16(vals, s), ref_idx,
+                                        st["scale"], 512, cpu("sinks"), lengths=ref_len)
+    _close(bf16_values(st["out"]).astype(np.float64), ref_o, "decode")
+    lse = cpu("lse").astype(np.float64)
+    assert np.all(np.abs(lse - ref_l) <= 2e-3 * np.maximum(1.0, np.abs(ref_l)))

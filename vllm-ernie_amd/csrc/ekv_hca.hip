@@ -73,7 +73,16 @@ struct CompressArgs {
   uint32_t* span_count;      // [B] arrivals per span (zero between calls)
   float* span_x;             // [B, D] softmax results
   float* span_part;          // [B, D/4] sums of squares per channel quad
+  // pools of bf16 rows (page = 64 rows of D bf16 values, no scales): the
+  // compressed row is stored rounded to bf16 (nearest even), not quantized
+  int32_t bf16_rows;
 };
+
+// 4 channels of a compressed row as bf16 (round to nearest even), 8 bytes.
+__device__ __forceinline__ uint2 bf16x4_pack(float y0, float y1, float y2, float y3) {
+  return make_uint2(f32_to_bf16(y0) | (static_cast<uint32_t>(f32_to_bf16(y1)) << 16),
+                    f32_to_bf16(y2) | (static_cast<uint32_t>(f32_to_bf16(y3)) << 16));
+}
 
 // Third descriptor word of a raw (unswizzled, unformatted) buffer resource.
 constexpr int kBufferWord3 = 0x00020000;
@@ -430,6 +439,10 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
   const int64_t off = slot % kPageTokens;
+  if (a.bf16_rows) {
+    if (owner) *reinterpret_cast<uint2*>(page + off * (2 * D) + 2 * c0) = bf16x4_pack(y[0], y[1], y[2], y[3]);
+    return;
+  }
   if (owner) {
     const uint32_t lo = f32x2_to_fp8(y[0] * inv, y[1] * inv);
     const uint32_t hi = f32x2_to_fp8(y[2] * inv, y[3] * inv);
@@ -588,6 +601,10 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
   if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
   const int64_t off = slot % kPageTokens;
+  if (a.bf16_rows) {
+    if ((tid & 3) == 0) *reinterpret_cast<uint2*>(page + off * (2 * D) + 2 * tid) = bf16x4_pack(y, y1, y2, y3);
+    return;
+  }
   if ((tid & 3) == 0) {
     const uint32_t lo = f32x2_to_fp8(y * inv, y1 * inv);
     const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
@@ -654,13 +671,18 @@ __device__ __forceinline__ void finish_span_wave(const CompressArgs& a, float* p
 #pragma unroll
   for (int i = 0; i < kSlabs; ++i) {
     const float y1 = __shfl_down(y[i], 1), y2 = __shfl_down(y[i], 2), y3 = __shfl_down(y[i], 3);
+    if (a.bf16_rows) {
+      if ((lane & 3) == 0)
+        *reinterpret_cast<uint2*>(page + off * (2 * D) + 2 * (64 * i + lane)) = bf16x4_pack(y[i], y1, y2, y3);
+      continue;
+    }
     if ((lane & 3) == 0) {
       const uint32_t lo = f32x2_to_fp8(y[i] * inv, y1 * inv);
       const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
       *reinterpret_cast<uint32_t*>(page + off * D + 64 * i + lane) = lo | (hi << 16);
     }
   }
-  if (lane == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
+  if (lane == 0 && !a.bf16_rows) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
 // Span j of sequence b compressed by D / 64 one-wave workgroups (prefill
@@ -786,19 +808,20 @@ int hca_compress_args(CompressArgs& a, const uint16_t* kv_score, int64_t kvs_str
                       const int32_t* qsl, int32_t dim, const uint16_t* state, const int32_t* state_slot,
                       int32_t num_state, const float* ape, const float* norm_w, float eps, const float* cos_sin,
                       int32_t max_spans, const int32_t* comp_block_table, int32_t comp_bt_stride, uint8_t* pool,
-                      int64_t page_stride, int64_t num_pages) {
+                      int64_t page_stride, int64_t num_pages, bool bf16_rows = false) {
   EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
   EKV_CHECK(kv_score && positions && qsl && ape && norm_w && cos_sin && comp_block_table && pool,
             "null pointer");
   EKV_CHECK(kvs_stride >= 2 * dim && kvs_stride % 4 == 0 && kvs_stride <= (int64_t{1} << 22),
             "kv_score stride must be in [2*dim, 2^22], a multiple of 4");
-  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(page_stride >= kPageTokens * (bf16_rows ? 2 * dim : dim + 4) && page_stride % 16 == 0,
+            "bad page_stride");
   EKV_CHECK(aligned16(ape) && aligned16(norm_w) && aligned8(kv_score) && aligned16(pool) &&
                 (state == nullptr || aligned8(state)),
             "misaligned buffers");
   a = CompressArgs{kv_score, kvs_stride, positions, qsl, state, state_slot, num_state, ape, norm_w, eps,
                    cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride, num_pages,
-                   nullptr, nullptr, nullptr};
+                   nullptr, nullptr, nullptr, bf16_rows ? 1 : 0};
   return 0;
 }
 
@@ -865,13 +888,14 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
                    const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
                    const int32_t* comp_block_table, int32_t comp_bt_stride, const int32_t* ring_pages,
                    int32_t ring_stride, int32_t ring, uint8_t* pool, int64_t page_stride, int64_t num_pages,
-                   void* workspace, int64_t workspace_bytes, const HcaIndexArgs* ix, void* stream) {
+                   void* workspace, int64_t workspace_bytes, const HcaIndexArgs* ix, void* stream,
+                   bool bf16_rows = false) {
   EKV_CHECK(num_tokens >= 0 && num_seqs >= 0 && max_query_len >= 0, "sizes must be >= 0");
   if (num_tokens == 0 || num_seqs == 0) return 0;
   CompressArgs c;
   int rc = hca_compress_args(c, kv_score, kvs_stride, positions, qsl, dim, state, state_slot, num_state, ape,
                              norm_w, eps, cos_sin, max_spans, comp_block_table, comp_bt_stride, pool, page_stride,
-                             num_pages);
+                             num_pages, bf16_rows);
   if (rc) return rc;
   int64_t ws_spans = 0;
   if (workspace != nullptr) {
@@ -886,7 +910,7 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
   AppendArgs ap;
   rc = hca_append_args(ap, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
                        token_seq, qsl, num_seqs, pool, page_stride, num_pages, ring_pages, ring_stride, ring, state,
-                       state_slot, num_state);
+                       state_slot, num_state, bf16_rows);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (max_query_len < kSpan) {  // decode-sized: compress, append (and index rows) in one launch
@@ -968,4 +992,44 @@ extern "C" int ekv_hca_write_step(const uint16_t* latent, int64_t latent_stride,
                         token_seq, qsl, num_seqs, max_query_len, state, state_slot, num_state, ape, norm_w, eps,
                         cos_sin, max_spans, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring, pool,
                         page_stride, num_pages, workspace, workspace_bytes, &ix, stream);
+}
+
+extern "C" int ekv_hca_write_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                                  int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                                  const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                                  int32_t num_seqs, int32_t max_query_len, uint16_t* state,
+                                  const int32_t* state_slot, int32_t num_state, const float* ape,
+                                  const float* norm_w, float eps, const float* cos_sin, int32_t max_spans,
+                                  const int32_t* comp_block_table, int32_t comp_bt_stride,
+                                  const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* pool,
+                                  int64_t page_stride, int64_t num_pages, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  return hca_write_impl(latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+                        token_seq, qsl, num_seqs, max_query_len, state, state_slot, num_state, ape, norm_w, eps,
+                        cos_sin, max_spans, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                        reinterpret_cast<uint8_t*>(pool), page_stride, num_pages, workspace, workspace_bytes, nullptr,
+                        stream, true);
+}
+
+extern "C" int ekv_hca_write_step_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                                       int64_t kvs_stride, int32_t num_tokens, int32_t dim,
+                                       const int64_t* slot_mapping, const int64_t* positions,
+                                       const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs,
+                                       int32_t max_query_len, uint16_t* state, const int32_t* state_slot,
+                                       int32_t num_state, const float* ape, const float* norm_w, float eps,
+                                       const float* cos_sin, int32_t max_spans, const int32_t* comp_block_table,
+                                       int32_t comp_bt_stride, const int32_t* ring_pages, int32_t ring_stride,
+                                       int32_t ring, uint16_t* pool, int64_t page_stride, int64_t num_pages,
+                                       void* workspace, int64_t workspace_bytes, int32_t window, int32_t* idx_out,
+                                       int64_t idx_stride, int32_t width, int32_t* lengths, void* stream) {
+  EKV_CHECK(ring_pages && idx_out && lengths, "null pointer");
+  EKV_CHECK(ring >= window && window >= 0 && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
+  EKV_CHECK(width >= 0 && idx_stride >= width, "idx_stride must be >= width >= 0");
+  const HcaIndexArgs ix{positions, token_seq, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                        window, qsl, slot_mapping, idx_out, idx_stride, width, lengths};
+  return hca_write_impl(latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping, positions,
+                        token_seq, qsl, num_seqs, max_query_len, state, state_slot, num_state, ape, norm_w, eps,
+                        cos_sin, max_spans, comp_block_table, comp_bt_stride, ring_pages, ring_stride, ring,
+                        reinterpret_cast<uint8_t*>(pool), page_stride, num_pages, workspace, workspace_bytes, &ix,
+                        stream, true);
 }

@@ -40,6 +40,9 @@ struct AppendArgs {
   float eps;
   const float* cos_sin;      // [cs_rows, 64]; nullptr = no prep
   int32_t cs_rows;
+  // HCA pools of bf16 rows (page = 64 rows of D bf16 values, no scales):
+  // the rows are stored as they come, not quantized
+  int32_t bf16_rows;
 };
 
 // ---------------------------------------------------------------------------
@@ -207,6 +210,25 @@ __device__ __forceinline__ void store_fp8_row(const AppendArgs& a, int64_t slot,
   if (ln == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = row.scale;
 }
 
+// Store a bf16 row at `slot`: quantized into a values-then-scales fp8 page
+// pool, or as it is into a pool of bf16 rows (a.bf16_rows).
+template <int D, int kLanes>
+__device__ __forceinline__ void store_row(const AppendArgs& a, int64_t slot, int ln,
+                                          const uint4 (&raw)[Fp8Row<D, kLanes>::kPerLane]) {
+  using R = Fp8Row<D, kLanes>;
+  if (!a.bf16_rows) {
+    store_fp8_row<D, kLanes>(a, slot, ln, quantize_row<D, kLanes>(raw));
+    return;
+  }
+  if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
+  uint8_t* row = a.cache + (slot / kPageTokens) * a.page_stride + (slot % kPageTokens) * (2 * D);
+#pragma unroll
+  for (int k = 0; k < R::kPerLane; ++k) {
+    const int c = ln + k * kLanes;
+    if (c < R::kChunks) *reinterpret_cast<uint4*>(row + 16 * c) = raw[k];
+  }
+}
+
 // Rows of workgroup `block`, stored at their slot_mapping slots: kWaves
 // waves, each taking kSeq groups of kRowsPerWave rows (4 rows of 16 lanes for
 // D = 128, else one row of 64 lanes).  A wave issues the loads of all its
@@ -245,7 +267,7 @@ __device__ __forceinline__ void append_rows(const AppendArgs& a, int block) {
 #pragma unroll
   for (int r = 0; r < kSeq; ++r) {
     if (t_first + r * kRowsPerWave >= a.num_tokens) return;  // whole row group exits together
-    store_fp8_row<D, kLanes>(a, slot[r], ln, quantize_row<D, kLanes>(raw[r]));
+    store_row<D, kLanes>(a, slot[r], ln, raw[r]);
   }
 }
 
@@ -300,7 +322,7 @@ __device__ __forceinline__ void hca_tail_range(const AppendArgs& a, int b, int k
         const int64_t sl =
             static_cast<int64_t>(a.ring_pages[static_cast<int64_t>(b) * a.ring_stride + rp / kPageTokens]) *
                 kPageTokens + rp % kPageTokens;
-        store_fp8_row<D, 64>(a, sl, lane, quantize_row<D, 64>(raw[u]));
+        store_row<D, 64>(a, sl, lane, raw[u]);
       }
       const int64_t rel = p % kStateRing - alias_lo;
       if (state_ok && k < kStateRing && (rel >= 0 && rel < alias_n) == in_alias) {
@@ -362,12 +384,13 @@ inline int hca_append_args(AppendArgs& a, const uint16_t* latent, int64_t latent
                            const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
                            int32_t num_seqs, uint8_t* pool, int64_t page_stride, int64_t num_pages,
                            const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* state,
-                           const int32_t* state_slot, int32_t num_state) {
+                           const int32_t* state_slot, int32_t num_state, bool bf16_rows = false) {
   EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
   EKV_CHECK(dim == 512 || dim == 576, "HCA dim must be 512 or 576");
   EKV_CHECK(latent && slot_mapping && positions && token_seq && qsl && pool, "null pointer");
   EKV_CHECK(latent_stride >= dim && latent_stride % 8 == 0, "bad latent_stride");
-  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0, "bad page_stride");
+  EKV_CHECK(page_stride >= kPageTokens * (bf16_rows ? 2 * dim : dim + 4) && page_stride % 16 == 0,
+            "bad page_stride");
   EKV_CHECK(ring_pages == nullptr || (ring >= kWindow && ring % kPageTokens == 0 && ring_stride >= ring / kPageTokens),
             "ring must be a multiple of 64, >= 128, with ring_stride >= ring/64");
   EKV_CHECK(state == nullptr || (kv_score && state_slot && kvs_stride >= 2 * dim && kvs_stride % 8 == 0),
@@ -381,6 +404,7 @@ inline int hca_append_args(AppendArgs& a, const uint16_t* latent, int64_t latent
   a.ring_pages = ring_pages; a.ring_stride = ring_stride; a.ring = ring;
   a.kv_score = kv_score; a.kvs_stride = kvs_stride; a.state = state; a.state_slot = state_slot;
   a.num_state = num_state;
+  a.bf16_rows = bf16_rows ? 1 : 0;
   return 0;
 }
 

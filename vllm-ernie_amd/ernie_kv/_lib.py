@@ -41,6 +41,16 @@ SIGNATURES: dict[str, tuple] = {
         [P, I64, P, I64, I32, I32, P, P, P, P, I32, I32, P, P, I32, P, P, F32, P, I32, P, I32, P, I32, I32, P, I64,
          I64, P, I64, I32, P, I64, I32, P, P],
     ),
+    "ekv_hca_write_bf16": (
+        I32,
+        [P, I64, P, I64, I32, I32, P, P, P, P, I32, I32, P, P, I32, P, P, F32, P, I32, P, I32, P, I32, I32, P, I64,
+         I64, P, I64, P],
+    ),
+    "ekv_hca_write_step_bf16": (
+        I32,
+        [P, I64, P, I64, I32, I32, P, P, P, P, I32, I32, P, P, I32, P, P, F32, P, I32, P, I32, P, I32, I32, P, I64,
+         I64, P, I64, I32, P, I64, I32, P, P],
+    ),
     "ekv_hca_decode_indices": (I32, [P, P, I32, P, I32, P, I32, I32, I32, P, P, P, I64, I32, P, P]),
     "ekv_merge_swa_topk": (I32, [P, I64, P, I64, P, I32, I32, I32, I32, P]),
     "ekv_hadamard_rows": (I32, [P, I64, P, I64, I32, I32, P]),

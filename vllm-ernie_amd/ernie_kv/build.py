@@ -66,16 +66,21 @@ def _run(cmd: list[str]) -> None:
 
 def build(verbose: bool = False) -> Path:
     """Compile every source and link ``libernie_kv.so`` next to this module."""
+    from concurrent.futures import ThreadPoolExecutor
+
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="ekv_build_") as tmp:
-        objs = []
+        objs, cmds = [], []
         for src, extra in SOURCES.items():
             obj = Path(tmp) / (Path(src).stem + ".o")
-            cmd = [cc, *COMMON, *extra, "-I", str(CSRC), "-c", str(CSRC / src), "-o", str(obj)]
+            cmds.append([cc, *COMMON, *extra, "-I", str(CSRC), "-c", str(CSRC / src), "-o", str(obj)])
             if verbose:
-                print(" ".join(cmd), flush=True)
-            _run(cmd)
+                print(" ".join(cmds[-1]), flush=True)
             objs.append(str(obj))
+        # one compiler process per source, at most as many as the cores allow
+        workers = max(1, min(len(cmds), len(os.sched_getaffinity(0)), 8))
+        with ThreadPoolExecutor(workers) as pool:
+            list(pool.map(_run, cmds))
         out_tmp = LIB_PATH.with_suffix(".so.tmp")
         _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(out_tmp)])
         os.replace(out_tmp, LIB_PATH)

@@ -164,13 +164,19 @@ def _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, m
         _need(state_slot is not None and state_slot.dtype == torch.int32, "state_slot int32")
     if workspace is not None:
         _need(workspace.dtype == torch.uint8 and workspace.is_contiguous(), "workspace: a uint8 hca_write_workspace")
+    if pool.dtype == torch.bfloat16:  # bf16 rows: the flat [-1, D] view, 64 rows a page
+        _need(pool.is_contiguous() and pool.numel() % (PAGE_TOKENS * D) == 0, "bf16 pool: contiguous rows of D")
+        page_stride, num_pages = PAGE_TOKENS * D * 2, pool.numel() // (PAGE_TOKENS * D)
+    else:
+        _need(pool.dtype == torch.uint8 and pool.dim() == 2 and pool.stride(1) == 1, "fp8 pool uint8 [pages, bytes]")
+        page_stride, num_pages = _rs(pool), pool.shape[0]
     return [
         latent.data_ptr(), _rs(latent), kv_score.data_ptr(), _rs(kv_score), T, D,
         slot_mapping.data_ptr(), positions.data_ptr(), token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1,
         int(max_query_len), _ptr(state), _ptr(state_slot), 0 if state is None else state.shape[0],
         ape.data_ptr(), norm_w.data_ptr(), float(eps), cos_sin.data_ptr(), cos_sin.shape[0],
         comp_block_table.data_ptr(), _rs(comp_block_table), _ptr(ring_pages),
-        0 if ring_pages is None else _rs(ring_pages), int(ring), pool.data_ptr(), _rs(pool), pool.shape[0],
+        0 if ring_pages is None else _rs(ring_pages), int(ring), pool.data_ptr(), page_stride, num_pages,
         _ptr(workspace), 0 if workspace is None else workspace.numel(),
     ]
 
@@ -199,10 +205,12 @@ def hca_write(
     one call.  With ``workspace`` (``hca_write_workspace``) decode-sized calls
     compress each completed span with four workgroups, and longer calls whose
     workspace was sized for their ``max_query_len`` with ``dim / 64`` (same
-    bytes)."""
+    bytes).  A bf16 ``pool`` (rows of D bf16 values, 64 a page) takes the
+    rows as they are and the compressed rows rounded to bf16; a uint8 pool
+    holds fp8 rows with per-token scales."""
     args = _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
                            ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace)
-    _lib.call("ekv_hca_write", *args, _stream())
+    _lib.call("ekv_hca_write_bf16" if pool.dtype == torch.bfloat16 else "ekv_hca_write", *args, _stream())
 
 
 def hca_write_step(
@@ -238,8 +246,8 @@ def hca_write_step(
     _need(lengths.dtype == torch.int32 and lengths.numel() >= latent.shape[0], "lengths must be int32 [T]")
     args = _hca_write_args(latent, kv_score, slot_mapping, positions, token_seq, qsl, max_query_len, state, state_slot,
                            ape, norm_w, eps, cos_sin, comp_block_table, ring_pages, ring, pool, workspace)
-    _lib.call("ekv_hca_write_step", *args, int(window), out.data_ptr(), out.stride(0), out.shape[1],
-              lengths.data_ptr(), _stream())
+    name = "ekv_hca_write_step_bf16" if pool.dtype == torch.bfloat16 else "ekv_hca_write_step"
+    _lib.call(name, *args, int(window), out.data_ptr(), out.stride(0), out.shape[1], lengths.data_ptr(), _stream())
 
 
 def hca_write_workspace(num_seqs: int, dim: int, device, max_query_len: int = 0) -> torch.Tensor:
