@@ -96,6 +96,16 @@ int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, const uint16_t
                    const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* state,
                    const int32_t* state_slot, int32_t num_state, void* stream);
 
+/* ekv_hca_append into a pool of bf16 rows (64 rows of dim bf16 values a
+ * page, page_stride >= 128 * dim bytes): rows stored as given.  The bf16 KV
+ * row of the non-fp8 HCA class (nvidia/attention.py:542-558). */
+int ekv_hca_append_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                        int64_t kvs_stride, int32_t num_tokens, int32_t dim, const int64_t* slot_mapping,
+                        const int64_t* positions, const int32_t* token_seq, const int32_t* qsl,
+                        int32_t num_seqs, uint16_t* pool, int64_t page_stride /*bytes*/, int64_t num_pages,
+                        const int32_t* ring_pages, int32_t ring_stride, int32_t ring, uint16_t* state,
+                        const int32_t* state_slot, int32_t num_state, void* stream);
+
 /*
  * The whole HCA write of one step in one call: ekv_hca_compress followed by
  * ekv_hca_append with the same arguments, both on `stream` (same bytes in the

@@ -65,11 +65,11 @@ def _dsa_setup(dev, rng, ctxs, rows_per_req, fp4=False):
     slot_mapping = paged.slots_from_block_table(bt, req, positions)
     T = len(positions)
     params = {
-        "indexer.wq_b": bf16_tensor(randn_bf16(rng, (64 * 128, 128), 128 ** -0.5), dev),
-        "indexer.wk_weights_proj": bf16_tensor(randn_bf16(rng, (128 + 64, 256), 256 ** -0.5), dev),
+        "indexer.wq_b.weight": bf16_tensor(randn_bf16(rng, (64 * 128, 128), 128 ** -0.5), dev),
+        "indexer.wk_weights_proj.weight": bf16_tensor(randn_bf16(rng, (128 + 64, 256), 256 ** -0.5), dev),
         "indexer.k_norm.weight": to_dev((1 + 0.1 * rng.standard_normal(128)).astype(np.float32), dev),
         "indexer.k_norm.bias": to_dev((0.1 * rng.standard_normal(128)).astype(np.float32), dev),
-        "kv_b_proj": bf16_tensor(randn_bf16(rng, (64 * (192 + 256), 512), 0.05), dev),
+        "kv_b_proj.weight": bf16_tensor(randn_bf16(rng, (64 * (192 + 256), 512), 0.05), dev),
         "attn_sink": to_dev(rng.standard_normal(64).astype(np.float32), dev),
     }
     md = A.DSAStepMetadata(slot_mapping=to_dev(slot_mapping, dev), block_table=to_dev(bt, dev),
@@ -77,7 +77,18 @@ def _dsa_setup(dev, rng, ctxs, rows_per_req, fp4=False):
     inputs = dict(hidden=randn_bf16(rng, (T, 256)), q_c=randn_bf16(rng, (T, 128)), q=randn_bf16(rng, (T, 64, 256)),
                   kv_c=randn_bf16(rng, (T, 512)), k_pe=randn_bf16(rng, (T, 1, 64)))
     return SimpleNamespace(cfg=cfg, bt=bt, kc=kc, lat=lat, req=req, positions=positions, slot_mapping=slot_mapping,
-                           T=T, params=params, md=md, inputs=inputs)
+                           T=T, params=params, md=md, inputs=inputs,
+                           vllm_config=A.ernie5_5_vllm_config(cfg, use_fp4_indexer_cache=fp4, device=dev))
+
+
+def _dsa_layer(case, topk_buf, swa_buf):
+    """Ernie5_5DSAAttention built as the reference builds it, with the
+    case's weights loaded."""
+    from ernie_kv import attention as A
+
+    layer = A.Ernie5_5DSAAttention(case.vllm_config, "model.layers.3.attn", topk_buf, swa_buf)
+    layer.load_weights(case.params.items())
+    return layer
 
 
 def _oracle_indexer(case, layer, dev):
@@ -114,11 +125,11 @@ def test_indexer_forward_vs_oracle(dev, fp4):
     case = _dsa_setup(dev, rng, [3000, 4500], [1, 3], fp4=fp4)
     topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
-    p = case.params
-    ix = A.Ernie5_5Indexer(case.cfg, topk_buf, swa_buf, prefix="model.layers.3.attn.indexer",
-                           wq_b=p["indexer.wq_b"], wk_weights_proj=p["indexer.wk_weights_proj"],
-                           k_norm_weight=p["indexer.k_norm.weight"], k_norm_bias=p["indexer.k_norm.bias"],
-                           use_fp4_kv=fp4)
+    vc = case.vllm_config
+    ix = A.Ernie5_5Indexer(vc, case.cfg, None, vc.cache_config, topk_buf, swa_buf,
+                           prefix="model.layers.3.attn.indexer")
+    ix.load_weights((k[len("indexer."):], v) for k, v in case.params.items() if k.startswith("indexer."))
+    assert ix.use_fp4_kv == fp4
     assert ix.k_cache.head_dim == (68 if fp4 else 132)
     ix.k_cache.kv_cache = to_dev(case.kc, dev)
     with A.set_forward_context({ix.k_cache.prefix: case.md}):
@@ -143,8 +154,7 @@ def test_dsa_indexer_and_attn_vs_oracle(dev, fp4):
     T = case.T
     topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
-    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params,
-                                   use_fp4_kv=fp4)
+    layer = _dsa_layer(case, topk_buf, swa_buf)
     layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
     layer.mla_attn.kv_cache = to_dev(case.lat, dev)
     captured = {}
@@ -209,8 +219,9 @@ def test_hca_prepare_and_attn_vs_oracle(dev):
               "compressor.ape": to_dev((rng.standard_normal((128, D)) * 0.5).astype(np.float32), dev),
               "compressor.norm.weight": to_dev((1 + 0.1 * rng.standard_normal(D)).astype(np.float32), dev)}
     cos_sin = oi.yarn_cos_sin(np.arange(8) * 128, 64, cfg.compress_rope_theta)
-    layer = A.select_ernie5_5_hca_cls("fp8")(cfg, "model.layers.0.attn", params=params, ring=ring,
-                                             compress_cos_sin=to_dev(cos_sin, dev))
+    layer = A.select_ernie5_5_hca_cls("fp8")(A.ernie5_5_vllm_config(cfg, device=dev), "model.layers.0.attn",
+                                             ring=ring, compress_cos_sin=to_dev(cos_sin, dev))
+    layer.load_weights(params.items())
     layer.kv_cache = torch.zeros((pages, paged.fp8_page_bytes(D)), dtype=torch.uint8, device=dev)
     layer.state_cache = torch.zeros((B, 256, 2 * D), dtype=torch.bfloat16, device=dev)
     st = oh.HcaState(pages, D, B)
@@ -233,8 +244,8 @@ def test_hca_prepare_and_attn_vs_oracle(dev):
                                state_slot=to_dev(state_slot, dev), max_seq_len=int(positions.max()) + 1)
         o_padded = torch.zeros((T, 64, D), dtype=torch.bfloat16, device=dev)
         with A.set_forward_context({layer.prefix: md}):
-            layer._prepare_and_attn_fn(bf16_tensor(q, dev), bf16_tensor(kv, dev), bf16_tensor(kv_score, dev),
-                                       to_dev(positions, dev), o_padded)
+            layer._cache_and_attn(bf16_tensor(q, dev), bf16_tensor(kv, dev), bf16_tensor(kv_score, dev),
+                                  to_dev(positions, dev), o_padded)
         torch.cuda.synchronize()
         oh.hca_write(st, kv, kv_score, positions, token_seq, qsl, slots, ring_pages, ring, comp_bt, state_slot,
                      params["compressor.ape"].cpu().numpy(), params["compressor.norm.weight"].cpu().numpy(),
@@ -360,8 +371,7 @@ def test_dsa_prefill_chunk_vs_oracle(dev, fp4):
     T = case.T
     topk_buf = torch.full((T, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((T, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
-    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params,
-                                   use_fp4_kv=fp4)
+    layer = _dsa_layer(case, topk_buf, swa_buf)
     layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
     layer.mla_attn.kv_cache = to_dev(case.lat, dev)
     captured = {}
@@ -454,7 +464,7 @@ def test_dsa_indexer_and_attn_graph_replay(dev):
     T = case.T
     topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
     swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
-    layer = A.Ernie5_5DSAAttention(case.cfg, "model.layers.3.attn", topk_buf, swa_buf, params=case.params)
+    layer = _dsa_layer(case, topk_buf, swa_buf)
     layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
     layer.mla_attn.kv_cache = to_dev(case.lat, dev)
     inp = {k: bf16_tensor(v, dev) for k, v in case.inputs.items()}
@@ -493,3 +503,214 @@ def test_dsa_indexer_and_attn_graph_replay(dev):
             assert torch.equal(a, b), f"replay {i} differs from the eager call"
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- layer forwards
+def _rel_err(got, ref):
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def _spy(obj, name, store):
+    orig = getattr(obj, name)
+
+    def wrapped(*args, **kwargs):
+        out = orig(*args, **kwargs)
+        store[name] = (args, kwargs, out)
+        return out
+
+    setattr(obj, name, wrapped)
+
+
+@pytest.mark.parametrize("fp8_o_proj", [False, True], ids=["bf16-o-proj", "fp8-o-proj"])
+def test_dsa_forward_vs_oracle(dev, fp8_o_proj):
+    """Ernie5_5DSAAttention(vllm_config, prefix, topk_indices_buffer,
+    swa_topk_buffer).forward(positions, hidden_states) (attention.py:1062-1203)
+    with every weight loaded by name: the KV path's results against the
+    oracle from the tensors the layer handed ``_indexer_and_attn`` (indexer K
+    and latent cache bytes, top-k and merged rows exact, the latent decode
+    within tolerance), and the layer output against an fp64 recomputation of
+    the reference's output side (W_UV, VHA head mix, sigmoid gate, wo_b) from
+    the oracle's decode.  With fp8_o_proj the wo_b input goes through
+    sigmoid_mul_quant_fp8 (1 x 128 fp8 groups), so the output tolerance is
+    the fp8 step's."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(71)
+    case = _dsa_setup(dev, rng, [3000, 4500], [1, 3])
+    T, H = case.T, 64
+    hidden, q_lora = 256, 128
+    w = dict(case.params)
+    w.update({
+        "fused_qkv_a_proj.weight": bf16_tensor(randn_bf16(rng, (q_lora + 512 + 64, hidden), hidden ** -0.5), dev),
+        "q_a_layernorm.weight": bf16_tensor(1 + 0.1 * randn_bf16(rng, (q_lora,)), dev),
+        "q_b_proj.weight": bf16_tensor(randn_bf16(rng, (H * 256, q_lora), q_lora ** -0.5), dev),
+        "kv_a_layernorm.weight": bf16_tensor(1 + 0.1 * randn_bf16(rng, (512,)), dev),
+        "o_gate.weight": bf16_tensor(randn_bf16(rng, (H * 256, q_lora), q_lora ** -0.5), dev),
+        "wo_b.weight": bf16_tensor(randn_bf16(rng, (hidden, H * 256), (H * 256) ** -0.5), dev),
+        "vha.U": bf16_tensor(randn_bf16(rng, (H, 16), 0.05), dev),
+        "vha.V": bf16_tensor(randn_bf16(rng, (H, 16), 0.05), dev),
+    })
+    topk_buf = torch.full((16, TOPK), -7, dtype=torch.int32, device=dev)
+    swa_buf = torch.full((16, TOPK + WINDOW), -7, dtype=torch.int32, device=dev)
+    vc = A.ernie5_5_vllm_config(case.cfg, device=dev)
+    layer = A.Ernie5_5DSAAttention(vc, "model.layers.3.attn", topk_buf, swa_buf, fp8_o_proj=fp8_o_proj)
+    loaded = layer.load_weights(w.items())
+    assert loaded == {n for n, _ in layer.named_parameters()}, "every parameter is loaded by name"
+    layer.indexer.k_cache.kv_cache = to_dev(case.kc, dev)
+    layer.mla_attn.kv_cache = to_dev(case.lat, dev)
+    seen = {}
+    _spy(layer, "_indexer_and_attn", seen)
+    _spy(layer.mla_attn.impl, "_fp8_flash_mla_kernel", seen)
+    hid = bf16_tensor(case.inputs["hidden"], dev)
+    pos_t = to_dev(case.positions, dev)
+    with A.set_forward_context({layer.mla_attn.prefix: case.md, layer.indexer.k_cache.prefix: case.md}):
+        y = layer(pos_t, hid)
+    torch.cuda.synchronize()
+    assert y.shape == (T, hidden) and y.dtype == torch.bfloat16
+    (_, q_c, _, q, kv_c_normed, k_pe, _), _, _ = seen["_indexer_and_attn"]
+    # the KV path from the layer's own projected tensors
+    case.inputs.update(q_c=bf16_values(q_c), q=bf16_values(q), kv_c=bf16_values(kv_c_normed),
+                       k_pe=bf16_values(k_pe).reshape(T, 1, 64))
+    kc_ref, top_ref = _oracle_indexer(case, layer.indexer, dev)
+    assert np.array_equal(layer.indexer.k_cache.kv_cache.cpu().numpy(), kc_ref), "indexer K cache bytes differ"
+    assert np.array_equal(topk_buf[:T].cpu().numpy(), top_ref), "top-k differs"
+    merged_ref = merge_swa_topk(top_ref, case.positions, TOPK + WINDOW, WINDOW)
+    assert np.array_equal(swa_buf[:T].cpu().numpy(), merged_ref), "merged rows differ"
+    lat = case.lat.copy()
+    codes, scale = quantize_rows(np.concatenate([case.inputs["kv_c"], case.inputs["k_pe"].reshape(T, 64)], axis=1))
+    paged.write_fp8_rows(lat, case.slot_mapping, codes, scale, 576)
+    assert np.array_equal(layer.mla_attn.kv_cache.cpu().numpy(), lat), "latent cache bytes differ"
+    q_abs = bf16_values(layer.mla_attn.absorb_q(q))
+    glob = logical_to_global(merged_ref, case.req, case.bt)
+    ref_o, _ = od.sparse_mla_decode(q_abs, lambda s: od.gather_rows_fp8(lat, s, 576), glob, 256 ** -0.5, 512,
+                                    case.params["attn_sink"].cpu().numpy())
+    # the decode's latent output, as the impl returned it to the layer
+    o_lat = seen["_fp8_flash_mla_kernel"][2][0][:, 0]
+    _check_decode(bf16_values(o_lat), ref_o, "latent decode output")
+    # the output side in fp64 from the oracle's decode
+    f64 = lambda t: t.detach().float().cpu().numpy().astype(np.float64)  # noqa: E731
+    w_uv = f64(layer.mla_attn.W_UV_T)                                     # [H, 512, 256]
+    attn = np.einsum("thc,hcv->thv", ref_o, w_uv)                          # [T, H, 256]
+    mix = f64(layer.vha.m)
+    o = np.einsum("hg,tgv->thv", mix, attn).reshape(T, -1)
+    gate = bf16_values(q_c).astype(np.float64) @ f64(layer.o_gate.weight).T
+    ref_y = (o / (1.0 + np.exp(-gate))) @ f64(layer.wo_b.weight).T
+    err = _rel_err(bf16_values(y).astype(np.float64), ref_y)
+    assert err < (4e-2 if fp8_o_proj else 1.5e-2), f"layer output rel err {err}"
+
+
+@pytest.mark.parametrize("fp8_o_proj", [False, True], ids=["bf16-o-proj", "fp8-o-proj"])
+@pytest.mark.parametrize("cache", ["fp8", "bfloat16"])
+def test_hca_forward_vs_oracle(dev, cache, fp8_o_proj):
+    """The HCA layer built by select_ernie5_5_hca_cls(kv_cache_dtype)(vllm_config,
+    prefix) with every weight loaded by name, forward(positions,
+    hidden_states) (attention.py:471-539) over a prefill chunk and two
+    decode steps (one and three query rows): the cache (fp8 pages, or bf16
+    rows for the FlashInfer class) and state ring bytes against the oracle
+    from the tensors the layer handed its KV path, o_padded within the
+    decode tolerance, and the layer output against an fp64 recomputation of
+    the output side (VHA mix, inverse RoPE of the rope part, grouped wo_a,
+    sigmoid gate, wo_b) from the oracle's attention output.  With fp8_o_proj
+    VHA + inverse RoPE + quant run in vha_inv_rope_fp8_quant and the wo_b
+    input in sigmoid_mul_quant_fp8."""
+    from ernie_kv import attention as A
+
+    rng = np.random.default_rng(72)
+    D, H, B, ring, hidden, q_lora, r, G = 512, 64, 2, 192, 512, 256, 256, 8
+    cfg = A.ernie5_5_config(hidden_size=hidden, q_lora_rank=q_lora, o_lora_rank=r, max_position_embeddings=4096)
+    lp, cp, rp = 8, 1, ring // 64
+    perm = rng.permutation(B * (lp + cp + rp)).astype(np.int32)
+    bt = perm[: B * lp].reshape(B, lp)
+    comp_bt = perm[B * lp: B * (lp + cp)].reshape(B, cp)
+    ring_pages = perm[B * (lp + cp):].reshape(B, rp)
+    pages = len(perm)
+    bf = lambda shape, s: bf16_tensor(randn_bf16(rng, shape, s), dev)  # noqa: E731
+    w = {"attn_sink": to_dev(rng.standard_normal(H).astype(np.float32), dev),
+         "compressor.ape": to_dev((rng.standard_normal((128, D)) * 0.5).astype(np.float32), dev),
+         "compressor.norm.weight": to_dev((1 + 0.1 * rng.standard_normal(D)).astype(np.float32), dev),
+         "compressor.fused_wkv_wgate.weight": bf((2 * D, hidden), hidden ** -0.5),
+         "fused_wqa_wkv.weight": bf((q_lora + D, hidden), hidden ** -0.5),
+         "q_norm.weight": bf16_tensor(1 + 0.1 * randn_bf16(rng, (q_lora,)), dev),
+         "kv_norm.weight": bf16_tensor(1 + 0.1 * randn_bf16(rng, (D,)), dev),
+         "wq_b.weight": bf((H * D, q_lora), q_lora ** -0.5),
+         "wo_a": bf((G, r, (H // G) * D), ((H // G) * D) ** -0.5),
+         "wo_b.weight": bf((hidden, G * r), (G * r) ** -0.5),
+         "o_gate.weight": bf((G * r, q_lora), q_lora ** -0.5),
+         "vha.U": bf((H, 16), 0.05), "vha.V": bf((H, 16), 0.05)}
+    vc = A.ernie5_5_vllm_config(cfg, cache_dtype=cache, device=dev)
+    cls = A.select_ernie5_5_hca_cls(cache)
+    assert cls is (A.Ernie5_5HCAFlashMLAAttention if cache == "fp8" else A.Ernie5_5HCAFlashInferAttention)
+    layer = cls(vc, "model.layers.0.attn", ring=ring, fp8_o_proj=fp8_o_proj)
+    loaded = layer.load_weights(w.items())
+    assert loaded == {n for n, _ in layer.named_parameters()}, "every parameter is loaded by name"
+    bf16_cache = cache != "fp8"
+    if bf16_cache:
+        layer.kv_cache = torch.zeros((pages * 64, D), dtype=torch.bfloat16, device=dev)
+    else:
+        layer.kv_cache = torch.zeros((pages, paged.fp8_page_bytes(D)), dtype=torch.uint8, device=dev)
+    layer.state_cache = torch.zeros((B, 256, 2 * D), dtype=torch.bfloat16, device=dev)
+    st = oh.HcaState(pages, D, B, bf16=bf16_cache)
+    state_slot = np.arange(B, dtype=np.int32)
+    sinks = w["attn_sink"].cpu().numpy()
+    cos_sin = layer.compress_cos_sin.cpu().numpy()
+    rope = layer.rotary_emb.cos_sin_cache.cpu().numpy().astype(np.float64)
+    f64 = lambda t: t.detach().float().cpu().numpy().astype(np.float64)  # noqa: E731
+    pos0 = [0, 0]
+    hist = {0: [], 1: []}
+    for counts in ([300, 257], [1, 3], [70, 2]):
+        positions = np.concatenate([np.arange(p, p + n) for p, n in zip(pos0, counts)]).astype(np.int64)
+        token_seq = np.concatenate([np.full(n, b, np.int32) for b, n in enumerate(counts)])
+        qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        T = len(positions)
+        slots = paged.slots_from_block_table(bt, token_seq, positions)
+        md = A.HCAStepMetadata(slot_mapping=to_dev(slots, dev), query_start_loc=to_dev(qsl, dev),
+                               token_seq=to_dev(token_seq, dev), max_query_len=int(max(counts)),
+                               comp_block_table=to_dev(comp_bt, dev), ring_pages=to_dev(ring_pages, dev),
+                               state_slot=to_dev(state_slot, dev), max_seq_len=int(positions.max()) + 1)
+        seen = {}
+        _spy(layer, "_prepare_and_attn_fn", seen)
+        _spy(layer, "_cache_and_attn", seen)
+        with A.set_forward_context({layer.prefix: md}):
+            y = layer(to_dev(positions, dev), bf16_tensor(randn_bf16(rng, (T, hidden)), dev))
+        torch.cuda.synchronize()
+        assert y.shape == (T, hidden)
+        (q, kv, kv_score, _, o_padded), _, _ = seen["_cache_and_attn"]
+        qr = seen["_prepare_and_attn_fn"][0][1]
+        q, kv, kv_score = bf16_values(q), bf16_values(kv), bf16_values(kv_score)
+        oh.hca_write(st, kv, kv_score, positions, token_seq, qsl, slots, ring_pages, ring, comp_bt, state_slot,
+                     w["compressor.ape"].cpu().numpy(), w["compressor.norm.weight"].cpu().numpy(), cfg.rms_norm_eps,
+                     cos_sin)
+        got_pool = layer.kv_cache.view(torch.uint8).reshape(pages, -1).cpu().numpy()
+        assert np.array_equal(got_pool, st.pool), f"cache bytes differ after {counts}"
+        assert np.array_equal(bf16_values(layer.state_cache).reshape(st.state.shape), st.state)
+        for t in range(T):
+            hist[int(token_seq[t])].append(kv[t])
+        ref_o = np.zeros((T, H, D))
+        for t in range(T):
+            p, b = int(positions[t]), int(token_seq[t])
+            n_c, wn = (p + 1) // 128, min(p + 1, WINDOW)
+            cs_ = np.array([oh.comp_slot(comp_bt, b, j) for j in range(n_c)], np.int64)
+            if bf16_cache:
+                vals = bf16_values(layer.kv_cache).reshape(-1, D) if n_c else None
+                comp = vals[cs_].astype(np.float64) if n_c else np.zeros((0, D))
+                win = np.stack(hist[b][p - wn + 1: p + 1]).astype(np.float64)
+            else:
+                comp = od.gather_rows_fp8(st.pool, cs_, D) if n_c else np.zeros((0, D))
+                wc, ws_ = quantize_rows(np.stack(hist[b][p - wn + 1: p + 1]))
+                win = wc_decode(wc, ws_)
+            kv_rows = np.concatenate([comp, win])
+            ref_o[t] = od.sparse_mla_decode(q[t:t + 1], lambda s: kv_rows[s], np.arange(len(kv_rows))[None],
+                                            D ** -0.5, 512, sinks)[0][0]
+        _check_decode(bf16_values(o_padded[:, :H]), ref_o, f"o_padded after {counts}")
+        # the output side in fp64 from the oracle's attention output
+        o = np.einsum("hg,tgd->thd", f64(layer.vha.m), ref_o)
+        cs = rope[positions]
+        c, s = cs[:, None, :32], cs[:, None, 32:]
+        e, od_ = o[..., 448::2].copy(), o[..., 449::2].copy()
+        o[..., 448::2], o[..., 449::2] = e * c + od_ * s, od_ * c - e * s
+        z = np.einsum("grk,tgk->tgr", f64(layer.wo_a), o.reshape(T, G, -1)).reshape(T, -1)
+        gate = bf16_values(qr).astype(np.float64) @ f64(layer.o_gate.weight).T
+        ref_y = (z / (1.0 + np.exp(-gate))) @ f64(layer.wo_b.weight).T
+        err = _rel_err(bf16_values(y).astype(np.float64), ref_y)
+        assert err < (5e-2 if fp8_o_proj else 1.5e-2), f"layer output rel err {err} after {counts}"
+        pos0 = [p + n for p, n in zip(pos0, counts)]

@@ -143,15 +143,13 @@ def test_attn_tp_and_sink_backend_errors():
 
 
 def _indexer(use_fp4_kv, pcp=1, dcp=1):
-    import torch
-
     from ernie_kv import attention as A
 
     cfg = A.ernie5_5_config(hidden_size=256, hybrid_mla_q_lora_rank=128)
-    return A.Ernie5_5Indexer(cfg, None, None, prefix="model.layers.0.self_attn.indexer",
-                             wq_b=torch.zeros(64 * 128, 128), wk_weights_proj=torch.zeros(192, 256),
-                             k_norm_weight=torch.ones(128), k_norm_bias=torch.zeros(128), use_fp4_kv=use_fp4_kv,
-                             prefill_context_parallel_size=pcp, decode_context_parallel_size=dcp)
+    vc = A.ernie5_5_vllm_config(cfg, use_fp4_indexer_cache=use_fp4_kv, device="cpu",
+                                prefill_context_parallel_size=pcp, decode_context_parallel_size=dcp)
+    return A.Ernie5_5Indexer(vc, cfg, vc.quant_config, vc.cache_config, None, None,
+                             prefix="model.layers.0.self_attn.indexer")
 
 
 @pytest.mark.parametrize("pcp,dcp", [(2, 1), (1, 2), (2, 2)])

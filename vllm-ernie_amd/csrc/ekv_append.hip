@@ -367,6 +367,24 @@ extern "C" int ekv_hca_append(const uint16_t* latent, int64_t latent_stride, con
   return launch_hca_append(a, dim, num_seqs, true, true, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int ekv_hca_append_bf16(const uint16_t* latent, int64_t latent_stride, const uint16_t* kv_score,
+                                   int64_t kvs_stride, int32_t num_tokens, int32_t dim,
+                                   const int64_t* slot_mapping, const int64_t* positions,
+                                   const int32_t* token_seq, const int32_t* qsl, int32_t num_seqs,
+                                   uint16_t* pool, int64_t page_stride, int64_t num_pages,
+                                   const int32_t* ring_pages, int32_t ring_stride, int32_t ring,
+                                   uint16_t* state, const int32_t* state_slot, int32_t num_state,
+                                   void* stream) {
+  EKV_CHECK(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return 0;
+  AppendArgs a;
+  const int rc = hca_append_args(a, latent, latent_stride, kv_score, kvs_stride, num_tokens, dim, slot_mapping,
+                                 positions, token_seq, qsl, num_seqs, reinterpret_cast<uint8_t*>(pool), page_stride,
+                                 num_pages, ring_pages, ring_stride, ring, state, state_slot, num_state, true);
+  if (rc) return rc;
+  return launch_hca_append(a, dim, num_seqs, true, true, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int ekv_merge_swa_topk(const int32_t* topk, int64_t topk_stride, int32_t* out,
                                   int64_t out_stride, const int64_t* positions, int32_t num_tokens,
                                   int32_t topk_width, int32_t out_width, int32_t window, void* stream) {

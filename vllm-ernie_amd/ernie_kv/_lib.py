@@ -30,6 +30,10 @@ SIGNATURES: dict[str, tuple] = {
         I32,
         [P, I64, P, I64, I32, I32, P, P, P, P, I32, P, I64, I64, P, I32, I32, P, P, I32, P],
     ),
+    "ekv_hca_append_bf16": (
+        I32,
+        [P, I64, P, I64, I32, I32, P, P, P, P, I32, P, I64, I64, P, I32, I32, P, P, I32, P],
+    ),
     "ekv_hca_write": (
         I32,
         [P, I64, P, I64, I32, I32, P, P, P, P, I32, I32, P, P, I32, P, P, F32, P, I32, P, I32, P, I32, I32, P, I64,

@@ -12,6 +12,7 @@ with the fields the path reads.
 from __future__ import annotations
 
 import contextlib
+import copy
 import dataclasses
 import enum
 import math
@@ -419,15 +420,150 @@ def _indexer_workspace(rows: int, max_len: int, device) -> torch.Tensor:
     return ws
 
 
+# --------------------------------------------------------------------------- layer building blocks
+class Linear(torch.nn.Module):
+    """A bias-free linear layer (stand-in for vLLM's parallel linear layers
+    at TP = 1): ``weight [out, in]``; returns ``(y, None)`` when
+    ``return_bias`` (the vLLM convention the reference's call sites index
+    with ``[0]``), else ``y``.  A plain library GEMM outside the KV path."""
+
+    def __init__(self, in_features: int, out_features: int, return_bias: bool = False, device=None,
+                 dtype=torch.bfloat16) -> None:
+        super().__init__()
+        self.input_size, self.output_size = in_features, out_features
+        self.return_bias = return_bias
+        self.weight = torch.nn.Parameter(torch.empty(out_features, in_features, device=device, dtype=dtype),
+                                          requires_grad=False)
+
+    def forward(self, x: torch.Tensor):
+        y = x @ self.weight.t()
+        return (y, None) if self.return_bias else y
+
+
+class RMSNorm(torch.nn.Module):
+    """``x / sqrt(mean(x^2) + eps) * weight``, computed in fp32 and returned
+    in the input dtype (vLLM's RMSNorm)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6, device=None, dtype=torch.bfloat16) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = torch.nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype), requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class InterleavedRotaryEmbedding:
+    """RoPE on interleaved pairs (2i, 2i + 1) (``is_neox_style=False``),
+    plain frequencies ``theta ** (-2i / rot_dim)``; ``cos_sin_cache`` is the
+    ``[max_position, rot_dim]`` cos | sin table (the layout the post-attention
+    inverse-RoPE kernel reads).  ``__call__(positions, q, k)`` returns the
+    rotated copies, computed in fp32 (torch ops around the KV path)."""
+
+    def __init__(self, rot_dim: int, max_position: int, rope_parameters: dict, device) -> None:
+        rope_type = rope_parameters.get("rope_type", "default")
+        if rope_type != "default":
+            raise NotImplementedError(f"rope_type {rope_type!r}: pass the layer a cos | sin table instead")
+        self.rot_dim = rot_dim
+        self.cos_sin_cache = rope_cos_sin_table(rot_dim, rope_parameters["rope_theta"], max_position, device)
+
+    @classmethod
+    def from_table(cls, cos_sin_cache: torch.Tensor) -> "InterleavedRotaryEmbedding":
+        """From a given ``[max_position, rot_dim]`` cos | sin table."""
+        self = cls.__new__(cls)
+        self.rot_dim = cos_sin_cache.shape[1]
+        self.cos_sin_cache = cos_sin_cache.contiguous()
+        return self
+
+    def rotate(self, positions: torch.Tensor, x: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+        half = self.rot_dim // 2
+        cs = self.cos_sin_cache[positions]
+        shape = (cs.shape[0],) + (1,) * (x.dim() - 2) + (half,)
+        c, s = cs[:, :half].reshape(shape), cs[:, half:].reshape(shape)
+        if inverse:
+            s = -s
+        xf = x.float()
+        e, o = xf[..., 0::2], xf[..., 1::2]
+        out = torch.stack([e * c - o * s, e * s + o * c], dim=-1).flatten(-2)
+        return out.to(x.dtype)
+
+    def __call__(self, positions: torch.Tensor, q: torch.Tensor, k: torch.Tensor):
+        return self.rotate(positions, q), self.rotate(positions, k)
+
+
+_fp8_luts: dict = {}
+
+
+def _fp8_values(codes: torch.Tensor) -> torch.Tensor:
+    """fp32 values of e4m3fn codes (a 256-entry table per device)."""
+    key = str(codes.device)
+    lut = _fp8_luts.get(key)
+    if lut is None:
+        lut = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).to(torch.float32).to(codes.device)
+        _fp8_luts[key] = lut
+    return lut[codes.view(torch.uint8).long()]
+
+
+def _ue8m0_bytes(packed: torch.Tensor) -> torch.Tensor:
+    """int32 words of four biased exponents -> their 4 bytes (last dim x4)."""
+    w = packed.to(torch.int64) & 0xFFFFFFFF
+    return torch.stack([(w >> (8 * c)) & 0xFF for c in range(4)], dim=-1).flatten(-2)
+
+
+def dequant_sigmoid_mul(data: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """Values of ``sigmoid_mul_quant_fp8``'s output: 1 x 128 groups scaled
+    by ``2 ** (byte - 127)`` (the exponents packed four per int32)."""
+    N, hidden = data.shape
+    exps = _ue8m0_bytes(scale)[:, : hidden // 128].float() - 127.0
+    return _fp8_values(data) * torch.exp2(exps).repeat_interleave(128, dim=1)
+
+
+def dequant_vha(data: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """Values of ``vha_inv_rope_fp8_quant``'s output ``[T, G, hpg * 512]``:
+    each head's four 128-wide chunks scaled by their exponent bytes."""
+    T, G, width = data.shape
+    exps = _ue8m0_bytes(scale).reshape(T, G, -1).float() - 127.0  # [T, G, hpg * 4]
+    return _fp8_values(data) * torch.exp2(exps).repeat_interleave(128, dim=2)
+
+
+def dsa_indexer_uses_fp4(vllm_config) -> bool:
+    """Stand-in for vLLM's MXFP4 indexer-cache selector: the
+    ``use_fp4_indexer_cache`` flag of ``vllm_config.attention_config``."""
+    return bool(getattr(getattr(vllm_config, "attention_config", None), "use_fp4_indexer_cache", False))
+
+
+def _device_of(vllm_config):
+    dc = getattr(vllm_config, "device_config", None)
+    return getattr(dc, "device", None) or ("cuda" if torch.cuda.is_available() else "cpu")
+
+
+def _load(module: torch.nn.Module, weights) -> set:
+    """vLLM-style ``load_weights``: copy each ``(name, tensor)`` into the
+    parameter or buffer of that name; returns the names loaded."""
+    params = dict(module.named_parameters())
+    params.update(dict(module.named_buffers()))
+    loaded = set()
+    for name, w in weights:
+        if name not in params:
+            raise KeyError(f"{type(module).__name__} has no weight {name!r}")
+        params[name].data.copy_(w.to(params[name].dtype))
+        loaded.add(name)
+    return loaded
+
+
 # Query rows scored per indexer call: one call's workspace holds
 # rows x max_len x 20 bytes, so long prefill chunks run in pieces.
 _INDEXER_WORKSPACE_BYTES = 1 << 30
 
 
 # --------------------------------------------------------------------------- layers
-class Ernie5_5Indexer:
+class Ernie5_5Indexer(torch.nn.Module):
     """Lightning indexer scoring the tokens older than the sliding window
-    (attention.py:863-984).
+    (attention.py:863-984), constructed as the reference's
+    ``(vllm_config, config, quant_config, cache_config, topk_indices_buffer,
+    swa_topk_buffer, prefix)``.
 
     ``forward(hidden_states, qr, positions)`` runs the reference's order:
     the two projections (``wq_b`` on ``qr``, ``wk_weights_proj`` on
@@ -438,54 +574,65 @@ class Ernie5_5Indexer:
     tokens, written to ``indexer_op.topk_indices_buffer[:T]``.
     ``topk_indices_buffer`` (the layer attribute) is the swa buffer the
     sparse MLA reads: the merged rows.  K cache rows are 132 bytes (fp8
-    values + fp32 scale) or, with ``use_fp4_kv``, 68 bytes (MXFP4 values +
-    four E8M0 scales; ``_quantize_fp4``, attention.py:986-1025), which the
-    reference allows only without context parallelism (:881-892)."""
+    values + fp32 scale) or, with the MXFP4 cache (``dsa_indexer_uses_fp4``),
+    68 bytes (MXFP4 values + four E8M0 scales; ``_quantize_fp4``,
+    attention.py:986-1025), which the reference allows only without context
+    parallelism (:881-892)."""
 
-    def __init__(self, config, topk_indices_buffer: torch.Tensor | None, swa_topk_buffer: torch.Tensor | None,
-                 prefix: str = "", *, wq_b: torch.Tensor, wk_weights_proj: torch.Tensor,
-                 k_norm_weight: torch.Tensor, k_norm_bias: torch.Tensor, use_fp4_kv: bool = False,
-                 prefill_context_parallel_size: int = 1, decode_context_parallel_size: int = 1) -> None:
-        self.use_fp4_kv = bool(use_fp4_kv)
+    def __init__(self, vllm_config, config, quant_config, cache_config, topk_indices_buffer: torch.Tensor | None,
+                 swa_topk_buffer: torch.Tensor | None, prefix: str = "") -> None:
+        super().__init__()
+        self.n_head = config.index_n_heads
+        self.head_dim = config.index_head_dim
+        self.rope_dim = config.mla_qk_rope_head_dim
+        self.use_fp4_kv = dsa_indexer_uses_fp4(vllm_config)
         if self.use_fp4_kv:
-            pcp_size, dcp_size = prefill_context_parallel_size, decode_context_parallel_size
+            parallel_config = vllm_config.parallel_config
+            pcp_size = parallel_config.prefill_context_parallel_size
+            dcp_size = parallel_config.decode_context_parallel_size
             if pcp_size != 1 or dcp_size != 1:
                 raise NotImplementedError(
                     "ERNIE 5.5 MXFP4 indexer currently requires PCP=DCP=1 "
                     "(prefill_context_parallel_size=1 and decode_context_parallel_size=1). "
                     f"Got PCP={pcp_size}, DCP={dcp_size}.")
-        self.n_head = config.index_n_heads
-        self.head_dim = config.index_head_dim
-        self.rope_dim = config.mla_qk_rope_head_dim
         if (self.n_head, self.head_dim, self.rope_dim) != (64, 128, 64):
             raise NotImplementedError("the indexer kernels take 64 heads x 128 dims with a 64-dim rope")
+        dev = _device_of(vllm_config)
+        self.wq_b = Linear(config.mla_q_lora_rank, self.n_head * self.head_dim, return_bias=True, device=dev)
+        self.wk_weights_proj = Linear(config.hidden_size, self.head_dim + self.n_head, return_bias=True, device=dev)
+        self.k_norm = torch.nn.LayerNorm(self.head_dim, eps=1e-6, device=dev, dtype=torch.float32)
         self.topk = config.index_topk
         self.window = config.sliding_window
-        self.rope_theta = config.rope_theta
+        self.rope_theta = config.mla_rope_parameters["rope_theta"]
         self.max_position = config.max_position_embeddings
-        self.wq_b = wq_b
-        self.wk_weights_proj = wk_weights_proj
-        self.k_norm_weight = k_norm_weight.float().contiguous()
-        self.k_norm_bias = k_norm_bias.float().contiguous()
-        self.k_norm_eps = 1e-6
         self.weights_scale = self.head_dim ** -0.5 * self.n_head ** -0.5
         self.topk_indices_buffer = swa_topk_buffer
         if self.use_fp4_kv:  # 64 packed values + 4 UE8M0 scales = 68 bytes
             k_cache_head_dim = self.head_dim // 2 + self.head_dim // MXFP4_BLOCK_SIZE
         else:  # 128 fp8 + 4-byte fp32 scale = 132 bytes
             k_cache_head_dim = self.head_dim + self.head_dim // INDEXER_QUANT_BLOCK * 4
-        self.k_cache = Ernie5_5IndexerCache(head_dim=k_cache_head_dim, dtype=torch.uint8, prefix=f"{prefix}.k_cache")
+        self.k_cache = Ernie5_5IndexerCache(head_dim=k_cache_head_dim, dtype=torch.uint8, prefix=f"{prefix}.k_cache",
+                                            cache_config=cache_config)
         self.indexer_op = SimpleNamespace(topk_indices_buffer=topk_indices_buffer, topk_tokens=self.topk)
         self._lengths: torch.Tensor | None = None
 
+    @property
+    def k_norm_weight(self) -> torch.Tensor:
+        return self.k_norm.weight.detach()
+
+    @property
+    def k_norm_bias(self) -> torch.Tensor:
+        return self.k_norm.bias.detach()
+
     def _project(self, hidden_states: torch.Tensor, qr: torch.Tensor):
-        q = (qr @ self.wq_b.t()).view(-1, self.n_head, self.head_dim)
-        kw = hidden_states @ self.wk_weights_proj.t()
+        q, _ = self.wq_b(qr)
+        q = q.view(-1, self.n_head, self.head_dim)
+        kw, _ = self.wk_weights_proj(hidden_states)
         k, weights = kw.split([self.head_dim, self.n_head], dim=-1)
         return q, k.contiguous(), weights.contiguous()
 
     def _prep_args(self, device):
-        return (self.k_norm_weight, self.k_norm_bias, self.k_norm_eps,
+        return (self.k_norm_weight.contiguous(), self.k_norm_bias.contiguous(), self.k_norm.eps,
                 rope_cos_sin_table(self.rope_dim, self.rope_theta, self.max_position, device))
 
     def _lengths_buf(self, T: int, device) -> torch.Tensor:
@@ -495,10 +642,10 @@ class Ernie5_5Indexer:
 
     def _topk(self, qa, qb, wf, md: DSAStepMetadata, lengths, positions, merged=None) -> None:
         """Exact top-k of every query row (filter + select, one launch when the
-        filter fits one), in row pieces
-        whose workspace fits _INDEXER_WORKSPACE_BYTES; with ``merged`` the
-        select also writes merge_swa_topk's rows.  ``(qa, qb)`` are the fp8
-        codes and digit planes, or the MXFP4 values and scale words."""
+        filter fits one), in row pieces whose workspace fits
+        _INDEXER_WORKSPACE_BYTES; with ``merged`` the select also writes
+        merge_swa_topk's rows.  ``(qa, qb)`` are the fp8 codes and digit
+        planes, or the MXFP4 values and scale words."""
         T = qa.shape[0]
         kcache = self.k_cache.kv_cache
         out = self.indexer_op.topk_indices_buffer
@@ -541,7 +688,8 @@ class Ernie5_5Indexer:
         self._topk(qa, qb, wf, md, lengths, positions)
         return self.indexer_op.topk_indices_buffer[:T]
 
-    __call__ = forward
+    def load_weights(self, weights) -> set:
+        return _load(self, weights)
 
 
 class Ernie5_5MLAAttention:
@@ -550,14 +698,17 @@ class Ernie5_5MLAAttention:
 
     Holds the impl (sink-capable sparse decode), the bound latent cache
     (``kv_cache``, fp8 pages of 576-byte rows + fp32 scales) and the
-    absorbed-MLA projections split from ``kv_b_proj``: W_UK maps the
-    nope part of q into the 512-d latent space, W_UV maps the decode's
-    latent output to the v heads (plain batched GEMMs)."""
+    absorbed-MLA projections split from ``kv_b_proj`` by
+    ``process_weights_after_loading``: W_UK maps the nope part of q into the
+    512-d latent space, W_UV maps the decode's latent output to the v heads
+    (plain batched GEMMs)."""
 
     def __init__(self, num_heads: int = 64, scale: float = 256 ** -0.5, qk_nope_head_dim: int = 192,
-                 qk_rope_head_dim: int = 64, v_head_dim: int = 256, kv_lora_rank: int = 512,
-                 kv_b_proj: torch.Tensor | None = None, prefix: str = "", sinks: torch.Tensor | None = None,
-                 head_size: int = 576, cache_block_size: int = 64) -> None:
+                 qk_rope_head_dim: int = 64, v_head_dim: int = 256, q_lora_rank: int | None = None,
+                 kv_lora_rank: int = 512, kv_b_proj: Linear | None = None, cache_config=None, quant_config=None,
+                 prefix: str = "", attn_backend=None, use_sparse: bool = True, indexer=None,
+                 topk_indices_buffer=None, sinks: torch.Tensor | None = None, head_size: int = 576,
+                 cache_block_size: int = 64) -> None:
         self.num_heads = num_heads
         self.head_size = head_size
         self.cache_block_size = cache_block_size
@@ -566,21 +717,33 @@ class Ernie5_5MLAAttention:
         self.v_head_dim = v_head_dim
         self.kv_lora_rank = kv_lora_rank
         self.prefix = prefix
+        self.indexer = indexer
+        self.topk_indices_buffer = topk_indices_buffer
+        self.kv_b_proj = kv_b_proj
         self.kv_cache: torch.Tensor | None = None
+        self.W_UK: torch.Tensor | None = None
+        self.W_UV_T: torch.Tensor | None = None
+        cache_dtype = getattr(cache_config, "cache_dtype", "fp8")
         self.impl = None
         if sinks is not None:
-            self.impl = Ernie5_5FlashMLASparseImpl(num_heads, head_size, scale, sinks=sinks)
-        if kv_b_proj is not None:
-            w = kv_b_proj.view(num_heads, qk_nope_head_dim + v_head_dim, kv_lora_rank)
-            self.W_UK = w[:, :qk_nope_head_dim].contiguous()                   # [H, 192, 512]
-            self.W_UV_T = w[:, qk_nope_head_dim:].transpose(1, 2).contiguous()  # [H, 512, 256]
+            self.impl = Ernie5_5FlashMLASparseImpl(num_heads, head_size, scale, kv_cache_dtype=cache_dtype,
+                                                   sinks=sinks)
 
     def get_kv_cache_spec(self, vllm_config) -> KVCacheSpec:
         base = KVCacheSpec(block_size=vllm_config.cache_config.block_size, head_size=self.head_size)
         return _dsa_page_spec(base, vllm_config)
 
+    def process_weights_after_loading(self) -> None:
+        """W_UK [H, 192, 512] and W_UV^T [H, 512, 256] from kv_b_proj."""
+        w = self.kv_b_proj.weight.detach().view(self.num_heads, self.qk_nope_head_dim + self.v_head_dim,
+                                                self.kv_lora_rank)
+        self.W_UK = w[:, : self.qk_nope_head_dim].contiguous()
+        self.W_UV_T = w[:, self.qk_nope_head_dim:].transpose(1, 2).contiguous()
+
     def absorb_q(self, q: torch.Tensor) -> torch.Tensor:
         """q [T, H, 192 + 64] -> [T, H, 512 + 64]: the nope part through W_UK."""
+        if self.W_UK is None:
+            self.process_weights_after_loading()
         T = q.shape[0]
         q_nope = q[..., : self.qk_nope_head_dim].transpose(0, 1).contiguous()  # [H, T, 192]
         q_lat = torch.bmm(q_nope, self.W_UK)                                    # [H, T, 512]
@@ -589,48 +752,104 @@ class Ernie5_5MLAAttention:
 
     def up_proj(self, o_latent: torch.Tensor) -> torch.Tensor:
         """[T, H, 512] -> [T, H * 256] through W_UV."""
+        if self.W_UV_T is None:
+            self.process_weights_after_loading()
         T = o_latent.shape[0]
         o = torch.bmm(o_latent.transpose(0, 1).contiguous(), self.W_UV_T)  # [H, T, 256]
         return o.transpose(0, 1).reshape(T, self.num_heads * self.v_head_dim)
 
 
-class Ernie5_5DSAAttention:
-    """The KV-cache part of the MLA + DSA layer (attention.py:1059-1226).
+class Ernie5_5DSAAttention(torch.nn.Module):
+    """MLA layer with a DSA indexer, attention sink, VHA and an output gate
+    (attention.py:1059-1226), constructed as the reference's
+    ``(vllm_config, prefix, topk_indices_buffer, swa_topk_buffer)``.
 
-    ``_indexer_and_attn(hidden_states, q_c, positions, q, kv_c_normed, k_pe,
-    out)`` keeps the reference's signature and order -- indexer (K insert,
-    scores, top-k), window merge, latent append, sparse MLA decode with the
-    sink -- with the decode step's launches fused: one prologue (indexer
-    prep, K insert, latent append, q quant, lengths), the filter, the select
-    (top-k and merged rows), the decode (block-table conversion in-kernel).
-    The projections around it (fused_qkv_a_proj, norms, rope, q_b_proj,
-    o_gate, VHA, wo_b) are the layer's plain GEMMs and stay outside this
-    path; the absorbed-MLA W_UK / W_UV products run as batched GEMMs."""
+    ``forward(positions, hidden_states, llama_4_scaling=None)`` follows the
+    reference: fused_qkv_a_proj, q_a_layernorm, o_gate, q_b_proj,
+    kv_a_layernorm and the interleaved RoPE of the q / k rope parts (torch
+    ops around the path), then ``_indexer_and_attn`` on the HIP library,
+    then VHA and the gated ``wo_b``.  ``_indexer_and_attn(hidden_states,
+    q_c, positions, q, kv_c_normed, k_pe, out)`` keeps the reference's
+    signature and order -- indexer (K insert, scores, top-k), window merge,
+    latent append, sparse MLA decode with the sink -- with the decode step's
+    launches fused: one prologue (indexer prep, K insert, latent append, q
+    quant, lengths), the top-k (filter, exact scoring, select, merged rows
+    in one launch), the decode (block-table conversion in-kernel).  The
+    absorbed-MLA W_UK / W_UV products run as batched GEMMs.  With
+    ``fp8_o_proj`` the gated ``wo_b`` input is quantized by
+    ``sigmoid_mul_quant_fp8`` (the reference's fused DeepGEMM input) and
+    dequantized for the bf16 GEMM."""
 
-    def __init__(self, config, prefix: str, topk_indices_buffer: torch.Tensor | None = None,
-                 swa_topk_buffer: torch.Tensor | None = None, *, params: dict, kv_cache_dtype: str = "fp8",
-                 use_fp4_kv: bool = False) -> None:
+    def __init__(self, vllm_config, prefix: str, topk_indices_buffer: torch.Tensor | None = None,
+                 swa_topk_buffer: torch.Tensor | None = None, **kwargs) -> None:
+        super().__init__()
+        config = vllm_config.model_config.hf_config
         _check_attn_tp(config)
-        self.num_heads = config.hybrid_mla_num_attention_heads
+        cache_config = copy.copy(vllm_config.cache_config)
+        dev = _device_of(vllm_config)
+        self.prefix = prefix
+        self.num_heads = config.mla_num_heads
         self.num_local_heads = self.num_heads
-        self.kv_lora_rank = config.hybrid_mla_kv_lora_rank
-        self.qk_nope_head_dim = config.hybrid_mla_qk_nope_head_dim
-        self.qk_rope_head_dim = config.hybrid_mla_qk_rope_head_dim
+        self.q_lora_rank = config.mla_q_lora_rank
+        self.kv_lora_rank = config.mla_kv_lora_rank
+        self.qk_nope_head_dim = config.mla_qk_nope_head_dim
+        self.qk_rope_head_dim = config.mla_qk_rope_head_dim
         self.qk_head_dim = self.qk_nope_head_dim + self.qk_rope_head_dim
-        self.v_head_dim = config.hybrid_mla_v_head_dim
+        self.v_head_dim = config.mla_v_head_dim
         self.window = config.sliding_window
-        _check_sink_backend(self.kv_lora_rank + self.qk_rope_head_dim, kv_cache_dtype)
-        if not kv_cache_dtype.startswith("fp8"):
-            raise NotImplementedError("the DSA latent append writes the fp8 page rows; use an fp8 KV cache")
-        self.attn_sink = params["attn_sink"].float().contiguous()
-        self.indexer = Ernie5_5Indexer(config, topk_indices_buffer, swa_topk_buffer, prefix=f"{prefix}.indexer",
-                                       wq_b=params["indexer.wq_b"], wk_weights_proj=params["indexer.wk_weights_proj"],
-                                       k_norm_weight=params["indexer.k_norm.weight"],
-                                       k_norm_bias=params["indexer.k_norm.bias"], use_fp4_kv=use_fp4_kv)
+        self.fp8_o_proj = bool(kwargs.get("fp8_o_proj", False))
+        self.fused_qkv_a_proj = Linear(config.hidden_size, self.q_lora_rank + self.kv_lora_rank + self.qk_rope_head_dim,
+                                       return_bias=True, device=dev)
+        self.q_a_layernorm = RMSNorm(self.q_lora_rank, eps=config.rms_norm_eps, device=dev)
+        self.q_b_proj = Linear(self.q_lora_rank, self.num_heads * self.qk_head_dim, return_bias=True, device=dev)
+        self.kv_a_layernorm = RMSNorm(self.kv_lora_rank, eps=config.rms_norm_eps, device=dev)
+        self.kv_b_proj = Linear(self.kv_lora_rank, self.num_heads * (self.qk_nope_head_dim + self.v_head_dim),
+                                return_bias=True, device=dev)
+        self.wo_b = Linear(self.num_heads * self.v_head_dim, config.hidden_size, device=dev)
+        self.o_gate = Linear(self.q_lora_rank, self.num_heads * self.v_head_dim, device=dev)
+        self.vha = VHAPostMix(self.num_heads, device=dev)
+        self.rotary_emb = InterleavedRotaryEmbedding(self.qk_rope_head_dim, config.max_position_embeddings,
+                                                     config.mla_rope_parameters, dev)
+        self.attn_sink = torch.nn.Parameter(torch.zeros(self.num_local_heads, dtype=torch.float32, device=dev),
+                                            requires_grad=False)
+        _check_sink_backend(self.kv_lora_rank + self.qk_rope_head_dim, cache_config.cache_dtype)
+        if not cache_config.cache_dtype.startswith("fp8"):
+            raise NotImplementedError("the DSA latent append writes fp8 page rows; use an fp8 KV cache")
+        self.indexer = Ernie5_5Indexer(vllm_config, config, None, cache_config, topk_indices_buffer, swa_topk_buffer,
+                                       prefix=f"{prefix}.indexer")
         self.mla_attn = Ernie5_5MLAAttention(
             num_heads=self.num_local_heads, scale=self.qk_head_dim ** -0.5, qk_nope_head_dim=self.qk_nope_head_dim,
-            qk_rope_head_dim=self.qk_rope_head_dim, v_head_dim=self.v_head_dim, kv_lora_rank=self.kv_lora_rank,
-            kv_b_proj=params["kv_b_proj"], prefix=f"{prefix}.attn", sinks=self.attn_sink)
+            qk_rope_head_dim=self.qk_rope_head_dim, v_head_dim=self.v_head_dim, q_lora_rank=self.q_lora_rank,
+            kv_lora_rank=self.kv_lora_rank, kv_b_proj=self.kv_b_proj, cache_config=cache_config,
+            prefix=f"{prefix}.attn", attn_backend=Ernie5_5FlashMLASparseBackend, use_sparse=True,
+            indexer=self.indexer, topk_indices_buffer=swa_topk_buffer, sinks=self.attn_sink)
+
+    def load_weights(self, weights) -> set:
+        loaded = _load(self, weights)
+        self.mla_attn.process_weights_after_loading()
+        self.vha.fold()
+        return loaded
+
+    def forward(self, positions: torch.Tensor, hidden_states: torch.Tensor,
+                llama_4_scaling: torch.Tensor | None = None) -> torch.Tensor:
+        num_tokens = hidden_states.shape[0]
+        q_c, kv_lora = self.fused_qkv_a_proj(hidden_states)[0].split(
+            [self.q_lora_rank, self.kv_lora_rank + self.qk_rope_head_dim], dim=-1)
+        q_c = self.q_a_layernorm(q_c)
+        gate = self.o_gate(q_c)
+        q = self.q_b_proj(q_c)[0].view(-1, self.num_local_heads, self.qk_head_dim)
+        kv_c, k_pe = kv_lora.split([self.kv_lora_rank, self.qk_rope_head_dim], -1)
+        kv_c_normed = self.kv_a_layernorm(kv_c)
+        q[..., self.qk_nope_head_dim:], k_pe = self.rotary_emb(positions, q[..., self.qk_nope_head_dim:],
+                                                               k_pe.unsqueeze(1))
+        attn_out = torch.empty((num_tokens, self.num_local_heads * self.v_head_dim), dtype=hidden_states.dtype,
+                               device=hidden_states.device)
+        self._indexer_and_attn(hidden_states, q_c, positions, q, kv_c_normed, k_pe, attn_out)
+        o = self.vha(attn_out.view(num_tokens, self.num_local_heads, self.v_head_dim))
+        if self.fp8_o_proj:
+            data, scale = sigmoid_mul_quant_fp8(o.flatten(1).contiguous(), gate.contiguous())
+            return self.wo_b(dequant_sigmoid_mul(data, scale).to(hidden_states.dtype))
+        return self.wo_b(o.flatten(1) * torch.sigmoid(gate))
 
     def _indexer_and_attn(self, hidden_states: torch.Tensor, q_c: torch.Tensor, positions: torch.Tensor,
                           q: torch.Tensor, kv_c_normed: torch.Tensor, k_pe: torch.Tensor, out: torch.Tensor) -> None:
@@ -660,45 +879,163 @@ class Ernie5_5DSAAttention:
         out.copy_(self.mla_attn.up_proj(o_latent[:, 0]))
 
 
-class Ernie5_5HCAAttentionMixin:
-    """The KV-cache half of the HCA layer's forward (attention.py:471-539):
-    the cache write and the sparse attention into ``o_padded`` that upstream
-    ``DeepseekV4Attention._prepare_and_attn_fn`` performs.
+class _Compressor(torch.nn.Module):
+    """The HCA layer's compressor parameters (``compressor.*``): the fused
+    ``fused_wkv_wgate`` projection of the hidden states to kv || score
+    (model.py:684-685), the position embedding ``ape [128, D]`` added to the
+    score, and the RMSNorm weight of the compressed row."""
 
-    ``_prepare_and_attn_fn(q, kv, kv_score, positions, o_padded)`` takes the
-    layer's projected, roped operands -- q ``[T, heads, D]``, the latent
-    rows kv ``[T, D]`` and the compressor input kv_score ``[T, 2D]`` (the
-    ``compressor.fused_wkv_wgate`` output, model.py:684-685) -- and on the
-    HIP library appends kv (fp8 rows, window ring, compressor state ring),
-    compresses every 128-token span that completes, builds each query row's
-    index row (its compressed entries, then its window) and runs the
-    64-head sparse decode with the sink into ``o_padded[:, :heads]``.
-    VHA, inverse RoPE and the output projections stay outside this path."""
+    def __init__(self, hidden_size: int, dim: int, eps: float, device) -> None:
+        super().__init__()
+        self.fused_wkv_wgate = Linear(hidden_size, 2 * dim, device=device)
+        self.ape = torch.nn.Parameter(torch.zeros(128, dim, dtype=torch.float32, device=device), requires_grad=False)
+        self.norm = RMSNorm(dim, eps=eps, device=device, dtype=torch.float32)
 
-    def __init__(self, config, prefix: str, *, params: dict, ring: int = 192, padded_heads: int = 64,
-                 compress_cos_sin: torch.Tensor, scale: float | None = None) -> None:
+
+class Ernie5_5HCAAttentionMixin(torch.nn.Module):
+    """The HCA attention layer (attention.py:410-539), constructed as the
+    reference's ``(vllm_config, prefix, **kwargs)``.
+
+    The reference subclasses upstream ``DeepseekV4Attention`` (absent: vLLM
+    is not in this tree); this class restates the parts its forward calls,
+    with the config's shapes: ``_run_parallel_input_projections`` (the fused
+    ``fused_wqa_wkv`` projection of the hidden states to the q low-rank
+    input and the latent row, and ``compressor.fused_wkv_wgate`` to the
+    compressor input), ``_split_qkv_and_norm`` (RMSNorms of both), and
+    ``_prepare_and_attn_fn(hidden_states, qr, kv, qr_scale, kv_score,
+    indexer_kv_score, indexer_weights, positions, o_padded)`` -- upstream's
+    nine-argument call (:495-505): ``wq_b``, the interleaved RoPE of the q
+    and latent rope parts at the token positions, then on the HIP library
+    the cache write (latent rows, window ring, compressor state ring, every
+    completed 128-token span compressed), each query row's index row (its
+    compressed entries, then its window) and the sparse decode with the
+    sink into ``o_padded[:, :heads]`` (``_cache_and_attn``).  ``forward
+    (positions, hidden_states, llama_4_scaling=None)`` is the reference's:
+    projections, the KV path, the ``o_gate`` gate, VHA, and the output
+    projection (inverse RoPE of the output's rope part, the grouped
+    ``wo_a``, the gated ``wo_b``; with ``fp8_o_proj`` VHA + inverse RoPE +
+    fp8 quant run as ``vha_inv_rope_fp8_quant`` and the gated ``wo_b`` input
+    as ``sigmoid_mul_quant_fp8``, dequantized for the bf16 GEMMs).  The KV
+    cache is fp8 pages of per-token-scaled rows (``Ernie5_5HCAFlashMLAAttention``)
+    or bf16 rows (``Ernie5_5HCAFlashInferAttention``)."""
+
+    kv_cache_dtype = "fp8"
+
+    def __init__(self, vllm_config, prefix: str, **kwargs) -> None:
+        config = vllm_config.model_config.hf_config
         _check_attn_tp(config)
+        super().__init__()
+        dev = _device_of(vllm_config)
         self.prefix = prefix
-        self.n_local_heads = config.num_attention_heads
-        self.padded_heads = max(padded_heads, self.n_local_heads)
+        self.n_heads = config.num_attention_heads
+        self.n_local_heads = self.n_heads
+        self.padded_heads = max(int(kwargs.get("padded_heads", 64)), self.n_local_heads)
         self.head_dim = config.head_dim
+        self.nope_head_dim = config.qk_nope_head_dim
+        self.rope_head_dim = config.qk_rope_head_dim
+        self.q_lora_rank = config.q_lora_rank
+        self.n_groups = config.o_groups
+        self.n_local_groups = self.n_groups
+        self.o_lora_rank = config.o_lora_rank
         self.window = config.sliding_window
-        self.ring = ring
-        if ring % DSA_BLOCK_SIZE or ring < self.window:
+        self.ring = int(kwargs.get("ring", 192))
+        if self.ring % DSA_BLOCK_SIZE or self.ring < self.window:
             raise ValueError("the window ring must be whole 64-row pages holding at least the window")
-        self.softmax_scale = self.head_dim ** -0.5 if scale is None else scale
-        self.attn_sink = params["attn_sink"].float().contiguous()
-        self.ape = params["compressor.ape"].float().contiguous()
-        self.norm_w = params["compressor.norm.weight"].float().contiguous()
+        self.softmax_scale = kwargs.get("scale") or self.head_dim ** -0.5
         self.norm_eps = config.rms_norm_eps
-        self.compress_cos_sin = compress_cos_sin
-        self.kv_cache: torch.Tensor | None = None     # fp8 pages [num_pages, 64 * (D + 4)]
+        self.fp8_o_proj = bool(kwargs.get("fp8_o_proj", False))
+        self.fused_wqa_wkv = Linear(config.hidden_size, self.q_lora_rank + self.head_dim, device=dev)
+        self.q_norm = RMSNorm(self.q_lora_rank, eps=config.rms_norm_eps, device=dev)
+        self.kv_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps, device=dev)
+        self.wq_b = Linear(self.q_lora_rank, self.n_heads * self.head_dim, device=dev)
+        self.compressor = _Compressor(config.hidden_size, self.head_dim, config.rms_norm_eps, dev)
+        hpg = self.n_heads // self.n_groups
+        self.wo_a = torch.nn.Parameter(torch.empty(self.n_groups, self.o_lora_rank, hpg * self.head_dim,
+                                                   dtype=torch.bfloat16, device=dev), requires_grad=False)
+        self.wo_b = Linear(self.n_groups * self.o_lora_rank, config.hidden_size, device=dev)
+        self.o_gate = Linear(self.q_lora_rank, self.n_groups * self.o_lora_rank, device=dev)
+        self.vha = VHAPostMix(self.n_heads, device=dev)
+        self.attn_sink = torch.nn.Parameter(torch.zeros(self.n_heads, dtype=torch.float32, device=dev),
+                                            requires_grad=False)
+        self.indexer = None
+        if kwargs.get("rope_cos_sin") is not None:  # a given cos | sin table (e.g. YaRN) for q / kv
+            self.rotary_emb = InterleavedRotaryEmbedding.from_table(kwargs["rope_cos_sin"])
+        else:
+            self.rotary_emb = InterleavedRotaryEmbedding(self.rope_head_dim, config.max_position_embeddings,
+                                                         config.rope_parameters, dev)
+        cs = kwargs.get("compress_cos_sin")
+        if cs is None:  # the compressed entry j rotated at position 128 j, compress_rope_theta
+            spans = config.max_position_embeddings // 128 + 1
+            cs = rope_cos_sin_table(self.rope_head_dim, config.compress_rope_theta, spans * 128, dev)[::128]
+        self.compress_cos_sin = cs.contiguous()
+        self.kv_cache: torch.Tensor | None = None     # fp8 pages [num_pages, 64 * (D + 4)] or bf16 rows [N, D]
         self.state_cache: torch.Tensor | None = None  # bf16 [num_state, 256, 2 D]
         self._idx: torch.Tensor | None = None
         self._ws: torch.Tensor | None = None
         self._write_ws: torch.Tensor | None = None
         self._write_spans = 0
 
+    # --- views of the compressor parameters the write kernels read
+    @property
+    def ape(self) -> torch.Tensor:
+        return self.compressor.ape.detach()
+
+    @property
+    def norm_w(self) -> torch.Tensor:
+        return self.compressor.norm.weight.detach()
+
+    def load_weights(self, weights) -> set:
+        loaded = _load(self, weights)
+        self.vha.fold()
+        return loaded
+
+    # --- the projections around the KV path
+    def _run_parallel_input_projections(self, hidden_states: torch.Tensor):
+        qr_kv = self.fused_wqa_wkv(hidden_states)
+        kv_score = self.compressor.fused_wkv_wgate(hidden_states)
+        return qr_kv, kv_score, None, None
+
+    def _split_qkv_and_norm(self, qr_kv: torch.Tensor):
+        qr, kv = qr_kv.split([self.q_lora_rank, self.head_dim], dim=-1)
+        return self.q_norm(qr), None, self.kv_norm(kv)
+
+    def _gate(self, qr: torch.Tensor) -> torch.Tensor:
+        return self.o_gate(qr) if self.fp8_o_proj else torch.sigmoid(self.o_gate(qr))
+
+    def forward(self, positions: torch.Tensor, hidden_states: torch.Tensor,
+                llama_4_scaling: torch.Tensor | None = None) -> torch.Tensor:
+        num_tokens = hidden_states.shape[0]
+        o_padded = torch.empty((num_tokens, self.padded_heads, self.head_dim), dtype=hidden_states.dtype,
+                               device=hidden_states.device)
+        qr_kv, kv_score, indexer_kv_score, indexer_weights = self._run_parallel_input_projections(hidden_states)
+        qr, qr_scale, kv = self._split_qkv_and_norm(qr_kv)
+        self._prepare_and_attn_fn(hidden_states, qr, kv, qr_scale, kv_score, indexer_kv_score, indexer_weights,
+                                  positions, o_padded)
+        gate = self._gate(qr)
+        o = o_padded[:, : self.n_local_heads, :]
+        return self._o_proj(o, positions, gate)
+
+    def _o_proj(self, o: torch.Tensor, positions: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        """VHA, inverse RoPE of the rope part, grouped wo_a, gated wo_b."""
+        T = o.shape[0]
+        G = self.n_local_groups
+        if self.fp8_o_proj:
+            data, scale = ops.vha_inv_rope_fp8_quant(o, self.vha.m, positions, self.rotary_emb.cos_sin_cache, G,
+                                                     self.nope_head_dim, self.rope_head_dim)
+            og = dequant_vha(data, scale).to(o.dtype)  # [T, G, hpg * D]
+        else:
+            o = self.vha(o)
+            o = torch.cat([o[..., : self.nope_head_dim],
+                           self.rotary_emb.rotate(positions, o[..., self.nope_head_dim:], inverse=True)], dim=-1)
+            og = o.reshape(T, G, -1)
+        z = torch.bmm(og.transpose(0, 1).contiguous(), self.wo_a.transpose(1, 2).contiguous())  # [G, T, r]
+        z = z.transpose(0, 1).reshape(T, G * self.o_lora_rank)
+        if self.fp8_o_proj:
+            data, scale = ops.sigmoid_mul_quant_fp8(z.contiguous(), gate.contiguous())
+            return self.wo_b(dequant_sigmoid_mul(data, scale).to(o.dtype))
+        return self.wo_b(z * gate)
+
+    # --- the KV path
     def _write_workspace(self, num_seqs: int, max_query_len: int, D: int, device) -> torch.Tensor:
         """The cache write's workspace, grown to the most span slots a call
         has had (one per sequence and 128 rows of its longest query, plus
@@ -710,7 +1047,7 @@ class Ernie5_5HCAAttentionMixin:
             self._write_ws = ops.hca_write_workspace(self._write_spans, D, device)
         return self._write_ws
 
-    def _buffers(self, T: int, width: int, device):
+    def _decode_buffers(self, T: int, width: int, device):
         if self._idx is None or self._idx.shape[0] < T or self._idx.shape[1] < width:
             self._idx = torch.empty((T, width), dtype=torch.int32, device=device)
             self._lens = torch.empty(T, dtype=torch.int32, device=device)
@@ -718,16 +1055,38 @@ class Ernie5_5HCAAttentionMixin:
             self._ws = ops.decode_workspace(T, self.padded_heads, width, device)
         return self._idx[:T, :width], self._lens[:T], self._lse[:T], self._ws
 
-    def _prepare_and_attn_fn(self, q: torch.Tensor, kv: torch.Tensor, kv_score: torch.Tensor,
+    def _prepare_and_attn_fn(self, hidden_states: torch.Tensor, qr: torch.Tensor, kv: torch.Tensor,
+                             qr_scale: torch.Tensor | None, kv_score: torch.Tensor,
+                             indexer_kv_score: torch.Tensor | None, indexer_weights: torch.Tensor | None,
                              positions: torch.Tensor, o_padded: torch.Tensor) -> None:
+        """Upstream's call (attention.py:495-505): q from ``wq_b(qr)``, the
+        interleaved RoPE of q's and kv's rope parts at ``positions``, then
+        ``_cache_and_attn``.  HCA layers have no indexer, so
+        ``indexer_kv_score`` / ``indexer_weights`` are None; ``qr_scale``
+        (a quantized-qr scale) is None for bf16 qr."""
+        T = qr.shape[0]
+        q = self.wq_b(qr).view(T, self.n_local_heads, self.head_dim)
+        nope = self.nope_head_dim
+        q = torch.cat([q[..., :nope], self.rotary_emb.rotate(positions, q[..., nope:])], dim=-1)
+        kv = torch.cat([kv[..., :nope], self.rotary_emb.rotate(positions, kv[..., nope:])], dim=-1)
+        self._cache_and_attn(q, kv.contiguous(), kv_score.contiguous(), positions, o_padded)
+
+    def _cache_and_attn(self, q: torch.Tensor, kv: torch.Tensor, kv_score: torch.Tensor, positions: torch.Tensor,
+                        o_padded: torch.Tensor) -> None:
+        """The HIP part of the layer: q ``[T, heads, D]``, the latent rows kv
+        ``[T, D]`` and the compressor input kv_score ``[T, 2D]``; appends kv
+        (pool rows, window ring, compressor state ring), compresses every
+        128-token span that completes, builds each query row's index row
+        and runs the sparse decode with the sink into ``o_padded[:, :heads]``."""
         md: HCAStepMetadata = get_forward_context().attn_metadata[self.prefix]
         T, H, D = q.shape
+        bf16_cache = self.kv_cache.dtype == torch.bfloat16
         # A request with more than ring - window rows in the call would
         # overwrite ring rows that its own first rows' windows still read:
         # such calls update the ring after the decode.
         late_ring = md.max_query_len > self.ring - self.window
         width = md.max_seq_len // 128 + self.window
-        idx, lens, lse, ws = self._buffers(T, width, q.device)
+        idx, lens, lse, ws = self._decode_buffers(T, width, q.device)
         write_ws = self._write_workspace(md.query_start_loc.numel() - 1, md.max_query_len, D, q.device)
         if late_ring:
             ops.hca_write(kv, kv_score, md.slot_mapping, positions, md.token_seq, md.query_start_loc,
@@ -745,11 +1104,11 @@ class Ernie5_5HCAAttentionMixin:
             qp = q.new_zeros((T, self.padded_heads, D))
             qp[:, :H] = q
             q = qp
-        sinks = self.attn_sink
+        sinks = self.attn_sink.detach().float()
         if sinks.numel() < self.padded_heads:
             sinks = torch.cat([sinks, sinks.new_full((self.padded_heads - sinks.numel(),), float("-inf"))])
-        ops.sparse_mla_decode(q, self.kv_cache, idx, self.softmax_scale, o_padded, lse, sinks=sinks, lengths=lens,
-                              workspace=ws)
+        ops.sparse_mla_decode(q, self.kv_cache, idx, self.softmax_scale, o_padded, lse, sinks=sinks.contiguous(),
+                              lengths=lens, cache_bf16=bf16_cache, workspace=ws)
         if late_ring:  # the window ring rows only (pool rows skipped, state ring already written)
             skip = torch.full((T,), -1, dtype=torch.int64, device=q.device)
             ops.hca_append(kv, None, skip, positions, md.token_seq, md.query_start_loc, self.kv_cache, md.ring_pages,
@@ -771,15 +1130,17 @@ class QuantizedActivation:
     quant_key: str = "fp8_dynamic_128_sym"
 
 
-class VHAPostMix:
+class VHAPostMix(torch.nn.Module):
     """Head mixing ``o[h] <- sum_g m[h, g] o[g]`` with ``m = I + V U^T``
     (attention.py:120-157, TP = 1): a plain batched product outside this
     path; ``m`` is what vha_inv_rope_fp8_quant fuses."""
 
     def __init__(self, num_heads: int, rank: int = VHA_RANK, device=None, dtype=torch.bfloat16) -> None:
-        self.U = torch.zeros(num_heads, rank, dtype=dtype, device=device)
-        self.V = torch.zeros(num_heads, rank, dtype=dtype, device=device)
-        self.m = torch.eye(num_heads, dtype=dtype, device=device)
+        super().__init__()
+        self.tp_size = 1
+        self.U = torch.nn.Parameter(torch.zeros(num_heads, rank, dtype=dtype, device=device), requires_grad=False)
+        self.V = torch.nn.Parameter(torch.zeros(num_heads, rank, dtype=dtype, device=device), requires_grad=False)
+        self.register_buffer("m", torch.eye(num_heads, dtype=dtype, device=device), persistent=False)
 
     def fold(self) -> None:
         eye = torch.eye(self.U.shape[0], dtype=self.U.dtype, device=self.U.device)
@@ -787,8 +1148,6 @@ class VHAPostMix:
 
     def forward(self, o: torch.Tensor) -> torch.Tensor:
         return torch.matmul(self.m, o)
-
-    __call__ = forward
 
 
 def vha_inv_rope_fp8_quant(o: torch.Tensor, mix: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor,
@@ -807,19 +1166,17 @@ def sigmoid_mul_quant_fp8(x: torch.Tensor, gate: torch.Tensor) -> tuple[torch.Te
 
 
 # --------------------------------------------------------------------------- HCA layer class choice
-class Ernie5_5HCAFlashInferAttention:
-    """HCA layer on a bf16 KV row (attention.py:542-545).  The write path
-    here stores fp8 page rows, so this class is named for the choice only
-    and refuses to run."""
+class Ernie5_5HCAFlashInferAttention(Ernie5_5HCAAttentionMixin):
+    """HCA layer on a bf16 KV row (attention.py:542-545): the cache is bf16
+    rows (64 a page); the write stores the latent rows as given and the
+    compressed rows rounded to bf16, the decode reads bf16 rows."""
 
     kv_cache_dtype = "bfloat16"
 
-    def __init__(self, *args, **kwargs) -> None:
-        raise NotImplementedError("bf16 HCA cache rows are not built; select an fp8 KV cache")
-
 
 class Ernie5_5HCAFlashMLAAttention(Ernie5_5HCAAttentionMixin):
-    """HCA layer on an fp8 KV row (attention.py:548-551)."""
+    """HCA layer on an fp8 KV row (attention.py:548-551): fp8 pages of
+    per-token-scaled rows (580 bytes at D = 576, 516 at D = 512)."""
 
     kv_cache_dtype = "fp8"
 
@@ -841,16 +1198,43 @@ def simple_vllm_config(head_dim=512, mla_kv_lora_rank=512, mla_qk_rope_head_dim=
 
 def ernie5_5_config(**overrides) -> SimpleNamespace:
     """The Ernie5_5Config fields this path reads, at their defaults
-    (src/vllm_ernie/models/ernie5_5/config.py:13-62)."""
-    cfg = dict(hidden_size=4096, num_attention_heads=64, head_dim=512, q_lora_rank=1024, o_groups=8,
-               sliding_window=128, hybrid_mla_num_attention_heads=64, hybrid_mla_q_lora_rank=1024,
-               hybrid_mla_kv_lora_rank=512, hybrid_mla_qk_nope_head_dim=192, hybrid_mla_qk_rope_head_dim=64,
-               hybrid_mla_v_head_dim=256, index_n_heads=64, index_head_dim=128, index_topk=2048,
-               max_position_embeddings=200192, rope_theta=2500000.0, compress_rope_theta=160000.0,
-               rms_norm_eps=1e-6)
+    (src/vllm_ernie/models/ernie5_5/config.py:13-62, 154-189)."""
+    cfg = dict(hidden_size=4096, num_attention_heads=64, head_dim=512, q_lora_rank=1024, kv_lora_rank=512,
+               qk_nope_head_dim=448, qk_rope_head_dim=64, o_groups=8, o_lora_rank=1024, sliding_window=128,
+               hybrid_mla_num_attention_heads=64, hybrid_mla_q_lora_rank=1024, hybrid_mla_kv_lora_rank=512,
+               hybrid_mla_qk_nope_head_dim=192, hybrid_mla_qk_rope_head_dim=64, hybrid_mla_v_head_dim=256,
+               index_n_heads=64, index_head_dim=128, index_topk=2048, max_position_embeddings=200192,
+               rope_theta=2500000.0, compress_rope_theta=160000.0, rms_norm_eps=1e-6, rope_parameters=None)
     cfg.update(overrides)
     ns = SimpleNamespace(**cfg)
-    ns.mla_qk_rope_head_dim = ns.hybrid_mla_qk_rope_head_dim
-    ns.mla_kv_lora_rank = ns.hybrid_mla_kv_lora_rank
+    if ns.rope_parameters is None:
+        ns.rope_parameters = {"rope_type": "default", "rope_theta": ns.rope_theta}
+    ns.mla_num_heads = ns.hybrid_mla_num_attention_heads
     ns.mla_q_lora_rank = ns.hybrid_mla_q_lora_rank
+    ns.mla_kv_lora_rank = ns.hybrid_mla_kv_lora_rank
+    ns.mla_qk_nope_head_dim = ns.hybrid_mla_qk_nope_head_dim
+    ns.mla_qk_rope_head_dim = ns.hybrid_mla_qk_rope_head_dim
+    ns.mla_v_head_dim = ns.hybrid_mla_v_head_dim
+    ns.mla_rope_parameters = {"rope_type": "default", "rope_theta": ns.rope_theta}
     return ns
+
+
+def ernie5_5_vllm_config(hf_config=None, cache_dtype: str = "fp8", block_size: int = 64,
+                         use_fp4_indexer_cache: bool = False, device=None, prefill_context_parallel_size: int = 1,
+                         decode_context_parallel_size: int = 1, max_model_len: int | None = None) -> SimpleNamespace:
+    """Stand-in for vLLM's VllmConfig with the fields the layers read:
+    ``model_config.hf_config`` (``ernie5_5_config()`` by default),
+    ``cache_config`` (block size, cache dtype), ``quant_config`` (None: bf16
+    weights), ``parallel_config`` (context-parallel sizes; TP = 1),
+    ``attention_config`` (the MXFP4 indexer-cache flag) and the device."""
+    hf = hf_config if hf_config is not None else ernie5_5_config()
+    return SimpleNamespace(
+        model_config=SimpleNamespace(hf_config=hf, max_model_len=max_model_len or hf.max_position_embeddings),
+        cache_config=SimpleNamespace(block_size=block_size, cache_dtype=cache_dtype),
+        quant_config=None,
+        parallel_config=SimpleNamespace(prefill_context_parallel_size=prefill_context_parallel_size,
+                                        decode_context_parallel_size=decode_context_parallel_size,
+                                        tensor_parallel_size=1),
+        attention_config=SimpleNamespace(use_fp4_indexer_cache=use_fp4_indexer_cache, sparse_mla_force_mqa=True),
+        device_config=SimpleNamespace(device=device),
+    )

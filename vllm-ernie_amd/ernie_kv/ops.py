@@ -133,10 +133,15 @@ def hca_append(
     _need(token_seq.dtype == torch.int32 and qsl.dtype == torch.int32, "token_seq/qsl int32")
     if ring_pages is not None:
         _need(ring_pages.dtype == torch.int32 and ring_pages.stride(1) == 1, "ring_pages int32 [B, R/64]")
+    if pool.dtype == torch.bfloat16:  # bf16 rows: the flat [-1, D] view, 64 rows a page
+        _need(pool.is_contiguous() and pool.numel() % (PAGE_TOKENS * D) == 0, "bf16 pool: contiguous rows of D")
+        name, page_stride, num_pages = "ekv_hca_append_bf16", PAGE_TOKENS * D * 2, pool.numel() // (PAGE_TOKENS * D)
+    else:
+        name, page_stride, num_pages = "ekv_hca_append", _rs(pool), pool.shape[0]
     _lib.call(
-        "ekv_hca_append", latent.data_ptr(), _rs(latent), _ptr(kv_score),
+        name, latent.data_ptr(), _rs(latent), _ptr(kv_score),
         0 if kv_score is None else _rs(kv_score), T, D, slot_mapping.data_ptr(), positions.data_ptr(),
-        token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1, pool.data_ptr(), _rs(pool), pool.shape[0],
+        token_seq.data_ptr(), qsl.data_ptr(), qsl.numel() - 1, pool.data_ptr(), page_stride, num_pages,
         _ptr(ring_pages), 0 if ring_pages is None else _rs(ring_pages), int(ring), _ptr(state),
         _ptr(state_slot), 0 if state is None else state.shape[0], _stream(),
     )
