@@ -76,17 +76,63 @@ def parse():
     return p.parse_args()
 
 
-def traffic_of(workload: str, kernel: str):
-    """HBM bytes per launch of `kernel` on `workload` from the committed
-    counter summary, or None."""
+def csrc_sha16() -> str:
+    """Hash of the library's kernel sources (names and bytes, sorted): the
+    key a committed counter reading must carry to describe this build."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in sorted((ROOT / "vllm-ernie_amd" / "csrc").iterdir()):
+        if p.is_file():
+            h.update(p.name.encode() + b"\0" + p.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def _counter_record(workload: str, kernel: str):
+    """The committed counter record of `kernel` on `workload`, or None when
+    the file holds none or was measured on other kernel sources (its
+    csrc_sha16 differs from this tree's)."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None
-    rec = data.get("workloads", {}).get(workload)
-    if not rec or rec.get("kernel") != kernel:
+    if data.get("csrc_sha16") != csrc_sha16():
         return None
-    return rec.get("bytes")
+    return data.get("workloads", {}).get(workload, {}).get(kernel)
+
+
+def traffic_of(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    counter summary (rocprofv3 FETCH_SIZE / WRITE_SIZE), or None."""
+    rec = _counter_record(workload, kernel)
+    return None if rec is None else rec.get("bytes")
+
+
+def mfma_report(workload: str, kernel: str, ms):
+    """MFMA utilisation of `kernel` from the committed counters: the busy
+    fraction of its matrix cores and, with the kernel's measured time `ms`,
+    the rate of the ops it issued against the dense peak of their type."""
+    m = mfma_of(workload, kernel)
+    if m is None:
+        return None
+    out = {"busy_frac": m.get("busy_frac"), "ops_per_launch": m.get("ops"),
+           "source": f"{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, "
+                     "SQ_INSTS_VALU_MFMA_MOPS_*)"}
+    peaks = {"F8": FP8_PEAK_TFLOPS, "I8": 5000.0, "BF16": BF16_PEAK_TFLOPS}
+    if ms:
+        out["rates"] = {k: {"tops": round(v / (ms * 1e-3) / 1e12, 1),
+                            "frac": round(v / (ms * 1e-3) / 1e12 / peaks[k], 4)}
+                        for k, v in (m.get("ops") or {}).items() if k in peaks and v}
+    return out
+
+
+def mfma_of(workload: str, kernel: str):
+    """The committed MFMA counters of `kernel` on `workload`: the fraction of
+    the dispatch's active cycles the SIMDs' matrix cores were busy
+    (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs)) and the MFMA ops
+    per dispatch by type (SQ_INSTS_VALU_MFMA_MOPS_* x 512), or None."""
+    rec = _counter_record(workload, kernel)
+    return None if rec is None else rec.get("mfma")
 
 
 # --------------------------------------------------------------------------- DSA step
@@ -1135,8 +1181,8 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
             "traffic_vs_algorithmic": round(traffic / by["indexer_k"], 4) if traffic else None,
             "ms": round(filt_ms, 4),
             "bytes_per_launch": by["indexer_k"],
-            "mfma_fp8_tflops": round(filt_tflops, 1),
-            "mfma_frac": round(filt_tflops / FP8_PEAK_TFLOPS, 4),
+            "mfma_fp8_tflops_algorithmic": round(filt_tflops, 1),
+            "mfma": mfma_report(workload, "filter_verify_kernel<12>", filt_ms),
         },
         "decode": {
             "kernels": "sparse_decode_kernel<576> + decode_combine_kernel (ekv_sparse_mla_decode), timed by events "
@@ -1144,8 +1190,8 @@ def measure_dsa(torch, ops, args, line: dict) -> None:
             "ms": round(dec_ms, 4),
             "bytes": by["gather"],
             "GB/s_gather": round(by["gather"] / (dec_ms * 1e-3) / 1e9, 1),
-            "mfma_bf16_tflops": round(dec_flops / (dec_ms * 1e-3) / 1e12, 1),
-            "mfma_frac": round(dec_flops / (dec_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "mfma_bf16_tflops_algorithmic": round(dec_flops / (dec_ms * 1e-3) / 1e12, 1),
+            "mfma": mfma_report(workload, "sparse_decode_kernel<576>", None),
         },
     })
 

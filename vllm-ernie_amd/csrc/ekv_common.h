@@ -42,6 +42,26 @@ __device__ __forceinline__ int ue8m0_exponent(float amax) {
   return (u & 0x7fffffu) ? e + 1 : e;
 }
 
+// Cross-workgroup hand-offs (a workgroup publishes results with
+// agent-scope stores or atomics, then arrives on a counter with a relaxed
+// agent-scope atomic add; the last to arrive reads the others' results with
+// agent-scope loads).  The ordering they need comes from the hardware: on
+// gfx950 agent-scope stores, loads and atomics bypass the non-coherent
+// caches (sc1), `s_waitcnt 0` retires every memory operation the wave has
+// issued, and loads issued after an atomic's returned value is tested are
+// issued after it.  An acquire / release pair would add a whole-L2
+// write-back and invalidate per arrival.  The compiler must not move memory
+// accesses across the wait, nor hoist the last arriver's loads above its
+// test: handoff_wait() is the wait between two compiler-only fences, and
+// compiler_fence() follows each arrival test.
+__device__ __forceinline__ void compiler_fence() { __atomic_signal_fence(__ATOMIC_SEQ_CST); }
+
+__device__ __forceinline__ void handoff_wait() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(0);
+  compiler_fence();
+}
+
 __device__ __forceinline__ float exp2i(int e) {  // 2**e for e in [-126, 127]
   return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
 }

@@ -551,7 +551,7 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
       __hip_atomic_store(a.span_part + static_cast<int64_t>(b) * (D / 4) + c / 4, part, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this workgroup's results are complete before it arrives (as in compress_span_slab)
+  handoff_wait();  // this workgroup's results are complete before it arrives (as in compress_span_slab)
   __syncthreads();
   if (tid == 0) {
     const uint32_t before = __hip_atomic_fetch_add(a.span_count + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -559,6 +559,7 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
   }
   __syncthreads();
   if (!ls.last) return;
+  compiler_fence();
 
   // Last arriver: the row from all quarters, thread tid = channel tid.
   if (tid == 0) __hip_atomic_store(a.span_count + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -710,11 +711,12 @@ __device__ __forceinline__ void compress_span_slab(const CompressArgs& a, float*
   // arrives; the last arriver's loads are agent-coherent and issued after its
   // add returns.  No acquire / release: their L2 write-back and invalidate on
   // every arrival would cost more than the span.
-  __builtin_amdgcn_s_waitcnt(0);
+  handoff_wait();
   uint32_t before = 0;
   if (lane == 0) before = __hip_atomic_fetch_add(a.span_count + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   before = __shfl(before, 0);
   if (before + 1u != static_cast<uint32_t>(D / 64)) return;
+  compiler_fence();
   finish_span_wave<D>(a, part_lds, slot, b, j);
 }
 

@@ -1333,7 +1333,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // loads and stores below are coherent across the L2s, and a histogram read
   // before some adds were visible could only lower the bound (more
   // candidates, still exact).
-  __builtin_amdgcn_s_waitcnt(0);
+  handoff_wait();
   __syncthreads();
   // (every lane is past the histogram: the q operands take its LDS now, so
   // they are not held in registers across the wait below)
@@ -1425,7 +1425,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // bound and arrival words (the last arriver departs after publishing).
   // With the in-launch select the workgroups depart after the select.
   if (tid == 0 && !sel) {
-    __builtin_amdgcn_s_waitcnt(0);
+    handoff_wait();
     const uint32_t before = __hip_atomic_fetch_add(arrive, 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((before >> 16) + 1u == static_cast<uint32_t>(groups_row)) {
       __hip_atomic_store(kword, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1622,7 +1622,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
   // Exchange: once every workgroup of the row has written its list and count
   // (agent-scope stores, completed before it arrives), each reads the counts.
-  __builtin_amdgcn_s_waitcnt(0);
+  handoff_wait();
   __syncthreads();
   if (tid == 0) {
     bool all_in = false;
@@ -1814,7 +1814,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         if (v) atomicAdd(hr + i, v);
       }
       if (tid == 0 && counted) atomicAdd(hr + kHistBins + 1, static_cast<uint32_t>(counted));
-      __builtin_amdgcn_s_waitcnt(0);
+      handoff_wait();
       __syncthreads();
       if (tid == 0) {
         const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1864,7 +1864,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             s_dec[1 + w] = static_cast<int>(pd[w]);
             st_agent(dec + 1 + w, pd[w]);
           }
-          __builtin_amdgcn_s_waitcnt(0);  // the payload before the word that announces it
+          handoff_wait();  // the payload before the word that announces it
           st_agent(dec, static_cast<uint32_t>(kind));
         }
         // leave the histogram zero (everyone has arrived; nobody reads it again)
@@ -1922,7 +1922,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       if (tid == 0) {
         st_agent(rec + 2 * x, static_cast<uint32_t>(gt_x));
         st_agent(rec + 2 * x + 1, static_cast<uint32_t>(eq_x));
-        __builtin_amdgcn_s_waitcnt(0);
+        handoff_wait();
         const uint32_t target = static_cast<uint32_t>((rnd + 2) * G);
         const uint32_t before = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         bool all_in = (before & 0xffffu) + 1u >= target;
@@ -1998,12 +1998,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 
   // Depart.  The last workgroup of the row to depart clears the row's words
   // and, if any wait of the row gave up, selects over the row's lists alone.
-  __builtin_amdgcn_s_waitcnt(0);
+  handoff_wait();
   __syncthreads();
   if (tid == 0) {
     if (failed) {
       st_agent(failw, 1u);
-      __builtin_amdgcn_s_waitcnt(0);
+      handoff_wait();
     }
     const uint32_t before = __hip_atomic_fetch_add(arrive, 1u << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_misc[16] = ((before >> 16) + 1u == static_cast<uint32_t>(G)) ? 1 : 0;
