@@ -190,3 +190,23 @@ def test_hca_write_workspace_size_in_span_slots():
     assert size(0, 576) == 0 and size(16, 0) == 0 and size(16, 1024) == 0
     # 16 sequences of 8192-row chunks complete at most 16 * 65 spans
     assert size(16 * (8192 // 128 + 1), 576) > size(16, 576)
+
+
+def test_torch_ops_registered_with_their_writes():
+    """torch.ops.ernie_kv.* (ernie_kv.torch_ops): every operator is registered
+    without a GPU, returns nothing and names the tensors it writes in its
+    schema (Tensor(a!)), so the dispatcher sees the in-place writes."""
+    import torch
+
+    import ernie_kv.torch_ops as T
+
+    writes = {"kv_append_quant": {"cache"}, "indexer_k_insert": {"kcache"}, "hca_write": {"pool", "state", "workspace"},
+              "hca_write_step": {"pool", "state", "out", "lengths", "workspace"},
+              "indexer_topk": {"topk_out", "workspace"}, "indexer_topk_merged": {"topk_out", "workspace", "merged"},
+              "merge_swa_topk": {"out"}, "sparse_mla_decode": {"out", "lse", "workspace"}}
+    assert set(T.OPS) == set(writes)
+    for name, expect in writes.items():
+        schema = getattr(torch.ops.ernie_kv, name).default._schema
+        assert len(schema.returns) == 0, name
+        got = {a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write}
+        assert got == expect, (name, got)

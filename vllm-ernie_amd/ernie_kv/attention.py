@@ -23,6 +23,7 @@ from typing import Any
 import torch
 
 from . import ops
+from . import torch_ops  # noqa: F401  (registers the path's operators as torch.ops.ernie_kv.*)
 
 DSA_BLOCK_SIZE = 64  # attention.py:97-98
 INDEXER_QUANT_BLOCK = 128  # attention.py:99
