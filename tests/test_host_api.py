@@ -210,3 +210,22 @@ def test_torch_ops_registered_with_their_writes():
         assert len(schema.returns) == 0, name
         got = {a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write}
         assert got == expect, (name, got)
+
+
+def test_torch_ops_trace_without_launching():
+    """Under FakeTensorMode (what torch.compile traces with) the operators
+    run their fake implementations: nothing is launched, no library call is
+    made, and the result is None."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import ernie_kv.torch_ops  # noqa: F401
+
+    with FakeTensorMode():
+        rows = torch.empty((4, 576), dtype=torch.bfloat16)
+        slots = torch.empty((4,), dtype=torch.int64)
+        cache = torch.empty((2, 64 * 580), dtype=torch.uint8)
+        assert torch.ops.ernie_kv.kv_append_quant(rows, slots, cache) is None
+        topk = torch.empty((4, 2048), dtype=torch.int32)
+        merged = torch.empty((4, 2176), dtype=torch.int32)
+        assert torch.ops.ernie_kv.merge_swa_topk(topk, merged, slots, 128) is None

@@ -8,8 +8,9 @@ Each operator here is a ``torch.library.custom_op`` over the same
 ``ernie_kv.ops`` wrapper the layers call: the caller owns every output,
 the operator writes it in place on the current stream and returns nothing,
 and the schema names the tensors it writes, so the dispatcher (and
-``torch.compile``) sees the mutation.  Registration needs no GPU; calling
-needs the HIP library, which fails loudly when it is missing.
+``torch.compile``, through each operator's fake implementation) sees the
+mutation.  Registration needs no GPU; calling needs the HIP library, which
+fails loudly when it is missing.
 """
 
 from __future__ import annotations
@@ -103,3 +104,14 @@ def sparse_mla_decode(q: torch.Tensor, cache: torch.Tensor, indices: torch.Tenso
 
 OPS = ("kv_append_quant", "indexer_k_insert", "hca_write", "hca_write_step", "indexer_topk", "indexer_topk_merged",
        "merge_swa_topk", "sparse_mla_decode")
+
+
+# Fake (meta) implementations: every operator only writes tensors the caller
+# passed, so under tracing (torch.compile, FakeTensorMode) it produces
+# nothing and launches nothing.
+def _no_output(*args, **kwargs) -> None:
+    return None
+
+
+for _name in OPS:
+    globals()[_name].register_fake(_no_output)
