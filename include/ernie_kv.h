@@ -114,7 +114,7 @@ int ekv_hca_append_bf16(const uint16_t* latent, int64_t latent_stride, const uin
  * ekv_hca_write_workspace_size(num_seqs, dim) bytes, zero-filled once before
  * its first use and left zero by every call; pass the same workspace_bytes on
  * every call that shares it) may be NULL; with it, decode-sized calls
- * (max_query_len < 128) compress each completed span with four workgroups
+ * (max_query_len < 128) compress each completed span with dim / 64 workgroups
  * instead of one, and longer calls whose workspace holds
  * num_seqs * (max_query_len / 128 + 1) spans compress each span with D / 64
  * one-wave workgroups -- same bytes either way.  Calls that share a

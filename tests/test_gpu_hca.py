@@ -56,7 +56,7 @@ def _run_call(dev, case, rng, starts, counts, gpu, fused=False):
     d = lambda a: to_dev(a, dev)  # noqa: E731
     kvs_t = bf16_tensor(kv_score, dev)
     if fused:
-        if fused == "ws" and "ws" not in gpu:  # decode-sized calls split each span over four workgroups
+        if fused == "ws" and "ws" not in gpu:  # decode-sized calls split each span over dim / 64 workgroups
             gpu["ws"] = ops.hca_write_workspace(case.B, D, dev)
         if fused == "ws-spans" and "ws" not in gpu:  # and prefill calls over D / 64 one-wave workgroups
             gpu["ws"] = ops.hca_write_workspace(case.B, D, dev, max_query_len=1000)

@@ -68,8 +68,8 @@ struct CompressArgs {
   uint8_t* pool;             // [num_pages, page_stride]
   int64_t page_stride;
   int64_t num_pages;
-  // Decode-sized writes with a workspace: a span's four channel quarters are
-  // compressed by four workgroups (null: one workgroup per span).
+  // Decode-sized writes with a workspace: a span is compressed by D / 64
+  // four-wave workgroups (null: one workgroup per span).
   uint32_t* span_count;      // [B] arrivals per span (zero between calls)
   float* span_x;             // [B, D] softmax results
   float* span_part;          // [B, D/4] sums of squares per channel quad
@@ -451,43 +451,56 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
-// compress_span split over four workgroups (decode-sized calls with a
-// workspace): workgroup k takes channels [k D/4, (k+1) D/4), one per lane --
-// wave w channels 16w .. 16w+15 of the quarter, lane l of row group l / 16 --
-// so each lane runs one channel's online softmax over its group's 32 rows
-// instead of four.  It writes its softmax results and its channel quads'
-// sums of squares to the workspace; the last of the four to arrive reads all
-// of them and finishes the row (RMSNorm with the sum in quad order, RoPE,
-// quant) as compress_span does: every operation on a channel, and the order
-// of the sums, is the same, so the bytes are too.  Every thread of the
-// workgroup must call it (it synchronizes).
-constexpr int kQuarters = 4;
+// compress_span split over D / 64 four-wave workgroups (decode-sized calls
+// with a workspace, one slot per sequence): workgroup k takes channels
+// [64 k, 64 k + 64), one per lane -- wave w channels 64 k + 16 w .. + 15,
+// lane l of row group l / 16 -- so each lane runs one channel's online
+// softmax over its group's 32 rows, and a span's work spreads over D / 64
+// CUs.  It writes its softmax results and its channel quads' sums of squares
+// to the workspace; the last of the span's workgroups to arrive reads all of
+// them and finishes the row (finish_span_block).  Every operation on a
+// channel, and the order of the sums, is compress_span's, so the bytes are
+// too.  Every thread of the workgroup must call it (it synchronizes).
+constexpr int kPartThreads = 256;
 
 template <int D>
-__device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, CompressLds<D>& ls, int b, int k,
-                                                      int t0, int64_t p0, int64_t j, int st) {
-  constexpr int kCh = D / kQuarters;
-  static_assert(kCh == 16 * (D / 64), "a quarter is 16 channels per wave");
+__device__ __forceinline__ void finish_span_block(const CompressArgs& a, CompressLds<D>& ls, int b, int64_t j);
+
+template <int D>
+__device__ __forceinline__ void compress_span_part(const CompressArgs& a, CompressLds<D>& ls, int b, int k, int t0,
+                                                   int64_t p0, int64_t j, int st) {
+  constexpr int kParts = D / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int grp = lane >> 4;
-  const int c = k * kCh + 16 * wave + (lane & 15);  // this lane's channel
+  const int c = 64 * k + 16 * wave + (lane & 15);  // this lane's channel
 
-  // Row i of the span, as in compress_span: the input for i >= split, else
-  // the state ring (a row without one reads the call's first row and counts
-  // as 0).  Lane bases of row group grp; rows i0 + grp.
+  // Row i = i0 + grp of the span: the state ring's row (j % 2) * 128 + i
+  // for i < split, else the call's input row i - split.  Both come through
+  // buffer resources, so a row is two unconditional loads whose
+  // out-of-range offsets read 0 (an input offset below the call's first
+  // row wraps past its end; without a ring the ring resource is empty, and
+  // such rows count as 0), and the lane keeps one of the two.
   const int64_t split64 = p0 - j * kSpan;
   const int split = static_cast<int>(split64 < 0 ? 0 : split64);
   const bool has_state = st >= 0 && st < a.num_state;
-  const uint16_t* ring = (has_state ? a.state + (static_cast<int64_t>(st) * kStateRing + (j & 1) * kSpan) * (2 * D)
-                                    : a.kv_score + t0 * a.kvs_stride - grp * (2 * D)) +
-                         grp * (2 * D) + c;
-  const uint16_t* input = a.kv_score + (t0 - split64 + grp) * a.kvs_stride + c;
+  const uint32_t in_row = static_cast<uint32_t>(a.kvs_stride) * 2u;
+  // (uniform values: the resources must live in scalar registers)
+  const uint32_t n_in = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(a.qsl[b + 1] - t0));
+  const __amdgpu_buffer_rsrc_t in_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.kv_score + static_cast<int64_t>(t0) * a.kvs_stride), 0, n_in * in_row, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t ring_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      has_state ? const_cast<uint16_t*>(a.state + (static_cast<int64_t>(st) * kStateRing + (j & 1) * kSpan) * (2 * D))
+                : const_cast<uint16_t*>(a.kv_score),
+      0, has_state ? kSpan * 2 * D * 2 : 0, kBufferWord3);
+  const uint32_t ring_lane = static_cast<uint32_t>((grp * 2 * D + c) * 2);
+  const uint32_t in_lane = static_cast<uint32_t>(grp) * in_row + static_cast<uint32_t>(c) * 2u;
   auto load_row = [&](int i0, int col) -> float {
     const bool from_ring = i0 + grp < split;
-    const uint16_t* r = from_ring ? ring + (has_state ? i0 * (2 * D) : 0) : input + i0 * a.kvs_stride;
-    const uint32_t v = r[col];
-    return (from_ring && !has_state) ? 0.0f : __uint_as_float(v << 16);
+    const uint32_t vr = __builtin_amdgcn_raw_buffer_load_b16(ring_rsrc, ring_lane + (i0 * 2 * D + col) * 2, 0, 0);
+    const uint32_t vi = __builtin_amdgcn_raw_buffer_load_b16(
+        in_rsrc, in_lane + static_cast<uint32_t>((i0 - split) * static_cast<int>(in_row)) + col * 2, 0, 0);
+    return __uint_as_float((from_ring ? vr : vi) << 16);
   };
   const float* ape = a.ape + grp * D + c;
   constexpr int kSteps = kGroupRows / kChunk;
@@ -555,16 +568,35 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
   __syncthreads();
   if (tid == 0) {
     const uint32_t before = __hip_atomic_fetch_add(a.span_count + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ls.last = (before + 1u == static_cast<uint32_t>(kQuarters)) ? 1 : 0;
+    ls.last = (before + 1u == static_cast<uint32_t>(kParts)) ? 1 : 0;
   }
   __syncthreads();
   if (!ls.last) return;
   compiler_fence();
+  finish_span_block<D>(a, ls, b, j);
+}
 
-  // Last arriver: the row from all quarters, thread tid = channel tid.
+// The row of span j of sequence b (workspace slot b) from the softmax
+// results and quad sums in the workspace, finished by the kPartThreads
+// threads of the last workgroup to arrive as compress_span finishes it:
+// RMSNorm with the quad sums added in quad order by thread 0, RoPE on the
+// last 64 channels, the per-token quant.  Thread tid takes channels
+// tid + kPartThreads i.  Clears the slot's arrival counter.
+template <int D>
+__device__ __forceinline__ void finish_span_block(const CompressArgs& a, CompressLds<D>& ls, int b, int64_t j) {
+  constexpr int kPer = (D + kPartThreads - 1) / kPartThreads;
+  constexpr int kWaves = kPartThreads / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   if (tid == 0) __hip_atomic_store(a.span_count + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const float xc = __hip_atomic_load(a.span_x + static_cast<int64_t>(b) * D + tid, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+  float xc[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = tid + kPartThreads * i;
+    xc[i] = c < D ? __hip_atomic_load(a.span_x + static_cast<int64_t>(b) * D + c, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT)
+                  : 0.0f;
+  }
   if (tid < D / 4)
     ls.part[tid] = __hip_atomic_load(a.span_part + static_cast<int64_t>(b) * (D / 4) + tid, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -580,38 +612,49 @@ __device__ __forceinline__ void compress_span_quarter(const CompressArgs& a, Com
   }
   __syncthreads();
   const float rn = ls.rn;
-  float y = (xc * rn) * a.norm_w[tid];
-  const float yp = __shfl_xor(y, 1);  // the RoPE pair (channels 2i, 2i+1)
-  if (tid >= D - 64) {
-    const int pi = (tid - (D - 64)) / 2;
-    const float cz = a.cos_sin[j * 64 + pi], sz = a.cos_sin[j * 64 + 32 + pi];
-    const float x0 = (tid & 1) ? yp : y, x1v = (tid & 1) ? y : yp;
-    y = (tid & 1) ? x0 * sz + x1v * cz : x0 * cz - x1v * sz;
+  float y[kPer];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = tid + kPartThreads * i;
+    float v = c < D ? (xc[i] * rn) * a.norm_w[c] : 0.0f;
+    const float vp = __shfl_xor(v, 1);  // the RoPE pair (channels 2i, 2i+1)
+    if (c >= D - 64 && c < D) {
+      const int pi = (c - (D - 64)) / 2;
+      const float cz = a.cos_sin[j * 64 + pi], sz = a.cos_sin[j * 64 + 32 + pi];
+      const float x0 = (c & 1) ? vp : v, x1v = (c & 1) ? v : vp;
+      v = (c & 1) ? x0 * sz + x1v * cz : x0 * cz - x1v * sz;
+    }
+    y[i] = v;
+    amax = fmaxf(amax, fabsf(v));
   }
-  float amax = wave_max_xor(fabsf(y), 64);
+  amax = wave_max_xor(amax, 64);
   if (lane == 0) ls.wmax[wave] = amax;
   __syncthreads();
   amax = ls.wmax[0];
 #pragma unroll
-  for (int wv = 1; wv < D / 64; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
+  for (int wv = 1; wv < kWaves; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
-  const int64_t slot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
-                           kPageTokens + j % kPageTokens;
-  const float y1 = __shfl_down(y, 1), y2 = __shfl_down(y, 2), y3 = __shfl_down(y, 3);
-  if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
-  uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
-  const int64_t off = slot % kPageTokens;
-  if (a.bf16_rows) {
-    if ((tid & 3) == 0) *reinterpret_cast<uint2*>(page + off * (2 * D) + 2 * tid) = bf16x4_pack(y, y1, y2, y3);
-    return;
+  const int64_t cslot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
+                            kPageTokens + j % kPageTokens;
+  if (cslot < 0 || cslot >= a.num_pages * kPageTokens) return;
+  uint8_t* page = a.pool + (cslot / kPageTokens) * a.page_stride;
+  const int64_t off = cslot % kPageTokens;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = tid + kPartThreads * i;
+    const float y1 = __shfl_down(y[i], 1), y2 = __shfl_down(y[i], 2), y3 = __shfl_down(y[i], 3);
+    if (c >= D || (c & 3) != 0) continue;
+    if (a.bf16_rows) {
+      *reinterpret_cast<uint2*>(page + off * (2 * D) + 2 * c) = bf16x4_pack(y[i], y1, y2, y3);
+    } else {
+      const uint32_t lo = f32x2_to_fp8(y[i] * inv, y1 * inv);
+      const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
+      *reinterpret_cast<uint32_t*>(page + off * D + c) = lo | (hi << 16);
+    }
   }
-  if ((tid & 3) == 0) {
-    const uint32_t lo = f32x2_to_fp8(y * inv, y1 * inv);
-    const uint32_t hi = f32x2_to_fp8(y2 * inv, y3 * inv);
-    *reinterpret_cast<uint32_t*>(page + off * D + tid) = lo | (hi << 16);
-  }
-  if (tid == 0) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
+  if (tid == 0 && !a.bf16_rows) *reinterpret_cast<float*>(page + kPageTokens * D + off * 4) = exp2i(e);
 }
 
 // The row of span j (workspace slot `slot`, compressed slot through
@@ -759,25 +802,54 @@ __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(5))) hca
 
 // Decode-sized HCA write (fewer than 128 new rows per sequence, so at most
 // one span per sequence completes: the one holding its first new position)
-// in one launch: workgroups [0, num_seqs) compress that span when the call
-// completes it, the rest run the append grid's blocks on their first 4
-// waves.  The two touch disjoint memory: the compressor reads this call's
-// inputs and state-ring rows of positions before the call, the append writes
-// this call's positions (rows, window ring, state ring).  Every span such a
-// call compresses starts in the state ring (all but its last rows precede the
-// call), so the ring path is pipelined here; one span per sequence leaves the
-// CUs lightly loaded, so the registers that takes cost no occupancy that
-// matters.
+// in one launch: the first workgroups compress that span when the call
+// completes it, the rest run the append grid's blocks and then the index
+// rows' blocks on their first 4 waves.  The two touch disjoint memory: the
+// compressor reads this call's inputs and state-ring rows of positions
+// before the call, the append writes this call's positions (rows, window
+// ring, state ring), the index rows only read tables.  Every span such a
+// call compresses starts in the state ring (all but its last rows precede
+// the call), so the ring path is pipelined here.
+//
+// Without a workspace: one D-thread workgroup per sequence (compress_span).
 template <int D>
 __global__ void __launch_bounds__(D) __attribute__((amdgpu_waves_per_eu(4)))
 hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows,
                        HcaIndexArgs ix, int append_blocks, int index_y) {
   __shared__ CompressLds<D> ls;
   const int block = static_cast<int>(blockIdx.x);
-  const bool quarters = c.span_count != nullptr;
-  const int compress_blocks = quarters ? kQuarters * num_seqs : num_seqs;
-  if (block < compress_blocks) {
-    const int seq = quarters ? block / kQuarters : block;
+  if (block < num_seqs) {
+    const int t0 = c.qsl[block];
+    const int n = c.qsl[block + 1] - t0;
+    if (n <= 0) return;
+    const int64_t p0 = c.positions[t0];
+    const int64_t j = p0 / kSpan;
+    if (j * kSpan + kSpan - 1 > p0 + n - 1 || j >= c.max_spans) return;  // no span completed by this call
+    compress_span<D, true>(c, ls, block, t0, p0, j, c.state_slot != nullptr ? c.state_slot[block] : -1);
+    return;
+  }
+  if (threadIdx.x >= 256) return;  // the append's and index rows' blocks are 4-wave, with no workgroup barrier
+  const int ab = block - num_seqs;
+  if (ab < append_blocks) {
+    hca_append_block<D>(a, ab, main_blocks, tail_rows);
+    return;
+  }
+  const int ib = ab - append_blocks;  // index rows (the step's decode reads them after this launch)
+  hca_index_block(ix, ib / index_y, ib % index_y);
+}
+
+// With a workspace (a slot per sequence): every block is 4 waves; a span is
+// compressed by D / 64 of them (compress_span_part), so the compressor's
+// arithmetic spreads over as many CUs.
+template <int D>
+__global__ void __launch_bounds__(kPartThreads)
+hca_write_small_ws_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_blocks, int tail_rows,
+                          HcaIndexArgs ix, int append_blocks, int index_y) {
+  __shared__ CompressLds<D> ls;
+  constexpr int kParts = D / 64;
+  const int block = static_cast<int>(blockIdx.x);
+  if (block < kParts * num_seqs) {
+    const int seq = block / kParts;
     const int t0 = c.qsl[seq];
     const int n = c.qsl[seq + 1] - t0;
     if (n <= 0) return;
@@ -785,12 +857,10 @@ hca_write_small_kernel(CompressArgs c, AppendArgs a, int num_seqs, int main_bloc
     const int64_t j = p0 / kSpan;
     if (j * kSpan + kSpan - 1 > p0 + n - 1 || j >= c.max_spans) return;  // no span completed by this call
     const int st = c.state_slot != nullptr ? c.state_slot[seq] : -1;
-    if (quarters) compress_span_quarter<D>(c, ls, seq, block % kQuarters, t0, p0, j, st);
-    else compress_span<D, true>(c, ls, seq, t0, p0, j, st);
+    compress_span_part<D>(c, ls, seq, block - seq * kParts, t0, p0, j, st);
     return;
   }
-  if (threadIdx.x >= 256) return;  // the append's and index rows' blocks are 4-wave, with no workgroup barrier
-  const int ab = block - compress_blocks;
+  const int ab = block - kParts * num_seqs;
   if (ab < append_blocks) {
     hca_append_block<D>(a, ab, main_blocks, tail_rows);
     return;
@@ -917,7 +987,7 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (max_query_len < kSpan) {  // decode-sized: compress, append (and index rows) in one launch
     int main_blocks = 0, tail_rows = 0;
-    const int64_t compress_blocks = (c.span_count ? int64_t{kQuarters} : int64_t{1}) * num_seqs;
+    const int64_t compress_blocks = (c.span_count ? int64_t{dim / 64} : int64_t{1}) * num_seqs;
     const int64_t append_blocks = hca_append_grid(ap, dim, num_seqs, true, true, main_blocks, tail_rows);
     const int index_y = ix ? hca_index_blocks_per_row(ix->width) : 1;
     const int64_t index_blocks = ix ? int64_t{num_tokens} * index_y : 0;
@@ -927,12 +997,20 @@ int hca_write_impl(const uint16_t* latent, int64_t latent_stride, const uint16_t
     const HcaIndexArgs& ia = ix ? *ix : none;
     const dim3 grid(static_cast<uint32_t>(blocks));
     const int ab = static_cast<int>(append_blocks);
-    if (dim == 512)
+    if (c.span_count != nullptr) {
+      if (dim == 512)
+        hipLaunchKernelGGL(hca_write_small_ws_kernel<512>, grid, dim3(kPartThreads), 0, s, c, ap, num_seqs,
+                           main_blocks, tail_rows, ia, ab, index_y);
+      else
+        hipLaunchKernelGGL(hca_write_small_ws_kernel<576>, grid, dim3(kPartThreads), 0, s, c, ap, num_seqs,
+                           main_blocks, tail_rows, ia, ab, index_y);
+    } else if (dim == 512) {
       hipLaunchKernelGGL(hca_write_small_kernel<512>, grid, dim3(512), 0, s, c, ap, num_seqs, main_blocks, tail_rows,
                          ia, ab, index_y);
-    else
+    } else {
       hipLaunchKernelGGL(hca_write_small_kernel<576>, grid, dim3(576), 0, s, c, ap, num_seqs, main_blocks, tail_rows,
                          ia, ab, index_y);
+    }
     return ekv_launch_status();
   }
   const int slots = max_query_len / kSpan + 1;  // spans that can complete per sequence

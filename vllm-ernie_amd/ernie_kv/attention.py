@@ -1040,7 +1040,7 @@ class Ernie5_5HCAAttentionMixin(torch.nn.Module):
     def _write_workspace(self, num_seqs: int, max_query_len: int, D: int, device) -> torch.Tensor:
         """The cache write's workspace, grown to the most span slots a call
         has had (one per sequence and 128 rows of its longest query, plus
-        one): decode-sized calls compress a span with four workgroups, longer
+        one): decode-sized calls compress a span with D / 64 workgroups, longer
         ones with D / 64."""
         spans = num_seqs * (max_query_len // 128 + 1)
         if self._write_ws is None or self._write_spans < spans:

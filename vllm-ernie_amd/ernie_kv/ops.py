@@ -208,7 +208,7 @@ def hca_write(
 ) -> None:
     """``hca_compress`` then ``hca_append`` (same arguments, same result) in
     one call.  With ``workspace`` (``hca_write_workspace``) decode-sized calls
-    compress each completed span with four workgroups, and longer calls whose
+    compress each completed span with ``dim / 64`` workgroups, and longer calls whose
     workspace was sized for their ``max_query_len`` with ``dim / 64`` (same
     bytes).  A bf16 ``pool`` (rows of D bf16 values, 64 a page) takes the
     rows as they are and the compressed rows rounded to bf16; a uint8 pool
