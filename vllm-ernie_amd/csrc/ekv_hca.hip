@@ -589,13 +589,20 @@ __device__ __forceinline__ void finish_span_block(const CompressArgs& a, Compres
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   if (tid == 0) __hip_atomic_store(a.span_count + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  float xc[kPer];
+  // the norm weights and the RoPE table entries of this thread's channels
+  // are loaded with the workspace reads, not after the norm
+  float xc[kPer], wc[kPer], cz[kPer], sz[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = tid + kPartThreads * i;
+    const bool rope = c >= D - 64 && c < D;
+    const int pi = rope ? (c - (D - 64)) / 2 : 0;
     xc[i] = c < D ? __hip_atomic_load(a.span_x + static_cast<int64_t>(b) * D + c, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT)
                   : 0.0f;
+    wc[i] = c < D ? a.norm_w[c] : 0.0f;
+    cz[i] = rope ? a.cos_sin[j * 64 + pi] : 0.0f;
+    sz[i] = rope ? a.cos_sin[j * 64 + 32 + pi] : 0.0f;
   }
   if (tid < D / 4)
     ls.part[tid] = __hip_atomic_load(a.span_part + static_cast<int64_t>(b) * (D / 4) + tid, __ATOMIC_RELAXED,
@@ -617,13 +624,11 @@ __device__ __forceinline__ void finish_span_block(const CompressArgs& a, Compres
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = tid + kPartThreads * i;
-    float v = c < D ? (xc[i] * rn) * a.norm_w[c] : 0.0f;
+    float v = c < D ? (xc[i] * rn) * wc[i] : 0.0f;
     const float vp = __shfl_xor(v, 1);  // the RoPE pair (channels 2i, 2i+1)
     if (c >= D - 64 && c < D) {
-      const int pi = (c - (D - 64)) / 2;
-      const float cz = a.cos_sin[j * 64 + pi], sz = a.cos_sin[j * 64 + 32 + pi];
       const float x0 = (c & 1) ? vp : v, x1v = (c & 1) ? v : vp;
-      v = (c & 1) ? x0 * sz + x1v * cz : x0 * cz - x1v * sz;
+      v = (c & 1) ? x0 * sz[i] + x1v * cz[i] : x0 * cz[i] - x1v * sz[i];
     }
     y[i] = v;
     amax = fmaxf(amax, fabsf(v));
