@@ -31,7 +31,10 @@
 // on the device (2^-10.95 of the largest product over 1M random and
 // adversarial dot products; |q|, |k| <= 448 by the UE8M0 quantization), and
 // 2^-9 covers the fp32 rounding of both head sums (each at most
-// 66 * 2^-24 * 128 * 448^2 * sum_h |w_h| ~ 2^-11 * 448^2 * sum_h |w_h|).
+// 66 * 2^-24 * 128 * 448^2 * sum_h |w_h| ~ 2^-11 * 448^2 * sum_h |w_h|; the
+// filter adds each head's term w_h * max(dot_h, 0) with one fused
+// multiply-add, the max taken on the bits: a float with its sign bit set
+// becomes +0).
 //
 // MFMA layouts (A = 16 heads of a head block, B = 16 tokens):
 //   i8 16x16x64:        lane l: row/col l%16, K bytes [16*(l/16), +16)
@@ -363,6 +366,10 @@ struct FilterArgs {
 };
 
 
+// max(x, 0) on the bits (x is a finite MFMA result): one integer max, where
+// fmaxf also quiets a signalling NaN first.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
 // The filter's approximate dot products: 16 heads (A rows, q codes) x 16
 // tokens (B columns, key codes) over the 128 dims on the fp8 MFMA, as
 // e4m3fn values without scales.  Its error against the exact dot product is
@@ -572,26 +579,9 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
     }
     ks = *reinterpret_cast<const uint32_t*>(pbase + (kFp4 ? kFp4PageBytes : kIdxPageBytes) + lane * 4);
   };
-  uint4 nxt[4][2];
-  uint32_t nks;
-  int lp = first;
-  int lp1 = next();
-  int64_t cur_page = page_of(lp);
-  load_page(cur_page, nxt, nks);
-  int64_t page1 = page_of(lp1);
-  while (lp < p_end) {
-    uint4 kb[4][2];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      kb[b][0] = nxt[b][0];
-      kb[b][1] = nxt[b][1];
-    }
-    const int64_t page = cur_page;
-    const uint32_t row_scale = nks;  // scale word of page row `lane`
-    load_page(page1, nxt, nks);  // in flight while this page is scored
-    cur_page = page1;
-    const int lp2 = next();
-    page1 = page_of(lp2);
+  // One page scored: its 64 tokens' approximate scores and bounds into the
+  // histogram and emit.
+  auto score_page = [&](const uint4 (&kb)[4][2], uint32_t row_scale, int64_t page, int lp) {
     float mine = 0.0f;  // after the 4 blocks: approximate head sum of token `lane` of the page
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -606,7 +596,7 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
       for (int hb = 0; hb < 4; ++hb) {
         const f32x4 cc = kFp4 ? filter_mfma_fp4(op.qa[hb], op.qsc[hb], kv, kscb) : filter_mfma(op.qa[hb], kv);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += op.wv[hb][i] * fmaxf(cc[i], 0.0f);
+        for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(op.wv[hb][i], relu_bits(cc[i]), acc);
       }
       acc += __shfl_xor(acc, 16);
       acc += __shfl_xor(acc, 32);
@@ -627,8 +617,39 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
     }
     if (s < n) atomicAdd(&s_hist[score_key((sc - e) + 0.0f) >> (32 - kHistBits)], 1u);
     emit(lp, page, sc, e);
-    lp = lp1;
-    lp1 = lp2;
+  };
+  // Two page buffers taken in turn (the next page loads into one while the
+  // other is scored), so no page is copied between registers.
+  uint4 buf_a[4][2], buf_b[4][2];
+  uint32_t ks_a, ks_b;
+  int lp = first;
+  int lp1 = next();
+  int64_t cur_page = page_of(lp);
+  load_page(cur_page, buf_a, ks_a);
+  int64_t page1 = page_of(lp1);
+  for (;;) {
+    if (lp >= p_end) break;
+    {
+      const int64_t page = cur_page;
+      load_page(page1, buf_b, ks_b);  // in flight while this page is scored
+      cur_page = page1;
+      const int lp2 = next();
+      page1 = page_of(lp2);
+      score_page(buf_a, ks_a, page, lp);
+      lp = lp1;
+      lp1 = lp2;
+    }
+    if (lp >= p_end) break;
+    {
+      const int64_t page = cur_page;
+      load_page(page1, buf_a, ks_a);
+      cur_page = page1;
+      const int lp2 = next();
+      page1 = page_of(lp2);
+      score_page(buf_b, ks_b, page, lp);
+      lp = lp1;
+      lp1 = lp2;
+    }
   }
 }
 

@@ -37,11 +37,15 @@ COMMON = [
     "-packed-fp32-ops",
 ]
 EXACT = ["-ffp-contract=off"]
+# MFMA results in ordinary VGPRs rather than accumulation registers, so the
+# indexer's page loops use them without a copy back (the scores they feed
+# are the same).
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCES = {
     "ekv_status.cpp": [],
     "ekv_append.hip": EXACT,
     "ekv_hca.hip": EXACT,
-    "ekv_indexer.hip": EXACT,
+    "ekv_indexer.hip": EXACT + MFMA_VGPR,
     "ekv_decode.hip": [],
     "ekv_quant.hip": EXACT,
     "ekv_mxfp4.hip": EXACT,
