@@ -495,44 +495,45 @@ __device__ __forceinline__ void compress_span_part(const CompressArgs& a, Compre
       0, has_state ? kSpan * 2 * D * 2 : 0, kBufferWord3);
   const uint32_t ring_lane = static_cast<uint32_t>((grp * 2 * D + c) * 2);
   const uint32_t in_lane = static_cast<uint32_t>(grp) * in_row + static_cast<uint32_t>(c) * 2u;
-  auto load_row = [&](int i0, int col) -> float {
-    const bool from_ring = i0 + grp < split;
-    const uint32_t vr = __builtin_amdgcn_raw_buffer_load_b16(ring_rsrc, ring_lane + (i0 * 2 * D + col) * 2, 0, 0);
-    const uint32_t vi = __builtin_amdgcn_raw_buffer_load_b16(
-        in_rsrc, in_lane + static_cast<uint32_t>((i0 - split) * static_cast<int>(in_row)) + col * 2, 0, 0);
-    return __uint_as_float((from_ring ? vr : vi) << 16);
+  auto ring_off = [&](int i0, int col) { return ring_lane + (i0 * 2 * D + col) * 2; };
+  auto in_off = [&](int i0, int col) {
+    return in_lane + static_cast<uint32_t>((i0 - split) * static_cast<int>(in_row)) + col * 2;
   };
   const float* ape = a.ape + grp * D + c;
-  constexpr int kSteps = kGroupRows / kChunk;
-  float sc[kChunk], ap[kChunk], kv[2][kChunk];
-  auto issue_kv = [&](int step, float (&k_)[kChunk]) {
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) k_[u] = load_row(kRowGroups * (step * kChunk + u), 0);
-  };
-  auto issue_gate = [&](int step) {
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int i0 = kRowGroups * (step * kChunk + u);
-      sc[u] = load_row(i0, D);
-      ap[u] = ape[i0 * D];
-    }
-  };
+  // The lane's 32 rows in two halves: every load of a half is issued
+  // before any of it is used (two memory latencies for the span part
+  // instead of one per chunk, in half the registers of one batch), and the
+  // chunks are folded in order as before.
+  constexpr int kHalf = kGroupRows / 2;
   float m = -INFINITY, Z = 0.0f, N = 0.0f;
-  issue_kv(0, kv[0]);
-  issue_gate(0);
 #pragma unroll
-  for (int step = 0; step < kSteps; ++step) {
-    const int cur = step & 1;
-    if (step + 1 < kSteps) issue_kv(step + 1, kv[cur ^ 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    float g[kChunk];
+  for (int h = 0; h < 2; ++h) {
+    uint32_t kr[kHalf], ki[kHalf], sr[kHalf], si[kHalf];
+    float ap[kHalf];
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u) g[u] = sc[u] + ap[u];
+    for (int q = 0; q < kHalf; ++q) {
+      const int i0 = kRowGroups * (h * kHalf + q);
+      kr[q] = __builtin_amdgcn_raw_buffer_load_b16(ring_rsrc, ring_off(i0, 0), 0, 0);
+      ki[q] = __builtin_amdgcn_raw_buffer_load_b16(in_rsrc, in_off(i0, 0), 0, 0);
+      sr[q] = __builtin_amdgcn_raw_buffer_load_b16(ring_rsrc, ring_off(i0, D), 0, 0);
+      si[q] = __builtin_amdgcn_raw_buffer_load_b16(in_rsrc, in_off(i0, D), 0, 0);
+      ap[q] = ape[i0 * D];
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (step + 1 < kSteps) issue_gate(step + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if (step == 0) softmax_terms1<true>(m, Z, N, g, kv[cur]);
-    else softmax_terms1<false>(m, Z, N, g, kv[cur]);
+#pragma unroll
+    for (int st = 0; st < kHalf / kChunk; ++st) {
+      const int step = h * (kHalf / kChunk) + st;
+      float g[kChunk], kv[kChunk];
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int q = st * kChunk + u;
+        const bool from_ring = kRowGroups * (h * kHalf + q) + grp < split;
+        g[u] = __uint_as_float((from_ring ? sr[q] : si[q]) << 16) + ap[q];
+        kv[u] = __uint_as_float((from_ring ? kr[q] : ki[q]) << 16);
+      }
+      if (step == 0) softmax_terms1<true>(m, Z, N, g, kv);
+      else softmax_terms1<false>(m, Z, N, g, kv);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 
