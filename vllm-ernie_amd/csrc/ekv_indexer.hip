@@ -547,23 +547,26 @@ __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t,
 // calls emit(lp, page, sc, e) with page = the block-table entry, or -1 when the
 // page is unmapped; the lower bound sc - e of every token s < n goes into the
 // LDS histogram.
-template <bool kFp4, class Next, class Emit>
-__device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
-                                              uint32_t* s_hist, const FilterOps& op, Emit emit) {
-  const int lane = threadIdx.x & 63;
-  const int g = lane >> 4, col = lane & 15;
-  const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
-  // Block-table entry of logical page lp, -1 outside the range, the table or
-  // the cache.  Unmapped pages load page 0 (always present) and score 0.
-  auto page_of = [&](int lp) -> int64_t {
+// The pages of row t a filter streams: block-table entry of logical page
+// lp (-1 outside [0, p_end), the table or the cache; unmapped pages load
+// page 0, always present, and score 0), and one page's loads: this lane's 32
+// bytes (fp4: 16) of each of the 4 blocks of 16 token rows, and the scale
+// (fp4: four scale bytes) of row `lane` (one coalesced 256-byte load per
+// page).  Loads are unconditional so the compiler keeps them in flight.
+template <bool kFp4>
+struct PageSource {
+  const FilterArgs& a;
+  const int32_t* bt;
+  int p_end;
+  __device__ PageSource(const FilterArgs& args, int t, int end)
+      : a(args), bt(args.block_table + static_cast<int64_t>(args.req_ids[t]) * args.bt_stride), p_end(end) {}
+  __device__ int64_t page_of(int lp) const {
     const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : -1;
     return (p >= 0 && p < a.num_pages) ? p : -1;
-  };
-  // One page = 4 blocks of 16 tokens; this lane's 32 bytes (fp4: 16) of each
-  // block row, and the scale (fp4: four scale bytes) of row `lane` (one
-  // coalesced 256-byte load per page).  Loads are unconditional so the
-  // compiler keeps them in flight.
-  auto load_page = [&](int64_t page, uint4 (&kb)[4][2], uint32_t& ks) {
+  }
+  __device__ void load(int64_t page, uint4 (&kb)[4][2], uint32_t& ks) const {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, col = lane & 15;
     const uint8_t* pbase = a.kcache + (page >= 0 ? page : 0) * a.page_stride;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -578,7 +581,26 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
       }
     }
     ks = *reinterpret_cast<const uint32_t*>(pbase + (kFp4 ? kFp4PageBytes : kIdxPageBytes) + lane * 4);
-  };
+  }
+};
+
+// A wave's first page, loaded before the stream starts (by the caller, so
+// its memory latency overlaps the caller's set-up).
+struct FirstPage {
+  uint4 kb[4][2];
+  uint32_t ks;
+  int64_t page;
+};
+
+template <bool kFp4, class Next, class Emit>
+__device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
+                                              uint32_t* s_hist, const FilterOps& op, Emit emit,
+                                              FirstPage* pre = nullptr) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, col = lane & 15;
+  const PageSource<kFp4> src(a, t, p_end);
+  auto page_of = [&](int lp) -> int64_t { return src.page_of(lp); };
+  auto load_page = [&](int64_t page, uint4 (&kb)[4][2], uint32_t& ks) { src.load(page, kb, ks); };
   // One page scored: its 64 tokens' approximate scores and bounds into the
   // histogram and emit.
   auto score_page = [&](const uint4 (&kb)[4][2], uint32_t row_scale, int64_t page, int lp) {
@@ -624,8 +646,19 @@ __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n,
   uint32_t ks_a, ks_b;
   int lp = first;
   int lp1 = next();
-  int64_t cur_page = page_of(lp);
-  load_page(cur_page, buf_a, ks_a);
+  int64_t cur_page;
+  if (pre != nullptr) {
+    cur_page = pre->page;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      buf_a[b][0] = pre->kb[b][0];
+      buf_a[b][1] = pre->kb[b][1];
+    }
+    ks_a = pre->ks;
+  } else {
+    cur_page = page_of(lp);
+    load_page(cur_page, buf_a, ks_a);
+  }
   int64_t page1 = page_of(lp1);
   for (;;) {
     if (lp >= p_end) break;
@@ -1255,6 +1288,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const int tid = threadIdx.x;
   const int t = blockIdx.y, x = blockIdx.x;
   const FilterArgs& f = a.f;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, col = lane & 15;
+  FilterOps op;
+  load_filter_operands<kFp4>(f, t, g, col, op);  // (issued with the row length's load)
   const int n = max(0, min(f.lengths[t], f.max_len));
   const int npages = (n + kPageTokens - 1) / kPageTokens;
   const int per_group = fused_group_pages(n, a.groups);
@@ -1287,6 +1324,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     if (tid == 0) *count = seg_len;
     return;
   }
+  // each wave's first page is requested before the LDS set-up, so its
+  // memory latency overlaps it and the q operands' (requested first)
+  FirstPage first_page;
+  {
+    const PageSource<kFp4> src(f, t, wg_p1);
+    first_page.page = src.page_of(wg_p0 + wave);
+    src.load(first_page.page, first_page.kb, first_page.ks);
+  }
   for (int i = tid; i < kHistBins; i += kThreads) s_hist[i] = 0;
   if constexpr (kFp4) {
     if (tid < kIdxHeads) s_table[tid] = static_cast<uint32_t>(f.q_scales[static_cast<int64_t>(t) * kIdxHeads + tid]);
@@ -1294,10 +1339,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     if (tid < 256) s_table[tid] = fp8_digit_pack(static_cast<uint32_t>(tid));
   }
   if (tid == 0) s_misc[18] = wg_p0 + kWaves;  // wave w starts at page wg_p0 + w
-  const int lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, col = lane & 15;
-  FilterOps op;
-  load_filter_operands<kFp4>(f, t, g, col, op);
   __syncthreads();
 
   // Phase 1: stream the pages; upper-bound prefixes and page entries to LDS.
@@ -1310,7 +1351,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                       [&](int lp, int64_t page, float sc, float e) {
                         s_pref[(lp - wg_p0) * kPageTokens + lane] = upper_prefix(sc, e);
                         if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
-                      });
+                      },
+                      &first_page);
   __syncthreads();
   uint32_t* const rowc = a.counters + static_cast<int64_t>(t) * kCounterRow;
   uint32_t* const gh = rowc;  // histogram A
