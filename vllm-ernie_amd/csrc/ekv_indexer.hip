@@ -538,15 +538,6 @@ __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t,
   }
 }
 
-// Streams logical pages of row t: `first`, then the pages next() returns (an
-// increasing sequence; the stream ends at the first page >= p_end).  The next
-// page's rows are in flight and the block-table entry of the one after that
-// already read while a page is scored, so start-up latency is paid once per
-// wave.  Per page, lane l gets the approximate score sc and error e of token
-// 64 lp + l (sc = e = 0 on an unmapped page, whose exact scores are 0) and
-// calls emit(lp, page, sc, e) with page = the block-table entry, or -1 when the
-// page is unmapped; the lower bound sc - e of every token s < n goes into the
-// LDS histogram.
 // The pages of row t a filter streams: block-table entry of logical page
 // lp (-1 outside [0, p_end), the table or the cache; unmapped pages load
 // page 0, always present, and score 0), and one page's loads: this lane's 32
@@ -592,6 +583,16 @@ struct FirstPage {
   int64_t page;
 };
 
+// Streams logical pages of row t: `first`, then the pages next() returns (an
+// increasing sequence; the stream ends at the first page >= p_end).  The next
+// page's rows are in flight and the block-table entry of the one after that
+// already read while a page is scored, so start-up latency is paid once per
+// wave.  Per page, lane l gets the approximate score sc and error e of token
+// 64 lp + l (sc = e = 0 on an unmapped page, whose exact scores are 0) and
+// calls emit(lp, page, sc, e) with page = the block-table entry, or -1 when the
+// page is unmapped; the lower bound sc - e of every token s < n goes into the
+// LDS histogram.  With `pre`, page `first` has been loaded already (its
+// rows and scale word in pre).
 template <bool kFp4, class Next, class Emit>
 __device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
                                               uint32_t* s_hist, const FilterOps& op, Emit emit,
