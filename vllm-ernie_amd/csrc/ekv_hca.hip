@@ -1069,6 +1069,8 @@ extern "C" int ekv_hca_write_step(const uint16_t* latent, int64_t latent_stride,
                                   int64_t page_stride, int64_t num_pages, void* workspace, int64_t workspace_bytes,
                                   int32_t window, int32_t* idx_out, int64_t idx_stride, int32_t width,
                                   int32_t* lengths, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
+  if (num_tokens == 0 || num_seqs == 0) return 0;  // nothing to write, no index rows
   EKV_CHECK(ring_pages && idx_out && lengths, "null pointer");
   EKV_CHECK(ring >= window && window >= 0 && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
   EKV_CHECK(width >= 0 && idx_stride >= width, "idx_stride must be >= width >= 0");
@@ -1108,6 +1110,8 @@ extern "C" int ekv_hca_write_step_bf16(const uint16_t* latent, int64_t latent_st
                                        int32_t ring, uint16_t* pool, int64_t page_stride, int64_t num_pages,
                                        void* workspace, int64_t workspace_bytes, int32_t window, int32_t* idx_out,
                                        int64_t idx_stride, int32_t width, int32_t* lengths, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && num_seqs >= 0, "sizes must be >= 0");
+  if (num_tokens == 0 || num_seqs == 0) return 0;  // nothing to write, no index rows
   EKV_CHECK(ring_pages && idx_out && lengths, "null pointer");
   EKV_CHECK(ring >= window && window >= 0 && ring % kPageTokens == 0, "ring must be a multiple of 64 and >= window");
   EKV_CHECK(width >= 0 && idx_stride >= width, "idx_stride must be >= width >= 0");

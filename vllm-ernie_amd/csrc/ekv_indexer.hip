@@ -2786,6 +2786,7 @@ int check_topk_args(const void* q, const float* w, const uint8_t* kcache, int64_
                     const int32_t* block_table, const int32_t* req_ids, const int32_t* lengths, int32_t num_tokens,
                     int32_t max_len, int32_t k, void* workspace, int64_t workspace_bytes, bool fp4) {
   EKV_CHECK(num_tokens >= 0 && max_len >= 0 && k > 0, "bad sizes");
+  if (num_tokens == 0) return 0;  // an empty batch: no buffer is read or written
   EKV_CHECK(q && w && kcache && block_table && req_ids && lengths, "null pointer");
   EKV_CHECK(page_stride >= kPageTokens * ((fp4 ? kFp4Row : kIdxDim) + 4) && page_stride % 16 == 0, "bad page_stride");
   EKV_CHECK(aligned16(q) && aligned16(kcache), "misaligned buffers");
@@ -2821,13 +2822,12 @@ int run_filter(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, i
   if (selected) *selected = false;
   int rc = check_topk_args(q.q, q.w, kcache, page_stride, block_table, req_ids, lengths, num_tokens, max_len, k,
                            workspace, workspace_bytes, kFp4);
-  if (rc) return rc;
+  if (rc || num_tokens == 0) return rc;
   if constexpr (kFp4) {
     EKV_CHECK(q.q_scales != nullptr, "q_scales must be a [T, 64] int32");
   } else {
     EKV_CHECK(q.q_digits != nullptr && aligned16(q.q_digits), "q_digits must be a 16-byte aligned [T, 3, 64, 128]");
   }
-  if (num_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   TopkWorkspace ws = carve(workspace, T, L);
@@ -2871,13 +2871,12 @@ int run_select(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, i
   int rc = check_topk_args(kFp4 ? static_cast<const void*>(q.q) : static_cast<const void*>(q.q_digits), q.w, kcache,
                            page_stride, block_table, req_ids, lengths, num_tokens, max_len, k, workspace,
                            workspace_bytes, kFp4);
-  if (rc) return rc;
+  if (rc || num_tokens == 0) return rc;
   if constexpr (kFp4) EKV_CHECK(q.q_scales != nullptr, "q_scales must be a [T, 64] int32");
   EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
   EKV_CHECK(merged_out == nullptr || (positions != nullptr && window >= 0 && merged_width >= 0 &&
                                       merged_stride >= merged_width),
             "merged_out needs positions, window >= 0 and merged_stride >= merged_width");
-  if (num_tokens == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t T = num_tokens, L = max_len > 0 ? max_len : 1;
   const int chunks = num_chunks(max_len);
@@ -2907,6 +2906,8 @@ int run_topk(const TopkQuery& q, const uint8_t* kcache, int64_t page_stride, int
              int32_t num_tokens, int32_t max_len, int32_t* topk_out, int64_t out_stride, int32_t k, void* workspace,
              int64_t workspace_bytes, int32_t* merged_out, int64_t merged_stride, int32_t merged_width,
              const int64_t* positions, int32_t window, int32_t merged_slots, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && max_len >= 0 && k > 0, "bad sizes");
+  if (num_tokens == 0) return 0;  // an empty batch: no buffer is read or written
   EKV_CHECK(topk_out != nullptr && out_stride >= k, "topk_out must be [T, >= k]");
   EKV_CHECK(merged_out == nullptr || (positions != nullptr && window >= 0 && merged_width >= 0 &&
                                       merged_stride >= merged_width),

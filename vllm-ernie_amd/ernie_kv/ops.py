@@ -8,6 +8,8 @@ Caches are ``uint8`` tensors ``[num_pages, page_stride_bytes]``.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -22,8 +24,11 @@ def _stream() -> int:
 
 def _rs(t: torch.Tensor) -> int:
     """Row stride of a 2-D+ tensor; a size-1 leading dim may carry stride 0
-    (e.g. a numpy ``[None]`` view), which would read as zero columns."""
-    return t.stride(0) if t.shape[0] > 1 else t[0].numel()
+    (e.g. a numpy ``[None]`` view), which would read as zero columns, and an
+    empty one has no row to measure (the row's element count stands in)."""
+    if t.shape[0] > 1:
+        return t.stride(0)
+    return t[0].numel() if t.shape[0] == 1 else math.prod(t.shape[1:])
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
