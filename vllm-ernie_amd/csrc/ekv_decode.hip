@@ -95,10 +95,11 @@ __device__ __forceinline__ int row_splits(int64_t extra, int tiles, int64_t tota
   return max(1, min(tiles, ns));  // never more splits than tiles
 }
 
-// Finds the row and split of logical workgroup l; t = -1 when l is past the
-// last split.  All threads of the workgroup call it.
+// Finds the row, its length and the split of logical workgroup l; t = -1
+// when l is past the last split.  All threads of the workgroup call it.
 template <int kN>
-__device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int& split, int& nsplit, int& first) {
+__device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int& len, int& split, int& nsplit,
+                             int& first) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int kW = kN / 64;
   const int T = a.rows;
@@ -107,13 +108,15 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
     const int tiles = (a.width + kTile - 1) / kTile;
     const int ns = row_splits(extra, tiles, static_cast<int64_t>(T) * tiles);
     t = (l / ns < T) ? l / ns : -1;
+    len = a.width;
     split = l % ns;
     nsplit = ns;
     first = l - split;
     return;
   }
   // total tiles (with T <= kN thread r reads row r's length once, here)
-  const int mine = (T <= kN && tid < T) ? (row_len(a, tid) + kTile - 1) / kTile : 0;
+  const int mylen = (T <= kN && tid < T) ? row_len(a, tid) : 0;
+  const int mine = (mylen + kTile - 1) / kTile;
   int64_t sum = 0;
   if (T <= kN) sum = mine;
   else
@@ -149,11 +152,13 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
   int pos = before + x - cnt;  // logical workgroups before row r0
   if (pos <= l && l < pos + cnt) {
     for (int r = r0; r < r1; ++r) {
-      const int ns = T <= kN ? cnt : row_splits(extra, (row_len(a, r) + kTile - 1) / kTile, total);
+      const int rl = T <= kN ? mylen : row_len(a, r);
+      const int ns = T <= kN ? cnt : row_splits(extra, (rl + kTile - 1) / kTile, total);
       if (l < pos + ns) {
         s_red[3 * kW] = r;
         s_red[3 * kW + 1] = l - pos;
         s_red[3 * kW + 2] = ns;
+        s_red[3 * kW + 3] = rl;
         break;
       }
       pos += ns;
@@ -161,6 +166,7 @@ __device__ void locate_split(const DecodeArgs& a, int l, int* s_red, int& t, int
   }
   __syncthreads();
   t = s_red[3 * kW];
+  len = s_red[3 * kW + 3];
   split = s_red[3 * kW + 1];
   nsplit = s_red[3 * kW + 2];
   first = l - split;
@@ -460,26 +466,56 @@ sparse_decode_kernel(DecodeArgs a) {
 
   const int b = blockIdx.x;
   const int l = (b % kXcds) * (a.groups / kXcds) + b / kXcds;
-  int t, split, nsplit, first;
-  locate_split<kThreads>(a, l, sm.red, t, split, nsplit, first);
-  if (t < 0) return;
-  if (split == 0 && tid == 0) a.ws_rows[t] = make_int2(first, nsplit);
-
-  const int len = row_len(a, t);
-  const int per_split = ((len + kTile - 1) / kTile + nsplit - 1) / nsplit * kTile;
-  const int e_begin = split * per_split;
-  const int e_cnt = max(0, min(e_begin + per_split, len) - e_begin);
-  const int ntiles = (e_cnt + kTile - 1) / kTile;
-  const int e_pad = ntiles * kTile;
 
   // Prologue: entries -> slots (index, then block table), each gather issued
-  // for all of the thread's entries before the next.
+  // for all of the thread's entries before the next.  The entries of the
+  // split this workgroup takes when every row has `width` entries (the
+  // closed form) are requested before the row lengths are read; they are
+  // kept when the lengths give the same row and entry range (uniform rows),
+  // and requested again otherwise.
   constexpr int kPrologue = kMaxSplitEntries / kThreads;
   int64_t sv[kPrologue];
+  auto split_range = [&](int row, int sp, int ns, int len, int& begin, int& cnt) {
+    const int per = ((len + kTile - 1) / kTile + ns - 1) / ns * kTile;
+    begin = sp * per;
+    cnt = (row >= 0) ? max(0, min(begin + per, len) - begin) : 0;
+  };
+  auto load_entries = [&](int row, int begin, int cnt) {
 #pragma unroll
-  for (int j = 0; j < kPrologue; ++j) {
-    const int e = tid + kThreads * j;
-    sv[j] = (e < e_cnt) ? a.indices[static_cast<int64_t>(t) * a.idx_stride + e_begin + e] : -1;
+    for (int j = 0; j < kPrologue; ++j) {
+      const int e = tid + kThreads * j;
+      sv[j] = (e < cnt) ? a.indices[static_cast<int64_t>(row) * a.idx_stride + begin + e] : -1;
+    }
+  };
+  int g_t, g_begin, g_cnt;
+  {
+    const int tiles = (a.width + kTile - 1) / kTile;
+    const int ns = row_splits(a.groups - a.rows, tiles, static_cast<int64_t>(a.rows) * tiles);
+    g_t = (l / ns < a.rows) ? l / ns : -1;
+    split_range(g_t, l % ns, ns, a.width, g_begin, g_cnt);
+  }
+  load_entries(g_t, g_begin, g_cnt);
+
+  int t, len, split, nsplit, first;
+  locate_split<kThreads>(a, l, sm.red, t, len, split, nsplit, first);
+  if (t < 0) {
+    wait_vm<0>();  // (the entries requested above)
+    return;
+  }
+  if (split == 0 && tid == 0) a.ws_rows[t] = make_int2(first, nsplit);
+
+  int e_begin, e_cnt;
+  split_range(t, split, nsplit, len, e_begin, e_cnt);
+  const int ntiles = (e_cnt + kTile - 1) / kTile;
+  const int e_pad = ntiles * kTile;
+  if (t != g_t || e_begin != g_begin || e_cnt != g_cnt) load_entries(t, e_begin, e_cnt);  // (workgroup-uniform)
+  // The q operands (scorer waves) are requested once the entries are.
+  bf16x8 qb[KS];  // B operand of S^T = K Q^T: head 16 grp + col, dims 32 ks + 8 kg .. +7
+  if (scorer && active) {
+    const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (16 * grp + col) * a.q_head_stride;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * kg));
   }
   if (a.block_table != nullptr) {
     const int32_t* bt = a.block_table + static_cast<int64_t>(a.req_ids[t]) * a.bt_stride;
@@ -503,8 +539,7 @@ sparse_decode_kernel(DecodeArgs a) {
   __syncthreads();
   // Data waves: the first kAhead tiles in flight (the only vector memory
   // operations they issue, so their load counter counts tiles).  Scorer
-  // waves: the row scales and the q operands.
-  bf16x8 qb[KS];  // B operand of S^T = K Q^T: head 16 grp + col, dims 32 ks + 8 kg .. +7
+  // waves: the row scales.
   const TileLanes<D, BF16> tl = tile_lanes<D, BF16>(grp);
   if (!scorer) {
     for (int i = 0; i < SM::kAhead && i < ntiles; ++i) issue_tile<D, BF16>(a, sm, tl, grp, i);
@@ -521,12 +556,6 @@ sparse_decode_kernel(DecodeArgs a) {
       else ksv[j] = s >= 0 ? *reinterpret_cast<const float*>(a.cache + static_cast<int64_t>(s >> 6) * a.page_stride +
                                                               kPageTokens * D + (s & 63) * 4)
                            : 0.0f;
-    }
-    if (active) {
-      const uint16_t* qrow = a.q + static_cast<int64_t>(t) * a.q_tok_stride + (16 * grp + col) * a.q_head_stride;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qb[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * kg));
     }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {

@@ -397,6 +397,8 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   const int c0 = 4 * quad;
   float x[4], part;
   span_softmax<D, kRingPipe>(a, quad, t0, p0, j, st, x, part);
+  // the row's page, requested before the norm
+  const int64_t cpage = a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens];
   // From here on the lanes of row group 0 carry the row: quad q's channels.
   const bool owner = grp == 0;
   if (owner) ls.part[quad] = part;
@@ -434,8 +436,7 @@ __device__ __forceinline__ void compress_span(const CompressArgs& a, CompressLds
   for (int wv = 1; wv < kWaves; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
-  const int64_t slot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
-                           kPageTokens + j % kPageTokens;
+  const int64_t slot = cpage * kPageTokens + j % kPageTokens;
   if (slot < 0 || slot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (slot / kPageTokens) * a.page_stride;
   const int64_t off = slot % kPageTokens;
@@ -593,6 +594,7 @@ __device__ __forceinline__ void finish_span_block(const CompressArgs& a, Compres
   // the norm weights and the RoPE table entries of this thread's channels
   // are loaded with the workspace reads, not after the norm
   float xc[kPer], wc[kPer], cz[kPer], sz[kPer];
+  const int64_t cpage = a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens];  // the row's page
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int c = tid + kPartThreads * i;
@@ -642,8 +644,7 @@ __device__ __forceinline__ void finish_span_block(const CompressArgs& a, Compres
   for (int wv = 1; wv < kWaves; ++wv) amax = fmaxf(amax, ls.wmax[wv]);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
-  const int64_t cslot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
-                            kPageTokens + j % kPageTokens;
+  const int64_t cslot = cpage * kPageTokens + j % kPageTokens;
   if (cslot < 0 || cslot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (cslot / kPageTokens) * a.page_stride;
   const int64_t off = cslot % kPageTokens;
@@ -677,6 +678,7 @@ __device__ __forceinline__ void finish_span_wave(const CompressArgs& a, float* p
   if (lane == 0) __hip_atomic_store(a.span_count + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float* sx = a.span_x + slot * D;
   const float* sp = a.span_part + slot * (D / 4);
+  const int64_t cpage = a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens];  // the row's page
   for (int q = lane; q < D / 4; q += 64)
     part_lds[q] = __hip_atomic_load(sp + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float xs[kSlabs];
@@ -713,8 +715,7 @@ __device__ __forceinline__ void finish_span_wave(const CompressArgs& a, float* p
   amax = wave_max_xor(amax, 64);
   const int e = ue8m0_exponent(amax);
   const float inv = exp2i(-e);
-  const int64_t cslot = static_cast<int64_t>(a.comp_bt[static_cast<int64_t>(b) * a.comp_bt_stride + j / kPageTokens]) *
-                            kPageTokens + j % kPageTokens;
+  const int64_t cslot = cpage * kPageTokens + j % kPageTokens;
   if (cslot < 0 || cslot >= a.num_pages * kPageTokens) return;
   uint8_t* page = a.pool + (cslot / kPageTokens) * a.page_stride;
   const int64_t off = cslot % kPageTokens;
