@@ -549,6 +549,42 @@ int ekv_indexer_score_fp4(const uint8_t* q_values, const int32_t* q_scales, cons
                           int64_t scores_stride, void* stream);
 
 /*
+ * ekv_dsa_decode_prologue followed by ekv_indexer_topk_merged over the keys
+ * in kcache (block_table .. merged_slots as there; lengths, q_fp8, w_out and
+ * q_digits are the prologue's outputs, which the top-k reads), with the same
+ * outputs as the two calls.  max_new_rows is the most query rows any one
+ * sequence has in the call (its newest positions; 1 for plain decode).  When
+ * 1 <= max_new_rows <= window no row scores a key the call appends, and when
+ * the top-k also runs as one launch that selects (64 heads, merged output)
+ * the prologue is folded into that launch: each workgroup prepares and
+ * quantizes its row's q itself, and one workgroup per row appends the new
+ * rows and writes the prologue's outputs while the row's bound is computed.
+ * Otherwise the two calls run.  Replaces
+ * the head of Ernie5_5DSAAttention._indexer_and_attn (nvidia/attention.py:
+ * 1205-1226: Ernie5_5Indexer.forward's prep, K insert and SparseAttnIndexer
+ * top-k (:942-984), the latent append [vLLM concat_and_cache_mla] and
+ * merge_swa_topk (:582-641)).
+ */
+int ekv_dsa_decode_prologue_topk_merged(
+    const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride, int64_t k_num_pages,
+    const uint16_t* latent, int64_t latent_stride, int32_t dim, uint8_t* cache, int64_t page_stride,
+    int64_t num_pages, const int64_t* slot_mapping, int32_t num_tokens, const uint16_t* q, int64_t q_tok_stride,
+    int64_t q_head_stride, const void* weights, int32_t weights_is_bf16, int64_t w_stride, int32_t heads,
+    uint8_t* q_fp8, float* w_out, int8_t* q_digits, const int64_t* positions, int32_t window,
+    int32_t max_new_rows, int32_t* lengths, const float* ln_w, const float* ln_b, float eps, const float* cos_sin,
+    int32_t cos_sin_rows, const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, int32_t max_len,
+    int32_t* topk_out, int64_t out_stride, int32_t k_top, void* workspace, int64_t workspace_bytes,
+    int32_t* merged_out, int64_t merged_stride, int32_t merged_width, int32_t merged_slots, void* stream);
+
+/*
+ * 1 when ekv_dsa_decode_prologue_topk_merged of num_tokens rows of at most
+ * max_len keys (64 heads, 1 <= max_new_rows <= window, merged output) runs
+ * as one launch on the current device, else 0 (the two calls run).  No counterpart in the
+ * reference: a plan query, as ekv_indexer_topk_workspace_size is.
+ */
+int32_t ekv_dsa_decode_prologue_folds(int32_t num_tokens, int32_t max_len);
+
+/*
  * MXFP4 counterparts of ekv_indexer_filter / _select / _topk / _topk_merged (same workspace,
  * ekv_indexer_topk_workspace_size): the filter runs the scaled fp4 MFMA over
  * every token with an error bound, the candidates are scored exactly as

@@ -1,8 +1,9 @@
 """GPU parity of the timed workloads at full size.
 
 The DSA decode step exactly as ``bench.py`` times it (``build_dsa_decode`` +
-``dsa_step``: prologue with indexer prep -> one-launch filter, exact scoring
-and select with the merged output as cache slots -> decode) at 32 x 131,072
+``dsa_step``: the prologue with indexer prep folded into the one-launch
+filter, exact scoring and select with the merged output as cache slots ->
+decode) at 32 x 131,072
 tokens with 5% spike keys at +4 sigma of each row's scores (every row's
 top-2048 ends in a lowest-index tie among its spikes), the same step with one
 random spike row in 5% of the positions, and the multi-token step at 8 x

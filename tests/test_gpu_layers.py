@@ -73,7 +73,7 @@ def _dsa_setup(dev, rng, ctxs, rows_per_req, fp4=False):
         "attn_sink": to_dev(rng.standard_normal(64).astype(np.float32), dev),
     }
     md = A.DSAStepMetadata(slot_mapping=to_dev(slot_mapping, dev), block_table=to_dev(bt, dev),
-                           req_ids=to_dev(req, dev), max_seq_len=int(max(ctxs)))
+                           req_ids=to_dev(req, dev), max_seq_len=int(max(ctxs)), max_query_len=int(max(rows_per_req)))
     inputs = dict(hidden=randn_bf16(rng, (T, 256)), q_c=randn_bf16(rng, (T, 128)), q=randn_bf16(rng, (T, 64, 256)),
                   kv_c=randn_bf16(rng, (T, 512)), k_pe=randn_bf16(rng, (T, 1, 64)))
     return SimpleNamespace(cfg=cfg, bt=bt, kc=kc, lat=lat, req=req, positions=positions, slot_mapping=slot_mapping,

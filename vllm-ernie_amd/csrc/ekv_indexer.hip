@@ -42,6 +42,7 @@
 //   C (both):           lane l: rows 4*(l/16)+i, column l%16
 #include "ekv_common.h"
 #include "ekv_internal.h"
+#include "ekv_rows.h"
 
 #include <algorithm>
 
@@ -497,23 +498,45 @@ struct FilterOps {
   float eb[4];
 };
 
+// fp8 keys: the operands from one row's q codes q8[h * 128 + d] and folded
+// weights w[h] (global memory, or the fused prologue's copy in LDS).
+__device__ __forceinline__ void filter_operands_fp8(const uint8_t* q8, const float* w, int g, int col, FilterOps& op) {
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    const uint4* src = reinterpret_cast<const uint4*>(q8 + (16 * hb + col) * kIdxDim + 32 * g);
+    const uint4 v0 = src[0], v1 = src[1];
+    op.qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
+                      static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
+    op.qsc[hb] = 0u;
+  }
+  float wabs = 0.0f;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float wi = w[16 * hb + 4 * g + i];
+      op.wv[hb][i] = wi;
+      wabs += fabsf(wi);
+    }
+  float ws = (col == 0) ? wabs : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
+  for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
+  op.eb[0] = ws * (448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+  op.eb[1] = op.eb[2] = op.eb[3] = 0.0f;
+}
+
 template <bool kFp4>
 __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t, int g, int col, FilterOps& op) {
   const int64_t th = static_cast<int64_t>(t) * kIdxHeads;
+  if constexpr (!kFp4) {
+    filter_operands_fp8(a.q_fp8 + th * kIdxDim, a.w + th, g, col, op);
+    return;
+  }
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) {
-    if constexpr (kFp4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.q_fp8 + (th + 16 * hb + col) * kFp4Row + 16 * g);
-      op.qa[hb] = i32x8{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w),
-                        0, 0, 0, 0};
-      op.qsc[hb] = (static_cast<uint32_t>(a.q_scales[th + 16 * hb + col]) >> (8 * g)) & 0xffu;
-    } else {
-      const uint4* src = reinterpret_cast<const uint4*>(a.q_fp8 + (th + 16 * hb + col) * kIdxDim + 32 * g);
-      const uint4 v0 = src[0], v1 = src[1];
-      op.qa[hb] = i32x8{static_cast<int>(v0.x), static_cast<int>(v0.y), static_cast<int>(v0.z), static_cast<int>(v0.w),
-                        static_cast<int>(v1.x), static_cast<int>(v1.y), static_cast<int>(v1.z), static_cast<int>(v1.w)};
-      op.qsc[hb] = 0u;
-    }
+    const uint4 v = *reinterpret_cast<const uint4*>(a.q_fp8 + (th + 16 * hb + col) * kFp4Row + 16 * g);
+    op.qa[hb] = i32x8{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w),
+                      0, 0, 0, 0};
+    op.qsc[hb] = (static_cast<uint32_t>(a.q_scales[th + 16 * hb + col]) >> (8 * g)) & 0xffu;
   }
   float wabs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -522,19 +545,15 @@ __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t,
     for (int i = 0; i < 4; ++i) {
       const float wi = a.w[th + 16 * hb + 4 * g + i];
       op.wv[hb][i] = wi;
-      if constexpr (kFp4) {
-        const uint32_t qs = static_cast<uint32_t>(a.q_scales[th + 16 * hb + 4 * g + i]);
+      const uint32_t qs = static_cast<uint32_t>(a.q_scales[th + 16 * hb + 4 * g + i]);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) wabs[b] += fabsf(wi) * e8m0_value((qs >> (8 * b)) & 0xffu);
-      } else {
-        wabs[0] += fabsf(wi);
-      }
+      for (int b = 0; b < 4; ++b) wabs[b] += fabsf(wi) * e8m0_value((qs >> (8 * b)) & 0xffu);
     }
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     float ws = (col == 0) ? wabs[b] : 0.0f;  // lanes 0, 16, 32, 48 hold all 64 heads between them
     for (int off = 32; off > 0; off >>= 1) ws += __shfl_xor(ws, off);
-    op.eb[b] = ws * (kFp4 ? kFp4BoundFactor : 448.0f * 448.0f * (0x1p-8f + 0x1p-9f));
+    op.eb[b] = ws * kFp4BoundFactor;
   }
 }
 
@@ -1072,6 +1091,183 @@ constexpr int kCounterRows = 1024;  // rows the fused path takes (at most 3 x CU
 constexpr int kHistRereads = 64;    // reads of a row histogram that does not yet sum to its tokens
 constexpr int64_t kCounterBytes = 256 + int64_t{kCounterRows} * kCounterRow * 4;
 
+// The DSA decode prologue (ekv_dsa_decode_prologue) folded into the fused
+// launch, for decode rows (the new tokens lie in their rows' windows, so no
+// row scores them): every workgroup prepares and quantizes its row's indexer
+// q into LDS as indexer_q_quant does, and takes the row's key count as
+// max(position + 1 - window, 0); the first workgroup of each row appends the
+// new token's indexer K row and latent row (two waves, while the others
+// stream) and writes the count, the q codes, the folded weights and the
+// digit planes out as the prologue would.
+struct FusedPrologue {
+  const uint16_t* q;         // [T, 64, 128] bf16 (the raw projection when cos_sin is set)
+  int64_t q_tok_stride, q_head_stride;
+  const void* w;             // [T, w_stride] bf16 or fp32 head weights
+  int32_t w_is_bf16;
+  int64_t w_stride;
+  const float* cos_sin;      // [cs_rows, 64] (RoPE and Hadamard of q first), or null
+  int32_t cs_rows;
+  int32_t* lengths;          // [T] out: max(position + 1 - window, 0)
+  uint8_t* q_fp8_out;        // [T, 64, 128] out (or null)
+  float* w_out;              // [T, 64] out (or null)
+  int8_t* q_digits_out;      // [T, 3, 64, 128] out (or null)
+  AppendArgs k_rows;         // the indexer K rows (D = 128; the prep fields with cos_sin)
+  AppendArgs latent;         // the latent rows
+  int32_t latent_dim;        // 512 or 576
+};
+
+// Row t's q rows as loaded (16 lanes per head, kThreads / 16 heads a pass)
+// and the head weights (lane 0 of each head).
+template <int kThreads>
+struct FusedQRows {
+  static constexpr int kPasses = (kIdxHeads * 16 + kThreads - 1) / kThreads;
+  uint4 raw[kPasses];
+  float wt[kPasses];
+  RopeLane rope;  // (the same position for every head)
+};
+
+template <int kThreads>
+__device__ __forceinline__ void fused_q_load(const FusedPrologue& p, int64_t t, int64_t pos, FusedQRows<kThreads>& r) {
+  const int ln = threadIdx.x & 15;
+  r.rope = rope_lane((p.cos_sin != nullptr && pos >= 0 && pos < p.cs_rows) ? p.cos_sin + pos * 64 : nullptr, ln);
+#pragma unroll
+  for (int ps = 0; ps < FusedQRows<kThreads>::kPasses; ++ps) {
+    const int h = ps * (kThreads / 16) + static_cast<int>(threadIdx.x >> 4);
+    r.raw[ps] = make_uint4(0, 0, 0, 0);
+    r.wt[ps] = 0.0f;
+    if (h < kIdxHeads) {
+      r.raw[ps] = *reinterpret_cast<const uint4*>(p.q + t * p.q_tok_stride + h * p.q_head_stride + 8 * ln);
+      if (ln == 0)
+        r.wt[ps] = p.w_is_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.w)[t * p.w_stride + h])
+                               : static_cast<const float*>(p.w)[t * p.w_stride + h];
+    }
+  }
+}
+
+// indexer_q_quant's arithmetic on row t (position pos): codes to
+// s_q8[h * 128 + d], folded weights to s_w[h].
+template <int kThreads>
+__device__ __forceinline__ void fused_q_quant(const FusedPrologue& p, const FusedQRows<kThreads>& r, uint8_t* s_q8,
+                                              float* s_w) {
+  const int ln = threadIdx.x & 15;
+#pragma unroll
+  for (int ps = 0; ps < FusedQRows<kThreads>::kPasses; ++ps) {
+    const int h = ps * (kThreads / 16) + static_cast<int>(threadIdx.x >> 4);
+    if (h >= kIdxHeads) continue;  // whole 16-lane groups
+    float v[8];
+    unpack_bf16x8(r.raw[ps], v);
+    if (p.cos_sin != nullptr) {
+      row_rope_neox64_lane(v, r.rope, ln);
+      row_hadamard(v, ln);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = wave_max_xor(amax, 16);
+    const int e = ue8m0_exponent(amax);
+    const float inv = exp2i(-e);
+    const uint32_t b0 = f32x2_to_fp8(v[0] * inv, v[1] * inv);
+    const uint32_t b1 = f32x2_to_fp8(v[2] * inv, v[3] * inv);
+    const uint32_t b2 = f32x2_to_fp8(v[4] * inv, v[5] * inv);
+    const uint32_t b3 = f32x2_to_fp8(v[6] * inv, v[7] * inv);
+    *reinterpret_cast<uint2*>(s_q8 + h * kIdxDim + 8 * ln) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+    if (ln == 0) s_w[h] = (r.wt[ps] * exp2i(e)) * 0x1.6a09e6p-7f;  // fl32(128**-0.5 * 64**-0.5)
+  }
+}
+
+// Digit d of 16 fp8 codes (byte i of the result: digit d of code i), with
+// pack(code) = fp8_digit_pack(code) or its table.
+template <class Pack>
+__device__ __forceinline__ i32x4 digit_word(const uint4& codes, int d, Pack pack) {
+  const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+  int out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) r |= ((pack((w[i] >> (8 * b)) & 0xffu) >> (8 * d)) & 0xffu) << (8 * b);
+    out[i] = static_cast<int>(r);
+  }
+  return i32x4{out[0], out[1], out[2], out[3]};
+}
+
+// The prologue's q outputs of row t from the LDS copy: the codes, the folded
+// weights and the digit planes [t][digit][h][128] (a null output skipped).
+template <int kThreads, class Pack>
+__device__ __forceinline__ void fused_store_q(const FusedPrologue& p, int64_t t, const uint8_t* s_q8, const float* s_w,
+                                              Pack pack) {
+  const int tid = threadIdx.x;
+  constexpr int kChunks = kIdxHeads * kIdxDim / 16;  // 16-byte chunks of codes
+  for (int c = tid; c < kChunks; c += kThreads) {
+    const uint4 v = *reinterpret_cast<const uint4*>(s_q8 + 16 * c);
+    if (p.q_fp8_out != nullptr) *reinterpret_cast<uint4*>(p.q_fp8_out + t * (kIdxHeads * kIdxDim) + 16 * c) = v;
+    if (p.q_digits_out != nullptr) {
+      const int h = c / (kIdxDim / 16), d0 = 16 * (c % (kIdxDim / 16));
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        *reinterpret_cast<i32x4*>(p.q_digits_out + ((t * 3 + d) * kIdxHeads + h) * kIdxDim + d0) =
+            digit_word(v, d, pack);
+    }
+  }
+  if (p.w_out != nullptr && tid < kIdxHeads) p.w_out[t * kIdxHeads + tid] = s_w[tid];
+}
+
+// The new token's rows of query row t, as the prologue appends them: wave
+// kWaves - 1 the indexer K row (16 lanes; the k_norm, RoPE and Hadamard prep
+// when k_rows.cos_sin is set), wave kWaves - 2 the latent row.
+template <int kWaves>
+__device__ __forceinline__ void fused_appends(const FusedPrologue& p, int64_t t) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave == kWaves - 1) {
+    const AppendArgs& a = p.k_rows;
+    const int ln = lane & 15;  // (the four 16-lane groups compute the row, the first stores it)
+    uint4 raw[1];
+    load_bf16_row<128, 16>(a.rows + t * a.row_stride, ln, raw);
+    const int64_t slot = a.slot_mapping[t];
+    if (a.cos_sin != nullptr) {
+      float v[8];
+      unpack_bf16x8(raw[0], v);
+      const int64_t pos = a.positions[t];
+      row_layer_norm(v, a.ln_w, a.ln_b, a.eps, ln);
+      row_rope_neox64(v, (pos >= 0 && pos < a.cs_rows) ? a.cos_sin + pos * 64 : nullptr, ln);
+      row_hadamard(v, ln);
+      raw[0] = pack_bf16x8(v);
+    }
+    if (lane < 16) store_row<128, 16>(a, slot, ln, raw);
+  } else if (wave == kWaves - 2) {
+    const AppendArgs& a = p.latent;
+    if (p.latent_dim == 576) {
+      uint4 raw[Fp8Row<576, 64>::kPerLane];
+      load_bf16_row<576, 64>(a.rows + t * a.row_stride, lane, raw);
+      store_row<576, 64>(a, a.slot_mapping[t], lane, raw);
+    } else {
+      uint4 raw[Fp8Row<512, 64>::kPerLane];
+      load_bf16_row<512, 64>(a.rows + t * a.row_stride, lane, raw);
+      store_row<512, 64>(a, a.slot_mapping[t], lane, raw);
+    }
+  }
+}
+
+// The prologue's outputs and appends of row t: after the stream (digits
+// through the LDS digit table), or alone in a row with nothing to score.
+template <int kThreads, int kWaves>
+__device__ __forceinline__ void fused_outputs(const FusedPrologue& p, int64_t t, const uint8_t* s_q8,
+                                              const float* s_w, const uint32_t* s_table) {
+  fused_store_q<kThreads>(p, t, s_q8, s_w, [=](uint32_t code) { return s_table[code]; });
+  fused_appends<kWaves>(p, t);
+}
+
+template <int kThreads, int kWaves>
+__device__ __forceinline__ void fused_prologue_only(const FusedPrologue& p, int64_t t, int64_t pos, uint8_t* s_q8,
+                                                    float* s_w) {
+  FusedQRows<kThreads> qr;
+  fused_q_load<kThreads>(p, t, pos, qr);
+  fused_q_quant<kThreads>(p, qr, s_q8, s_w);
+  __syncthreads();
+  fused_store_q<kThreads>(p, t, s_q8, s_w, [](uint32_t code) { return fp8_digit_pack(code); });
+  fused_appends<kWaves>(p, t);
+}
+
 struct FusedArgs {
   FilterArgs f;              // f.upper and f.hist are not used
   const int8_t* q_digits;    // [T, 3, 64, 128]
@@ -1094,6 +1290,11 @@ struct FusedArgs {
   const int64_t* positions;
   int32_t window;
   int32_t merged_slots;      // merged entries as cache slots through the block table
+  // The folded prologue (fp8 keys, in-launch select with merged rows): q, the
+  // weights and the key counts come from `pro`, not from f.q_fp8, f.w,
+  // q_digits and f.lengths.
+  int32_t prologue;
+  FusedPrologue pro;
 };
 
 __device__ __forceinline__ uint32_t ld_agent(const void* p) {
@@ -1228,7 +1429,7 @@ struct SelRow {
   int64_t seq, m_topk, width, window;
   const int32_t* bt;  // null unless merged_slots
   int64_t bt_stride, num_pages;
-  __device__ SelRow(const FusedArgs& a, int t)
+  __device__ __forceinline__ SelRow(const FusedArgs& a, int t)
       : out(a.sel_out + static_cast<int64_t>(t) * a.sel_stride),
         merged(a.merged ? a.merged + static_cast<int64_t>(t) * a.merged_stride : nullptr),
         seq(0), m_topk(0), width(a.merged_width), window(a.window), bt(nullptr), bt_stride(a.f.bt_stride),
@@ -1239,19 +1440,19 @@ struct SelRow {
       if (a.merged_slots) bt = a.f.block_table + static_cast<int64_t>(a.f.req_ids[t]) * a.f.bt_stride;
     }
   }
-  __device__ uint32_t entry(int64_t i) const {
+  __device__ __forceinline__ uint32_t entry(int64_t i) const {
     if (bt == nullptr || i < 0) return static_cast<uint32_t>(i);
     if ((i >> 6) >= bt_stride) return 0xffffffffu;
     const int64_t p = bt[i >> 6];
     return (p >= 0 && p < num_pages) ? static_cast<uint32_t>(p * kPageTokens + (i & 63)) : 0xffffffffu;
   }
   // output entry pos = token tok (or -1); the merged entry from the block table
-  __device__ void emit(int64_t pos, int64_t tok) const {
+  __device__ __forceinline__ void emit(int64_t pos, int64_t tok) const {
     st_agent(out + pos, static_cast<uint32_t>(tok));
     if (merged && pos < m_topk) st_agent(merged + pos, entry(tok));
   }
   // the same with the token's page known (-1: unmapped)
-  __device__ void emit_paged(int64_t pos, int64_t tok, int64_t page) const {
+  __device__ __forceinline__ void emit_paged(int64_t pos, int64_t tok, int64_t page) const {
     st_agent(out + pos, static_cast<uint32_t>(tok));
     if (merged && pos < m_topk)
       st_agent(merged + pos, bt == nullptr ? static_cast<uint32_t>(tok)
@@ -1259,7 +1460,7 @@ struct SelRow {
                                                         : 0xffffffffu));
   }
   // entries [m_topk, width) of the merged row: the window, then -1
-  __device__ void window_part(int tid, int nthreads) const {
+  __device__ __forceinline__ void window_part(int tid, int nthreads) const {
     if (!merged) return;
     const int64_t w = min(seq, window);
     for (int64_t c = m_topk + tid; c < width; c += nthreads)
@@ -1271,7 +1472,7 @@ struct SelRow {
 constexpr int kFusedQ4Words = 4 * 4 * 64;
 static_assert(kFusedQ4Words * 8 <= kFusedQdBytes, "fp4 q operands share the digit operands' LDS");
 
-template <int kWaves, bool kFp4>
+template <int kWaves, bool kFp4, bool kPro = false>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) filter_verify_kernel(FusedArgs a) {
   using Lay = FusedLayout<kWaves>;
   constexpr int kThreads = Lay::kThreads;
@@ -1291,9 +1492,24 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const FilterArgs& f = a.f;
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, col = lane & 15;
+  // The folded prologue's q codes and weights (8 KB + 256 B) sit in the list's
+  // LDS until the list is built.
+  uint8_t* const s_q8 = reinterpret_cast<uint8_t*>(s_list);
+  float* const s_qw = reinterpret_cast<float*>(s_q8 + kIdxHeads * kIdxDim);
+  static_assert(kIdxHeads * (kIdxDim + 4) <= 2 * Lay::kList * 4, "the prologue's q fits the list's LDS");
+  static_assert(!(kPro && kFp4), "the folded prologue takes fp8 keys");
+  constexpr bool pro = kPro;  // (a.prologue set)
   FilterOps op;
-  load_filter_operands<kFp4>(f, t, g, col, op);  // (issued with the row length's load)
-  const int n = max(0, min(f.lengths[t], f.max_len));
+  int64_t pos = 0, wl = 0;
+  int n;
+  if (pro) {
+    pos = a.positions[t];
+    wl = max(pos + 1 - static_cast<int64_t>(a.window), int64_t{0});
+    n = static_cast<int>(min(wl, static_cast<int64_t>(f.max_len)));
+  } else {
+    load_filter_operands<kFp4>(f, t, g, col, op);  // (issued with the row length's load)
+    n = max(0, min(f.lengths[t], f.max_len));
+  }
   const int npages = (n + kPageTokens - 1) / kPageTokens;
   const int per_group = fused_group_pages(n, a.groups);
   const int wg_p0 = x * per_group, wg_p1 = min(wg_p0 + per_group, npages);
@@ -1311,7 +1527,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     if (n <= f.k)
       for (int i = n + tid; i < f.k; i += kThreads) so.emit(i, -1);
   }
+  if (pro && x == 0 && tid == 0 && a.pro.lengths != nullptr) a.pro.lengths[t] = static_cast<int32_t>(wl);
+  // (the first workgroup of a row with nothing to score still writes the
+  // prologue's outputs and appends)
   if (seg_len <= 0) {  // no pages in this segment
+    if (pro && x == 0) fused_prologue_only<kThreads, kWaves>(a.pro, t, pos, s_q8, s_qw);
     if (tid == 0) *count = 0;
     return;
   }
@@ -1322,9 +1542,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     } else {
       for (int i = tid; i < seg_len; i += kThreads) a.cand_idx[out0 + i] = seg0 + i;
     }
+    if (pro && x == 0) fused_prologue_only<kThreads, kWaves>(a.pro, t, pos, s_q8, s_qw);
     if (tid == 0) *count = seg_len;
     return;
   }
+  // (the folded prologue's q rows, weights and RoPE entries are requested
+  // with the block-table entry, and quantized while the first pages load)
+  FusedQRows<kThreads> qr;
+  if (pro) fused_q_load<kThreads>(a.pro, t, pos, qr);
   // each wave's first page is requested before the LDS set-up, so its
   // memory latency overlaps it and the q operands' (requested first)
   FirstPage first_page;
@@ -1333,6 +1558,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     first_page.page = src.page_of(wg_p0 + wave);
     src.load(first_page.page, first_page.kb, first_page.ks);
   }
+  if (pro) fused_q_quant<kThreads>(a.pro, qr, s_q8, s_qw);
   for (int i = tid; i < kHistBins; i += kThreads) s_hist[i] = 0;
   if constexpr (kFp4) {
     if (tid < kIdxHeads) s_table[tid] = static_cast<uint32_t>(f.q_scales[static_cast<int64_t>(t) * kIdxHeads + tid]);
@@ -1341,6 +1567,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   }
   if (tid == 0) s_misc[18] = wg_p0 + kWaves;  // wave w starts at page wg_p0 + w
   __syncthreads();
+  if (pro) filter_operands_fp8(s_q8, s_qw, g, col, op);
 
   // Phase 1: stream the pages; upper-bound prefixes and page entries to LDS.
   auto grab = [&]() -> int {
@@ -1388,8 +1615,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
       const int e = idx >> 6, ln = idx & 63;
       const int hb = e / 6, d = (e / 2) % 3, kh = e & 1;
       const int lg = ln >> 4, lc = ln & 15;
-      qd_regs[j] = *reinterpret_cast<const i32x4*>(
-          a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads + 16 * hb + lc) * kIdxDim + 64 * kh + 16 * lg);
+      if (pro)  // digit d of the 16 codes, through the digit table
+        qd_regs[j] = digit_word(*reinterpret_cast<const uint4*>(s_q8 + (16 * hb + lc) * kIdxDim + 64 * kh + 16 * lg), d,
+                                [&](uint32_t code) { return s_table[code]; });
+      else
+        qd_regs[j] = *reinterpret_cast<const i32x4*>(a.q_digits + ((static_cast<int64_t>(t) * 3 + d) * kIdxHeads +
+                                                                   16 * hb + lc) * kIdxDim + 64 * kh + 16 * lg);
     }
   }
   // Every histogram atomic of the workgroup has completed before it arrives.
@@ -1436,8 +1667,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     s_misc[16] = ((before & 0xffffu) + 1u == static_cast<uint32_t>(groups_row)) ? 1 : 0;
     s_misc[17] = 0;
     s_misc[19] = 0;  // a wait of this workgroup gave up
+    s_misc[26] = ((before & 0xffffu) == 0u) ? 1 : 0;  // the row's first arrival
   }
   __syncthreads();
+  // The folded prologue's outputs and appends: by the row's first workgroup
+  // to arrive, while it waits for the bound (after publishing it, in a row of
+  // one workgroup).
+  const bool pro_out = pro && s_misc[26] != 0;
+  if (pro_out && !s_misc[16]) fused_outputs<kThreads, kWaves>(a.pro, t, s_q8, s_qw, s_table);
   if (s_misc[16]) {
     int excl = 0, total = 0;
     // The row histogram counts each of the row's n tokens once.  Every
@@ -1485,6 +1722,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     s_misc[17] = static_cast<int>(v >> (32 - kHistBits));
   }
+  if (pro_out && s_misc[16]) fused_outputs<kThreads, kWaves>(a.pro, t, s_q8, s_qw, s_table);
   // depart: the last workgroup of the row to hold the bound clears the
   // bound and arrival words (the last arriver departs after publishing).
   // With the in-launch select the workgroups depart after the select.
@@ -2978,6 +3216,159 @@ extern "C" int ekv_indexer_topk_merged(const uint8_t* q_fp8, const int8_t* q_dig
                          bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k, workspace,
                          workspace_bytes, merged_out, merged_stride, merged_width, positions, window, merged_slots,
                          stream);
+}
+
+// ---------------------------------------------------------------------------
+// The DSA decode prologue and the merged top-k in one call: one launch of
+// the fused kernel with the prologue folded in (FusedPrologue) when the plan
+// selects in that launch, else ekv_dsa_decode_prologue then
+// ekv_indexer_topk_merged.  The outputs are those of the two calls.
+// ---------------------------------------------------------------------------
+extern "C" int ekv_dsa_decode_prologue(const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride,
+                                       int64_t k_num_pages, const uint16_t* latent, int64_t latent_stride,
+                                       int32_t dim, uint8_t* cache, int64_t page_stride, int64_t num_pages,
+                                       const int64_t* slot_mapping, int32_t num_tokens, const uint16_t* q,
+                                       int64_t q_tok_stride, int64_t q_head_stride, const void* weights,
+                                       int32_t weights_is_bf16, int64_t w_stride, int32_t heads, uint8_t* q_fp8,
+                                       float* w_out, int8_t* q_digits, const int64_t* positions, int32_t window,
+                                       int32_t* lengths, const float* ln_w, const float* ln_b, float eps,
+                                       const float* cos_sin, int32_t cos_sin_rows, void* stream);
+
+namespace {
+
+// The prologue's checks of one appended row set (ekv_append.hip).
+int check_rows(const uint16_t* rows, int64_t row_stride, int32_t dim, const int64_t* slot_mapping,
+               const uint8_t* cache, int64_t page_stride) {
+  EKV_CHECK(rows && slot_mapping && cache, "null pointer");
+  EKV_CHECK(row_stride >= dim && row_stride % 8 == 0, "row_stride must be >= dim and a multiple of 8");
+  EKV_CHECK(page_stride >= kPageTokens * (dim + 4) && page_stride % 16 == 0,
+            "page_stride must hold 64 rows + 64 scales and be a multiple of 16");
+  EKV_CHECK(aligned16(rows) && aligned16(cache), "rows and cache must be 16-byte aligned");
+  return 0;
+}
+
+// The plan of a folded call over T rows of at most max_len keys: the fused
+// plan that selects in its launch, with the folded kernel as resident as the
+// plan needs (plan.fused false: the two calls run).
+FilterPlan folded_plan(int64_t T, int32_t max_len) {
+  FilterPlan plan = plan_filter<false>(T, max_len);
+  if (!plan.fused || plan.groups > kSelMaxGroups) {
+    plan.fused = false;
+    return plan;
+  }
+  const void* kernel = plan.waves == 12 ? reinterpret_cast<const void*>(filter_verify_kernel<12, false, true>)
+                                        : reinterpret_cast<const void*>(filter_verify_kernel<4, false, true>);
+  int dev = 0, cus = 0;
+  plan.fused = hipGetDevice(&dev) == hipSuccess &&
+               hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+               T * plan.groups <= static_cast<int64_t>(occupancy(kernel, 64 * plan.waves, plan.smem)) * cus;
+  return plan;
+}
+
+AppendArgs rows_args(const uint16_t* rows, int64_t row_stride, int32_t num_tokens, const int64_t* slot_mapping,
+                     uint8_t* cache, int64_t page_stride, int64_t num_pages) {
+  AppendArgs a{};
+  a.rows = rows; a.row_stride = row_stride; a.num_tokens = num_tokens; a.slot_mapping = slot_mapping;
+  a.cache = cache; a.page_stride = page_stride; a.num_pages = num_pages;
+  return a;
+}
+
+}  // namespace
+
+extern "C" int32_t ekv_dsa_decode_prologue_folds(int32_t num_tokens, int32_t max_len) {
+  return (num_tokens > 0 && max_len >= 0 && folded_plan(num_tokens, max_len).fused) ? 1 : 0;
+}
+
+extern "C" int ekv_dsa_decode_prologue_topk_merged(
+    const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride, int64_t k_num_pages,
+    const uint16_t* latent, int64_t latent_stride, int32_t dim, uint8_t* cache, int64_t page_stride,
+    int64_t num_pages, const int64_t* slot_mapping, int32_t num_tokens, const uint16_t* q, int64_t q_tok_stride,
+    int64_t q_head_stride, const void* weights, int32_t weights_is_bf16, int64_t w_stride, int32_t heads,
+    uint8_t* q_fp8, float* w_out, int8_t* q_digits, const int64_t* positions, int32_t window,
+    int32_t max_new_rows, int32_t* lengths, const float* ln_w, const float* ln_b, float eps, const float* cos_sin,
+    int32_t cos_sin_rows, const int32_t* block_table, int64_t bt_stride, const int32_t* req_ids, int32_t max_len,
+    int32_t* topk_out, int64_t out_stride, int32_t k_top, void* workspace, int64_t workspace_bytes,
+    int32_t* merged_out, int64_t merged_stride, int32_t merged_width, int32_t merged_slots, void* stream) {
+  EKV_CHECK(num_tokens >= 0 && window >= 0 && max_len >= 0 && k_top > 0, "bad sizes");
+  if (num_tokens == 0) return 0;
+  const int64_t T = num_tokens;
+  FilterPlan plan{false, 4, 1, 0, 0};
+  // folded only when no row can score a key this call appends: every
+  // sequence's new rows (its last positions) number at most `window`
+  if (heads == kIdxHeads && max_new_rows >= 1 && max_new_rows <= window && merged_out != nullptr)
+    plan = folded_plan(T, max_len);
+  if (!plan.fused) {
+    const int rc = ekv_dsa_decode_prologue(k, k_stride, kcache, k_page_stride, k_num_pages, latent, latent_stride,
+                                           dim, cache, page_stride, num_pages, slot_mapping, num_tokens, q,
+                                           q_tok_stride, q_head_stride, weights, weights_is_bf16, w_stride, heads,
+                                           q_fp8, w_out, q_digits, positions, window, lengths, ln_w, ln_b, eps,
+                                           cos_sin, cos_sin_rows, stream);
+    if (rc) return rc;
+    return ekv_indexer_topk_merged(q_fp8, q_digits, w_out, kcache, k_page_stride, k_num_pages, block_table,
+                                   bt_stride, req_ids, lengths, num_tokens, max_len, topk_out, out_stride, k_top,
+                                   workspace, workspace_bytes, merged_out, merged_stride, merged_width, positions,
+                                   window, merged_slots, stream);
+  }
+  // the checks the two calls make
+  EKV_CHECK(cos_sin == nullptr || (ln_w && ln_b && cos_sin_rows >= 0 && aligned16(ln_w) && aligned16(ln_b) &&
+                                   aligned16(cos_sin)),
+            "the indexer prep needs 16-byte aligned ln_w, ln_b and cos_sin");
+  EKV_CHECK(dim == 512 || dim == 576, "latent dim must be 512 or 576");
+  int rc = check_rows(k, k_stride, 128, slot_mapping, kcache, k_page_stride);
+  if (rc) return rc;
+  rc = check_rows(latent, latent_stride, dim, slot_mapping, cache, page_stride);
+  if (rc) return rc;
+  EKV_CHECK(q && weights && q_fp8 && w_out, "null pointer");
+  EKV_CHECK(q_head_stride % 8 == 0 && q_tok_stride % 8 == 0, "strides must be multiples of 8");
+  EKV_CHECK(aligned16(q), "misaligned buffers");
+  EKV_CHECK(positions && lengths, "null pointer");
+  EKV_CHECK(topk_out != nullptr && out_stride >= k_top, "topk_out must be [T, >= k]");
+  EKV_CHECK(merged_width >= 0 && merged_stride >= merged_width,
+            "merged_out needs positions, window >= 0 and merged_stride >= merged_width");
+  rc = check_topk_args(q_fp8, w_out, kcache, k_page_stride, block_table, req_ids, lengths, num_tokens, max_len,
+                       k_top, workspace, workspace_bytes, false);
+  if (rc) return rc;
+  EKV_CHECK(q_digits != nullptr && aligned16(q_digits), "q_digits must be a 16-byte aligned [T, 3, 64, 128]");
+
+  const int64_t L = max_len > 0 ? max_len : 1;
+  TopkWorkspace ws = carve(workspace, T, L);
+  FilterArgs f{q_fp8, w_out, kcache, k_page_stride, k_num_pages, block_table, bt_stride, req_ids, lengths,
+               max_len, k_top, ws.upper, ws.hist, num_tokens, plan.groups, nullptr};
+  FusedArgs fa{f, q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts, plan.groups,
+               plan.stage_pages, g_spin_limit, topk_out, out_stride, merged_out, merged_stride, merged_width,
+               positions, window, merged_slots ? 1 : 0};
+  fa.prologue = 1;
+  FusedPrologue& pro = fa.pro;
+  pro.q = q;
+  pro.q_tok_stride = q_tok_stride;
+  pro.q_head_stride = q_head_stride;
+  pro.w = weights;
+  pro.w_is_bf16 = weights_is_bf16;
+  pro.w_stride = w_stride;
+  pro.cos_sin = cos_sin;
+  pro.cs_rows = cos_sin_rows;
+  pro.lengths = lengths;
+  pro.q_fp8_out = q_fp8;
+  pro.w_out = w_out;
+  pro.q_digits_out = q_digits;
+  pro.k_rows = rows_args(k, k_stride, num_tokens, slot_mapping, kcache, k_page_stride, k_num_pages);
+  if (cos_sin != nullptr) {
+    pro.k_rows.positions = positions;
+    pro.k_rows.ln_w = ln_w;
+    pro.k_rows.ln_b = ln_b;
+    pro.k_rows.eps = eps;
+    pro.k_rows.cos_sin = cos_sin;
+    pro.k_rows.cs_rows = cos_sin_rows;
+  }
+  pro.latent = rows_args(latent, latent_stride, num_tokens, slot_mapping, cache, page_stride, num_pages);
+  pro.latent_dim = dim;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(plan.groups), num_tokens);
+  if (plan.waves == 12)
+    hipLaunchKernelGGL((filter_verify_kernel<12, false, true>), grid, dim3(64 * 12), plan.smem, s, fa);
+  else
+    hipLaunchKernelGGL((filter_verify_kernel<4, false, true>), grid, dim3(64 * 4), plan.smem, s, fa);
+  return ekv_launch_status();
 }
 
 extern "C" int ekv_indexer_filter_fp4(const uint8_t* q_values, const int32_t* q_scales, const float* w,

@@ -80,22 +80,41 @@ __device__ __forceinline__ void row_layer_norm(float (&v)[8], const float* w, co
   for (int e = 0; e < 8; ++e) v[e] = bf16_to_f32(f32_to_bf16((d[e] * rstd) * ww[e] + bb[e]));
 }
 
-// NeoX rotation of dims 0..63 by (cos_i, sin_i) = (cs[i], cs[32 + i]): dim i
-// (lanes 0..3) pairs with dim i + 32 (lanes 4..7); cs == nullptr leaves the
-// row as it is.
-__device__ __forceinline__ void row_rope_neox64(float (&v)[8], const float* cs, int j) {
-  float p[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], 4);
-  if (cs == nullptr || j >= 8) return;
+// The cos / sin entries lane j of a 16-lane row group uses in
+// row_rope_neox64 (lanes 0..7; cs == nullptr: none).
+struct RopeLane {
+  float c[8], sn[8];
+  bool on;
+};
+__device__ __forceinline__ RopeLane rope_lane(const float* cs, int j) {
+  RopeLane r;
+  r.on = cs != nullptr && j < 8;
   const int i0 = 8 * (j & 3);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float c = cs[i0 + e], sn = cs[32 + i0 + e];
-    const float r = (j < 4) ? (v[e] * c) - (p[e] * sn)   // x1 c - x2 s
-                            : (v[e] * c) + (p[e] * sn);  // x2 c + x1 s
-    v[e] = bf16_to_f32(f32_to_bf16(r));
+    r.c[e] = r.on ? cs[i0 + e] : 0.0f;
+    r.sn[e] = r.on ? cs[32 + i0 + e] : 0.0f;
   }
+  return r;
+}
+
+// NeoX rotation of dims 0..63 by (cos_i, sin_i) = (cs[i], cs[32 + i]): dim i
+// (lanes 0..3) pairs with dim i + 32 (lanes 4..7); cs == nullptr leaves the
+// row as it is.  The _lane form takes lane j's entries already loaded.
+__device__ __forceinline__ void row_rope_neox64_lane(float (&v)[8], const RopeLane& r, int j) {
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(v[e], 4);
+  if (!r.on) return;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float res = (j < 4) ? (v[e] * r.c[e]) - (p[e] * r.sn[e])   // x1 c - x2 s
+                              : (v[e] * r.c[e]) + (p[e] * r.sn[e]);  // x2 c + x1 s
+    v[e] = bf16_to_f32(f32_to_bf16(res));
+  }
+}
+__device__ __forceinline__ void row_rope_neox64(float (&v)[8], const float* cs, int j) {
+  row_rope_neox64_lane(v, rope_lane(cs, j), j);
 }
 
 // Orthonormal Walsh-Hadamard of the row: spans 1, 2, ..., 64 with

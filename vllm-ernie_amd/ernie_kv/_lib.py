@@ -73,6 +73,12 @@ SIGNATURES: dict[str, tuple] = {
         I32,
         [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, I32, P, I64, P, I64, I32, P, I32, I32, P],
     ),
+    "ekv_dsa_decode_prologue_folds": (I32, [I32, I32]),
+    "ekv_dsa_decode_prologue_topk_merged": (
+        I32,
+        [P, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I32, P, I64, I64, P, I32, I64, I32, P, P, P, P, I32, I32, P,
+         P, P, F32, P, I32, P, I64, P, I32, P, I64, I32, P, I64, P, I64, I32, I32, P],
+    ),
     "ekv_indexer_topk_counter_bytes": (I64, []),
     "ekv_indexer_set_spin_limit": (I32, [I32]),
     "ekv_sparse_mla_decode_workspace_size": (I64, [I32, I32, I32]),

@@ -371,6 +371,7 @@ class DSAStepMetadata:
     block_table: torch.Tensor   # [B, P] int32
     req_ids: torch.Tensor       # [T] int32, query row -> request (row of block_table)
     max_seq_len: int            # tokens of the longest request
+    max_query_len: int = 0      # most query rows of one request in the step (0: not given)
 
 
 @dataclass
@@ -867,12 +868,23 @@ class Ernie5_5DSAAttention(torch.nn.Module):
             qa, qb, wf = ix._quantize_fp4(qp, kp, iw, md.slot_mapping)
             ops.kv_append_quant(latent, md.slot_mapping, self.mla_attn.kv_cache)
             ops.indexer_windowed_lengths(positions, self.window, lengths)
-        else:  # one prologue launch
+        merged = ix.topk_indices_buffer[:num_tokens]
+        L = max(int(md.max_seq_len), 1)
+        if ix.use_fp4_kv:
+            ix._topk(qa, qb, wf, md, lengths, positions, merged=merged)
+        elif md.max_query_len >= 1 and num_tokens * 20 * L <= _INDEXER_WORKSPACE_BYTES:
+            # the prologue and the top-k in one call (in one launch when the
+            # step's rows are decode rows and the top-k is one launch)
+            ops.dsa_decode_prologue_topk_merged(
+                ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions,
+                self.window, lengths, md.block_table, md.req_ids, L,
+                ix.indexer_op.topk_indices_buffer[:num_tokens, : ix.topk], _indexer_workspace(num_tokens, L, q.device),
+                merged, prep=ix._prep_args(q.device), max_new_rows=md.max_query_len)
+        else:  # one prologue launch, then the top-k
             qa, wf, qb = ops.dsa_decode_prologue(
                 ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions,
                 self.window, lengths, prep=ix._prep_args(q.device))
-        merged = ix.topk_indices_buffer[:num_tokens]
-        ix._topk(qa, qb, wf, md, lengths, positions, merged=merged)
+            ix._topk(qa, qb, wf, md, lengths, positions, merged=merged)
         q_abs = self.mla_attn.absorb_q(q)
         o_latent, _ = self.mla_attn.impl._fp8_flash_mla_kernel(
             q_abs[:, None], self.mla_attn.kv_cache, merged[:, None],

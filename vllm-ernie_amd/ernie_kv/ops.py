@@ -608,6 +608,86 @@ def indexer_topk_merged(q_fp8, q_digits, w, kcache, block_table, req_ids, length
     )
 
 
+def dsa_decode_prologue_folds(num_tokens: int, max_len: int) -> bool:
+    """Whether ``dsa_decode_prologue_topk_merged`` of ``num_tokens`` rows of
+    at most ``max_len`` keys runs as one launch on the current device."""
+    return bool(_lib.load().ekv_dsa_decode_prologue_folds(int(num_tokens), int(max_len)))
+
+
+def dsa_decode_prologue_topk_merged(
+    k: torch.Tensor,
+    kcache: torch.Tensor,
+    latent: torch.Tensor,
+    cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    q: torch.Tensor,
+    weights: torch.Tensor,
+    positions: torch.Tensor,
+    window: int,
+    lengths: torch.Tensor,
+    block_table: torch.Tensor,
+    req_ids: torch.Tensor,
+    max_len: int,
+    topk_out: torch.Tensor,
+    workspace: torch.Tensor,
+    merged: torch.Tensor,
+    merged_slots: bool = False,
+    prep: tuple | None = None,
+    max_new_rows: int = 1,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``dsa_decode_prologue(k, kcache, latent, cache, slot_mapping, q,
+    weights, positions, window, lengths, prep)`` then ``indexer_topk_merged``
+    of its outputs over ``kcache`` (the top-k, the merged rows), in one call.
+    ``max_new_rows`` is the most query rows any one sequence has in the call
+    (its newest positions; 1 for plain decode): with ``1 <= max_new_rows <=
+    window`` no row scores a key the call appends, and the prologue runs in
+    the top-k's launch when that is one launch.  Returns the prologue's
+    ``(q_fp8, w, q_digits)``."""
+    _check_dev(k, kcache, latent, cache, slot_mapping, q, weights, positions, lengths, block_table, req_ids,
+               topk_out, workspace, merged)
+    ln_w = ln_b = cos_sin = None
+    eps = 0.0
+    if prep is not None:
+        ln_w, ln_b, eps, cos_sin = prep
+        _check_dev(ln_w, ln_b, cos_sin)
+        _need(ln_w.shape == (128,) and ln_b.shape == (128,) and ln_w.dtype == torch.float32
+              and ln_b.dtype == torch.float32 and ln_w.is_contiguous() and ln_b.is_contiguous(), "ln_w, ln_b fp32 [128]")
+        _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(),
+              "cos_sin fp32 [N, 64]")
+    _bits16(k)
+    _bits16(latent)
+    _bits16(q)
+    T = k.shape[0]
+    _need(k.shape == (T, 128) and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
+    _need(latent.dim() == 2 and latent.shape[0] == T and latent.stride(1) == 1, "latent must be [T, D] row-contiguous")
+    _need(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= T, "slot_mapping int64 [T]")
+    for c in (kcache, cache):
+        _need(c.dtype == torch.uint8 and c.dim() == 2 and c.stride(1) == 1, "caches uint8 [pages, bytes]")
+    _need(q.dim() == 3 and q.shape[0] == T and q.shape[2] == 128 and q.stride(2) == 1, "q must be [T, H, 128]")
+    H = q.shape[1]
+    _need(weights.shape[:2] == (T, H) and weights.stride(1) == 1, "weights [T, H]")
+    _need(weights.dtype in (torch.bfloat16, torch.float32), "weights bf16 or fp32")
+    _need(positions.dtype == torch.int64 and lengths.dtype == torch.int32, "positions int64, lengths int32")
+    _need(block_table.dtype == torch.int32 and block_table.stride(1) == 1, "block_table int32")
+    _need(req_ids.dtype == torch.int32, "req_ids int32")
+    _need(topk_out.dtype == torch.int32 and topk_out.stride(1) == 1, "topk_out int32 [T, K]")
+    m_ptr, m_stride, m_width, p_ptr = _merged_args(merged, positions, window, topk_out, T)
+    q_fp8 = torch.empty((T, H, 128), dtype=torch.uint8, device=q.device)
+    w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
+    digits = torch.empty((T, 3, H, 128), dtype=torch.int8, device=q.device)
+    _lib.call(
+        "ekv_dsa_decode_prologue_topk_merged", k.data_ptr(), _rs(k), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
+        latent.data_ptr(), _rs(latent), latent.shape[1], cache.data_ptr(), _rs(cache), cache.shape[0],
+        slot_mapping.data_ptr(), T, q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), _rs(weights), H, q_fp8.data_ptr(), w_out.data_ptr(), digits.data_ptr(),
+        p_ptr, int(window), int(max_new_rows), lengths.data_ptr(), _ptr(ln_w), _ptr(ln_b), float(eps), _ptr(cos_sin),
+        0 if cos_sin is None else cos_sin.shape[0], block_table.data_ptr(), _rs(block_table), req_ids.data_ptr(),
+        int(max_len), topk_out.data_ptr(), _rs(topk_out), topk_out.shape[1], workspace.data_ptr(), workspace.numel(),
+        m_ptr, m_stride, m_width, int(bool(merged_slots)), _stream(),
+    )
+    return q_fp8, w_out, digits
+
+
 def indexer_topk_counter_bytes() -> int:
     """Bytes at the front of a top-k workspace holding the one-launch path's
     per-row counters (zero between calls)."""
