@@ -557,7 +557,9 @@ __device__ __forceinline__ void load_filter_operands(const FilterArgs& a, int t,
   }
 }
 
-// The pages of row t a filter streams: block-table entry of logical page
+// The pages of a row a filter streams (its request `req`, the row of the
+// block table, read by the caller before the row's length is known, so the
+// two loads overlap): block-table entry of logical page
 // lp (-1 outside [0, p_end), the table or the cache; unmapped pages load
 // page 0, always present, and score 0), and one page's loads: this lane's 32
 // bytes (fp4: 16) of each of the 4 blocks of 16 token rows, and the scale
@@ -568,8 +570,8 @@ struct PageSource {
   const FilterArgs& a;
   const int32_t* bt;
   int p_end;
-  __device__ PageSource(const FilterArgs& args, int t, int end)
-      : a(args), bt(args.block_table + static_cast<int64_t>(args.req_ids[t]) * args.bt_stride), p_end(end) {}
+  __device__ PageSource(const FilterArgs& args, int32_t req, int end)
+      : a(args), bt(args.block_table + static_cast<int64_t>(req) * args.bt_stride), p_end(end) {}
   __device__ int64_t page_of(int lp) const {
     const int64_t p = (lp < p_end && lp < a.bt_stride) ? static_cast<int64_t>(bt[lp]) : -1;
     return (p >= 0 && p < a.num_pages) ? p : -1;
@@ -613,12 +615,12 @@ struct FirstPage {
 // LDS histogram.  With `pre`, page `first` has been loaded already (its
 // rows and scale word in pre).
 template <bool kFp4, class Next, class Emit>
-__device__ __forceinline__ void filter_stream(const FilterArgs& a, int t, int n, int first, int p_end, Next next,
+__device__ __forceinline__ void filter_stream(const FilterArgs& a, int32_t req, int n, int first, int p_end, Next next,
                                               uint32_t* s_hist, const FilterOps& op, Emit emit,
                                               FirstPage* pre = nullptr) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, col = lane & 15;
-  const PageSource<kFp4> src(a, t, p_end);
+  const PageSource<kFp4> src(a, req, p_end);
   auto page_of = [&](int lp) -> int64_t { return src.page_of(lp); };
   auto load_page = [&](int64_t page, uint4 (&kb)[4][2], uint32_t& ks) { src.load(page, kb, ks); };
   // One page scored: its 64 tokens' approximate scores and bounds into the
@@ -735,7 +737,8 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   const int b = static_cast<int>(blockIdx.x);
   const int slot = b >> 3;
   const int t = slot % a.rows;
-  const int x = 8 * (slot / a.rows) + (((b & 7) + a.req_ids[t]) & 7);
+  const int32_t req = a.req_ids[t];
+  const int x = 8 * (slot / a.rows) + (((b & 7) + req) & 7);
   if (x >= a.groups) return;
   if (tid == 0) s_maxn = 0;
   __syncthreads();
@@ -776,7 +779,7 @@ __global__ void __launch_bounds__(256) filter_kernel(FilterArgs a) {
   };
   int staged = 0, stage_first = p_begin;
   int seq = p_begin;
-  filter_stream<kFp4>(a, t, n, p_begin, p_end, [&] { return ++seq; }, s_hist, op,
+  filter_stream<kFp4>(a, req, n, p_begin, p_end, [&] { return ++seq; }, s_hist, op,
                       [&](int lp, int64_t, float sc, float e) {
     stage[staged * kPageTokens + lane] = bf16_round_up(sc + e);
     if (++staged == kFilterStage) {  // wave-uniform
@@ -1095,10 +1098,11 @@ constexpr int64_t kCounterBytes = 256 + int64_t{kCounterRows} * kCounterRow * 4;
 // launch, for decode rows (the new tokens lie in their rows' windows, so no
 // row scores them): every workgroup prepares and quantizes its row's indexer
 // q into LDS as indexer_q_quant does, and takes the row's key count as
-// max(position + 1 - window, 0); the first workgroup of each row appends the
-// new token's indexer K row and latent row (two waves, while the others
-// stream) and writes the count, the q codes, the folded weights and the
-// digit planes out as the prologue would.
+// max(position + 1 - window, 0); the row's first workgroup to arrive at the
+// bound (workgroup 0 of a row with nothing to score) appends the new token's
+// indexer K row and latent row (two waves) and writes the q codes, the
+// folded weights and the digit planes out as the prologue would, while the
+// bound is computed; workgroup 0 writes the count.
 struct FusedPrologue {
   const uint16_t* q;         // [T, 64, 128] bf16 (the raw projection when cos_sin is set)
   int64_t q_tok_stride, q_head_stride;
@@ -1122,8 +1126,8 @@ template <int kThreads>
 struct FusedQRows {
   static constexpr int kPasses = (kIdxHeads * 16 + kThreads - 1) / kThreads;
   uint4 raw[kPasses];
-  float wt[kPasses];
-  RopeLane rope;  // (the same position for every head)
+  uint32_t wbits[kPasses];  // the weight as loaded (bf16 or fp32 bits), converted when used
+  RopeLane rope;            // (the same position for every head)
 };
 
 template <int kThreads>
@@ -1134,12 +1138,12 @@ __device__ __forceinline__ void fused_q_load(const FusedPrologue& p, int64_t t, 
   for (int ps = 0; ps < FusedQRows<kThreads>::kPasses; ++ps) {
     const int h = ps * (kThreads / 16) + static_cast<int>(threadIdx.x >> 4);
     r.raw[ps] = make_uint4(0, 0, 0, 0);
-    r.wt[ps] = 0.0f;
+    r.wbits[ps] = 0u;
     if (h < kIdxHeads) {
       r.raw[ps] = *reinterpret_cast<const uint4*>(p.q + t * p.q_tok_stride + h * p.q_head_stride + 8 * ln);
       if (ln == 0)
-        r.wt[ps] = p.w_is_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.w)[t * p.w_stride + h])
-                               : static_cast<const float*>(p.w)[t * p.w_stride + h];
+        r.wbits[ps] = p.w_is_bf16 ? static_cast<uint32_t>(static_cast<const uint16_t*>(p.w)[t * p.w_stride + h])
+                                  : static_cast<const uint32_t*>(p.w)[t * p.w_stride + h];
     }
   }
 }
@@ -1171,7 +1175,10 @@ __device__ __forceinline__ void fused_q_quant(const FusedPrologue& p, const Fuse
     const uint32_t b2 = f32x2_to_fp8(v[4] * inv, v[5] * inv);
     const uint32_t b3 = f32x2_to_fp8(v[6] * inv, v[7] * inv);
     *reinterpret_cast<uint2*>(s_q8 + h * kIdxDim + 8 * ln) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-    if (ln == 0) s_w[h] = (r.wt[ps] * exp2i(e)) * 0x1.6a09e6p-7f;  // fl32(128**-0.5 * 64**-0.5)
+    if (ln == 0) {
+      const float wt = p.w_is_bf16 ? bf16_to_f32(static_cast<uint16_t>(r.wbits[ps])) : __uint_as_float(r.wbits[ps]);
+      s_w[h] = (wt * exp2i(e)) * 0x1.6a09e6p-7f;  // fl32(128**-0.5 * 64**-0.5)
+    }
   }
 }
 
@@ -1290,10 +1297,10 @@ struct FusedArgs {
   const int64_t* positions;
   int32_t window;
   int32_t merged_slots;      // merged entries as cache slots through the block table
-  // The folded prologue (fp8 keys, in-launch select with merged rows): q, the
-  // weights and the key counts come from `pro`, not from f.q_fp8, f.w,
-  // q_digits and f.lengths.
-  int32_t prologue;
+  // The folded prologue, read by filter_verify_kernel<W, false, true> only
+  // (fp8 keys, in-launch select with merged rows): q, the weights and the
+  // key counts come from `pro`, not from f.q_fp8, f.w, q_digits and
+  // f.lengths.
   FusedPrologue pro;
 };
 
@@ -1498,7 +1505,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   float* const s_qw = reinterpret_cast<float*>(s_q8 + kIdxHeads * kIdxDim);
   static_assert(kIdxHeads * (kIdxDim + 4) <= 2 * Lay::kList * 4, "the prologue's q fits the list's LDS");
   static_assert(!(kPro && kFp4), "the folded prologue takes fp8 keys");
-  constexpr bool pro = kPro;  // (a.prologue set)
+  constexpr bool pro = kPro;
+  const int32_t req = f.req_ids[t];  // (requested with the row's length or position)
   FilterOps op;
   int64_t pos = 0, wl = 0;
   int n;
@@ -1554,7 +1562,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   // memory latency overlaps it and the q operands' (requested first)
   FirstPage first_page;
   {
-    const PageSource<kFp4> src(f, t, wg_p1);
+    const PageSource<kFp4> src(f, req, wg_p1);
     first_page.page = src.page_of(wg_p0 + wave);
     src.load(first_page.page, first_page.kb, first_page.ks);
   }
@@ -1575,7 +1583,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     if (lane == 0) v = atomicAdd(&s_misc[18], 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  filter_stream<kFp4>(f, t, n, wg_p0 + wave, wg_p1, grab, s_hist, op,
+  filter_stream<kFp4>(f, req, n, wg_p0 + wave, wg_p1, grab, s_hist, op,
                       [&](int lp, int64_t page, float sc, float e) {
                         s_pref[(lp - wg_p0) * kPageTokens + lane] = upper_prefix(sc, e);
                         if (lane == 0) s_pages[lp - wg_p0] = static_cast<int32_t>(page);
@@ -3337,7 +3345,6 @@ extern "C" int ekv_dsa_decode_prologue_topk_merged(
   FusedArgs fa{f, q_digits, ws.counters, ws.timeouts, ws.cand_score, ws.cand_idx, ws.counts, plan.groups,
                plan.stage_pages, g_spin_limit, topk_out, out_stride, merged_out, merged_stride, merged_width,
                positions, window, merged_slots ? 1 : 0};
-  fa.prologue = 1;
   FusedPrologue& pro = fa.pro;
   pro.q = q;
   pro.q_tok_stride = q_tok_stride;
