@@ -535,6 +535,26 @@ int ekv_indexer_store_fp4(const uint8_t* values, int64_t values_stride, const ui
                           uint8_t* kcache, int64_t page_stride /*bytes*/, int64_t num_pages, void* stream);
 
 /*
+ * The MXFP4 counterpart of ekv_dsa_decode_prologue, in one launch: with
+ * cos_sin non-null ekv_indexer_prep of q and k first, then
+ * ekv_indexer_k_insert_fp4 of k at slot_mapping, ekv_indexer_q_quant_fp4 of q
+ * and weights (values [T, heads, 64], scale words [T, heads], folded weights),
+ * ekv_kv_append_quant of the latent rows and ekv_indexer_windowed_lengths --
+ * the same bytes as those calls.  Replaces, for a decode step with
+ * use_fp4_indexer_cache, the head of Ernie5_5Indexer.forward with
+ * _quantize_fp4 (nvidia/attention.py:955-1025), the latent append [vLLM
+ * concat_and_cache_mla] and the metadata lengths (nvidia/attention.py:669-675).
+ */
+int ekv_dsa_decode_prologue_fp4(const uint16_t* k, int64_t k_stride, uint8_t* kcache, int64_t k_page_stride,
+                                int64_t k_num_pages, const uint16_t* latent, int64_t latent_stride, int32_t dim,
+                                uint8_t* cache, int64_t page_stride, int64_t num_pages, const int64_t* slot_mapping,
+                                int32_t num_tokens, const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                const void* weights, int32_t weights_is_bf16, int64_t w_stride, int32_t heads,
+                                uint8_t* q_values, int32_t* q_scales, float* w_out, const int64_t* positions,
+                                int32_t window, int32_t* lengths, const float* ln_w, const float* ln_b, float eps,
+                                const float* cos_sin, int32_t cos_sin_rows, void* stream);
+
+/*
  * Exact MXFP4 indexer scores, as ekv_indexer_score for 68-byte key rows: per
  * head, block sums D_b of the integers 2 * e2m1 (exact), T_b =
  * fl32(D_b * 2^(sq_b + sk_b - 256)), dot = ((T_0 + T_1) + T_2) + T_3 in fp32,

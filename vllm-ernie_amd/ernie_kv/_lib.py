@@ -98,6 +98,8 @@ SIGNATURES: dict[str, tuple] = {
     "ekv_indexer_q_quant_fp4": (I32, [P, I64, I64, P, I32, I64, I32, I32, P, P, P, P]),
     "ekv_indexer_k_insert_fp4": (I32, [P, I64, I32, P, P, I64, I64, P]),
     "ekv_indexer_store_fp4": (I32, [P, I64, P, I64, I32, P, P, I64, I64, P]),
+    "ekv_dsa_decode_prologue_fp4": (I32, [P, I64, P, I64, I64, P, I64, I32, P, I64, I64, P, I32, P, I64, I64, P, I32,
+                                          I64, I32, P, P, P, P, I32, P, P, P, F32, P, I32, P]),
     "ekv_indexer_score_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, P, I64, P]),
     "ekv_indexer_filter_fp4": (I32, [P, P, P, P, I64, I64, P, I64, P, P, I32, I32, I32, P, I64, P]),
     "ekv_indexer_select_fp4": (

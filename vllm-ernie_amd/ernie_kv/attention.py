@@ -863,11 +863,10 @@ class Ernie5_5DSAAttention(torch.nn.Module):
         iq, ik, iw = ix._project(hidden_states, q_c)
         latent = torch.cat([kv_c_normed, k_pe.reshape(num_tokens, -1)], dim=-1).contiguous()
         lengths = ix._lengths_buf(num_tokens, q.device)
-        if ix.use_fp4_kv:  # prep, MXFP4 K insert and q, latent append, lengths
-            qp, kp = ops.indexer_prep(iq, ik, *ix._prep_args(q.device), positions)
-            qa, qb, wf = ix._quantize_fp4(qp, kp, iw, md.slot_mapping)
-            ops.kv_append_quant(latent, md.slot_mapping, self.mla_attn.kv_cache)
-            ops.indexer_windowed_lengths(positions, self.window, lengths)
+        if ix.use_fp4_kv:  # prep, MXFP4 K insert and q, latent append, lengths: one launch
+            qa, qb, wf = ops.dsa_decode_prologue_fp4(
+                ik, ix.k_cache.kv_cache, latent, self.mla_attn.kv_cache, md.slot_mapping, iq, iw, positions,
+                self.window, lengths, prep=ix._prep_args(q.device))
         merged = ix.topk_indices_buffer[:num_tokens]
         L = max(int(md.max_seq_len), 1)
         if ix.use_fp4_kv:

@@ -438,6 +438,63 @@ def dsa_decode_prologue(
     return q_fp8, w_out, digits
 
 
+def dsa_decode_prologue_fp4(
+    k: torch.Tensor,
+    kcache: torch.Tensor,
+    latent: torch.Tensor,
+    cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    q: torch.Tensor,
+    weights: torch.Tensor,
+    positions: torch.Tensor,
+    window: int,
+    lengths: torch.Tensor,
+    prep: tuple | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The MXFP4 ``dsa_decode_prologue``, one launch: with ``prep = (ln_w,
+    ln_b, eps, cos_sin)`` ``indexer_prep`` of q and k first, then
+    ``indexer_k_insert_fp4(k, slot_mapping, kcache)``, ``indexer_q_quant_fp4(q,
+    weights)`` (returned: values, scale words, folded weights),
+    ``kv_append_quant(latent, slot_mapping, cache)`` and
+    ``indexer_windowed_lengths(positions, window, lengths)``."""
+    _check_dev(k, kcache, latent, cache, slot_mapping, q, weights, positions, lengths)
+    ln_w = ln_b = cos_sin = None
+    eps = 0.0
+    if prep is not None:
+        ln_w, ln_b, eps, cos_sin = prep
+        _check_dev(ln_w, ln_b, cos_sin)
+        _need(ln_w.shape == (128,) and ln_b.shape == (128,) and ln_w.dtype == torch.float32
+              and ln_b.dtype == torch.float32 and ln_w.is_contiguous() and ln_b.is_contiguous(), "ln_w, ln_b fp32 [128]")
+        _need(cos_sin.dtype == torch.float32 and cos_sin.shape[1] == 64 and cos_sin.is_contiguous(),
+              "cos_sin fp32 [N, 64]")
+    _bits16(k)
+    _bits16(latent)
+    _bits16(q)
+    T = k.shape[0]
+    _need(k.shape == (T, 128) and k.stride(1) == 1, "k must be [T, 128] row-contiguous")
+    _need(latent.dim() == 2 and latent.shape[0] == T and latent.stride(1) == 1, "latent must be [T, D] row-contiguous")
+    _need(slot_mapping.dtype == torch.int64 and slot_mapping.numel() >= T, "slot_mapping int64 [T]")
+    for c in (kcache, cache):
+        _need(c.dtype == torch.uint8 and c.dim() == 2 and c.stride(1) == 1, "caches uint8 [pages, bytes]")
+    _need(q.dim() == 3 and q.shape[0] == T and q.shape[2] == 128 and q.stride(2) == 1, "q must be [T, H, 128]")
+    H = q.shape[1]
+    _need(weights.shape[:2] == (T, H) and weights.stride(1) == 1, "weights [T, H]")
+    _need(weights.dtype in (torch.bfloat16, torch.float32), "weights bf16 or fp32")
+    _need(positions.dtype == torch.int64 and lengths.dtype == torch.int32, "positions int64, lengths int32")
+    values = torch.empty((T, H, 64), dtype=torch.uint8, device=q.device)
+    scales = torch.empty((T, H), dtype=torch.int32, device=q.device)
+    w_out = torch.empty((T, H), dtype=torch.float32, device=q.device)
+    _lib.call(
+        "ekv_dsa_decode_prologue_fp4", k.data_ptr(), _rs(k), kcache.data_ptr(), _rs(kcache), kcache.shape[0],
+        latent.data_ptr(), _rs(latent), latent.shape[1], cache.data_ptr(), _rs(cache), cache.shape[0],
+        slot_mapping.data_ptr(), T, q.data_ptr(), _rs(q), q.stride(1), weights.data_ptr(),
+        int(weights.dtype == torch.bfloat16), _rs(weights), H, values.data_ptr(), scales.data_ptr(), w_out.data_ptr(),
+        positions.data_ptr(), int(window), lengths.data_ptr(), _ptr(ln_w), _ptr(ln_b), float(eps), _ptr(cos_sin),
+        0 if cos_sin is None else cos_sin.shape[0], _stream(),
+    )
+    return values, scales, w_out
+
+
 def indexer_windowed_lengths(positions: torch.Tensor, window: int, out: torch.Tensor) -> None:
     _check_dev(positions, out)
     _need(positions.dtype == torch.int64 and out.dtype == torch.int32, "positions int64, out int32")
