@@ -460,15 +460,51 @@ def measure_indexer_fp4(torch, ops, seed: int, B: int = 32, ctx: int = 131072, r
     n = max(ctx - 128, 0)
     k_bytes = B * n * 68
     timeouts = int(ws[:16].view(torch.int32).sum())
-    del kcache
+
+    # the indexer half of an MXFP4 DSA decode step from the raw projections:
+    # the one-launch prologue (prep, MXFP4 K insert and q quant, latent
+    # append, lengths), then the top-k; and the same with the prologue as
+    # the separate calls it replaces
+    k_new = torch.randn(B, 128, device=dev, generator=g).to(torch.bfloat16)
+    lat_new = torch.randn(B, 576, device=dev, generator=g).to(torch.bfloat16)
+    latent = torch.empty((num_pages, 64 * 580), dtype=torch.uint8, device=dev)  # only the appended rows are written
+    slots = (block_table[:, (ctx - 1) // 64].to(torch.int64) * 64 + (ctx - 1) % 64).contiguous()
+    ang = torch.arange(ctx, device=dev, dtype=torch.float64)[:, None] * (
+        1e4 ** (-torch.arange(32, device=dev, dtype=torch.float64) * 2.0 / 64))[None, :]
+    prep = ((1.0 + 0.1 * torch.randn(128, device=dev, generator=g)).contiguous(),
+            (0.1 * torch.randn(128, device=dev, generator=g)).contiguous(), 1e-6,
+            torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).float().contiguous())
+    lens = torch.empty(B, dtype=torch.int32, device=dev)
+
+    def indexer_step():
+        a, b, c = ops.dsa_decode_prologue_fp4(k_new, kcache, lat_new, latent, slots, q, w, positions, 128, lens,
+                                              prep=prep)
+        ops.indexer_topk_merged_fp4(a, b, c, kcache, block_table, req, lens, ctx, topk, ws, merged=merged,
+                                    positions=positions, window=128)
+
+    def indexer_step_separate():
+        qp, kp = ops.indexer_prep(q, k_new, *prep, positions)
+        ops.indexer_k_insert_fp4(kp, slots, kcache)
+        a, b, c = ops.indexer_q_quant_fp4(qp, w)
+        ops.kv_append_quant(lat_new, slots, latent)
+        ops.indexer_windowed_lengths(positions, 128, lens)
+        ops.indexer_topk_merged_fp4(a, b, c, kcache, block_table, req, lens, ctx, topk, ws, merged=merged,
+                                    positions=positions, window=128)
+
+    step_ms = time_ms(torch, indexer_step, reps)
+    step_sep_ms = time_ms(torch, indexer_step_separate, reps)
+    del kcache, latent
     return {
         "workload": f"indexer_fp4_b{B}_ctx{ctx}",
         "ms": round(ms, 4), "key_bytes": k_bytes, "GB/s_keys": round(k_bytes / (ms * 1e-3) / 1e9, 1),
         "frac_keys": round(k_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "wait_timeouts": timeouts,
+        "indexer_step_ms": round(step_ms, 4), "indexer_step_separate_ms": round(step_sep_ms, 4),
         "what": "ekv_indexer_topk_merged_fp4 (filter, exact scoring of the candidates, exact top-2048 and the "
                 "merged rows in one launch) over 68-byte MXFP4 key rows, q pre-quantized; frac_keys = key bytes "
-                "/ call time / 8 TB/s",
+                "/ call time / 8 TB/s; indexer_step_ms = the indexer half of an MXFP4 DSA decode step from the raw "
+                "projections (ekv_dsa_decode_prologue_fp4, one launch, then the top-k), "
+                "indexer_step_separate_ms = the same with the prologue as its five separate calls",
     }
 
 
