@@ -78,3 +78,27 @@ def test_folded_prologue_matches_two_calls(dev, label, ctxs, R, prep_on, spikes,
         bad = (a != b).nonzero()
         assert bad.numel() == 0, f"{label}: {key} differs at {bad[:8].tolist()} ({bad.shape[0]} entries)"
     assert ref["counters_zero"] and got["counters_zero"]
+
+
+def test_folded_prologue_when_every_wait_gives_up(dev):
+    """With the waits' poll limit at 0 every row's workgroups stop waiting for
+    one another (each row then selects alone, exactly): the folded
+    prologue's outputs and appends, written by the row's first workgroup to
+    arrive before it waits, must still be the two calls' bytes."""
+    import bench
+    from ernie_kv import ops
+
+    st = bench.build_dsa_decode(torch, ops, [5000, 20000, 2177, 9000], 7, spikes="random_row")
+    prep = (st["ln_w"], st["ln_b"], 1e-6, st["rope"])
+    ref = _run(st, prep, st["w_idx"], WINDOW, folded=False)
+    prev = ops.indexer_set_spin_limit(0)
+    try:
+        got = _run(st, prep, st["w_idx"], WINDOW, folded=True)
+    finally:
+        ops.indexer_set_spin_limit(prev)
+    for key in ("kcache", "latent", "lengths", "q8", "w", "digits", "topk", "merged"):
+        a, b = ref[key], got[key]
+        if a.dtype == torch.float32:
+            a, b = a.view(torch.int32), b.view(torch.int32)
+        assert torch.equal(a, b), key
+    assert got["counters_zero"]
